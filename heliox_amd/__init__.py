@@ -1,0 +1,9 @@
+"""MI355X-native HelioX simulation core: HIP kernels behind a C ABI
+(include/heliox.h), a ``heliox.Sim``-compatible Python surface and seeded
+synthetic workloads."""
+from .spec import MechSpec, ModelSpec, NetConSpec, VecPlaySpec
+from .synth import build_config
+from .sim import HelioxError, Sim, emulate_tree_solve, lib
+
+__all__ = ["MechSpec", "ModelSpec", "NetConSpec", "VecPlaySpec", "build_config", "Sim", "HelioxError",
+           "emulate_tree_solve", "lib"]

@@ -1,0 +1,199 @@
+// Internal types shared by the host runtime and the HIP kernels.
+//
+// HBM layout (one model per handle):
+//   * node arrays (v, d, rhs, a, b, cm, area) are stored in solver order:
+//     cells are contiguous, and inside a cell nodes are grouped in chunks
+//     (unbranched runs of at most kChunk nodes) ordered root-round first;
+//   * every mechanism is a structure of arrays: column c of mechanism m lives
+//     at base + c * stride (stride = instance count rounded up to 64), and
+//     instances are sorted by solver-order node index;
+//   * a mechanism that has one instance on every node is "dense": instance i
+//     sits on node i and is processed by the fused node-parallel kernel;
+//     the others are "sparse" and run instance-parallel.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace hx {
+
+// Mechanism ids in CoreNEURON type order: currents are accumulated in this
+// order (coredat_to_innerdat.cpp:176-181 keeps CoreNEURON's order).
+enum MechId : int {
+    M_PAS = 0, M_NA_ION, M_K_ION, M_HH, M_ICLAMP, M_EXPSYN, M_EXP2SYN, M_VECSTIM,
+    M_CA_ION, M_CADYN, M_CAHVA, M_HALFGAP, M_HDLA, M_COUNT
+};
+
+// Column layouts: parameters, then states, then assigned variables.
+enum PasCol { PAS_G = 0, PAS_E, PAS_I, PAS_NCOL };
+enum IonCol { ION_EREV = 0, ION_CONCI, ION_CONCO, ION_CUR, ION_DCURDV, ION_NCOL };
+enum HHCol {
+    HH_GNABAR = 0, HH_GKBAR, HH_GL, HH_EL, HH_M, HH_H, HH_N, HH_ENA, HH_EK, HH_INA, HH_IK, HH_IL,
+    HH_GNA, HH_GK, HH_MINF, HH_HINF, HH_NINF, HH_MTAU, HH_HTAU, HH_NTAU, HH_NCOL
+};
+enum IClampCol { IC_DELAY = 0, IC_DUR, IC_AMP, IC_I, IC_NCOL };
+enum ExpSynCol { ES_TAU = 0, ES_E, ES_G, ES_I, ES_NCOL };
+enum Exp2SynCol { E2_TAU1 = 0, E2_TAU2, E2_E, E2_A, E2_B, E2_FACTOR, E2_G, E2_I, E2_NCOL };
+enum CaDynCol { CD_GAMMA = 0, CD_DECAY, CD_DEPTH, CD_MINCAI, CD_NCOL };
+enum CaHVACol {
+    CH_GBAR = 0, CH_M, CH_H, CH_ECA, CH_ICA, CH_G, CH_IMECH, CH_MINF, CH_MTAU, CH_MALPHA, CH_MBETA,
+    CH_HINF, CH_HTAU, CH_HALPHA, CH_HBETA, CH_NCOL
+};
+enum HalfGapCol { HG_G = 0, HG_VGAP, HG_I, HG_NCOL };
+enum HdLaCol { HD_GHDBAR = 0, HD_VHALFL, HD_TAU, HD_L, HD_I, HD_LINF, HD_TAUL, HD_GHD, HD_NCOL };
+
+// Per-mechanism device view.
+struct MechDev {
+    double* base = nullptr;       // column c at base + c * stride
+    long long stride = 0;
+    int n = 0;
+    int dense = 0;                // instance i on node i for every node
+    const int* node = nullptr;    // solver-order node of each instance
+    const int* ion[3] = {nullptr, nullptr, nullptr};   // na, k, ca instance of each instance
+    const int* iontype = nullptr; // ions only
+    __host__ __device__ double* col(int c) const { return base + c * stride; }
+};
+
+// Global constants of the hot-path mechanisms, computed once on the host
+// with the same expressions the reference evaluates per call.
+struct MechConsts {
+    double hh_q10;                // pow(3, (celsius - 6.3) / 10)            hh_templated.cu:87
+    double hd_qt;                 // pow(q10, (celsius - 33) / 10)           hd_la.cu:94
+    double hd_ehd, hd_kl, hd_vhalft, hd_a0t, hd_zetat, hd_gmt, hd_qtl;
+    double ktf;                   // 1000 R (celsius + 273.15) / F           eion.cuh:33-36
+};
+
+struct StepArgs {
+    int N;                        // nodes
+    double* v;
+    double* d;
+    double* rhs;
+    const double* area;
+    MechDev m[M_COUNT];
+    unsigned dense_mask;          // mechanisms processed by the fused node kernel
+    int do_state;                 // finish the previous step's state update first
+    int do_current;
+    int write_assigned;           // also store assigned outputs (i, ina, gna, minf, ...)
+    double t;                     // time of the current evaluation (t_n + dt/2)
+    double dt;
+    MechConsts c;
+};
+
+// Chunked tree-solve schedule (one wavefront per cell).
+struct ChunkDesc {
+    int start;        // cell-relative solver index of the chunk head (proximal node)
+    int len;          // nodes in the chunk (<= kChunk), head..tail contiguous
+    int slot;         // LDS slot of this chunk
+    int parent_slot;  // LDS slot of the chunk holding the head's parent (-1 for the root chunk)
+    int head_parent;  // cell-relative solver index of the head's parent (-1 for the root)
+    int child_begin;  // LDS slots of the chunks hanging off the tail: [child_begin, +child_count)
+    int child_count;
+    int pad;
+};
+constexpr int kChunk = 8;
+constexpr int kWave = 64;
+
+struct SolveArgs {
+    int ncell;
+    const int* cell_node_begin;   // [ncell+1]
+    const int* cell_round_begin;  // [ncell+1]
+    const int* round_desc_begin;  // [nround+1]
+    const ChunkDesc* desc;
+    double* v;
+    double* d;
+    double* rhs;
+    const double* a;
+    const double* b;
+    const double* cm;
+    double cfac;                  // 1e-3 * cj (capac.cpp:68-80)
+};
+
+// Event ring: one slot per delivery step (mod nslot), fixed capacity per slot.
+struct EventRing {
+    int* count;                   // [nslot]
+    int* entry;                   // [nslot * cap], packed (type << 30) | instance
+    int nslot;                    // power of two
+    int cap;
+    int* overflow;                // set to 1 when a slot overflowed
+};
+
+// Fan-out tables: source -> synapse targets (packed type|instance) with delays.
+struct FanOut {
+    const int* begin;             // [nsrc+1]
+    const int* target;
+    const double* delay;
+};
+
+struct SpikeArgs {
+    int npre;
+    const double* v;
+    const int* node;              // solver-order node of each detector
+    const double* thr;
+    int* flag;
+    const int* gid;
+    double t;                     // step start time t_k
+    int k;                        // step index (delivery slot base)
+    double* log_t;                // spike log
+    int* log_gid;
+    int* log_count;
+    int log_cap;
+    FanOut fo;
+    EventRing ring;
+    const double* ttab;           // t of every step since finitialize
+    int kmax;                     // last valid ttab index
+    double half_dt;
+};
+
+struct InputArgs {
+    const double* eff_time;       // sorted effective VecStim event times
+    const int* inst;              // VecStim instance of each event
+    int n;
+    int* cursor;                  // first unprocessed event
+    double tcut;                  // t_k + dt/2
+    double t;                     // t_k
+    int k;
+    FanOut fo;
+    EventRing ring;
+    const double* ttab;
+    int kmax;
+    double half_dt;
+};
+
+struct DeliverArgs {
+    EventRing ring;
+    int k;
+    MechDev es;                   // ExpSyn
+    MechDev e2;                   // Exp2Syn
+    const double* es_weight;
+    const double* e2_weight;
+};
+
+struct VecPlayDev {
+    double* target;
+    const double* tvec;
+    const double* yvec;
+    int len;
+    int last_index;
+    int next_idx;
+    int done;
+    double next_time;
+};
+
+// launch wrappers (kernels.hip)
+void launch_dense(const StepArgs& a, hipStream_t s);
+void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
+void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
+void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
+void launch_init(int mech, const StepArgs& a, hipStream_t s);
+void launch_set_v(double* v, int n, double val, hipStream_t s);
+void launch_solve(const SolveArgs& a, int max_slots, hipStream_t s);
+void launch_spike(const SpikeArgs& a, hipStream_t s);
+void launch_input(const InputArgs& a, hipStream_t s);
+void launch_deliver(const DeliverArgs& a, hipStream_t s);
+void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s);
+void launch_vecplay_reset(VecPlayDev* items, int n, hipStream_t s);
+void launch_record(double* const* ptrs, int n, double* out, hipStream_t s);
+void launch_gap(const double* v, const int* src_node, double* vgap_col, const int* halfgap_inst, int n,
+                hipStream_t s);
+void launch_clear_ints(int* p, long long n, hipStream_t s);
+
+}  // namespace hx

@@ -1,0 +1,672 @@
+// HIP kernels of the per-step simulation core (CDNA4 / gfx950, wave64).
+//
+// One fixed step (reference order: simulate.cpp:410-442, simulate.cu:722-771):
+//   deliver events -> t+dt/2 -> VecPlay -> currents (FD Jacobian) -> capacitance
+//   + axial terms -> tree solve -> v += dv -> gap copy -> t+dt/2 -> VecPlay ->
+//   states (ion writers first) -> record.
+//
+// Kernels here:
+//   k_dense ........ node-parallel fused mechanisms; optionally finishes the
+//                    previous step's cnexp state update before evaluating this
+//                    step's currents, so each state is read and written once
+//   k_sparse<M> .... the same arithmetic for mechanisms present on a subset of
+//                    nodes (instance-parallel, gather v / update d, rhs)
+//   k_point<M> ..... point-process currents (IClamp, ExpSyn, Exp2Syn, HalfGap),
+//                    scaled by 1e2/area and accumulated with fp64 atomics
+//   k_solve ........ one wavefront per cell: capacitance + axial assembly, the
+//                    Hines elimination over chunked unbranched runs, back
+//                    substitution and v update; junction values through LDS
+//   k_spike ........ threshold detection, wave-ballot compaction into the spike
+//                    log, fan-out of deliveries into the device event ring
+//   k_input ........ VecStim trains (sorted on the host) entering the ring
+//   k_deliver ...... NET_RECEIVE of the events due this step
+//   k_vecplay, k_record, k_gap, init kernels.
+#include "hx_internal.h"
+#include "mech_math.h"
+#include "solve_chunk.h"
+
+namespace hx {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ int ion_index(const MechDev& m, int which, int j) {
+    const int* p = m.ion[which];
+    return p ? p[j] : j;
+}
+
+// ---------------------------------------------------------------------------
+// per-mechanism state updates (shared by the dense and sparse kernels)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void hh_state(const StepArgs& A, const MechDev& m, int j, double v) {
+    double minf, mtau, hinf, htau, ninf, ntau;
+    hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
+    double* M = m.col(HH_M);
+    double* H = m.col(HH_H);
+    double* Nn = m.col(HH_N);
+    M[j] = hh_cnexp(M[j], minf, mtau, A.dt);
+    H[j] = hh_cnexp(H[j], hinf, htau, A.dt);
+    Nn[j] = hh_cnexp(Nn[j], ninf, ntau, A.dt);
+    if (A.write_assigned) {
+        m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
+        m.col(HH_HINF)[j] = hinf; m.col(HH_HTAU)[j] = htau;
+        m.col(HH_NINF)[j] = ninf; m.col(HH_NTAU)[j] = ntau;
+    }
+}
+
+__device__ __forceinline__ void cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
+                                            const double* ca_erev, int ci) {
+    double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
+    cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
+    double* M = m.col(CH_M);
+    double* H = m.col(CH_H);
+    M[j] = M[j] + (1.0 - exp(-A.dt / mTau)) * (mInf - M[j]);
+    H[j] = H[j] + (1.0 - exp(-A.dt / hTau)) * (hInf - H[j]);
+    if (A.write_assigned) {
+        m.col(CH_ECA)[j] = ca_erev[ci];
+        m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
+        m.col(CH_HINF)[j] = hInf; m.col(CH_HTAU)[j] = hTau; m.col(CH_HALPHA)[j] = hAlpha; m.col(CH_HBETA)[j] = hBeta;
+    }
+}
+
+__device__ __forceinline__ void hdla_state(const StepArgs& A, const MechDev& m, int j, double v) {
+    double linf, taul;
+    hdla_rate(v, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
+    double* L = m.col(HD_L);
+    L[j] = L[j] + (1.0 - exp(-A.dt / taul)) * (linf - L[j]);
+    if (A.write_assigned) { m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul; }
+}
+
+__device__ __forceinline__ void cadyn_state(const StepArgs& A, const MechDev& m, int j, double* ca_conci,
+                                            const double* ca_cur, int ci) {
+    ca_conci[ci] = cadyn_step(ca_conci[ci], ca_cur[ci], m.col(CD_GAMMA)[j], m.col(CD_DECAY)[j],
+                              m.col(CD_DEPTH)[j], m.col(CD_MINCAI)[j], A.dt);
+}
+
+// ---------------------------------------------------------------------------
+// per-mechanism FD currents: returns I(v), sets g = (I(v+0.001) - I(v)) / 0.001
+// (mech_template.cuh:616-626); ion currents are added on the I(v) evaluation
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
+    double gp = m.col(PAS_G)[j], ep = m.col(PAS_E)[j];
+    double v1 = v + 0.001;
+    double i1 = gp * (v1 - ep);
+    double i0 = gp * (v - ep);
+    g = (i1 - i0) / 0.001;
+    if (A.write_assigned) m.col(PAS_I)[j] = i0;
+    return i0;
+}
+
+__device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g,
+                                         const double* na_erev, double* na_cur, int nai,
+                                         const double* k_erev, double* k_cur, int ki) {
+    double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
+    double gl = m.col(HH_GL)[j], el = m.col(HH_EL)[j];
+    double mm = m.col(HH_M)[j], hh = m.col(HH_H)[j], nn = m.col(HH_N)[j];
+    double ena = na_erev[nai], ek = k_erev[ki];
+    double gna, ina, gk, ik, il;
+    double v1 = v + 0.001;
+    double i1 = hh_current(v1, gnabar, gkbar, gl, el, mm, hh, nn, ena, ek, gna, ina, gk, ik, il);
+    double i0 = hh_current(v, gnabar, gkbar, gl, el, mm, hh, nn, ena, ek, gna, ina, gk, ik, il);
+    na_cur[nai] += ina;
+    k_cur[ki] += ik;
+    g = (i1 - i0) / 0.001;
+    if (A.write_assigned) {
+        m.col(HH_ENA)[j] = ena; m.col(HH_EK)[j] = ek; m.col(HH_INA)[j] = ina; m.col(HH_IK)[j] = ik;
+        m.col(HH_IL)[j] = il; m.col(HH_GNA)[j] = gna; m.col(HH_GK)[j] = gk;
+    }
+    return i0;
+}
+
+__device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g,
+                                            const double* ca_erev, double* ca_cur, int ci) {
+    double gbar = m.col(CH_GBAR)[j], mm = m.col(CH_M)[j], hh = m.col(CH_H)[j];
+    double eca = ca_erev[ci];
+    double v1 = v + 0.001;
+    double gg = gbar * mm * mm * hh;
+    double i1 = gg * (v1 - eca);
+    double i0 = gg * (v - eca);
+    ca_cur[ci] += i0;
+    g = (i1 - i0) / 0.001;
+    if (A.write_assigned) {
+        m.col(CH_ECA)[j] = eca; m.col(CH_G)[j] = gg; m.col(CH_ICA)[j] = i0; m.col(CH_IMECH)[j] = i0;
+    }
+    return i0;
+}
+
+__device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
+    double ghd = m.col(HD_GHDBAR)[j] * m.col(HD_L)[j];
+    double v1 = v + 0.001;
+    double i1 = ghd * (v1 - A.c.hd_ehd);
+    double i0 = ghd * (v - A.c.hd_ehd);
+    g = (i1 - i0) / 0.001;
+    if (A.write_assigned) { m.col(HD_GHD)[j] = ghd; m.col(HD_I)[j] = i0; }
+    return i0;
+}
+
+__device__ __forceinline__ void ion_cur(const MechDev& m, int j, double z, double ktf, int write_dcurdv) {
+    m.col(ION_CUR)[j] = 0.;
+    if (write_dcurdv) m.col(ION_DCURDV)[j] = 0.;
+    if (m.iontype[j] & 0100)
+        m.col(ION_EREV)[j] = nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf);
+}
+
+#define HAS(bit) (A.dense_mask & (1u << (bit)))
+
+// ---------------------------------------------------------------------------
+// fused node-parallel kernel for dense mechanisms
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.N) return;
+    const double v = A.v[i];
+    const MechDev& na = A.m[M_NA_ION];
+    const MechDev& kk = A.m[M_K_ION];
+    const MechDev& ca = A.m[M_CA_ION];
+    if (A.do_state) {
+        // ion-writing mechanisms first (simulate.cpp:822-834)
+        if (HAS(M_CADYN)) cadyn_state(A, A.m[M_CADYN], i, ca.col(ION_CONCI), ca.col(ION_CUR), i);
+        if (HAS(M_HH)) hh_state(A, A.m[M_HH], i, v);
+        if (HAS(M_CAHVA)) cahva_state(A, A.m[M_CAHVA], i, v, ca.col(ION_EREV), i);
+        if (HAS(M_HDLA)) hdla_state(A, A.m[M_HDLA], i, v);
+    }
+    if (!A.do_current) return;
+    double rhs = 0.0, d = 0.0, g, cur;
+    if (HAS(M_PAS)) { cur = pas_cur(A, A.m[M_PAS], i, v, g); rhs -= cur; d += g; }
+    if (HAS(M_NA_ION)) ion_cur(na, i, 1.0, A.c.ktf, A.write_assigned);
+    if (HAS(M_K_ION)) ion_cur(kk, i, 1.0, A.c.ktf, A.write_assigned);
+    if (HAS(M_HH)) {
+        cur = hh_cur(A, A.m[M_HH], i, v, g, na.col(ION_EREV), na.col(ION_CUR), i, kk.col(ION_EREV),
+                     kk.col(ION_CUR), i);
+        rhs -= cur; d += g;
+    }
+    if (HAS(M_CA_ION)) ion_cur(ca, i, 2.0, A.c.ktf, A.write_assigned);
+    if (HAS(M_CAHVA)) {
+        cur = cahva_cur(A, A.m[M_CAHVA], i, v, g, ca.col(ION_EREV), ca.col(ION_CUR), i);
+        rhs -= cur; d += g;
+    }
+    if (HAS(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, g); rhs -= cur; d += g; }
+    A.d[i] = d;
+    A.rhs[i] = rhs;
+}
+
+// ---------------------------------------------------------------------------
+// sparse density mechanisms: instance-parallel, at most one instance per node
+// ---------------------------------------------------------------------------
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const double v = A.v[node];
+    if (MECH == M_NA_ION || MECH == M_K_ION || MECH == M_CA_ION) {
+        if (A.do_current) ion_cur(m, j, MECH == M_CA_ION ? 2.0 : 1.0, A.c.ktf, A.write_assigned);
+        return;
+    }
+    const MechDev& na = A.m[M_NA_ION];
+    const MechDev& kk = A.m[M_K_ION];
+    const MechDev& ca = A.m[M_CA_ION];
+    if (A.do_state) {
+        if (MECH == M_CADYN) cadyn_state(A, m, j, ca.col(ION_CONCI), ca.col(ION_CUR), ion_index(m, 2, j));
+        if (MECH == M_HH) hh_state(A, m, j, v);
+        if (MECH == M_CAHVA) cahva_state(A, m, j, v, ca.col(ION_EREV), ion_index(m, 2, j));
+        if (MECH == M_HDLA) hdla_state(A, m, j, v);
+    }
+    if (!A.do_current || MECH == M_CADYN) return;
+    double g = 0.0, cur = 0.0;
+    if (MECH == M_PAS) cur = pas_cur(A, m, j, v, g);
+    if (MECH == M_HH)
+        cur = hh_cur(A, m, j, v, g, na.col(ION_EREV), na.col(ION_CUR), ion_index(m, 0, j), kk.col(ION_EREV),
+                     kk.col(ION_CUR), ion_index(m, 1, j));
+    if (MECH == M_CAHVA) cur = cahva_cur(A, m, j, v, g, ca.col(ION_EREV), ca.col(ION_CUR), ion_index(m, 2, j));
+    if (MECH == M_HDLA) cur = hdla_cur(A, m, j, v, g);
+    A.rhs[node] -= cur;
+    A.d[node] += g;
+}
+
+// ---------------------------------------------------------------------------
+// point processes: FD current, x 1e2/area, fp64 atomics (several per node)
+// ---------------------------------------------------------------------------
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const double v = A.v[node];
+    const double v1 = v + 0.001;
+    double i1 = 0.0, i0 = 0.0;
+    bool electrode = false;
+    if (MECH == M_ICLAMP) {
+        double del = m.col(IC_DELAY)[j], dur = m.col(IC_DUR)[j];
+        double cur = 0.0;
+        if (A.t < del + dur && A.t >= del) cur = m.col(IC_AMP)[j];
+        i1 = cur; i0 = cur;
+        if (A.write_assigned) m.col(IC_I)[j] = cur;
+        electrode = true;
+    } else if (MECH == M_HALFGAP) {
+        double vg = m.col(HG_VGAP)[j], gg = m.col(HG_G)[j];
+        i1 = (vg - v1) * gg;
+        i0 = (vg - v) * gg;
+        if (A.write_assigned) m.col(HG_I)[j] = i0;
+        electrode = true;
+    } else if (MECH == M_EXPSYN) {
+        double gg = m.col(ES_G)[j], e = m.col(ES_E)[j];
+        i1 = gg * (v1 - e);
+        i0 = gg * (v - e);
+        if (A.write_assigned) m.col(ES_I)[j] = i0;
+    } else if (MECH == M_EXP2SYN) {
+        double gg = m.col(E2_B)[j] - m.col(E2_A)[j];
+        double e = m.col(E2_E)[j];
+        i1 = gg * (v1 - e);
+        i0 = gg * (v - e);
+        if (A.write_assigned) { m.col(E2_G)[j] = gg; m.col(E2_I)[j] = i0; }
+    }
+    double g = (i1 - i0) / 0.001;
+    double mfact = 1.e2 / A.area[node];
+    g *= mfact;
+    i0 *= mfact;
+    if (electrode) {
+        atomicAdd(&A.rhs[node], i0);
+        atomicAdd(&A.d[node], -g);
+    } else {
+        atomicAdd(&A.rhs[node], -i0);
+        atomicAdd(&A.d[node], g);
+    }
+}
+
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_point_state(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    if (MECH == M_EXPSYN) {
+        double* g = m.col(ES_G);
+        g[j] = expsyn_decay(g[j], m.col(ES_TAU)[j], A.dt);
+    } else if (MECH == M_EXP2SYN) {
+        double* a = m.col(E2_A);
+        double* b = m.col(E2_B);
+        double aa = a[j], bb = b[j];
+        a[j] = exp2syn_decay(aa, m.col(E2_TAU1)[j], A.dt);
+        b[j] = exp2syn_decay(bb, m.col(E2_TAU2)[j], A.dt);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// finitialize: mechanism INITIAL blocks (mech_template.cuh:552-585, eion.cuh:183-197)
+// ---------------------------------------------------------------------------
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_init(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    if (MECH == M_NA_ION || MECH == M_K_ION || MECH == M_CA_ION) {
+        const double z = MECH == M_CA_ION ? 2.0 : 1.0;
+        const double ci0 = MECH == M_NA_ION ? 10.0 : (MECH == M_K_ION ? 140.0 : 5.e-5);
+        const double co0 = MECH == M_NA_ION ? 140.0 : (MECH == M_K_ION ? 4.0 : 2.0);
+        int it = m.iontype[j];
+        if (it & 04) { m.col(ION_CONCI)[j] = ci0; m.col(ION_CONCO)[j] = co0; }
+        if (it & 040) m.col(ION_EREV)[j] = nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, A.c.ktf);
+        return;
+    }
+    const int node = m.dense ? j : m.node[j];
+    const double v = A.v[node];
+    if (MECH == M_HH) {
+        const MechDev& na = A.m[M_NA_ION];
+        const MechDev& kk = A.m[M_K_ION];
+        double minf, mtau, hinf, htau, ninf, ntau;
+        hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
+        m.col(HH_ENA)[j] = na.col(ION_EREV)[ion_index(m, 0, j)];
+        m.col(HH_EK)[j] = kk.col(ION_EREV)[ion_index(m, 1, j)];
+        m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau; m.col(HH_HINF)[j] = hinf;
+        m.col(HH_HTAU)[j] = htau; m.col(HH_NINF)[j] = ninf; m.col(HH_NTAU)[j] = ntau;
+        m.col(HH_M)[j] = minf; m.col(HH_H)[j] = hinf; m.col(HH_N)[j] = ninf;
+    } else if (MECH == M_CAHVA) {
+        double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
+        cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
+        m.col(CH_ECA)[j] = A.m[M_CA_ION].col(ION_EREV)[ion_index(m, 2, j)];
+        m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
+        m.col(CH_HINF)[j] = hInf; m.col(CH_HTAU)[j] = hTau; m.col(CH_HALPHA)[j] = hAlpha; m.col(CH_HBETA)[j] = hBeta;
+        m.col(CH_M)[j] = mInf;
+        m.col(CH_H)[j] = hInf;
+    } else if (MECH == M_HDLA) {
+        double linf, taul;
+        hdla_rate(v, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
+        m.col(HD_LINF)[j] = linf;
+        m.col(HD_TAUL)[j] = taul;
+        m.col(HD_L)[j] = linf;
+    } else if (MECH == M_ICLAMP) {
+        m.col(IC_I)[j] = 0.0;
+    } else if (MECH == M_HALFGAP) {
+        m.col(HG_I)[j] = 0.0;
+    } else if (MECH == M_EXPSYN) {
+        m.col(ES_G)[j] = 0;
+    } else if (MECH == M_EXP2SYN) {
+        double tau1 = m.col(E2_TAU1)[j], tau2 = m.col(E2_TAU2)[j];
+        if (tau1 / tau2 > 0.9999) { tau1 = 0.9999 * tau2; m.col(E2_TAU1)[j] = tau1; }
+        if (tau1 / tau2 < 1e-9) { tau1 = tau2 * 1e-9; m.col(E2_TAU1)[j] = tau1; }
+        m.col(E2_A)[j] = 0.0;
+        m.col(E2_B)[j] = 0.0;
+        double tp = (tau1 * tau2) / (tau2 - tau1) * log(tau2 / tau1);
+        m.col(E2_FACTOR)[j] = 1.0 / (-exp(-tp / tau1) + exp(-tp / tau2));
+    }
+    // CaDynamics_E2 keeps cai in the ca_ion conci column (its INITIAL copies it
+    // back unchanged, CaDynamics_E2.cu:87-96); pas has no INITIAL block.
+}
+
+__global__ void k_set_v(double* v, int n, double val) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) v[i] = val;
+}
+
+// ---------------------------------------------------------------------------
+// Tree solve: one wavefront per cell.  Forward rounds run leaves -> root, each
+// lane eliminating one chunk (an unbranched run of <= kChunk nodes) into its
+// parent; the head's contribution to the parent chunk's tail is passed through
+// an LDS slot.  Back substitution runs the rounds in reverse.
+//   assembly: simulate.cpp:527-555, capacitance capac.cpp:68-80
+//   elimination / back substitution: simulate.cpp:558-581
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S) {
+    extern __shared__ double slots[];     // 2 doubles per chunk
+    const int c = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int nb = S.cell_node_begin[c];
+    const int r0 = S.cell_round_begin[c];
+    const int r1 = S.cell_round_begin[c + 1];
+
+    for (int r = r1 - 1; r >= r0; --r) {
+        const int db = S.round_desc_begin[r];
+        if (db + lane < S.round_desc_begin[r + 1])
+            chunk_forward(S.desc[db + lane], nb, S.v, S.d, S.rhs, S.a, S.b, S.cm, S.cfac, slots);
+        __syncthreads();
+    }
+    for (int r = r0; r < r1; ++r) {
+        const int db = S.round_desc_begin[r];
+        double xtail = 0.0;
+        int myslot = -1;
+        if (db + lane < S.round_desc_begin[r + 1]) {
+            const ChunkDesc q = S.desc[db + lane];
+            xtail = chunk_back(q, nb, S.v, S.d, S.rhs, S.b, slots);
+            myslot = q.slot;
+        }
+        __syncthreads();
+        if (myslot >= 0) slots[2 * myslot] = xtail;
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// events
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int delivery_step(const double* ttab, int k, int kmax, double T, double half_dt) {
+    // first step m >= k whose receive window t_m + dt/2 covers T (postsyn.cpp:43-61)
+    int m = k;
+    const double est = (T - ttab[k]) / (2.0 * half_dt);
+    if (est > 2.0) m = est - 1.0 < static_cast<double>(kmax - k) ? k + static_cast<int>(est) - 1 : kmax;
+    while (m < kmax && ttab[m] + half_dt < T) ++m;
+    while (m > k && ttab[m - 1] + half_dt >= T) --m;
+    return m;
+}
+
+__device__ __forceinline__ void ring_push(const EventRing& R, int m, int packed) {
+    const int slot = m & (R.nslot - 1);
+    const int pos = atomicAdd(&R.count[slot], 1);
+    if (pos < R.cap) R.entry[static_cast<long long>(slot) * R.cap + pos] = packed;
+    else atomicOr(R.overflow, 1);
+}
+
+__global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    bool fire = false;
+    if (i < S.npre) {
+        const double vv = S.v[S.node[i]];
+        const double th = S.thr[i];
+        if (vv > th && !S.flag[i]) {           // presyn.cpp:140-157
+            fire = true;
+            S.flag[i] = 1;
+        } else if (vv <= th) {
+            S.flag[i] = 0;
+        }
+    }
+    // wave-level compaction of the spikes into the log
+    const unsigned long long ballot = __ballot(fire);
+    const int lane = __lane_id();
+    int base = 0;
+    if (ballot) {
+        if (lane == __ffsll(static_cast<long long>(ballot)) - 1)
+            base = atomicAdd(S.log_count, __popcll(ballot));
+        base = __shfl(base, __ffsll(static_cast<long long>(ballot)) - 1);
+    }
+    if (!fire) return;
+    const int pos = base + __popcll(ballot & ((1ull << lane) - 1ull));
+    if (pos < S.log_cap) {
+        S.log_t[pos] = S.t;
+        S.log_gid[pos] = S.gid[i];
+    }
+    for (int e = S.fo.begin[i]; e < S.fo.begin[i + 1]; ++e) {
+        const int m = delivery_step(S.ttab, S.k, S.kmax, S.t + S.fo.delay[e], S.half_dt);
+        ring_push(S.ring, m, S.fo.target[e]);
+    }
+}
+
+__global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
+    int cur = *I.cursor;
+    for (;;) {
+        const int idx = cur + static_cast<int>(threadIdx.x);
+        const bool take = idx < I.n && I.eff_time[idx] <= I.tcut;
+        const int cnt = __syncthreads_count(take);
+        if (take) {
+            const int s = I.inst[idx];
+            for (int e = I.fo.begin[s]; e < I.fo.begin[s + 1]; ++e) {
+                const int m = delivery_step(I.ttab, I.k, I.kmax, I.t + I.fo.delay[e], I.half_dt);
+                ring_push(I.ring, m, I.fo.target[e]);
+            }
+        }
+        cur += cnt;
+        if (cnt < static_cast<int>(blockDim.x)) break;
+    }
+    if (threadIdx.x == 0) *I.cursor = cur;
+}
+
+__global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
+    const int slot = D.k & (D.ring.nslot - 1);
+    int cnt = D.ring.count[slot];
+    if (cnt > D.ring.cap) cnt = D.ring.cap;
+    const long long off = static_cast<long long>(slot) * D.ring.cap;
+    for (int e = threadIdx.x; e < cnt; e += blockDim.x) {
+        const int packed = D.ring.entry[off + e];
+        const int type = packed >> 30;
+        const int inst = packed & 0x3fffffff;
+        if (type == 0) {                        // ExpSyn: g += w (expsyn.cpp net_receive)
+            atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
+        } else {                                // Exp2Syn: A,B += w * factor
+            const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
+            atomicAdd(&D.e2.col(E2_A)[inst], wf);
+            atomicAdd(&D.e2.col(E2_B)[inst], wf);
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) D.ring.count[slot] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// VecPlay continuous playback (vecplay.cu:19-111)
+// ---------------------------------------------------------------------------
+__global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    VecPlayDev it = items[i];
+    const double* tv = it.tvec;
+    const double* yv = it.yvec;
+    if (do_play) {
+        for (;;) {
+            if (it.done || it.next_time > t) break;
+            it.last_index = it.next_idx;
+            if (it.next_idx < it.len - 1) { it.next_idx++; it.next_time = tv[it.next_idx]; }
+            else it.done = 1;
+        }
+    }
+    double val;
+    if (t >= tv[it.next_idx]) {
+        it.last_index = it.next_idx;
+        if (it.last_index == 0) { val = yv[0]; goto store; }
+    } else if (t <= tv[0]) {
+        it.last_index = 0;
+        val = yv[0];
+        goto store;
+    } else {
+        while (t < tv[it.last_index]) --it.last_index;
+        while (t >= tv[it.last_index]) ++it.last_index;
+    }
+    {
+        const double x0 = yv[it.last_index - 1], x1 = yv[it.last_index];
+        const double t0 = tv[it.last_index - 1], t1 = tv[it.last_index];
+        if (t0 == t1) val = (x0 + x1) / 2.;
+        else val = x0 + (x1 - x0) * ((t - t0) / (t1 - t0));
+    }
+store:
+    *it.target = val;
+    items[i] = it;
+}
+
+__global__ void k_vecplay_reset(VecPlayDev* items, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    VecPlayDev it = items[i];
+    it.last_index = 0;
+    it.next_idx = 0;
+    it.done = 0;
+    if (it.len > 0) it.next_time = it.tvec[0];
+    else { it.next_time = 0.0; it.done = 1; }
+    items[i] = it;
+}
+
+__global__ void k_record(double* const* ptrs, int n, double* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = *ptrs[i];
+}
+
+__global__ void k_gap(const double* v, const int* src_node, double* vgap, const int* inst, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) vgap[inst[i]] = v[src_node[i]];
+}
+
+__global__ void k_clear_ints(int* p, long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+inline dim3 grid_for(long long n, int block = kBlock) {
+    return dim3(static_cast<unsigned>((n + block - 1) / block));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// launch wrappers
+// ---------------------------------------------------------------------------
+void launch_dense(const StepArgs& a, hipStream_t s) {
+    if (a.N <= 0) return;
+    hipLaunchKernelGGL(k_dense, grid_for(a.N), dim3(kBlock), 0, s, a);
+}
+
+void launch_sparse(int mech, const StepArgs& a, hipStream_t s) {
+    const int n = a.m[mech].n;
+    if (n <= 0) return;
+    switch (mech) {
+        case M_PAS: hipLaunchKernelGGL(k_sparse<M_PAS>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_NA_ION: hipLaunchKernelGGL(k_sparse<M_NA_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_K_ION: hipLaunchKernelGGL(k_sparse<M_K_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HH: hipLaunchKernelGGL(k_sparse<M_HH>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_CA_ION: hipLaunchKernelGGL(k_sparse<M_CA_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_CADYN: hipLaunchKernelGGL(k_sparse<M_CADYN>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_CAHVA: hipLaunchKernelGGL(k_sparse<M_CAHVA>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HDLA: hipLaunchKernelGGL(k_sparse<M_HDLA>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        default: break;
+    }
+}
+
+void launch_point_current(int mech, const StepArgs& a, hipStream_t s) {
+    const int n = a.m[mech].n;
+    if (n <= 0) return;
+    switch (mech) {
+        case M_ICLAMP: hipLaunchKernelGGL(k_point<M_ICLAMP>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_EXPSYN: hipLaunchKernelGGL(k_point<M_EXPSYN>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_EXP2SYN: hipLaunchKernelGGL(k_point<M_EXP2SYN>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HALFGAP: hipLaunchKernelGGL(k_point<M_HALFGAP>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        default: break;
+    }
+}
+
+void launch_point_state(int mech, const StepArgs& a, hipStream_t s) {
+    const int n = a.m[mech].n;
+    if (n <= 0) return;
+    if (mech == M_EXPSYN) hipLaunchKernelGGL(k_point_state<M_EXPSYN>, grid_for(n), dim3(kBlock), 0, s, a);
+    if (mech == M_EXP2SYN) hipLaunchKernelGGL(k_point_state<M_EXP2SYN>, grid_for(n), dim3(kBlock), 0, s, a);
+}
+
+void launch_init(int mech, const StepArgs& a, hipStream_t s) {
+    const int n = a.m[mech].n;
+    if (n <= 0) return;
+    switch (mech) {
+        case M_NA_ION: hipLaunchKernelGGL(k_init<M_NA_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_K_ION: hipLaunchKernelGGL(k_init<M_K_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_CA_ION: hipLaunchKernelGGL(k_init<M_CA_ION>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HH: hipLaunchKernelGGL(k_init<M_HH>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_CAHVA: hipLaunchKernelGGL(k_init<M_CAHVA>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HDLA: hipLaunchKernelGGL(k_init<M_HDLA>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_ICLAMP: hipLaunchKernelGGL(k_init<M_ICLAMP>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_HALFGAP: hipLaunchKernelGGL(k_init<M_HALFGAP>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_EXPSYN: hipLaunchKernelGGL(k_init<M_EXPSYN>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        case M_EXP2SYN: hipLaunchKernelGGL(k_init<M_EXP2SYN>, grid_for(n), dim3(kBlock), 0, s, a); break;
+        default: break;
+    }
+}
+
+void launch_set_v(double* v, int n, double val, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_set_v, grid_for(n), dim3(kBlock), 0, s, v, n, val);
+}
+
+void launch_solve(const SolveArgs& a, int max_slots, hipStream_t s) {
+    if (a.ncell <= 0) return;
+    const size_t lds = static_cast<size_t>(max_slots > 0 ? max_slots : 1) * 2 * sizeof(double);
+    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a);
+}
+
+void launch_spike(const SpikeArgs& a, hipStream_t s) {
+    if (a.npre > 0) hipLaunchKernelGGL(k_spike, grid_for(a.npre), dim3(kBlock), 0, s, a);
+}
+
+void launch_input(const InputArgs& a, hipStream_t s) {
+    if (a.n > 0) hipLaunchKernelGGL(k_input, dim3(1), dim3(kBlock), 0, s, a);
+}
+
+void launch_deliver(const DeliverArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_deliver, dim3(1), dim3(1024), 0, s, a);
+}
+
+void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_vecplay, grid_for(n, 64), dim3(64), 0, s, items, n, t, do_play);
+}
+
+void launch_vecplay_reset(VecPlayDev* items, int n, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_vecplay_reset, grid_for(n, 64), dim3(64), 0, s, items, n);
+}
+
+void launch_record(double* const* ptrs, int n, double* out, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_record, grid_for(n), dim3(kBlock), 0, s, ptrs, n, out);
+}
+
+void launch_gap(const double* v, const int* src_node, double* vgap_col, const int* halfgap_inst, int n,
+                hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_gap, grid_for(n), dim3(kBlock), 0, s, v, src_node, vgap_col, halfgap_inst, n);
+}
+
+void launch_clear_ints(int* p, long long n, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_clear_ints, grid_for(n), dim3(kBlock), 0, s, p, n);
+}
+
+}  // namespace hx

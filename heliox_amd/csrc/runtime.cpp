@@ -1,0 +1,1607 @@
+// Host runtime of the HIP simulation core: model storage, HBM layout, the
+// per-step launch pipeline and the C ABI declared in include/heliox.h.
+//
+// The step pipeline reproduces Simulate::fadvance (simulate.cpp:410-442,
+// simulate.cu:722-771).  Two schedules are used:
+//   fused:  step k launches the dense/sparse mechanism kernels with the state
+//           update of step k-1 folded in front of the current of step k, so a
+//           mechanism's state columns are read and written once per step;
+//   split:  the reference order (currents ... solve ... states) as separate
+//           passes.  Used when a VecPlay targets a density-mechanism variable,
+//           when a monitor samples an assigned variable, or when an
+//           ion-writing mechanism (CaDynamics_E2) is not on every node.
+// Both give the same values at every observable point (end of a run call,
+// every recorded sample).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <numeric>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/heliox.h"
+#include "hx_internal.h"
+#include "schedule.h"
+#include "solve_chunk.h"
+
+using namespace hx;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// mechanism registry (the reference's MechanismFactory, mechanism.h:125-164)
+// ---------------------------------------------------------------------------
+struct MechMeta {
+    const char* name;
+    int ncol;
+    int nparam;
+    int nstate;
+    std::vector<const char*> cols;
+    std::vector<double> dflt;
+    bool point;
+    bool ion;
+    bool artificial;
+    bool write_ion;     // WRITE_EION_IN_STATE (mech_template_utils.cuh:26-33)
+    int ion_use;        // bit0 na, bit1 k, bit2 ca
+    bool has_state;
+};
+
+const std::vector<MechMeta>& registry() {
+    static const std::vector<MechMeta> R = [] {
+        std::vector<MechMeta> r(M_COUNT);
+        r[M_PAS] = {"pas", PAS_NCOL, 2, 0, {"g_pas", "e_pas", "i"}, {0.00016666, -60, 0}, false, false, false, false, 0, false};
+        r[M_NA_ION] = {"na_ion", ION_NCOL, 3, 0, {"erev", "conci", "conco", "cur", "dcurdv"}, {0, 10.0, 140.0, 0, 0},
+                       false, true, false, false, 0, false};
+        r[M_K_ION] = {"k_ion", ION_NCOL, 3, 0, {"erev", "conci", "conco", "cur", "dcurdv"}, {0, 140.0, 4.0, 0, 0},
+                      false, true, false, false, 0, false};
+        r[M_HH] = {"hh", HH_NCOL, 4, 3,
+                   {"gnabar", "gkbar", "gl", "el", "m", "h", "n", "ena", "ek", "ina", "ik", "il", "gna", "gk", "minf",
+                    "hinf", "ninf", "mtau", "htau", "ntau"},
+                   {0.25, 0.036, 0.00016666, -60.0, 0, 0, 0, 50, -77, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0},
+                   false, false, false, false, 3, true};
+        r[M_ICLAMP] = {"IClamp", IC_NCOL, 3, 0, {"delay", "dur", "amp", "i"}, {0, 0, 0, 0}, true, false, false, false, 0,
+                       false};
+        r[M_EXPSYN] = {"ExpSyn", ES_NCOL, 2, 1, {"tau", "e", "g", "i"}, {0.1, 0, 0, 0}, true, false, false, false, 0, true};
+        r[M_EXP2SYN] = {"Exp2Syn", E2_NCOL, 3, 2, {"tau1", "tau2", "e", "A", "B", "factor", "g", "i"},
+                        {0.1, 10.0, 0, 0, 0, 0, 0, 0}, true, false, false, false, 0, true};
+        r[M_VECSTIM] = {"VecStim", 0, 0, 0, {}, {}, true, false, true, false, 0, false};
+        r[M_CA_ION] = {"ca_ion", ION_NCOL, 3, 0, {"erev", "conci", "conco", "cur", "dcurdv"}, {0, 5.e-5, 2.0, 0, 0},
+                       false, true, false, false, 0, false};
+        r[M_CADYN] = {"CaDynamics_E2", CD_NCOL, 4, 0, {"gamma", "decay", "depth", "minCai"}, {0.05, 80.0, 0.1, 1e-4},
+                      false, false, false, true, 4, true};
+        r[M_CAHVA] = {"Ca_HVA", CH_NCOL, 1, 2,
+                      {"gbar", "m", "h", "eca", "ica", "g", "i_mech", "mInf", "mTau", "mAlpha", "mBeta", "hInf", "hTau",
+                       "hAlpha", "hBeta"},
+                      {0.1, 0, 0, 140.0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, false, false, false, false, 4, true};
+        r[M_HALFGAP] = {"HalfGap", HG_NCOL, 2, 0, {"g", "vgap", "i"}, {0, 0, 0}, true, false, false, false, 0, false};
+        r[M_HDLA] = {"hd_la", HD_NCOL, 3, 1, {"ghdbar", "vhalfl", "tau", "l", "i", "linf", "taul", "ghd"},
+                     {0.0001, -81.0, 1.0, 0, 0, 0, 0, 0}, false, false, false, false, 0, true};
+        return r;
+    }();
+    return R;
+}
+
+int mech_id(const std::string& name) {
+    const auto& R = registry();
+    for (int i = 0; i < M_COUNT; ++i)
+        if (name == R[i].name) return i;
+    return -1;
+}
+
+int col_id(int mech, const std::string& var) {
+    const auto& m = registry()[mech];
+    for (int c = 0; c < m.ncol; ++c)
+        if (var == m.cols[c]) return c;
+    return -1;
+}
+
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define HXC(x)                                                                              \
+    do {                                                                                    \
+        hipError_t e_ = (x);                                                                \
+        if (e_ != hipSuccess)                                                               \
+            throw HipError(std::string(#x) + ": " + hipGetErrorString(e_));                 \
+    } while (0)
+
+template <class T>
+T* dalloc(std::vector<void*>& owned, size_t n) {
+    void* p = nullptr;
+    HXC(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)));
+    owned.push_back(p);
+    return static_cast<T*>(p);
+}
+
+template <class T>
+T* dupload(std::vector<void*>& owned, const std::vector<T>& h) {
+    T* p = dalloc<T>(owned, h.size());
+    if (!h.empty()) HXC(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    return p;
+}
+
+// ---------------------------------------------------------------------------
+// host model
+// ---------------------------------------------------------------------------
+struct HostMech {
+    bool present = false;
+    int n = 0;
+    std::vector<int> node;                     // user node per user instance
+    std::vector<std::vector<double>> col;      // user-order columns (load time)
+    std::vector<int> iontype;
+    // layout
+    std::vector<int> perm;                     // user instance -> device instance
+    std::vector<int> iperm;                    // device instance -> user instance
+    bool dense = false;
+    MechDev dev;
+};
+
+struct NetCon { int src_kind; int src; int mech; int inst; double weight; double delay; };
+
+struct VecPlayHost {
+    std::string mech, var;
+    int idx;
+    std::vector<double> tvec, yvec;
+    double* target = nullptr;
+    double* d_t = nullptr;
+    double* d_y = nullptr;
+};
+
+struct Ref { double* dev = nullptr; int klass = 0; };   // klass 0 param/state, 1 assigned
+
+struct Timer {
+    std::vector<hipEvent_t> pool;
+    std::vector<std::pair<int, int>> pending;   // (start, stop) indices into pool
+    size_t used = 0;
+    double ms = 0;
+    long long launches = 0;
+};
+
+const char* kTimerNames[] = {"mech", "sparse", "point", "solve", "spike", "events", "other"};
+enum TimerId { T_MECH = 0, T_SPARSE, T_POINT, T_SOLVE, T_SPIKE, T_EVENTS, T_OTHER, T_COUNT };
+
+}  // namespace
+
+struct hx_sim {
+    std::string err;
+    double dt = 0.025;
+    double celsius = 6.3;
+    // nodes (user order)
+    int ncell = 0, nnode = 0;
+    std::vector<int> parent;
+    std::vector<double> a, b, area, cm;
+    HostMech mech[M_COUNT];
+    std::map<std::string, double> globals[M_COUNT];
+    std::vector<int> pre_gid, pre_node;
+    std::vector<double> pre_thr;
+    std::vector<std::vector<double>> vecstim;
+    std::vector<NetCon> netcons;
+    std::vector<std::pair<int, int>> gaps;     // (src node, halfgap inst)
+    std::vector<VecPlayHost> vecplay;
+    int event_cap_request = 0;
+    int fusion_allowed = 1;
+    bool loaded = false;
+
+    // layout
+    std::vector<int> node_perm, node_iperm;    // user <-> solver order
+    std::vector<int> cell_node_begin, cell_round_begin, round_desc_begin;
+    std::vector<ChunkDesc> descs;
+    int max_slots = 0, max_rounds = 0;
+    unsigned dense_mask = 0;
+    bool fused = false;
+    bool write_assigned = false;
+    bool need_split_for_monitor = false;
+
+    // device
+    std::vector<void*> owned;
+    hipStream_t stream = nullptr;
+    double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
+           *d_area = nullptr;
+    int *d_cell_node_begin = nullptr, *d_cell_round_begin = nullptr, *d_round_desc_begin = nullptr;
+    ChunkDesc* d_desc = nullptr;
+    // spikes / events
+    int npre = 0;
+    int *d_pre_node = nullptr, *d_pre_flag = nullptr, *d_pre_gid = nullptr;
+    double* d_pre_thr = nullptr;
+    int *d_pre_fo_begin = nullptr, *d_pre_fo_target = nullptr;
+    double* d_pre_fo_delay = nullptr;
+    int *d_vs_fo_begin = nullptr, *d_vs_fo_target = nullptr;
+    double* d_vs_fo_delay = nullptr;
+    double *d_es_weight = nullptr, *d_e2_weight = nullptr;
+    EventRing ring{};
+    double max_delay = 0;
+    double* d_spk_t = nullptr;
+    int* d_spk_gid = nullptr;
+    int* d_spk_count = nullptr;
+    int spk_cap = 0;
+    double* d_in_time = nullptr;
+    int* d_in_inst = nullptr;
+    int* d_in_cursor = nullptr;
+    int n_in = 0;
+    bool inputs_dirty = true;
+    // time table
+    std::vector<double> ttab;
+    double* d_ttab = nullptr;
+    int ttab_cap = 0;
+    // gap
+    int* d_gap_src = nullptr;
+    int* d_gap_inst = nullptr;
+    // vecplay
+    VecPlayDev* d_vecplay = nullptr;
+    std::vector<std::tuple<std::string, std::string, int>> vecplay_keys;
+    bool vecplay_dirty = true;
+    // recorder
+    std::vector<std::pair<std::string, std::string>> mon_name;
+    std::vector<int> mon_idx;
+    std::vector<Ref> mon_ref;
+    std::vector<std::vector<double>> mon_data;
+    double** d_mon_ptr = nullptr;
+    double* d_mon_buf = nullptr;
+    long long mon_buf_cap = 0;     // samples
+    long long mon_buf_fill = 0;
+    bool mon_dirty = true;
+    // handles
+    std::vector<Ref> handles;
+    // spike output (host)
+    std::vector<std::pair<double, int>> spikes;
+    std::unordered_map<int, std::vector<double>> spk_by_gid;
+    // time stepping
+    double t = 0.0;
+    int k = 0;                       // step index since finitialize
+    bool state_pending = false;
+    bool initialized = false;
+    // profiling
+    bool profiling = false;
+    Timer timers[T_COUNT];
+
+    ~hx_sim() {
+        for (auto& tm : timers)
+            for (auto e : tm.pool) (void)hipEventDestroy(e);
+        for (void* p : owned) (void)hipFree(p);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    int fail(const char* fmt, ...) {
+        char buf[1024];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        err = buf;
+        return -1;
+    }
+
+    // ------------------------------------------------------------ timing
+    void tbegin(int id) {
+        if (!profiling) return;
+        Timer& tm = timers[id];
+        while (tm.pool.size() < tm.used + 2) {
+            hipEvent_t e;
+            HXC(hipEventCreate(&e));
+            tm.pool.push_back(e);
+        }
+        HXC(hipEventRecord(tm.pool[tm.used], stream));
+        tm.pending.push_back({static_cast<int>(tm.used), static_cast<int>(tm.used + 1)});
+        tm.used += 2;
+    }
+    void tend(int id) {
+        if (!profiling) return;
+        Timer& tm = timers[id];
+        HXC(hipEventRecord(tm.pool[tm.pending.back().second], stream));
+    }
+    void tcollect() {
+        for (auto& tm : timers) {
+            for (auto& pr : tm.pending) {
+                float ms = 0;
+                HXC(hipEventElapsedTime(&ms, tm.pool[pr.first], tm.pool[pr.second]));
+                tm.ms += ms;
+                tm.launches++;
+            }
+            tm.pending.clear();
+            tm.used = 0;
+        }
+    }
+
+    // ------------------------------------------------------------ layout
+    void build_layout();
+    void recompute_fused();
+    void upload();
+    void upload_inputs();
+    void upload_vecplay();
+    void upload_monitors();
+    void ensure_ttab(int kneed);
+    Ref resolve(const std::string& mechname, const std::string& var, int idx);
+    StepArgs step_args(double tcur, int do_state, int do_current) const;
+    // ------------------------------------------------------------ stepping
+    void launch_mech_pass(int do_state, int do_current, double tcur);
+    void launch_point_currents(double tcur);
+    void launch_events(int kk, double tk);
+    void launch_detect(int kk, double tk);
+    void launch_record();
+    void step_once();
+    void finish_pending();
+    int run_steps(int nstep);
+    void sync_outputs();
+    void finitialize(double v_init);
+};
+
+// ===========================================================================
+// layout
+// ===========================================================================
+void hx_sim::build_layout() {
+    const auto& R = registry();
+    // per-cell node lists (user order, increasing)
+    std::vector<int> cell_of(nnode);
+    for (int i = 0; i < ncell; ++i) cell_of[i] = i;
+    for (int i = ncell; i < nnode; ++i) cell_of[i] = cell_of[parent[i]];
+    std::vector<int> cnt(ncell, 0);
+    for (int i = 0; i < nnode; ++i) cnt[cell_of[i]]++;
+    std::vector<int> cbeg(ncell + 1, 0);
+    for (int c = 0; c < ncell; ++c) cbeg[c + 1] = cbeg[c] + cnt[c];
+    std::vector<int> cnodes(nnode), fill(cbeg.begin(), cbeg.end() - 1);
+    for (int i = 0; i < nnode; ++i) cnodes[fill[cell_of[i]]++] = i;   // increasing user index per cell
+    std::vector<int> local(nnode);
+    node_perm.assign(nnode, -1);
+    node_iperm.assign(nnode, -1);
+    cell_node_begin.assign(ncell + 1, 0);
+    cell_round_begin.assign(ncell + 1, 0);
+    round_desc_begin.assign(1, 0);
+    descs.clear();
+    max_slots = 0;
+    max_rounds = 0;
+    int pos = 0;
+    for (int c = 0; c < ncell; ++c) {
+        const int n = cnt[c];
+        std::vector<int> lp(n);
+        for (int j = 0; j < n; ++j) local[cnodes[cbeg[c] + j]] = j;
+        for (int j = 0; j < n; ++j) {
+            const int u = cnodes[cbeg[c] + j];
+            lp[j] = (j == 0) ? -1 : local[parent[u]];
+        }
+        CellSchedule cs;
+        build_cell_schedule(lp, kChunk, kWave, cs);
+        cell_node_begin[c] = pos;
+        for (int s = 0; s < n; ++s) {
+            const int u = cnodes[cbeg[c] + cs.order[s]];
+            node_perm[u] = pos + s;
+            node_iperm[pos + s] = u;
+        }
+        pos += n;
+        cell_round_begin[c] = static_cast<int>(round_desc_begin.size()) - 1;
+        const int dbase = static_cast<int>(descs.size());
+        for (auto& d : cs.desc) descs.push_back(d);
+        for (int r = 1; r <= cs.nround; ++r) round_desc_begin.push_back(dbase + cs.round_begin[r]);
+        max_slots = std::max(max_slots, cs.nchunk);
+        max_rounds = std::max(max_rounds, cs.nround);
+    }
+    cell_node_begin[ncell] = pos;
+    cell_round_begin[ncell] = static_cast<int>(round_desc_begin.size()) - 1;
+
+    // mechanism instance order: by solver-order node (stable)
+    for (int id = 0; id < M_COUNT; ++id) {
+        HostMech& m = mech[id];
+        if (!m.present) continue;
+        std::vector<int> idx(m.n);
+        std::iota(idx.begin(), idx.end(), 0);
+        std::stable_sort(idx.begin(), idx.end(), [&](int x, int y) { return node_perm[m.node[x]] < node_perm[m.node[y]]; });
+        m.iperm = idx;
+        m.perm.assign(m.n, 0);
+        for (int j = 0; j < m.n; ++j) m.perm[idx[j]] = j;
+        m.dense = false;
+        if (!R[id].point && !R[id].artificial && m.n == nnode) {
+            bool ok = true;
+            for (int j = 0; j < m.n && ok; ++j) ok = node_perm[m.node[idx[j]]] == j;
+            m.dense = ok;
+        }
+    }
+    // a mechanism that reads an ion can be fused only if the ion is dense too
+    dense_mask = 0;
+    for (int id = 0; id < M_COUNT; ++id) {
+        HostMech& m = mech[id];
+        if (!m.present || !m.dense) continue;
+        int use = R[id].ion_use;
+        bool ok = true;
+        if ((use & 1) && !mech[M_NA_ION].dense) ok = false;
+        if ((use & 2) && !mech[M_K_ION].dense) ok = false;
+        if ((use & 4) && !mech[M_CA_ION].dense) ok = false;
+        if (ok) dense_mask |= 1u << id;
+        else m.dense = false;
+    }
+    recompute_fused();
+}
+
+// Fusing the state update of step k-1 into the current pass of step k is exact
+// unless something observes or changes density-mechanism values between the two.
+void hx_sim::recompute_fused() {
+    const auto& R = registry();
+    bool fuse = fusion_allowed != 0;
+    if (mech[M_CADYN].present && !(dense_mask & (1u << M_CADYN))) fuse = false;
+    for (auto& vp : vecplay) {
+        int id = mech_id(vp.mech);
+        if (id >= 0 && !R[id].point) fuse = false;
+        if (id < 0) fuse = false;   // node / capacitance variables
+    }
+    if (need_split_for_monitor) fuse = false;
+    fused = fuse;
+}
+
+void hx_sim::upload() {
+    const auto& R = registry();
+    if (!stream) HXC(hipStreamCreate(&stream));
+    auto perm_nodes = [&](const std::vector<double>& u) {
+        std::vector<double> g(nnode);
+        for (int i = 0; i < nnode; ++i) g[node_perm[i]] = u[i];
+        return g;
+    };
+    d_v = dalloc<double>(owned, nnode);
+    d_d = dalloc<double>(owned, nnode);
+    d_rhs = dalloc<double>(owned, nnode);
+    HXC(hipMemset(d_v, 0, sizeof(double) * nnode));
+    HXC(hipMemset(d_d, 0, sizeof(double) * nnode));
+    HXC(hipMemset(d_rhs, 0, sizeof(double) * nnode));
+    d_a = dupload(owned, perm_nodes(a));
+    d_b = dupload(owned, perm_nodes(b));
+    d_cm = dupload(owned, perm_nodes(cm));
+    d_area = dupload(owned, perm_nodes(area));
+    d_cell_node_begin = dupload(owned, cell_node_begin);
+    d_cell_round_begin = dupload(owned, cell_round_begin);
+    d_round_desc_begin = dupload(owned, round_desc_begin);
+    d_desc = dupload(owned, descs);
+    {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        HXC(hipGetDevice(&dev));
+        HXC(hipGetDeviceProperties(&prop, dev));
+        const size_t lds = static_cast<size_t>(std::max(max_slots, 1)) * 2 * sizeof(double);
+        if (lds > prop.sharedMemPerBlock)
+            throw std::runtime_error("a cell has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
+                                     " B of junction slots exceed the " + std::to_string(prop.sharedMemPerBlock) +
+                                     " B of LDS per workgroup");
+    }
+
+    // ion node -> device instance maps
+    std::vector<int> ion_at[3];
+    const int ion_ids[3] = {M_NA_ION, M_K_ION, M_CA_ION};
+    for (int x = 0; x < 3; ++x) {
+        ion_at[x].assign(nnode, -1);
+        HostMech& im = mech[ion_ids[x]];
+        if (!im.present) continue;
+        for (int j = 0; j < im.n; ++j) ion_at[x][node_perm[im.node[im.iperm[j]]]] = j;
+    }
+    for (int id = 0; id < M_COUNT; ++id) {
+        HostMech& m = mech[id];
+        MechDev& d = m.dev;
+        d = MechDev();
+        if (!m.present) continue;
+        d.n = m.n;
+        d.dense = m.dense ? 1 : 0;
+        const int ncol = R[id].ncol;
+        d.stride = ((m.n + 63) / 64) * 64;
+        if (ncol > 0) {
+            std::vector<double> blk(static_cast<size_t>(ncol) * d.stride, 0.0);
+            for (int c = 0; c < ncol; ++c)
+                for (int j = 0; j < m.n; ++j) blk[c * d.stride + j] = m.col[c][m.iperm[j]];
+            d.base = dupload(owned, blk);
+        }
+        std::vector<int> nodes(m.n);
+        for (int j = 0; j < m.n; ++j) nodes[j] = node_perm[m.node[m.iperm[j]]];
+        d.node = dupload(owned, nodes);
+        if (R[id].ion) {
+            std::vector<int> it(m.n);
+            for (int j = 0; j < m.n; ++j) it[j] = m.iontype[m.iperm[j]];
+            d.iontype = dupload(owned, it);
+        }
+        for (int x = 0; x < 3; ++x) {
+            if (!(R[id].ion_use & (1 << x))) continue;
+            std::vector<int> map(m.n);
+            bool ident = true;
+            for (int j = 0; j < m.n; ++j) {
+                map[j] = ion_at[x][nodes[j]];
+                if (map[j] < 0)
+                    throw std::runtime_error(std::string(R[id].name) + " instance without " + R[ion_ids[x]].name +
+                                             " at its node");
+                ident = ident && map[j] == j;
+            }
+            if (!ident) d.ion[x] = dupload(owned, map);
+        }
+    }
+
+    // spike detectors
+    npre = static_cast<int>(pre_node.size());
+    std::vector<int> pn(npre);
+    for (int i = 0; i < npre; ++i) pn[i] = node_perm[pre_node[i]];
+    d_pre_node = dupload(owned, pn);
+    d_pre_thr = dupload(owned, pre_thr);
+    d_pre_gid = dupload(owned, pre_gid);
+    d_pre_flag = dalloc<int>(owned, npre);
+    HXC(hipMemset(d_pre_flag, 0, sizeof(int) * std::max(npre, 1)));
+
+    // netcons: the last one per synapse instance wins (coredat_to_innerdat.cpp:356-364)
+    std::map<std::pair<int, int>, NetCon> by_syn;
+    for (auto& nc : netcons) by_syn[{nc.mech, nc.inst}] = nc;
+    const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
+    std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs);
+    std::vector<double> esw(mech[M_EXPSYN].present ? mech[M_EXPSYN].n : 0, 0.0);
+    std::vector<double> e2w(mech[M_EXP2SYN].present ? mech[M_EXP2SYN].n : 0, 0.0);
+    max_delay = 0;
+    for (auto& kv : by_syn) {
+        const NetCon& nc = kv.second;
+        const int dinst = mech[nc.mech].perm[nc.inst];
+        const int packed = ((nc.mech == M_EXP2SYN ? 1 : 0) << 30) | dinst;
+        if (nc.mech == M_EXPSYN) esw[dinst] = nc.weight;
+        else e2w[dinst] = nc.weight;
+        if (nc.src_kind == 0) pre_fo[nc.src].push_back({packed, nc.delay});
+        else vs_fo[nc.src].push_back({packed, nc.delay});
+        max_delay = std::max(max_delay, nc.delay);
+    }
+    auto csr = [&](const std::vector<std::vector<std::pair<int, double>>>& fo, int*& beg, int*& tgt, double*& dl) {
+        std::vector<int> b(fo.size() + 1, 0), tg;
+        std::vector<double> de;
+        for (size_t i = 0; i < fo.size(); ++i) {
+            for (auto& pr : fo[i]) { tg.push_back(pr.first); de.push_back(pr.second); }
+            b[i + 1] = static_cast<int>(tg.size());
+        }
+        beg = dupload(owned, b);
+        tgt = dupload(owned, tg);
+        dl = dupload(owned, de);
+        return static_cast<long long>(tg.size());
+    };
+    long long ntgt = csr(pre_fo, d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay);
+    ntgt += csr(vs_fo, d_vs_fo_begin, d_vs_fo_target, d_vs_fo_delay);
+    d_es_weight = dupload(owned, esw);
+    d_e2_weight = dupload(owned, e2w);
+
+    // event ring: one slot per step, enough slots to cover the longest delay
+    int steps = static_cast<int>(std::ceil(max_delay / dt)) + 4;
+    int nslot = 8;
+    while (nslot < steps) nslot <<= 1;
+    long long cap = event_cap_request > 0 ? event_cap_request : std::max<long long>(4096, std::min<long long>(ntgt, 1 << 20));
+    ring.nslot = nslot;
+    ring.cap = static_cast<int>(cap);
+    ring.count = dalloc<int>(owned, nslot);
+    ring.entry = dalloc<int>(owned, static_cast<size_t>(nslot) * cap);
+    ring.overflow = dalloc<int>(owned, 1);
+    HXC(hipMemset(ring.count, 0, sizeof(int) * nslot));
+    HXC(hipMemset(ring.overflow, 0, sizeof(int)));
+
+    spk_cap = std::max(1 << 20, npre * 64);
+    d_spk_t = dalloc<double>(owned, spk_cap);
+    d_spk_gid = dalloc<int>(owned, spk_cap);
+    d_spk_count = dalloc<int>(owned, 1);
+    HXC(hipMemset(d_spk_count, 0, sizeof(int)));
+    d_in_cursor = dalloc<int>(owned, 1);
+
+    // gap transfers
+    std::vector<int> gs, gi;
+    for (auto& g : gaps) { gs.push_back(node_perm[g.first]); gi.push_back(mech[M_HALFGAP].perm[g.second]); }
+    d_gap_src = dupload(owned, gs);
+    d_gap_inst = dupload(owned, gi);
+
+    inputs_dirty = true;
+    vecplay_dirty = true;
+    mon_dirty = true;
+    ttab_cap = 0;
+}
+
+// VecStim trains -> globally sorted effective event times.  A train element is
+// processed at the first step whose window t+dt/2 reaches it, but never before
+// the previous element of the same train (vecevent.cpp:172-199 chains the
+// self-events), hence the running maximum.
+void hx_sim::upload_inputs() {
+    std::vector<std::pair<double, int>> ev;
+    const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
+    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) {
+        double run_max = -INFINITY;
+        for (double e : vecstim[s]) {
+            run_max = std::max(run_max, e);
+            ev.push_back({run_max, s});
+        }
+    }
+    std::stable_sort(ev.begin(), ev.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    std::vector<double> tt(ev.size());
+    std::vector<int> ii(ev.size());
+    for (size_t i = 0; i < ev.size(); ++i) { tt[i] = ev[i].first; ii[i] = ev[i].second; }
+    n_in = static_cast<int>(ev.size());
+    d_in_time = dupload(owned, tt);
+    d_in_inst = dupload(owned, ii);
+    inputs_dirty = false;
+}
+
+void hx_sim::upload_vecplay() {
+    // keep the playback position of items that were already on the device
+    std::map<std::tuple<std::string, std::string, int>, VecPlayDev> prev;
+    if (d_vecplay && !vecplay_keys.empty()) {
+        std::vector<VecPlayDev> old(vecplay_keys.size());
+        HXC(hipMemcpy(old.data(), d_vecplay, sizeof(VecPlayDev) * old.size(), hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < old.size(); ++i) prev[vecplay_keys[i]] = old[i];
+    }
+    std::vector<VecPlayDev> items;
+    vecplay_keys.clear();
+    for (auto& vp : vecplay) {
+        if (!vp.d_t) {
+            vp.d_t = dupload(owned, vp.tvec);
+            vp.d_y = dupload(owned, vp.yvec);
+        }
+        VecPlayDev it{};
+        it.target = vp.target;
+        it.tvec = vp.d_t;
+        it.yvec = vp.d_y;
+        it.len = static_cast<int>(vp.tvec.size());
+        it.next_time = vp.tvec.empty() ? 0.0 : vp.tvec[0];
+        auto key = std::make_tuple(vp.mech, vp.var, vp.idx);
+        auto pv = prev.find(key);
+        if (pv != prev.end() && pv->second.tvec == it.tvec && pv->second.len == it.len) {
+            it.last_index = pv->second.last_index;
+            it.next_idx = pv->second.next_idx;
+            it.done = pv->second.done;
+            it.next_time = pv->second.next_time;
+        }
+        vecplay_keys.push_back(key);
+        items.push_back(it);
+    }
+    d_vecplay = dupload(owned, items);
+    vecplay_dirty = false;
+}
+
+void hx_sim::upload_monitors() {
+    std::vector<double*> ptrs;
+    for (auto& r : mon_ref) ptrs.push_back(r.dev);
+    d_mon_ptr = dupload(owned, ptrs);
+    mon_dirty = false;
+}
+
+// t of every step since finitialize, accumulated exactly as Simulate::fadvance
+// does (t += 0.5*dt twice, simulate.cpp:417,774).
+void hx_sim::ensure_ttab(int kneed) {
+    const int margin = static_cast<int>(std::ceil(max_delay / dt)) + 8;
+    const int want = kneed + margin;
+    if (static_cast<int>(ttab.size()) < want + 1) {
+        if (ttab.empty()) ttab.push_back(0.0);
+        while (static_cast<int>(ttab.size()) < want + 1) {
+            double x = ttab.back();
+            x += 0.5 * dt;
+            x += 0.5 * dt;
+            ttab.push_back(x);
+        }
+    }
+    if (ttab_cap < static_cast<int>(ttab.size())) {
+        ttab_cap = static_cast<int>(ttab.size()) * 2;
+        d_ttab = dalloc<double>(owned, ttab_cap);
+        HXC(hipMemcpy(d_ttab, ttab.data(), sizeof(double) * ttab.size(), hipMemcpyHostToDevice));
+    } else {
+        HXC(hipMemcpy(d_ttab, ttab.data(), sizeof(double) * ttab.size(), hipMemcpyHostToDevice));
+    }
+}
+
+Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
+    Ref r;
+    if (mn == "global" || mn == "node") {
+        if (idx < 0 || idx >= nnode) return r;
+        const int g = node_perm[idx];
+        if (var == "v") r.dev = d_v + g;
+        else if (var == "d") { r.dev = d_d + g; r.klass = 1; }
+        else if (var == "rhs") { r.dev = d_rhs + g; r.klass = 1; }
+        else if (var == "a") r.dev = d_a + g;
+        else if (var == "b") r.dev = d_b + g;
+        else if (var == "area") r.dev = d_area + g;
+        return r;
+    }
+    if (mn == "capacitance") {
+        if (idx < 0 || idx >= nnode || var != "cm") return r;
+        r.dev = d_cm + node_perm[idx];
+        return r;
+    }
+    int id = mech_id(mn);
+    if (id < 0 || !mech[id].present) return r;
+    const auto& M = registry()[id];
+    HostMech& m = mech[id];
+    if (M.ion) {
+        if (idx < 0 || idx >= nnode) return r;
+        const int g = node_perm[idx];
+        int inst = -1;
+        for (int j = 0; j < m.n; ++j)
+            if (node_perm[m.node[m.iperm[j]]] == g) { inst = j; break; }
+        const int c = col_id(id, var);
+        if (inst < 0 || c < 0) return r;
+        r.dev = m.dev.col(c) + inst;
+        r.klass = (c == ION_CONCI || c == ION_CONCO) ? 0 : 1;
+        return r;
+    }
+    if (id == M_CADYN && (var == "cai" || var == "ica")) {
+        // CaDynamics_E2 keeps cai / ica in the ca_ion columns of its node
+        if (idx < 0 || idx >= m.n) return r;
+        return resolve("ca_ion", var == "cai" ? "conci" : "cur", m.node[idx]);
+    }
+    const int c = col_id(id, var);
+    if (c < 0 || idx < 0 || idx >= m.n) return r;
+    r.dev = m.dev.col(c) + m.perm[idx];
+    r.klass = c >= M.nparam + M.nstate ? 1 : 0;
+    if (id == M_EXP2SYN && c == E2_FACTOR) r.klass = 0;   // written by INITIAL
+    if (id == M_HALFGAP && c == HG_VGAP) r.klass = 0;     // written by the gap transfer
+    return r;
+}
+
+StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
+    StepArgs A{};
+    A.N = nnode;
+    A.v = d_v;
+    A.d = d_d;
+    A.rhs = d_rhs;
+    A.area = d_area;
+    for (int id = 0; id < M_COUNT; ++id) A.m[id] = mech[id].dev;
+    A.dense_mask = dense_mask;
+    A.do_state = do_state;
+    A.do_current = do_current;
+    A.write_assigned = write_assigned ? 1 : 0;
+    A.t = tcur;
+    A.dt = dt;
+    auto G = [&](int id, const char* k, double dflt) {
+        auto it = globals[id].find(k);
+        return it == globals[id].end() ? dflt : it->second;
+    };
+    const double hh_cel = G(M_HH, "celsius", celsius);
+    A.c.hh_q10 = std::pow(3.0, (hh_cel - 6.3) / 10);
+    const double hd_cel = G(M_HDLA, "celsius", celsius);
+    A.c.hd_qt = std::pow(G(M_HDLA, "q10", 4.5), ((hd_cel - 33.0) / 10.0));
+    A.c.hd_ehd = G(M_HDLA, "ehd", -30.0);
+    A.c.hd_kl = G(M_HDLA, "kl", -8.0);
+    A.c.hd_vhalft = G(M_HDLA, "vhalft", -75.0);
+    A.c.hd_a0t = G(M_HDLA, "a0t", 0.011);
+    A.c.hd_zetat = G(M_HDLA, "zetat", 2.2);
+    A.c.hd_gmt = G(M_HDLA, "gmt", 0.4);
+    A.c.hd_qtl = G(M_HDLA, "qtl", 1.0);
+    const double R = 1.380649e-23 * 6.02214076e+23, F = 1.602176634e-19 * 6.02214076e+23;
+    A.c.ktf = 1000. * R * (celsius + 273.15) / F;
+    return A;
+}
+
+// ===========================================================================
+// stepping
+// ===========================================================================
+static const int kSparseOrder[] = {M_PAS, M_NA_ION, M_K_ION, M_HH, M_CA_ION, M_CADYN, M_CAHVA, M_HDLA};
+
+void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur) {
+    StepArgs A = step_args(tcur, do_state, do_current);
+    tbegin(T_MECH);
+    if (do_current) {
+        launch_dense(A, stream);
+    } else if (dense_mask) {
+        launch_dense(A, stream);
+    }
+    tend(T_MECH);
+    bool any_sparse = false;
+    for (int id : kSparseOrder) any_sparse |= mech[id].present && !(dense_mask & (1u << id));
+    if (!any_sparse) return;
+    tbegin(T_SPARSE);
+    if (do_state && !do_current) {
+        // ion writers first (simulate.cpp:822-834)
+        if (mech[M_CADYN].present && !(dense_mask & (1u << M_CADYN))) launch_sparse(M_CADYN, A, stream);
+        for (int id : kSparseOrder)
+            if (id != M_CADYN && mech[id].present && !(dense_mask & (1u << id))) launch_sparse(id, A, stream);
+    } else {
+        for (int id : kSparseOrder)
+            if (mech[id].present && !(dense_mask & (1u << id))) launch_sparse(id, A, stream);
+    }
+    tend(T_SPARSE);
+}
+
+void hx_sim::launch_point_currents(double tcur) {
+    StepArgs A = step_args(tcur, 0, 1);
+    const int pts[] = {M_ICLAMP, M_EXPSYN, M_EXP2SYN, M_HALFGAP};   // CoreNEURON order
+    bool any = false;
+    for (int id : pts) any |= mech[id].present && mech[id].n > 0;
+    if (!any) return;
+    tbegin(T_POINT);
+    for (int id : pts)
+        if (mech[id].present) launch_point_current(id, A, stream);
+    tend(T_POINT);
+}
+
+void hx_sim::launch_events(int kk, double tk) {
+    if (!(mech[M_EXPSYN].present || mech[M_EXP2SYN].present)) return;
+    tbegin(T_EVENTS);
+    if (n_in > 0) {
+        InputArgs I{};
+        I.eff_time = d_in_time;
+        I.inst = d_in_inst;
+        I.n = n_in;
+        I.cursor = d_in_cursor;
+        I.tcut = tk + dt / 2;
+        I.t = tk;
+        I.k = kk;
+        I.fo = FanOut{d_vs_fo_begin, d_vs_fo_target, d_vs_fo_delay};
+        I.ring = ring;
+        I.ttab = d_ttab;
+        I.kmax = static_cast<int>(ttab.size()) - 1;
+        I.half_dt = dt / 2;
+        launch_input(I, stream);
+    }
+    DeliverArgs D{};
+    D.ring = ring;
+    D.k = kk;
+    D.es = mech[M_EXPSYN].dev;
+    D.e2 = mech[M_EXP2SYN].dev;
+    D.es_weight = d_es_weight;
+    D.e2_weight = d_e2_weight;
+    launch_deliver(D, stream);
+    tend(T_EVENTS);
+}
+
+void hx_sim::launch_detect(int kk, double tk) {
+    if (npre == 0) return;
+    tbegin(T_SPIKE);
+    SpikeArgs S{};
+    S.npre = npre;
+    S.v = d_v;
+    S.node = d_pre_node;
+    S.thr = d_pre_thr;
+    S.flag = d_pre_flag;
+    S.gid = d_pre_gid;
+    S.t = tk;
+    S.k = kk;
+    S.log_t = d_spk_t;
+    S.log_gid = d_spk_gid;
+    S.log_count = d_spk_count;
+    S.log_cap = spk_cap;
+    S.fo = FanOut{d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay};
+    S.ring = ring;
+    S.ttab = d_ttab;
+    S.kmax = static_cast<int>(ttab.size()) - 1;
+    S.half_dt = dt / 2;
+    launch_spike(S, stream);
+    tend(T_SPIKE);
+}
+
+void hx_sim::launch_record() {
+    if (mon_ref.empty()) return;
+    if (mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    tbegin(T_OTHER);
+    hx::launch_record(d_mon_ptr, static_cast<int>(mon_ref.size()), d_mon_buf + mon_buf_fill * mon_ref.size(), stream);
+    tend(T_OTHER);
+    mon_buf_fill++;
+}
+
+// One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
+// have been detected (end of the previous step or finitialize).
+void hx_sim::step_once() {
+    const double tk = t;
+    const double tmid = tk + 0.5 * dt;
+    const bool has_vp = !vecplay.empty();
+    const int nvp = static_cast<int>(vecplay.size());
+    if (fused) {
+        launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
+        if (state_pending) launch_record();
+        launch_events(k, tk);
+        if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+    } else {
+        launch_events(k, tk);
+        if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        launch_mech_pass(0, 1, tmid);
+    }
+    launch_point_currents(tmid);
+    SolveArgs S{};
+    S.ncell = ncell;
+    S.cell_node_begin = d_cell_node_begin;
+    S.cell_round_begin = d_cell_round_begin;
+    S.round_desc_begin = d_round_desc_begin;
+    S.desc = d_desc;
+    S.v = d_v;
+    S.d = d_d;
+    S.rhs = d_rhs;
+    S.a = d_a;
+    S.b = d_b;
+    S.cm = d_cm;
+    S.cfac = 0.001 * (1.0 / dt);
+    tbegin(T_SOLVE);
+    launch_solve(S, max_slots, stream);
+    tend(T_SOLVE);
+    if (!gaps.empty()) {
+        tbegin(T_OTHER);
+        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
+        tend(T_OTHER);
+    }
+    // t += dt/2 twice, exactly as the reference accumulates it
+    double tn = tk;
+    tn += 0.5 * dt;
+    tn += 0.5 * dt;
+    t = tn;
+    k += 1;
+    launch_detect(k, t);              // spike_deliver of the next step detects on v_{k}
+    if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, t, 0, stream); tend(T_OTHER); }
+    StepArgs A = step_args(t, 1, 0);
+    if (mech[M_EXPSYN].present || mech[M_EXP2SYN].present) {
+        tbegin(T_POINT);
+        launch_point_state(M_EXPSYN, A, stream);
+        launch_point_state(M_EXP2SYN, A, stream);
+        tend(T_POINT);
+    }
+    if (fused) {
+        state_pending = true;
+    } else {
+        launch_mech_pass(1, 0, t);
+        launch_record();
+    }
+}
+
+void hx_sim::finish_pending() {
+    if (!state_pending) return;
+    launch_mech_pass(1, 0, t);
+    launch_record();
+    state_pending = false;
+}
+
+void hx_sim::sync_outputs() {
+    HXC(hipStreamSynchronize(stream));
+    if (profiling) tcollect();
+    int ov = 0;
+    HXC(hipMemcpy(&ov, ring.overflow, sizeof(int), hipMemcpyDeviceToHost));
+    if (ov) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
+    int ns = 0;
+    HXC(hipMemcpy(&ns, d_spk_count, sizeof(int), hipMemcpyDeviceToHost));
+    if (ns > spk_cap) throw std::runtime_error("spike log overflow");
+    if (ns > 0) {
+        std::vector<double> st(ns);
+        std::vector<int> sg(ns);
+        HXC(hipMemcpy(st.data(), d_spk_t, sizeof(double) * ns, hipMemcpyDeviceToHost));
+        HXC(hipMemcpy(sg.data(), d_spk_gid, sizeof(int) * ns, hipMemcpyDeviceToHost));
+        for (int i = 0; i < ns; ++i) {
+            spikes.push_back({st[i], sg[i]});
+            spk_by_gid[sg[i]].push_back(st[i]);
+        }
+        HXC(hipMemset(d_spk_count, 0, sizeof(int)));
+    }
+    if (!mon_ref.empty() && mon_buf_fill > 0) {
+        const size_t nm = mon_ref.size();
+        std::vector<double> buf(static_cast<size_t>(mon_buf_fill) * nm);
+        HXC(hipMemcpy(buf.data(), d_mon_buf, sizeof(double) * buf.size(), hipMemcpyDeviceToHost));
+        for (long long s = 0; s < mon_buf_fill; ++s)
+            for (size_t i = 0; i < nm; ++i) mon_data[i].push_back(buf[s * nm + i]);
+        mon_buf_fill = 0;
+    }
+}
+
+int hx_sim::run_steps(int nstep) {
+    if (!initialized) throw std::runtime_error("finitialize must be called before stepping");
+    ensure_ttab(k + nstep + 1);
+    if (mon_dirty) upload_monitors();
+    if (vecplay_dirty) upload_vecplay();
+    if (!mon_ref.empty() && mon_buf_cap < nstep + 2) {
+        mon_buf_cap = nstep + 2;
+        d_mon_buf = dalloc<double>(owned, static_cast<size_t>(mon_buf_cap) * mon_ref.size());
+        mon_buf_fill = 0;
+    }
+    for (int s = 0; s < nstep; ++s) step_once();
+    finish_pending();
+    sync_outputs();
+    return 0;
+}
+
+// Simulate::finitialize (simulate.cpp:106-141, 271-339)
+void hx_sim::finitialize(double v_init) {
+    if (inputs_dirty) upload_inputs();
+    if (vecplay_dirty) upload_vecplay();
+    if (mon_dirty) upload_monitors();
+    t = 0.0;
+    k = 0;
+    state_pending = false;
+    ensure_ttab(1);
+    if (!mon_ref.empty() && mon_buf_cap < 2) {
+        mon_buf_cap = 2;
+        d_mon_buf = dalloc<double>(owned, static_cast<size_t>(mon_buf_cap) * mon_ref.size());
+    }
+    mon_buf_fill = 0;
+    for (auto& md : mon_data) md.clear();
+    spikes.clear();
+    spk_by_gid.clear();
+    const int nvp = static_cast<int>(vecplay.size());
+    if (nvp) {
+        launch_vecplay_reset(d_vecplay, nvp, stream);
+        launch_vecplay(d_vecplay, nvp, 0.0, 1, stream);
+    }
+    launch_clear_ints(ring.count, ring.nslot, stream);
+    launch_clear_ints(ring.overflow, 1, stream);
+    launch_clear_ints(d_pre_flag, npre, stream);
+    launch_clear_ints(d_spk_count, 1, stream);
+    launch_clear_ints(d_in_cursor, 1, stream);
+    launch_set_v(d_v, nnode, v_init, stream);
+    if (!gaps.empty())
+        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
+    StepArgs A = step_args(0.0, 0, 0);
+    for (int id = 0; id < M_COUNT; ++id)           // CoreNEURON order, ions before their users
+        if (mech[id].present) launch_init(id, A, stream);
+    launch_record();
+    launch_detect(0, 0.0);
+    launch_events(0, 0.0);
+    launch_mech_pass(0, 1, 0.0);
+    launch_point_currents(0.0);
+    initialized = true;
+    sync_outputs();
+}
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+#define API_BEGIN try {
+#define API_END                                         \
+    }                                                   \
+    catch (const std::exception& e) {                   \
+        return sim->fail("%s", e.what());               \
+    }
+
+static bool check_loaded(hx_sim* sim) {
+    if (!sim->loaded) { sim->fail("model not loaded (call hx_load_model)"); return false; }
+    return true;
+}
+
+extern "C" {
+
+int hx_create(hx_sim** out) {
+    if (!out) return -1;
+    try {
+        *out = new hx_sim();
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+void hx_destroy(hx_sim* sim) { delete sim; }
+
+const char* hx_last_error(hx_sim* sim) { return sim ? sim->err.c_str() : "null handle"; }
+
+int hx_set_device(hx_sim* sim, const char* dev) {
+    if (!dev || std::string(dev) != "gpu")
+        return sim->fail("device '%s' is not served by this library (only \"gpu\")", dev ? dev : "");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return sim->fail("no HIP device visible");
+    return 0;
+}
+
+int hx_set_dt(hx_sim* sim, double dt) {
+    if (!(dt > 0)) return sim->fail("dt must be positive");
+    if (sim->loaded && dt != sim->dt) {
+        sim->dt = dt;
+        sim->ttab.clear();
+        sim->ttab_cap = 0;
+        return 0;
+    }
+    sim->dt = dt;
+    return 0;
+}
+
+double hx_get_dt(hx_sim* sim) { return sim->dt; }
+
+int hx_set_celsius(hx_sim* sim, double c) {
+    sim->celsius = c;
+    return 0;
+}
+
+int hx_model_set_nodes(hx_sim* sim, int ncell, int nnode, const int* parent, const double* a, const double* b,
+                       const double* area) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (ncell <= 0 || nnode < ncell || !parent || !a || !b || !area) return sim->fail("invalid node arrays");
+    for (int i = 0; i < ncell; ++i)
+        if (parent[i] != -1) return sim->fail("nodes [0, ncell) must be roots");
+    for (int i = ncell; i < nnode; ++i)
+        if (parent[i] < 0 || parent[i] >= i) return sim->fail("node %d: parent must satisfy 0 <= parent < node", i);
+    sim->ncell = ncell;
+    sim->nnode = nnode;
+    sim->parent.assign(parent, parent + nnode);
+    sim->a.assign(a, a + nnode);
+    sim->b.assign(b, b + nnode);
+    sim->area.assign(area, area + nnode);
+    sim->cm.assign(nnode, 1.0);
+    return 0;
+}
+
+int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* nodes) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (sim->nnode == 0) return sim->fail("set nodes before inserting mechanisms");
+    const int id = mech_id(mech ? mech : "");
+    if (id < 0) return sim->fail("unknown mechanism '%s'", mech ? mech : "");
+    HostMech& m = sim->mech[id];
+    if (m.present) return sim->fail("mechanism '%s' inserted twice", mech);
+    if (n < 0 || (n > 0 && !nodes)) return sim->fail("invalid instance list");
+    const auto& M = registry()[id];
+    std::vector<char> seen(sim->nnode, 0);
+    for (int j = 0; j < n; ++j) {
+        if (nodes[j] < 0 || nodes[j] >= sim->nnode) return sim->fail("%s: node index out of range", mech);
+        if (!M.point) {
+            if (seen[nodes[j]]) return sim->fail("%s: density mechanism twice on node %d", mech, nodes[j]);
+            seen[nodes[j]] = 1;
+        }
+    }
+    if (n >= (1 << 30)) return sim->fail("too many instances");
+    m.present = true;
+    m.n = n;
+    m.node.assign(nodes, nodes + n);
+    m.col.assign(M.ncol, {});
+    for (int c = 0; c < M.ncol; ++c) m.col[c].assign(n, M.dflt[c]);
+    if (M.ion) m.iontype.assign(n, 0);
+    if (id == M_VECSTIM) sim->vecstim.assign(n, {});
+    return 0;
+}
+
+int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, const double* vals) {
+    if (sim->loaded) return sim->fail("model already loaded; use variable handles");
+    std::string mn = mech ? mech : "", vn = var ? var : "";
+    if (mn == "capacitance" && vn == "cm") {
+        if (n != sim->nnode) return sim->fail("cm needs one value per node");
+        sim->cm.assign(vals, vals + n);
+        return 0;
+    }
+    const int id = mech_id(mn);
+    if (id < 0 || !sim->mech[id].present) return sim->fail("mechanism '%s' not inserted", mn.c_str());
+    const int c = col_id(id, vn);
+    if (c < 0) return sim->fail("%s has no variable '%s'", mn.c_str(), vn.c_str());
+    if (n != sim->mech[id].n) return sim->fail("%s.%s: expected %d values", mn.c_str(), vn.c_str(), sim->mech[id].n);
+    sim->mech[id].col[c].assign(vals, vals + n);
+    return 0;
+}
+
+int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double value) {
+    const int id = mech_id(mech ? mech : "");
+    if (id != M_HH && id != M_HDLA) return sim->fail("mechanism '%s' has no globals", mech ? mech : "");
+    static const char* hh_g[] = {"celsius"};
+    static const char* hd_g[] = {"celsius", "ehd", "kl", "vhalft", "a0t", "zetat", "gmt", "q10", "qtl"};
+    bool ok = false;
+    if (id == M_HH) for (auto g : hh_g) ok |= std::string(var) == g;
+    if (id == M_HDLA) for (auto g : hd_g) ok |= std::string(var) == g;
+    if (!ok) return sim->fail("%s has no global '%s'", mech, var);
+    sim->globals[id][var] = value;
+    return 0;
+}
+
+int hx_model_set_iontype(hx_sim* sim, const char* ion, int n, const int* it) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    const int id = mech_id(ion ? ion : "");
+    if (id < 0 || !registry()[id].ion || !sim->mech[id].present) return sim->fail("ion '%s' not inserted", ion ? ion : "");
+    if (n != sim->mech[id].n) return sim->fail("iontype needs one value per ion instance");
+    sim->mech[id].iontype.assign(it, it + n);
+    return 0;
+}
+
+int hx_model_add_presyn(hx_sim* sim, int gid, int node, double thr) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (node < 0 || node >= sim->nnode) return sim->fail("presyn node out of range");
+    sim->pre_gid.push_back(gid);
+    sim->pre_node.push_back(node);
+    sim->pre_thr.push_back(thr);
+    return static_cast<int>(sim->pre_node.size()) - 1;
+}
+
+int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
+    HostMech& m = sim->mech[M_VECSTIM];
+    if (!m.present || inst < 0 || inst >= m.n) return sim->fail("VecStim instance %d does not exist", inst);
+    if (n < 0 || (n > 0 && !times)) return sim->fail("invalid spike-time array");
+    sim->vecstim[inst].assign(times, times + n);
+    sim->inputs_dirty = true;
+    return 0;
+}
+
+int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double w, double delay) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    const int id = mech_id(target ? target : "");
+    if (id != M_EXPSYN && id != M_EXP2SYN) return sim->fail("netcon target must be ExpSyn or Exp2Syn");
+    if (!sim->mech[id].present || inst < 0 || inst >= sim->mech[id].n) return sim->fail("netcon target instance out of range");
+    if (src_kind == 0 && (src < 0 || src >= static_cast<int>(sim->pre_node.size())))
+        return sim->fail("netcon source detector out of range");
+    if (src_kind == 1 && (!sim->mech[M_VECSTIM].present || src < 0 || src >= sim->mech[M_VECSTIM].n))
+        return sim->fail("netcon source VecStim out of range");
+    if (src_kind != 0 && src_kind != 1) return sim->fail("src_kind must be 0 or 1");
+    if (!(delay >= 0)) return sim->fail("netcon delay must be >= 0");
+    sim->netcons.push_back({src_kind, src, id, inst, w, delay});
+    return 0;
+}
+
+int hx_model_add_gap(hx_sim* sim, int src_node, int hg) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (src_node < 0 || src_node >= sim->nnode) return sim->fail("gap source node out of range");
+    if (!sim->mech[M_HALFGAP].present || hg < 0 || hg >= sim->mech[M_HALFGAP].n)
+        return sim->fail("HalfGap instance out of range");
+    sim->gaps.push_back({src_node, hg});
+    return 0;
+}
+
+int hx_load_model(hx_sim* sim) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (sim->nnode == 0) return sim->fail("no nodes");
+    API_BEGIN
+    sim->build_layout();
+    sim->upload();
+    sim->loaded = true;
+    // resolve vecplay targets / monitors registered before load
+    for (auto& vp : sim->vecplay) {
+        Ref r = sim->resolve(vp.mech, vp.var, vp.idx);
+        if (!r.dev) return sim->fail("vecplay target %s.%s[%d] not found", vp.mech.c_str(), vp.var.c_str(), vp.idx);
+        vp.target = r.dev;
+    }
+    for (size_t i = 0; i < sim->mon_name.size(); ++i) {
+        Ref r = sim->resolve(sim->mon_name[i].first, sim->mon_name[i].second, sim->mon_idx[i]);
+        if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", sim->mon_name[i].first.c_str(),
+                                     sim->mon_name[i].second.c_str(), sim->mon_idx[i]);
+        sim->mon_ref[i] = r;
+    }
+    return 0;
+    API_END
+}
+
+int hx_finitialize(hx_sim* sim, double v_init) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    sim->finitialize(v_init);
+    return 0;
+    API_END
+}
+
+int hx_run(hx_sim* sim, double tstop) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    int nstep = static_cast<int>(tstop / sim->dt);   // simulate.cpp:345 (int nstep = tstop / dt)
+    // Simulate::run restarts t at 0 without re-initializing (simulate.cpp:346)
+    if (sim->k != 0) {
+        sim->t = 0.0;
+        sim->k = 0;
+    }
+    if (nstep > 0) sim->run_steps(nstep);
+    return 0;
+    API_END
+}
+
+int hx_continue_run(hx_sim* sim, double runtime) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    int nstep = static_cast<int>(runtime / sim->dt);
+    if (nstep > 0) sim->run_steps(nstep);
+    return 0;
+    API_END
+}
+
+int hx_fadvance(hx_sim* sim) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    sim->run_steps(1);
+    return 0;
+    API_END
+}
+
+double hx_get_t(hx_sim* sim) { return sim->t; }
+
+int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx) {
+    if (!mech || !var) return sim->fail("null monitor name");
+    Ref r;
+    if (sim->loaded) {
+        API_BEGIN
+        r = sim->resolve(mech, var, idx);
+        if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", mech, var, idx);
+        if (r.klass == 1 && !sim->need_split_for_monitor) {
+            sim->need_split_for_monitor = true;
+            sim->write_assigned = true;
+            sim->fused = false;
+            if (sim->state_pending) { sim->finish_pending(); sim->sync_outputs(); }
+        }
+        API_END
+    }
+    sim->mon_name.push_back({mech, var});
+    sim->mon_idx.push_back(idx);
+    sim->mon_ref.push_back(r);
+    sim->mon_data.emplace_back();
+    sim->mon_dirty = true;
+    sim->mon_buf_cap = 0;
+    return static_cast<int>(sim->mon_name.size()) - 1;
+}
+
+int hx_get_monitor_len(hx_sim* sim, int h) {
+    if (h < 0 || h >= static_cast<int>(sim->mon_data.size())) return sim->fail("bad monitor handle");
+    return static_cast<int>(sim->mon_data[h].size());
+}
+
+int hx_get_monitor_data(hx_sim* sim, int h, double* out, int cap) {
+    if (h < 0 || h >= static_cast<int>(sim->mon_data.size())) return sim->fail("bad monitor handle");
+    auto& d = sim->mon_data[h];
+    int n = std::min<int>(cap, static_cast<int>(d.size()));
+    if (n > 0) std::memcpy(out, d.data(), sizeof(double) * n);
+    return n;
+}
+
+int hx_flush_recorders(hx_sim* sim) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    sim->sync_outputs();
+    return 0;
+    API_END
+}
+
+int hx_get_variable_handle(hx_sim* sim, const char* mech, const char* var, int idx) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
+    if (!r.dev) return sim->fail("variable %s.%s[%d] not found", mech, var, idx);
+    if (r.klass == 1) sim->write_assigned = true;
+    sim->handles.push_back(r);
+    return static_cast<int>(sim->handles.size()) - 1;
+    API_END
+}
+
+int hx_get_variable_by_handle(hx_sim* sim, int h, double* out) {
+    if (h < 0 || h >= static_cast<int>(sim->handles.size()) || !out) return sim->fail("bad variable handle");
+    API_BEGIN
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemcpy(out, sim->handles[h].dev, sizeof(double), hipMemcpyDeviceToHost));
+    return 0;
+    API_END
+}
+
+int hx_set_variable_by_handle(hx_sim* sim, int h, double value) {
+    if (h < 0 || h >= static_cast<int>(sim->handles.size())) return sim->fail("bad variable handle");
+    API_BEGIN
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemcpy(sim->handles[h].dev, &value, sizeof(double), hipMemcpyHostToDevice));
+    return 0;
+    API_END
+}
+
+int hx_get_variables_by_handles(hx_sim* sim, int n, const int* hs, double* out) {
+    for (int i = 0; i < n; ++i)
+        if (hx_get_variable_by_handle(sim, hs[i], out + i) != 0) return -1;
+    return 0;
+}
+
+int hx_get_variables_by_handles_f32_into(hx_sim* sim, int n, const int* hs, float* out) {
+    for (int i = 0; i < n; ++i) {
+        double x;
+        if (hx_get_variable_by_handle(sim, hs[i], &x) != 0) return -1;
+        out[i] = static_cast<float>(x);
+    }
+    return 0;
+}
+
+int hx_set_variables_by_handles(hx_sim* sim, int n, const int* hs, const double* vals) {
+    for (int i = 0; i < n; ++i)
+        if (hx_set_variable_by_handle(sim, hs[i], vals[i]) != 0) return -1;
+    return 0;
+}
+
+int hx_get_variable_value(hx_sim* sim, const char* mech, const char* var, int idx, double* out) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
+    if (!r.dev) return sim->fail("variable %s.%s[%d] not found", mech, var, idx);
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemcpy(out, r.dev, sizeof(double), hipMemcpyDeviceToHost));
+    return 0;
+    API_END
+}
+
+int hx_set_variable_value(hx_sim* sim, double value, const char* mech, const char* var, int idx) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
+    if (!r.dev) return sim->fail("variable %s.%s[%d] not found", mech, var, idx);
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemcpy(r.dev, &value, sizeof(double), hipMemcpyHostToDevice));
+    return 0;
+    API_END
+}
+
+int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, int cap) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    std::string mn = mech ? mech : "", vn = var ? var : "";
+    HXC(hipStreamSynchronize(sim->stream));
+    if (mn == "global" || mn == "node" || mn == "capacitance") {
+        double* src = nullptr;
+        if (mn == "capacitance") src = vn == "cm" ? sim->d_cm : nullptr;
+        else if (vn == "v") src = sim->d_v;
+        else if (vn == "d") src = sim->d_d;
+        else if (vn == "rhs") src = sim->d_rhs;
+        else if (vn == "a") src = sim->d_a;
+        else if (vn == "b") src = sim->d_b;
+        else if (vn == "area") src = sim->d_area;
+        if (!src) return sim->fail("node variable '%s' not found", vn.c_str());
+        if (cap < sim->nnode) return sim->fail("output too small");
+        std::vector<double> g(sim->nnode);
+        HXC(hipMemcpy(g.data(), src, sizeof(double) * sim->nnode, hipMemcpyDeviceToHost));
+        for (int i = 0; i < sim->nnode; ++i) out[i] = g[sim->node_perm[i]];
+        return sim->nnode;
+    }
+    int id = mech_id(mn);
+    if (id < 0 || !sim->mech[id].present) return sim->fail("mechanism '%s' not present", mn.c_str());
+    if (id == M_CADYN && (vn == "cai" || vn == "ica")) {
+        HostMech& m = sim->mech[id];
+        if (cap < m.n) return sim->fail("output too small");
+        for (int j = 0; j < m.n; ++j) {
+            Ref r = sim->resolve("ca_ion", vn == "cai" ? "conci" : "cur", m.node[j]);
+            HXC(hipMemcpy(out + j, r.dev, sizeof(double), hipMemcpyDeviceToHost));
+        }
+        return m.n;
+    }
+    const int c = col_id(id, vn);
+    if (c < 0) return sim->fail("%s has no variable '%s'", mn.c_str(), vn.c_str());
+    HostMech& m = sim->mech[id];
+    if (cap < m.n) return sim->fail("output too small");
+    std::vector<double> g(m.n);
+    if (m.n) HXC(hipMemcpy(g.data(), m.dev.col(c), sizeof(double) * m.n, hipMemcpyDeviceToHost));
+    for (int j = 0; j < m.n; ++j) out[j] = g[m.perm[j]];
+    return m.n;
+    API_END
+}
+
+int hx_add_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tv, const double* yv) {
+    if (n <= 0 || !tv || !yv) return sim->fail("vecplay needs at least one (t, y) point");
+    if (hx_has_vecplay(sim, mech, var, idx) == 1) return hx_update_vecplay(sim, mech, var, idx, n, tv, yv);
+    VecPlayHost vp;
+    vp.mech = mech;
+    vp.var = var;
+    vp.idx = idx;
+    vp.tvec.assign(tv, tv + n);
+    vp.yvec.assign(yv, yv + n);
+    if (sim->loaded) {
+        API_BEGIN
+        Ref r = sim->resolve(mech, var, idx);
+        if (!r.dev) return sim->fail("vecplay target %s.%s[%d] not found", mech, var, idx);
+        vp.target = r.dev;
+        API_END
+    }
+    sim->vecplay.push_back(std::move(vp));
+    if (sim->loaded) {
+        API_BEGIN
+        if (sim->state_pending) { sim->finish_pending(); sim->sync_outputs(); }
+        sim->recompute_fused();
+        API_END
+    }
+    sim->vecplay_dirty = true;
+    return 0;
+}
+
+int hx_update_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tv, const double* yv) {
+    for (auto& vp : sim->vecplay)
+        if (vp.mech == mech && vp.var == var && vp.idx == idx) {
+            vp.tvec.assign(tv, tv + n);
+            vp.yvec.assign(yv, yv + n);
+            vp.d_t = vp.d_y = nullptr;
+            sim->vecplay_dirty = true;
+            return 0;
+        }
+    return sim->fail("vecplay %s.%s[%d] not found", mech, var, idx);
+}
+
+int hx_remove_vecplay(hx_sim* sim, const char* mech, const char* var, int idx) {
+    for (size_t i = 0; i < sim->vecplay.size(); ++i) {
+        auto& vp = sim->vecplay[i];
+        if (vp.mech == mech && vp.var == var && vp.idx == idx) {
+            sim->vecplay.erase(sim->vecplay.begin() + i);
+            sim->vecplay_dirty = true;
+            return 0;
+        }
+    }
+    return sim->fail("vecplay %s.%s[%d] not found", mech, var, idx);
+}
+
+int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx) {
+    for (auto& vp : sim->vecplay)
+        if (vp.mech == mech && vp.var == var && vp.idx == idx) return 1;
+    return 0;
+}
+
+int hx_get_spike_count(hx_sim* sim) { return static_cast<int>(sim->spikes.size()); }
+
+int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap) {
+    int n = std::min<int>(cap, static_cast<int>(sim->spikes.size()));
+    for (int i = 0; i < n; ++i) {
+        t[i] = sim->spikes[i].first;
+        gid[i] = sim->spikes[i].second;
+    }
+    return n;
+}
+
+int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap) {
+    auto it = sim->spk_by_gid.find(gid);
+    if (it == sim->spk_by_gid.end()) return 0;
+    int n = std::min<int>(cap, static_cast<int>(it->second.size()));
+    for (int i = 0; i < n; ++i) out[i] = it->second[i];
+    return n;
+}
+
+int hx_set_event_capacity(hx_sim* sim, int per_step) {
+    if (sim->loaded) return sim->fail("set the event capacity before hx_load_model");
+    if (per_step <= 0) return sim->fail("capacity must be positive");
+    sim->event_cap_request = per_step;
+    return 0;
+}
+
+int hx_set_fusion(hx_sim* sim, int enable) {
+    sim->fusion_allowed = enable ? 1 : 0;
+    if (sim->loaded) {
+        API_BEGIN
+        if (sim->state_pending) { sim->finish_pending(); sim->sync_outputs(); }
+        sim->recompute_fused();
+        API_END
+    }
+    return 0;
+}
+
+int hx_set_profiling(hx_sim* sim, int enable) {
+    sim->profiling = enable != 0;
+    for (auto& tm : sim->timers) { tm.ms = 0; tm.launches = 0; }
+    return 0;
+}
+
+int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches) {
+    for (int i = 0; i < T_COUNT; ++i)
+        if (kernel && std::string(kernel) == kTimerNames[i]) {
+            if (ms) *ms = sim->timers[i].ms;
+            if (launches) *launches = sim->timers[i].launches;
+            return 0;
+        }
+    return sim->fail("unknown kernel class '%s'", kernel ? kernel : "");
+}
+
+// Host emulation of one device tree solve over the same chunk schedule: for
+// every cell, rounds in the kernel's order, each lane's chunk in turn.  Lanes
+// of a round touch disjoint nodes and slots, so running them one after the
+// other gives the device result bit for bit.
+int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
+                          const double* cm, double cfac, double* v, const double* d, const double* rhs,
+                          int* nchunk_max, int* nround_max) {
+    try {
+        hx_sim tmp;
+        if (hx_model_set_nodes(&tmp, ncell, nnode, parent, a, b, a) != 0) return -1;
+        tmp.build_layout();
+        const int N = nnode;
+        std::vector<double> gv(N), gd(N), gr(N), ga(N), gb(N), gcm(N);
+        for (int i = 0; i < N; ++i) {
+            const int g = tmp.node_perm[i];
+            gv[g] = v[i]; gd[g] = d[i]; gr[g] = rhs[i]; ga[g] = a[i]; gb[g] = b[i]; gcm[g] = cm[i];
+        }
+        std::vector<double> slots(2 * static_cast<size_t>(std::max(tmp.max_slots, 1)));
+        for (int c = 0; c < ncell; ++c) {
+            const int nb = tmp.cell_node_begin[c];
+            const int r0 = tmp.cell_round_begin[c], r1 = tmp.cell_round_begin[c + 1];
+            for (int r = r1 - 1; r >= r0; --r)
+                for (int q = tmp.round_desc_begin[r]; q < tmp.round_desc_begin[r + 1]; ++q)
+                    chunk_forward(tmp.descs[q], nb, gv.data(), gd.data(), gr.data(), ga.data(), gb.data(), gcm.data(),
+                                  cfac, slots.data());
+            for (int r = r0; r < r1; ++r) {
+                std::vector<std::pair<int, double>> tails;
+                for (int q = tmp.round_desc_begin[r]; q < tmp.round_desc_begin[r + 1]; ++q)
+                    tails.push_back({tmp.descs[q].slot, chunk_back(tmp.descs[q], nb, gv.data(), gd.data(), gr.data(),
+                                                                   gb.data(), slots.data())});
+                for (auto& tl : tails) slots[2 * tl.first] = tl.second;
+            }
+        }
+        for (int i = 0; i < N; ++i) v[i] = gv[tmp.node_perm[i]];
+        if (nchunk_max) *nchunk_max = tmp.max_slots;
+        if (nround_max) *nround_max = tmp.max_rounds;
+        return 0;
+    } catch (...) {
+        return -1;
+    }
+}
+
+long long hx_get_info(hx_sim* sim, const char* key) {
+    std::string k = key ? key : "";
+    if (k == "nnode") return sim->nnode;
+    if (k == "ncell") return sim->ncell;
+    if (k == "nchunk_max") return sim->max_slots;
+    if (k == "nround_max") return sim->max_rounds;
+    if (k == "dense_mask") return sim->dense_mask;
+    if (k == "fused") return sim->fused ? 1 : 0;
+    if (k == "nround_total") return static_cast<long long>(sim->round_desc_begin.size()) - 1;
+    if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
+    if (k == "event_slots") return sim->ring.nslot;
+    if (k == "event_cap") return sim->ring.cap;
+    return -1;
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// Host-side tree-solve scheduler: replaces the reference's DHS ordering
+// (permute_order.cpp:145-210 node_order_branch, 641-722; 971-1170
+// dynamic_interleave2 / admin_dynamic2), which packs cells into 32-lane groups
+// that rely on implicit warp lockstep (simulate.cu:119-189).
+//
+// Here every cell is solved by one 64-lane wavefront.  The cell's tree is cut
+// into chunks: unbranched runs of at most kChunk nodes (a node with exactly
+// one child continues its chunk).  A chunk's height is 0 for a leaf chunk and
+// 1 + the largest child height otherwise; chunks of equal height are
+// independent, so they form rounds of up to 64 lanes.  Elimination walks the
+// rounds by increasing height, back substitution by decreasing height, with a
+// barrier between rounds.  Chunk ids are breadth-first so that the chunks
+// hanging off one tail are consecutive LDS slots.
+#include <algorithm>
+#include <cstdint>
+#include <numeric>
+#include <stdexcept>
+#include <vector>
+
+#include "schedule.h"
+
+namespace hx {
+
+void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, int lanes, CellSchedule& out) {
+    const int n = static_cast<int>(local_parent.size());
+    out = CellSchedule();
+    if (n == 0) return;
+    if (local_parent[0] != -1) throw std::runtime_error("cell root must be local node 0");
+    std::vector<int> nchild(n, 0);
+    for (int i = 1; i < n; ++i) {
+        const int p = local_parent[i];
+        if (p < 0 || p >= i) throw std::runtime_error("cell nodes must satisfy parent < child");
+        nchild[p]++;
+    }
+    std::vector<int> cbeg(n + 1, 0);
+    for (int i = 0; i < n; ++i) cbeg[i + 1] = cbeg[i] + nchild[i];
+    std::vector<int> cfill(cbeg.begin(), cbeg.end() - 1), clist(std::max(n - 1, 0));
+    for (int i = 1; i < n; ++i) clist[cfill[local_parent[i]]++] = i;
+
+    // breadth-first chunk construction: children of one chunk get consecutive ids
+    struct Chunk { int head; int len; int parent; int child_begin; int child_count; std::vector<int> nodes; };
+    std::vector<Chunk> chunks;
+    chunks.reserve(n / 2 + 1);
+    chunks.push_back({0, 0, -1, 0, 0, {}});
+    for (size_t q = 0; q < chunks.size(); ++q) {
+        int cur = chunks[q].head;
+        std::vector<int> nodes{cur};
+        while (nchild[cur] == 1 && static_cast<int>(nodes.size()) < chunk_max) {
+            cur = clist[cbeg[cur]];
+            nodes.push_back(cur);
+        }
+        chunks[q].nodes = nodes;
+        chunks[q].len = static_cast<int>(nodes.size());
+        chunks[q].child_begin = static_cast<int>(chunks.size());
+        chunks[q].child_count = nchild[cur];
+        for (int e = cbeg[cur]; e < cbeg[cur + 1]; ++e)
+            chunks.push_back({clist[e], 0, static_cast<int>(q), 0, 0, {}});
+    }
+    const int nchunk = static_cast<int>(chunks.size());
+    std::vector<int> height(nchunk, 0);
+    for (int q = nchunk - 1; q >= 0; --q) {
+        int h = 0;
+        for (int c = 0; c < chunks[q].child_count; ++c) h = std::max(h, height[chunks[q].child_begin + c] + 1);
+        height[q] = h;
+    }
+    const int hmax = height[0];
+    std::vector<std::vector<int>> by_h(hmax + 1);
+    for (int q = 0; q < nchunk; ++q) by_h[height[q]].push_back(q);
+    // back-substitution order: root height first; within a height, longest chunks first
+    std::vector<std::vector<int>> rounds;
+    for (int h = hmax; h >= 0; --h) {
+        auto& v = by_h[h];
+        std::stable_sort(v.begin(), v.end(), [&](int x, int y) { return chunks[x].len > chunks[y].len; });
+        for (size_t s = 0; s < v.size(); s += lanes)
+            rounds.emplace_back(v.begin() + s, v.begin() + std::min(v.size(), s + lanes));
+    }
+    // solver order of the cell's nodes
+    std::vector<int> start(nchunk, 0);
+    out.order.reserve(n);
+    for (auto& r : rounds)
+        for (int q : r) {
+            start[q] = static_cast<int>(out.order.size());
+            for (int nd : chunks[q].nodes) out.order.push_back(nd);
+        }
+    out.round_begin.push_back(0);
+    for (auto& r : rounds) {
+        for (int q : r) {
+            ChunkDesc d{};
+            d.start = start[q];
+            d.len = chunks[q].len;
+            d.slot = q;
+            d.parent_slot = chunks[q].parent;
+            d.head_parent = chunks[q].parent >= 0 ? start[chunks[q].parent] + chunks[chunks[q].parent].len - 1 : -1;
+            d.child_begin = chunks[q].child_begin;
+            d.child_count = chunks[q].child_count;
+            out.desc.push_back(d);
+        }
+        out.round_begin.push_back(static_cast<int>(out.desc.size()));
+    }
+    out.nchunk = nchunk;
+    out.nround = static_cast<int>(rounds.size());
+}
+
+}  // namespace hx

@@ -1,0 +1,378 @@
+"""Python surface of the MI355X simulation core.
+
+``Sim`` mirrors the reference's ``heliox.Sim`` (src/python_api/PyBindings.cpp:15-266,
+SimWrapper.h) for the step-loop path: ``set_device``, ``set_dt``/``get_dt``,
+``finitialize``, ``run``, ``continue_run``, ``fadvance``, ``get_t``,
+``add_monitor``/``get_monitor_data``/``get_multiple_monitor_data``,
+``get_variable_handle``/``get_variable_by_handle``/``set_variable_by_handle``
+(and their batched forms), ``get_variable_value``/``set_variable_value``,
+``add_vecplay``/``update_vecplay``/``remove_vecplay``/``has_vecplay``,
+``get_spk_by_gid``, and ``add_gap_source``/``add_gap_target``.  Methods
+return 0 / -1 like the reference; ``RuntimeError`` is raised only where the
+reference raises.  The model comes from a ``ModelSpec`` (``load_model_from_spec``)
+instead of a CoreNEURON export directory.
+
+Every call goes through the C ABI of ``libheliox_amd.so`` (include/heliox.h);
+there is no CPU fallback: without the library (or without a GPU) the calls
+fail.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+from .spec import ModelSpec
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libheliox_amd.so")
+_lib = None
+
+_D = C.POINTER(C.c_double)
+_I = C.POINTER(C.c_int)
+_F = C.POINTER(C.c_float)
+_P = C.c_void_p
+_S = C.c_char_p
+
+# name: (restype, argtypes) for every entry point of include/heliox.h
+SIGNATURES = {
+    "hx_create": (C.c_int, [C.POINTER(_P)]),
+    "hx_destroy": (None, [_P]),
+    "hx_last_error": (C.c_char_p, [_P]),
+    "hx_set_device": (C.c_int, [_P, _S]),
+    "hx_set_dt": (C.c_int, [_P, C.c_double]),
+    "hx_get_dt": (C.c_double, [_P]),
+    "hx_set_celsius": (C.c_int, [_P, C.c_double]),
+    "hx_model_set_nodes": (C.c_int, [_P, C.c_int, C.c_int, _I, _D, _D, _D]),
+    "hx_model_insert": (C.c_int, [_P, _S, C.c_int, _I]),
+    "hx_model_set_param": (C.c_int, [_P, _S, _S, C.c_int, _D]),
+    "hx_model_set_global": (C.c_int, [_P, _S, _S, C.c_double]),
+    "hx_model_set_iontype": (C.c_int, [_P, _S, C.c_int, _I]),
+    "hx_model_add_presyn": (C.c_int, [_P, C.c_int, C.c_int, C.c_double]),
+    "hx_model_set_vecstim": (C.c_int, [_P, C.c_int, C.c_int, _D]),
+    "hx_model_add_netcon": (C.c_int, [_P, C.c_int, C.c_int, _S, C.c_int, C.c_double, C.c_double]),
+    "hx_model_add_gap": (C.c_int, [_P, C.c_int, C.c_int]),
+    "hx_load_model": (C.c_int, [_P]),
+    "hx_finitialize": (C.c_int, [_P, C.c_double]),
+    "hx_run": (C.c_int, [_P, C.c_double]),
+    "hx_continue_run": (C.c_int, [_P, C.c_double]),
+    "hx_fadvance": (C.c_int, [_P]),
+    "hx_get_t": (C.c_double, [_P]),
+    "hx_add_monitor": (C.c_int, [_P, _S, _S, C.c_int]),
+    "hx_get_monitor_len": (C.c_int, [_P, C.c_int]),
+    "hx_get_monitor_data": (C.c_int, [_P, C.c_int, _D, C.c_int]),
+    "hx_flush_recorders": (C.c_int, [_P]),
+    "hx_get_variable_handle": (C.c_int, [_P, _S, _S, C.c_int]),
+    "hx_get_variable_by_handle": (C.c_int, [_P, C.c_int, _D]),
+    "hx_set_variable_by_handle": (C.c_int, [_P, C.c_int, C.c_double]),
+    "hx_get_variables_by_handles": (C.c_int, [_P, C.c_int, _I, _D]),
+    "hx_get_variables_by_handles_f32_into": (C.c_int, [_P, C.c_int, _I, _F]),
+    "hx_set_variables_by_handles": (C.c_int, [_P, C.c_int, _I, _D]),
+    "hx_get_variable_value": (C.c_int, [_P, _S, _S, C.c_int, _D]),
+    "hx_set_variable_value": (C.c_int, [_P, C.c_double, _S, _S, C.c_int]),
+    "hx_get_array": (C.c_int, [_P, _S, _S, _D, C.c_int]),
+    "hx_add_vecplay": (C.c_int, [_P, _S, _S, C.c_int, C.c_int, _D, _D]),
+    "hx_update_vecplay": (C.c_int, [_P, _S, _S, C.c_int, C.c_int, _D, _D]),
+    "hx_remove_vecplay": (C.c_int, [_P, _S, _S, C.c_int]),
+    "hx_has_vecplay": (C.c_int, [_P, _S, _S, C.c_int]),
+    "hx_get_spike_count": (C.c_int, [_P]),
+    "hx_get_spikes": (C.c_int, [_P, _D, _I, C.c_int]),
+    "hx_get_spk_by_gid": (C.c_int, [_P, C.c_int, _D, C.c_int]),
+    "hx_set_event_capacity": (C.c_int, [_P, C.c_int]),
+    "hx_set_fusion": (C.c_int, [_P, C.c_int]),
+    "hx_set_profiling": (C.c_int, [_P, C.c_int]),
+    "hx_get_kernel_time": (C.c_int, [_P, _S, _D, C.POINTER(C.c_longlong)]),
+    "hx_get_info": (C.c_longlong, [_P, _S]),
+    "hx_emulate_tree_solve": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, _I, _I]),
+}
+
+
+def lib() -> C.CDLL:
+    """Load ``libheliox_amd.so``; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m heliox_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _dp(a: np.ndarray):
+    return a.ctypes.data_as(_D)
+
+
+def _ip(a: np.ndarray):
+    return a.ctypes.data_as(_I)
+
+
+def _b(s: str) -> bytes:
+    return s.encode()
+
+
+class HelioxError(RuntimeError):
+    pass
+
+
+class Sim:
+    """One model on one GPU (the reference keeps one model group per process)."""
+
+    def __init__(self):
+        L = lib()
+        h = _P()
+        if L.hx_create(C.byref(h)) != 0:
+            raise HelioxError("hx_create failed")
+        self._h = h
+        self._gap_sources: Dict[int, int] = {}
+        self._next_sid = 0
+        self.spec: Optional[ModelSpec] = None
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            lib().hx_destroy(h)
+            self._h = None
+
+    # --------------------------------------------------------------- helpers
+    @property
+    def handle(self):
+        return self._h
+
+    def last_error(self) -> str:
+        return lib().hx_last_error(self._h).decode()
+
+    def _chk(self, rc: int, what: str) -> int:
+        if rc < 0:
+            raise HelioxError(f"{what}: {self.last_error()}")
+        return rc
+
+    def _rc(self, rc: int) -> int:
+        """Reference convention: return 0 / -1 and keep the message for last_error()."""
+        return 0 if rc >= 0 else -1
+
+    # --------------------------------------------------------------- settings
+    def set_device(self, dev: str) -> int:
+        return self._rc(lib().hx_set_device(self._h, _b(dev)))
+
+    def set_dt(self, dt: float) -> int:
+        return self._rc(lib().hx_set_dt(self._h, float(dt)))
+
+    def get_dt(self) -> float:
+        return lib().hx_get_dt(self._h)
+
+    def set_celsius(self, c: float) -> int:
+        return self._rc(lib().hx_set_celsius(self._h, float(c)))
+
+    def set_event_capacity(self, n: int) -> int:
+        return self._rc(lib().hx_set_event_capacity(self._h, int(n)))
+
+    def set_fusion(self, enable: bool) -> int:
+        return self._rc(lib().hx_set_fusion(self._h, 1 if enable else 0))
+
+    # --------------------------------------------------------------- model
+    def load_model_from_spec(self, spec: ModelSpec, add_monitors: bool = True) -> int:
+        """Build the model of ``spec`` and upload it (replaces set_data_path + load_model)."""
+        spec.validate()
+        L = lib()
+        h = self._h
+        self._keep = []
+        self._chk(L.hx_set_dt(h, spec.dt), "set_dt")
+        self._chk(L.hx_set_celsius(h, spec.celsius), "set_celsius")
+        parent = np.ascontiguousarray(spec.parent, np.int32)
+        arrs = [np.ascontiguousarray(x, np.float64) for x in (spec.a, spec.b, spec.area)]
+        self._chk(L.hx_model_set_nodes(h, spec.ncell, spec.nnode, _ip(parent), *[_dp(x) for x in arrs]), "set_nodes")
+        cm = np.ascontiguousarray(spec.cm, np.float64)
+        self._chk(L.hx_model_set_param(h, b"capacitance", b"cm", spec.nnode, _dp(cm)), "cm")
+        order = sorted(spec.mechs.keys(), key=lambda k: 0 if k.endswith("_ion") else 1)
+        for name in order:
+            m = spec.mechs[name]
+            nodes = np.ascontiguousarray(m.nodes, np.int32)
+            self._chk(L.hx_model_insert(h, _b(name), m.n, _ip(nodes)), f"insert {name}")
+            for k, v in m.params.items():
+                v = np.ascontiguousarray(v, np.float64)
+                self._chk(L.hx_model_set_param(h, _b(name), _b(k), m.n, _dp(v)), f"{name}.{k}")
+            for k, v in m.globals.items():
+                self._chk(L.hx_model_set_global(h, _b(name), _b(k), float(v)), f"global {name}.{k}")
+            if m.iontype is not None:
+                it = np.ascontiguousarray(m.iontype, np.int32)
+                self._chk(L.hx_model_set_iontype(h, _b(name), m.n, _ip(it)), f"iontype {name}")
+        for gid, nd, thr in zip(spec.presyn_gid, spec.presyn_node, spec.presyn_thr):
+            self._chk(L.hx_model_add_presyn(h, int(gid), int(nd), float(thr)), "presyn")
+        for k in range(spec.n_vecstim):
+            tr = np.ascontiguousarray(spec.vecstim_train(k), np.float64)
+            if tr.size:
+                self._chk(L.hx_model_set_vecstim(h, k, tr.size, _dp(tr)), "vecstim")
+        for tgt, nc in spec.netcons.items():
+            tb = _b(tgt)
+            for i in range(nc.inst.shape[0]):
+                self._chk(L.hx_model_add_netcon(h, int(nc.src_kind[i]), int(nc.src[i]), tb, int(nc.inst[i]),
+                                                float(nc.weight[i]), float(nc.delay[i])), "netcon")
+        for s, g in zip(spec.gap_src_node, spec.gap_halfgap):
+            self._chk(L.hx_model_add_gap(h, int(s), int(g)), "gap")
+        for vp in spec.vecplay:
+            tv = np.ascontiguousarray(vp.tvec, np.float64)
+            yv = np.ascontiguousarray(vp.yvec, np.float64)
+            self._chk(L.hx_add_vecplay(h, _b(vp.mech), _b(vp.var), vp.idx, tv.size, _dp(tv), _dp(yv)), "vecplay")
+        self.monitor_handles: List[int] = []
+        if add_monitors:
+            for mech, var, idx in spec.monitors:
+                self.monitor_handles.append(self._chk(L.hx_add_monitor(h, _b(mech), _b(var), int(idx)),
+                                                      f"monitor {mech}.{var}[{idx}]"))
+        self._chk(L.hx_load_model(h), "load_model")
+        self.spec = spec
+        return 0
+
+    def info(self, key: str) -> int:
+        return int(lib().hx_get_info(self._h, _b(key)))
+
+    # --------------------------------------------------------------- stepping
+    def finitialize(self, v_init: float = -65.0) -> int:
+        return self._chk(lib().hx_finitialize(self._h, float(v_init)), "finitialize")
+
+    def run(self, tstop: float) -> int:
+        return self._chk(lib().hx_run(self._h, float(tstop)), "run")
+
+    def continue_run(self, runtime: float) -> int:
+        return self._chk(lib().hx_continue_run(self._h, float(runtime)), "continue_run")
+
+    def fadvance(self) -> int:
+        return self._chk(lib().hx_fadvance(self._h), "fadvance")
+
+    def get_t(self) -> float:
+        return lib().hx_get_t(self._h)
+
+    # --------------------------------------------------------------- monitors
+    def add_monitor(self, mech: str, var: str, idx: int) -> int:
+        return lib().hx_add_monitor(self._h, _b(mech), _b(var), int(idx))
+
+    def flush_recorders(self) -> int:
+        return self._rc(lib().hx_flush_recorders(self._h))
+
+    def get_monitor_data(self, handle: int) -> List[float]:
+        return self.monitor_array(handle).tolist()
+
+    def monitor_array(self, handle: int) -> np.ndarray:
+        L = lib()
+        n = L.hx_get_monitor_len(self._h, handle)
+        if n < 0:
+            return np.zeros(0)
+        out = np.empty(n)
+        L.hx_get_monitor_data(self._h, handle, _dp(out), n)
+        return out
+
+    def get_multiple_monitor_data(self, handles: Sequence[int]) -> Dict[int, List[float]]:
+        return {h: self.get_monitor_data(h) for h in handles}
+
+    def traces(self) -> np.ndarray:
+        hs = getattr(self, "monitor_handles", [])
+        return np.stack([self.monitor_array(h) for h in hs]) if hs else np.zeros((0, 0))
+
+    # --------------------------------------------------------------- variables
+    def get_variable_handle(self, mech: str, var: str, idx: int) -> int:
+        return lib().hx_get_variable_handle(self._h, _b(mech), _b(var), int(idx))
+
+    def get_variable_by_handle(self, handle: int) -> float:
+        out = np.zeros(1)
+        self._chk(lib().hx_get_variable_by_handle(self._h, int(handle), _dp(out)), "get_variable_by_handle")
+        return float(out[0])
+
+    def set_variable_by_handle(self, handle: int, value: float) -> int:
+        return self._rc(lib().hx_set_variable_by_handle(self._h, int(handle), float(value)))
+
+    def get_variables_by_handles(self, handles: Sequence[int]) -> List[float]:
+        hs = np.ascontiguousarray(handles, np.int32)
+        out = np.zeros(hs.size)
+        self._chk(lib().hx_get_variables_by_handles(self._h, hs.size, _ip(hs), _dp(out)), "get_variables_by_handles")
+        return out.tolist()
+
+    def get_variables_by_handles_f32_into(self, handles: np.ndarray, out: np.ndarray) -> int:
+        hs = np.ascontiguousarray(handles, np.int32)
+        if out.dtype != np.float32 or not out.flags.c_contiguous or out.size < hs.size:
+            raise ValueError("out must be a C-contiguous float32 array of at least len(handles)")
+        return self._rc(lib().hx_get_variables_by_handles_f32_into(self._h, hs.size, _ip(hs),
+                                                                    out.ctypes.data_as(_F)))
+
+    def set_variables_by_handles(self, handles: Sequence[int], values: Sequence[float]) -> int:
+        hs = np.ascontiguousarray(handles, np.int32)
+        vs = np.ascontiguousarray(values, np.float64)
+        return self._rc(lib().hx_set_variables_by_handles(self._h, hs.size, _ip(hs), _dp(vs)))
+
+    def get_variable_value(self, mech: str, var: str, idx: int) -> float:
+        out = np.zeros(1)
+        self._chk(lib().hx_get_variable_value(self._h, _b(mech), _b(var), int(idx), _dp(out)), "get_variable_value")
+        return float(out[0])
+
+    def set_variable_value(self, val: float, mech: str, var: str, idx: int) -> int:
+        return self._rc(lib().hx_set_variable_value(self._h, float(val), _b(mech), _b(var), int(idx)))
+
+    def get_array(self, mech: str, var: str) -> np.ndarray:
+        n = self.spec.nnode if mech in ("global", "node", "capacitance") else self.spec.mechs[mech].n
+        out = np.empty(n)
+        self._chk(lib().hx_get_array(self._h, _b(mech), _b(var), _dp(out), n), f"get_array {mech}.{var}")
+        return out
+
+    # --------------------------------------------------------------- vecplay
+    def add_vecplay(self, mech: str, var: str, idx: int, tvec, yvec) -> int:
+        tv = np.ascontiguousarray(tvec, np.float64)
+        yv = np.ascontiguousarray(yvec, np.float64)
+        if tv.size != yv.size:
+            return -1
+        return self._rc(lib().hx_add_vecplay(self._h, _b(mech), _b(var), int(idx), tv.size, _dp(tv), _dp(yv)))
+
+    def update_vecplay(self, mech: str, var: str, idx: int, tvec, yvec) -> int:
+        tv = np.ascontiguousarray(tvec, np.float64)
+        yv = np.ascontiguousarray(yvec, np.float64)
+        return self._rc(lib().hx_update_vecplay(self._h, _b(mech), _b(var), int(idx), tv.size, _dp(tv), _dp(yv)))
+
+    def remove_vecplay(self, mech: str, var: str, idx: int) -> int:
+        return self._rc(lib().hx_remove_vecplay(self._h, _b(mech), _b(var), int(idx)))
+
+    def has_vecplay(self, mech: str, var: str, idx: int) -> bool:
+        return lib().hx_has_vecplay(self._h, _b(mech), _b(var), int(idx)) == 1
+
+    # --------------------------------------------------------------- spikes
+    def spikes(self):
+        L = lib()
+        n = L.hx_get_spike_count(self._h)
+        t = np.empty(n)
+        g = np.empty(n, np.int32)
+        L.hx_get_spikes(self._h, _dp(t), _ip(g), n)
+        return t, g
+
+    def get_spk_by_gid(self, gid: int) -> List[float]:
+        L = lib()
+        n = L.hx_get_spike_count(self._h)
+        out = np.empty(max(n, 1))
+        k = L.hx_get_spk_by_gid(self._h, int(gid), _dp(out), out.size)
+        return out[:k].tolist()
+
+    # --------------------------------------------------------------- profiling
+    def set_profiling(self, enable: bool) -> int:
+        return self._rc(lib().hx_set_profiling(self._h, 1 if enable else 0))
+
+    def kernel_time(self, kernel: str):
+        ms = C.c_double()
+        n = C.c_longlong()
+        self._chk(lib().hx_get_kernel_time(self._h, _b(kernel), C.byref(ms), C.byref(n)), "kernel_time")
+        return ms.value, n.value
+
+
+def emulate_tree_solve(ncell, parent, a, b, cm, cfac, v, d, rhs):
+    """Host emulation of the device tree solve (same chunk schedule); returns (v_new, nchunk_max, nround_max)."""
+    L = lib()
+    parent = np.ascontiguousarray(parent, np.int32)
+    a, b, cm, d, rhs = (np.ascontiguousarray(x, np.float64) for x in (a, b, cm, d, rhs))
+    vv = np.array(v, np.float64)
+    nc = C.c_int()
+    nr = C.c_int()
+    rc = L.hx_emulate_tree_solve(int(ncell), parent.size, _ip(parent), _dp(a), _dp(b), _dp(cm), float(cfac),
+                                 _dp(vv), _dp(d), _dp(rhs), C.byref(nc), C.byref(nr))
+    if rc != 0:
+        raise HelioxError("hx_emulate_tree_solve failed")
+    return vv, nc.value, nr.value

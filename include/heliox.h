@@ -1,0 +1,140 @@
+/*
+ * heliox.h -- C ABI of the MI355X (gfx950) HelioX simulation core.
+ *
+ * One opaque handle holds one model (the reference keeps one model group per
+ * process: read_coredat.cpp:43, simulate.cpp:201).  All calls are made from a
+ * single host thread per handle.  Every entry point returns 0 (or a
+ * non-negative handle / count) on success and -1 on failure, like the
+ * reference's SimWrapper (SimWrapper.cpp: `printf` + `return -1`); the failure
+ * text is available from hx_last_error().  No call throws across the ABI.
+ *
+ * Units follow the reference: ms, mV, um, S/cm2, uS (synaptic weights), nA.
+ * Variables are addressed as in the reference's VarDescriptor
+ * (utils.h, Simulate::getVarPtr simulate.cpp:143-184):
+ *   mech "global" (or "node"), var "v" | "d" | "rhs" | "a" | "b" | "area", idx = node
+ *   mech "capacitance", var "cm", idx = node
+ *   mech "na_ion" | "k_ion" | "ca_ion", var "erev" | "conci" | "conco" | "cur" | "dcurdv",
+ *        idx = NODE index (eion.cuh:270-300)
+ *   any other mechanism, var = column name, idx = instance index
+ *   mechanism globals (e.g. "hd_la" "ehd") through hx_model_set_global.
+ *
+ * The replacement binds to the reference's Python surface (heliox.Sim,
+ * src/python_api/PyBindings.cpp:15-266) through heliox_amd/sim.py.
+ */
+#ifndef HELIOX_AMD_H
+#define HELIOX_AMD_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct hx_sim hx_sim;
+
+/* SimWrapper::SimWrapper / ~SimWrapper (SimWrapper.cpp:18-36). */
+int hx_create(hx_sim** out);
+void hx_destroy(hx_sim* sim);
+/* Text of the last failure on this handle ("" if none). */
+const char* hx_last_error(hx_sim* sim);
+
+/* SimWrapper::set_device (SimWrapper.cpp): only "gpu" is served by this library. */
+int hx_set_device(hx_sim* sim, const char* dev);
+/* SimWrapper::set_dt / get_dt. */
+int hx_set_dt(hx_sim* sim, double dt);
+double hx_get_dt(hx_sim* sim);
+/* Model temperature (globals.dat "celsius", global_vars.cpp:12-88). */
+int hx_set_celsius(hx_sim* sim, double celsius);
+
+/* ---- model construction: replaces set_data_path + load_model, i.e. the
+ *      CoreNEURON reader read_coredat.cpp:36-1141 and
+ *      coredat_to_innerdat.cpp:42-603, with in-memory arrays.              */
+/* Node arrays: nodes [0, ncell) are roots (parent -1); parent[i] < i otherwise. */
+int hx_model_set_nodes(hx_sim* sim, int ncell, int nnode, const int* parent, const double* a,
+                       const double* b, const double* area);
+/* Mechanism instances by name (MechanismFactory::createMechanism, mechanism.h:125-164). */
+int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* node_indices);
+/* One parameter column, n values in instance order (read_data_from_coredat). */
+int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, const double* values);
+/* Mechanism global (GlobalVarNames, e.g. hd_la ehd/kl/vhalft/a0t/zetat/gmt/q10/qtl). */
+int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double value);
+/* Ion style bits per ion instance (eion.cuh:155-197: 04 conc init, 040 erev init, 0100 erev each step). */
+int hx_model_set_iontype(hx_sim* sim, const char* ion, int n, const int* iontype);
+/* Threshold detector of a real cell (PreSyn, presyn.cpp:133-177); returns the detector index. */
+int hx_model_add_presyn(hx_sim* sim, int gid, int node, double threshold);
+/* VecStim spike times of one instance (VecEvent::update_sequence, vecevent.cpp:292-309). */
+int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times);
+/* NetCon into synapse `target` instance `inst` (ExpSyn / Exp2Syn).  src_kind 0: detector index,
+ * 1: VecStim instance.  One source per synapse instance; a later netcon replaces an earlier one
+ * (coredat_to_innerdat.cpp:356-364). */
+int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double weight,
+                        double delay);
+/* Gap-junction transfer after each update: HalfGap[halfgap_inst].vgap = v[src_node]
+ * (Simulate::add_gap_source/add_gap_target, simulate.cpp:953-966). */
+int hx_model_add_gap(hx_sim* sim, int src_node, int halfgap_inst);
+/* SimWrapper::load_model: builds the solver layout and uploads the model to HBM. */
+int hx_load_model(hx_sim* sim);
+
+/* ---- step API (Simulate::finitialize/run/continue_run/fadvance, simulate.h:17-76) ---- */
+int hx_finitialize(hx_sim* sim, double v_init);
+int hx_run(hx_sim* sim, double tstop);
+int hx_continue_run(hx_sim* sim, double runtime);
+int hx_fadvance(hx_sim* sim);
+double hx_get_t(hx_sim* sim);
+
+/* ---- monitors (SimWrapper::add_monitor / get_monitor_data / flush_recorders) ---- */
+int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx);
+int hx_get_monitor_len(hx_sim* sim, int handle);
+int hx_get_monitor_data(hx_sim* sim, int handle, double* out, int cap);
+int hx_flush_recorders(hx_sim* sim);
+
+/* ---- variable handles (SimRuntimeCore handle cache, SimRuntimeCore.h:197-205) ---- */
+int hx_get_variable_handle(hx_sim* sim, const char* mech, const char* var, int idx);
+int hx_get_variable_by_handle(hx_sim* sim, int handle, double* out);
+int hx_set_variable_by_handle(hx_sim* sim, int handle, double value);
+int hx_get_variables_by_handles(hx_sim* sim, int n, const int* handles, double* out);
+int hx_get_variables_by_handles_f32_into(hx_sim* sim, int n, const int* handles, float* out);
+int hx_set_variables_by_handles(hx_sim* sim, int n, const int* handles, const double* values);
+int hx_get_variable_value(hx_sim* sim, const char* mech, const char* var, int idx, double* out);
+int hx_set_variable_value(hx_sim* sim, double value, const char* mech, const char* var, int idx);
+/* Whole column in instance (or node) order; returns the count written. */
+int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, int cap);
+
+/* ---- VecPlay (SimWrapper::add_vecplay/update_vecplay/remove_vecplay/has_vecplay) ---- */
+int hx_add_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tvec,
+                   const double* yvec);
+int hx_update_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tvec,
+                      const double* yvec);
+int hx_remove_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
+int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
+
+/* ---- spikes (Simulate::output_spikes simulate.cpp:892-909, get_spk_by_gid) ---- */
+int hx_get_spike_count(hx_sim* sim);
+int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap);
+int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap);
+
+/* ---- capacity and diagnostics ---- */
+/* Event-ring capacity per delivery step (default sized from the model). */
+int hx_set_event_capacity(hx_sim* sim, int per_step);
+/* enable = 1 (default): fold each step's state update into the next step's current pass when that is
+ * exact; 0: always run the reference's separate current and state passes. */
+int hx_set_fusion(hx_sim* sim, int enable);
+/* Per-kernel timing with HIP events on the library's stream: enable, then read
+ * accumulated milliseconds and launch counts for a kernel class
+ * ("mech", "sparse", "point", "solve", "spike", "events", "other"). */
+int hx_set_profiling(hx_sim* sim, int enable);
+int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches);
+/* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused". */
+long long hx_get_info(hx_sim* sim, const char* key);
+
+/* Host emulation of the device tree solve (no counterpart in the reference;
+ * a diagnostic for CPU-only checks of the solver schedule): capacitance and
+ * axial assembly, elimination and back substitution over the same chunk
+ * schedule the kernel uses, then v += dv.  Arrays are in node order; d and rhs
+ * hold the membrane-mechanism diagonal and right-hand side. */
+int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
+                          const double* cm, double cfac, double* v, const double* d, const double* rhs,
+                          int* nchunk_max, int* nround_max);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HELIOX_AMD_H */
