@@ -1,0 +1,180 @@
+"""Benchmark of the per-timestep simulation core on one MI355X.
+
+Workload: configuration 3 -- 2000 pyramidal-like cells x 5000 compartments
+(1e7 compartments), fp64, hh + pas + Ih (hd_la) + Ca_HVA + CaDynamics_E2 on
+every compartment, 200 Exp2Syn per cell driven by 5 Hz Poisson VecStim trains,
+dt = 0.025 ms.  A step is one fadvance of the whole model; inputs and state are
+resident in HBM before the timed region starts.
+
+Prints one JSON line:
+  value ........ compartment-steps/s of the whole job (1e7 x steps / wall time)
+  roofline ..... the dominant kernel (the fused mechanism kernel): algorithmic
+                 bytes per launch / its mean launch time from HIP events on the
+                 library's stream, against MI355X's 8 TB/s HBM peak
+  cpu_baseline . the CPU oracle (a restatement of the reference CPU step loop)
+                 on a bounded sample of the same workload, one host core
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "compartment-steps/s (2000×5000-comp fp64) + achieved HBM GB/s"
+
+# Algorithmic bytes per compartment for the fused mechanism kernel on this
+# workload: every per-compartment input read once, every state read and
+# written once, d and rhs written once (fp64):
+#   v 8 + (d, rhs) 16 + pas (g, e) 16 + hh (m,h,n r/w 48; gnabar, gkbar, gl, el 32;
+#   ena, ek 16) 96 + Ca_HVA (m,h r/w 32; gbar 8) 40 + hd_la (l r/w 16; ghdbar,
+#   vhalfl, tau 24) 40 + CaDynamics_E2 + ca_ion (cai r/w 16; gamma, decay, depth,
+#   minCai 32; cao 8) 56  =  272 B
+MECH_BYTES_PER_COMP = 272
+
+
+def _traffic_from_profiles():
+    """HBM bytes per launch of the mechanism kernel from the committed rocprof counter summary."""
+    path = os.path.join(ROOT, "profiles", "k_dense_config3_counters.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(ncell: int, nstep: int):
+    import oracle
+    from heliox_amd import build_config
+
+    spec = build_config(3, ncell, nstep * 0.025 + 1.0)
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(-65.0)
+    t0 = time.perf_counter()
+    o.nsteps(nstep)
+    el = time.perf_counter() - t0
+    rate = spec.nnode * nstep / el
+    return {"value": rate, "unit": "compartment-steps/s", "cores": 1, "kind": "port",
+            "sample": f"config 3, first {ncell} cells x 5000 compartments, {nstep} steps "
+                      f"({spec.nnode * nstep:.3g} compartment-steps, {el:.1f} s on one core)"}
+
+
+def calibrate_copy(gib: float = 1.0, reps: int = 5):
+    """A plain device copy of known size, for scaling rocprof FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    n = int(gib * (1 << 30) // 8)
+    x = torch.ones(n, dtype=torch.float64, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 8, "copy_bytes_written": n * 8, "reps": reps}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--ncell", type=int, default=2000, help="cells of config 3 (2000 = the benchmark)")
+    ap.add_argument("--cpu-cells", type=int, default=12)
+    ap.add_argument("--cpu-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (cells would be sharded "
+              "across GPUs with spike exchange; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
+
+    from heliox_amd import Sim, build_config
+
+    t_build = time.perf_counter()
+    tstop_needed = (args.warmup + args.steps + 10) * 0.025
+    spec = build_config(3, args.ncell, tstop_needed)
+    sim = Sim()
+    sim.load_model_from_spec(spec)
+    t_build = time.perf_counter() - t_build
+    nnode = spec.nnode
+    dt = spec.dt
+
+    sim.finitialize(-65.0)
+    if args.warmup:
+        sim.continue_run((args.warmup + 0.5) * dt)
+    sim.set_profiling(not args.no_kernel_timing)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sim.continue_run((args.steps + 0.5) * dt)      # returns after the stream is synchronized
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    value = nnode * args.steps / wall
+    ms_per_step = wall * 1e3 / args.steps
+    kernels = {}
+    for k in ("mech", "sparse", "point", "solve", "spike", "events", "other"):
+        ms, n = sim.kernel_time(k)
+        if n:
+            kernels[k] = {"ms_total": ms, "launches": n, "us_per_launch": ms * 1e3 / n}
+    roofline = None
+    if "mech" in kernels:
+        per_launch_s = kernels["mech"]["ms_total"] / kernels["mech"]["launches"] / 1e3
+        alg = MECH_BYTES_PER_COMP * nnode
+        achieved = alg / per_launch_s / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profiles(),
+                    "kernel": "k_dense (fused hh/pas/Ih/Ca_HVA/CaDynamics_E2 state+current)",
+                    "alg_bytes_per_launch": alg}
+    print(json.dumps({"kernel_times": kernels, "build_s": round(t_build, 2), "nnode": nnode,
+                      "spikes": sim.spikes()[0].size, "t_end": sim.get_t()}), file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_cells, args.cpu_steps)
+
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "compartment-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"config 3: {args.ncell} pyramidal-like cells x 5000 compartments, fp64, "
+                               f"hh+pas+Ih+Ca_HVA+CaDynamics_E2 everywhere, 200 Exp2Syn/cell with 5 Hz "
+                               f"Poisson VecStim input, dt 0.025 ms",
+                   "ncell": args.ncell, "compartments": nnode, "dt_ms": dt,
+                   "wall_s_per_simulated_s": ms_per_step * 40.0},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

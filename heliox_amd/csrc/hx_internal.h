@@ -78,25 +78,31 @@ struct StepArgs {
     MechConsts c;
 };
 
-// Chunked tree-solve schedule (one wavefront per cell).
+// Chunked tree-solve schedule (one wavefront per cell).  Indices are relative
+// to the cell (cells are limited to 65535 nodes and 65535 chunks), so a
+// descriptor packs into 12 bytes and a whole cell's schedule can be staged in
+// LDS next to the junction slots.
 struct ChunkDesc {
-    int start;        // cell-relative solver index of the chunk head (proximal node)
-    int len;          // nodes in the chunk (<= kChunk), head..tail contiguous
-    int slot;         // LDS slot of this chunk
-    int parent_slot;  // LDS slot of the chunk holding the head's parent (-1 for the root chunk)
-    int head_parent;  // cell-relative solver index of the head's parent (-1 for the root)
-    int child_begin;  // LDS slots of the chunks hanging off the tail: [child_begin, +child_count)
-    int child_count;
-    int pad;
+    uint16_t start;        // solver index of the first node of the chunk's round
+    uint16_t head_parent;  // solver index of the head's parent (kNone for the root chunk)
+    uint16_t slot;         // junction slot of this chunk
+    uint16_t parent_slot;  // slot of the chunk holding the head's parent
+    uint16_t child_begin;  // slots of the chunks hanging off the tail: [child_begin, +child_count)
+    uint8_t len;           // nodes in the chunk (<= kChunk); a round's chunks are sorted by len, longest first
+    uint8_t child_count;
 };
-constexpr int kChunk = 8;
+static_assert(sizeof(ChunkDesc) == 12, "ChunkDesc must stay 12 bytes");
+constexpr uint16_t kNone = 0xFFFF;
+constexpr int kChunk = 16;
 constexpr int kWave = 64;
+constexpr int kMaxCellNodes = 65535;
 
 struct SolveArgs {
     int ncell;
-    const int* cell_node_begin;   // [ncell+1]
-    const int* cell_round_begin;  // [ncell+1]
-    const int* round_desc_begin;  // [nround+1]
+    const int* cell_node_begin;   // [ncell+1] first solver-order node of each cell
+    const int* cell_desc_begin;   // [ncell+1] first descriptor of each cell
+    const int* cell_round_begin;  // [ncell+1] first round-table entry of each cell
+    const uint16_t* round_begin;  // per cell: nround+1 descriptor offsets (cell-relative)
     const ChunkDesc* desc;
     double* v;
     double* d;
@@ -178,6 +184,13 @@ struct VecPlayDev {
     double next_time;
 };
 
+// LDS bytes of the solve kernel: slots, then descriptors, then the round table
+inline size_t solve_lds_bytes(int max_chunks, int max_rounds) {
+    const int mc = max_chunks > 0 ? max_chunks : 1;
+    return static_cast<size_t>(mc) * (2 * sizeof(double) + sizeof(ChunkDesc)) +
+           static_cast<size_t>(max_rounds + 2) * sizeof(uint16_t);
+}
+
 // launch wrappers (kernels.hip)
 void launch_dense(const StepArgs& a, hipStream_t s);
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
@@ -185,7 +198,7 @@ void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);
-void launch_solve(const SolveArgs& a, int max_slots, hipStream_t s);
+void launch_solve(const SolveArgs& a, int max_chunks, int max_rounds, hipStream_t s);
 void launch_spike(const SpikeArgs& a, hipStream_t s);
 void launch_input(const InputArgs& a, hipStream_t s);
 void launch_deliver(const DeliverArgs& a, hipStream_t s);

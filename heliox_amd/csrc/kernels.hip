@@ -369,32 +369,72 @@ __global__ void k_set_v(double* v, int n, double val) {
 //   assembly: simulate.cpp:527-555, capacitance capac.cpp:68-80
 //   elimination / back substitution: simulate.cpp:558-581
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S) {
-    extern __shared__ double slots[];     // 2 doubles per chunk
+// The workgroup is exactly one wavefront: LDS accesses of a wavefront execute
+// in program order, so a round boundary only needs the compiler not to move
+// LDS accesses across it (no workgroup barrier, which would also wait for the
+// round's global stores to land).
+__device__ __forceinline__ void round_boundary() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Node k of this lane's chunk in a position-major round: the round's chunks are
+// sorted by length, so the lanes holding a k-th node are 0 .. W_k-1 and row k
+// starts after the rows 0..k-1 (W_j = lanes whose chunk is longer than j).
+__device__ __forceinline__ void round_indices(int len, int round_base, int lane, int* idx) {
+    int off = round_base;
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        const unsigned long long m = __ballot(len > k);
+        idx[k] = off + lane;
+        off += __popcll(m);
+    }
+}
+
+__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, int max_chunks) {
+    // LDS: junction slots (2 doubles per chunk), then the cell's descriptors and
+    // round table, staged once so that per-round metadata never waits on the
+    // global stores of the previous round
+    extern __shared__ double lds[];
+    double* slots = lds;
+    ChunkDesc* sdesc = reinterpret_cast<ChunkDesc*>(lds + 2 * max_chunks);
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
     const int nb = S.cell_node_begin[c];
-    const int r0 = S.cell_round_begin[c];
-    const int r1 = S.cell_round_begin[c + 1];
-
-    for (int r = r1 - 1; r >= r0; --r) {
-        const int db = S.round_desc_begin[r];
-        if (db + lane < S.round_desc_begin[r + 1])
-            chunk_forward(S.desc[db + lane], nb, S.v, S.d, S.rhs, S.a, S.b, S.cm, S.cfac, slots);
-        __syncthreads();
+    const int d0 = S.cell_desc_begin[c];
+    const int nd = S.cell_desc_begin[c + 1] - d0;
+    const int rb = S.cell_round_begin[c];
+    const int nround = S.cell_round_begin[c + 1] - rb - 1;
+    uint16_t* sround = reinterpret_cast<uint16_t*>(sdesc + nd);
+    {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.desc + d0);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(sdesc);
+        for (int i = lane; i < nd * 3; i += kWave) dst[i] = src[i];
+        for (int i = lane; i <= nround; i += kWave) sround[i] = S.round_begin[rb + i];
     }
-    for (int r = r0; r < r1; ++r) {
-        const int db = S.round_desc_begin[r];
+    __syncthreads();
+
+    ChunkDesc none{};
+    for (int r = nround - 1; r >= 0; --r) {
+        const int q = sround[r] + lane;
+        const bool act = q < sround[r + 1];
+        const ChunkDesc dsc = act ? sdesc[q] : none;
+        int idx[kChunk];
+        round_indices(dsc.len, nb + sdesc[sround[r]].start, lane, idx);
+        if (act) chunk_forward(dsc, idx, nb, S.v, S.d, S.rhs, S.a, S.b, S.cm, S.cfac, slots);
+        round_boundary();
+    }
+    for (int r = 0; r < nround; ++r) {
+        const int q = sround[r] + lane;
+        const bool act = q < sround[r + 1];
+        const ChunkDesc dsc = act ? sdesc[q] : none;
+        int idx[kChunk];
+        round_indices(dsc.len, nb + sdesc[sround[r]].start, lane, idx);
         double xtail = 0.0;
-        int myslot = -1;
-        if (db + lane < S.round_desc_begin[r + 1]) {
-            const ChunkDesc q = S.desc[db + lane];
-            xtail = chunk_back(q, nb, S.v, S.d, S.rhs, S.b, slots);
-            myslot = q.slot;
-        }
-        __syncthreads();
-        if (myslot >= 0) slots[2 * myslot] = xtail;
-        __syncthreads();
+        if (act) xtail = chunk_back(dsc, idx, S.v, S.d, S.rhs, S.b, slots);
+        round_boundary();
+        if (act) slots[2 * dsc.slot] = xtail;
+        round_boundary();
     }
 }
 
@@ -630,10 +670,10 @@ void launch_set_v(double* v, int n, double val, hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_set_v, grid_for(n), dim3(kBlock), 0, s, v, n, val);
 }
 
-void launch_solve(const SolveArgs& a, int max_slots, hipStream_t s) {
+void launch_solve(const SolveArgs& a, int max_chunks, int max_rounds, hipStream_t s) {
     if (a.ncell <= 0) return;
-    const size_t lds = static_cast<size_t>(max_slots > 0 ? max_slots : 1) * 2 * sizeof(double);
-    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a);
+    const size_t lds = solve_lds_bytes(max_chunks, max_rounds);
+    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a, max_chunks);
 }
 
 void launch_spike(const SpikeArgs& a, hipStream_t s) {

@@ -28,7 +28,7 @@
 #include <unordered_map>
 #include <vector>
 
-#include "../../include/heliox.h"
+#include "heliox.h"
 #include "hx_internal.h"
 #include "schedule.h"
 #include "solve_chunk.h"
@@ -194,7 +194,8 @@ struct hx_sim {
 
     // layout
     std::vector<int> node_perm, node_iperm;    // user <-> solver order
-    std::vector<int> cell_node_begin, cell_round_begin, round_desc_begin;
+    std::vector<int> cell_node_begin, cell_desc_begin, cell_round_begin;
+    std::vector<uint16_t> round_begin;   // per cell: nround+1 cell-relative descriptor offsets
     std::vector<ChunkDesc> descs;
     int max_slots = 0, max_rounds = 0;
     unsigned dense_mask = 0;
@@ -207,7 +208,8 @@ struct hx_sim {
     hipStream_t stream = nullptr;
     double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
            *d_area = nullptr;
-    int *d_cell_node_begin = nullptr, *d_cell_round_begin = nullptr, *d_round_desc_begin = nullptr;
+    int *d_cell_node_begin = nullptr, *d_cell_desc_begin = nullptr, *d_cell_round_begin = nullptr;
+    uint16_t* d_round_begin = nullptr;
     ChunkDesc* d_desc = nullptr;
     // spikes / events
     int npre = 0;
@@ -354,8 +356,9 @@ void hx_sim::build_layout() {
     node_perm.assign(nnode, -1);
     node_iperm.assign(nnode, -1);
     cell_node_begin.assign(ncell + 1, 0);
+    cell_desc_begin.assign(ncell + 1, 0);
     cell_round_begin.assign(ncell + 1, 0);
-    round_desc_begin.assign(1, 0);
+    round_begin.clear();
     descs.clear();
     max_slots = 0;
     max_rounds = 0;
@@ -377,15 +380,16 @@ void hx_sim::build_layout() {
             node_iperm[pos + s] = u;
         }
         pos += n;
-        cell_round_begin[c] = static_cast<int>(round_desc_begin.size()) - 1;
-        const int dbase = static_cast<int>(descs.size());
+        cell_desc_begin[c] = static_cast<int>(descs.size());
+        cell_round_begin[c] = static_cast<int>(round_begin.size());
         for (auto& d : cs.desc) descs.push_back(d);
-        for (int r = 1; r <= cs.nround; ++r) round_desc_begin.push_back(dbase + cs.round_begin[r]);
+        for (int x : cs.round_begin) round_begin.push_back(static_cast<uint16_t>(x));
         max_slots = std::max(max_slots, cs.nchunk);
         max_rounds = std::max(max_rounds, cs.nround);
     }
     cell_node_begin[ncell] = pos;
-    cell_round_begin[ncell] = static_cast<int>(round_desc_begin.size()) - 1;
+    cell_desc_begin[ncell] = static_cast<int>(descs.size());
+    cell_round_begin[ncell] = static_cast<int>(round_begin.size());
 
     // mechanism instance order: by solver-order node (stable)
     for (int id = 0; id < M_COUNT; ++id) {
@@ -454,18 +458,19 @@ void hx_sim::upload() {
     d_cm = dupload(owned, perm_nodes(cm));
     d_area = dupload(owned, perm_nodes(area));
     d_cell_node_begin = dupload(owned, cell_node_begin);
+    d_cell_desc_begin = dupload(owned, cell_desc_begin);
     d_cell_round_begin = dupload(owned, cell_round_begin);
-    d_round_desc_begin = dupload(owned, round_desc_begin);
+    d_round_begin = dupload(owned, round_begin);
     d_desc = dupload(owned, descs);
     {
         int dev = 0;
         hipDeviceProp_t prop;
         HXC(hipGetDevice(&dev));
         HXC(hipGetDeviceProperties(&prop, dev));
-        const size_t lds = static_cast<size_t>(std::max(max_slots, 1)) * 2 * sizeof(double);
+        const size_t lds = solve_lds_bytes(max_slots, max_rounds);
         if (lds > prop.sharedMemPerBlock)
             throw std::runtime_error("a cell has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
-                                     " B of junction slots exceed the " + std::to_string(prop.sharedMemPerBlock) +
+                                     " B solver schedule exceeds the " + std::to_string(prop.sharedMemPerBlock) +
                                      " B of LDS per workgroup");
     }
 
@@ -892,8 +897,9 @@ void hx_sim::step_once() {
     SolveArgs S{};
     S.ncell = ncell;
     S.cell_node_begin = d_cell_node_begin;
+    S.cell_desc_begin = d_cell_desc_begin;
     S.cell_round_begin = d_cell_round_begin;
-    S.round_desc_begin = d_round_desc_begin;
+    S.round_begin = d_round_begin;
     S.desc = d_desc;
     S.v = d_v;
     S.d = d_d;
@@ -903,7 +909,7 @@ void hx_sim::step_once() {
     S.cm = d_cm;
     S.cfac = 0.001 * (1.0 / dt);
     tbegin(T_SOLVE);
-    launch_solve(S, max_slots, stream);
+    launch_solve(S, max_slots, max_rounds, stream);
     tend(T_SOLVE);
     if (!gaps.empty()) {
         tbegin(T_OTHER);
@@ -1231,7 +1237,13 @@ int hx_load_model(hx_sim* sim) {
         if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", sim->mon_name[i].first.c_str(),
                                      sim->mon_name[i].second.c_str(), sim->mon_idx[i]);
         sim->mon_ref[i] = r;
+        if (r.klass == 1) {
+            // assigned outputs are sampled where the reference records them: split passes
+            sim->need_split_for_monitor = true;
+            sim->write_assigned = true;
+        }
     }
+    sim->recompute_fused();
     return 0;
     API_END
 }
@@ -1567,16 +1579,32 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
         std::vector<double> slots(2 * static_cast<size_t>(std::max(tmp.max_slots, 1)));
         for (int c = 0; c < ncell; ++c) {
             const int nb = tmp.cell_node_begin[c];
-            const int r0 = tmp.cell_round_begin[c], r1 = tmp.cell_round_begin[c + 1];
-            for (int r = r1 - 1; r >= r0; --r)
-                for (int q = tmp.round_desc_begin[r]; q < tmp.round_desc_begin[r + 1]; ++q)
-                    chunk_forward(tmp.descs[q], nb, gv.data(), gd.data(), gr.data(), ga.data(), gb.data(), gcm.data(),
+            const ChunkDesc* cd = tmp.descs.data() + tmp.cell_desc_begin[c];
+            const uint16_t* rt = tmp.round_begin.data() + tmp.cell_round_begin[c];
+            const int nround = tmp.cell_round_begin[c + 1] - tmp.cell_round_begin[c] - 1;
+            auto indices = [&](int r, int q, int* idx) {
+                int off = nb + cd[rt[r]].start;
+                for (int kk = 0; kk < kChunk; ++kk) {
+                    idx[kk] = off + (q - rt[r]);
+                    int w = 0;
+                    for (int j = rt[r]; j < rt[r + 1]; ++j) w += cd[j].len > kk;
+                    off += w;
+                }
+            };
+            int idx[kChunk];
+            for (int r = nround - 1; r >= 0; --r)
+                for (int q = rt[r]; q < rt[r + 1]; ++q) {
+                    indices(r, q, idx);
+                    chunk_forward(cd[q], idx, nb, gv.data(), gd.data(), gr.data(), ga.data(), gb.data(), gcm.data(),
                                   cfac, slots.data());
-            for (int r = r0; r < r1; ++r) {
+                }
+            for (int r = 0; r < nround; ++r) {
                 std::vector<std::pair<int, double>> tails;
-                for (int q = tmp.round_desc_begin[r]; q < tmp.round_desc_begin[r + 1]; ++q)
-                    tails.push_back({tmp.descs[q].slot, chunk_back(tmp.descs[q], nb, gv.data(), gd.data(), gr.data(),
-                                                                   gb.data(), slots.data())});
+                for (int q = rt[r]; q < rt[r + 1]; ++q) {
+                    indices(r, q, idx);
+                    tails.push_back({cd[q].slot, chunk_back(cd[q], idx, gv.data(), gd.data(), gr.data(), gb.data(),
+                                                            slots.data())});
+                }
                 for (auto& tl : tails) slots[2 * tl.first] = tl.second;
             }
         }
@@ -1597,7 +1625,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "nround_max") return sim->max_rounds;
     if (k == "dense_mask") return sim->dense_mask;
     if (k == "fused") return sim->fused ? 1 : 0;
-    if (k == "nround_total") return static_cast<long long>(sim->round_desc_begin.size()) - 1;
+    if (k == "nround_total") return static_cast<long long>(sim->round_begin.size()) - sim->ncell;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->ring.nslot;
     if (k == "event_cap") return sim->ring.cap;

@@ -10,7 +10,8 @@
 // independent, so they form rounds of up to 64 lanes.  Elimination walks the
 // rounds by increasing height, back substitution by decreasing height, with a
 // barrier between rounds.  Chunk ids are breadth-first so that the chunks
-// hanging off one tail are consecutive LDS slots.
+// hanging off one tail are consecutive LDS slots.  Each round is stored
+// position-major (see below) so its lanes access memory coalesced.
 #include <algorithm>
 #include <cstdint>
 #include <numeric>
@@ -74,25 +75,46 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         for (size_t s = 0; s < v.size(); s += lanes)
             rounds.emplace_back(v.begin() + s, v.begin() + std::min(v.size(), s + lanes));
     }
-    // solver order of the cell's nodes
-    std::vector<int> start(nchunk, 0);
+    // solver order of the cell's nodes.  Inside a round the chunks are sorted by
+    // length (longest first) and stored position-major: node k of every chunk
+    // that has one, then node k+1, ...  Node k of lane l sits at
+    // round_base + sum_{j<k} W_j + l, where W_j = number of chunks longer than j,
+    // so the lanes of a round read and write contiguous memory.
+    std::vector<int> round_base(rounds.size(), 0), lane_of(nchunk, 0), round_of(nchunk, 0);
+    std::vector<int> tail_pos(nchunk, 0);
     out.order.reserve(n);
-    for (auto& r : rounds)
-        for (int q : r) {
-            start[q] = static_cast<int>(out.order.size());
-            for (int nd : chunks[q].nodes) out.order.push_back(nd);
+    for (size_t ri = 0; ri < rounds.size(); ++ri) {
+        auto& r = rounds[ri];
+        round_base[ri] = static_cast<int>(out.order.size());
+        int maxlen = 0;
+        for (size_t l = 0; l < r.size(); ++l) {
+            lane_of[r[l]] = static_cast<int>(l);
+            round_of[r[l]] = static_cast<int>(ri);
+            maxlen = std::max(maxlen, chunks[r[l]].len);
         }
+        for (int k = 0; k < maxlen; ++k)
+            for (size_t l = 0; l < r.size(); ++l) {
+                const int q = r[l];
+                if (chunks[q].len > k) {
+                    if (k == chunks[q].len - 1) tail_pos[q] = static_cast<int>(out.order.size());
+                    out.order.push_back(chunks[q].nodes[k]);
+                }
+            }
+    }
+    if (n > kMaxCellNodes || nchunk > kMaxCellNodes)
+        throw std::runtime_error("cell too large for the solver schedule (max 65535 nodes)");
     out.round_begin.push_back(0);
-    for (auto& r : rounds) {
-        for (int q : r) {
+    for (size_t ri = 0; ri < rounds.size(); ++ri) {
+        for (int q : rounds[ri]) {
             ChunkDesc d{};
-            d.start = start[q];
-            d.len = chunks[q].len;
-            d.slot = q;
-            d.parent_slot = chunks[q].parent;
-            d.head_parent = chunks[q].parent >= 0 ? start[chunks[q].parent] + chunks[chunks[q].parent].len - 1 : -1;
-            d.child_begin = chunks[q].child_begin;
-            d.child_count = chunks[q].child_count;
+            d.start = static_cast<uint16_t>(round_base[ri]);
+            d.len = static_cast<uint8_t>(chunks[q].len);
+            d.slot = static_cast<uint16_t>(q);
+            d.parent_slot = chunks[q].parent >= 0 ? static_cast<uint16_t>(chunks[q].parent) : kNone;
+            d.head_parent = chunks[q].parent >= 0 ? static_cast<uint16_t>(tail_pos[chunks[q].parent]) : kNone;
+            d.child_begin = static_cast<uint16_t>(chunks[q].child_begin);
+            if (chunks[q].child_count > 255) throw std::runtime_error("node with more than 255 children");
+            d.child_count = static_cast<uint8_t>(chunks[q].child_count);
             out.desc.push_back(d);
         }
         out.round_begin.push_back(static_cast<int>(out.desc.size()));

@@ -135,8 +135,11 @@ class Sim:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h:
-            lib().hx_destroy(h)
+        if h and _lib is not None:
+            try:
+                _lib.hx_destroy(h)
+            except Exception:   # interpreter shutdown
+                pass
             self._h = None
 
     # --------------------------------------------------------------- helpers

@@ -1,0 +1,169 @@
+"""CPU-side checks of the HIP library: exported C ABI, host-side solver schedule,
+workload generator, and error behaviour that needs no GPU."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from heliox_amd import Sim, build_config, emulate_tree_solve, lib
+from heliox_amd.sim import SIGNATURES
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "heliox.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    L = lib()
+    syms = header_symbols()
+    assert len(syms) > 40
+    for s in syms:
+        assert hasattr(L, s), f"{s} declared in include/heliox.h but not exported"
+    # and the Python binding types every one of them
+    assert set(syms) == set(SIGNATURES), set(syms) ^ set(SIGNATURES)
+
+
+def test_nm_exports_match_header():
+    so = os.path.join(ROOT, "heliox_amd", "libheliox_amd.so")
+    out = os.popen(f"nm -D --defined-only {so}").read()
+    exported = set(re.findall(r"\b(hx_[a-z0-9_]+)\b", out))
+    assert set(header_symbols()) <= exported
+
+
+# ---------------------------------------------------------------------------
+# solver schedule (host emulation of the device tree solve)
+# ---------------------------------------------------------------------------
+def assemble_and_solve_reference(spec, v, dm, rm, cfac):
+    n = spec.nnode
+    d = dm + cfac * spec.cm
+    rhs = rm.copy()
+    p = spec.parent
+    for i in range(spec.ncell, n):
+        dv = v[p[i]] - v[i]
+        rhs[i] -= spec.b[i] * dv
+        rhs[p[i]] += spec.a[i] * dv
+    for i in range(spec.ncell, n):
+        d[i] -= spec.b[i]
+        d[p[i]] -= spec.a[i]
+    return v + oracle.solve_serial(spec.ncell, p, spec.a, spec.b, d, rhs)
+
+
+@pytest.mark.parametrize("config,ncell", [(1, 3), (2, 4), (3, 2), (4, 6), (5, 2)])
+def test_emulated_chunk_solve_matches_serial_hines(config, ncell):
+    spec = build_config(config, ncell, 1.0)
+    rng = np.random.default_rng(config)
+    n = spec.nnode
+    v = rng.uniform(-80, 20, n)
+    dm = rng.uniform(0.5, 2.0, n) * 1e-3
+    rm = rng.normal(0, 1e-3, n)
+    cfac = 1e-3 / 0.025
+    ref = assemble_and_solve_reference(spec, v, dm, rm, cfac)
+    got, nchunk, nround = emulate_tree_solve(spec.ncell, spec.parent, spec.a, spec.b, spec.cm, cfac, v, dm, rm)
+    dx = ref - v
+    assert np.max(np.abs(got - ref)) <= 1e-12 * max(1.0, np.max(np.abs(dx)))
+    assert nchunk > 0 and nround > 0
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_emulated_chunk_solve_random_trees(seed):
+    """Random shapes: chains longer than a chunk, bushy nodes, single-node cells."""
+    rng = np.random.default_rng(100 + seed)
+    ncell = int(rng.integers(1, 6))
+    sizes = rng.integers(1, 120, ncell)
+    parent = [-1] * ncell
+    a, b = [0.0] * ncell, [0.0] * ncell
+    for c in range(ncell):
+        local = [c]
+        for j in range(1, int(sizes[c])):
+            mode = rng.random()
+            if mode < 0.5:
+                p = local[-1]                       # extend a chain
+            elif mode < 0.8:
+                p = local[int(rng.integers(0, len(local)))]
+            else:
+                p = local[0]                        # many children on the root
+            parent.append(p)
+            local.append(len(parent) - 1)
+            a.append(-rng.uniform(0.05, 3))
+            b.append(-rng.uniform(0.05, 3))
+    # renumber so that roots come first and parent < child
+    n = len(parent)
+    parent = np.array(parent, np.int32)
+    order = list(range(ncell)) + [i for i in range(n) if i >= ncell]
+    assert all(parent[i] < i for i in range(ncell, n))
+    from heliox_amd.spec import ModelSpec
+    spec = ModelSpec(ncell=ncell, parent=parent, a=np.array(a), b=np.array(b), area=np.ones(n), cm=np.ones(n))
+    v = rng.uniform(-80, 20, n)
+    dm = rng.uniform(0.5, 2.0, n) * 1e-3
+    rm = rng.normal(0, 1e-3, n)
+    cfac = 40.0
+    ref = assemble_and_solve_reference(spec, v, dm, rm, cfac)
+    got, _, _ = emulate_tree_solve(ncell, parent, spec.a, spec.b, spec.cm, cfac, v, dm, rm)
+    assert np.max(np.abs(got - ref)) <= 1e-12 * max(1.0, np.max(np.abs(ref - v)))
+
+
+# ---------------------------------------------------------------------------
+# workload generator
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("config,ncell,nper", [(1, 5, 101), (2, 3, 500), (3, 2, 5000), (4, 4, 200), (5, 3, 500)])
+def test_generator_shapes(config, ncell, nper):
+    spec = build_config(config, ncell, 50.0)
+    spec.validate()
+    assert spec.ncell == ncell and spec.nnode == ncell * nper
+    cell = spec.cell_of_node()
+    assert np.all(np.bincount(cell) == nper)
+    assert np.all(spec.area > 0) and np.all(spec.a[spec.ncell:] < 0) and np.all(spec.b[spec.ncell:] < 0)
+
+
+def test_generator_cells_do_not_depend_on_model_size():
+    small = build_config(3, 2, 20.0)
+    big = build_config(3, 5, 20.0)
+    cs = small.cell_of_node()
+    cb = big.cell_of_node()
+    for c in range(2):
+        assert np.array_equal(small.a[cs == c], big.a[cb == c])
+        assert np.array_equal(small.b[cs == c], big.b[cb == c])
+    assert np.array_equal(small.vecstim_times, big.vecstim_times[: small.vecstim_times.size])
+
+
+def test_generator_is_deterministic():
+    x = build_config(2, 3, 100.0)
+    y = build_config(2, 3, 100.0)
+    assert np.array_equal(x.parent, y.parent) and np.array_equal(x.a, y.a)
+    assert np.array_equal(x.vecstim_times, y.vecstim_times)
+    assert np.array_equal(x.netcons["ExpSyn"].weight, y.netcons["ExpSyn"].weight)
+
+
+# ---------------------------------------------------------------------------
+# error behaviour (reference convention: -1 and a message, never an abort)
+# ---------------------------------------------------------------------------
+def test_error_paths_without_gpu():
+    s = Sim()
+    assert s.set_device("cpu") == -1 and "gpu" in s.last_error()
+    L = lib()
+    h = s.handle
+    # mechanisms need nodes first; unknown mechanism names are rejected
+    nodes = np.array([0], np.int32)
+    assert L.hx_model_insert(h, b"hh", 1, nodes.ctypes.data_as(__import__("ctypes").POINTER(__import__("ctypes").c_int))) == -1
+    parent = np.array([-1, 0], np.int32)
+    a = np.array([0.0, -1.0])
+    C = __import__("ctypes")
+    dp = lambda x: x.ctypes.data_as(C.POINTER(C.c_double))
+    ip = lambda x: x.ctypes.data_as(C.POINTER(C.c_int))
+    bad_parent = np.array([-1, 1], np.int32)
+    assert L.hx_model_set_nodes(h, 1, 2, ip(bad_parent), dp(a), dp(a), dp(a)) == -1
+    assert L.hx_model_set_nodes(h, 1, 2, ip(parent), dp(a), dp(a), dp(np.array([1.0, 1.0]))) == 0
+    assert L.hx_model_insert(h, b"not_a_mech", 1, ip(nodes)) == -1
+    assert "unknown mechanism" in s.last_error()
+    assert L.hx_model_insert(h, b"pas", 2, ip(np.array([0, 0], np.int32))) == -1   # density mech twice on a node
+    assert L.hx_model_insert(h, b"pas", 2, ip(np.array([0, 1], np.int32))) == 0
+    assert L.hx_model_set_param(h, b"pas", b"nope", 2, dp(a)) == -1
+    assert L.hx_model_add_netcon(h, 0, 0, b"ExpSyn", 0, 1.0, 1.0) == -1
+    assert L.hx_finitialize(h, -65.0) == -1 and "not loaded" in s.last_error()
+    assert s.get_variable_handle("global", "v", 0) == -1

@@ -1,0 +1,167 @@
+"""Wider parity cases of the HIP path against the CPU oracle: active networks,
+events at the delivery-window boundaries, gap junctions, VecPlay, state
+columns, split-mode monitors, handles, stepping APIs and full-size models."""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle
+from heliox_amd import Sim, build_config
+from heliox_amd.spec import MechSpec, NetConSpec
+from parity_util import V_TOL, compare_spikes, run_both
+
+pytestmark = pytest.mark.gpu
+
+
+def active_network(ncell=60, seed=5, tstop=60.0, wscale=3.0):
+    """Config-4 wiring made active: 1 ms current pulses every 10 ms on a third
+    of the cells, recurrent weights rescaled, delays spread down to 0 and
+    exactly dt/2."""
+    spec = build_config(4, ncell, tstop)
+    rng = np.random.default_rng(seed)
+    nc = spec.netcons["ExpSyn"]
+    nc.weight = nc.weight * wscale
+    d = nc.delay.copy()
+    d[::7] = 0.0
+    d[3::11] = 0.0125
+    d[5::13] = rng.uniform(0.0, 0.1, d[5::13].size)
+    nc.delay = d
+    drive = np.arange(0, ncell, 3, dtype=np.int32)
+    starts = np.arange(2.0, tstop, 10.0)
+    nodes = np.repeat(drive, starts.size)
+    dl = np.tile(starts, drive.size) + rng.uniform(0, 3, nodes.size)
+    ic = spec.mechs["IClamp"]
+    spec.mechs["IClamp"] = MechSpec(np.concatenate([ic.nodes, nodes]),
+                                    {"delay": np.concatenate([ic.params["delay"], dl]),
+                                     "dur": np.concatenate([ic.params["dur"], np.full(nodes.size, 1.0)]),
+                                     "amp": np.concatenate([ic.params["amp"], np.full(nodes.size, 2.0)])})
+    return spec
+
+
+@pytest.mark.parametrize("fusion", [True, False])
+def test_active_network_with_gaps_and_vecplay(gpu_lib, fusion):
+    spec = active_network()
+    print(f"case active network ncell={spec.ncell} fusion={fusion}", flush=True)
+    o, g = run_both(spec, 60.0, fusion=fusion)
+    n = compare_spikes(o, g, spec.dt)
+    assert n > 50, "the network should be active"
+    err = float(np.max(np.abs(o.traces() - g.traces())))
+    print(f"  spikes {n}, max |dv| {err:.3e}", flush=True)
+    assert err < V_TOL
+    assert np.max(np.abs(o.array("ExpSyn", "g") - g.get_array("ExpSyn", "g"))) < 1e-12
+    assert np.max(np.abs(o.array("HalfGap", "vgap") - g.get_array("HalfGap", "vgap"))) < V_TOL
+
+
+def test_vecstim_boundary_delays(gpu_lib):
+    spec = build_config(2, 8, 80.0)
+    nc = spec.netcons["ExpSyn"]
+    rng = np.random.default_rng(2)
+    nc.delay = rng.choice([0.0, 0.0125, 0.025, 0.0375, 0.3, 2.5], nc.delay.size)
+    nc.weight = nc.weight * 30
+    # force some trains to have elements inside one window and out of order
+    t = spec.vecstim_times.copy()
+    t[::5] = np.round(t[::5] / 0.0125) * 0.0125
+    spec.vecstim_times = t
+    print("case vecstim boundary delays", flush=True)
+    o, g = run_both(spec, 80.0)
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+    assert np.max(np.abs(o.array("ExpSyn", "g") - g.get_array("ExpSyn", "g"))) < 1e-12
+    compare_spikes(o, g, spec.dt)
+
+
+@pytest.mark.parametrize("config,ncell", [(3, 2), (2, 4), (4, 30)])
+def test_state_columns(gpu_lib, config, ncell):
+    spec = build_config(config, ncell, 30.0)
+    print(f"case state columns config={config}", flush=True)
+    o, g = run_both(spec, 30.0)
+    checks = {"hh": ("m", "h", "n"), "Exp2Syn": ("A", "B"), "ExpSyn": ("g",), "hd_la": ("l",), "Ca_HVA": ("m", "h")}
+    for mech, cols in checks.items():
+        if mech not in spec.mechs:
+            continue
+        for c in cols:
+            err = np.max(np.abs(o.array(mech, c) - g.get_array(mech, c)))
+            assert err < 1e-9, f"{mech}.{c}: {err}"
+    if "ca_ion" in spec.mechs:
+        assert np.max(np.abs(o.array("ca_ion", "conci") - g.get_array("ca_ion", "conci"))) < 1e-12
+        assert np.max(np.abs(o.array("ca_ion", "erev") - g.get_array("ca_ion", "erev"))) < 1e-8
+
+
+def test_monitors_on_assigned_variables_use_split_schedule(gpu_lib):
+    spec = build_config(3, 1, 20.0)
+    mons = [("global", "v", 0), ("hh", "ina", 0), ("hh", "minf", 5), ("Ca_HVA", "ica", 11), ("ca_ion", "cur", 3),
+            ("hd_la", "i", 7), ("pas", "i", 2), ("CaDynamics_E2", "cai", 9), ("Exp2Syn", "g", 0)]
+    print("case assigned-variable monitors", flush=True)
+    o, g = run_both(spec, 20.0, monitors=mons)
+    assert g.info("fused") == 0
+    to, tg = o.traces(), g.traces()
+    for i, m in enumerate(mons):
+        scale = max(1.0, float(np.max(np.abs(to[i]))))
+        err = np.max(np.abs(to[i] - tg[i])) / scale
+        assert err < 1e-9, f"monitor {m}: {err}"
+
+
+def test_state_monitors_keep_fused_schedule(gpu_lib):
+    spec = build_config(3, 1, 20.0)
+    mons = [("global", "v", 0), ("hh", "m", 0), ("hd_la", "l", 40), ("Exp2Syn", "A", 0), ("ca_ion", "conci", 3)]
+    o, g = run_both(spec, 20.0, monitors=mons)
+    assert g.info("fused") == 1
+    assert np.max(np.abs(o.traces() - g.traces())) < 1e-9
+
+
+def test_stepping_apis_agree(gpu_lib):
+    """run, continue_run in chunks and fadvance give the same trajectory."""
+    spec = build_config(2, 3, 30.0)
+    o, g = run_both(spec, 0.0, chunks=[5.0, 2.5, 7.5])
+    for _ in range(12):
+        o.fadvance()
+        g.fadvance()
+    assert o.t == g.get_t()
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+
+
+def test_handles_and_reinitialisation(gpu_lib):
+    spec = build_config(1, 3, 40.0)
+    o, g = run_both(spec, 20.0)
+    # change a parameter through a handle on both and continue
+    h = g.get_variable_handle("IClamp", "amp", 1)
+    assert h >= 0
+    g.set_variable_by_handle(h, 0.9)
+    o.set("IClamp", "amp", 1, 0.9)
+    assert g.get_variable_by_handle(h) == 0.9
+    hv = g.get_variable_handle("global", "v", 1)
+    assert abs(g.get_variable_by_handle(hv) - o.get("global", "v", 1)) < V_TOL
+    g.set_variable_value(0.0, "IClamp", "delay", 2)
+    o.set("IClamp", "delay", 2, 0.0)
+    o.continue_run(20.0)
+    g.continue_run(20.0)
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+    compare_spikes(o, g, spec.dt)
+    # finitialize + run twice reproduces the same trajectory on the GPU
+    g.finitialize(-65.0)
+    g.continue_run(40.0)
+    first = g.traces().copy()
+    g.finitialize(-65.0)
+    g.continue_run(40.0)
+    assert np.array_equal(first, g.traces())
+
+
+@pytest.mark.parametrize("config,ncell,nref", [(3, 2000, 3), (2, 10000, 4)])
+def test_full_size_prefix(gpu_lib, config, ncell, nref):
+    """Cells of configs 2 and 3 are independent, so the first cells of the
+    full-size GPU model must match an oracle model of just those cells."""
+    tstop = 5.0
+    full = build_config(config, ncell, tstop)
+    small = build_config(config, nref, tstop)
+    mons = [("global", "v", i) for i in range(nref)]
+    print(f"case full-size prefix config={config} ncell={ncell}", flush=True)
+    g = Sim()
+    g.load_model_from_spec(dataclasses.replace(full, monitors=mons))
+    g.finitialize(-65.0)
+    g.run(tstop)
+    o = oracle.OracleSim(small, monitors=mons)
+    o.finitialize(-65.0)
+    o.run(tstop)
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+    v = g.get_array("global", "v")
+    assert np.all(np.isfinite(v))

@@ -1,0 +1,426 @@
+"""Pin the CPU oracle against mathematics it must reproduce.
+
+The reference ships no golden vectors for this path (its tests need NEURON and a
+CUDA build), so each oracle function is checked against a closed form, an
+independent textbook restatement, an invariant, or brute force -- chosen so that
+a plausible transcription mistake (sign, index, dropped term, swapped operand)
+fails.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from heliox_amd.spec import MechSpec, ModelSpec, NetConSpec, VecPlaySpec
+
+F = 1.602176634e-19 * 6.02214076e23
+R = 1.380649e-23 * 6.02214076e23
+
+
+def single_compartment(area=1000.0, cm=1.0, dt=0.025, celsius=6.3):
+    return ModelSpec(ncell=1, parent=np.array([-1], np.int32), a=np.zeros(1), b=np.zeros(1),
+                     area=np.array([area]), cm=np.array([cm]), dt=dt, celsius=celsius)
+
+
+# ---------------------------------------------------------------------------
+# tree solve (simulate.cpp:558-581)
+# ---------------------------------------------------------------------------
+def random_forest(rng, ncell, n):
+    parent = -np.ones(n, np.int32)
+    for i in range(ncell, n):
+        parent[i] = rng.integers(0, i)
+    a = -rng.uniform(0.1, 2.0, n)
+    b = -rng.uniform(0.1, 2.0, n)
+    a[:ncell] = 0
+    b[:ncell] = 0
+    return parent, a, b
+
+
+def dense_matrix(parent, a, b, d):
+    n = len(parent)
+    M = np.diag(d.copy())
+    for i in range(n):
+        p = parent[i]
+        if p >= 0:
+            M[i, p] = b[i]
+            M[p, i] = a[i]
+    return M
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_solve_serial_equals_dense_solve(seed):
+    rng = np.random.default_rng(seed)
+    ncell = int(rng.integers(1, 4))
+    n = int(rng.integers(ncell + 1, 64))
+    parent, a, b = random_forest(rng, ncell, n)
+    # the reference's matrix: d holds the full diagonal, a/b the off-diagonals
+    d = rng.uniform(5.0, 10.0, n)
+    rhs = rng.normal(size=n)
+    x = oracle.solve_serial(ncell, parent, a, b, d, rhs)
+    x_dense = np.linalg.solve(dense_matrix(parent, a, b, d), rhs)
+    assert np.allclose(x, x_dense, rtol=1e-12, atol=1e-12)
+
+
+def test_solve_serial_single_node():
+    x = oracle.solve_serial(1, np.array([-1]), np.zeros(1), np.zeros(1), np.array([4.0]), np.array([2.0]))
+    assert x[0] == 0.5
+
+
+def test_solve_serial_relabel_invariant():
+    """Renumbering nodes (keeping parent < child) permutes the solution."""
+    rng = np.random.default_rng(7)
+    n = 40
+    parent, a, b = random_forest(rng, 1, n)
+    d = rng.uniform(5, 9, n)
+    rhs = rng.normal(size=n)
+    x = oracle.solve_serial(1, parent, a, b, d, rhs)
+    # a different topological order: breadth-first relabelling
+    children = [[] for _ in range(n)]
+    for i in range(1, n):
+        children[parent[i]].append(i)
+    order = [0]
+    for u in order:
+        order.extend(children[u][::-1])
+    new = np.empty(n, int)
+    new[order] = np.arange(n)
+    p2 = np.array([-1] + [new[parent[u]] for u in order[1:]], np.int32)
+    x2 = oracle.solve_serial(1, p2, a[order], b[order], d[order], rhs[order])
+    assert np.allclose(x2, x[order], rtol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# passive compartment + IClamp (capacitance capac.cpp:54-80, backward Euler)
+# ---------------------------------------------------------------------------
+def test_passive_iclamp_backward_euler_closed_form():
+    dt, area, cm, g, e, amp = 0.025, 800.0, 1.3, 2e-4, -70.0, 0.2
+    spec = single_compartment(area=area, cm=cm, dt=dt)
+    spec.mechs["pas"] = MechSpec(np.array([0], np.int32), {"g_pas": np.array([g]), "e_pas": np.array([e])})
+    spec.mechs["IClamp"] = MechSpec(np.array([0], np.int32), {"delay": np.array([1.0]), "dur": np.array([2.0]),
+                                                              "amp": np.array([amp])})
+    spec.monitors = [("global", "v", 0)]
+    o = oracle.OracleSim(spec)
+    o.finitialize(-65.0)
+    o.run(5.0)
+    v = o.traces()[0]
+    cfac = 1e-3 / dt
+    iscale = amp * 1e2 / area
+    vv, t, ref = -65.0, 0.0, [-65.0]
+    for _ in range(len(v) - 1):
+        tmid = t + 0.5 * dt
+        inj = iscale if (1.0 <= tmid < 3.0) else 0.0
+        vv = (cfac * cm * vv + g * e + inj) / (g + cfac * cm)
+        t = tmid + 0.5 * dt
+        ref.append(vv)
+    assert np.allclose(v, ref, rtol=0, atol=1e-10)
+
+
+def test_sealed_cable_steady_state():
+    """A long passive cable with current injected at one end reaches the
+    analytic sealed-end profile V(x) ~ cosh((L - x)/lambda) / cosh(L/lambda)."""
+    nseg, L, diam, Ra, g, e = 200, 1000.0, 2.0, 100.0, 1e-4, -65.0
+    dx = L / nseg
+    area = np.full(nseg, math.pi * diam * dx)
+    rhalf = 1e-2 * Ra * (dx / 2) / (math.pi * (diam / 2) ** 2)
+    gax = 1.0 / (2 * rhalf)
+    parent = np.arange(-1, nseg - 1, dtype=np.int32)
+    a = np.full(nseg, -1e2 * gax / area[0])
+    b = np.full(nseg, -1e2 * gax / area[0])
+    a[0] = b[0] = 0
+    spec = ModelSpec(ncell=1, parent=parent, a=a, b=b, area=area, cm=np.ones(nseg), dt=0.1)
+    spec.mechs["pas"] = MechSpec(np.arange(nseg, dtype=np.int32), {"g_pas": np.full(nseg, g), "e_pas": np.full(nseg, e)})
+    spec.mechs["IClamp"] = MechSpec(np.array([0], np.int32), {"delay": np.array([0.0]), "dur": np.array([1e9]),
+                                                              "amp": np.array([0.05])})
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(e)
+    o.run(500.0)
+    v = o.array("global", "v") - e
+    lam = math.sqrt((diam * 1e-4) / (4 * Ra * g)) * 1e4     # um
+    x = (np.arange(nseg) + 0.5) * dx
+    shape = np.cosh((L - x) / lam)
+    shape = shape / shape[0] * v[0]
+    assert np.max(np.abs(v - shape)) / v[0] < 2e-2
+
+
+# ---------------------------------------------------------------------------
+# hh (hh_templated.cu) against the textbook Hodgkin-Huxley rate functions
+# ---------------------------------------------------------------------------
+def hh_textbook(v, celsius=6.3):
+    q10 = 3.0 ** ((celsius - 6.3) / 10)
+
+    def lin(x, y):   # x / (1 - exp(-x/y)) with its limit y at x = 0
+        return y if abs(x) < 1e-12 else x / (1 - math.exp(-x / y))
+
+    am = 0.1 * lin(v + 40, 10)
+    bm = 4 * math.exp(-(v + 65) / 18)
+    ah = 0.07 * math.exp(-(v + 65) / 20)
+    bh = 1 / (1 + math.exp(-(v + 35) / 10))
+    an = 0.01 * lin(v + 55, 10)
+    bn = 0.125 * math.exp(-(v + 65) / 80)
+    return (am / (am + bm), 1 / (q10 * (am + bm)), ah / (ah + bh), 1 / (q10 * (ah + bh)),
+            an / (an + bn), 1 / (q10 * (an + bn)))
+
+
+def hh_cell(v_init, celsius=6.3):
+    spec = single_compartment(celsius=celsius)
+    n = np.array([0], np.int32)
+    spec.mechs["hh"] = MechSpec(n, {"gnabar": np.array([0.12]), "gkbar": np.array([0.036]), "gl": np.array([3e-4]),
+                                    "el": np.array([-54.3])})
+    spec.mechs["na_ion"] = MechSpec(n.copy(), {"erev": np.array([50.0])}, iontype=np.zeros(1, np.int32))
+    spec.mechs["k_ion"] = MechSpec(n.copy(), {"erev": np.array([-77.0])}, iontype=np.zeros(1, np.int32))
+    return spec
+
+
+@pytest.mark.parametrize("v0", [-80.0, -65.0, -40.0, -20.0, 10.0])
+@pytest.mark.parametrize("celsius", [6.3, 16.3])
+def test_hh_init_matches_textbook_rates(v0, celsius):
+    o = oracle.OracleSim(hh_cell(v0, celsius), monitors=[])
+    o.finitialize(v0)
+    got = [o.get("hh", k, 0) for k in ("minf", "mtau", "hinf", "htau", "ninf", "ntau")]
+    ref = hh_textbook(v0, celsius)
+    assert np.allclose(got, ref, rtol=1e-12)
+    assert o.get("hh", "m", 0) == got[0] and o.get("hh", "h", 0) == got[2] and o.get("hh", "n", 0) == got[4]
+
+
+def test_hh_fd_jacobian_equals_conductance():
+    """The FD Jacobian (I(v+0.001)-I(v))/0.001 of hh is gna+gk+gl because the
+    current is linear in v at fixed gates (mech_template.cuh:616-626)."""
+    o = oracle.OracleSim(hh_cell(-60.0), monitors=[])
+    o.finitialize(-60.0)
+    m, h, n = (o.get("hh", k, 0) for k in ("m", "h", "n"))
+    g = 0.12 * m ** 3 * h + 0.036 * n ** 4 + 3e-4
+    cfac = 1e-3 / 0.025
+    d = o.array("global", "d")[0]        # after finitialize: mech g + capacitance
+    assert abs((d - cfac) - g) / g < 1e-6
+    i = 0.12 * m ** 3 * h * (-60 - 50) + 0.036 * n ** 4 * (-60 + 77) + 3e-4 * (-60 + 54.3)
+    assert abs(o.array("global", "rhs")[0] + i) < 1e-12
+
+
+def test_hh_gates_fixed_point_at_clamp():
+    """With v held (huge capacitance), gates initialised at x_inf stay there."""
+    spec = hh_cell(-30.0)
+    spec.cm[:] = 1e12
+    o = oracle.OracleSim(spec, monitors=[("hh", "m", 0), ("hh", "n", 0)])
+    o.finitialize(-30.0)
+    o.run(5.0)
+    m = o.monitor(0)
+    n = o.monitor(1)
+    assert np.max(np.abs(m - m[0])) < 1e-9 and np.max(np.abs(n - n[0])) < 1e-9
+
+
+# ---------------------------------------------------------------------------
+# synapses: cnexp decays are exact exponentials; Exp2Syn peak is normalised
+# ---------------------------------------------------------------------------
+def synapse_cell(mech, params, times, weight, delay=0.0):
+    spec = single_compartment()
+    n = np.array([0], np.int32)
+    spec.mechs["pas"] = MechSpec(n, {"g_pas": np.array([1e-4]), "e_pas": np.array([-65.0])})
+    spec.mechs[mech] = MechSpec(n.copy(), {k: np.array([v]) for k, v in params.items()})
+    spec.mechs["VecStim"] = MechSpec(n.copy(), {})
+    spec.vecstim_offsets = np.array([0, len(times)])
+    spec.vecstim_times = np.asarray(times, float)
+    spec.netcons[mech] = NetConSpec(np.array([0], np.int32), np.array([1], np.int8), np.array([0], np.int32),
+                                    np.array([weight]), np.array([delay]))
+    return spec
+
+
+def test_expsyn_decay_closed_form():
+    tau, w = 2.0, 0.003
+    spec = synapse_cell("ExpSyn", {"tau": tau, "e": 0.0}, [0.1], w, delay=0.0)
+    o = oracle.OracleSim(spec, monitors=[("ExpSyn", "g", 0)])
+    o.finitialize(-65.0)
+    o.run(20.0)
+    g = o.monitor(0)
+    k0 = int(np.argmax(g > 0))
+    n = np.arange(len(g) - k0)
+    ref = g[k0] * np.exp(-n * 0.025 / tau)
+    assert np.allclose(g[k0:], ref, rtol=1e-12)
+    # the event (weight w) lands before the first state update of its step
+    assert abs(g[k0] - w * math.exp(-0.025 / tau)) < 1e-15
+
+
+def test_exp2syn_peak_is_weight():
+    t1, t2, w = 0.5, 5.0, 0.002
+    spec = synapse_cell("Exp2Syn", {"tau1": t1, "tau2": t2, "e": 0.0}, [0.1], w)
+    o = oracle.OracleSim(spec, monitors=[("Exp2Syn", "A", 0), ("Exp2Syn", "B", 0)])
+    o.finitialize(-65.0)
+    o.run(30.0)
+    g = o.monitor(1) - o.monitor(0)
+    tp = t1 * t2 / (t2 - t1) * math.log(t2 / t1)
+    assert abs(g.max() / w - 1) < 2e-3        # sampled within one dt of the peak
+    k0 = int(np.argmax(g > 0))
+    n = np.arange(len(g) - k0) + 1
+    f = 1 / (math.exp(-tp / t2) - math.exp(-tp / t1))
+    ref = w * f * (np.exp(-n * 0.025 / t2) - np.exp(-n * 0.025 / t1))
+    assert np.allclose(g[k0:], ref, rtol=1e-9, atol=1e-18)
+
+
+# ---------------------------------------------------------------------------
+# ions and calcium dynamics
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("celsius", [6.3, 34.0])
+def test_nernst_closed_form(celsius):
+    spec = single_compartment(celsius=celsius)
+    n = np.array([0], np.int32)
+    spec.mechs["ca_ion"] = MechSpec(n, {"conci": np.array([5e-5]), "conco": np.array([2.0])},
+                                    iontype=np.array([0o4 | 0o40 | 0o100], np.int32))
+    spec.mechs["CaDynamics_E2"] = MechSpec(n.copy(), {})
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(-65.0)
+    ref = 1000 * R * (celsius + 273.15) / F / 2 * math.log(2.0 / 5e-5)
+    assert abs(o.get("ca_ion", "erev", 0) - ref) < 1e-12
+
+
+def test_cadynamics_relaxation_closed_form():
+    """With no calcium current, cai relaxes to minCai with time constant decay."""
+    spec = single_compartment()
+    n = np.array([0], np.int32)
+    spec.mechs["ca_ion"] = MechSpec(n, {"conci": np.array([5e-5]), "conco": np.array([2.0])},
+                                    iontype=np.array([0o4 | 0o40 | 0o100], np.int32))
+    spec.mechs["CaDynamics_E2"] = MechSpec(n.copy(), {"decay": np.array([80.0]), "minCai": np.array([1e-4])})
+    o = oracle.OracleSim(spec, monitors=[("ca_ion", "conci", 0)])
+    o.finitialize(-65.0)
+    o.run(100.0)
+    c = o.monitor(0)
+    k = np.arange(len(c))
+    ref = 1e-4 + (5e-5 - 1e-4) * np.exp(-k * 0.025 / 80.0)
+    assert np.allclose(c, ref, rtol=1e-11)
+
+
+def test_cahva_and_ih_steady_states():
+    """Gates start at their steady state (Ca_HVA mInf/hInf, hd_la linf) at v_init."""
+    spec = single_compartment()
+    n = np.array([0], np.int32)
+    spec.mechs["ca_ion"] = MechSpec(n, {}, iontype=np.array([0o4 | 0o40 | 0o100], np.int32))
+    spec.mechs["Ca_HVA"] = MechSpec(n.copy(), {"gbar": np.array([1e-4])})
+    spec.mechs["hd_la"] = MechSpec(n.copy(), {"ghdbar": np.array([1e-4])})
+    o = oracle.OracleSim(spec, monitors=[])
+    v = -52.0
+    o.finitialize(v)
+    ma = 0.055 * (-27 - v) / (math.exp((-27 - v) / 3.8) - 1)
+    mb = 0.94 * math.exp((-75 - v) / 17)
+    ha = 0.000457 * math.exp((-13 - v) / 50)
+    hb = 0.0065 / (math.exp((-v - 15) / 28) + 1)
+    assert abs(o.get("Ca_HVA", "m", 0) - ma / (ma + mb)) < 1e-14
+    assert abs(o.get("Ca_HVA", "h", 0) - ha / (ha + hb)) < 1e-14
+    linf = 1 / (1 + math.exp(-(v + 81) / -8))
+    assert abs(o.get("hd_la", "l", 0) - linf) < 1e-14
+    qt = 4.5 ** ((6.3 - 33) / 10)
+    a = math.exp(0.0378 * 2.2 * (v + 75))
+    taul = math.exp(0.0378 * 2.2 * 0.4 * (v + 75)) / (qt * 0.011 * (1 + a))
+    assert abs(o.get("hd_la", "taul", 0) / taul - 1) < 1e-13
+
+
+# ---------------------------------------------------------------------------
+# spike delivery: brute force of the receive rule (postsyn.cpp:43-61)
+# ---------------------------------------------------------------------------
+def step_times(dt, nstep):
+    t = [0.0]
+    for _ in range(nstep):
+        x = t[-1]
+        x += 0.5 * dt
+        x += 0.5 * dt
+        t.append(x)
+    return np.array(t)
+
+
+@pytest.mark.parametrize("delay", [0.0, 0.0125, 0.0126, 0.5, 1.0, 1.37])
+def test_vecstim_delivery_step_rule(delay):
+    dt = 0.025
+    times = [0.3, 0.31, 2.0125, 4.7]
+    spec = synapse_cell("ExpSyn", {"tau": 1e9, "e": 0.0}, times, 1e-3, delay=delay)
+    o = oracle.OracleSim(spec, monitors=[("ExpSyn", "g", 0)])
+    o.finitialize(-65.0)
+    o.run(8.0)
+    g = o.monitor(0)
+    # brute force: a VecStim element e fires at the first step k with e <= t_k + dt/2,
+    # stamped t_k; its target receives at the first step m >= k with t_k + delay <= t_m + dt/2
+    t = step_times(dt, len(g))
+    expect = np.zeros(len(g))
+    for e in times:
+        k = int(np.argmax(e <= t + dt / 2))
+        m = k + int(np.argmax(t[k] + delay <= t[k:] + dt / 2))
+        expect[m + 1:] += 1e-3   # sample j is taken at the end of step j-1: step m's delivery shows in sample m+1
+    assert np.allclose(g, expect, atol=1e-15)
+
+
+def test_threshold_detection_and_netcon_delay():
+    """A driven hh cell spikes (stamped with the step-start time, no
+    interpolation, presyn.cpp:150) and its netcon delivers after the delay."""
+    spec = hh_cell(-65.0)
+    n = np.array([0], np.int32)
+    spec.mechs["IClamp"] = MechSpec(n.copy(), {"delay": np.array([1.0]), "dur": np.array([5.0]),
+                                               "amp": np.array([0.5])})
+    spec.mechs["ExpSyn"] = MechSpec(n.copy(), {"tau": np.array([1e9]), "e": np.array([0.0])})
+    spec.presyn_gid = np.array([7], np.int32)
+    spec.presyn_node = np.array([0], np.int32)
+    spec.presyn_thr = np.array([0.0])
+    spec.netcons["ExpSyn"] = NetConSpec(np.array([0], np.int32), np.array([0], np.int8), np.array([0], np.int32),
+                                        np.array([1e-9]), np.array([1.0]))
+    spec.monitors = [("global", "v", 0), ("ExpSyn", "g", 0)]
+    o = oracle.OracleSim(spec)
+    o.finitialize(-65.0)
+    o.run(10.0)
+    v = o.monitor(0)
+    g = o.monitor(1)
+    ts, gid = o.spikes()
+    assert len(ts) >= 1 and np.all(gid == 7)
+    t = step_times(0.025, len(v))
+    # spike at step k: v at the start of step k (sample k) exceeds 0 for the first time
+    k = int(np.argmax(v > 0.0))
+    assert abs(ts[0] - t[k]) < 1e-12
+    m = k + int(np.argmax(t[k] + 1.0 <= t[k:] + 0.0125))
+    assert g[m] == 0.0 and g[m + 1] > 0.0
+
+
+# ---------------------------------------------------------------------------
+# VecPlay: linear interpolation (vecplay.cu:57-79)
+# ---------------------------------------------------------------------------
+def test_vecplay_linear_interpolation():
+    spec = single_compartment()
+    n = np.array([0], np.int32)
+    spec.mechs["pas"] = MechSpec(n, {})
+    spec.mechs["IClamp"] = MechSpec(n.copy(), {"delay": np.array([0.0]), "dur": np.array([1e9])})
+    tv = np.array([0.0, 1.0, 1.0, 3.0, 10.0])
+    yv = np.array([0.0, 2.0, 4.0, -1.0, 6.0])
+    spec.vecplay = [VecPlaySpec("IClamp", "amp", 0, tv, yv)]
+    o = oracle.OracleSim(spec, monitors=[("IClamp", "amp", 0)])
+    o.finitialize(-65.0)
+    o.run(12.0)
+    amp = o.monitor(0)
+    t = step_times(0.025, len(amp) - 1)
+
+    def interp(x):
+        if x <= tv[0]:
+            return yv[0]
+        if x >= tv[-1]:     # past the last point the reference keeps extrapolating the last segment
+            return yv[-2] + (yv[-1] - yv[-2]) * (x - tv[-2]) / (tv[-1] - tv[-2])
+        j = int(np.searchsorted(tv, x, side="right"))
+        return yv[j - 1] + (yv[j] - yv[j - 1]) * (x - tv[j - 1]) / (tv[j] - tv[j - 1])
+
+    ref = np.array([interp(x) for x in t])
+    assert np.allclose(amp, ref, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Adam (optimizer.cpp:351-393) against Kingma & Ba
+# ---------------------------------------------------------------------------
+def test_adam_closed_form():
+    rng = np.random.default_rng(3)
+    w = rng.normal(size=4)
+    w0 = w.copy()
+    m = np.zeros(4)
+    v = np.zeros(4)
+    gsz = np.array([1, 2, 3, 1], np.int32)
+    lr, b1, b2, eps, imp, inv = 1e-3, 0.9, 0.999, 1e-8, 2.0, 0.5
+    mr = np.zeros(4)
+    vr = np.zeros(4)
+    wr = w0.copy()
+    for step in range(1, 6):
+        grads = rng.normal(size=gsz.sum())
+        oracle.adam_step(w, grads, gsz, m, v, step, lr, inv, imp, b1, b2, eps)
+        g = np.add.reduceat(grads, np.r_[0, np.cumsum(gsz)[:-1]]) / gsz * imp * inv
+        mr = b1 * mr + (1 - b1) * g
+        vr = b2 * vr + (1 - b2) * g * g
+        wr = wr - lr * (mr / (1 - b1 ** step)) / (np.sqrt(vr / (1 - b2 ** step)) + eps)
+    assert np.allclose(w, wr, rtol=1e-14)
