@@ -80,33 +80,49 @@ struct StepArgs {
 
 // Chunked tree-solve schedule (one wavefront per cell).  Indices are relative
 // to the cell (cells are limited to 65535 nodes and 65535 chunks), so a
-// descriptor packs into 12 bytes and a whole cell's schedule can be staged in
-// LDS next to the junction slots.
+// descriptor packs into 8 bytes.
+constexpr uint16_t kNone = 0xFFFF;
+constexpr int kChunk = 16;        // max nodes per chunk (one lane's serial run)
+constexpr int kWave = 64;
+constexpr int kMaxCellNodes = 65535;
+constexpr int kRoundMax = 192;    // max nodes per round (one LDS stage)
+constexpr int kPer = kRoundMax / kWave;   // stage elements per lane per array
+constexpr int kDepth = 3;         // rounds loaded ahead of the one being solved
+
 struct ChunkDesc {
-    uint16_t start;        // solver index of the first node of the chunk's round
-    uint16_t head_parent;  // solver index of the head's parent (kNone for the root chunk)
-    uint16_t slot;         // junction slot of this chunk
-    uint16_t parent_slot;  // slot of the chunk holding the head's parent
+    uint16_t slot;         // junction slot of this chunk (its breadth-first id)
+    uint16_t parent_slot;  // slot of the chunk whose tail is the head's parent (kNone for the root chunk)
     uint16_t child_begin;  // slots of the chunks hanging off the tail: [child_begin, +child_count)
     uint8_t len;           // nodes in the chunk (<= kChunk); a round's chunks are sorted by len, longest first
     uint8_t child_count;
 };
-static_assert(sizeof(ChunkDesc) == 12, "ChunkDesc must stay 12 bytes");
-constexpr uint16_t kNone = 0xFFFF;
-constexpr int kChunk = 16;
-constexpr int kWave = 64;
-constexpr int kMaxCellNodes = 65535;
+static_assert(sizeof(ChunkDesc) == 8, "ChunkDesc must stay 8 bytes");
+
+// One round of a cell's schedule: its descriptors and its contiguous,
+// position-major block of nodes (all cell-relative).  Node k of the chunk on
+// lane l sits at node_base + off[k] + l, where off[k] = sum_{j<k} W_j and W_j
+// is the number of the round's chunks longer than j.
+struct alignas(16) RoundInfo {
+    uint16_t desc_begin;
+    uint16_t desc_count;
+    uint16_t node_base;
+    uint16_t node_count;
+    uint8_t off[kChunk];
+    uint32_t pad[2];
+};
+static_assert(sizeof(RoundInfo) == 32, "RoundInfo must stay 32 bytes");
 
 struct SolveArgs {
     int ncell;
     const int* cell_node_begin;   // [ncell+1] first solver-order node of each cell
     const int* cell_desc_begin;   // [ncell+1] first descriptor of each cell
-    const int* cell_round_begin;  // [ncell+1] first round-table entry of each cell
-    const uint16_t* round_begin;  // per cell: nround+1 descriptor offsets (cell-relative)
+    const int* cell_round_begin;  // [ncell+1] first round of each cell
+    const RoundInfo* rounds;
     const ChunkDesc* desc;
     double* v;
-    double* d;
-    double* rhs;
+    double* d;                    // in: assembled diagonal; out: eliminated diagonal D
+    double* rhs;                  // in: assembled right-hand side; out: solution x (v += x)
+    double* w;                    // scratch: b / D per node, written by elimination
     const double* a;
     const double* b;
     const double* cm;
@@ -184,11 +200,15 @@ struct VecPlayDev {
     double next_time;
 };
 
-// LDS bytes of the solve kernel: slots, then descriptors, then the round table
-inline size_t solve_lds_bytes(int max_chunks, int max_rounds) {
+// LDS of the solve kernel: two junction values per chunk, then one round
+// stage of kStageArrays arrays, each with a neutral entry and a write sink
+// after its kRoundMax nodes.
+constexpr int kStageArrays = 5;
+constexpr int kStageStride = kRoundMax + 2;
+inline size_t solve_lds_bytes(int max_chunks) {
     const int mc = max_chunks > 0 ? max_chunks : 1;
-    return static_cast<size_t>(mc) * (2 * sizeof(double) + sizeof(ChunkDesc)) +
-           static_cast<size_t>(max_rounds + 2) * sizeof(uint16_t);
+    return static_cast<size_t>(mc) * 2 * sizeof(double) +
+           static_cast<size_t>(kStageArrays * kStageStride) * sizeof(double);
 }
 
 // launch wrappers (kernels.hip)
@@ -198,7 +218,7 @@ void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);
-void launch_solve(const SolveArgs& a, int max_chunks, int max_rounds, hipStream_t s);
+void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s);
 void launch_spike(const SpikeArgs& a, hipStream_t s);
 void launch_input(const InputArgs& a, hipStream_t s);
 void launch_deliver(const DeliverArgs& a, hipStream_t s);

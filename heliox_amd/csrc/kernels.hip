@@ -371,70 +371,302 @@ __global__ void k_set_v(double* v, int n, double val) {
 // ---------------------------------------------------------------------------
 // The workgroup is exactly one wavefront: LDS accesses of a wavefront execute
 // in program order, so a round boundary only needs the compiler not to move
-// LDS accesses across it (no workgroup barrier, which would also wait for the
-// round's global stores to land).
+// LDS accesses across it (a workgroup barrier would also wait for the round's
+// global stores to land).
 __device__ __forceinline__ void round_boundary() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
 }
 
-// Node k of this lane's chunk in a position-major round: the round's chunks are
-// sorted by length, so the lanes holding a k-th node are 0 .. W_k-1 and row k
-// starts after the rows 0..k-1 (W_j = lanes whose chunk is longer than j).
-__device__ __forceinline__ void round_indices(int len, int round_base, int lane, int* idx) {
-    int off = round_base;
+constexpr int kNeutral = kRoundMax;       // stage entry holding the padding value
+constexpr int kSink = kRoundMax + 1;      // stage entry absorbing padding writes
+
+// 1/x: hardware reciprocal estimate refined by two Newton-Raphson steps
+// (each step squares the relative error), correct to about an ulp.
+__device__ __forceinline__ double rcp_nr(double x) {
+    double r = __builtin_amdgcn_rcp(x);
+    double e = __builtin_fma(-x, r, 1.0);
+    r = __builtin_fma(r, e, r);
+    e = __builtin_fma(-x, r, 1.0);
+    return __builtin_fma(r, e, r);
+}
+
+// A RoundInfo on its way in: every lane loads the same 32 bytes with vector
+// loads issued a round ahead of use (the schedule's scalar reads would have
+// to wait for the round's vector stores), then moves them to uniform
+// registers.
+struct RoundV {
+    uint4 lo, hi;
+};
+struct RoundU {
+    int desc_begin, desc_count, node_base, node_count;
+    uint32_t off[4];      // off[k] in byte k % 4 of off[k / 4]
+    __device__ __forceinline__ int offset(int k) const { return (off[k >> 2] >> (8 * (k & 3))) & 0xFF; }
+};
+__device__ __forceinline__ RoundV load_round(const RoundInfo* rounds, int r) {
+    const uint4* p = reinterpret_cast<const uint4*>(rounds + r);
+    return {p[0], p[1]};
+}
+__device__ __forceinline__ RoundU uniform_round(const RoundV& v) {
+    RoundU u;
+    const uint32_t w0 = __builtin_amdgcn_readfirstlane(v.lo.x);
+    const uint32_t w1 = __builtin_amdgcn_readfirstlane(v.lo.y);
+    u.desc_begin = w0 & 0xFFFF;
+    u.desc_count = w0 >> 16;
+    u.node_base = w1 & 0xFFFF;
+    u.node_count = w1 >> 16;
+    u.off[0] = __builtin_amdgcn_readfirstlane(v.lo.z);
+    u.off[1] = __builtin_amdgcn_readfirstlane(v.lo.w);
+    u.off[2] = __builtin_amdgcn_readfirstlane(v.hi.x);
+    u.off[3] = __builtin_amdgcn_readfirstlane(v.hi.y);
+    return u;
+}
+
+// Round data in flight: every lane loads kPer elements of each array of the
+// round's contiguous node block (coalesced, unconditional, clamped to the
+// block) plus its chunk descriptor, so each round issues the same number of
+// vector-memory instructions and the compiler's wait counts stay static.
+struct FwdBuf {
+    double x[6][kPer];    // d rhs a b v cm
+    uint2 q;              // ChunkDesc
+    RoundU ri;
+};
+struct BackBuf {
+    double x[3][kPer];    // u (rhs) w v
+    uint2 q;
+    RoundU ri;
+};
+
+struct SolveCtx {
+    const SolveArgs& S;
+    const RoundInfo* __restrict__ rounds;   // this cell's rounds
+    const uint2* __restrict__ desc;         // this cell's descriptors
+    int nb;                                 // first node of the cell
+    double* slots;                          // LDS, 2 per chunk
+    double* stage;                          // LDS, kStageArrays x kStageStride
+    int lane;
+};
+
+// Stage positions of the lane's chunk: read from the neutral entry and write
+// to the sink past the chunk's length.
+__device__ __forceinline__ void round_positions(const RoundU& ri, int len, int lane, int* rp, int* wp) {
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const unsigned long long m = __ballot(len > k);
-        idx[k] = off + lane;
-        off += __popcll(m);
+        const int p = ri.offset(k) + lane;
+        rp[k] = k < len ? p : kNeutral;
+        wp[k] = k < len ? p : kSink;
     }
 }
 
-__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, int max_chunks) {
-    // LDS: junction slots (2 doubles per chunk), then the cell's descriptors and
-    // round table, staged once so that per-round metadata never waits on the
-    // global stores of the previous round
+struct StageIn {
+    const double* stage;
+    const int* rp;
+    __device__ __forceinline__ double operator()(int arr, int k) const { return stage[arr * kStageStride + rp[k]]; }
+};
+
+__device__ __forceinline__ unsigned clamp_index(int lane, int j, int count) {
+    const unsigned e = static_cast<unsigned>(lane + kWave * j);
+    const unsigned last = static_cast<unsigned>(count - 1);
+    return e < last ? e : last;
+}
+
+__device__ __forceinline__ uint2 load_desc(const SolveCtx& C, const RoundU& ri) {
+    const int top = ri.desc_count > 0 ? ri.desc_count - 1 : 0;
+    return C.desc[ri.desc_begin + (C.lane < top ? C.lane : top)];
+}
+
+__device__ __forceinline__ void fwd_load(const SolveCtx& C, FwdBuf& B, const RoundV& rv) {
+    const RoundU ri = uniform_round(rv);
+    const int base = C.nb + ri.node_base;
+    const double* d = C.S.d + base;
+    const double* rhs = C.S.rhs + base;
+    const double* a = C.S.a + base;
+    const double* b = C.S.b + base;
+    const double* v = C.S.v + base;
+    const double* cm = C.S.cm + base;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const unsigned e = clamp_index(C.lane, j, ri.node_count);
+        B.x[0][j] = d[e];
+        B.x[1][j] = rhs[e];
+        B.x[2][j] = a[e];
+        B.x[3][j] = b[e];
+        B.x[4][j] = v[e];
+        B.x[5][j] = cm[e];
+    }
+    B.q = load_desc(C, ri);
+    B.ri = ri;
+}
+
+__device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B) {
+    const RoundU& ri = B.ri;
+    double* st = C.stage;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int e = C.lane + kWave * j;
+        st[SA_DB * kStageStride + e] = B.x[0][j] + C.S.cfac * B.x[5][j];
+        st[SA_RM * kStageStride + e] = B.x[1][j];
+        st[SA_A * kStageStride + e] = B.x[2][j];
+        st[SA_B * kStageStride + e] = B.x[3][j];
+        st[SA_V * kStageStride + e] = B.x[4][j];
+    }
+    round_boundary();
+    const bool act = C.lane < ri.desc_count;
+    const int slot = B.q.x & 0xFFFF;
+    const bool has_parent = (B.q.x >> 16) != kNone;
+    const int child_begin = B.q.y & 0xFFFF;
+    const int len = act ? (B.q.y >> 16) & 0xFF : 0;
+    const int nchild = act ? B.q.y >> 24 : 0;
+    double acd = 0.0, ace = 0.0;
+    for (int ch = 0; ch < nchild; ++ch) {
+        acd += C.slots[2 * (child_begin + ch)];
+        ace += C.slots[2 * (child_begin + ch) + 1];
+    }
+    int rp[kChunk], wp[kChunk];
+    round_positions(ri, len, C.lane, rp, wp);
+    double cd, ce;
+    chunk_forward_math(
+        len, has_parent, StageIn{st, rp},
+        [&](int k, double D, double u, double w) {
+            st[SA_DB * kStageStride + wp[k]] = D;
+            st[SA_RM * kStageStride + wp[k]] = u;
+            st[SA_B * kStageStride + wp[k]] = w;
+        },
+        rcp_nr, acd, ace, cd, ce);
+    if (act && has_parent) {
+        C.slots[2 * slot] = cd;
+        C.slots[2 * slot + 1] = ce;
+    }
+    round_boundary();
+    if (ri.desc_count > 0) {   // padding rounds write nothing
+        const int base = C.nb + ri.node_base;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const unsigned e = clamp_index(C.lane, j, ri.node_count);
+            C.S.d[base + e] = st[SA_DB * kStageStride + e];
+            C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
+            C.S.w[base + e] = st[SA_B * kStageStride + e];
+        }
+    }
+    round_boundary();
+}
+
+__device__ __forceinline__ void back_load(const SolveCtx& C, BackBuf& B, const RoundV& rv) {
+    const RoundU ri = uniform_round(rv);
+    const int base = C.nb + ri.node_base;
+    const double* u = C.S.rhs + base;
+    const double* w = C.S.w + base;
+    const double* v = C.S.v + base;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const unsigned e = clamp_index(C.lane, j, ri.node_count);
+        B.x[0][j] = u[e];
+        B.x[1][j] = w[e];
+        B.x[2][j] = v[e];
+    }
+    B.q = load_desc(C, ri);
+    B.ri = ri;
+}
+
+__device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B) {
+    const RoundU& ri = B.ri;
+    double* st = C.stage;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int e = C.lane + kWave * j;
+        st[SA_RM * kStageStride + e] = B.x[0][j];
+        st[SA_A * kStageStride + e] = B.x[1][j];
+        st[SA_V * kStageStride + e] = B.x[2][j];
+    }
+    round_boundary();
+    const bool act = C.lane < ri.desc_count;
+    const int slot = B.q.x & 0xFFFF;
+    const int parent_slot = B.q.x >> 16;
+    const int len = act ? (B.q.y >> 16) & 0xFF : 0;
+    const double vpar = (act && parent_slot != kNone) ? C.slots[2 * parent_slot] : 0.0;
+    int rp[kChunk], wp[kChunk];
+    round_positions(ri, len, C.lane, rp, wp);
+    const double vtail = chunk_back_math(len, StageIn{st, rp},
+                                         [&](int k, double vn, double x) {
+                                             st[SA_V * kStageStride + wp[k]] = vn;
+                                             st[SA_RM * kStageStride + wp[k]] = x;
+                                         },
+                                         vpar);
+    if (act) C.slots[2 * slot] = vtail;
+    round_boundary();
+    if (ri.desc_count > 0) {
+        const int base = C.nb + ri.node_base;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const unsigned e = clamp_index(C.lane, j, ri.node_count);
+            C.S.v[base + e] = st[SA_V * kStageStride + e];
+            C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
+        }
+    }
+    round_boundary();
+}
+
+// One wavefront per cell.  Elimination walks the rounds from the leaves
+// (round nround-1) to the root, back substitution from the root out; the data
+// of the next kDepth rounds and the round table entry after them are in
+// flight while a round is solved.  A cell's round count is a multiple of
+// kDepth (the schedule appends padding rounds with no chunks), so each loop
+// trip solves exactly kDepth rounds; round indices past either end are
+// clamped to a real round, whose loads are issued but never used.
+__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* __restrict__ rounds_all,
+                                                 const uint2* __restrict__ desc, int max_chunks) {
     extern __shared__ double lds[];
-    double* slots = lds;
-    ChunkDesc* sdesc = reinterpret_cast<ChunkDesc*>(lds + 2 * max_chunks);
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
-    const int nb = S.cell_node_begin[c];
-    const int d0 = S.cell_desc_begin[c];
-    const int nd = S.cell_desc_begin[c + 1] - d0;
     const int rb = S.cell_round_begin[c];
-    const int nround = S.cell_round_begin[c + 1] - rb - 1;
-    uint16_t* sround = reinterpret_cast<uint16_t*>(sdesc + nd);
-    {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(S.desc + d0);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(sdesc);
-        for (int i = lane; i < nd * 3; i += kWave) dst[i] = src[i];
-        for (int i = lane; i <= nround; i += kWave) sround[i] = S.round_begin[rb + i];
-    }
-    __syncthreads();
+    const int nround = S.cell_round_begin[c + 1] - rb;
+    const int last = nround - 1;
+    double* slots = lds;
+    double* stage = slots + 2 * max_chunks;
+    if (lane < kStageArrays) stage[lane * kStageStride + kNeutral] = lane == SA_DB ? 1.0 : 0.0;
+    round_boundary();
+    const RoundInfo* rounds = rounds_all + rb;
+    const SolveCtx C{S, rounds, desc + S.cell_desc_begin[c], S.cell_node_begin[c], slots, stage, lane};
+    auto fwd_idx = [&](int r) { return r > 0 ? r : 0; };
+    auto back_idx = [&](int r) { return r < last ? r : last; };
 
-    ChunkDesc none{};
-    for (int r = nround - 1; r >= 0; --r) {
-        const int q = sround[r] + lane;
-        const bool act = q < sround[r + 1];
-        const ChunkDesc dsc = act ? sdesc[q] : none;
-        int idx[kChunk];
-        round_indices(dsc.len, nb + sdesc[sround[r]].start, lane, idx);
-        if (act) chunk_forward(dsc, idx, nb, S.v, S.d, S.rhs, S.a, S.b, S.cm, S.cfac, slots);
-        round_boundary();
+    {
+        FwdBuf b0, b1, b2;
+        fwd_load(C, b0, load_round(rounds, fwd_idx(last)));
+        fwd_load(C, b1, load_round(rounds, fwd_idx(last - 1)));
+        fwd_load(C, b2, load_round(rounds, fwd_idx(last - 2)));
+        RoundV nx = load_round(rounds, fwd_idx(last - 3));
+        for (int r = last; r >= 0; r -= kDepth) {
+            fwd_round(C, b0);
+            RoundV n = load_round(rounds, fwd_idx(r - 4));
+            fwd_load(C, b0, nx);
+            fwd_round(C, b1);
+            nx = load_round(rounds, fwd_idx(r - 5));
+            fwd_load(C, b1, n);
+            fwd_round(C, b2);
+            n = load_round(rounds, fwd_idx(r - 6));
+            fwd_load(C, b2, nx);
+            nx = n;
+        }
     }
-    for (int r = 0; r < nround; ++r) {
-        const int q = sround[r] + lane;
-        const bool act = q < sround[r + 1];
-        const ChunkDesc dsc = act ? sdesc[q] : none;
-        int idx[kChunk];
-        round_indices(dsc.len, nb + sdesc[sround[r]].start, lane, idx);
-        double xtail = 0.0;
-        if (act) xtail = chunk_back(dsc, idx, S.v, S.d, S.rhs, S.b, slots);
-        round_boundary();
-        if (act) slots[2 * dsc.slot] = xtail;
-        round_boundary();
+    {
+        BackBuf b0, b1, b2;
+        back_load(C, b0, load_round(rounds, back_idx(0)));
+        back_load(C, b1, load_round(rounds, back_idx(1)));
+        back_load(C, b2, load_round(rounds, back_idx(2)));
+        RoundV nx = load_round(rounds, back_idx(3));
+        for (int r = 0; r <= last; r += kDepth) {
+            back_round(C, b0);
+            RoundV n = load_round(rounds, back_idx(r + 4));
+            back_load(C, b0, nx);
+            back_round(C, b1);
+            nx = load_round(rounds, back_idx(r + 5));
+            back_load(C, b1, n);
+            back_round(C, b2);
+            n = load_round(rounds, back_idx(r + 6));
+            back_load(C, b2, nx);
+            nx = n;
+        }
     }
 }
 
@@ -670,10 +902,11 @@ void launch_set_v(double* v, int n, double val, hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_set_v, grid_for(n), dim3(kBlock), 0, s, v, n, val);
 }
 
-void launch_solve(const SolveArgs& a, int max_chunks, int max_rounds, hipStream_t s) {
+void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
     if (a.ncell <= 0) return;
-    const size_t lds = solve_lds_bytes(max_chunks, max_rounds);
-    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a, max_chunks);
+    const size_t lds = solve_lds_bytes(max_chunks);
+    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a, a.rounds,
+                       reinterpret_cast<const uint2*>(a.desc), max_chunks);
 }
 
 void launch_spike(const SpikeArgs& a, hipStream_t s) {

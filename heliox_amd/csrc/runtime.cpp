@@ -195,7 +195,7 @@ struct hx_sim {
     // layout
     std::vector<int> node_perm, node_iperm;    // user <-> solver order
     std::vector<int> cell_node_begin, cell_desc_begin, cell_round_begin;
-    std::vector<uint16_t> round_begin;   // per cell: nround+1 cell-relative descriptor offsets
+    std::vector<RoundInfo> rounds;       // all cells' rounds, cell by cell
     std::vector<ChunkDesc> descs;
     int max_slots = 0, max_rounds = 0;
     unsigned dense_mask = 0;
@@ -207,9 +207,9 @@ struct hx_sim {
     std::vector<void*> owned;
     hipStream_t stream = nullptr;
     double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
-           *d_area = nullptr;
+           *d_area = nullptr, *d_w = nullptr;
     int *d_cell_node_begin = nullptr, *d_cell_desc_begin = nullptr, *d_cell_round_begin = nullptr;
-    uint16_t* d_round_begin = nullptr;
+    RoundInfo* d_rounds = nullptr;
     ChunkDesc* d_desc = nullptr;
     // spikes / events
     int npre = 0;
@@ -358,7 +358,7 @@ void hx_sim::build_layout() {
     cell_node_begin.assign(ncell + 1, 0);
     cell_desc_begin.assign(ncell + 1, 0);
     cell_round_begin.assign(ncell + 1, 0);
-    round_begin.clear();
+    rounds.clear();
     descs.clear();
     max_slots = 0;
     max_rounds = 0;
@@ -372,7 +372,7 @@ void hx_sim::build_layout() {
             lp[j] = (j == 0) ? -1 : local[parent[u]];
         }
         CellSchedule cs;
-        build_cell_schedule(lp, kChunk, kWave, cs);
+        build_cell_schedule(lp, kChunk, kWave, kRoundMax, cs);
         cell_node_begin[c] = pos;
         for (int s = 0; s < n; ++s) {
             const int u = cnodes[cbeg[c] + cs.order[s]];
@@ -381,15 +381,15 @@ void hx_sim::build_layout() {
         }
         pos += n;
         cell_desc_begin[c] = static_cast<int>(descs.size());
-        cell_round_begin[c] = static_cast<int>(round_begin.size());
+        cell_round_begin[c] = static_cast<int>(rounds.size());
         for (auto& d : cs.desc) descs.push_back(d);
-        for (int x : cs.round_begin) round_begin.push_back(static_cast<uint16_t>(x));
+        for (auto& r : cs.rounds) rounds.push_back(r);
         max_slots = std::max(max_slots, cs.nchunk);
         max_rounds = std::max(max_rounds, cs.nround);
     }
     cell_node_begin[ncell] = pos;
     cell_desc_begin[ncell] = static_cast<int>(descs.size());
-    cell_round_begin[ncell] = static_cast<int>(round_begin.size());
+    cell_round_begin[ncell] = static_cast<int>(rounds.size());
 
     // mechanism instance order: by solver-order node (stable)
     for (int id = 0; id < M_COUNT; ++id) {
@@ -453,6 +453,7 @@ void hx_sim::upload() {
     HXC(hipMemset(d_v, 0, sizeof(double) * nnode));
     HXC(hipMemset(d_d, 0, sizeof(double) * nnode));
     HXC(hipMemset(d_rhs, 0, sizeof(double) * nnode));
+    d_w = dalloc<double>(owned, nnode);
     d_a = dupload(owned, perm_nodes(a));
     d_b = dupload(owned, perm_nodes(b));
     d_cm = dupload(owned, perm_nodes(cm));
@@ -460,14 +461,14 @@ void hx_sim::upload() {
     d_cell_node_begin = dupload(owned, cell_node_begin);
     d_cell_desc_begin = dupload(owned, cell_desc_begin);
     d_cell_round_begin = dupload(owned, cell_round_begin);
-    d_round_begin = dupload(owned, round_begin);
+    d_rounds = dupload(owned, rounds);
     d_desc = dupload(owned, descs);
     {
         int dev = 0;
         hipDeviceProp_t prop;
         HXC(hipGetDevice(&dev));
         HXC(hipGetDeviceProperties(&prop, dev));
-        const size_t lds = solve_lds_bytes(max_slots, max_rounds);
+        const size_t lds = solve_lds_bytes(max_slots);
         if (lds > prop.sharedMemPerBlock)
             throw std::runtime_error("a cell has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
                                      " B solver schedule exceeds the " + std::to_string(prop.sharedMemPerBlock) +
@@ -899,17 +900,18 @@ void hx_sim::step_once() {
     S.cell_node_begin = d_cell_node_begin;
     S.cell_desc_begin = d_cell_desc_begin;
     S.cell_round_begin = d_cell_round_begin;
-    S.round_begin = d_round_begin;
+    S.rounds = d_rounds;
     S.desc = d_desc;
     S.v = d_v;
     S.d = d_d;
     S.rhs = d_rhs;
+    S.w = d_w;
     S.a = d_a;
     S.b = d_b;
     S.cm = d_cm;
     S.cfac = 0.001 * (1.0 / dt);
     tbegin(T_SOLVE);
-    launch_solve(S, max_slots, max_rounds, stream);
+    launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
     if (!gaps.empty()) {
         tbegin(T_OTHER);
@@ -1560,9 +1562,10 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
 }
 
 // Host emulation of one device tree solve over the same chunk schedule: for
-// every cell, rounds in the kernel's order, each lane's chunk in turn.  Lanes
+// every cell, rounds in the kernel's order, each lane's chunk in turn, with the
+// kernel's per-chunk arithmetic (reciprocals here are plain divisions).  Lanes
 // of a round touch disjoint nodes and slots, so running them one after the
-// other gives the device result bit for bit.
+// other is what the wavefront computes.
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max) {
@@ -1571,43 +1574,80 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
         if (hx_model_set_nodes(&tmp, ncell, nnode, parent, a, b, a) != 0) return -1;
         tmp.build_layout();
         const int N = nnode;
-        std::vector<double> gv(N), gd(N), gr(N), ga(N), gb(N), gcm(N);
+        // solver-order arrays: DB RM A B V (the kernel's stage arrays) and w
+        std::vector<double> arr[kStageArrays], gw(N);
+        for (auto& x : arr) x.assign(N, 0.0);
         for (int i = 0; i < N; ++i) {
             const int g = tmp.node_perm[i];
-            gv[g] = v[i]; gd[g] = d[i]; gr[g] = rhs[i]; ga[g] = a[i]; gb[g] = b[i]; gcm[g] = cm[i];
+            arr[SA_DB][g] = d[i] + cfac * cm[i];
+            arr[SA_RM][g] = rhs[i];
+            arr[SA_A][g] = a[i];
+            arr[SA_B][g] = b[i];
+            arr[SA_V][g] = v[i];
         }
+        const double neutral[kStageArrays] = {1.0, 0.0, 0.0, 0.0, 0.0};
         std::vector<double> slots(2 * static_cast<size_t>(std::max(tmp.max_slots, 1)));
+        auto rcp = [](double x) { return 1.0 / x; };
         for (int c = 0; c < ncell; ++c) {
             const int nb = tmp.cell_node_begin[c];
             const ChunkDesc* cd = tmp.descs.data() + tmp.cell_desc_begin[c];
-            const uint16_t* rt = tmp.round_begin.data() + tmp.cell_round_begin[c];
-            const int nround = tmp.cell_round_begin[c + 1] - tmp.cell_round_begin[c] - 1;
-            auto indices = [&](int r, int q, int* idx) {
-                int off = nb + cd[rt[r]].start;
-                for (int kk = 0; kk < kChunk; ++kk) {
-                    idx[kk] = off + (q - rt[r]);
-                    int w = 0;
-                    for (int j = rt[r]; j < rt[r + 1]; ++j) w += cd[j].len > kk;
-                    off += w;
-                }
-            };
+            const RoundInfo* ri = tmp.rounds.data() + tmp.cell_round_begin[c];
+            const int nround = tmp.cell_round_begin[c + 1] - tmp.cell_round_begin[c];
             int idx[kChunk];
+            auto positions = [&](int r, int l, int len) {
+                for (int k = 0; k < kChunk; ++k) idx[k] = k < len ? nb + ri[r].node_base + ri[r].off[k] + l : -1;
+            };
+            struct In {
+                std::vector<double>* const* arr;
+                const double* neutral;
+                const int* idx;
+                double operator()(int x, int k) const { return idx[k] >= 0 ? (*arr[x])[idx[k]] : neutral[x]; }
+            };
+            std::vector<double>* fwd[kStageArrays] = {&arr[SA_DB], &arr[SA_RM], &arr[SA_A], &arr[SA_B], &arr[SA_V]};
+            // back substitution reads u from RM, w from A and v from V
+            std::vector<double>* back[kStageArrays] = {nullptr, &arr[SA_RM], &gw, nullptr, &arr[SA_V]};
             for (int r = nround - 1; r >= 0; --r)
-                for (int q = rt[r]; q < rt[r + 1]; ++q) {
-                    indices(r, q, idx);
-                    chunk_forward(cd[q], idx, nb, gv.data(), gd.data(), gr.data(), ga.data(), gb.data(), gcm.data(),
-                                  cfac, slots.data());
+                for (int l = 0; l < ri[r].desc_count; ++l) {
+                    const ChunkDesc& q = cd[ri[r].desc_begin + l];
+                    positions(r, l, q.len);
+                    double acd = 0.0, ace = 0.0;
+                    for (int ch = 0; ch < q.child_count; ++ch) {
+                        acd += slots[2 * (q.child_begin + ch)];
+                        ace += slots[2 * (q.child_begin + ch) + 1];
+                    }
+                    // results are written after the chunk is done (the kernel writes
+                    // in place; a node's inputs are read before its outputs exist)
+                    double D[kChunk], U[kChunk], W[kChunk], cdd, cee;
+                    chunk_forward_math(
+                        q.len, q.parent_slot != kNone, In{fwd, neutral, idx},
+                        [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp,
+                        acd, ace, cdd, cee);
+                    for (int k = 0; k < q.len; ++k) {
+                        arr[SA_DB][idx[k]] = D[k];
+                        arr[SA_RM][idx[k]] = U[k];
+                        gw[idx[k]] = W[k];
+                    }
+                    if (q.parent_slot != kNone) {
+                        slots[2 * q.slot] = cdd;
+                        slots[2 * q.slot + 1] = cee;
+                    }
                 }
-            for (int r = 0; r < nround; ++r) {
-                std::vector<std::pair<int, double>> tails;
-                for (int q = rt[r]; q < rt[r + 1]; ++q) {
-                    indices(r, q, idx);
-                    tails.push_back({cd[q].slot, chunk_back(cd[q], idx, gv.data(), gd.data(), gr.data(), gb.data(),
-                                                            slots.data())});
+            for (int r = 0; r < nround; ++r)
+                for (int l = 0; l < ri[r].desc_count; ++l) {
+                    const ChunkDesc& q = cd[ri[r].desc_begin + l];
+                    positions(r, l, q.len);
+                    const double vpar = q.parent_slot != kNone ? slots[2 * q.parent_slot] : 0.0;
+                    double VN[kChunk], X[kChunk];
+                    const double vt = chunk_back_math(q.len, In{back, neutral, idx},
+                                                      [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
+                    for (int k = 0; k < q.len; ++k) {
+                        arr[SA_V][idx[k]] = VN[k];
+                        arr[SA_RM][idx[k]] = X[k];
+                    }
+                    slots[2 * q.slot] = vt;
                 }
-                for (auto& tl : tails) slots[2 * tl.first] = tl.second;
-            }
         }
+        std::vector<double>& gv = arr[SA_V];
         for (int i = 0; i < N; ++i) v[i] = gv[tmp.node_perm[i]];
         if (nchunk_max) *nchunk_max = tmp.max_slots;
         if (nround_max) *nround_max = tmp.max_rounds;
@@ -1625,7 +1665,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "nround_max") return sim->max_rounds;
     if (k == "dense_mask") return sim->dense_mask;
     if (k == "fused") return sim->fused ? 1 : 0;
-    if (k == "nround_total") return static_cast<long long>(sim->round_begin.size()) - sim->ncell;
+    if (k == "nround_total") return static_cast<long long>(sim->rounds.size());
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->ring.nslot;
     if (k == "event_cap") return sim->ring.cap;

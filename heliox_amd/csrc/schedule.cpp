@@ -22,11 +22,14 @@
 
 namespace hx {
 
-void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, int lanes, CellSchedule& out) {
+void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, int lanes, int round_max,
+                         CellSchedule& out) {
     const int n = static_cast<int>(local_parent.size());
     out = CellSchedule();
     if (n == 0) return;
     if (local_parent[0] != -1) throw std::runtime_error("cell root must be local node 0");
+    if (chunk_max < 1 || chunk_max > kChunk || round_max < chunk_max || round_max > 255)
+        throw std::runtime_error("solver schedule: chunk or round size out of range");
     std::vector<int> nchild(n, 0);
     for (int i = 1; i < n; ++i) {
         const int p = local_parent[i];
@@ -72,55 +75,73 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
     for (int h = hmax; h >= 0; --h) {
         auto& v = by_h[h];
         std::stable_sort(v.begin(), v.end(), [&](int x, int y) { return chunks[x].len > chunks[y].len; });
-        for (size_t s = 0; s < v.size(); s += lanes)
-            rounds.emplace_back(v.begin() + s, v.begin() + std::min(v.size(), s + lanes));
+        // a round holds at most `lanes` chunks and `round_max` nodes (one LDS stage)
+        std::vector<int> cur;
+        int nodes = 0;
+        for (int q : v) {
+            if (!cur.empty() && (static_cast<int>(cur.size()) == lanes || nodes + chunks[q].len > round_max)) {
+                rounds.push_back(cur);
+                cur.clear();
+                nodes = 0;
+            }
+            cur.push_back(q);
+            nodes += chunks[q].len;
+        }
+        if (!cur.empty()) rounds.push_back(cur);
     }
     // solver order of the cell's nodes.  Inside a round the chunks are sorted by
     // length (longest first) and stored position-major: node k of every chunk
     // that has one, then node k+1, ...  Node k of lane l sits at
     // round_base + sum_{j<k} W_j + l, where W_j = number of chunks longer than j,
     // so the lanes of a round read and write contiguous memory.
-    std::vector<int> round_base(rounds.size(), 0), lane_of(nchunk, 0), round_of(nchunk, 0);
-    std::vector<int> tail_pos(nchunk, 0);
+    std::vector<int> round_base(rounds.size(), 0);
     out.order.reserve(n);
     for (size_t ri = 0; ri < rounds.size(); ++ri) {
         auto& r = rounds[ri];
         round_base[ri] = static_cast<int>(out.order.size());
         int maxlen = 0;
-        for (size_t l = 0; l < r.size(); ++l) {
-            lane_of[r[l]] = static_cast<int>(l);
-            round_of[r[l]] = static_cast<int>(ri);
-            maxlen = std::max(maxlen, chunks[r[l]].len);
-        }
+        for (int q : r) maxlen = std::max(maxlen, chunks[q].len);
         for (int k = 0; k < maxlen; ++k)
-            for (size_t l = 0; l < r.size(); ++l) {
-                const int q = r[l];
-                if (chunks[q].len > k) {
-                    if (k == chunks[q].len - 1) tail_pos[q] = static_cast<int>(out.order.size());
-                    out.order.push_back(chunks[q].nodes[k]);
-                }
-            }
+            for (int q : r)
+                if (chunks[q].len > k) out.order.push_back(chunks[q].nodes[k]);
     }
     if (n > kMaxCellNodes || nchunk > kMaxCellNodes)
         throw std::runtime_error("cell too large for the solver schedule (max 65535 nodes)");
-    out.round_begin.push_back(0);
     for (size_t ri = 0; ri < rounds.size(); ++ri) {
+        RoundInfo info{};
+        info.desc_begin = static_cast<uint16_t>(out.desc.size());
+        info.desc_count = static_cast<uint16_t>(rounds[ri].size());
+        info.node_base = static_cast<uint16_t>(round_base[ri]);
+        int cnt = 0;
         for (int q : rounds[ri]) {
             ChunkDesc d{};
-            d.start = static_cast<uint16_t>(round_base[ri]);
             d.len = static_cast<uint8_t>(chunks[q].len);
             d.slot = static_cast<uint16_t>(q);
             d.parent_slot = chunks[q].parent >= 0 ? static_cast<uint16_t>(chunks[q].parent) : kNone;
-            d.head_parent = chunks[q].parent >= 0 ? static_cast<uint16_t>(tail_pos[chunks[q].parent]) : kNone;
             d.child_begin = static_cast<uint16_t>(chunks[q].child_begin);
             if (chunks[q].child_count > 255) throw std::runtime_error("node with more than 255 children");
             d.child_count = static_cast<uint8_t>(chunks[q].child_count);
             out.desc.push_back(d);
+            cnt += chunks[q].len;
         }
-        out.round_begin.push_back(static_cast<int>(out.desc.size()));
+        info.node_count = static_cast<uint16_t>(cnt);
+        // off[k] = number of the round's nodes at positions < k (chunks sorted by length)
+        int off = 0;
+        for (int k = 0; k < kChunk; ++k) {
+            info.off[k] = static_cast<uint8_t>(off);
+            for (int q : rounds[ri]) off += chunks[q].len > k;
+        }
+        out.rounds.push_back(info);
+    }
+    // padding rounds (no chunks; their loads read node 0 and they write
+    // nothing) make the round count a multiple of the kernel's pipeline depth
+    while (out.rounds.size() % kDepth) {
+        RoundInfo pad{};
+        pad.node_count = 1;
+        out.rounds.push_back(pad);
     }
     out.nchunk = nchunk;
-    out.nround = static_cast<int>(rounds.size());
+    out.nround = static_cast<int>(out.rounds.size());
 }
 
 }  // namespace hx
