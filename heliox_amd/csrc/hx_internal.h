@@ -73,6 +73,8 @@ struct StepArgs {
     int do_state;                 // finish the previous step's state update first
     int do_current;
     int write_assigned;           // also store assigned outputs (i, ina, gna, minf, ...)
+    unsigned ion_store;           // ion x (0 na, 1 k, 2 ca): bit 2x stores cur, bit 2x+1 stores erev
+    int ion_type[3];              // iontype shared by every instance of ion x, or -1 (read per instance)
     double t;                     // time of the current evaluation (t_n + dt/2)
     double dt;
     MechConsts c;

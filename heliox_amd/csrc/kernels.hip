@@ -37,56 +37,71 @@ __device__ __forceinline__ int ion_index(const MechDev& m, int which, int j) {
 }
 
 // ---------------------------------------------------------------------------
-// per-mechanism state updates (shared by the dense and sparse kernels)
+// per-mechanism state updates (shared by the dense and sparse kernels).  Each
+// takes the state it updates as values and returns the new values (also
+// stored), so a kernel that goes on to the current evaluation keeps them in
+// registers instead of reading back what it just wrote.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void hh_state(const StepArgs& A, const MechDev& m, int j, double v) {
+struct HHState { double m, h, n; };
+struct CaHVAState { double m, h; };
+
+__device__ __forceinline__ HHState hh_load(const MechDev& m, int j) {
+    return {m.col(HH_M)[j], m.col(HH_H)[j], m.col(HH_N)[j]};
+}
+__device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) { return {m.col(CH_M)[j], m.col(CH_H)[j]}; }
+
+__device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s) {
     double minf, mtau, hinf, htau, ninf, ntau;
     hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
-    double* M = m.col(HH_M);
-    double* H = m.col(HH_H);
-    double* Nn = m.col(HH_N);
-    M[j] = hh_cnexp(M[j], minf, mtau, A.dt);
-    H[j] = hh_cnexp(H[j], hinf, htau, A.dt);
-    Nn[j] = hh_cnexp(Nn[j], ninf, ntau, A.dt);
+    s.m = hh_cnexp(s.m, minf, mtau, A.dt);
+    s.h = hh_cnexp(s.h, hinf, htau, A.dt);
+    s.n = hh_cnexp(s.n, ninf, ntau, A.dt);
+    m.col(HH_M)[j] = s.m;
+    m.col(HH_H)[j] = s.h;
+    m.col(HH_N)[j] = s.n;
     if (A.write_assigned) {
         m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
         m.col(HH_HINF)[j] = hinf; m.col(HH_HTAU)[j] = htau;
         m.col(HH_NINF)[j] = ninf; m.col(HH_NTAU)[j] = ntau;
     }
+    return s;
 }
 
-__device__ __forceinline__ void cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
-                                            const double* ca_erev, int ci) {
+__device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
+                                                  CaHVAState s, const double* ca_erev, int ci) {
     double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
     cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
-    double* M = m.col(CH_M);
-    double* H = m.col(CH_H);
-    M[j] = M[j] + (1.0 - exp(-A.dt / mTau)) * (mInf - M[j]);
-    H[j] = H[j] + (1.0 - exp(-A.dt / hTau)) * (hInf - H[j]);
+    s.m = s.m + (1.0 - exp(-A.dt / mTau)) * (mInf - s.m);
+    s.h = s.h + (1.0 - exp(-A.dt / hTau)) * (hInf - s.h);
+    m.col(CH_M)[j] = s.m;
+    m.col(CH_H)[j] = s.h;
     if (A.write_assigned) {
         m.col(CH_ECA)[j] = ca_erev[ci];
         m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
         m.col(CH_HINF)[j] = hInf; m.col(CH_HTAU)[j] = hTau; m.col(CH_HALPHA)[j] = hAlpha; m.col(CH_HBETA)[j] = hBeta;
     }
+    return s;
 }
 
-__device__ __forceinline__ void hdla_state(const StepArgs& A, const MechDev& m, int j, double v) {
+__device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l) {
     double linf, taul;
     hdla_rate(v, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
-    double* L = m.col(HD_L);
-    L[j] = L[j] + (1.0 - exp(-A.dt / taul)) * (linf - L[j]);
+    l = l + (1.0 - exp(-A.dt / taul)) * (linf - l);
+    m.col(HD_L)[j] = l;
     if (A.write_assigned) { m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul; }
+    return l;
 }
 
-__device__ __forceinline__ void cadyn_state(const StepArgs& A, const MechDev& m, int j, double* ca_conci,
-                                            const double* ca_cur, int ci) {
-    ca_conci[ci] = cadyn_step(ca_conci[ci], ca_cur[ci], m.col(CD_GAMMA)[j], m.col(CD_DECAY)[j],
-                              m.col(CD_DEPTH)[j], m.col(CD_MINCAI)[j], A.dt);
+// returns the new cai (the caller stores it)
+__device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& m, int j, double cai, double ica) {
+    return cadyn_step(cai, ica, m.col(CD_GAMMA)[j], m.col(CD_DECAY)[j], m.col(CD_DEPTH)[j], m.col(CD_MINCAI)[j],
+                      A.dt);
 }
 
 // ---------------------------------------------------------------------------
 // per-mechanism FD currents: returns I(v), sets g = (I(v+0.001) - I(v)) / 0.001
-// (mech_template.cuh:616-626); ion currents are added on the I(v) evaluation
+// (mech_template.cuh:616-626); ion currents of the I(v) evaluation are
+// returned for the caller to accumulate
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
     double gp = m.col(PAS_G)[j], ep = m.col(PAS_E)[j];
@@ -98,19 +113,14 @@ __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, i
     return i0;
 }
 
-__device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g,
-                                         const double* na_erev, double* na_cur, int nai,
-                                         const double* k_erev, double* k_cur, int ki) {
+__device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, const HHState& s,
+                                         double ena, double ek, double& g, double& ina, double& ik) {
     double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
     double gl = m.col(HH_GL)[j], el = m.col(HH_EL)[j];
-    double mm = m.col(HH_M)[j], hh = m.col(HH_H)[j], nn = m.col(HH_N)[j];
-    double ena = na_erev[nai], ek = k_erev[ki];
-    double gna, ina, gk, ik, il;
+    double gna, gk, il;
     double v1 = v + 0.001;
-    double i1 = hh_current(v1, gnabar, gkbar, gl, el, mm, hh, nn, ena, ek, gna, ina, gk, ik, il);
-    double i0 = hh_current(v, gnabar, gkbar, gl, el, mm, hh, nn, ena, ek, gna, ina, gk, ik, il);
-    na_cur[nai] += ina;
-    k_cur[ki] += ik;
+    double i1 = hh_current(v1, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
+    double i0 = hh_current(v, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
     g = (i1 - i0) / 0.001;
     if (A.write_assigned) {
         m.col(HH_ENA)[j] = ena; m.col(HH_EK)[j] = ek; m.col(HH_INA)[j] = ina; m.col(HH_IK)[j] = ik;
@@ -119,15 +129,13 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
     return i0;
 }
 
-__device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g,
-                                            const double* ca_erev, double* ca_cur, int ci) {
-    double gbar = m.col(CH_GBAR)[j], mm = m.col(CH_M)[j], hh = m.col(CH_H)[j];
-    double eca = ca_erev[ci];
+__device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v,
+                                            const CaHVAState& s, double eca, double& g) {
+    double gbar = m.col(CH_GBAR)[j];
     double v1 = v + 0.001;
-    double gg = gbar * mm * mm * hh;
+    double gg = gbar * s.m * s.m * s.h;
     double i1 = gg * (v1 - eca);
     double i0 = gg * (v - eca);
-    ca_cur[ci] += i0;
     g = (i1 - i0) / 0.001;
     if (A.write_assigned) {
         m.col(CH_ECA)[j] = eca; m.col(CH_G)[j] = gg; m.col(CH_ICA)[j] = i0; m.col(CH_IMECH)[j] = i0;
@@ -135,8 +143,9 @@ __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m,
     return i0;
 }
 
-__device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
-    double ghd = m.col(HD_GHDBAR)[j] * m.col(HD_L)[j];
+__device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double l,
+                                           double& g) {
+    double ghd = m.col(HD_GHDBAR)[j] * l;
     double v1 = v + 0.001;
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);
@@ -145,6 +154,9 @@ __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, 
     return i0;
 }
 
+// Per-step part of an ion (eion.cuh:155-166): zero cur and dcurdv, and
+// recompute erev from the concentrations when iontype has 0100.  Used by the
+// instance-parallel ion kernel; the fused kernel keeps cur in registers.
 __device__ __forceinline__ void ion_cur(const MechDev& m, int j, double z, double ktf, int write_dcurdv) {
     m.col(ION_CUR)[j] = 0.;
     if (write_dcurdv) m.col(ION_DCURDV)[j] = 0.;
@@ -152,10 +164,31 @@ __device__ __forceinline__ void ion_cur(const MechDev& m, int j, double z, doubl
         m.col(ION_EREV)[j] = nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf);
 }
 
+// erev of ion x at dense instance i for this step's current evaluation.  ci:
+// the inside concentration when the caller already holds it (have_ci).
+__device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDev& ion, int x, int i, double z,
+                                                 bool have_ci, double ci) {
+    const int type = A.ion_type[x] >= 0 ? A.ion_type[x] : ion.iontype[i];
+    if (type & 0100) {
+        const double e = nernst(have_ci ? ci : ion.col(ION_CONCI)[i], ion.col(ION_CONCO)[i], z, A.c.ktf);
+        if (A.ion_store & (2u << (2 * x))) ion.col(ION_EREV)[i] = e;
+        return e;
+    }
+    return ion.col(ION_EREV)[i];
+}
+
+__device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {
+    if (A.ion_store & (1u << (2 * x))) ion.col(ION_CUR)[i] = cur;
+    if (A.write_assigned) ion.col(ION_DCURDV)[i] = 0.;
+}
+
 #define HAS(bit) (A.dense_mask & (1u << (bit)))
 
 // ---------------------------------------------------------------------------
-// fused node-parallel kernel for dense mechanisms
+// fused node-parallel kernel for dense mechanisms: the previous step's state
+// update (ion writers first, simulate.cpp:822-834) and this step's currents in
+// CoreNEURON mechanism order.  Ion currents are summed in registers and each
+// ion array is written once.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -164,31 +197,49 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     const MechDev& na = A.m[M_NA_ION];
     const MechDev& kk = A.m[M_K_ION];
     const MechDev& ca = A.m[M_CA_ION];
+    HHState hs{};
+    CaHVAState cs{};
+    double hl = 0.0, cai = 0.0;
+    const bool have_cai = A.do_state && HAS(M_CADYN);
     if (A.do_state) {
-        // ion-writing mechanisms first (simulate.cpp:822-834)
-        if (HAS(M_CADYN)) cadyn_state(A, A.m[M_CADYN], i, ca.col(ION_CONCI), ca.col(ION_CUR), i);
-        if (HAS(M_HH)) hh_state(A, A.m[M_HH], i, v);
-        if (HAS(M_CAHVA)) cahva_state(A, A.m[M_CAHVA], i, v, ca.col(ION_EREV), i);
-        if (HAS(M_HDLA)) hdla_state(A, A.m[M_HDLA], i, v);
+        if (HAS(M_CADYN)) {
+            double* conci = ca.col(ION_CONCI);
+            cai = cadyn_state(A, A.m[M_CADYN], i, conci[i], ca.col(ION_CUR)[i]);
+            conci[i] = cai;
+        }
+        if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, hh_load(A.m[M_HH], i));
+        if (HAS(M_CAHVA)) cs = cahva_state(A, A.m[M_CAHVA], i, v, cahva_load(A.m[M_CAHVA], i), ca.col(ION_EREV), i);
+        if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, A.m[M_HDLA].col(HD_L)[i]);
+    } else if (A.do_current) {
+        if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
+        if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
+        if (HAS(M_HDLA)) hl = A.m[M_HDLA].col(HD_L)[i];
     }
     if (!A.do_current) return;
     double rhs = 0.0, d = 0.0, g, cur;
+    double ena = 0.0, ek = 0.0, eca = 0.0, ina = 0.0, ik = 0.0, ica = 0.0;
     if (HAS(M_PAS)) { cur = pas_cur(A, A.m[M_PAS], i, v, g); rhs -= cur; d += g; }
-    if (HAS(M_NA_ION)) ion_cur(na, i, 1.0, A.c.ktf, A.write_assigned);
-    if (HAS(M_K_ION)) ion_cur(kk, i, 1.0, A.c.ktf, A.write_assigned);
+    if (HAS(M_NA_ION)) ena = dense_ion_erev(A, na, 0, i, 1.0, false, 0.0);
+    if (HAS(M_K_ION)) ek = dense_ion_erev(A, kk, 1, i, 1.0, false, 0.0);
     if (HAS(M_HH)) {
-        cur = hh_cur(A, A.m[M_HH], i, v, g, na.col(ION_EREV), na.col(ION_CUR), i, kk.col(ION_EREV),
-                     kk.col(ION_CUR), i);
+        double ina_h, ik_h;
+        cur = hh_cur(A, A.m[M_HH], i, v, hs, ena, ek, g, ina_h, ik_h);
+        ina += ina_h;
+        ik += ik_h;
         rhs -= cur; d += g;
     }
-    if (HAS(M_CA_ION)) ion_cur(ca, i, 2.0, A.c.ktf, A.write_assigned);
+    if (HAS(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai, cai);
     if (HAS(M_CAHVA)) {
-        cur = cahva_cur(A, A.m[M_CAHVA], i, v, g, ca.col(ION_EREV), ca.col(ION_CUR), i);
+        cur = cahva_cur(A, A.m[M_CAHVA], i, v, cs, eca, g);
+        ica += cur;
         rhs -= cur; d += g;
     }
-    if (HAS(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, g); rhs -= cur; d += g; }
+    if (HAS(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, hl, g); rhs -= cur; d += g; }
     A.d[i] = d;
     A.rhs[i] = rhs;
+    if (HAS(M_NA_ION)) dense_ion_store(A, na, 0, i, ina);
+    if (HAS(M_K_ION)) dense_ion_store(A, kk, 1, i, ik);
+    if (HAS(M_CA_ION)) dense_ion_store(A, ca, 2, i, ica);
 }
 
 // ---------------------------------------------------------------------------
@@ -208,20 +259,39 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
     const MechDev& na = A.m[M_NA_ION];
     const MechDev& kk = A.m[M_K_ION];
     const MechDev& ca = A.m[M_CA_ION];
+    HHState hs{};
+    CaHVAState cs{};
+    double hl = 0.0;
     if (A.do_state) {
-        if (MECH == M_CADYN) cadyn_state(A, m, j, ca.col(ION_CONCI), ca.col(ION_CUR), ion_index(m, 2, j));
-        if (MECH == M_HH) hh_state(A, m, j, v);
-        if (MECH == M_CAHVA) cahva_state(A, m, j, v, ca.col(ION_EREV), ion_index(m, 2, j));
-        if (MECH == M_HDLA) hdla_state(A, m, j, v);
+        if (MECH == M_CADYN) {
+            const int ci = ion_index(m, 2, j);
+            double* conci = ca.col(ION_CONCI);
+            conci[ci] = cadyn_state(A, m, j, conci[ci], ca.col(ION_CUR)[ci]);
+        }
+        if (MECH == M_HH) hs = hh_state(A, m, j, v, hh_load(m, j));
+        if (MECH == M_CAHVA) cs = cahva_state(A, m, j, v, cahva_load(m, j), ca.col(ION_EREV), ion_index(m, 2, j));
+        if (MECH == M_HDLA) hl = hdla_state(A, m, j, v, m.col(HD_L)[j]);
+    } else if (A.do_current) {
+        if (MECH == M_HH) hs = hh_load(m, j);
+        if (MECH == M_CAHVA) cs = cahva_load(m, j);
+        if (MECH == M_HDLA) hl = m.col(HD_L)[j];
     }
     if (!A.do_current || MECH == M_CADYN) return;
     double g = 0.0, cur = 0.0;
     if (MECH == M_PAS) cur = pas_cur(A, m, j, v, g);
-    if (MECH == M_HH)
-        cur = hh_cur(A, m, j, v, g, na.col(ION_EREV), na.col(ION_CUR), ion_index(m, 0, j), kk.col(ION_EREV),
-                     kk.col(ION_CUR), ion_index(m, 1, j));
-    if (MECH == M_CAHVA) cur = cahva_cur(A, m, j, v, g, ca.col(ION_EREV), ca.col(ION_CUR), ion_index(m, 2, j));
-    if (MECH == M_HDLA) cur = hdla_cur(A, m, j, v, g);
+    if (MECH == M_HH) {
+        const int ni = ion_index(m, 0, j), ki = ion_index(m, 1, j);
+        double ina, ik;
+        cur = hh_cur(A, m, j, v, hs, na.col(ION_EREV)[ni], kk.col(ION_EREV)[ki], g, ina, ik);
+        na.col(ION_CUR)[ni] += ina;
+        kk.col(ION_CUR)[ki] += ik;
+    }
+    if (MECH == M_CAHVA) {
+        const int ci = ion_index(m, 2, j);
+        cur = cahva_cur(A, m, j, v, cs, ca.col(ION_EREV)[ci], g);
+        ca.col(ION_CUR)[ci] += cur;
+    }
+    if (MECH == M_HDLA) cur = hdla_cur(A, m, j, v, hl, g);
     A.rhs[node] -= cur;
     A.d[node] += g;
 }

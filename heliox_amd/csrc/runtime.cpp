@@ -198,6 +198,7 @@ struct hx_sim {
     std::vector<RoundInfo> rounds;       // all cells' rounds, cell by cell
     std::vector<ChunkDesc> descs;
     int max_slots = 0, max_rounds = 0;
+    int ion_type_uniform[3] = {-1, -1, -1};
     unsigned dense_mask = 0;
     bool fused = false;
     bool write_assigned = false;
@@ -261,6 +262,7 @@ struct hx_sim {
     double t = 0.0;
     int k = 0;                       // step index since finitialize
     bool state_pending = false;
+    bool final_step = false;   // the last step of a run call also stores every assigned variable
     bool initialized = false;
     // profiling
     bool profiling = false;
@@ -506,6 +508,10 @@ void hx_sim::upload() {
             std::vector<int> it(m.n);
             for (int j = 0; j < m.n; ++j) it[j] = m.iontype[m.iperm[j]];
             d.iontype = dupload(owned, it);
+            const int x = id == M_NA_ION ? 0 : (id == M_K_ION ? 1 : 2);
+            ion_type_uniform[x] = -1;
+            if (m.n > 0 && std::all_of(it.begin(), it.end(), [&](int t) { return t == it[0]; }))
+                ion_type_uniform[x] = it[0];
         }
         for (int x = 0; x < 3; ++x) {
             if (!(R[id].ion_use & (1 << x))) continue;
@@ -748,7 +754,24 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.dense_mask = dense_mask;
     A.do_state = do_state;
     A.do_current = do_current;
-    A.write_assigned = write_assigned ? 1 : 0;
+    const bool assigned = write_assigned || final_step;
+    A.write_assigned = assigned ? 1 : 0;
+    // An ion's cur and erev are stored when something outside the fused kernel
+    // reads them: a mechanism run instance-parallel, CaDynamics_E2 (reads ica in
+    // the next state update) or a handle/monitor on an assigned variable.
+    {
+        const auto& R = registry();
+        unsigned need = 0;
+        for (int id = 0; id < M_COUNT; ++id)
+            if (mech[id].present && !(dense_mask & (1u << id))) need |= static_cast<unsigned>(R[id].ion_use);
+        A.ion_store = 0;
+        for (int x = 0; x < 3; ++x) {
+            const bool ext = assigned || (need & (1u << x));
+            if (ext || (x == 2 && mech[M_CADYN].present)) A.ion_store |= 1u << (2 * x);
+            if (ext) A.ion_store |= 2u << (2 * x);
+            A.ion_type[x] = ion_type_uniform[x];
+        }
+    }
     A.t = tcur;
     A.dt = dt;
     auto G = [&](int id, const char* k, double dflt) {
@@ -988,8 +1011,17 @@ int hx_sim::run_steps(int nstep) {
         d_mon_buf = dalloc<double>(owned, static_cast<size_t>(mon_buf_cap) * mon_ref.size());
         mon_buf_fill = 0;
     }
-    for (int s = 0; s < nstep; ++s) step_once();
+    // Assigned variables (ion currents and reversal potentials, hh ina, minf,
+    // ...) with no reader inside the step are not stored on every step; the
+    // last step of the call stores them all, so they read back as after the
+    // reference's last step.
+    final_step = false;
+    for (int s = 0; s < nstep; ++s) {
+        final_step = s == nstep - 1;
+        step_once();
+    }
     finish_pending();
+    final_step = false;
     sync_outputs();
     return 0;
 }
@@ -1030,8 +1062,10 @@ void hx_sim::finitialize(double v_init) {
     launch_record();
     launch_detect(0, 0.0);
     launch_events(0, 0.0);
+    final_step = true;
     launch_mech_pass(0, 1, 0.0);
     launch_point_currents(0.0);
+    final_step = false;
     initialized = true;
     sync_outputs();
 }
