@@ -32,11 +32,11 @@ METRIC = "compartment-steps/s (2000×5000-comp fp64) + achieved HBM GB/s"
 # Algorithmic bytes per compartment for the fused mechanism kernel on this
 # workload: every per-compartment input read once, every state read and
 # written once, d and rhs written once (fp64):
-#   v 8 + (d, rhs) 16 + pas (g, e) 16 + hh (m,h,n r/w 48; gnabar, gkbar, gl, el 32;
-#   ena, ek 16) 96 + Ca_HVA (m,h r/w 32; gbar 8) 40 + hd_la (l r/w 16; ghdbar,
-#   vhalfl, tau 24) 40 + CaDynamics_E2 + ca_ion (cai r/w 16; gamma, decay, depth,
-#   minCai 32; cao 8) 56  =  272 B
-MECH_BYTES_PER_COMP = 272
+#   v, cm 16 + (d, rhs) 16 + pas (g, e) 16 + hh (m,h,n r/w 48; gnabar, gkbar, gl,
+#   el 32; ena, ek 16) 96 + Ca_HVA (m,h r/w 32; gbar 8) 40 + hd_la (l r/w 16;
+#   ghdbar, vhalfl, tau 24) 40 + CaDynamics_E2 + ca_ion (cai r/w 16; gamma, decay,
+#   depth, minCai 32; cao 8) 56  =  280 B
+MECH_BYTES_PER_COMP = 280
 
 
 def _traffic_from_profiles():

@@ -68,6 +68,8 @@ struct StepArgs {
     double* d;
     double* rhs;
     const double* area;
+    const double* cm;             // capacitance, added to d by the current pass
+    double cfac;                  // 1e-3 * cj (capac.cpp:68-80)
     MechDev m[M_COUNT];
     unsigned dense_mask;          // mechanisms processed by the fused node kernel
     int do_state;                 // finish the previous step's state update first
@@ -89,7 +91,6 @@ constexpr int kWave = 64;
 constexpr int kMaxCellNodes = 65535;
 constexpr int kRoundMax = 192;    // max nodes per round (one LDS stage)
 constexpr int kPer = kRoundMax / kWave;   // stage elements per lane per array
-constexpr int kDepth = 3;         // rounds loaded ahead of the one being solved
 
 struct ChunkDesc {
     uint16_t slot;         // junction slot of this chunk (its breadth-first id)
@@ -122,13 +123,11 @@ struct SolveArgs {
     const RoundInfo* rounds;
     const ChunkDesc* desc;
     double* v;
-    double* d;                    // in: assembled diagonal; out: eliminated diagonal D
-    double* rhs;                  // in: assembled right-hand side; out: solution x (v += x)
+    double* d;                    // in: membrane + capacitance diagonal; out: eliminated diagonal D
+    double* rhs;                  // in: membrane right-hand side; out: solution x (v += x)
     double* w;                    // scratch: b / D per node, written by elimination
     const double* a;
     const double* b;
-    const double* cm;
-    double cfac;                  // 1e-3 * cj (capac.cpp:68-80)
 };
 
 // Event ring: one slot per delivery step (mod nslot), fixed capacity per slot.
@@ -203,10 +202,12 @@ struct VecPlayDev {
 };
 
 // LDS of the solve kernel: two junction values per chunk, then one round
-// stage of kStageArrays arrays, each with a neutral entry and a write sink
-// after its kRoundMax nodes.
+// stage of kStageArrays arrays, each with a neutral entry and kSinkWays write
+// sinks after its kRoundMax nodes (padding writes of a 16-lane LDS access group
+// land on 16 different banks pairs instead of one address).
 constexpr int kStageArrays = 5;
-constexpr int kStageStride = kRoundMax + 2;
+constexpr int kSinkWays = 16;
+constexpr int kStageStride = kRoundMax + 1 + kSinkWays;
 inline size_t solve_lds_bytes(int max_chunks) {
     const int mc = max_chunks > 0 ? max_chunks : 1;
     return static_cast<size_t>(mc) * 2 * sizeof(double) +

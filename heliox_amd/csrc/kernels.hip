@@ -216,7 +216,9 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
         if (HAS(M_HDLA)) hl = A.m[M_HDLA].col(HD_L)[i];
     }
     if (!A.do_current) return;
-    double rhs = 0.0, d = 0.0, g, cur;
+    // the capacitance term of the diagonal (capac.cpp:68-80) is added here,
+    // ahead of the membrane conductances, so the solve reads one diagonal
+    double rhs = 0.0, d = A.cfac * A.cm[i], g, cur;
     double ena = 0.0, ek = 0.0, eca = 0.0, ina = 0.0, ik = 0.0, ica = 0.0;
     if (HAS(M_PAS)) { cur = pas_cur(A, A.m[M_PAS], i, v, g); rhs -= cur; d += g; }
     if (HAS(M_NA_ION)) ena = dense_ion_erev(A, na, 0, i, 1.0, false, 0.0);
@@ -449,7 +451,7 @@ __device__ __forceinline__ void round_boundary() {
 }
 
 constexpr int kNeutral = kRoundMax;       // stage entry holding the padding value
-constexpr int kSink = kRoundMax + 1;      // stage entry absorbing padding writes
+constexpr int kSink = kRoundMax + 1;      // first of the kSinkWays entries absorbing padding writes
 
 // 1/x: hardware reciprocal estimate refined by two Newton-Raphson steps
 // (each step squares the relative error), correct to about an ulp.
@@ -497,7 +499,7 @@ __device__ __forceinline__ RoundU uniform_round(const RoundV& v) {
 // block) plus its chunk descriptor, so each round issues the same number of
 // vector-memory instructions and the compiler's wait counts stay static.
 struct FwdBuf {
-    double x[6][kPer];    // d rhs a b v cm
+    double x[5][kPer];    // d rhs a b v
     uint2 q;              // ChunkDesc
     RoundU ri;
 };
@@ -518,20 +520,26 @@ struct SolveCtx {
 };
 
 // Stage positions of the lane's chunk: read from the neutral entry and write
-// to the sink past the chunk's length.
-__device__ __forceinline__ void round_positions(const RoundU& ri, int len, int lane, int* rp, int* wp) {
+// to a sink past the chunk's length; tp = position of the tail.
+__device__ __forceinline__ void round_positions(const RoundU& ri, int len, int lane, int* rp, int* wp, int& tp) {
+    tp = kNeutral;
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
         const int p = ri.offset(k) + lane;
         rp[k] = k < len ? p : kNeutral;
-        wp[k] = k < len ? p : kSink;
+        wp[k] = k < len ? p : kSink + (lane & (kSinkWays - 1));
+        if (k == len - 1) tp = p;
     }
 }
 
 struct StageIn {
-    const double* stage;
+    const double* st;
     const int* rp;
-    __device__ __forceinline__ double operator()(int arr, int k) const { return stage[arr * kStageStride + rp[k]]; }
+    __device__ __forceinline__ double at(int arr, int k) const { return st[arr * kStageStride + rp[k]]; }
+    __device__ __forceinline__ FwdNode fwd(int k) const {
+        return {at(SA_DB, k), at(SA_RM, k), at(SA_A, k), at(SA_B, k), at(SA_V, k)};
+    }
+    __device__ __forceinline__ BackNode back(int k) const { return {at(SA_RM, k), at(SA_A, k), at(SA_V, k)}; }
 };
 
 __device__ __forceinline__ unsigned clamp_index(int lane, int j, int count) {
@@ -541,7 +549,7 @@ __device__ __forceinline__ unsigned clamp_index(int lane, int j, int count) {
 }
 
 __device__ __forceinline__ uint2 load_desc(const SolveCtx& C, const RoundU& ri) {
-    const int top = ri.desc_count > 0 ? ri.desc_count - 1 : 0;
+    const int top = ri.desc_count > 0 ? ri.desc_count - 1 : 0;   // padding rounds: any descriptor
     return C.desc[ri.desc_begin + (C.lane < top ? C.lane : top)];
 }
 
@@ -553,7 +561,6 @@ __device__ __forceinline__ void fwd_load(const SolveCtx& C, FwdBuf& B, const Rou
     const double* a = C.S.a + base;
     const double* b = C.S.b + base;
     const double* v = C.S.v + base;
-    const double* cm = C.S.cm + base;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const unsigned e = clamp_index(C.lane, j, ri.node_count);
@@ -562,61 +569,69 @@ __device__ __forceinline__ void fwd_load(const SolveCtx& C, FwdBuf& B, const Rou
         B.x[2][j] = a[e];
         B.x[3][j] = b[e];
         B.x[4][j] = v[e];
-        B.x[5][j] = cm[e];
     }
     B.q = load_desc(C, ri);
     B.ri = ri;
 }
 
-__device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B) {
+// Solves the round held in B; once B is staged, the next round (table entry
+// `next`, already loaded) is requested into N.
+__device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, FwdBuf& N, const RoundV& next) {
     const RoundU& ri = B.ri;
+    const uint2 q = B.q;
     double* st = C.stage;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int e = C.lane + kWave * j;
-        st[SA_DB * kStageStride + e] = B.x[0][j] + C.S.cfac * B.x[5][j];
+        st[SA_DB * kStageStride + e] = B.x[0][j];
         st[SA_RM * kStageStride + e] = B.x[1][j];
         st[SA_A * kStageStride + e] = B.x[2][j];
         st[SA_B * kStageStride + e] = B.x[3][j];
         st[SA_V * kStageStride + e] = B.x[4][j];
     }
     round_boundary();
+    fwd_load(C, N, next);
     const bool act = C.lane < ri.desc_count;
-    const int slot = B.q.x & 0xFFFF;
-    const bool has_parent = (B.q.x >> 16) != kNone;
-    const int child_begin = B.q.y & 0xFFFF;
-    const int len = act ? (B.q.y >> 16) & 0xFF : 0;
-    const int nchild = act ? B.q.y >> 24 : 0;
-    double acd = 0.0, ace = 0.0;
-    for (int ch = 0; ch < nchild; ++ch) {
-        acd += C.slots[2 * (child_begin + ch)];
-        ace += C.slots[2 * (child_begin + ch) + 1];
+    const int slot = q.x & 0xFFFF;
+    const bool has_parent = (q.x >> 16) != kNone;
+    const int child_begin = q.y & 0xFFFF;
+    const int len = act ? (q.y >> 16) & 0xFF : 0;
+    const int nchild = act ? q.y >> 24 : 0;
+    int rp[kChunk], wp[kChunk], tp;
+    round_positions(ri, len, C.lane, rp, wp, tp);
+    if (nchild > 0) {
+        double acd = 0.0, ace = 0.0;
+        for (int ch = 0; ch < nchild; ++ch) {
+            acd += C.slots[2 * (child_begin + ch)];
+            ace += C.slots[2 * (child_begin + ch) + 1];
+        }
+        double db = st[SA_DB * kStageStride + tp], rm = st[SA_RM * kStageStride + tp];
+        tail_inject(db, rm, st[SA_V * kStageStride + tp], acd, ace);
+        st[SA_DB * kStageStride + tp] = db;
+        st[SA_RM * kStageStride + tp] = rm;
     }
-    int rp[kChunk], wp[kChunk];
-    round_positions(ri, len, C.lane, rp, wp);
     double cd, ce;
     chunk_forward_math(
-        len, has_parent, StageIn{st, rp},
+        has_parent, StageIn{st, rp},
         [&](int k, double D, double u, double w) {
             st[SA_DB * kStageStride + wp[k]] = D;
             st[SA_RM * kStageStride + wp[k]] = u;
             st[SA_B * kStageStride + wp[k]] = w;
         },
-        rcp_nr, acd, ace, cd, ce);
+        rcp_nr, cd, ce);
     if (act && has_parent) {
         C.slots[2 * slot] = cd;
         C.slots[2 * slot + 1] = ce;
     }
     round_boundary();
-    if (ri.desc_count > 0) {   // padding rounds write nothing
-        const int base = C.nb + ri.node_base;
+    // a padding round writes back node 0's staged values unchanged
+    const int base = C.nb + ri.node_base;
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const unsigned e = clamp_index(C.lane, j, ri.node_count);
-            C.S.d[base + e] = st[SA_DB * kStageStride + e];
-            C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
-            C.S.w[base + e] = st[SA_B * kStageStride + e];
-        }
+    for (int j = 0; j < kPer; ++j) {
+        const unsigned e = clamp_index(C.lane, j, ri.node_count);
+        C.S.d[base + e] = st[SA_DB * kStageStride + e];
+        C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
+        C.S.w[base + e] = st[SA_B * kStageStride + e];
     }
     round_boundary();
 }
@@ -638,8 +653,9 @@ __device__ __forceinline__ void back_load(const SolveCtx& C, BackBuf& B, const R
     B.ri = ri;
 }
 
-__device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B) {
+__device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, BackBuf& N, const RoundV& next) {
     const RoundU& ri = B.ri;
+    const uint2 q = B.q;
     double* st = C.stage;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -649,40 +665,47 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B) 
         st[SA_V * kStageStride + e] = B.x[2][j];
     }
     round_boundary();
+    back_load(C, N, next);
     const bool act = C.lane < ri.desc_count;
-    const int slot = B.q.x & 0xFFFF;
-    const int parent_slot = B.q.x >> 16;
-    const int len = act ? (B.q.y >> 16) & 0xFF : 0;
+    const int slot = q.x & 0xFFFF;
+    const int parent_slot = q.x >> 16;
+    const int len = act ? (q.y >> 16) & 0xFF : 0;
     const double vpar = (act && parent_slot != kNone) ? C.slots[2 * parent_slot] : 0.0;
-    int rp[kChunk], wp[kChunk];
-    round_positions(ri, len, C.lane, rp, wp);
-    const double vtail = chunk_back_math(len, StageIn{st, rp},
-                                         [&](int k, double vn, double x) {
-                                             st[SA_V * kStageStride + wp[k]] = vn;
-                                             st[SA_RM * kStageStride + wp[k]] = x;
-                                         },
-                                         vpar);
-    if (act) C.slots[2 * slot] = vtail;
+    int rp[kChunk], wp[kChunk], tp;
+    round_positions(ri, len, C.lane, rp, wp, tp);
+    chunk_back_math(StageIn{st, rp},
+                    [&](int k, double vn, double x) {
+                        st[SA_V * kStageStride + wp[k]] = vn;
+                        st[SA_RM * kStageStride + wp[k]] = x;
+                    },
+                    vpar);
+    if (act) C.slots[2 * slot] = st[SA_V * kStageStride + tp];   // the tail's new voltage
     round_boundary();
-    if (ri.desc_count > 0) {
-        const int base = C.nb + ri.node_base;
+    const int base = C.nb + ri.node_base;
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            const unsigned e = clamp_index(C.lane, j, ri.node_count);
-            C.S.v[base + e] = st[SA_V * kStageStride + e];
-            C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
-        }
+    for (int j = 0; j < kPer; ++j) {
+        const unsigned e = clamp_index(C.lane, j, ri.node_count);
+        C.S.v[base + e] = st[SA_V * kStageStride + e];
+        C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
     }
     round_boundary();
 }
 
+// Waits for every outstanding vector-memory access (s_waitcnt vmcnt(0); the
+// other counters are left alone).  Used once before each sweep's loop, so the
+// compiler's wait counts at the loop head only have to cover the loop's own
+// steady state (one round's stores after the buffer's loads).
+__device__ __forceinline__ void drain_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // One wavefront per cell.  Elimination walks the rounds from the leaves
-// (round nround-1) to the root, back substitution from the root out; the data
-// of the next kDepth rounds and the round table entry after them are in
-// flight while a round is solved.  A cell's round count is a multiple of
-// kDepth (the schedule appends padding rounds with no chunks), so each loop
-// trip solves exactly kDepth rounds; round indices past either end are
-// clamped to a real round, whose loads are issued but never used.
+// (round nround-1) to the root, back substitution from the root out.  While a
+// round is solved from one register buffer, the next round's data is loaded
+// into the other (a round takes longer than an HBM round trip); the round-table
+// entry is fetched a round earlier still.  A cell's round count is even (the
+// schedule appends a padding round with no chunks when needed), so each loop
+// trip solves two rounds and the buffers never trade registers.  Round indices
+// past either end are clamped to a real round, whose loads are issued but
+// never used.
 __global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* __restrict__ rounds_all,
                                                  const uint2* __restrict__ desc, int max_chunks) {
     extern __shared__ double lds[];
@@ -701,41 +724,27 @@ __global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* _
     auto back_idx = [&](int r) { return r < last ? r : last; };
 
     {
-        FwdBuf b0, b1, b2;
-        fwd_load(C, b0, load_round(rounds, fwd_idx(last)));
-        fwd_load(C, b1, load_round(rounds, fwd_idx(last - 1)));
-        fwd_load(C, b2, load_round(rounds, fwd_idx(last - 2)));
-        RoundV nx = load_round(rounds, fwd_idx(last - 3));
-        for (int r = last; r >= 0; r -= kDepth) {
-            fwd_round(C, b0);
-            RoundV n = load_round(rounds, fwd_idx(r - 4));
-            fwd_load(C, b0, nx);
-            fwd_round(C, b1);
-            nx = load_round(rounds, fwd_idx(r - 5));
-            fwd_load(C, b1, n);
-            fwd_round(C, b2);
-            n = load_round(rounds, fwd_idx(r - 6));
-            fwd_load(C, b2, nx);
-            nx = n;
+        FwdBuf x, y;
+        fwd_load(C, x, load_round(rounds, last));
+        RoundV nx = load_round(rounds, last - 1);
+        drain_vector_memory();
+        for (int r = last; r > 0; r -= 2) {
+            RoundV n = load_round(rounds, fwd_idx(r - 2));
+            fwd_round(C, x, y, nx);
+            nx = load_round(rounds, fwd_idx(r - 3));
+            fwd_round(C, y, x, n);
         }
     }
     {
-        BackBuf b0, b1, b2;
-        back_load(C, b0, load_round(rounds, back_idx(0)));
-        back_load(C, b1, load_round(rounds, back_idx(1)));
-        back_load(C, b2, load_round(rounds, back_idx(2)));
-        RoundV nx = load_round(rounds, back_idx(3));
-        for (int r = 0; r <= last; r += kDepth) {
-            back_round(C, b0);
-            RoundV n = load_round(rounds, back_idx(r + 4));
-            back_load(C, b0, nx);
-            back_round(C, b1);
-            nx = load_round(rounds, back_idx(r + 5));
-            back_load(C, b1, n);
-            back_round(C, b2);
-            n = load_round(rounds, back_idx(r + 6));
-            back_load(C, b2, nx);
-            nx = n;
+        BackBuf x, y;
+        back_load(C, x, load_round(rounds, 0));
+        RoundV nx = load_round(rounds, 1);
+        drain_vector_memory();
+        for (int r = 0; r < last; r += 2) {
+            RoundV n = load_round(rounds, back_idx(r + 2));
+            back_round(C, x, y, nx);
+            nx = load_round(rounds, back_idx(r + 3));
+            back_round(C, y, x, n);
         }
     }
 }

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -750,6 +751,8 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.d = d_d;
     A.rhs = d_rhs;
     A.area = d_area;
+    A.cm = d_cm;
+    A.cfac = 0.001 * (1.0 / dt);
     for (int id = 0; id < M_COUNT; ++id) A.m[id] = mech[id].dev;
     A.dense_mask = dense_mask;
     A.do_state = do_state;
@@ -931,8 +934,6 @@ void hx_sim::step_once() {
     S.w = d_w;
     S.a = d_a;
     S.b = d_b;
-    S.cm = d_cm;
-    S.cfac = 0.001 * (1.0 / dt);
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
@@ -1631,31 +1632,35 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
             auto positions = [&](int r, int l, int len) {
                 for (int k = 0; k < kChunk; ++k) idx[k] = k < len ? nb + ri[r].node_base + ri[r].off[k] + l : -1;
             };
+            // kernel stage arrays: DB RM A B V; back substitution reads u from RM, w from w, v from V
+            auto val = [&](int x, int k) { return idx[k] >= 0 ? arr[x][idx[k]] : neutral[x]; };
             struct In {
-                std::vector<double>* const* arr;
-                const double* neutral;
-                const int* idx;
-                double operator()(int x, int k) const { return idx[k] >= 0 ? (*arr[x])[idx[k]] : neutral[x]; }
+                std::function<double(int, int)> f;
+                std::function<double(int)> w;
+                FwdNode fwd(int k) const { return {f(SA_DB, k), f(SA_RM, k), f(SA_A, k), f(SA_B, k), f(SA_V, k)}; }
+                BackNode back(int k) const { return {f(SA_RM, k), w(k), f(SA_V, k)}; }
             };
-            std::vector<double>* fwd[kStageArrays] = {&arr[SA_DB], &arr[SA_RM], &arr[SA_A], &arr[SA_B], &arr[SA_V]};
-            // back substitution reads u from RM, w from A and v from V
-            std::vector<double>* back[kStageArrays] = {nullptr, &arr[SA_RM], &gw, nullptr, &arr[SA_V]};
+            const In in{val, [&](int k) { return idx[k] >= 0 ? gw[idx[k]] : 0.0; }};
             for (int r = nround - 1; r >= 0; --r)
                 for (int l = 0; l < ri[r].desc_count; ++l) {
                     const ChunkDesc& q = cd[ri[r].desc_begin + l];
                     positions(r, l, q.len);
-                    double acd = 0.0, ace = 0.0;
-                    for (int ch = 0; ch < q.child_count; ++ch) {
-                        acd += slots[2 * (q.child_begin + ch)];
-                        ace += slots[2 * (q.child_begin + ch) + 1];
+                    if (q.child_count > 0) {
+                        double acd = 0.0, ace = 0.0;
+                        for (int ch = 0; ch < q.child_count; ++ch) {
+                            acd += slots[2 * (q.child_begin + ch)];
+                            ace += slots[2 * (q.child_begin + ch) + 1];
+                        }
+                        const int t = idx[q.len - 1];
+                        tail_inject(arr[SA_DB][t], arr[SA_RM][t], arr[SA_V][t], acd, ace);
                     }
                     // results are written after the chunk is done (the kernel writes
                     // in place; a node's inputs are read before its outputs exist)
                     double D[kChunk], U[kChunk], W[kChunk], cdd, cee;
                     chunk_forward_math(
-                        q.len, q.parent_slot != kNone, In{fwd, neutral, idx},
-                        [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp,
-                        acd, ace, cdd, cee);
+                        q.parent_slot != kNone, in,
+                        [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp, cdd,
+                        cee);
                     for (int k = 0; k < q.len; ++k) {
                         arr[SA_DB][idx[k]] = D[k];
                         arr[SA_RM][idx[k]] = U[k];
@@ -1672,13 +1677,12 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     positions(r, l, q.len);
                     const double vpar = q.parent_slot != kNone ? slots[2 * q.parent_slot] : 0.0;
                     double VN[kChunk], X[kChunk];
-                    const double vt = chunk_back_math(q.len, In{back, neutral, idx},
-                                                      [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
+                    chunk_back_math(in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
                     for (int k = 0; k < q.len; ++k) {
                         arr[SA_V][idx[k]] = VN[k];
                         arr[SA_RM][idx[k]] = X[k];
                     }
-                    slots[2 * q.slot] = vt;
+                    slots[2 * q.slot] = VN[q.len - 1];
                 }
         }
         std::vector<double>& gv = arr[SA_V];

@@ -133,9 +133,9 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         }
         out.rounds.push_back(info);
     }
-    // padding rounds (no chunks; their loads read node 0 and they write
-    // nothing) make the round count a multiple of the kernel's pipeline depth
-    while (out.rounds.size() % kDepth) {
+    // the solve kernel runs two rounds per loop trip: an odd count gets a padding
+    // round with no chunks (its loads read node 0 and it writes nothing)
+    if (out.rounds.size() % 2) {
         RoundInfo pad{};
         pad.node_count = 1;
         out.rounds.push_back(pad);

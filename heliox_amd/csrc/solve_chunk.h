@@ -23,16 +23,18 @@
 // * The head's parent voltage v_p enters R_head only through -b_head v_p.
 //   Leaving it out, the head hands its parent the pair (cd, ce) with
 //   cd = a + (a/D) b and ce = -a v_head - (a/D) R'_head, and the parent's tail
-//   adds v_tail * sum cd + sum ce to its R (this is exactly the reference's
-//   child term).  In back substitution the missing -w_head v_p term is added
-//   back together with -w_head x_p as -w_head (v_p + x_p), i.e. with the
-//   parent's updated voltage.  Elimination therefore never reads another
-//   chunk's voltages.
+//   takes -sum cd into its diagonal and v_tail * sum cd + sum ce into its
+//   right-hand side (exactly the reference's child terms).  In back
+//   substitution the missing -w_head v_p term is added back together with
+//   -w_head x_p as -w_head (v_p + x_p), i.e. with the parent's updated
+//   voltage.  Elimination therefore never reads another chunk's voltages.
 //
-// Nodes k >= len are padding with the neutral values dm = 1, rm = a = b = v = 0;
-// they leave every quantity of the real nodes unchanged, so the loops run
-// all kChunk nodes without branches.  The results agree with the reference's
-// serial order to rounding.
+// The child terms are added to the tail's inputs before the chunk runs
+// (tail_inject), so the per-node loop has no special cases.  Nodes k >= len
+// are padding with the neutral values db = 1, rm = a = b = v = 0; they leave
+// every quantity of the real nodes unchanged, so the loops run all kChunk
+// nodes without branches.  The results agree with the reference's serial
+// order to rounding.
 #pragma once
 #include <cmath>
 
@@ -45,39 +47,53 @@ namespace hx {
 // and writes x into RM and the new v into V
 enum StageArr { SA_DB = 0, SA_RM = 1, SA_A = 2, SA_B = 3, SA_V = 4 };
 
-// In(arr, k): node k's value of stage array arr (neutral for k >= len); rcp(x)
-// returns 1/x.  Out(k, D, u, w) receives node k's results (ignored by the
-// caller for k >= len).  acd and ace: sums of cd and ce over the chunks hanging
-// off the tail.  cd and ce: this chunk's pair for its parent.
+struct FwdNode {
+    double db, rm, a, b, v;    // db = dm + cfac cm
+};
+struct BackNode {
+    double u, w, v;
+};
+
+// The tail's inputs after adding the chunk's children: acd = sum cd,
+// ace = sum ce over the chunks hanging off the tail.
+__host__ __device__ __forceinline__ void tail_inject(double& db, double& rm, double v, double acd, double ace) {
+    db = db - acd;
+    rm = rm + (v * acd + ace);
+}
+
+// in.fwd(k): node k's inputs (neutral for k >= len, tail already injected);
+// rcp(x) returns 1/x.  out(k, D, u, w) receives node k's results (ignored by
+// the caller for k >= len).  cd, ce: this chunk's pair for its parent.
+// Node k-1's inputs are fetched before node k's results are handed out, so a
+// caller reading and writing one buffer overlaps the read with the math.
 template <class In, class Out, class Rcp>
-__host__ __device__ __forceinline__ void chunk_forward_math(int len, bool has_parent, const In& in, Out&& out,
-                                                            Rcp rcp, double acd, double ace, double& cd,
-                                                            double& ce) {
+__host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, const In& in, Out&& out, Rcp rcp,
+                                                            double& cd, double& ce) {
     double P1 = 1.0, P2 = 0.0, r1 = 1.0, a1 = 0.0, ab1 = 0.0, accr = 0.0;
     cd = 0.0;
     ce = 0.0;
+    FwdNode cur = in.fwd(kChunk - 1);
 #pragma unroll
     for (int k = kChunk - 1; k >= 0; --k) {
-        double a = in(SA_A, k), b = in(SA_B, k);
+        FwdNode nxt{};
+        if (k > 0) nxt = in.fwd(k - 1);
+        double a = cur.a, b = cur.b;
         if (k == 0 && !has_parent) {
             a = 0.0;
             b = 0.0;
         }
-        const double v = in(SA_V, k);
-        const double dv = (k > 0 ? in(SA_V, k - 1) : 0.0) - v;
-        const bool tail = k == len - 1;
-        const double Db = in(SA_DB, k) - b - (tail ? acd : 0.0);
-        const double Rb = in(SA_RM, k) - b * dv + (tail ? v * acd + ace : 0.0);
-        const double P = (Db - a1) * P1 - ab1 * P2;
+        const double dv = (k > 0 ? nxt.v : 0.0) - cur.v;
+        const double Db = cur.db - b;
+        const double Rb = fma(-b, dv, cur.rm);
+        const double P = fma(Db - a1, P1, -(ab1 * P2));
         const double r = rcp(P);
         const double rD = P1 * r;     // 1 / D_k
-        const double D = P * r1;      // P_k / P_{k+1}
         const double R = Rb + accr;
         const double p = a * rD;
-        accr = a * dv - p * R;
-        out(k, D, R * rD, b * rD);
+        accr = fma(a, dv, -(p * R));
+        out(k, P * r1, R * rD, b * rD);
         if (k == 0) {
-            cd = a + p * b;
+            cd = fma(p, b, a);
             ce = accr;
         }
         P2 = P1;
@@ -85,24 +101,25 @@ __host__ __device__ __forceinline__ void chunk_forward_math(int len, bool has_pa
         r1 = r;
         a1 = a;
         ab1 = a * b;
+        cur = nxt;
     }
 }
 
-// In(arr, k) as above (RM = u, A = w, V = v); vpar_new: updated voltage of the
-// head's parent (0 for the root chunk, whose w_0 is 0).  Out(k, v_new, x).
-// Returns the tail's updated voltage.
+// in.back(k): node k's (u, w, v) (neutral for k >= len); vpar_new: updated
+// voltage of the head's parent (0 for the root chunk, whose w_0 is 0).
+// out(k, v_new, x).
 template <class In, class Out>
-__host__ __device__ __forceinline__ double chunk_back_math(int len, const In& in, Out&& out, double vpar_new) {
-    double x = vpar_new, vtail = 0.0;
+__host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new) {
+    double x = vpar_new;
+    BackNode cur = in.back(0);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
-        const double u = in(SA_RM, k), w = in(SA_A, k), v = in(SA_V, k);
-        x = u - w * x;
-        const double vn = v + x;
-        out(k, vn, x);
-        if (k == len - 1) vtail = vn;
+        BackNode nxt{};
+        if (k + 1 < kChunk) nxt = in.back(k + 1);
+        x = fma(-cur.w, x, cur.u);
+        out(k, cur.v + x, x);
+        cur = nxt;
     }
-    return vtail;
 }
 
 }  // namespace hx
