@@ -50,6 +50,14 @@ struct MechDev {
     const int* node = nullptr;    // solver-order node of each instance
     const int* ion[3] = {nullptr, nullptr, nullptr};   // na, k, ca instance of each instance
     const int* iontype = nullptr; // ions only
+    // point processes: instances grouped by node (instances are sorted by node):
+    // group g is node grp_node[g] with instances [grp_begin[g], grp_begin[g+1])
+    const int* grp_node = nullptr;
+    const int* grp_begin = nullptr;
+    int ngrp = 0;
+    // synapses folded into the node kernel: instances on the nodes of node-kernel
+    // block b are [blk_begin[b], blk_begin[b+1])
+    const int* blk_begin = nullptr;
     __host__ __device__ double* col(int c) const { return base + c * stride; }
 };
 
@@ -76,6 +84,7 @@ struct StepArgs {
     int do_current;
     int write_assigned;           // also store assigned outputs (i, ina, gna, minf, ...)
     unsigned ion_store;           // ion x (0 na, 1 k, 2 ca): bit 2x stores cur, bit 2x+1 stores erev
+    unsigned fold_mask;           // point processes whose currents the node kernel adds (bit = MechId)
     int ion_type[3];              // iontype shared by every instance of ion x, or -1 (read per instance)
     double t;                     // time of the current evaluation (t_n + dt/2)
     double dt;
@@ -85,6 +94,7 @@ struct StepArgs {
 // Chunked tree-solve schedule (one wavefront per cell).  Indices are relative
 // to the cell (cells are limited to 65535 nodes and 65535 chunks), so a
 // descriptor packs into 8 bytes.
+constexpr int kBlock = 256;       // threads per block of the node-parallel kernels
 constexpr uint16_t kNone = 0xFFFF;
 constexpr int kChunk = 16;        // max nodes per chunk (one lane's serial run)
 constexpr int kWave = 64;

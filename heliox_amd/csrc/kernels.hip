@@ -29,7 +29,6 @@ namespace hx {
 
 namespace {
 
-constexpr int kBlock = 256;
 
 __device__ __forceinline__ int ion_index(const MechDev& m, int which, int j) {
     const int* p = m.ion[which];
@@ -184,16 +183,25 @@ __device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev
 
 #define HAS(bit) (A.dense_mask & (1u << (bit)))
 
+// Point-process currents of one mechanism on the nodes of this block, summed
+// in instance order (instances are sorted by node).  s_first / s_last: LDS
+// tables of kBlock ints.  Every thread of the block must call it.
+template <int MECH>
+__device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, double v, int* s_first,
+                                           int* s_last, double& rhs, double& d);
+
 // ---------------------------------------------------------------------------
 // fused node-parallel kernel for dense mechanisms: the previous step's state
 // update (ion writers first, simulate.cpp:822-834) and this step's currents in
-// CoreNEURON mechanism order.  Ion currents are summed in registers and each
-// ion array is written once.
+// CoreNEURON mechanism order, with the synapse (ExpSyn, Exp2Syn) currents of
+// the block's nodes added in their place.  Ion currents are summed in
+// registers and each ion array is written once.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
+    __shared__ int s_first[kBlock], s_last[kBlock];
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= A.N) return;
-    const double v = A.v[i];
+    const bool live = i < A.N;
+    const double v = live ? A.v[i] : 0.0;
     const MechDev& na = A.m[M_NA_ION];
     const MechDev& kk = A.m[M_K_ION];
     const MechDev& ca = A.m[M_CA_ION];
@@ -201,24 +209,31 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     CaHVAState cs{};
     double hl = 0.0, cai = 0.0;
     const bool have_cai = A.do_state && HAS(M_CADYN);
-    if (A.do_state) {
-        if (HAS(M_CADYN)) {
-            double* conci = ca.col(ION_CONCI);
-            cai = cadyn_state(A, A.m[M_CADYN], i, conci[i], ca.col(ION_CUR)[i]);
-            conci[i] = cai;
+    if (live) {
+        if (A.do_state) {
+            if (HAS(M_CADYN)) {
+                double* conci = ca.col(ION_CONCI);
+                cai = cadyn_state(A, A.m[M_CADYN], i, conci[i], ca.col(ION_CUR)[i]);
+                conci[i] = cai;
+            }
+            if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, hh_load(A.m[M_HH], i));
+            if (HAS(M_CAHVA))
+                cs = cahva_state(A, A.m[M_CAHVA], i, v, cahva_load(A.m[M_CAHVA], i), ca.col(ION_EREV), i);
+            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, A.m[M_HDLA].col(HD_L)[i]);
+        } else if (A.do_current) {
+            if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
+            if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
+            if (HAS(M_HDLA)) hl = A.m[M_HDLA].col(HD_L)[i];
         }
-        if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, hh_load(A.m[M_HH], i));
-        if (HAS(M_CAHVA)) cs = cahva_state(A, A.m[M_CAHVA], i, v, cahva_load(A.m[M_CAHVA], i), ca.col(ION_EREV), i);
-        if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, A.m[M_HDLA].col(HD_L)[i]);
-    } else if (A.do_current) {
-        if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
-        if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
-        if (HAS(M_HDLA)) hl = A.m[M_HDLA].col(HD_L)[i];
     }
     if (!A.do_current) return;
     // the capacitance term of the diagonal (capac.cpp:68-80) is added here,
     // ahead of the membrane conductances, so the solve reads one diagonal
-    double rhs = 0.0, d = A.cfac * A.cm[i], g, cur;
+    double rhs = 0.0, d = live ? A.cfac * A.cm[i] : 0.0, g, cur;
+    double prhs = 0.0, pd = 0.0;
+    if (A.fold_mask & (1u << M_EXPSYN)) fold_point<M_EXPSYN>(A, i, live, v, s_first, s_last, prhs, pd);
+    if (A.fold_mask & (1u << M_EXP2SYN)) fold_point<M_EXP2SYN>(A, i, live, v, s_first, s_last, prhs, pd);
+    if (!live) return;
     double ena = 0.0, ek = 0.0, eca = 0.0, ina = 0.0, ik = 0.0, ica = 0.0;
     if (HAS(M_PAS)) { cur = pas_cur(A, A.m[M_PAS], i, v, g); rhs -= cur; d += g; }
     if (HAS(M_NA_ION)) ena = dense_ion_erev(A, na, 0, i, 1.0, false, 0.0);
@@ -230,6 +245,8 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
         ik += ik_h;
         rhs -= cur; d += g;
     }
+    rhs += prhs;   // ExpSyn, Exp2Syn (mechanism types 5, 6)
+    d += pd;
     if (HAS(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai, cai);
     if (HAS(M_CAHVA)) {
         cur = cahva_cur(A, A.m[M_CAHVA], i, v, cs, eca, g);
@@ -299,54 +316,98 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// point processes: FD current, x 1e2/area, fp64 atomics (several per node)
+// point processes: FD current x 1e2/area (mech_template.cuh:616-646).  One
+// thread per node that carries instances of the mechanism sums them and
+// updates d and rhs of that node once, so no atomics are needed (each launch
+// covers one mechanism; launches are ordered on the stream).
 // ---------------------------------------------------------------------------
 template <int MECH>
-__global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
-    const MechDev& m = A.m[MECH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const double v = A.v[node];
+__device__ __forceinline__ void point_current(const StepArgs& A, const MechDev& m, int j, double v, double& i0,
+                                              double& g) {
     const double v1 = v + 0.001;
-    double i1 = 0.0, i0 = 0.0;
-    bool electrode = false;
+    double i1 = 0.0;
+    i0 = 0.0;
     if (MECH == M_ICLAMP) {
-        double del = m.col(IC_DELAY)[j], dur = m.col(IC_DUR)[j];
+        const double del = m.col(IC_DELAY)[j], dur = m.col(IC_DUR)[j];
         double cur = 0.0;
         if (A.t < del + dur && A.t >= del) cur = m.col(IC_AMP)[j];
-        i1 = cur; i0 = cur;
+        i1 = cur;
+        i0 = cur;
         if (A.write_assigned) m.col(IC_I)[j] = cur;
-        electrode = true;
     } else if (MECH == M_HALFGAP) {
-        double vg = m.col(HG_VGAP)[j], gg = m.col(HG_G)[j];
+        const double vg = m.col(HG_VGAP)[j], gg = m.col(HG_G)[j];
         i1 = (vg - v1) * gg;
         i0 = (vg - v) * gg;
         if (A.write_assigned) m.col(HG_I)[j] = i0;
-        electrode = true;
     } else if (MECH == M_EXPSYN) {
-        double gg = m.col(ES_G)[j], e = m.col(ES_E)[j];
+        const double gg = m.col(ES_G)[j], e = m.col(ES_E)[j];
         i1 = gg * (v1 - e);
         i0 = gg * (v - e);
         if (A.write_assigned) m.col(ES_I)[j] = i0;
     } else if (MECH == M_EXP2SYN) {
-        double gg = m.col(E2_B)[j] - m.col(E2_A)[j];
-        double e = m.col(E2_E)[j];
+        const double gg = m.col(E2_B)[j] - m.col(E2_A)[j];
+        const double e = m.col(E2_E)[j];
         i1 = gg * (v1 - e);
         i0 = gg * (v - e);
         if (A.write_assigned) { m.col(E2_G)[j] = gg; m.col(E2_I)[j] = i0; }
     }
-    double g = (i1 - i0) / 0.001;
-    double mfact = 1.e2 / A.area[node];
-    g *= mfact;
-    i0 *= mfact;
-    if (electrode) {
-        atomicAdd(&A.rhs[node], i0);
-        atomicAdd(&A.d[node], -g);
-    } else {
-        atomicAdd(&A.rhs[node], -i0);
-        atomicAdd(&A.d[node], g);
+    g = (i1 - i0) / 0.001;
+}
+
+template <int MECH>
+__device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, double v, int* s_first,
+                                           int* s_last, double& rhs, double& d) {
+    const MechDev& m = A.m[MECH];
+    const int b0 = blockIdx.x * kBlock;
+    const int s0 = m.blk_begin[blockIdx.x], s1 = m.blk_begin[blockIdx.x + 1];
+    if (s1 == s0) return;                        // same for the whole block
+    const int t = threadIdx.x;
+    s_first[t] = 0;
+    s_last[t] = 0;
+    __syncthreads();
+    for (int s = s0 + t; s < s1; s += kBlock) {
+        const int node = m.node[s];
+        if (s == s0 || m.node[s - 1] != node) s_first[node - b0] = s;
+        if (s == s1 - 1 || m.node[s + 1] != node) s_last[node - b0] = s + 1;
     }
+    __syncthreads();
+    const int f = s_first[t], l = s_last[t];
+    if (live && l > f) {
+        const double mfact = 1.e2 / A.area[i];
+        for (int j = f; j < l; ++j) {
+            double i0, g;
+            point_current<MECH>(A, m, j, v, i0, g);
+            rhs -= i0 * mfact;
+            d += g * mfact;
+        }
+    }
+    __syncthreads();                             // the tables are reused by the next mechanism
+}
+
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= m.ngrp) return;
+    const int node = m.grp_node[q];
+    const double v = A.v[node];
+    const double mfact = 1.e2 / A.area[node];
+    double rhs = 0.0, d = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) {
+        double i0, g;
+        point_current<MECH>(A, m, j, v, i0, g);
+        g *= mfact;
+        i0 *= mfact;
+        if (MECH == M_ICLAMP || MECH == M_HALFGAP) {   // ELECTRODE_CURRENT: the sign flips
+            rhs += i0;
+            d -= g;
+        } else {
+            rhs -= i0;
+            d += g;
+        }
+    }
+    A.rhs[node] += rhs;
+    A.d[node] += d;
 }
 
 template <int MECH>
@@ -941,7 +1002,7 @@ void launch_sparse(int mech, const StepArgs& a, hipStream_t s) {
 }
 
 void launch_point_current(int mech, const StepArgs& a, hipStream_t s) {
-    const int n = a.m[mech].n;
+    const int n = a.m[mech].ngrp;
     if (n <= 0) return;
     switch (mech) {
         case M_ICLAMP: hipLaunchKernelGGL(k_point<M_ICLAMP>, grid_for(n), dim3(kBlock), 0, s, a); break;

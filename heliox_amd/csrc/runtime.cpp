@@ -158,7 +158,9 @@ struct VecPlayHost {
     double* d_y = nullptr;
 };
 
-struct Ref { double* dev = nullptr; int klass = 0; };   // klass 0 param/state, 1 assigned
+// klass 0 param/state, 1 assigned; point: a point-process column (its values
+// change at event delivery, which the fused schedule runs before the record)
+struct Ref { double* dev = nullptr; int klass = 0; bool point = false; };
 
 struct Timer {
     std::vector<hipEvent_t> pool;
@@ -505,6 +507,25 @@ void hx_sim::upload() {
         std::vector<int> nodes(m.n);
         for (int j = 0; j < m.n; ++j) nodes[j] = node_perm[m.node[m.iperm[j]]];
         d.node = dupload(owned, nodes);
+        if (R[id].point && m.n > 0) {
+            std::vector<int> gnode, gbeg;
+            for (int j = 0; j < m.n; ++j)
+                if (j == 0 || nodes[j] != nodes[j - 1]) {
+                    gnode.push_back(nodes[j]);
+                    gbeg.push_back(j);
+                }
+            gbeg.push_back(m.n);
+            d.ngrp = static_cast<int>(gnode.size());
+            d.grp_node = dupload(owned, gnode);
+            d.grp_begin = dupload(owned, gbeg);
+            if (id == M_EXPSYN || id == M_EXP2SYN) {
+                const int nblk = (nnode + kBlock - 1) / kBlock;
+                std::vector<int> bb(nblk + 1);
+                for (int b = 0; b <= nblk; ++b)
+                    bb[b] = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), b * kBlock) - nodes.begin());
+                d.blk_begin = dupload(owned, bb);
+            }
+        }
         if (R[id].ion) {
             std::vector<int> it(m.n);
             for (int j = 0; j < m.n; ++j) it[j] = m.iontype[m.iperm[j]];
@@ -739,6 +760,7 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     if (c < 0 || idx < 0 || idx >= m.n) return r;
     r.dev = m.dev.col(c) + m.perm[idx];
     r.klass = c >= M.nparam + M.nstate ? 1 : 0;
+    r.point = M.point;
     if (id == M_EXP2SYN && c == E2_FACTOR) r.klass = 0;   // written by INITIAL
     if (id == M_HALFGAP && c == HG_VGAP) r.klass = 0;     // written by the gap transfer
     return r;
@@ -775,6 +797,9 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
             A.ion_type[x] = ion_type_uniform[x];
         }
     }
+    A.fold_mask = 0;
+    for (int id : {M_EXPSYN, M_EXP2SYN})
+        if (mech[id].present && mech[id].n > 0) A.fold_mask |= 1u << id;
     A.t = tcur;
     A.dt = dt;
     auto G = [&](int id, const char* k, double dflt) {
@@ -831,11 +856,11 @@ void hx_sim::launch_point_currents(double tcur) {
     StepArgs A = step_args(tcur, 0, 1);
     const int pts[] = {M_ICLAMP, M_EXPSYN, M_EXP2SYN, M_HALFGAP};   // CoreNEURON order
     bool any = false;
-    for (int id : pts) any |= mech[id].present && mech[id].n > 0;
+    for (int id : pts) any |= mech[id].present && mech[id].n > 0 && !(A.fold_mask & (1u << id));
     if (!any) return;
     tbegin(T_POINT);
-    for (int id : pts)
-        if (mech[id].present) launch_point_current(id, A, stream);
+    for (int id : pts)   // synapse currents are added by the node kernel
+        if (mech[id].present && !(A.fold_mask & (1u << id))) launch_point_current(id, A, stream);
     tend(T_POINT);
 }
 
@@ -911,10 +936,14 @@ void hx_sim::step_once() {
     const bool has_vp = !vecplay.empty();
     const int nvp = static_cast<int>(vecplay.size());
     if (fused) {
-        launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
-        if (state_pending) launch_record();
+        // events and VecPlay touch only point processes here (a non-point VecPlay
+        // target selects the split schedule), so they may precede the previous
+        // step's deferred state update; the node kernel then adds the synapse
+        // currents with this step's deliveries in place
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
+        if (state_pending) launch_record();
     } else {
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
@@ -1274,7 +1303,7 @@ int hx_load_model(hx_sim* sim) {
         if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", sim->mon_name[i].first.c_str(),
                                      sim->mon_name[i].second.c_str(), sim->mon_idx[i]);
         sim->mon_ref[i] = r;
-        if (r.klass == 1) {
+        if (r.klass == 1 || r.point) {
             // assigned outputs are sampled where the reference records them: split passes
             sim->need_split_for_monitor = true;
             sim->write_assigned = true;
@@ -1333,9 +1362,9 @@ int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx) {
         API_BEGIN
         r = sim->resolve(mech, var, idx);
         if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", mech, var, idx);
-        if (r.klass == 1 && !sim->need_split_for_monitor) {
+        if ((r.klass == 1 || r.point) && !sim->need_split_for_monitor) {
             sim->need_split_for_monitor = true;
-            sim->write_assigned = true;
+            sim->write_assigned = sim->write_assigned || r.klass == 1;
             sim->fused = false;
             if (sim->state_pending) { sim->finish_pending(); sim->sync_outputs(); }
         }

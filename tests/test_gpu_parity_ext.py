@@ -103,9 +103,20 @@ def test_monitors_on_assigned_variables_use_split_schedule(gpu_lib):
 
 def test_state_monitors_keep_fused_schedule(gpu_lib):
     spec = build_config(3, 1, 20.0)
-    mons = [("global", "v", 0), ("hh", "m", 0), ("hd_la", "l", 40), ("Exp2Syn", "A", 0), ("ca_ion", "conci", 3)]
+    mons = [("global", "v", 0), ("hh", "m", 0), ("hd_la", "l", 40), ("ca_ion", "conci", 3)]
     o, g = run_both(spec, 20.0, monitors=mons)
     assert g.info("fused") == 1
+    assert np.max(np.abs(o.traces() - g.traces())) < 1e-9
+
+
+def test_point_process_monitors_use_split_schedule(gpu_lib):
+    """Event delivery runs before the deferred state update in the fused
+    schedule, so a monitor on a synapse variable selects the split schedule,
+    where it samples at the reference's record point."""
+    spec = build_config(3, 1, 20.0)
+    mons = [("global", "v", 0), ("Exp2Syn", "A", 0), ("Exp2Syn", "B", 3), ("hh", "m", 0)]
+    o, g = run_both(spec, 20.0, monitors=mons)
+    assert g.info("fused") == 0
     assert np.max(np.abs(o.traces() - g.traces())) < 1e-9
 
 
