@@ -91,6 +91,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--all-kernel-timing", action="store_true",
+                    help="time every kernel class (adds event records to the timed region)")
     ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
 
@@ -122,7 +124,9 @@ def main():
     sim.finitialize(-65.0)
     if args.warmup:
         sim.continue_run((args.warmup + 0.5) * dt)
-    sim.set_profiling(not args.no_kernel_timing)
+    # only the dominant kernel is timed with events on the stream (each timed
+    # class adds two event records per step to the timed region)
+    sim.set_profiling(not args.no_kernel_timing, classes=None if args.all_kernel_timing else ["mech"])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     sim.continue_run((args.steps + 0.5) * dt)      # returns after the stream is synchronized

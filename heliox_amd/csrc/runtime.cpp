@@ -269,6 +269,7 @@ struct hx_sim {
     bool initialized = false;
     // profiling
     bool profiling = false;
+    unsigned prof_mask = ~0u;   // timed kernel classes (bit = TimerId)
     Timer timers[T_COUNT];
 
     ~hx_sim() {
@@ -290,7 +291,7 @@ struct hx_sim {
 
     // ------------------------------------------------------------ timing
     void tbegin(int id) {
-        if (!profiling) return;
+        if (!profiling || !(prof_mask & (1u << id))) return;
         Timer& tm = timers[id];
         while (tm.pool.size() < tm.used + 2) {
             hipEvent_t e;
@@ -302,7 +303,7 @@ struct hx_sim {
         tm.used += 2;
     }
     void tend(int id) {
-        if (!profiling) return;
+        if (!profiling || !(prof_mask & (1u << id))) return;
         Timer& tm = timers[id];
         HXC(hipEventRecord(tm.pool[tm.pending.back().second], stream));
     }
@@ -1611,6 +1612,30 @@ int hx_set_fusion(hx_sim* sim, int enable) {
 
 int hx_set_profiling(hx_sim* sim, int enable) {
     sim->profiling = enable != 0;
+    sim->prof_mask = ~0u;
+    for (auto& tm : sim->timers) { tm.ms = 0; tm.launches = 0; }
+    return 0;
+}
+
+int hx_set_profiling_classes(hx_sim* sim, const char* classes) {
+    unsigned mask = 0;
+    std::string all = classes ? classes : "";
+    size_t pos = 0;
+    while (pos <= all.size()) {
+        size_t e = all.find(',', pos);
+        if (e == std::string::npos) e = all.size();
+        const std::string name = all.substr(pos, e - pos);
+        if (!name.empty()) {
+            int id = -1;
+            for (int i = 0; i < T_COUNT; ++i)
+                if (name == kTimerNames[i]) id = i;
+            if (id < 0) return sim->fail("unknown kernel class '%s'", name.c_str());
+            mask |= 1u << id;
+        }
+        pos = e + 1;
+    }
+    sim->profiling = mask != 0;
+    sim->prof_mask = mask;
     for (auto& tm : sim->timers) { tm.ms = 0; tm.launches = 0; }
     return 0;
 }

@@ -83,6 +83,7 @@ SIGNATURES = {
     "hx_set_event_capacity": (C.c_int, [_P, C.c_int]),
     "hx_set_fusion": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling": (C.c_int, [_P, C.c_int]),
+    "hx_set_profiling_classes": (C.c_int, [_P, _S]),
     "hx_get_kernel_time": (C.c_int, [_P, _S, _D, C.POINTER(C.c_longlong)]),
     "hx_get_info": (C.c_longlong, [_P, _S]),
     "hx_emulate_tree_solve": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, _I, _I]),
@@ -356,7 +357,10 @@ class Sim:
         return out[:k].tolist()
 
     # --------------------------------------------------------------- profiling
-    def set_profiling(self, enable: bool) -> int:
+    def set_profiling(self, enable: bool, classes: Optional[Sequence[str]] = None) -> int:
+        """Per-kernel-class HIP-event timing; ``classes`` limits it to those classes."""
+        if enable and classes is not None:
+            return self._rc(lib().hx_set_profiling_classes(self._h, _b(",".join(classes))))
         return self._rc(lib().hx_set_profiling(self._h, 1 if enable else 0))
 
     def kernel_time(self, kernel: str):

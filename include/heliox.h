@@ -121,6 +121,9 @@ int hx_set_fusion(hx_sim* sim, int enable);
  * accumulated milliseconds and launch counts for a kernel class
  * ("mech", "sparse", "point", "solve", "spike", "events", "other"). */
 int hx_set_profiling(hx_sim* sim, int enable);
+/* Time only the listed classes (comma-separated, e.g. "mech"); "" turns timing off.
+ * Fewer timed classes means fewer events on the stream, so less perturbation. */
+int hx_set_profiling_classes(hx_sim* sim, const char* classes);
 int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches);
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused". */
 long long hx_get_info(hx_sim* sim, const char* key);
