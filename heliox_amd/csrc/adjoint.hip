@@ -1,0 +1,232 @@
+// Adjoint (vector-Jacobian) backward step of the fixed-step simulation, for
+// models made of pas, hh, ExpSyn (+ ions with fixed reversal potentials and
+// IClamp).  No reference code exists for this; it differentiates the step the
+// forward kernels take (simulate.cpp:410-442 order).
+//
+// Step n maps (v^n, x^n, g^n) to (v^{n+1}, x^{n+1}, g^{n+1}):
+//   g_eff = g^n + sum of the weights delivered at step n         (ExpSyn)
+//   M (v^{n+1} - v^n) = -I(v^n) - K v^n,  M = C + G + K           (tree solve)
+//     C = 1e-3 cm / dt, G = membrane conductance (all mechanisms here are
+//     linear in v, so the FD Jacobian is G), K = the axial matrix
+//   x^{n+1} = cnexp(x^n, v^{n+1})                                 (hh gates)
+//   g^{n+1} = g_eff exp(-dt / tau)                                (ExpSyn decay)
+// With I linear in v:  dv^{n+1}/dv^n = M^{-1} C  and, for anything p that G
+// depends on,  dv^{n+1}/dp = -M^{-1} dG/dp (v^{n+1} - E).  So with
+// mu = M^{-T} lambda_v^{n+1}:
+//   lambda_v^n = C mu (+ loss term),
+//   dL/dp     += -mu_i dI_i/dp evaluated at v^{n+1},
+// and the gates add their cnexp derivative (dual numbers through the rate
+// functions) to lambda_v^{n+1} before the solve.  M^T is solved with the same
+// tree kernel by swapping a and b and correcting the diagonal (the kernel
+// assembles it from a and b).
+#include "hx_internal.h"
+#include "mech_math.h"
+
+namespace hx {
+namespace {
+
+__device__ __forceinline__ int ion_of(const MechDev& m, int which, int j) {
+    return m.ion[which] ? m.ion[which][j] : j;
+}
+
+// hh gates: lambda_x <- alpha lambda_x, lambda_v[node] += dx^{n+1}/dv^{n+1} . lambda_x
+__global__ void k_adj_hh_state(AdjStep A) {
+    const MechDev& m = A.m[M_HH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const Dual v1{A.v1[node], 1.0};
+    Dual minf, mtau, hinf, htau, ninf, ntau;
+    hh_rates(v1, A.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
+    const double x0[3] = {A.x0[j], A.x0[A.xstride + j], A.x0[2 * A.xstride + j]};
+    const Dual xn[3] = {hh_cnexp(x0[0], minf, mtau, A.dt), hh_cnexp(x0[1], hinf, htau, A.dt),
+                        hh_cnexp(x0[2], ninf, ntau, A.dt)};
+    const double tau[3] = {mtau.v, htau.v, ntau.v};
+    double dv = 0.0;
+    for (int g = 0; g < 3; ++g) {
+        const double lx = A.lam_x[g * A.xstride + j];
+        dv += xn[g].d * lx;
+        A.lam_x[g * A.xstride + j] = exp(A.dt * (-1.0 / tau[g])) * lx;   // d cnexp / d x
+    }
+    A.lam_v[node] += dv;
+}
+
+// ExpSyn decay: lambda_geff = exp(-dt/tau) lambda_g (in place)
+__global__ void k_adj_syn_state(AdjStep A) {
+    const MechDev& m = A.m[M_EXPSYN];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    A.lam_g[j] = exp(-A.dt / m.col(ES_TAU)[j]) * A.lam_g[j];
+}
+
+// transposed system: d = C + delta, rhs = lambda_v, v = 0
+__global__ void k_adj_assemble(AdjStep A) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.N) return;
+    A.dT[i] = A.cfac * A.cm[i] + A.delta[i];
+    A.rhsT[i] = A.lam_v[i];
+    A.vT[i] = 0.0;
+}
+
+// membrane conductances G at step n (one instance per node for pas and hh)
+__global__ void k_adj_cond_pas(AdjStep A) {
+    const MechDev& m = A.m[M_PAS];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    A.dT[m.node[j]] += m.col(PAS_G)[j];
+}
+
+__global__ void k_adj_cond_hh(AdjStep A) {
+    const MechDev& m = A.m[M_HH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
+    A.dT[m.node[j]] += m.col(HH_GNABAR)[j] * mm * mm * mm * hh + m.col(HH_GKBAR)[j] * nn * nn * nn * nn +
+                       m.col(HH_GL)[j];
+}
+
+// synapses grouped by node: sum of g_eff x 1e2/area
+__global__ void k_adj_cond_syn(AdjStep A) {
+    const MechDev& m = A.m[M_EXPSYN];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= m.ngrp) return;
+    const int node = m.grp_node[q];
+    double g = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.geff[j];
+    A.dT[node] += g * (1.e2 / A.area[node]);
+}
+
+// lambda_v^n = C mu
+__global__ void k_adj_node(AdjStep A) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.N) return;
+    A.lam_v_new[i] = A.cfac * A.cm[i] * A.mu[i];
+}
+
+__global__ void k_adj_hh_param(AdjStep A) {
+    const MechDev& m = A.m[M_HH];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const double mu = A.mu[node], v1 = A.v1[node];
+    const double ena = A.m[M_NA_ION].col(ION_EREV)[ion_of(m, 0, j)];
+    const double ek = A.m[M_K_ION].col(ION_EREV)[ion_of(m, 1, j)];
+    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
+    const double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
+    A.lam_x[j] -= mu * 3.0 * gnabar * mm * mm * hh * (v1 - ena);
+    A.lam_x[A.xstride + j] -= mu * gnabar * mm * mm * mm * (v1 - ena);
+    A.lam_x[2 * A.xstride + j] -= mu * 4.0 * gkbar * nn * nn * nn * (v1 - ek);
+    A.grad_gnabar[j] -= mu * mm * mm * mm * hh * (v1 - ena);
+    A.grad_gkbar[j] -= mu * nn * nn * nn * nn * (v1 - ek);
+}
+
+__global__ void k_adj_pas_param(AdjStep A) {
+    const MechDev& m = A.m[M_PAS];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    A.grad_gpas[j] -= A.mu[node] * (A.v1[node] - m.col(PAS_E)[j]);
+}
+
+// lambda_geff += -mu (v^{n+1} - e) 1e2/area
+__global__ void k_adj_syn_param(AdjStep A) {
+    const MechDev& m = A.m[M_EXPSYN];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    A.lam_g[j] -= A.mu[node] * (A.v1[node] - m.col(ES_E)[j]) * (1.e2 / A.area[node]);
+}
+
+// events delivered at step n: dL/dw += lambda_geff (one block)
+__global__ void __launch_bounds__(256) k_adj_events(AdjStep A) {
+    const int cnt = A.ev_count[0];
+    for (int e = threadIdx.x; e < cnt; e += blockDim.x) {
+        const int inst = A.ev[e];
+        atomicAdd(&A.grad_w[inst], A.lam_g[inst]);
+    }
+}
+
+// loss term of v^n: lambda_v^n[node] += 2 scale (v^n - target^n)
+__global__ void k_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale,
+                           double* lam) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    lam[nodes[j]] += 2.0 * scale * (v[nodes[j]] - target[j]);
+}
+
+// out[r * nnodes + j] = tape_v[r * row + nodes[j]]
+__global__ void k_adj_gather(const double* tape_v, long long row, const int* nodes, int nnodes, int nrows,
+                             double* out) {
+    const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<long long>(nnodes) * nrows) return;
+    const long long r = t / nnodes;
+    const int j = static_cast<int>(t - r * nnodes);
+    out[t] = tape_v[r * row + nodes[j]];
+}
+
+// Adam: one thread per tied group (optimizer.cpp:351-393, optimizer_kernels.cu:173-195)
+__global__ void k_adam(AdamArgs A) {
+    const int g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= A.ngroup) return;
+    const int b0 = A.begin[g], b1 = A.begin[g + 1];
+    if (b1 <= b0) return;
+    double sum = 0.0;
+    for (int k = b0; k < b1; ++k) sum += *A.grad[k];
+    const double avg = sum / static_cast<double>(b1 - b0);
+    const double sg = avg * A.impedance[g] * A.inv_record_steps;
+    const double m = A.beta1 * A.m[g] + (1.0 - A.beta1) * sg;
+    const double v = A.beta2 * A.v[g] + (1.0 - A.beta2) * sg * sg;
+    A.m[g] = m;
+    A.v[g] = v;
+    const double mhat = m / (1.0 - pow(A.beta1, static_cast<double>(A.step)));
+    const double vhat = v / (1.0 - pow(A.beta2, static_cast<double>(A.step)));
+    const double w = *A.w[b0] - A.lr * mhat / (sqrt(vhat) + A.eps);
+    for (int k = b0; k < b1; ++k) {
+        *A.w[k] = w;
+        *A.grad[k] = 0.0;
+    }
+}
+
+inline dim3 grid_of(long long n, int block = kBlock) {
+    long long g = (n + block - 1) / block;
+    return dim3(static_cast<unsigned>(g > 0 ? g : 1));
+}
+
+}  // namespace
+
+void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
+    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_state, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_adj_assemble, grid_of(a.N), dim3(kBlock), 0, s, a);
+    if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_cond_hh, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXPSYN].ngrp > 0)
+        hipLaunchKernelGGL(k_adj_cond_syn, grid_of(a.m[M_EXPSYN].ngrp), dim3(kBlock), 0, s, a);
+}
+
+void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_adj_node, grid_of(a.N), dim3(kBlock), 0, s, a);
+    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXPSYN].n > 0) {
+        hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
+    }
+}
+
+void launch_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale, double* lam,
+                     hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_adj_loss, grid_of(n), dim3(kBlock), 0, s, v, nodes, target, n, scale, lam);
+}
+
+void launch_adj_gather(const double* tape_v, long long row, const int* nodes, int nnodes, int nrows, double* out,
+                       hipStream_t s) {
+    const long long n = static_cast<long long>(nnodes) * nrows;
+    if (n > 0) hipLaunchKernelGGL(k_adj_gather, grid_of(n), dim3(kBlock), 0, s, tape_v, row, nodes, nnodes, nrows, out);
+}
+
+void launch_adam(const AdamArgs& a, hipStream_t s) {
+    if (a.ngroup > 0) hipLaunchKernelGGL(k_adam, grid_of(a.ngroup), dim3(kBlock), 0, s, a);
+}
+
+}  // namespace hx

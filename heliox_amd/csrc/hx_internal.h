@@ -198,6 +198,51 @@ struct DeliverArgs {
     MechDev e2;                   // Exp2Syn
     const double* es_weight;
     const double* e2_weight;
+    int* log_count;               // when set: ExpSyn instances receiving an event are appended
+    int* log;                     // to log[0 .. *log_count) (capacity ring.cap), for the adjoint
+};
+
+// One backward step of the adjoint (adjoint.hip).  v1, x0, geff: the taped
+// v^{n+1} (node order), hh gates x^n (3 columns of xstride) and ExpSyn g_eff^n.
+struct AdjStep {
+    int N;
+    double dt, cfac, hh_q10;
+    const double* cm;
+    const double* area;
+    const double* delta;          // diagonal correction of the transposed solve
+    MechDev m[M_COUNT];
+    const double* v1;
+    const double* x0;
+    long long xstride;
+    const double* geff;
+    double* lam_v;                // adjoint of v^{n+1}
+    double* lam_v_new;            // adjoint of v^n
+    double* lam_x;                // adjoint of the gates (x^{n+1} in, x^n out)
+    double* lam_g;                // adjoint of ExpSyn g (g^{n+1} in, g^n out)
+    double* dT;
+    double* rhsT;
+    double* vT;
+    const double* mu;             // M^{-T} lam_v (the transposed solve's solution)
+    double* grad_gnabar;
+    double* grad_gkbar;
+    double* grad_gpas;
+    double* grad_w;               // ExpSyn netcon weights
+    const int* ev_count;          // events delivered at step n
+    const int* ev;
+};
+
+// Adam over tied parameter groups (optimizer.cpp:351-393): group g covers
+// entries [begin[g], begin[g+1]) of the weight and gradient pointer lists.
+struct AdamArgs {
+    int ngroup;
+    const int* begin;
+    double* const* w;
+    double* const* grad;
+    const double* impedance;
+    double* m;
+    double* v;
+    double lr, inv_record_steps, beta1, beta2, eps;
+    long long step;
 };
 
 struct VecPlayDev {
@@ -232,6 +277,13 @@ void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s);
+void launch_adj_before_solve(const AdjStep& a, hipStream_t s);
+void launch_adj_after_solve(const AdjStep& a, hipStream_t s);
+void launch_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale, double* lam,
+                     hipStream_t s);
+void launch_adj_gather(const double* tape_v, long long row, const int* nodes, int nnodes, int nrows, double* out,
+                       hipStream_t s);
+void launch_adam(const AdamArgs& a, hipStream_t s);
 void launch_spike(const SpikeArgs& a, hipStream_t s);
 void launch_input(const InputArgs& a, hipStream_t s);
 void launch_deliver(const DeliverArgs& a, hipStream_t s);

@@ -894,6 +894,10 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
         const int inst = packed & 0x3fffffff;
         if (type == 0) {                        // ExpSyn: g += w (expsyn.cpp net_receive)
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
+            if (D.log) {
+                const int pos = atomicAdd(D.log_count, 1);
+                if (pos < D.ring.cap) D.log[pos] = inst;
+            }
         } else {                                // Exp2Syn: A,B += w * factor
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
             atomicAdd(&D.e2.col(E2_A)[inst], wf);

@@ -29,14 +29,45 @@ __device__ __forceinline__ double nernst(double ci, double co, double z, double 
 }
 
 // ---------------- hh ----------------
-__device__ __forceinline__ double hh_vtrap(double x, double y) {
-    if (fabs(x / y) < 1e-6) return y * (1 - x / y / 2);
+// The rate functions are templates so that the adjoint can evaluate them on
+// dual numbers (value + derivative) and get d/dv of exactly these formulas.
+struct Dual {
+    double v, d;
+};
+__host__ __device__ __forceinline__ Dual operator+(Dual a, Dual b) { return {a.v + b.v, a.d + b.d}; }
+__host__ __device__ __forceinline__ Dual operator-(Dual a, Dual b) { return {a.v - b.v, a.d - b.d}; }
+__host__ __device__ __forceinline__ Dual operator-(Dual a) { return {-a.v, -a.d}; }
+__host__ __device__ __forceinline__ Dual operator*(Dual a, Dual b) { return {a.v * b.v, a.d * b.v + a.v * b.d}; }
+__host__ __device__ __forceinline__ Dual operator/(Dual a, Dual b) {
+    return {a.v / b.v, (a.d * b.v - a.v * b.d) / (b.v * b.v)};
+}
+__host__ __device__ __forceinline__ Dual operator+(Dual a, double b) { return {a.v + b, a.d}; }
+__host__ __device__ __forceinline__ Dual operator+(double a, Dual b) { return {a + b.v, b.d}; }
+__host__ __device__ __forceinline__ Dual operator-(Dual a, double b) { return {a.v - b, a.d}; }
+__host__ __device__ __forceinline__ Dual operator-(double a, Dual b) { return {a - b.v, -b.d}; }
+__host__ __device__ __forceinline__ Dual operator*(Dual a, double b) { return {a.v * b, a.d * b}; }
+__host__ __device__ __forceinline__ Dual operator*(double a, Dual b) { return {a * b.v, a * b.d}; }
+__host__ __device__ __forceinline__ Dual operator/(Dual a, double b) { return {a.v / b, a.d / b}; }
+__host__ __device__ __forceinline__ Dual operator/(double a, Dual b) { return {a / b.v, -a * b.d / (b.v * b.v)}; }
+__device__ __forceinline__ Dual exp(Dual a) {
+    const double e = ::exp(a.v);
+    return {e, e * a.d};
+}
+// keeps the library exp visible next to the Dual overload inside this namespace
+__device__ __forceinline__ double exp(double a) { return ::exp(a); }
+__host__ __device__ __forceinline__ double value_of(double a) { return a; }
+__host__ __device__ __forceinline__ double value_of(Dual a) { return a.v; }
+
+template <class T>
+__device__ __forceinline__ T hh_vtrap(T x, double y) {
+    if (fabs(value_of(x) / y) < 1e-6) return y * (1 - x / y / 2);
     else return x / (exp(x / y) - 1);
 }
 
-__device__ __forceinline__ void hh_rates(double volt, double q10, double& minf, double& mtau, double& hinf,
-                                         double& htau, double& ninf, double& ntau) {
-    double alpha, beta, sum;
+template <class T>
+__device__ __forceinline__ void hh_rates(T volt, double q10, T& minf, T& mtau, T& hinf, T& htau, T& ninf,
+                                         T& ntau) {
+    T alpha, beta, sum;
     alpha = 0.1 * hh_vtrap(-(volt + 40), 10);
     beta = 4 * exp(-(volt + 65) / 18);
     sum = alpha + beta;
@@ -54,7 +85,8 @@ __device__ __forceinline__ void hh_rates(double volt, double q10, double& minf, 
     ninf = alpha / sum;
 }
 
-__device__ __forceinline__ double hh_cnexp(double x, double xinf, double xtau, double dt) {
+template <class T>
+__device__ __forceinline__ T hh_cnexp(double x, T xinf, T xtau, double dt) {
     return x + (1.0 - exp(dt * (-1.0 / xtau))) * ((xinf / xtau) / (1.0 / xtau) - x);
 }
 

@@ -267,12 +267,48 @@ struct hx_sim {
     bool state_pending = false;
     bool final_step = false;   // the last step of a run call also stores every assigned variable
     bool initialized = false;
+    // adjoint tape (hx_tape_begin): row n holds v^{n+1} (after step n's solve), the
+    // hh gates x^n and ExpSyn g_eff^n that step n used, and the ExpSyn instances
+    // that received events at step n
+    bool tape_on = false;
+    int tape_cap = 0, tape_n = 0, tape_evcap = 0;
+    double *d_tape_v = nullptr, *d_tape_x = nullptr, *d_tape_g = nullptr;
+    int *d_tape_evn = nullptr, *d_tape_ev = nullptr;
+    // adjoint work arrays and per-instance gradients (hx_adjoint)
+    double *d_adj_delta = nullptr, *d_lv = nullptr, *d_lv2 = nullptr, *d_lx = nullptr, *d_lg = nullptr,
+           *d_dT = nullptr, *d_rhsT = nullptr, *d_vT = nullptr, *d_wT = nullptr;
+    double *d_grad_gnabar = nullptr, *d_grad_gkbar = nullptr, *d_grad_gpas = nullptr, *d_grad_w = nullptr;
+    bool have_grad = false;
+    struct AdamHost {
+        double beta1 = 0.9, beta2 = 0.999, eps = 1e-8;
+        long long step = 0;
+        std::vector<int> begin{0};
+        std::vector<double*> w, g;
+        std::vector<double> imp, m, v;
+        bool dirty = true;
+        int* d_begin = nullptr;
+        double** d_w = nullptr;
+        double** d_g = nullptr;
+        double *d_imp = nullptr, *d_m = nullptr, *d_v = nullptr;
+    };
+    std::vector<AdamHost> adams;
+    void tape_free() {
+        for (void* p : {static_cast<void*>(d_tape_v), static_cast<void*>(d_tape_x), static_cast<void*>(d_tape_g),
+                        static_cast<void*>(d_tape_evn), static_cast<void*>(d_tape_ev)})
+            if (p) (void)hipFree(p);
+        d_tape_v = d_tape_x = d_tape_g = nullptr;
+        d_tape_evn = d_tape_ev = nullptr;
+        tape_cap = 0;
+    }
+    void tape_record();
+    double grad_sq(int which);
     // profiling
     bool profiling = false;
     unsigned prof_mask = ~0u;   // timed kernel classes (bit = TimerId)
     Timer timers[T_COUNT];
 
     ~hx_sim() {
+        tape_free();
         for (auto& tm : timers)
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
@@ -891,6 +927,10 @@ void hx_sim::launch_events(int kk, double tk) {
     D.e2 = mech[M_EXP2SYN].dev;
     D.es_weight = d_es_weight;
     D.e2_weight = d_e2_weight;
+    if (tape_on && tape_n < tape_cap) {
+        D.log_count = d_tape_evn + tape_n;
+        D.log = d_tape_ev + static_cast<size_t>(tape_n) * tape_evcap;
+    }
     launch_deliver(D, stream);
     tend(T_EVENTS);
 }
@@ -931,6 +971,25 @@ void hx_sim::launch_record() {
 
 // One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
 // have been detected (end of the previous step or finitialize).
+void hx_sim::tape_record() {
+    if (tape_n >= tape_cap)
+        throw std::runtime_error("adjoint tape full (" + std::to_string(tape_cap) + " steps): call hx_tape_begin "
+                                 "with more steps");
+    const size_t n = static_cast<size_t>(tape_n);
+    HXC(hipMemcpyAsync(d_tape_v + n * nnode, d_v, sizeof(double) * nnode, hipMemcpyDeviceToDevice, stream));
+    if (mech[M_HH].present && mech[M_HH].n > 0) {
+        const MechDev& h = mech[M_HH].dev;   // columns m, h, n are consecutive
+        HXC(hipMemcpyAsync(d_tape_x + n * 3 * h.stride, h.col(HH_M), sizeof(double) * 3 * h.stride,
+                           hipMemcpyDeviceToDevice, stream));
+    }
+    if (mech[M_EXPSYN].present && mech[M_EXPSYN].n > 0) {
+        const MechDev& e = mech[M_EXPSYN].dev;
+        HXC(hipMemcpyAsync(d_tape_g + n * e.n, e.col(ES_G), sizeof(double) * e.n, hipMemcpyDeviceToDevice,
+                           stream));
+    }
+    ++tape_n;
+}
+
 void hx_sim::step_once() {
     const double tk = t;
     const double tmid = tk + 0.5 * dt;
@@ -967,6 +1026,7 @@ void hx_sim::step_once() {
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
+    if (tape_on) tape_record();
     if (!gaps.empty()) {
         tbegin(T_OTHER);
         launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
@@ -1084,6 +1144,10 @@ void hx_sim::finitialize(double v_init) {
     launch_clear_ints(d_pre_flag, npre, stream);
     launch_clear_ints(d_spk_count, 1, stream);
     launch_clear_ints(d_in_cursor, 1, stream);
+    if (tape_on) {
+        tape_n = 0;
+        launch_clear_ints(d_tape_evn, tape_cap, stream);
+    }
     launch_set_v(d_v, nnode, v_init, stream);
     if (!gaps.empty())
         launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
@@ -1762,6 +1826,290 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "event_slots") return sim->ring.nslot;
     if (k == "event_cap") return sim->ring.cap;
     return -1;
+}
+
+// ---------------------------------------------------------------------------
+// adjoint (no reference counterpart) and Adam
+// ---------------------------------------------------------------------------
+int hx_tape_begin(hx_sim* sim, int max_steps) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    sim->tape_on = false;
+    sim->tape_n = 0;
+    if (max_steps <= 0) {
+        sim->tape_free();
+        return 0;
+    }
+    const auto& R = registry();
+    for (int id = 0; id < M_COUNT; ++id) {
+        if (!sim->mech[id].present) continue;
+        if (id != M_PAS && id != M_NA_ION && id != M_K_ION && id != M_HH && id != M_ICLAMP && id != M_EXPSYN &&
+            id != M_VECSTIM)
+            return sim->fail("the adjoint supports pas, hh, ExpSyn, IClamp, VecStim and the na/k ions; "
+                             "the model has %s", R[id].name);
+    }
+    for (int x : {M_NA_ION, M_K_ION})
+        if (sim->mech[x].present)
+            for (int t : sim->mech[x].iontype)
+                if (t & 0100) return sim->fail("the adjoint needs fixed reversal potentials (%s iontype 0100)",
+                                               R[x].name);
+    if (!sim->vecplay.empty()) return sim->fail("the adjoint does not support VecPlay");
+    sim->tape_free();
+    const size_t cap = static_cast<size_t>(max_steps);
+    HXC(hipMalloc(&sim->d_tape_v, sizeof(double) * cap * sim->nnode));
+    if (sim->mech[M_HH].present && sim->mech[M_HH].n > 0)
+        HXC(hipMalloc(&sim->d_tape_x, sizeof(double) * cap * 3 * sim->mech[M_HH].dev.stride));
+    if (sim->mech[M_EXPSYN].present && sim->mech[M_EXPSYN].n > 0)
+        HXC(hipMalloc(&sim->d_tape_g, sizeof(double) * cap * sim->mech[M_EXPSYN].n));
+    sim->tape_evcap = std::max(sim->ring.cap, 1);
+    HXC(hipMalloc(&sim->d_tape_evn, sizeof(int) * cap));
+    HXC(hipMalloc(&sim->d_tape_ev, sizeof(int) * cap * sim->tape_evcap));
+    HXC(hipMemsetAsync(sim->d_tape_evn, 0, sizeof(int) * cap, sim->stream));
+    sim->tape_cap = max_steps;
+    sim->tape_on = true;
+    return 0;
+    API_END
+}
+
+int hx_tape_length(hx_sim* sim) { return sim->tape_on ? sim->tape_n : 0; }
+
+int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* target, int nsample, double* loss) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (!sim->tape_on || sim->tape_n == 0) return sim->fail("no taped steps (hx_tape_begin, finitialize, run)");
+    if (nsample != sim->tape_n)
+        return sim->fail("target has %d samples, the tape holds %d steps", nsample, sim->tape_n);
+    if (nloss <= 0) return sim->fail("no loss nodes");
+    const int N = sim->nnode;
+    std::vector<int> ln(nloss);
+    for (int j = 0; j < nloss; ++j) {
+        if (loss_nodes[j] < 0 || loss_nodes[j] >= N) return sim->fail("loss node %d out of range", loss_nodes[j]);
+        ln[j] = sim->node_perm[loss_nodes[j]];
+    }
+    hipStream_t st = sim->stream;
+    auto& owned = sim->owned;
+    int* d_ln = dupload(owned, ln);
+    std::vector<double> tgt(target, target + static_cast<size_t>(nsample) * nloss);
+    double* d_tgt = dupload(owned, tgt);
+    // loss: mean over samples 1..nsample and loss nodes of (v - target)^2
+    double* d_samp = dalloc<double>(owned, static_cast<size_t>(nsample) * nloss);
+    launch_adj_gather(sim->d_tape_v, N, d_ln, nloss, nsample, d_samp, st);
+    std::vector<double> samp(static_cast<size_t>(nsample) * nloss);
+    HXC(hipMemcpyAsync(samp.data(), d_samp, sizeof(double) * samp.size(), hipMemcpyDeviceToHost, st));
+    HXC(hipStreamSynchronize(st));
+    const double scale = 1.0 / (static_cast<double>(nsample) * nloss);
+    double L = 0.0;
+    for (size_t k = 0; k < samp.size(); ++k) L += (samp[k] - tgt[k]) * (samp[k] - tgt[k]);
+    if (loss) *loss = L * scale;
+    // diagonal correction of the transposed solve: the tree kernel assembles
+    // d - b_i - sum_c a_c from the (swapped) coefficients, M^T needs the original
+    if (!sim->d_adj_delta) {
+        std::vector<double> delta(N, 0.0);
+        for (int i = sim->ncell; i < N; ++i) {
+            delta[i] += sim->a[i] - sim->b[i];
+            delta[sim->parent[i]] += sim->b[i] - sim->a[i];
+        }
+        std::vector<double> g(N);
+        for (int i = 0; i < N; ++i) g[sim->node_perm[i]] = delta[i];
+        sim->d_adj_delta = dupload(owned, g);
+        for (double** p : {&sim->d_lv, &sim->d_lv2, &sim->d_dT, &sim->d_rhsT, &sim->d_vT, &sim->d_wT})
+            *p = dalloc<double>(owned, N);
+        const HostMech& hh = sim->mech[M_HH];
+        const HostMech& es = sim->mech[M_EXPSYN];
+        const HostMech& pas = sim->mech[M_PAS];
+        sim->d_lx = dalloc<double>(owned, std::max<long long>(1, 3 * (hh.present ? hh.dev.stride : 0)));
+        sim->d_lg = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+        sim->d_grad_gnabar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
+        sim->d_grad_gkbar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
+        sim->d_grad_gpas = dalloc<double>(owned, std::max(1, pas.present ? pas.n : 0));
+        sim->d_grad_w = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+    }
+    const HostMech& hh = sim->mech[M_HH];
+    const HostMech& es = sim->mech[M_EXPSYN];
+    const HostMech& pas = sim->mech[M_PAS];
+    const long long xs = hh.present ? hh.dev.stride : 0;
+    HXC(hipMemsetAsync(sim->d_lv, 0, sizeof(double) * N, st));
+    HXC(hipMemsetAsync(sim->d_lx, 0, sizeof(double) * std::max<long long>(1, 3 * xs), st));
+    HXC(hipMemsetAsync(sim->d_lg, 0, sizeof(double) * std::max(1, es.present ? es.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_grad_gnabar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_grad_gkbar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_grad_gpas, 0, sizeof(double) * std::max(1, pas.present ? pas.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_grad_w, 0, sizeof(double) * std::max(1, es.present ? es.n : 0), st));
+    const StepArgs SA = sim->step_args(sim->t, 0, 0);
+    AdjStep A{};
+    A.N = N;
+    A.dt = sim->dt;
+    A.cfac = SA.cfac;
+    A.hh_q10 = SA.c.hh_q10;
+    A.cm = sim->d_cm;
+    A.area = sim->d_area;
+    A.delta = sim->d_adj_delta;
+    for (int id = 0; id < M_COUNT; ++id) A.m[id] = SA.m[id];
+    A.xstride = xs;
+    A.lam_x = sim->d_lx;
+    A.lam_g = sim->d_lg;
+    A.dT = sim->d_dT;
+    A.rhsT = sim->d_rhsT;
+    A.vT = sim->d_vT;
+    A.mu = sim->d_rhsT;
+    A.grad_gnabar = sim->d_grad_gnabar;
+    A.grad_gkbar = sim->d_grad_gkbar;
+    A.grad_gpas = sim->d_grad_gpas;
+    A.grad_w = sim->d_grad_w;
+    SolveArgs S{};
+    S.ncell = sim->ncell;
+    S.cell_node_begin = sim->d_cell_node_begin;
+    S.cell_desc_begin = sim->d_cell_desc_begin;
+    S.cell_round_begin = sim->d_cell_round_begin;
+    S.rounds = sim->d_rounds;
+    S.desc = sim->d_desc;
+    S.v = sim->d_vT;
+    S.d = sim->d_dT;
+    S.rhs = sim->d_rhsT;
+    S.w = sim->d_wT;
+    S.a = sim->d_b;       // M^T: the coefficients trade places
+    S.b = sim->d_a;
+    double* lv = sim->d_lv;
+    double* lv2 = sim->d_lv2;
+    const size_t row = static_cast<size_t>(N);
+    launch_adj_loss(sim->d_tape_v + (nsample - 1) * row, d_ln, d_tgt + static_cast<size_t>(nsample - 1) * nloss,
+                    nloss, scale, lv, st);
+    for (int n = nsample - 1; n >= 0; --n) {
+        A.v1 = sim->d_tape_v + n * row;
+        A.x0 = sim->d_tape_x ? sim->d_tape_x + static_cast<size_t>(n) * 3 * xs : nullptr;
+        A.geff = sim->d_tape_g ? sim->d_tape_g + static_cast<size_t>(n) * es.n : nullptr;
+        A.ev_count = sim->d_tape_evn + n;
+        A.ev = sim->d_tape_ev + static_cast<size_t>(n) * sim->tape_evcap;
+        A.lam_v = lv;
+        A.lam_v_new = lv2;
+        launch_adj_before_solve(A, st);
+        launch_solve(S, sim->max_slots, st);
+        launch_adj_after_solve(A, st);
+        if (n >= 1)
+            launch_adj_loss(sim->d_tape_v + (n - 1) * row, d_ln, d_tgt + static_cast<size_t>(n - 1) * nloss, nloss,
+                            scale, lv2, st);
+        std::swap(lv, lv2);
+    }
+    HXC(hipStreamSynchronize(st));
+    sim->have_grad = true;
+    return 0;
+    API_END
+}
+
+int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out, int cap) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (!sim->have_grad) return sim->fail("no gradients (call hx_adjoint)");
+    const std::string mn = mech ? mech : "", vn = var ? var : "";
+    double* src = nullptr;
+    int id = -1;
+    if (mn == "hh" && vn == "gnabar") { src = sim->d_grad_gnabar; id = M_HH; }
+    else if (mn == "hh" && vn == "gkbar") { src = sim->d_grad_gkbar; id = M_HH; }
+    else if (mn == "pas" && vn == "g_pas") { src = sim->d_grad_gpas; id = M_PAS; }
+    else if (mn == "ExpSyn" && vn == "weight") { src = sim->d_grad_w; id = M_EXPSYN; }
+    if (!src || !sim->mech[id].present) return sim->fail("no gradient for %s.%s", mn.c_str(), vn.c_str());
+    const HostMech& m = sim->mech[id];
+    if (cap < m.n) return sim->fail("output too small");
+    std::vector<double> g(m.n);
+    HXC(hipMemcpy(g.data(), src, sizeof(double) * m.n, hipMemcpyDeviceToHost));
+    for (int j = 0; j < m.n; ++j) out[m.iperm[j]] = g[j];
+    return m.n;
+    API_END
+}
+
+int hx_adam_create(hx_sim* sim, double beta1, double beta2, double eps) {
+    if (!check_loaded(sim)) return -1;
+    hx_sim::AdamHost o;
+    o.beta1 = beta1;
+    o.beta2 = beta2;
+    o.eps = eps;
+    sim->adams.push_back(o);
+    return static_cast<int>(sim->adams.size()) - 1;
+}
+
+int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, int n, const int* inst,
+                      double impedance) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
+    if (n <= 0) return sim->fail("empty parameter group");
+    const std::string mn = mech ? mech : "", vn = var ? var : "";
+    double* grad = nullptr;
+    int id = -1;
+    if (mn == "hh" && vn == "gnabar") { grad = sim->d_grad_gnabar; id = M_HH; }
+    else if (mn == "hh" && vn == "gkbar") { grad = sim->d_grad_gkbar; id = M_HH; }
+    else if (mn == "pas" && vn == "g_pas") { grad = sim->d_grad_gpas; id = M_PAS; }
+    else if (mn == "ExpSyn" && vn == "weight") { grad = sim->d_grad_w; id = M_EXPSYN; }
+    if (id < 0 || !sim->mech[id].present) return sim->fail("no trainable parameter %s.%s", mn.c_str(), vn.c_str());
+    if (!grad) return sim->fail("gradients are allocated by the first hx_adjoint call");
+    auto& o = sim->adams[opt];
+    const HostMech& m = sim->mech[id];
+    for (int k = 0; k < n; ++k) {
+        if (inst[k] < 0 || inst[k] >= m.n) return sim->fail("instance %d out of range", inst[k]);
+        const int dj = m.perm[inst[k]];
+        double* w = id == M_EXPSYN ? sim->d_es_weight + dj : sim->resolve(mn, vn, inst[k]).dev;
+        o.w.push_back(w);
+        o.g.push_back(grad + dj);
+    }
+    o.begin.push_back(static_cast<int>(o.w.size()));
+    o.imp.push_back(impedance);
+    o.m.push_back(0.0);
+    o.v.push_back(0.0);
+    o.dirty = true;
+    return static_cast<int>(o.imp.size()) - 1;
+    API_END
+}
+
+int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
+    auto& o = sim->adams[opt];
+    auto& owned = sim->owned;
+    const int ng = static_cast<int>(o.imp.size());
+    if (o.dirty) {   // (re)upload the groups; the host copies of m and v are current
+        o.d_begin = dupload(owned, o.begin);
+        o.d_w = dupload(owned, o.w);
+        o.d_g = dupload(owned, o.g);
+        o.d_imp = dupload(owned, o.imp);
+        o.d_m = dupload(owned, o.m);
+        o.d_v = dupload(owned, o.v);
+        o.dirty = false;
+    }
+    ++o.step;
+    AdamArgs A{};
+    A.ngroup = ng;
+    A.begin = o.d_begin;
+    A.w = o.d_w;
+    A.grad = o.d_g;
+    A.impedance = o.d_imp;
+    A.m = o.d_m;
+    A.v = o.d_v;
+    A.lr = lr;
+    A.inv_record_steps = inv_record_steps;
+    A.beta1 = o.beta1;
+    A.beta2 = o.beta2;
+    A.eps = o.eps;
+    A.step = o.step;
+    launch_adam(A, sim->stream);
+    HXC(hipMemcpyAsync(o.m.data(), o.d_m, sizeof(double) * ng, hipMemcpyDeviceToHost, sim->stream));
+    HXC(hipMemcpyAsync(o.v.data(), o.d_v, sizeof(double) * ng, hipMemcpyDeviceToHost, sim->stream));
+    HXC(hipStreamSynchronize(sim->stream));
+    return 0;
+    API_END
+}
+
+int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
+    const auto& o = sim->adams[opt];
+    const int ng = static_cast<int>(o.imp.size());
+    if (step) *step = o.step;
+    if (cap < ng) return sim->fail("output too small");
+    for (int g = 0; g < ng; ++g) {
+        if (m) m[g] = o.m[g];
+        if (v) v[g] = o.v[g];
+    }
+    return ng;
 }
 
 }  // extern "C"

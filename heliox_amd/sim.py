@@ -84,6 +84,14 @@ SIGNATURES = {
     "hx_set_fusion": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling_classes": (C.c_int, [_P, _S]),
+    "hx_tape_begin": (C.c_int, [_P, C.c_int]),
+    "hx_tape_length": (C.c_int, [_P]),
+    "hx_adjoint": (C.c_int, [_P, C.c_int, _I, _D, C.c_int, _D]),
+    "hx_get_gradient": (C.c_int, [_P, _S, _S, _D, C.c_int]),
+    "hx_adam_create": (C.c_int, [_P, C.c_double, C.c_double, C.c_double]),
+    "hx_adam_add_group": (C.c_int, [_P, C.c_int, _S, _S, C.c_int, _I, C.c_double]),
+    "hx_adam_step": (C.c_int, [_P, C.c_int, C.c_double, C.c_double]),
+    "hx_adam_get_state": (C.c_int, [_P, C.c_int, C.POINTER(C.c_longlong), _D, _D, C.c_int]),
     "hx_get_kernel_time": (C.c_int, [_P, _S, _D, C.POINTER(C.c_longlong)]),
     "hx_get_info": (C.c_longlong, [_P, _S]),
     "hx_emulate_tree_solve": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, _I, _I]),
@@ -186,6 +194,7 @@ class Sim:
         L = lib()
         h = self._h
         self._keep = []
+        self._spec = spec
         self._chk(L.hx_set_dt(h, spec.dt), "set_dt")
         self._chk(L.hx_set_celsius(h, spec.celsius), "set_celsius")
         parent = np.ascontiguousarray(spec.parent, np.int32)
@@ -362,6 +371,56 @@ class Sim:
         if enable and classes is not None:
             return self._rc(lib().hx_set_profiling_classes(self._h, _b(",".join(classes))))
         return self._rc(lib().hx_set_profiling(self._h, 1 if enable else 0))
+
+    # ---- adjoint and Adam ----
+    def tape_begin(self, max_steps: int) -> int:
+        """Record the next run for the adjoint (call before finitialize)."""
+        return self._chk(lib().hx_tape_begin(self._h, int(max_steps)), "tape_begin")
+
+    def tape_length(self) -> int:
+        return lib().hx_tape_length(self._h)
+
+    def adjoint(self, loss_nodes, target) -> float:
+        """Backward sweep for loss = mean((v[loss_nodes] after each taped step - target)^2);
+        target has shape (tape_length, len(loss_nodes)).  Returns the loss."""
+        nodes = np.ascontiguousarray(loss_nodes, np.int32)
+        tgt = np.ascontiguousarray(target, np.float64)
+        if tgt.ndim != 2 or tgt.shape[1] != nodes.size:
+            raise ValueError("target must have shape (steps, len(loss_nodes))")
+        out = C.c_double()
+        self._chk(lib().hx_adjoint(self._h, int(nodes.size), _ip(nodes), _dp(tgt), int(tgt.shape[0]),
+                                   C.byref(out)), "adjoint")
+        return out.value
+
+    def gradient(self, mech: str, var: str) -> np.ndarray:
+        n = self._spec_count(mech)
+        out = np.zeros(max(n, 1))
+        k = self._chk(lib().hx_get_gradient(self._h, _b(mech), _b(var), _dp(out), out.size), "get_gradient")
+        return out[:k]
+
+    def _spec_count(self, mech: str) -> int:
+        spec = getattr(self, "_spec", None)
+        if spec is not None and mech in spec.mechs:
+            return spec.mechs[mech].nodes.size
+        return 1 << 22
+
+    def adam_create(self, beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8) -> int:
+        return self._chk(lib().hx_adam_create(self._h, beta1, beta2, eps), "adam_create")
+
+    def adam_add_group(self, opt: int, mech: str, var: str, instances, impedance: float = 1.0) -> int:
+        inst = np.ascontiguousarray(instances, np.int32)
+        return self._chk(lib().hx_adam_add_group(self._h, opt, _b(mech), _b(var), int(inst.size), _ip(inst),
+                                                 impedance), "adam_add_group")
+
+    def adam_step(self, opt: int, lr: float, inv_record_steps: float = 1.0) -> int:
+        return self._chk(lib().hx_adam_step(self._h, opt, lr, inv_record_steps), "adam_step")
+
+    def adam_state(self, opt: int, ngroup: int):
+        step = C.c_longlong()
+        m = np.zeros(max(ngroup, 1))
+        v = np.zeros(max(ngroup, 1))
+        self._chk(lib().hx_adam_get_state(self._h, opt, C.byref(step), _dp(m), _dp(v), m.size), "adam_state")
+        return step.value, m[:ngroup], v[:ngroup]
 
     def kernel_time(self, kernel: str):
         ms = C.c_double()

@@ -447,3 +447,23 @@ def _set_trains(spec: ModelSpec, trains: List[np.ndarray]) -> None:
     off[1:] = np.cumsum(counts)
     spec.vecstim_offsets = off
     spec.vecstim_times = np.concatenate(trains) if trains else np.zeros(0)
+
+
+def perturb_config5(spec: ModelSpec, seed: int = 1) -> ModelSpec:
+    """The config-5 target model: per cell, gnabar, gkbar and g_pas (each tied
+    over the cell's instances) and each of the cell's ExpSyn netcon weights are
+    scaled by U(0.8, 1.2).  Returns a new spec; ``spec`` is unchanged."""
+    import copy
+    out = copy.deepcopy(spec)
+    cell = spec.cell_of_node()
+    rng = cell_rng(5, 0x7A1F00 + seed)
+    f = rng.uniform(0.8, 1.2, (spec.ncell, 3))
+    hh = out.mechs["hh"]
+    hc = cell[hh.nodes]
+    hh.params["gnabar"] = hh.params["gnabar"] * f[hc, 0]
+    hh.params["gkbar"] = hh.params["gkbar"] * f[hc, 1]
+    pas = out.mechs["pas"]
+    pas.params["g_pas"] = pas.params["g_pas"] * f[cell[pas.nodes], 2]
+    nc = out.netcons["ExpSyn"]
+    nc.weight = nc.weight * rng.uniform(0.8, 1.2, nc.weight.size)
+    return out

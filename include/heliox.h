@@ -128,6 +128,38 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused". */
 long long hx_get_info(hx_sim* sim, const char* key);
 
+/* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the
+ *      parameter gradients that the reference's learn surface feeds its optimizer
+ *      (LearnRuntime::replay_compute_dw_from_cached_signals_into,
+ *      LearnRuntime.cpp:2298-2457), here as the exact gradient of a voltage loss
+ *      through the fixed-step simulation.  Models: pas, hh, ExpSyn (VecStim or
+ *      detector sources), IClamp, na/k ions with fixed reversal potentials. ---- */
+/* Record the next run into HBM, up to max_steps steps (0 stops and frees the tape).
+ * Call before hx_finitialize: deliveries at finitialize belong to step 0. */
+int hx_tape_begin(hx_sim* sim, int max_steps);
+/* Steps on the tape. */
+int hx_tape_length(hx_sim* sim);
+/* Loss = mean over samples s = 1..nsample (v after step s) and the nloss nodes of
+ * (v - target[(s-1)*nloss + j])^2; nsample must equal the tape length.  Runs the
+ * backward sweep and leaves per-instance gradients for hx_get_gradient. */
+int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* target, int nsample, double* loss);
+/* dLoss/dparam per instance (user order): ("hh","gnabar"), ("hh","gkbar"),
+ * ("pas","g_pas"), ("ExpSyn","weight") (the weight of the netcon into that instance). */
+int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out, int cap);
+
+/* ---- Adam over tied parameter groups (AdamOptimizer::step_gpu, optimizer.cpp:351-457;
+ *      SimWrapper::create_optimizer / configure_optimizer / optimizer_add_param_batch /
+ *      optimizer_step_with_inv_record_steps, SimWrapper.cpp:159-283).  Gradients are
+ *      the ones hx_adjoint left; a step zeroes them. ---- */
+int hx_adam_create(hx_sim* sim, double beta1, double beta2, double eps);
+/* One tied group: instances inst[0..n) of (mech, var) share one moment pair; the step
+ * uses the mean of their gradients x impedance x inv_record_steps and writes the same
+ * new value to all of them.  Returns the group index. */
+int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, int n, const int* inst,
+                      double impedance);
+int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps);
+int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap);
+
 /* Host emulation of the device tree solve (no counterpart in the reference;
  * a diagnostic for CPU-only checks of the solver schedule): capacitance and
  * axial assembly, elimination and back substitution over the same chunk

@@ -1,0 +1,138 @@
+"""Adjoint (VJP) gradients of the config-5 loss on the GPU against central finite
+differences of the same loss computed with the CPU oracle, and the device Adam
+step against the Kingma-Ba update.
+
+The loss is the mean over steps 1..N and cells of (soma v - target)^2, the
+target coming from the config-5 model with perturbed parameters.  Tolerance:
+1e-6 relative on every checked gradient."""
+import copy
+
+import numpy as np
+import pytest
+
+import oracle
+from heliox_amd import Sim, build_config
+from heliox_amd.synth import perturb_config5
+
+pytestmark = pytest.mark.gpu
+
+NCELL = 2
+TSTOP = 40.0
+REL_TOL = 1e-6
+
+
+def soma_trace(spec, tstop):
+    mons = [("global", "v", i) for i in range(spec.ncell)]
+    o = oracle.OracleSim(spec, monitors=mons)
+    o.finitialize(-65.0)
+    o.run(tstop)
+    return o.traces()[:, 1:].T          # samples after steps 1..N, shape (N, ncell)
+
+
+def loss_of(spec, target, tstop):
+    v = soma_trace(spec, tstop)
+    return float(np.mean((v - target) ** 2))
+
+
+@pytest.fixture(scope="module")
+def problem():
+    base = build_config(5, NCELL, TSTOP)
+    target = soma_trace(perturb_config5(base, seed=3), TSTOP)
+    nstep = target.shape[0]
+    g = Sim()
+    g.load_model_from_spec(base, add_monitors=False)
+    g.tape_begin(nstep)
+    g.finitialize(-65.0)
+    g.run(TSTOP)
+    assert g.tape_length() == nstep
+    loss = g.adjoint(np.arange(base.ncell), target)
+    grads = {k: g.gradient(*k) for k in [("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas"), ("ExpSyn", "weight")]}
+    return base, target, loss, grads, g
+
+
+def scaled(spec, mech, var, mask, factor):
+    s = copy.deepcopy(spec)
+    if mech == "ExpSyn":
+        s.netcons["ExpSyn"].weight = np.where(mask, s.netcons["ExpSyn"].weight * factor,
+                                              s.netcons["ExpSyn"].weight)
+    else:
+        p = s.mechs[mech].params
+        p[var] = np.where(mask, p[var] * factor, p[var])
+    return s
+
+
+def fd_relative(spec, target, mech, var, mask, h=1e-4):
+    """d loss / d alpha for param *= (1 + alpha) on the masked instances."""
+    lp = loss_of(scaled(spec, mech, var, mask, 1.0 + h), target, TSTOP)
+    lm = loss_of(scaled(spec, mech, var, mask, 1.0 - h), target, TSTOP)
+    return (lp - lm) / (2.0 * h)
+
+
+def test_loss_matches_oracle(problem):
+    base, target, loss, _, _ = problem
+    ref = loss_of(base, target, TSTOP)
+    assert abs(loss - ref) <= 1e-9 * abs(ref)
+
+
+@pytest.mark.parametrize("mech,var", [("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas")])
+def test_tied_conductance_gradients_match_fd(problem, mech, var):
+    base, target, _, grads, _ = problem
+    cell = base.cell_of_node()
+    ms = base.mechs[mech]
+    vals = ms.params[var]
+    for c in range(base.ncell):
+        mask = cell[ms.nodes] == c
+        adj = float(np.sum(vals[mask] * grads[(mech, var)][mask]))   # d/d alpha of the tied scale
+        fd = fd_relative(base, target, mech, var, mask)
+        print(f"  {mech}.{var} cell {c}: adjoint {adj:.12e} fd {fd:.12e}", flush=True)
+        assert abs(adj - fd) <= REL_TOL * abs(fd), (adj, fd)
+
+
+def test_synaptic_weight_gradients_match_fd(problem):
+    base, target, _, grads, _ = problem
+    nc = base.netcons["ExpSyn"]
+    gw = grads[("ExpSyn", "weight")]
+    checked = 0
+    infl = np.abs(gw[nc.inst] * nc.weight)
+    assert np.count_nonzero(infl) >= 4, "too few synapses received events in the window"
+    for k in np.argsort(-infl)[:4]:   # the four most influential weights
+        mask = np.arange(nc.weight.size) == k
+        adj = float(nc.weight[k] * gw[nc.inst[k]])
+        fd = fd_relative(base, target, "ExpSyn", "weight", mask)
+        print(f"  weight {k}: adjoint {adj:.12e} fd {fd:.12e}", flush=True)
+        assert fd != 0.0 and abs(adj - fd) <= REL_TOL * abs(fd), (k, adj, fd)
+        checked += 1
+    assert checked == 4
+    # a synapse that received no event in the window has no gradient
+    quiet = np.nonzero(infl == 0)[0]
+    if quiet.size:
+        k = quiet[0]
+        assert fd_relative(base, target, "ExpSyn", "weight", np.arange(nc.weight.size) == k) == 0.0
+
+
+def test_adam_step_on_tied_groups(problem):
+    base, _, _, grads, g = problem
+    cell = base.cell_of_node()
+    hh = base.mechs["hh"]
+    opt = g.adam_create(0.9, 0.999, 1e-8)
+    groups = [np.nonzero(cell[hh.nodes] == c)[0] for c in range(base.ncell)]
+    for inst in groups:
+        g.adam_add_group(opt, "hh", "gnabar", inst, impedance=1.0)
+    w0 = g.get_array("hh", "gnabar").copy()
+    lr, inv = 1e-3, 0.5
+    g.adam_step(opt, lr, inv)
+    w1 = g.get_array("hh", "gnabar")
+    # the same update from the oracle's restatement of AdamOptimizer::step_cpu
+    ww = np.array([w0[i[0]] for i in groups])
+    gsz = np.array([i.size for i in groups], np.int32)
+    m = np.zeros(len(groups))
+    v = np.zeros(len(groups))
+    oracle.adam_step(ww, np.concatenate([grads[("hh", "gnabar")][i] for i in groups]), gsz, m, v, 1, lr, inv)
+    for k, inst in enumerate(groups):
+        assert np.allclose(w1[inst], ww[k], rtol=1e-14, atol=0)
+    step, mg, vg = g.adam_state(opt, len(groups))
+    assert step == 1 and np.allclose(mg, m, rtol=1e-14) and np.allclose(vg, v, rtol=1e-14)
+    # a step zeroes the gradients it used: a second step only decays the moments
+    g.adam_step(opt, lr, inv)
+    _, mg2, _ = g.adam_state(opt, len(groups))
+    assert np.allclose(mg2, 0.9 * mg, rtol=1e-14)
