@@ -69,6 +69,63 @@ def cpu_baseline(ncell: int, nstep: int):
                       f"({spec.nnode * nstep:.3g} compartment-steps, {el:.1f} s on one core)"}
 
 
+def train_bench(args):
+    """Config 5: one differentiable training step = taped forward run (1000 cells x 500
+    compartments, 200 ms), adjoint backward pass for the soma-v MSE against the perturbed
+    model's trace, and one Adam step (lr 1e-3) over 13 parameters per cell (gnabar, gkbar,
+    g_pas tied per cell; 10 ExpSyn weights)."""
+    import numpy as np
+    import torch
+    from heliox_amd import Sim, build_config
+    from heliox_amd.synth import perturb_config5
+
+    tstop = 200.0
+    base = build_config(5, args.train_cells, tstop)
+    nstep = int(round(tstop / base.dt))
+    soma = list(range(base.ncell))
+    tg = Sim()
+    tg.load_model_from_spec(perturb_config5(base, seed=1), add_monitors=False)
+    for c in soma:
+        tg.add_monitor("global", "v", c)
+    tg.finitialize(-65.0)
+    tg.run(tstop)
+    target = np.ascontiguousarray(tg.traces()[:, 1:].T)
+    del tg
+    g = Sim()
+    g.load_model_from_spec(base, add_monitors=False)
+    g.tape_begin(nstep)
+    cell = base.cell_of_node()
+
+    def forward_backward():
+        t0 = time.perf_counter()
+        g.finitialize(-65.0)
+        g.run(tstop)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        loss = g.adjoint(soma, target)
+        return loss, t1 - t0, time.perf_counter() - t1
+
+    forward_backward()                           # warm-up (no parameter update)
+    opt = g.adam_create(0.9, 0.999, 1e-8)
+    for mech, var in (("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas")):
+        cn = cell[base.mechs[mech].nodes]
+        for c in range(base.ncell):
+            g.adam_add_group(opt, mech, var, np.nonzero(cn == c)[0])
+    for k in range(base.mechs["ExpSyn"].nodes.size):
+        g.adam_add_group(opt, "ExpSyn", "weight", [k])
+    loss, tf, tb = forward_backward()
+    t2 = time.perf_counter()
+    g.adam_step(opt, 1e-3, 1.0)
+    ta = time.perf_counter() - t2
+    total = tf + tb + ta
+    print(json.dumps({"metric": "config-5 training steps/s (1000x500-comp fp64, 200 ms forward + adjoint + Adam)",
+                      "value": 1.0 / total, "unit": "training steps/s", "n_gpus": 1, "steps": 1, "warmup": 1,
+                      "ms_per_step": total * 1e3, "higher_is_better": True, "scaling": "weak",
+                      "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+                      "config": {"workload": f"config 5: {base.ncell} cells x 500 compartments, {nstep} steps",
+                                 "forward_s": tf, "adjoint_s": tb, "adam_s": ta, "loss": loss}}))
+
+
 def calibrate_copy(gib: float = 1.0, reps: int = 5):
     """A plain device copy of known size, for scaling rocprof FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -94,6 +151,8 @@ def main():
     ap.add_argument("--all-kernel-timing", action="store_true",
                     help="time every kernel class (adds event records to the timed region)")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--train", action="store_true", help="time the config-5 training step instead")
+    ap.add_argument("--train-cells", type=int, default=1000)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -108,6 +167,9 @@ def main():
     torch.cuda.set_device(0)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.train:
+        train_bench(args)
         return
 
     from heliox_amd import Sim, build_config

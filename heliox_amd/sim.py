@@ -262,7 +262,12 @@ class Sim:
 
     # --------------------------------------------------------------- monitors
     def add_monitor(self, mech: str, var: str, idx: int) -> int:
-        return lib().hx_add_monitor(self._h, _b(mech), _b(var), int(idx))
+        h = lib().hx_add_monitor(self._h, _b(mech), _b(var), int(idx))
+        if h >= 0:
+            if not hasattr(self, "monitor_handles"):
+                self.monitor_handles = []
+            self.monitor_handles.append(h)
+        return h
 
     def flush_recorders(self) -> int:
         return self._rc(lib().hx_flush_recorders(self._h))
