@@ -31,6 +31,7 @@
 
 #include "heliox.h"
 #include "hx_internal.h"
+#include "learn.h"
 #include "schedule.h"
 #include "solve_chunk.h"
 
@@ -307,7 +308,16 @@ struct hx_sim {
     unsigned prof_mask = ~0u;   // timed kernel classes (bit = TimerId)
     Timer timers[T_COUNT];
 
+    // learn gradient surface (capture + LRDS replay), created on first use
+    std::unique_ptr<LearnRuntime> learn;
+    LearnRuntime& learn_rt() {
+        if (!learn) learn.reset(new LearnRuntime(stream));
+        return *learn;
+    }
+    void require_sample_point(const Ref& r);
+
     ~hx_sim() {
+        learn.reset();
         tape_free();
         for (auto& tm : timers)
             for (auto e : tm.pool) (void)hipEventDestroy(e);
@@ -961,12 +971,24 @@ void hx_sim::launch_detect(int kk, double tk) {
 }
 
 void hx_sim::launch_record() {
+    if (learn && learn->capturing()) learn->sample();
     if (mon_ref.empty()) return;
     if (mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
     tbegin(T_OTHER);
     hx::launch_record(d_mon_ptr, static_cast<int>(mon_ref.size()), d_mon_buf + mon_buf_fill * mon_ref.size(), stream);
     tend(T_OTHER);
     mon_buf_fill++;
+}
+
+// A sampled assigned variable (klass 1) or point-process variable is only
+// valid at the reference's record point under the split schedule.
+void hx_sim::require_sample_point(const Ref& r) {
+    if ((r.klass == 1 || r.point) && !need_split_for_monitor) {
+        need_split_for_monitor = true;
+        write_assigned = write_assigned || r.klass == 1;
+        fused = false;
+        if (state_pending) { finish_pending(); sync_outputs(); }
+    }
 }
 
 // One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
@@ -1427,12 +1449,7 @@ int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx) {
         API_BEGIN
         r = sim->resolve(mech, var, idx);
         if (!r.dev) return sim->fail("monitor %s.%s[%d] not found", mech, var, idx);
-        if ((r.klass == 1 || r.point) && !sim->need_split_for_monitor) {
-            sim->need_split_for_monitor = true;
-            sim->write_assigned = sim->write_assigned || r.klass == 1;
-            sim->fused = false;
-            if (sim->state_pending) { sim->finish_pending(); sim->sync_outputs(); }
-        }
+        sim->require_sample_point(r);
         API_END
     }
     sim->mon_name.push_back({mech, var});
@@ -2110,6 +2127,314 @@ int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* 
         if (v) v[g] = o.v[g];
     }
     return ng;
+}
+
+
+// ---------------------------------------------------------------------------
+// learn gradient surface (LearnRuntime.cpp:197-2457)
+// ---------------------------------------------------------------------------
+int hx_set_dense_blocks_f32(hx_sim* sim, int nblk, const float* const* blocks, const int* bn, const int* k_len) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (nblk < 0 || (nblk > 0 && (!blocks || !bn || !k_len))) return sim->fail("set_dense_blocks_f32: bad arguments");
+    LearnRuntime& L = sim->learn_rt();
+    const int r = L.set_dense_blocks(nblk, blocks, bn, k_len);
+    if (r < 0) return sim->fail("%s", L.err.c_str());
+    return r;
+    API_END
+}
+
+int hx_clear_dense_blocks(hx_sim* sim) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    sim->learn_rt().clear_dense_blocks();
+    return 0;
+    API_END
+}
+
+namespace {
+
+bool resolve_handles(hx_sim* sim, const char* fn, const char* what, int n, const int* hs, std::vector<double*>& out) {
+    out.resize(n);
+    for (int i = 0; i < n; ++i) {
+        if (hs[i] < 0 || hs[i] >= static_cast<int>(sim->handles.size())) {
+            sim->fail("%s: invalid %s handle", fn, what);
+            return false;
+        }
+        const Ref& r = sim->handles[hs[i]];
+        sim->require_sample_point(r);
+        out[i] = r.dev;
+    }
+    return true;
+}
+
+// Steps from a run length, with the reference's tstop check
+// (LearnRuntime.cpp:1719-1725, 286-292).
+bool check_tstop(hx_sim* sim, const char* fn, int total_steps, double tstop_ms) {
+    const double from_steps = static_cast<double>(total_steps) * sim->dt;
+    if (tstop_ms > 0.0 && std::abs(tstop_ms - from_steps) > sim->dt * 0.5) {
+        sim->fail("%s: tstop mismatch (tstop_ms=%f, steps*dt=%f)", fn, tstop_ms, from_steps);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+int hx_simulate_output_vs_into(hx_sim* sim, float* output_vs_tn, int t_steps_plus1, int n_output,
+                               const int* output_v_handles, double tstop_ms, double v_init) {
+    static const char* fn = "simulate_output_vs_into";
+    if (!check_loaded(sim)) return -1;
+    if (!output_vs_tn) return sim->fail("%s: output buffer is null", fn);
+    if (!(sim->dt > 0.0)) return sim->fail("%s: invalid dt", fn);
+    if (n_output <= 0 || !output_v_handles) return sim->fail("%s: output handles mismatch", fn);
+    if (t_steps_plus1 < 2) return sim->fail("%s: invalid steps", fn);
+    API_BEGIN
+    const int total_steps = t_steps_plus1 - 1;
+    if (!check_tstop(sim, fn, total_steps, tstop_ms)) return -1;
+    std::vector<double*> outp;
+    if (!resolve_handles(sim, fn, "output", n_output, output_v_handles, outp)) return -1;
+    LearnRuntime& L = sim->learn_rt();
+    L.begin_capture(t_steps_plus1, outp, 0, 0, 1, false, nullptr, 0, false);
+    try {
+        sim->finitialize(v_init);
+        sim->run_steps(total_steps);
+    } catch (...) {
+        L.end_capture(nullptr);
+        throw;
+    }
+    L.end_capture(output_vs_tn);
+    return 0;
+    API_END
+}
+
+namespace {
+
+// simulate_and_capture_mapped_signals_{cached,into}: N_into > 0 gives N and T
+// and copies the signals to to_host[3] instead of caching them.
+int capture_common(hx_sim* sim, const char* fn, float* output_vs_tn, int total_steps_plus1, int n_output,
+                   const int* output_v_handles, int n_pure_i, const int* pure_i_handles, const int* pure_i_dest,
+                   const float* pure_i_scale, int n_didv, const int* didv_handles, const int* didv_dest,
+                   const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+                   const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init, int N_into,
+                   int T_into, float* const* to_host) {
+    if (k_mul <= 0) return sim->fail("%s: k_mul must be positive", fn);
+    if (!(sim->dt > 0.0)) return sim->fail("%s: invalid dt", fn);
+    if (!output_vs_tn) return sim->fail("%s: output_vs_tn is null", fn);
+    if (n_output <= 0 || !output_v_handles) return sim->fail("%s: output_v_handles size mismatch", fn);
+    if (total_steps_plus1 < 2) return sim->fail("%s: total_steps_plus1 must be >= 2", fn);
+    const int total_steps = total_steps_plus1 - 1;
+    const int ksteps = total_steps / k_mul;
+    if (ksteps <= 0) return sim->fail("%s: ksteps_total must be positive", fn);
+    if (n_pure_i < 0 || n_didv < 0 || n_didvpre < 0) return sim->fail("%s: negative channel size", fn);
+    // cached: N is the largest pure_i destination + 1 (LearnRuntime.cpp:1671-1682)
+    int N = N_into;
+    if (!to_host) {
+        N = 0;
+        for (int i = 0; i < n_pure_i; ++i) N = std::max(N, pure_i_dest[i] + 1);
+        if (N <= 0) return sim->fail("%s: inferred N is non-positive", fn);
+    } else if (N <= 0) {
+        return sim->fail("%s: N must be positive", fn);
+    } else if (T_into < 2) {
+        return sim->fail("%s: ksteps_total_plus1 must be >= 2", fn);
+    }
+    const int* hs[3] = {pure_i_handles, didv_handles, didvpre_handles};
+    const int* ds[3] = {pure_i_dest, didv_dest, didvpre_dest};
+    const float* sc[3] = {pure_i_scale, didv_scale, didvpre_scale};
+    const int cnt[3] = {n_pure_i, n_didv, n_didvpre};
+    const char* names[3] = {"pure_i", "didv", "didvpre"};
+    const int nch = percise ? 3 : 1;
+    for (int c = 0; c < nch; ++c) {
+        if (cnt[c] > 0 && (!hs[c] || !ds[c] || !sc[c])) return sim->fail("%s: %s handles/dest/scale missing", fn, names[c]);
+        for (int i = 0; i < cnt[c]; ++i)
+            if (ds[c][i] < 0 || ds[c][i] >= N)
+                return sim->fail("%s: %s_dest out of range at %d (%d)", fn, names[c], i, ds[c][i]);
+    }
+    API_BEGIN
+    if (!check_tstop(sim, fn, total_steps, tstop_ms)) return -1;
+    std::vector<double*> outp;
+    if (!resolve_handles(sim, fn, "output", n_output, output_v_handles, outp)) return -1;
+    LearnRuntime::Channel ch[3];
+    for (int c = 0; c < nch; ++c) {
+        if (!resolve_handles(sim, fn, names[c], cnt[c], hs[c], ch[c].ptr)) return -1;
+        ch[c].dest.assign(ds[c], ds[c] + cnt[c]);
+        ch[c].scale.assign(sc[c], sc[c] + cnt[c]);
+    }
+    LearnRuntime& L = sim->learn_rt();
+    L.begin_capture(total_steps_plus1, outp, N, T_into, k_mul, percise != 0, ch, nch, to_host != nullptr);
+    try {
+        sim->finitialize(v_init);
+        sim->run_steps(total_steps);
+    } catch (...) {
+        L.end_capture(nullptr);
+        throw;
+    }
+    L.end_capture(output_vs_tn, to_host);
+    return 0;
+    API_END
+}
+
+}  // namespace
+
+int hx_simulate_and_capture_mapped_signals_cached(
+    hx_sim* sim, float* output_vs_tn, int total_steps_plus1, int n_output, const int* output_v_handles, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init) {
+    if (!check_loaded(sim)) return -1;
+    return capture_common(sim, "simulate_and_capture_mapped_signals_cached", output_vs_tn, total_steps_plus1,
+                          n_output, output_v_handles, n_pure_i, pure_i_handles, pure_i_dest, pure_i_scale, n_didv,
+                          didv_handles, didv_dest, didv_scale, n_didvpre, didvpre_handles, didvpre_dest,
+                          didvpre_scale, tstop_ms, k_mul, percise, v_init, 0, 0, nullptr);
+}
+
+int hx_simulate_and_capture_mapped_signals_into(
+    hx_sim* sim, float* output_vs_tn, int total_steps_plus1, int n_output, float* it_lr_tn, float* ditdv_lr_tn,
+    float* ditdvpre_lr_tn, int ksteps_total_plus1, int N, const int* output_v_handles, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init) {
+    static const char* fn = "simulate_and_capture_mapped_signals_into";
+    if (!check_loaded(sim)) return -1;
+    if (!output_vs_tn || !it_lr_tn || !ditdv_lr_tn || !ditdvpre_lr_tn)
+        return sim->fail("%s: output buffers must be non-null", fn);
+    float* host[3] = {it_lr_tn, ditdv_lr_tn, ditdvpre_lr_tn};
+    return capture_common(sim, fn, output_vs_tn, total_steps_plus1, n_output, output_v_handles, n_pure_i,
+                          pure_i_handles, pure_i_dest, pure_i_scale, n_didv, didv_handles, didv_dest, didv_scale,
+                          n_didvpre, didvpre_handles, didvpre_dest, didvpre_scale, tstop_ms, k_mul, percise, v_init,
+                          N, ksteps_total_plus1, host);
+}
+
+namespace {
+
+int replay_common(hx_sim* sim, const char* fn, bool cached, const float* dL, int ksteps, int n_output,
+                  const int* poutput, const int* pinput, int n_input, const int* pre_of_col, int n_pre,
+                  float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
+                  double thr, int clip_strategy, int clip_every) {
+    LearnRuntime& L = sim->learn_rt();
+    if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
+    const int N = cached ? L.capture_N() : n_pre;
+    if (cached) {
+        if (L.capture_N() <= 0 || L.capture_T() < 2) return sim->fail("%s: cached capture buffers not initialized", fn);
+        if (percise && !L.capture_percise())
+            return sim->fail("%s: percise requested but cached didv buffers missing", fn);
+        if (ksteps != L.capture_T() - 1)
+            return sim->fail("%s: ksteps_total mismatch (%d vs %d)", fn, ksteps, L.capture_T() - 1);
+    }
+    if (!dL || !poutput || !pre_of_col || !dw_out_n || (n_input > 0 && (!pinput || !dx_lr_it)))
+        return sim->fail("%s: null input/output pointer", fn);
+    if (n_output <= 0) return sim->fail("%s: empty poutput/pinput", fn);
+    if (n_pre != N) return sim->fail("%s: pre_of_col has %d entries, N is %d", fn, n_pre, N);
+    // indices are checked here: the kernels gather with them
+    for (int o = 0; o < n_output; ++o)
+        if (poutput[o] < 0 || poutput[o] >= N) return sim->fail("%s: poutput[%d]=%d out of range", fn, o, poutput[o]);
+    for (int j = 0; j < n_input; ++j)
+        if (pinput[j] < 0 || pinput[j] >= N) return sim->fail("%s: pinput[%d]=%d out of range", fn, j, pinput[j]);
+    for (int i = 0; i < N; ++i)
+        if (pre_of_col[i] < -1 || pre_of_col[i] >= N)
+            return sim->fail("%s: pre_of_col[%d]=%d out of range", fn, i, pre_of_col[i]);
+    int sum_bn = 0;
+    for (int b = 0; b < static_cast<int>(L.block_sizes().size()); ++b) sum_bn += L.block_sizes()[b];
+    if (sum_bn != N) return sim->fail("%s: dense blocks total N mismatch (sum=%d vs N=%d)", fn, sum_bn, N);
+    LearnRuntime::ReplayIn in;
+    in.dl = dL;
+    in.ksteps = ksteps;
+    in.n_out = n_output;
+    in.n_in = n_input;
+    in.po = poutput;
+    in.pin = pinput;
+    in.pre = pre_of_col;
+    in.dw_out = dw_out_n;
+    in.dx_out = dx_lr_it;
+    in.dt = dt_ms;
+    in.grad_scale = grad_scale;
+    in.eps = eps;
+    in.thr = thr;
+    in.percise = percise != 0;
+    in.clip_strategy = clip_strategy;
+    in.clip_every = std::max(1, clip_every);
+    in.cached = cached;
+    if (L.replay(in) != 0) return sim->fail("%s: %s", fn, L.err.c_str());
+    return 0;
+}
+
+}  // namespace
+
+int hx_replay_compute_dw_from_cached_signals_into(hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total,
+                                                  int n_output, const int* poutput, const int* pre_of_col, int n_pre,
+                                                  float* dw_out_n, double dt_ms, int percise, double grad_scale,
+                                                  double eps, double grad_l2norm_threshold, int clip_strategy,
+                                                  int clip_check_every) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    return replay_common(sim, "replay_compute_dw_from_cached_signals_into", true, dLtdv_lr_to, ksteps_total,
+                         n_output, poutput, nullptr, 0, pre_of_col, n_pre, dw_out_n, nullptr, dt_ms, percise,
+                         grad_scale, eps, grad_l2norm_threshold, clip_strategy, clip_check_every);
+    API_END
+}
+
+int hx_replay_compute_dw_dx_from_cached_signals_into(hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total,
+                                                     int n_output, const int* poutput, const int* pinput, int n_input,
+                                                     const int* pre_of_col, int n_pre, float* dw_out_n,
+                                                     float* dx_lr_it, double dt_ms, int percise, double grad_scale,
+                                                     double eps, double grad_l2norm_threshold, int clip_strategy,
+                                                     int clip_check_every) {
+    static const char* fn = "replay_compute_dw_dx_from_cached_signals_into";
+    if (!check_loaded(sim)) return -1;
+    if (n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
+    API_BEGIN
+    return replay_common(sim, fn, true, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput, n_input, pre_of_col,
+                         n_pre, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps, grad_l2norm_threshold,
+                         clip_strategy, clip_check_every);
+    API_END
+}
+
+int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt, const float* ditdv_lr_nt,
+                                              const float* ditdvpre_lr_nt, int N, int T, const float* dLtdv_lr_to,
+                                              int ksteps_total, int n_output, const int* poutput, const int* pinput,
+                                              int n_input, const int* pre_of_col, float* dw_out_n, float* dx_lr_it,
+                                              double dt_ms, int percise, double grad_scale, double eps,
+                                              double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    static const char* fn = "replay_compute_dw_dx_from_signals_into";
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    LearnRuntime& L = sim->learn_rt();
+    // LearnRuntime.cpp:402-450
+    if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
+    if (!it_lr_nt || !dLtdv_lr_to || !poutput || !pinput || !pre_of_col || !dw_out_n || !dx_lr_it)
+        return sim->fail("%s: null pointer input/output", fn);
+    if (N <= 0 || T < 2) return sim->fail("%s: invalid it_lr_nt shape (%d, %d)", fn, N, T);
+    if (ksteps_total != T - 1) return sim->fail("%s: ksteps_total mismatch (%d vs T-1=%d)", fn, ksteps_total, T - 1);
+    if (n_output <= 0 || n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
+    if (!(dt_ms > 0.0) || !(eps > 0.0)) return sim->fail("%s: invalid dt_ms/eps", fn);
+    if (!(grad_l2norm_threshold > 0.0)) return sim->fail("%s: invalid grad_l2norm_threshold", fn);
+    clip_strategy = std::max(0, clip_strategy);
+    clip_check_every = std::max(1, clip_check_every);
+    if (percise && (!ditdv_lr_nt || !ditdvpre_lr_nt))
+        return sim->fail("%s: percise requested but ditdv buffers are null", fn);
+    int sum_bn = 0;
+    for (int bn : L.block_sizes()) sum_bn += bn;
+    if (sum_bn != N) return sim->fail("%s: dense blocks total N mismatch (sum=%d vs N=%d)", fn, sum_bn, N);
+    if (L.load_signals(it_lr_nt, ditdv_lr_nt, ditdvpre_lr_nt, N, T, percise != 0) != 0)
+        return sim->fail("%s", L.err.c_str());
+    return replay_common(sim, fn, false, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput, n_input, pre_of_col,
+                         N, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps, grad_l2norm_threshold,
+                         clip_strategy, clip_check_every);
+    API_END
+}
+
+int hx_set_replay_timing(hx_sim* sim, int enable) {
+    if (!check_loaded(sim)) return -1;
+    sim->learn_rt().timing = enable != 0;
+    return 0;
+}
+
+int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches) {
+    if (!check_loaded(sim)) return -1;
+    LearnRuntime& L = sim->learn_rt();
+    if (ms) *ms = L.corr_ms;
+    if (launches) *launches = L.corr_launches;
+    return 0;
 }
 
 }  // extern "C"

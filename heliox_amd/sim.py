@@ -95,6 +95,26 @@ SIGNATURES = {
     "hx_get_kernel_time": (C.c_int, [_P, _S, _D, C.POINTER(C.c_longlong)]),
     "hx_get_info": (C.c_longlong, [_P, _S]),
     "hx_emulate_tree_solve": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, _I, _I]),
+    "hx_set_dense_blocks_f32": (C.c_int, [_P, C.c_int, C.POINTER(_F), _I, _I]),
+    "hx_clear_dense_blocks": (C.c_int, [_P]),
+    "hx_simulate_output_vs_into": (C.c_int, [_P, _F, C.c_int, C.c_int, _I, C.c_double, C.c_double]),
+    "hx_simulate_and_capture_mapped_signals_cached": (
+        C.c_int, [_P, _F, C.c_int, C.c_int, _I, C.c_int, _I, _I, _F, C.c_int, _I, _I, _F, C.c_int, _I, _I, _F,
+                  C.c_double, C.c_int, C.c_int, C.c_double]),
+    "hx_simulate_and_capture_mapped_signals_into": (
+        C.c_int, [_P, _F, C.c_int, C.c_int, _F, _F, _F, C.c_int, C.c_int, _I, C.c_int, _I, _I, _F, C.c_int, _I, _I,
+                  _F, C.c_int, _I, _I, _F, C.c_double, C.c_int, C.c_int, C.c_double]),
+    "hx_replay_compute_dw_from_cached_signals_into": (
+        C.c_int, [_P, _F, C.c_int, C.c_int, _I, _I, C.c_int, _F, C.c_double, C.c_int, C.c_double, C.c_double,
+                  C.c_double, C.c_int, C.c_int]),
+    "hx_replay_compute_dw_dx_from_cached_signals_into": (
+        C.c_int, [_P, _F, C.c_int, C.c_int, _I, _I, C.c_int, _I, C.c_int, _F, _F, C.c_double, C.c_int, C.c_double,
+                  C.c_double, C.c_double, C.c_int, C.c_int]),
+    "hx_replay_compute_dw_dx_from_signals_into": (
+        C.c_int, [_P, _F, _F, _F, C.c_int, C.c_int, _F, C.c_int, C.c_int, _I, _I, C.c_int, _I, _F, _F, C.c_double,
+                  C.c_int, C.c_double, C.c_double, C.c_double, C.c_int, C.c_int]),
+    "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
+    "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
 
 
@@ -123,6 +143,28 @@ def _ip(a: np.ndarray):
 
 def _b(s: str) -> bytes:
     return s.encode()
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a, ndim=None) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    if ndim is not None and a.ndim != ndim:
+        raise ValueError(f"expected a {ndim}-D float32 array")
+    return a
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, np.int32).reshape(-1))
+
+
+def _out_f32(a: np.ndarray, name: str) -> np.ndarray:
+    """Caller-owned output buffer: C-contiguous float32, written in place."""
+    if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError(f"{name} must be a C-contiguous float32 ndarray")
+    return a
 
 
 class HelioxError(RuntimeError):
@@ -157,15 +199,25 @@ class Sim:
         return self._h
 
     def last_error(self) -> str:
+        py = getattr(self, "_py_err", None)
+        if py:
+            return py
         return lib().hx_last_error(self._h).decode()
 
+    def _pyfail(self, msg: str) -> int:
+        """Argument check failed before reaching the library (the reference prints and returns -1)."""
+        self._py_err = msg
+        return -1
+
     def _chk(self, rc: int, what: str) -> int:
+        self._py_err = None
         if rc < 0:
             raise HelioxError(f"{what}: {self.last_error()}")
         return rc
 
     def _rc(self, rc: int) -> int:
         """Reference convention: return 0 / -1 and keep the message for last_error()."""
+        self._py_err = None
         return 0 if rc >= 0 else -1
 
     # --------------------------------------------------------------- settings
@@ -426,6 +478,157 @@ class Sim:
         v = np.zeros(max(ngroup, 1))
         self._chk(lib().hx_adam_get_state(self._h, opt, C.byref(step), _dp(m), _dp(v), m.size), "adam_state")
         return step.value, m[:ngroup], v[:ngroup]
+
+    # ---- learn gradient surface (SimWrapper.cpp:533-1183; PyBindings.cpp:88-200).
+    # Like the reference's bindings these return 0 / -1; last_error() holds the message.
+    def set_dense_blocks_f32(self, blocks) -> int:
+        """Upload (bn, bn, K_len) float32 blocks; returns K_len or -1 (SimWrapper.cpp:533-572)."""
+        self._py_err = None
+        arrs = [np.ascontiguousarray(b, np.float32) for b in blocks]
+        for a in arrs:
+            if a.ndim != 3 or a.shape[0] != a.shape[1]:
+                return self._pyfail("set_dense_blocks_f32: blocks must be (bn, bn, K_len)")
+        ptrs = (_F * max(len(arrs), 1))(*[_fp(a) for a in arrs])
+        bn = _i32([a.shape[0] for a in arrs] or [0])
+        kl = _i32([a.shape[2] for a in arrs] or [0])
+        self._blocks_keepalive = arrs
+        return lib().hx_set_dense_blocks_f32(self._h, len(arrs), ptrs, _ip(bn), _ip(kl))
+
+    def clear_dense_blocks(self) -> None:
+        self._chk(lib().hx_clear_dense_blocks(self._h), "clear_dense_blocks")
+
+    def simulate_output_vs_into(self, output_vs_tn: np.ndarray, output_v_handles, tstop_ms: float,
+                                v_init: float) -> int:
+        self._py_err = None
+        out = _out_f32(output_vs_tn, "output_vs_tn")
+        if out.ndim != 2:
+            return self._pyfail("simulate_output_vs_into: output_vs_tn must be 2D")
+        hs = _i32(output_v_handles)
+        if hs.size != out.shape[1]:
+            return self._pyfail("simulate_output_vs_into: output handles mismatch")
+        return self._rc(lib().hx_simulate_output_vs_into(self._h, _fp(out), out.shape[0], hs.size, _ip(hs),
+                                                         tstop_ms, v_init))
+
+    @staticmethod
+    def _channel(handles, dest, scale):
+        h, d, sc = _i32(handles), _i32(dest), _f32(np.asarray(scale).reshape(-1))
+        if not (h.size == d.size == sc.size):
+            raise ValueError("handles/dest/scale size mismatch")
+        return h, d, sc
+
+    def simulate_and_capture_mapped_signals_cached(self, output_vs_tn, output_v_handles, pure_i_handles,
+                                                   pure_i_dest, pure_i_scale, didv_handles, didv_dest, didv_scale,
+                                                   didvpre_handles, didvpre_dest, didvpre_scale, tstop_ms: float,
+                                                   k_mul: int, percise: bool, v_init: float) -> int:
+        self._py_err = None
+        out = _out_f32(output_vs_tn, "output_vs_tn")
+        hs = _i32(output_v_handles)
+        try:
+            ch = [self._channel(pure_i_handles, pure_i_dest, pure_i_scale),
+                  self._channel(didv_handles, didv_dest, didv_scale),
+                  self._channel(didvpre_handles, didvpre_dest, didvpre_scale)]
+        except ValueError as e:
+            return self._pyfail(f"simulate_and_capture_mapped_signals_cached: {e}")
+        if out.ndim != 2 or out.shape[1] != hs.size:
+            return self._pyfail("simulate_and_capture_mapped_signals_cached: output_v_handles size mismatch")
+        args = []
+        for h, d, sc in ch:
+            args += [h.size, _ip(h), _ip(d), _fp(sc)]
+        return self._rc(lib().hx_simulate_and_capture_mapped_signals_cached(
+            self._h, _fp(out), out.shape[0], hs.size, _ip(hs), *args, tstop_ms, int(k_mul), int(bool(percise)),
+            v_init))
+
+    def simulate_and_capture_mapped_signals_into(self, output_vs_tn, it_lr_tn, ditdv_lr_tn, ditdvpre_lr_tn,
+                                                 output_v_handles, pure_i_handles, pure_i_dest, pure_i_scale,
+                                                 didv_handles, didv_dest, didv_scale, didvpre_handles, didvpre_dest,
+                                                 didvpre_scale, tstop_ms: float, k_mul: int, percise: bool,
+                                                 v_init: float) -> int:
+        self._py_err = None
+        out = _out_f32(output_vs_tn, "output_vs_tn")
+        bufs = [_out_f32(b, n) for b, n in ((it_lr_tn, "it_lr_tn"), (ditdv_lr_tn, "ditdv_lr_tn"),
+                                             (ditdvpre_lr_tn, "ditdvpre_lr_tn"))]
+        if any(b.ndim != 2 or b.shape != bufs[0].shape for b in bufs) or out.ndim != 2:
+            return self._pyfail("simulate_and_capture_mapped_signals_into: outputs must be 2D arrays")
+        hs = _i32(output_v_handles)
+        if out.shape[1] != hs.size:
+            return self._pyfail("simulate_and_capture_mapped_signals_into: output_vs_tn shape mismatch")
+        try:
+            ch = [self._channel(pure_i_handles, pure_i_dest, pure_i_scale),
+                  self._channel(didv_handles, didv_dest, didv_scale),
+                  self._channel(didvpre_handles, didvpre_dest, didvpre_scale)]
+        except ValueError as e:
+            return self._pyfail(f"simulate_and_capture_mapped_signals_into: {e}")
+        args = []
+        for h, d, sc in ch:
+            args += [h.size, _ip(h), _ip(d), _fp(sc)]
+        T, N = bufs[0].shape
+        return self._rc(lib().hx_simulate_and_capture_mapped_signals_into(
+            self._h, _fp(out), out.shape[0], hs.size, _fp(bufs[0]), _fp(bufs[1]), _fp(bufs[2]), T, N, _ip(hs),
+            *args, tstop_ms, int(k_mul), int(bool(percise)), v_init))
+
+    def replay_compute_dw_from_cached_signals_into(self, dLtdv_lr_ot, poutput, pre_of_col, dw_out_n, dt_ms: float,
+                                                   percise: bool, grad_scale: float = 1.0, eps: float = 1e-6,
+                                                   grad_l2norm_threshold: float = 1e6, clip_strategy: int = 1,
+                                                   clip_check_every: int = 1) -> int:
+        self._py_err = None
+        dl = _f32(dLtdv_lr_ot, 2)
+        po, pre = _i32(poutput), _i32(pre_of_col)
+        dw = _out_f32(dw_out_n, "dw_out_n")
+        if dw.size != pre.size:
+            return self._pyfail("replay_compute_dw_from_cached_signals_into: dw_out_n must have N entries")
+        return self._rc(lib().hx_replay_compute_dw_from_cached_signals_into(
+            self._h, _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pre), pre.size, _fp(dw), dt_ms,
+            int(bool(percise)), grad_scale, eps, grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))
+
+    def replay_compute_dw_dx_from_cached_signals_into(self, dLtdv_lr_ot, poutput, pinput, pre_of_col, dw_out_n,
+                                                      dx_lr_it, dt_ms: float, percise: bool, grad_scale: float = 1.0,
+                                                      eps: float = 1e-6, grad_l2norm_threshold: float = 1e6,
+                                                      clip_strategy: int = 1, clip_check_every: int = 1) -> int:
+        self._py_err = None
+        dl = _f32(dLtdv_lr_ot, 2)
+        po, pin, pre = _i32(poutput), _i32(pinput), _i32(pre_of_col)
+        dw = _out_f32(dw_out_n, "dw_out_n")
+        dx = _out_f32(dx_lr_it, "dx_lr_it")
+        if dw.size != pre.size or dx.shape != (pin.size, dl.shape[0]):
+            return self._pyfail("replay_compute_dw_dx_from_cached_signals_into: output shape mismatch")
+        return self._rc(lib().hx_replay_compute_dw_dx_from_cached_signals_into(
+            self._h, _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, _ip(pre), pre.size, _fp(dw),
+            _fp(dx), dt_ms, int(bool(percise)), grad_scale, eps, grad_l2norm_threshold, int(clip_strategy),
+            int(clip_check_every)))
+
+    def replay_compute_dw_dx_from_signals_into(self, it_lr_nt, ditdv_lr_nt, ditdvpre_lr_nt, dLtdv_lr_to, poutput,
+                                               pinput, pre_of_col, dw_out_n, dx_lr_it, dt_ms: float, percise: bool,
+                                               grad_scale: float = 1.0, eps: float = 1e-6,
+                                               grad_l2norm_threshold: float = 1e6, clip_strategy: int = 1,
+                                               clip_check_every: int = 1) -> int:
+        self._py_err = None
+        it = _f32(it_lr_nt, 2)
+        dv = _f32(ditdv_lr_nt, 2) if ditdv_lr_nt is not None else None
+        dp = _f32(ditdvpre_lr_nt, 2) if ditdvpre_lr_nt is not None else None
+        dl = _f32(dLtdv_lr_to, 2)
+        po, pin, pre = _i32(poutput), _i32(pinput), _i32(pre_of_col)
+        dw = _out_f32(dw_out_n, "dw_out_n")
+        dx = _out_f32(dx_lr_it, "dx_lr_it")
+        N, T = it.shape
+        for a in (dv, dp):
+            if a is not None and a.shape != it.shape:
+                return self._pyfail("replay_compute_dw_dx_from_signals_into: signal shape mismatch")
+        if pre.size != N or dw.size != N or dx.shape != (pin.size, dl.shape[0]):
+            return self._pyfail("replay_compute_dw_dx_from_signals_into: output shape mismatch")
+        null = C.cast(None, _F)
+        return self._rc(lib().hx_replay_compute_dw_dx_from_signals_into(
+            self._h, _fp(it), _fp(dv) if dv is not None else null, _fp(dp) if dp is not None else null, N, T,
+            _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, _ip(pre), _fp(dw), _fp(dx), dt_ms,
+            int(bool(percise)), grad_scale, eps, grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))
+
+    def set_replay_timing(self, enable: bool) -> None:
+        self._chk(lib().hx_set_replay_timing(self._h, int(bool(enable))), "set_replay_timing")
+
+    def replay_kernel_time(self):
+        ms = C.c_double()
+        n = C.c_longlong()
+        self._chk(lib().hx_get_replay_kernel_time(self._h, C.byref(ms), C.byref(n)), "replay_kernel_time")
+        return ms.value, n.value
 
     def kernel_time(self, kernel: str):
         ms = C.c_double()

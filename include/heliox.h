@@ -160,6 +160,69 @@ int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, i
 int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps);
 int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap);
 
+/* ---- Learn gradient surface: learning-signal capture and LRDS replay
+ *      (LearnRuntime.cpp:197-2457, kernels replay_dw_dx.cu:9-731; Python surface
+ *      heliox_learn/signals.py:102-276).  Signals and gradients are fp32. ---- */
+/* LearnRuntime::set_dense_blocks_f32 (LearnRuntime.cpp:197-244; SimWrapper.cpp:533-572):
+ * block b is a C-contiguous (bn[b], bn[b], k_len[b]) fp32 array; all k_len equal.
+ * Blocks partition the replay columns in order.  Drops any cached capture.
+ * Returns K_len (0 for nblk 0) or -1. */
+int hx_set_dense_blocks_f32(hx_sim* sim, int nblk, const float* const* blocks, const int* bn, const int* k_len);
+/* LearnRuntime::clear_dense_blocks (LearnRuntime.cpp:246-257) */
+int hx_clear_dense_blocks(hx_sim* sim);
+/* LearnRuntime::simulate_output_vs_into (LearnRuntime.cpp:259-370): finitialize(v_init),
+ * then t_steps_plus1 - 1 steps; output_vs_tn[(t_steps_plus1, n_output)] receives the
+ * handles' values (fp32) after finitialize and after every step. */
+int hx_simulate_output_vs_into(hx_sim* sim, float* output_vs_tn, int t_steps_plus1, int n_output,
+                               const int* output_v_handles, double tstop_ms, double v_init);
+/* LearnRuntime::simulate_and_capture_mapped_signals_cached (LearnRuntime.cpp:1619-1984):
+ * as hx_simulate_output_vs_into, and every k_mul steps each mapped channel (pure_i; with
+ * percise also didv and didvpre) gathers its handles' values, rounds them to fp32,
+ * multiplies by scale and sums them into column dest of the cached (T, N) signal,
+ * T = (total_steps_plus1 - 1) / k_mul + 1, N = max(pure_i_dest) + 1. */
+int hx_simulate_and_capture_mapped_signals_cached(
+    hx_sim* sim, float* output_vs_tn, int total_steps_plus1, int n_output, const int* output_v_handles, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init);
+/* LearnRuntime::simulate_and_capture_mapped_signals_into (LearnRuntime.cpp:1289-1618): the
+ * same capture with N and T = ksteps_total_plus1 given, written to the host (T, N) arrays
+ * it/ditdv/ditdvpre (zeros for the dIt channels without percise); the cache is untouched. */
+int hx_simulate_and_capture_mapped_signals_into(
+    hx_sim* sim, float* output_vs_tn, int total_steps_plus1, int n_output, float* it_lr_tn, float* ditdv_lr_tn,
+    float* ditdvpre_lr_tn, int ksteps_total_plus1, int N, const int* output_v_handles, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init);
+/* LearnRuntime::replay_compute_dw_from_cached_signals_into (LearnRuntime.cpp:2329-2359):
+ * dLtdv_lr_to is (ksteps_total, n_output); pre_of_col has n_pre == N entries (-1: none);
+ * dw_out_n receives N values.  Index arrays are range-checked. */
+int hx_replay_compute_dw_from_cached_signals_into(hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total,
+                                                  int n_output, const int* poutput, const int* pre_of_col, int n_pre,
+                                                  float* dw_out_n, double dt_ms, int percise, double grad_scale,
+                                                  double eps, double grad_l2norm_threshold, int clip_strategy,
+                                                  int clip_check_every);
+/* LearnRuntime::replay_compute_dw_dx_from_cached_signals_into (LearnRuntime.cpp:2298-2328):
+ * as above, plus dx_lr_it[(n_input, ksteps_total)] for the input columns pinput. */
+int hx_replay_compute_dw_dx_from_cached_signals_into(hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total,
+                                                     int n_output, const int* poutput, const int* pinput, int n_input,
+                                                     const int* pre_of_col, int n_pre, float* dw_out_n,
+                                                     float* dx_lr_it, double dt_ms, int percise, double grad_scale,
+                                                     double eps, double grad_l2norm_threshold, int clip_strategy,
+                                                     int clip_check_every);
+/* LearnRuntime::replay_compute_dw_dx_from_signals_into (LearnRuntime.cpp:372-727): the same
+ * replay over host signals it/ditdv/ditdvpre given as (N, T) arrays. */
+int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt, const float* ditdv_lr_nt,
+                                              const float* ditdvpre_lr_nt, int N, int T, const float* dLtdv_lr_to,
+                                              int ksteps_total, int n_output, const int* poutput, const int* pinput,
+                                              int n_input, const int* pre_of_col, float* dw_out_n, float* dx_lr_it,
+                                              double dt_ms, int percise, double grad_scale, double eps,
+                                              double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
+/* Timing of the replay's correction-GEMM launches with HIP events on the library stream
+ * (no counterpart in the reference; used by the benchmark). */
+int hx_set_replay_timing(hx_sim* sim, int enable);
+int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches);
+
 /* Host emulation of the device tree solve (no counterpart in the reference;
  * a diagnostic for CPU-only checks of the solver schedule): capacitance and
  * axial assembly, elimination and back substitution over the same chunk
