@@ -126,6 +126,94 @@ def train_bench(args):
                                  "forward_s": tf, "adjoint_s": tb, "adam_s": ta, "loss": loss}}))
 
 
+MFMA_F32_PEAK_TFS = 157.3
+
+
+def lrds_problem(N, bn, K_len, ksteps, n_out, n_in, seed=0):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    T = ksteps + 1
+    blocks = [(rng.normal(0, 1, (bn, bn, K_len)) * 0.5 / np.sqrt(bn)).astype(np.float32) for _ in range(N // bn)]
+    it = rng.normal(0, 1, (N, T)).astype(np.float32)
+    dv = rng.normal(0, 0.3, (N, T)).astype(np.float32)
+    dp = rng.normal(0, 0.3, (N, T)).astype(np.float32)
+    it[:, 0] = dv[:, 0] = dp[:, 0] = 0
+    pre = np.where(rng.random(N) < 0.6, rng.integers(0, N, N), -1).astype(np.int32)
+    po = np.sort(rng.choice(N, n_out, replace=False)).astype(np.int32)
+    pin = np.sort(rng.choice(N, n_in, replace=False)).astype(np.int32)
+    dL = rng.normal(0, 1, (ksteps, n_out)).astype(np.float32)
+    return blocks, it, dv, dp, pre, po, pin, dL
+
+
+def lrds_cpu_baseline(N, bn, K_len, ksteps, rows):
+    """The oracle replay (fp64 numpy, one BLAS thread) on a row subset over every
+    tick: rows of dv/dw are independent recurrences, so the full-problem rate is
+    the subset rate x rows / N."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import lrds
+    blocks, it, dv, dp, pre, po, pin, dL = lrds_problem(N, bn, K_len, ksteps, 64, 16)
+    sel = np.linspace(0, N - 1, rows).astype(np.int64)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        lrds.replay(it, dv, dp, blocks, dL, po, pre, dt=0.025, percise=True, clip_strategy=0, rows=sel)
+        el = time.perf_counter() - t0
+    return {"value": ksteps * rows / N / el, "unit": "LR ticks/s", "cores": 1, "kind": "port",
+            "sample": f"oracle replay of {rows} of {N} rows over all {ksteps} ticks ({el:.1f} s on one core; "
+                      f"dx and clipping need every row and are left out of the sample)"}
+
+
+def lrds_bench(args):
+    """LRDS replay (the learn gradient surface): N = 2048 columns in 16 dense blocks
+    of 128, K_len = 64, 256 LR ticks, precise correction, dw and dx for 16 inputs,
+    Frobenius clip checked every tick (the reference's defaults).  Signals are
+    uploaded once; a step is one LR tick of the replay."""
+    import numpy as np
+    import torch
+    from heliox_amd import Sim, build_config
+
+    N, bn, K_len, ks = args.lrds_n, 128, 64, args.lrds_ticks
+    blocks, it, dv, dp, pre, po, pin, dL = lrds_problem(N, bn, K_len, ks, 64, 16)
+    g = Sim()
+    g.load_model_from_spec(build_config(1, 1, 1.0), add_monitors=False)
+    assert g.set_dense_blocks_f32(blocks) == K_len
+    dw = np.zeros(N, np.float32)
+    dx = np.zeros((pin.size, ks), np.float32)
+
+    def replay():
+        rc = g.replay_compute_dw_dx_from_signals_into(it, dv, dp, dL, po, pin, pre, dw, dx, 0.025, True)
+        if rc != 0:
+            raise RuntimeError(g.last_error())
+
+    replay()                                    # warm-up: workspace and signal upload paths
+    # timed: the replay loop only (signals uploaded inside the call are part of it)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    replay()
+    wall = time.perf_counter() - t0
+    g.set_replay_timing(True)
+    replay()
+    corr_ms, launches = g.replay_kernel_time()
+    g.set_replay_timing(False)
+    # algorithmic flops of the correction GEMM: 2 N bn^2 tw per block per tick
+    flops = sum(2.0 * N * bn * bn * min(t, K_len) * (N // bn) for t in range(1, ks + 1))
+    achieved = flops / (corr_ms / 1e3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F32_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": round(achieved / MFMA_F32_PEAK_TFS, 4), "traffic": None,
+                "kernel": "k_rp_corr (fp32 MFMA 32x32x2 correction GEMM)",
+                "alg_flops_per_launch": flops / ks, "us_per_launch": corr_ms * 1e3 / launches}
+    cpu = None if args.no_cpu_baseline else lrds_cpu_baseline(N, bn, K_len, ks, args.lrds_cpu_rows)
+    print(json.dumps({
+        "metric": "LRDS replay LR ticks/s (N=2048, 16x128 blocks, K_len 64, precise, fp32)",
+        "value": ks / wall, "unit": "LR ticks/s", "n_gpus": 1, "steps": ks, "warmup": 1,
+        "ms_per_step": wall * 1e3 / ks, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"LRDS replay: N={N} columns, {N // bn} blocks of {bn}, K_len {K_len}, {ks} ticks, "
+                               f"precise, 64 outputs, 16 inputs, clip every tick",
+                   "replay_s": wall},
+        "roofline": roofline, "cpu_baseline": cpu}))
+
+
 def calibrate_copy(gib: float = 1.0, reps: int = 5):
     """A plain device copy of known size, for scaling rocprof FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -153,6 +241,10 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--train", action="store_true", help="time the config-5 training step instead")
     ap.add_argument("--train-cells", type=int, default=1000)
+    ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
+    ap.add_argument("--lrds-n", type=int, default=2048)
+    ap.add_argument("--lrds-ticks", type=int, default=256)
+    ap.add_argument("--lrds-cpu-rows", type=int, default=6)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -170,6 +262,9 @@ def main():
         return
     if args.train:
         train_bench(args)
+        return
+    if args.lrds:
+        lrds_bench(args)
         return
 
     from heliox_amd import Sim, build_config

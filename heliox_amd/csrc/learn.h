@@ -12,6 +12,9 @@
 //   * the dv/dw history is a ring of K_len + 1 row-major N x N fp32 slices:
 //     tick tau lives in slot tau % (K_len + 1), slot 0 starts as the zero slice
 //     of tick 0, and the slot a tick writes is never in its own read window.
+//     A second ring holds each slice's column-gathered copy G[i][c] =
+//     D[i][pre(c)], written once per tick, so the correction's pre operand is a
+//     contiguous read instead of a gather per (row, tap);
 //     A per-slot fp32 scale carries the Frobenius clip's rescaling of the history
 //     instead of rewriting K_len slices.
 #pragma once
@@ -57,6 +60,7 @@ struct ReplayBaseArgs {
 
 struct ReplayCorrArgs {
     const float* hist = nullptr;
+    const float* ghist = nullptr;     // column-gathered copies: ghist[h][i][c] = hist[h][i][pre(c)]
     long long slice = 0;              // N * N
     const float* slot_scale = nullptr;
     int R = 1;                        // ring slots
@@ -80,7 +84,8 @@ struct ReplayCorrArgs {
 
 void launch_lr_capture(const CaptureArgs& a, int sample, int lr, hipStream_t s);
 void launch_rp_base(const ReplayBaseArgs& a, int nblk, int max_bn, hipStream_t s);
-void launch_rp_corr(const ReplayCorrArgs& a, int ntiles, hipStream_t s);
+void launch_rp_corr(const ReplayCorrArgs& a, int ntiles, int tile_cols, hipStream_t s);
+void launch_rp_pregather(const float* D, const int* pre, int N, float* G, hipStream_t s);
 int rp_corr_row_tiles(int N);
 void launch_rp_clip(const double* part, const int* flag, int n, float thr, float* gs, float* slot_scale, int R,
                     float* tick_scale, hipStream_t s);
@@ -158,7 +163,7 @@ private:
 
     hipStream_t stream_;
     // dense blocks
-    int k_len_ = 0, nblk_ = 0, max_bn_ = 0;
+    int k_len_ = 0, nblk_ = 0, max_bn_ = 0, tile_cols_ = 64;
     std::vector<int> bn_, start_;
     std::vector<long long> koff_, boff_;
     std::vector<int2> tiles_;
@@ -186,7 +191,7 @@ private:
     std::vector<void*> ws_mem_;
     std::vector<long long> ws_key_;
     struct Workspace {
-        float *hist = nullptr, *slot_scale = nullptr, *gs = nullptr, *tick_scale = nullptr, *w_tick = nullptr,
+        float *hist = nullptr, *ghist = nullptr, *slot_scale = nullptr, *gs = nullptr, *tick_scale = nullptr, *w_tick = nullptr,
               *dw_acc = nullptr, *dl = nullptr, *dx = nullptr, *dw_out = nullptr;
         int *po = nullptr, *pre = nullptr, *pin = nullptr, *flag_part = nullptr;
         double* norm_part = nullptr;

@@ -13,7 +13,9 @@
 // (base term replay_dw_dx.cu:227-274, correction :282-325).  The correction is
 // a GEMM per block, (N x bn*tw) X times (bn*tw x bn) K: k_rp_corr computes it
 // with v_mfma_f32_32x32x2f32, forming X on the fly from the history slices as
-// it stages each 64-row x 32-tap chunk through LDS.
+// it stages each 128-row x 32-tap chunk through LDS.  The pre(s+k) operand is
+// read from a column-gathered copy of each slice made once when the slice is
+// written (k_rp_pregather), so every history read is a contiguous row segment.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -73,16 +75,27 @@ __global__ void k_rp_base(ReplayBaseArgs A) {
 }
 
 // ---------------------------------------------------------------- correction GEMM
-constexpr int kTI = 64;        // rows of dvtdw per workgroup
-constexpr int kTJ = 64;        // columns per workgroup (one column tile of a block)
-constexpr int kKC = 32;        // taps (k) per staged chunk
+// Workgroup tile: 128 rows x TJ columns of one block (TJ = 64 or 128), 8 waves
+// as 4 row groups x 2 column groups; a wave owns 32 rows x TJ/2 columns, i.e.
+// TJ/64 accumulators of v_mfma_f32_32x32x2f32.  The reduction runs over
+// (tap u, chunk of 32 columns k).  Each chunk stages X -- formed from the
+// history slice D and its column-gathered copy G, both read as contiguous row
+// segments -- and the K taps through LDS, double-buffered, with the next
+// chunk's global loads in flight while the MFMAs run.
+constexpr int kCorrThreads = 512;
+constexpr int kTI = 128;
+constexpr int kKC = 32;
 constexpr int kAPad = kTI + 1;
 
-__global__ __launch_bounds__(kThreads) void k_rp_corr(ReplayCorrArgs A) {
-    __shared__ float As[2][kKC][kAPad];     // X chunk, [k][i]
-    __shared__ float Bs[2][kKC][kTJ];       // K chunk, [k][j]
-    __shared__ double red_s[kThreads / 64];
-    __shared__ int red_f[kThreads / 64];
+template <int TJ>
+__global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
+    constexpr int NACC = TJ / 64;                       // 32-column accumulators per wave
+    constexpr int BSTEP = kCorrThreads / TJ;            // B rows covered per pass
+    constexpr int BR = kKC / BSTEP;                     // B elements per thread
+    __shared__ float As[2][kKC][kAPad];                 // X chunk, [k][i]
+    __shared__ float Bs[2][kKC][TJ];                    // K chunk, [k][j]
+    __shared__ double red_s[kCorrThreads / 64];
+    __shared__ int red_f[kCorrThreads / 64];
 
     const int2 tl = A.tiles[blockIdx.x];
     const int b = tl.x, j0 = tl.y;
@@ -96,102 +109,110 @@ __global__ __launch_bounds__(kThreads) void k_rp_corr(ReplayCorrArgs A) {
     const int nkc = (bn + kKC - 1) / kKC;
     const int nchunk = A.tw * nkc;
 
-    // staging coordinates: A element (row ai + 8r, tap ak), B element (tap bk + 4r, column bj)
+    // staging coordinates: A element (row ai + 16r, tap ak), B element (tap bk + BSTEP r, column bj)
     const int ak = tid & 31, ai = tid >> 5;
-    const int bj = tid & 63, bk = tid >> 6;
-    float rv[8], rp[8], rb[8];
+    const int bj = tid % TJ, bk = tid / TJ;
+    float rd[8], rg[8], rb[BR];
     float ca = 0.f, cp = 0.f;
 
     auto fetch = [&](int c) {
         const int u = c / nkc;
         const int k0 = (c - u * nkc) * kKC;
         const int h = (A.t_lr - A.tw + u) % A.R;
-        const float* H = A.hist + static_cast<size_t>(h) * A.slice;
+        const size_t hoff = static_cast<size_t>(h) * A.slice;
+        const float* D = A.hist + hoff;
+        const float* G = A.ghist + hoff;
         const int kc = k0 + ak;
         const bool kin = kc < bn;
         const int col = s + kc;
         const size_t tau = static_cast<size_t>(A.it_t0 + u);
-        int pc = -1;
         ca = 0.f;
         cp = 0.f;
         if (kin) {
             const float sig = A.slot_scale[h];
             ca = sig * A.dv[tau * N + col];
             cp = sig * A.dp[tau * N + col];
-            pc = A.pre[col];
         }
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            const int i = i0 + ai + 8 * r;
+            const int i = i0 + ai + 16 * r;
             float x = 0.f, y = 0.f;
             if (kin && i < N) {
-                const float* Hr = H + static_cast<size_t>(i) * N;
-                x = Hr[col];
-                if (pc >= 0) y = Hr[pc];
+                const size_t o = static_cast<size_t>(i) * N + col;
+                x = D[o];
+                y = G[o];
             }
-            rv[r] = x;
-            rp[r] = y;
+            rd[r] = x;
+            rg[r] = y;
         }
         const float* Kt = Kb + static_cast<size_t>(A.k_t0 + u) * plane;
         const int jj = j0 + bj;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int k = k0 + bk + 4 * r;
+        for (int r = 0; r < BR; ++r) {
+            const int k = k0 + bk + BSTEP * r;
             rb[r] = (jj < bn && k < bn) ? Kt[static_cast<size_t>(k) * bn + jj] : 0.f;
         }
     };
     auto stage = [&](int buf) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) As[buf][ak][ai + 8 * r] = rv[r] * ca + rp[r] * cp;
+        for (int r = 0; r < 8; ++r) As[buf][ak][ai + 16 * r] = rd[r] * ca + rg[r] * cp;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) Bs[buf][bk + 4 * r][bj] = rb[r];
+        for (int r = 0; r < BR; ++r) Bs[buf][bk + BSTEP * r][bj] = rb[r];
     };
 
-    f16v acc;
+    f16v acc[NACC];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int n = 0; n < NACC; ++n)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
 
     if (nchunk > 0) {
         fetch(0);
         stage(0);
         __syncthreads();
+        const int kr = lane >> 5;
+        const int ia = wr * 32 + (lane & 31);
+        const int jb = wc * (TJ / 2) + (lane & 31);
         for (int c = 0; c < nchunk; ++c) {
             const int buf = c & 1;
             if (c + 1 < nchunk) fetch(c + 1);
-            const int kr = lane >> 5;
-            const int ia = wr * 32 + (lane & 31);
-            const int jb = wc * 32 + (lane & 31);
 #pragma unroll
             for (int q = 0; q < kKC / 2; ++q) {
                 const float a = As[buf][2 * q + kr][ia];
-                const float bb = Bs[buf][2 * q + kr][jb];
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc, 0, 0, 0);
+#pragma unroll
+                for (int n = 0; n < NACC; ++n) {
+                    const float bb = Bs[buf][2 * q + kr][jb + 32 * n];
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc[n], 0, 0, 0);
+                }
             }
             if (c + 1 < nchunk) stage(buf ^ 1);
             __syncthreads();
         }
     }
 
-    // epilogue: lane holds rows 8(r/4) + 4(lane/32) + r%4 and column lane%32 of
-    // its wave's 32 x 32 sub-tile
+    // epilogue: accumulator n of a lane holds rows 8(r/4) + 4(lane/32) + r%4 and
+    // column 32n + lane%32 of its wave's sub-tile
     double sq = 0.0;
     int bad = 0;
-    const int jw = j0 + wc * 32 + (lane & 31);
     const float* base = A.base + A.boff[b];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = i0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= N || jw >= bn) continue;
-        float v = acc[r] * A.dt;
-        if (row >= s && row < s + bn) v = base[static_cast<size_t>(row - s) * bn + jw] + v;
-        if (A.sanitize) {
-            if (!isfinite(v)) {
-                v = 0.f;
-                bad = 1;
+    for (int n = 0; n < NACC; ++n) {
+        const int jw = j0 + wc * (TJ / 2) + 32 * n + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = i0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (row >= N || jw >= bn) continue;
+            float v = acc[n][r] * A.dt;
+            if (row >= s && row < s + bn) v = base[static_cast<size_t>(row - s) * bn + jw] + v;
+            if (A.sanitize) {
+                if (!isfinite(v)) {
+                    v = 0.f;
+                    bad = 1;
+                }
+                sq += static_cast<double>(v) * v;
             }
-            sq += static_cast<double>(v) * v;
+            A.out[static_cast<size_t>(row) * N + s + jw] = v;
         }
-        A.out[static_cast<size_t>(row) * N + s + jw] = v;
     }
     if (A.sanitize) {
         for (int o = 32; o > 0; o >>= 1) {
@@ -206,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void k_rp_corr(ReplayCorrArgs A) {
         if (tid == 0) {
             double t = 0.0;
             int f = 0;
-            for (int w = 0; w < kThreads / 64; ++w) {
+            for (int w = 0; w < kCorrThreads / 64; ++w) {
                 t += red_s[w];
                 f |= red_f[w];
             }
@@ -215,6 +236,16 @@ __global__ __launch_bounds__(kThreads) void k_rp_corr(ReplayCorrArgs A) {
             A.flag_part[wg] = f;
         }
     }
+}
+
+// G[i][c] = D[i][pre(c)] (0 without a pre column): the column-gathered copy of
+// a new history slice, so the correction reads both operands row-contiguous.
+__global__ void k_rp_pregather(const float* D, const int* pre, int N, float* G) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= N) return;
+    const size_t row = static_cast<size_t>(blockIdx.y) * N;
+    const int p = pre[c];
+    G[row + c] = p >= 0 ? D[row + p] : 0.f;
 }
 
 // ---------------------------------------------------------------- clip
@@ -348,8 +379,16 @@ void launch_rp_base(const ReplayBaseArgs& a, int nblk, int max_bn, hipStream_t s
 
 int rp_corr_row_tiles(int N) { return (N + kTI - 1) / kTI; }
 
-void launch_rp_corr(const ReplayCorrArgs& a, int ntiles, hipStream_t s) {
-    hipLaunchKernelGGL(k_rp_corr, dim3(ntiles, rp_corr_row_tiles(a.N)), dim3(kThreads), 0, s, a);
+void launch_rp_corr(const ReplayCorrArgs& a, int ntiles, int tile_cols, hipStream_t s) {
+    const dim3 grid(ntiles, rp_corr_row_tiles(a.N));
+    if (tile_cols == 128)
+        hipLaunchKernelGGL(k_rp_corr<128>, grid, dim3(kCorrThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_rp_corr<64>, grid, dim3(kCorrThreads), 0, s, a);
+}
+
+void launch_rp_pregather(const float* D, const int* pre, int N, float* G, hipStream_t s) {
+    hipLaunchKernelGGL(k_rp_pregather, dim3((N + kThreads - 1) / kThreads, N), dim3(kThreads), 0, s, D, pre, N, G);
 }
 
 void launch_rp_clip(const double* part, const int* flag, int n, float thr, float* gs, float* slot_scale, int R,

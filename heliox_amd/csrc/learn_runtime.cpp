@@ -127,13 +127,16 @@ int LearnRuntime::set_dense_blocks(int nblk, const float* const* data, const int
                         kt1[koff + tau * plane + static_cast<size_t>(i) * n + j] = v;
                         kt2[koff + tau * plane + static_cast<size_t>(j) * n + i] = v;
                     }
-            for (int j0 = 0; j0 < n; j0 += 64) tiles_.push_back(make_int2(b, j0));
             start += n;
             koff += static_cast<long long>(plane) * kl;
             boff += static_cast<long long>(plane);
         }
         k_len_ = kl;
         nblk_ = nblk;
+        // column tile of the correction GEMM: 128 when a block is wider than 64
+        tile_cols_ = max_bn_ > 64 ? 128 : 64;
+        for (int b = 0; b < nblk; ++b)
+            for (int j0 = 0; j0 < bn_[b]; j0 += tile_cols_) tiles_.push_back(make_int2(b, j0));
         d_kt1_ = lupload(blk_mem_, kt1.data(), kt1.size());
         d_kt2_ = lupload(blk_mem_, kt2.data(), kt2.size());
         d_koff_ = lupload(blk_mem_, koff_.data(), koff_.size());
@@ -272,11 +275,12 @@ int LearnRuntime::replay(const ReplayIn& in) {
         const size_t slice = static_cast<size_t>(N) * N;
         const int ntiles = static_cast<int>(tiles_.size());
         const int nwg = ntiles * rp_corr_row_tiles(N);
-        const std::vector<long long> key = {N, R, ks, in.n_out, in.n_in, nwg};
+        const std::vector<long long> key = {N, R, ks, in.n_out, in.n_in, nwg, in.percise ? 1 : 0};
         if (key != ws_key_) {
             free_all(ws_mem_);
             ws_key_.clear();
             ws_.hist = lalloc<float>(ws_mem_, slice * R);
+            ws_.ghist = in.percise ? lalloc<float>(ws_mem_, slice * R) : nullptr;
             ws_.slot_scale = lalloc<float>(ws_mem_, R);
             ws_.gs = lalloc<float>(ws_mem_, 1);
             ws_.tick_scale = lalloc<float>(ws_mem_, 1);
@@ -293,6 +297,7 @@ int LearnRuntime::replay(const ReplayIn& in) {
             ws_key_ = key;
         }
         float* hist = ws_.hist;
+        float* ghist = ws_.ghist;
         float* slot_scale = ws_.slot_scale;
         float* gs = ws_.gs;
         float* tick_scale = ws_.tick_scale;
@@ -313,6 +318,7 @@ int LearnRuntime::replay(const ReplayIn& in) {
         if (need_dx) LRC(hipMemcpyAsync(pin, in.pin, sizeof(int) * in.n_in, hipMemcpyHostToDevice, stream_));
 
         launch_fill_f32(hist, 0.f, static_cast<long long>(slice), stream_);      // slot 0: tick 0
+        if (in.percise) launch_fill_f32(ghist, 0.f, static_cast<long long>(slice), stream_);
         launch_fill_f32(slot_scale, 1.f, R, stream_);
         launch_fill_f32(gs, static_cast<float>(in.grad_scale), 1, stream_);
         launch_fill_f32(tick_scale, 1.f, 1, stream_);
@@ -358,6 +364,7 @@ int LearnRuntime::replay(const ReplayIn& in) {
 
             ReplayCorrArgs C{};
             C.hist = hist;
+            C.ghist = ghist;
             C.slice = static_cast<long long>(slice);
             C.slot_scale = slot_scale;
             C.R = R;
@@ -386,12 +393,13 @@ int LearnRuntime::replay(const ReplayIn& in) {
                 LRC(hipEventCreate(&a));
                 LRC(hipEventCreate(&b));
                 LRC(hipEventRecord(a, stream_));
-                launch_rp_corr(C, ntiles, stream_);
+                launch_rp_corr(C, ntiles, tile_cols_, stream_);
                 LRC(hipEventRecord(b, stream_));
                 evs.push_back({a, b});
             } else {
-                launch_rp_corr(C, ntiles, stream_);
+                launch_rp_corr(C, ntiles, tile_cols_, stream_);
             }
+            if (in.percise) launch_rp_pregather(out, pre, N, ghist + static_cast<size_t>(cur) * slice, stream_);
             if (due) launch_rp_clip(norm_part, flag_part, nwg, thr, gs, slot_scale, R, tick_scale, stream_);
             launch_rp_wtick(out, slot_scale, cur, N, po, in.n_out, dl + static_cast<size_t>(t_lr - 1) * in.n_out,
                             due ? 1 : 0, tick_scale, w_tick, dw_acc, stream_);
