@@ -122,17 +122,20 @@ public:
         std::vector<int> dest;
         std::vector<float> scale;
     };
-    // T <= 0 derives T = (nsample - 1) / k_mul + 1.  to_host captures into
-    // session buffers that end_capture copies out (the _into variant), leaving
-    // the cache untouched.
+    // Where a capture's signals go: the cache that cached replays read, host
+    // buffers given to end_capture (the _into variant), or a private set kept for
+    // one streaming replay.  Only CACHE touches the cache.
+    enum Sink { SINK_CACHE = 0, SINK_HOST, SINK_STREAM };
+    // T <= 0 derives T = (nsample - 1) / k_mul + 1.
     void begin_capture(int nsample, const std::vector<double*>& out_ptr, int N, int T, int k_mul, bool percise,
-                       const Channel* ch, int nch, bool to_host);
+                       const Channel* ch, int nch, Sink sink);
     bool capturing() const { return capturing_; }
     void sample();                                   // one record point
     void end_capture(float* out_vs_host, float* const* sig_host = nullptr);
 
-    // Replay over the cached capture (cached = true) or over host signals loaded
-    // by load_signals (cached = false).
+    // Replay over the cached capture, host signals loaded by load_signals, or the
+    // last streaming capture; the clip schedule follows the entry point.
+    enum Source { SRC_CACHE = 0, SRC_HOST, SRC_STREAM };
     struct ReplayIn {
         const float* dl = nullptr;   // (ksteps, n_out)
         int ksteps = 0, n_out = 0, n_in = 0;
@@ -144,7 +147,8 @@ public:
         double dt = 0, grad_scale = 1, eps = 1e-6, thr = 1e6;
         bool percise = false;
         int clip_strategy = 1, clip_every = 1;
-        bool cached = true;
+        Source source = SRC_CACHE;
+        bool cached_clip_rule = true;   // strategy 1 every tick, others every clip_every
     };
     int replay(const ReplayIn& in);
     int load_signals(const float* it_nt, const float* dv_nt, const float* dp_nt, int N, int T, bool percise);
@@ -180,7 +184,10 @@ private:
     // capture session
     bool capturing_ = false;
     int sample_ = 0, nsample_ = 0, kmul_ = 1, sess_T_ = 0;
-    bool to_host_ = false;
+    Sink sink_ = SINK_CACHE;
+    std::vector<void*> sess_sig_mem_;   // HOST / STREAM signal buffers
+    float* d_stream_[kLrMaxChannels] = {nullptr, nullptr, nullptr};
+    int stream_N_ = 0, stream_T_ = 0;
     CaptureArgs cargs_{};
     std::vector<void*> sess_mem_;
     // host-loaded signals (T, N)

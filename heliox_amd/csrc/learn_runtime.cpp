@@ -153,8 +153,11 @@ int LearnRuntime::set_dense_blocks(int nblk, const float* const* data, const int
 }
 
 void LearnRuntime::begin_capture(int nsample, const std::vector<double*>& out_ptr, int N, int T, int k_mul,
-                                 bool percise, const Channel* ch, int nch, bool to_host) {
+                                 bool percise, const Channel* ch, int nch, Sink sink) {
     free_all(sess_mem_);
+    free_all(sess_sig_mem_);
+    for (int c = 0; c < kLrMaxChannels; ++c) d_stream_[c] = nullptr;
+    stream_N_ = stream_T_ = 0;
     cargs_ = CaptureArgs{};
     cargs_.n_out = static_cast<int>(out_ptr.size());
     cargs_.out_ptr = lupload(sess_mem_, out_ptr.data(), out_ptr.size());
@@ -164,14 +167,14 @@ void LearnRuntime::begin_capture(int nsample, const std::vector<double*>& out_pt
     nsample_ = nsample;
     sample_ = 0;
     kmul_ = k_mul;
-    to_host_ = to_host;
+    sink_ = sink;
     sess_T_ = 0;
     if (N > 0) {
         if (T <= 0) T = (nsample - 1) / k_mul + 1;
         sess_T_ = T;
         float* buf[kLrMaxChannels] = {nullptr, nullptr, nullptr};
-        if (to_host) {
-            for (int c = 0; c < nch; ++c) buf[c] = lalloc<float>(sess_mem_, static_cast<size_t>(T) * N);
+        if (sink != SINK_CACHE) {
+            for (int c = 0; c < nch; ++c) buf[c] = lalloc<float>(sess_sig_mem_, static_cast<size_t>(T) * N);
         } else {
             if (cap_N_ != N || cap_T_ != T || cap_kmul_ != k_mul || cap_percise_ != percise) {
                 free_all(cap_mem_);
@@ -224,7 +227,7 @@ void LearnRuntime::end_capture(float* out_vs_host, float* const* sig_host) {
     if (out_vs_host && cargs_.n_out > 0)
         LRC(hipMemcpy(out_vs_host, cargs_.out_vs, sizeof(float) * static_cast<size_t>(nsample_) * cargs_.n_out,
                       hipMemcpyDeviceToHost));
-    if (to_host_ && sig_host) {
+    if (sink_ == SINK_HOST && sig_host) {
         const size_t n = static_cast<size_t>(sess_T_) * cargs_.N;
         for (int c = 0; c < kLrMaxChannels; ++c) {
             if (!sig_host[c]) continue;
@@ -233,6 +236,13 @@ void LearnRuntime::end_capture(float* out_vs_host, float* const* sig_host) {
             else
                 std::fill(sig_host[c], sig_host[c] + n, 0.f);
         }
+    }
+    if (sink_ == SINK_STREAM) {
+        for (int c = 0; c < kLrMaxChannels; ++c) d_stream_[c] = c < cargs_.nch ? cargs_.ch[c].buf : nullptr;
+        stream_N_ = cargs_.N;
+        stream_T_ = sess_T_;
+    } else {
+        free_all(sess_sig_mem_);
     }
     free_all(sess_mem_);
 }
@@ -263,9 +273,10 @@ int LearnRuntime::load_signals(const float* it_nt, const float* dv_nt, const flo
 }
 
 int LearnRuntime::replay(const ReplayIn& in) {
-    const int N = in.cached ? cap_N_ : sig_N_;
-    const int T = in.cached ? cap_T_ : sig_T_;
-    float* const* sig = in.cached ? d_cap_ : d_sig_;
+    const int N = in.source == SRC_CACHE ? cap_N_ : in.source == SRC_HOST ? sig_N_ : stream_N_;
+    const int T = in.source == SRC_CACHE ? cap_T_ : in.source == SRC_HOST ? sig_T_ : stream_T_;
+    float* const* sig = in.source == SRC_CACHE ? d_cap_ : in.source == SRC_HOST ? d_sig_ : d_stream_;
+    if (N <= 0 || T != in.ksteps + 1) return fail("replay: no signals of %d ticks", in.ksteps);
     const int K_len = k_len_;
     const int ks = in.ksteps;
     const bool need_dx = in.n_in > 0;
@@ -340,7 +351,7 @@ int LearnRuntime::replay(const ReplayIn& in) {
             float* out = hist + static_cast<size_t>(cur) * slice;
             bool due = false;
             if (in.clip_strategy != 0) {
-                if (in.cached) due = in.clip_strategy == 1 || (t_lr % in.clip_every) == 0;
+                if (in.cached_clip_rule) due = in.clip_strategy == 1 || (t_lr % in.clip_every) == 0;
                 else due = in.clip_strategy == 1 && (t_lr % in.clip_every) == 0;
             }
 

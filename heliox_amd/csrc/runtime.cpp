@@ -2195,7 +2195,7 @@ int hx_simulate_output_vs_into(hx_sim* sim, float* output_vs_tn, int t_steps_plu
     std::vector<double*> outp;
     if (!resolve_handles(sim, fn, "output", n_output, output_v_handles, outp)) return -1;
     LearnRuntime& L = sim->learn_rt();
-    L.begin_capture(t_steps_plus1, outp, 0, 0, 1, false, nullptr, 0, false);
+    L.begin_capture(t_steps_plus1, outp, 0, 0, 1, false, nullptr, 0, LearnRuntime::SINK_CACHE);
     try {
         sim->finitialize(v_init);
         sim->run_steps(total_steps);
@@ -2261,7 +2261,8 @@ int capture_common(hx_sim* sim, const char* fn, float* output_vs_tn, int total_s
         ch[c].scale.assign(sc[c], sc[c] + cnt[c]);
     }
     LearnRuntime& L = sim->learn_rt();
-    L.begin_capture(total_steps_plus1, outp, N, T_into, k_mul, percise != 0, ch, nch, to_host != nullptr);
+    L.begin_capture(total_steps_plus1, outp, N, T_into, k_mul, percise != 0, ch, nch,
+                    to_host ? LearnRuntime::SINK_HOST : LearnRuntime::SINK_CACHE);
     try {
         sim->finitialize(v_init);
         sim->run_steps(total_steps);
@@ -2307,12 +2308,13 @@ int hx_simulate_and_capture_mapped_signals_into(
 
 namespace {
 
-int replay_common(hx_sim* sim, const char* fn, bool cached, const float* dL, int ksteps, int n_output,
+int replay_common(hx_sim* sim, const char* fn, LearnRuntime::Source src, const float* dL, int ksteps, int n_output,
                   const int* poutput, const int* pinput, int n_input, const int* pre_of_col, int n_pre,
                   float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
                   double thr, int clip_strategy, int clip_every) {
     LearnRuntime& L = sim->learn_rt();
     if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
+    const bool cached = src == LearnRuntime::SRC_CACHE;
     const int N = cached ? L.capture_N() : n_pre;
     if (cached) {
         if (L.capture_N() <= 0 || L.capture_T() < 2) return sim->fail("%s: cached capture buffers not initialized", fn);
@@ -2353,7 +2355,8 @@ int replay_common(hx_sim* sim, const char* fn, bool cached, const float* dL, int
     in.percise = percise != 0;
     in.clip_strategy = clip_strategy;
     in.clip_every = std::max(1, clip_every);
-    in.cached = cached;
+    in.source = src;
+    in.cached_clip_rule = src != LearnRuntime::SRC_HOST;
     if (L.replay(in) != 0) return sim->fail("%s: %s", fn, L.err.c_str());
     return 0;
 }
@@ -2367,7 +2370,8 @@ int hx_replay_compute_dw_from_cached_signals_into(hx_sim* sim, const float* dLtd
                                                   int clip_check_every) {
     if (!check_loaded(sim)) return -1;
     API_BEGIN
-    return replay_common(sim, "replay_compute_dw_from_cached_signals_into", true, dLtdv_lr_to, ksteps_total,
+    return replay_common(sim, "replay_compute_dw_from_cached_signals_into", LearnRuntime::SRC_CACHE, dLtdv_lr_to,
+                         ksteps_total,
                          n_output, poutput, nullptr, 0, pre_of_col, n_pre, dw_out_n, nullptr, dt_ms, percise,
                          grad_scale, eps, grad_l2norm_threshold, clip_strategy, clip_check_every);
     API_END
@@ -2383,7 +2387,8 @@ int hx_replay_compute_dw_dx_from_cached_signals_into(hx_sim* sim, const float* d
     if (!check_loaded(sim)) return -1;
     if (n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
     API_BEGIN
-    return replay_common(sim, fn, true, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput, n_input, pre_of_col,
+    return replay_common(sim, fn, LearnRuntime::SRC_CACHE, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput,
+                         n_input, pre_of_col,
                          n_pre, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps, grad_l2norm_threshold,
                          clip_strategy, clip_check_every);
     API_END
@@ -2417,9 +2422,77 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
     if (sum_bn != N) return sim->fail("%s: dense blocks total N mismatch (sum=%d vs N=%d)", fn, sum_bn, N);
     if (L.load_signals(it_lr_nt, ditdv_lr_nt, ditdvpre_lr_nt, N, T, percise != 0) != 0)
         return sim->fail("%s", L.err.c_str());
-    return replay_common(sim, fn, false, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput, n_input, pre_of_col,
+    return replay_common(sim, fn, LearnRuntime::SRC_HOST, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput,
+                         n_input, pre_of_col,
                          N, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps, grad_l2norm_threshold,
                          clip_strategy, clip_check_every);
+    API_END
+}
+
+// LearnRuntime::simulate_and_replay_dw_dx_streaming_into (LearnRuntime.cpp:729-1288): the
+// reference keeps only a K_len ring of signals and replays while it steps; with
+// 288 GB of HBM the whole run's signals are captured first and replayed after,
+// with the same windows, taps and clip schedule as a cached replay.
+int hx_simulate_and_replay_dw_dx_streaming_into(
+    hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total, int n_output, const int* poutput, const int* pinput,
+    int n_input, int N, const int* pre_of_col, float* dw_out_n, float* dx_lr_it, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init, double dt_ms,
+    double grad_scale, double eps, double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    static const char* fn = "simulate_and_replay_dw_dx_streaming_into";
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    LearnRuntime& L = sim->learn_rt();
+    // LearnRuntime.cpp:767-866
+    if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
+    if (k_mul <= 0) return sim->fail("%s: k_mul must be positive", fn);
+    if (!(sim->dt > 0.0)) return sim->fail("%s: invalid dt", fn);
+    if (dt_ms > 0.0 && std::abs(dt_ms - sim->dt) > sim->dt * 0.5)
+        return sim->fail("%s: dt_ms mismatch (dt_ms=%f, sim->dt=%f)", fn, dt_ms, sim->dt);
+    if (clip_check_every <= 0) clip_check_every = 1;
+    if (N <= 0) return sim->fail("%s: pre_of_col must be non-empty", fn);
+    if (n_output <= 0 || n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
+    if (ksteps_total <= 0) return sim->fail("%s: dLtdv_lr_to must have at least 1 tick", fn);
+    if (!dLtdv_lr_to || !poutput || !pinput || !pre_of_col || !dw_out_n || !dx_lr_it)
+        return sim->fail("%s: null pointer input/output", fn);
+    int sum_bn = 0;
+    for (int bn : L.block_sizes()) sum_bn += bn;
+    if (sum_bn != N) return sim->fail("%s: dense block sum mismatch (sum=%d N=%d)", fn, sum_bn, N);
+    const int* hs[3] = {pure_i_handles, didv_handles, didvpre_handles};
+    const int* ds[3] = {pure_i_dest, didv_dest, didvpre_dest};
+    const float* sc[3] = {pure_i_scale, didv_scale, didvpre_scale};
+    const int cnt[3] = {n_pure_i, n_didv, n_didvpre};
+    const char* names[3] = {"pure_i", "didv", "didvpre"};
+    const int nch = percise ? 3 : 1;
+    for (int c = 0; c < nch; ++c) {
+        if (cnt[c] < 0 || (cnt[c] > 0 && (!hs[c] || !ds[c] || !sc[c])))
+            return sim->fail("%s: %s handles/dest/scale size mismatch", fn, names[c]);
+        for (int i = 0; i < cnt[c]; ++i)
+            if (ds[c][i] < 0 || ds[c][i] >= N)
+                return sim->fail("%s: %s_dest out of range at %d (%d)", fn, names[c], i, ds[c][i]);
+    }
+    const int total_steps = ksteps_total * k_mul;
+    if (!check_tstop(sim, fn, total_steps, tstop_ms)) return -1;
+    LearnRuntime::Channel ch[3];
+    for (int c = 0; c < nch; ++c) {
+        if (!resolve_handles(sim, fn, names[c], cnt[c], hs[c], ch[c].ptr)) return -1;
+        ch[c].dest.assign(ds[c], ds[c] + cnt[c]);
+        ch[c].scale.assign(sc[c], sc[c] + cnt[c]);
+    }
+    L.begin_capture(total_steps + 1, {}, N, ksteps_total + 1, k_mul, percise != 0, ch, nch,
+                    LearnRuntime::SINK_STREAM);
+    try {
+        sim->finitialize(v_init);
+        sim->run_steps(total_steps);
+    } catch (...) {
+        L.end_capture(nullptr);
+        throw;
+    }
+    L.end_capture(nullptr);
+    return replay_common(sim, fn, LearnRuntime::SRC_STREAM, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput,
+                         n_input, pre_of_col, N, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps,
+                         grad_l2norm_threshold, clip_strategy, clip_check_every);
     API_END
 }
 

@@ -113,6 +113,10 @@ SIGNATURES = {
     "hx_replay_compute_dw_dx_from_signals_into": (
         C.c_int, [_P, _F, _F, _F, C.c_int, C.c_int, _F, C.c_int, C.c_int, _I, _I, C.c_int, _I, _F, _F, C.c_double,
                   C.c_int, C.c_double, C.c_double, C.c_double, C.c_int, C.c_int]),
+    "hx_simulate_and_replay_dw_dx_streaming_into": (
+        C.c_int, [_P, _F, C.c_int, C.c_int, _I, _I, C.c_int, C.c_int, _I, _F, _F, C.c_int, _I, _I, _F, C.c_int, _I,
+                  _I, _F, C.c_int, _I, _I, _F, C.c_double, C.c_int, C.c_int, C.c_double, C.c_double, C.c_double,
+                  C.c_double, C.c_double, C.c_int, C.c_int]),
     "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
@@ -620,6 +624,34 @@ class Sim:
             self._h, _fp(it), _fp(dv) if dv is not None else null, _fp(dp) if dp is not None else null, N, T,
             _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, _ip(pre), _fp(dw), _fp(dx), dt_ms,
             int(bool(percise)), grad_scale, eps, grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))
+
+    def simulate_and_replay_dw_dx_streaming_into(self, dLtdv_lr_ot, poutput, pinput, pre_of_col, dw_out_n, dx_lr_it,
+                                                 pure_i_handles, pure_i_dest, pure_i_scale, didv_handles, didv_dest,
+                                                 didv_scale, didvpre_handles, didvpre_dest, didvpre_scale,
+                                                 tstop_ms: float, k_mul: int, percise: bool, v_init: float,
+                                                 dt_ms: float, grad_scale: float = 1.0, eps: float = 1e-6,
+                                                 grad_l2norm_threshold: float = 1e6, clip_strategy: int = 1,
+                                                 clip_check_every: int = 1) -> int:
+        self._py_err = None
+        dl = _f32(dLtdv_lr_ot, 2)
+        po, pin, pre = _i32(poutput), _i32(pinput), _i32(pre_of_col)
+        dw = _out_f32(dw_out_n, "dw_out_n")
+        dx = _out_f32(dx_lr_it, "dx_lr_it")
+        if dw.size != pre.size or dx.shape != (pin.size, dl.shape[0]):
+            return self._pyfail("simulate_and_replay_dw_dx_streaming_into: output shape mismatch")
+        try:
+            ch = [self._channel(pure_i_handles, pure_i_dest, pure_i_scale),
+                  self._channel(didv_handles, didv_dest, didv_scale),
+                  self._channel(didvpre_handles, didvpre_dest, didvpre_scale)]
+        except ValueError as e:
+            return self._pyfail(f"simulate_and_replay_dw_dx_streaming_into: {e}")
+        args = []
+        for h, d, sc in ch:
+            args += [h.size, _ip(h), _ip(d), _fp(sc)]
+        return self._rc(lib().hx_simulate_and_replay_dw_dx_streaming_into(
+            self._h, _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, pre.size, _ip(pre), _fp(dw),
+            _fp(dx), *args, tstop_ms, int(k_mul), int(bool(percise)), v_init, dt_ms, grad_scale, eps,
+            grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))
 
     def set_replay_timing(self, enable: bool) -> None:
         self._chk(lib().hx_set_replay_timing(self._h, int(bool(enable))), "set_replay_timing")

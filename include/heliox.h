@@ -218,6 +218,17 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
                                               int n_input, const int* pre_of_col, float* dw_out_n, float* dx_lr_it,
                                               double dt_ms, int percise, double grad_scale, double eps,
                                               double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
+/* LearnRuntime::simulate_and_replay_dw_dx_streaming_into (LearnRuntime.cpp:729-1288):
+ * finitialize(v_init), ksteps_total * k_mul steps with the mapped channels captured every
+ * k_mul steps into N columns, then the replay (cached clip schedule) into dw_out_n[N] and
+ * dx_lr_it[(n_input, ksteps_total)].  dt_ms > 0 must match the model's dt. */
+int hx_simulate_and_replay_dw_dx_streaming_into(
+    hx_sim* sim, const float* dLtdv_lr_to, int ksteps_total, int n_output, const int* poutput, const int* pinput,
+    int n_input, int N, const int* pre_of_col, float* dw_out_n, float* dx_lr_it, int n_pure_i,
+    const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
+    const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
+    const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init, double dt_ms,
+    double grad_scale, double eps, double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
 /* Timing of the replay's correction-GEMM launches with HIP events on the library stream
  * (no counterpart in the reference; used by the benchmark). */
 int hx_set_replay_timing(hx_sim* sim, int enable);

@@ -159,6 +159,19 @@ def test_cached_capture_and_replay_match_oracle(sim):
     dw_only = learn.replay_dw_from_cached_signals(g, dLtdv_lr_ot=dL, poutput=po, pre_of_col=pre, dt_ms=0.1,
                                                   percise=True, eps=eps)
     assert np.array_equal(dw_only, grads.dw_out_n)
+    # the streaming entry point (its own capture, then the replay) reproduces the
+    # cached capture + replay exactly
+    dw_c = np.zeros(nsyn, np.float32)
+    dx_c = np.zeros((pin.size, T - 1), np.float32)
+    assert g.replay_compute_dw_dx_from_cached_signals_into(dL, po, pin, pre, dw_c, dx_c, spec.dt, True,
+                                                          eps=eps) == 0, g.last_error()
+    dw_s = np.zeros(nsyn, np.float32)
+    dx_s = np.zeros((pin.size, T - 1), np.float32)
+    assert g.simulate_and_replay_dw_dx_streaming_into(
+        dL, po, pin, pre, dw_s, dx_s, hp, dest, scale, hd, dest, np.ones(nsyn, np.float32), hq, dest,
+        np.full(nsyn, 1e-3, np.float32), total * spec.dt, k_mul, True, -65.0, spec.dt, eps=eps) == 0, g.last_error()
+    assert np.array_equal(dw_s, dw_c) and np.array_equal(dx_s, dx_c)
+    assert np.count_nonzero(dw_s) > 0
 
 
 def test_full_size_rows_match_oracle(sim):
