@@ -241,6 +241,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--train", action="store_true", help="time the config-5 training step instead")
     ap.add_argument("--train-cells", type=int, default=1000)
+    ap.add_argument("--cell-groups", type=int, default=0,
+                    help="cell groups issued on separate streams (0: the library's choice, 1: one stream)")
     ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
     ap.add_argument("--lrds-n", type=int, default=2048)
     ap.add_argument("--lrds-ticks", type=int, default=256)
@@ -273,8 +275,10 @@ def main():
     tstop_needed = (args.warmup + args.steps + 10) * 0.025
     spec = build_config(3, args.ncell, tstop_needed)
     sim = Sim()
+    sim.set_cell_groups(args.cell_groups)
     sim.load_model_from_spec(spec)
     t_build = time.perf_counter() - t_build
+    groups = sim.info("cell_groups")
     nnode = spec.nnode
     dt = spec.dt
 
@@ -299,14 +303,17 @@ def main():
             kernels[k] = {"ms_total": ms, "launches": n, "us_per_launch": ms * 1e3 / n}
     roofline = None
     if "mech" in kernels:
+        # each step runs the node kernel once per cell group; a launch covers
+        # nnode / groups compartments on average
         per_launch_s = kernels["mech"]["ms_total"] / kernels["mech"]["launches"] / 1e3
-        alg = MECH_BYTES_PER_COMP * nnode
+        alg = MECH_BYTES_PER_COMP * nnode / groups
         achieved = alg / per_launch_s / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profiles(),
                     "kernel": "k_dense (fused hh/pas/Ih/Ca_HVA/CaDynamics_E2 state+current)",
                     "alg_bytes_per_launch": alg}
     print(json.dumps({"kernel_times": kernels, "build_s": round(t_build, 2), "nnode": nnode,
+                      "cell_groups": groups, "multi_stream": sim.info("multi_stream"),
                       "spikes": sim.spikes()[0].size, "t_end": sim.get_t()}), file=sys.stderr)
 
     cpu = None
@@ -329,7 +336,7 @@ def main():
         "config": {"workload": f"config 3: {args.ncell} pyramidal-like cells x 5000 compartments, fp64, "
                                f"hh+pas+Ih+Ca_HVA+CaDynamics_E2 everywhere, 200 Exp2Syn/cell with 5 Hz "
                                f"Poisson VecStim input, dt 0.025 ms",
-                   "ncell": args.ncell, "compartments": nnode, "dt_ms": dt,
+                   "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "roofline": roofline,
         "cpu_baseline": cpu,

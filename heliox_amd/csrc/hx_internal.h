@@ -71,7 +71,9 @@ struct MechConsts {
 };
 
 struct StepArgs {
-    int N;                        // nodes
+    int N;                        // node kernels cover nodes [node0, N)
+    int node0;                    // first node (a cell group's range; 0 for the whole model)
+    int pt0, pt1;                 // synapse-decay launches cover instances [pt0, min(pt1, n))
     double* v;
     double* d;
     double* rhs;
@@ -199,7 +201,8 @@ struct DeliverArgs {
     const double* es_weight;
     const double* e2_weight;
     int* log_count;               // when set: ExpSyn instances receiving an event are appended
-    int* log;                     // to log[0 .. *log_count) (capacity ring.cap), for the adjoint
+    int* log;                     // to log[0 .. *log_count) (capacity log_cap), for the adjoint
+    int log_cap;
 };
 
 // One backward step of the adjoint (adjoint.hip).  v1, x0, geff: the taped

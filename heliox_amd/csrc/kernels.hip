@@ -21,6 +21,8 @@
 //   k_input ........ VecStim trains (sorted on the host) entering the ring
 //   k_deliver ...... NET_RECEIVE of the events due this step
 //   k_vecplay, k_record, k_gap, init kernels.
+#include <algorithm>
+
 #include "hx_internal.h"
 #include "mech_math.h"
 #include "solve_chunk.h"
@@ -199,7 +201,7 @@ __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, 
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     __shared__ int s_first[kBlock], s_last[kBlock];
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int i = A.node0 + blockIdx.x * blockDim.x + threadIdx.x;
     const bool live = i < A.N;
     const double v = live ? A.v[i] : 0.0;
     const MechDev& na = A.m[M_NA_ION];
@@ -267,8 +269,8 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
 template <int MECH>
 __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
     const MechDev& m = A.m[MECH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
+    const int j = A.pt0 + blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n || j >= A.pt1) return;
     const int node = m.node[j];
     const double v = A.v[node];
     if (MECH == M_NA_ION || MECH == M_K_ION || MECH == M_CA_ION) {
@@ -358,7 +360,7 @@ template <int MECH>
 __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, double v, int* s_first,
                                            int* s_last, double& rhs, double& d) {
     const MechDev& m = A.m[MECH];
-    const int b0 = blockIdx.x * kBlock;
+    const int b0 = A.node0 + blockIdx.x * kBlock;   // blk_begin covers the launch's blocks
     const int s0 = m.blk_begin[blockIdx.x], s1 = m.blk_begin[blockIdx.x + 1];
     if (s1 == s0) return;                        // same for the whole block
     const int t = threadIdx.x;
@@ -413,8 +415,8 @@ __global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
 template <int MECH>
 __global__ void __launch_bounds__(kBlock) k_point_state(StepArgs A) {
     const MechDev& m = A.m[MECH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
+    const int j = A.pt0 + blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n || j >= A.pt1) return;
     if (MECH == M_EXPSYN) {
         double* g = m.col(ES_G);
         g[j] = expsyn_decay(g[j], m.col(ES_TAU)[j], A.dt);
@@ -896,7 +898,7 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
             if (D.log) {
                 const int pos = atomicAdd(D.log_count, 1);
-                if (pos < D.ring.cap) D.log[pos] = inst;
+                if (pos < D.log_cap) D.log[pos] = inst;
             }
         } else {                                // Exp2Syn: A,B += w * factor
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
@@ -985,12 +987,12 @@ inline dim3 grid_for(long long n, int block = kBlock) {
 // launch wrappers
 // ---------------------------------------------------------------------------
 void launch_dense(const StepArgs& a, hipStream_t s) {
-    if (a.N <= 0) return;
-    hipLaunchKernelGGL(k_dense, grid_for(a.N), dim3(kBlock), 0, s, a);
+    if (a.N - a.node0 <= 0) return;
+    hipLaunchKernelGGL(k_dense, grid_for(a.N - a.node0), dim3(kBlock), 0, s, a);
 }
 
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s) {
-    const int n = a.m[mech].n;
+    const int n = std::min(a.m[mech].n, a.pt1) - a.pt0;
     if (n <= 0) return;
     switch (mech) {
         case M_PAS: hipLaunchKernelGGL(k_sparse<M_PAS>, grid_for(n), dim3(kBlock), 0, s, a); break;
@@ -1018,7 +1020,7 @@ void launch_point_current(int mech, const StepArgs& a, hipStream_t s) {
 }
 
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s) {
-    const int n = a.m[mech].n;
+    const int n = std::min(a.m[mech].n, a.pt1) - a.pt0;
     if (n <= 0) return;
     if (mech == M_EXPSYN) hipLaunchKernelGGL(k_point_state<M_EXPSYN>, grid_for(n), dim3(kBlock), 0, s, a);
     if (mech == M_EXP2SYN) hipLaunchKernelGGL(k_point_state<M_EXP2SYN>, grid_for(n), dim3(kBlock), 0, s, a);

@@ -20,6 +20,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <limits>
 #include <map>
 #include <memory>
 #include <numeric>
@@ -218,24 +219,53 @@ struct hx_sim {
     ChunkDesc* d_desc = nullptr;
     // spikes / events
     int npre = 0;
+    std::vector<int> h_pre_node_dev;          // solver-order node of each device detector
+    bool pre_fanout_empty = true;             // no netcon is driven by a detector
+    std::vector<int> syn_node[2];             // solver-order node of each ExpSyn / Exp2Syn instance
+    std::vector<int> inst_node[M_COUNT];      // the same for every mechanism outside the node kernel
     int *d_pre_node = nullptr, *d_pre_flag = nullptr, *d_pre_gid = nullptr;
     double* d_pre_thr = nullptr;
     int *d_pre_fo_begin = nullptr, *d_pre_fo_target = nullptr;
     double* d_pre_fo_delay = nullptr;
-    int *d_vs_fo_begin = nullptr, *d_vs_fo_target = nullptr;
-    double* d_vs_fo_delay = nullptr;
     double *d_es_weight = nullptr, *d_e2_weight = nullptr;
-    EventRing ring{};
     double max_delay = 0;
     double* d_spk_t = nullptr;
     int* d_spk_gid = nullptr;
     int* d_spk_count = nullptr;
     int spk_cap = 0;
-    double* d_in_time = nullptr;
-    int* d_in_inst = nullptr;
-    int* d_in_cursor = nullptr;
-    int n_in = 0;
     bool inputs_dirty = true;
+    // Cell groups.  Cells are split into contiguous groups, each with its own
+    // event ring, VecStim input list and fan-out (targets inside the group).
+    // When nothing couples the groups (no detector netcons, gaps or VecPlay,
+    // every density mechanism in the node kernel, synapses folded) and the run
+    // allows it, each group's step chain -- events, node kernel, solve,
+    // detection, synapse decay -- is issued on a stream of its own, so one
+    // group's latency-bound solve overlaps another group's HBM-bound node pass.
+    struct CellGroup {
+        int node0 = 0, node1 = 0, cell0 = 0, cell1 = 0;
+        int pre0 = 0, pre1 = 0;                   // detectors (sorted by node)
+        int es0 = 0, es1 = 0, e20 = 0, e21 = 0;   // ExpSyn / Exp2Syn instances
+        int inst0[M_COUNT] = {}, inst1[M_COUNT] = {};   // instances of mechanisms outside the node kernel
+        int* d_blk_es = nullptr;                  // fold tables over the group's node blocks
+        int* d_blk_e2 = nullptr;
+        EventRing ring{};
+        double* d_in_time = nullptr;
+        int* d_in_inst = nullptr;
+        int* d_in_cursor = nullptr;
+        int n_in = 0;
+        int *d_vs_fo_begin = nullptr, *d_vs_fo_target = nullptr;
+        double* d_vs_fo_delay = nullptr;
+        std::vector<char> vs_used;                // VecStim instance has a target in the group
+        int mon0 = 0, mon1 = 0;                   // monitor buffer columns of the group
+        hipStream_t s = nullptr;
+        hipEvent_t done = nullptr;
+    };
+    std::vector<CellGroup> groups;                // one group unless the model decouples
+    int group_request = 0;                        // hx_set_cell_groups (0: automatic)
+    bool groups_coupled = true;                   // structural: something couples the groups
+    bool multi_stream = false;                    // the current run issues groups on their streams
+    bool last_multi_stream = false;
+    hipEvent_t ev_main = nullptr;
     // time table
     std::vector<double> ttab;
     double* d_ttab = nullptr;
@@ -251,6 +281,8 @@ struct hx_sim {
     std::vector<std::pair<std::string, std::string>> mon_name;
     std::vector<int> mon_idx;
     std::vector<Ref> mon_ref;
+    std::vector<int> mon_col;       // sample-buffer column of each monitor (grouped by cell group)
+    bool mon_all_v = true;          // every monitor samples a node voltage
     std::vector<std::vector<double>> mon_data;
     double** d_mon_ptr = nullptr;
     double* d_mon_buf = nullptr;
@@ -319,6 +351,11 @@ struct hx_sim {
     ~hx_sim() {
         learn.reset();
         tape_free();
+        for (auto& g : groups) {
+            if (g.done) (void)hipEventDestroy(g.done);
+            if (g.s) (void)hipStreamDestroy(g.s);
+        }
+        if (ev_main) (void)hipEventDestroy(ev_main);
         for (auto& tm : timers)
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
@@ -336,7 +373,7 @@ struct hx_sim {
     }
 
     // ------------------------------------------------------------ timing
-    void tbegin(int id) {
+    void tbegin(int id, hipStream_t on = nullptr) {
         if (!profiling || !(prof_mask & (1u << id))) return;
         Timer& tm = timers[id];
         while (tm.pool.size() < tm.used + 2) {
@@ -344,14 +381,14 @@ struct hx_sim {
             HXC(hipEventCreate(&e));
             tm.pool.push_back(e);
         }
-        HXC(hipEventRecord(tm.pool[tm.used], stream));
+        HXC(hipEventRecord(tm.pool[tm.used], on ? on : stream));
         tm.pending.push_back({static_cast<int>(tm.used), static_cast<int>(tm.used + 1)});
         tm.used += 2;
     }
-    void tend(int id) {
+    void tend(int id, hipStream_t on = nullptr) {
         if (!profiling || !(prof_mask & (1u << id))) return;
         Timer& tm = timers[id];
-        HXC(hipEventRecord(tm.pool[tm.pending.back().second], stream));
+        HXC(hipEventRecord(tm.pool[tm.pending.back().second], on ? on : stream));
     }
     void tcollect() {
         for (auto& tm : timers) {
@@ -377,11 +414,15 @@ struct hx_sim {
     Ref resolve(const std::string& mechname, const std::string& var, int idx);
     StepArgs step_args(double tcur, int do_state, int do_current) const;
     // ------------------------------------------------------------ stepping
-    void launch_mech_pass(int do_state, int do_current, double tcur);
+    void launch_mech_pass(int do_state, int do_current, double tcur, int grp = -1, hipStream_t on = nullptr);
     void launch_point_currents(double tcur);
     void launch_events(int kk, double tk);
+    void launch_events_group(int g, int kk, double tk, hipStream_t on);
     void launch_detect(int kk, double tk);
     void launch_record();
+    void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
+    bool want_multi_stream() const;
+    void step_once_groups();
     void step_once();
     void finish_pending();
     int run_steps(int nstep);
@@ -554,6 +595,10 @@ void hx_sim::upload() {
         std::vector<int> nodes(m.n);
         for (int j = 0; j < m.n; ++j) nodes[j] = node_perm[m.node[m.iperm[j]]];
         d.node = dupload(owned, nodes);
+        if (id == M_EXPSYN) syn_node[0] = nodes;
+        if (id == M_EXP2SYN) syn_node[1] = nodes;
+        inst_node[id].clear();
+        if (!m.dense) inst_node[id] = nodes;
         if (R[id].point && m.n > 0) {
             std::vector<int> gnode, gbeg;
             for (int j = 0; j < m.n; ++j)
@@ -597,13 +642,28 @@ void hx_sim::upload() {
         }
     }
 
-    // spike detectors
+    // spike detectors, in solver-node order so a cell group's detectors are a
+    // contiguous range (the gid travels with each detector)
     npre = static_cast<int>(pre_node.size());
-    std::vector<int> pn(npre);
-    for (int i = 0; i < npre; ++i) pn[i] = node_perm[pre_node[i]];
-    d_pre_node = dupload(owned, pn);
-    d_pre_thr = dupload(owned, pre_thr);
-    d_pre_gid = dupload(owned, pre_gid);
+    std::vector<int> pre_dev(npre), pre_order(npre);
+    std::iota(pre_order.begin(), pre_order.end(), 0);
+    std::stable_sort(pre_order.begin(), pre_order.end(),
+                     [&](int x, int y) { return node_perm[pre_node[x]] < node_perm[pre_node[y]]; });
+    {
+        std::vector<int> pn(npre), pg(npre);
+        std::vector<double> pt(npre);
+        for (int r = 0; r < npre; ++r) {
+            const int u = pre_order[r];
+            pre_dev[u] = r;
+            pn[r] = node_perm[pre_node[u]];
+            pg[r] = pre_gid[u];
+            pt[r] = pre_thr[u];
+        }
+        h_pre_node_dev = pn;
+        d_pre_node = dupload(owned, pn);
+        d_pre_thr = dupload(owned, pt);
+        d_pre_gid = dupload(owned, pg);
+    }
     d_pre_flag = dalloc<int>(owned, npre);
     HXC(hipMemset(d_pre_flag, 0, sizeof(int) * std::max(npre, 1)));
 
@@ -621,46 +681,33 @@ void hx_sim::upload() {
         const int packed = ((nc.mech == M_EXP2SYN ? 1 : 0) << 30) | dinst;
         if (nc.mech == M_EXPSYN) esw[dinst] = nc.weight;
         else e2w[dinst] = nc.weight;
-        if (nc.src_kind == 0) pre_fo[nc.src].push_back({packed, nc.delay});
+        if (nc.src_kind == 0) pre_fo[pre_dev[nc.src]].push_back({packed, nc.delay});
         else vs_fo[nc.src].push_back({packed, nc.delay});
         max_delay = std::max(max_delay, nc.delay);
     }
-    auto csr = [&](const std::vector<std::vector<std::pair<int, double>>>& fo, int*& beg, int*& tgt, double*& dl) {
-        std::vector<int> b(fo.size() + 1, 0), tg;
+    long long ntgt = 0;
+    {
+        std::vector<int> b(pre_fo.size() + 1, 0), tg;
         std::vector<double> de;
-        for (size_t i = 0; i < fo.size(); ++i) {
-            for (auto& pr : fo[i]) { tg.push_back(pr.first); de.push_back(pr.second); }
+        for (size_t i = 0; i < pre_fo.size(); ++i) {
+            for (auto& pr : pre_fo[i]) { tg.push_back(pr.first); de.push_back(pr.second); }
             b[i + 1] = static_cast<int>(tg.size());
         }
-        beg = dupload(owned, b);
-        tgt = dupload(owned, tg);
-        dl = dupload(owned, de);
-        return static_cast<long long>(tg.size());
-    };
-    long long ntgt = csr(pre_fo, d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay);
-    ntgt += csr(vs_fo, d_vs_fo_begin, d_vs_fo_target, d_vs_fo_delay);
+        d_pre_fo_begin = dupload(owned, b);
+        d_pre_fo_target = dupload(owned, tg);
+        d_pre_fo_delay = dupload(owned, de);
+        ntgt += static_cast<long long>(tg.size());
+        pre_fanout_empty = tg.empty();
+    }
     d_es_weight = dupload(owned, esw);
     d_e2_weight = dupload(owned, e2w);
-
-    // event ring: one slot per step, enough slots to cover the longest delay
-    int steps = static_cast<int>(std::ceil(max_delay / dt)) + 4;
-    int nslot = 8;
-    while (nslot < steps) nslot <<= 1;
-    long long cap = event_cap_request > 0 ? event_cap_request : std::max<long long>(4096, std::min<long long>(ntgt, 1 << 20));
-    ring.nslot = nslot;
-    ring.cap = static_cast<int>(cap);
-    ring.count = dalloc<int>(owned, nslot);
-    ring.entry = dalloc<int>(owned, static_cast<size_t>(nslot) * cap);
-    ring.overflow = dalloc<int>(owned, 1);
-    HXC(hipMemset(ring.count, 0, sizeof(int) * nslot));
-    HXC(hipMemset(ring.overflow, 0, sizeof(int)));
 
     spk_cap = std::max(1 << 20, npre * 64);
     d_spk_t = dalloc<double>(owned, spk_cap);
     d_spk_gid = dalloc<int>(owned, spk_cap);
     d_spk_count = dalloc<int>(owned, 1);
     HXC(hipMemset(d_spk_count, 0, sizeof(int)));
-    d_in_cursor = dalloc<int>(owned, 1);
+    build_groups(vs_fo, ntgt);
 
     // gap transfers
     std::vector<int> gs, gi;
@@ -672,6 +719,106 @@ void hx_sim::upload() {
     vecplay_dirty = true;
     mon_dirty = true;
     ttab_cap = 0;
+}
+
+// Cell groups (see CellGroup).  Groups are contiguous cell ranges of about
+// equal node count; each owns the VecStim fan-out into its synapses, an event
+// ring, its detectors and its synapse instances.
+void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt) {
+    for (auto& g : groups) {
+        if (g.done) (void)hipEventDestroy(g.done);
+        if (g.s) (void)hipStreamDestroy(g.s);
+    }
+    groups.clear();
+    const auto& R = registry();
+    bool coupled = !pre_fanout_empty || !gaps.empty();
+    for (int id = 0; id < M_COUNT; ++id) {
+        if (!mech[id].present || mech[id].n == 0) continue;
+        if (id == M_ICLAMP || id == M_HALFGAP) coupled = true;        // point currents outside the node kernel
+    }
+    (void)R;
+    groups_coupled = coupled;
+    int G = 1;
+    if (!coupled) {
+        G = group_request > 0 ? group_request : 2;
+        G = std::min(G, std::max(1, ncell / 8));
+    }
+    // event ring geometry: one slot per step, enough slots to cover the longest delay
+    const int steps = static_cast<int>(std::ceil(max_delay / dt)) + 4;
+    int nslot = 8;
+    while (nslot < steps) nslot <<= 1;
+    groups.resize(G);
+    int c0 = 0;
+    for (int g = 0; g < G; ++g) {
+        CellGroup& cg = groups[g];
+        int c1 = ncell;
+        if (g < G - 1) {
+            const long long target = static_cast<long long>(nnode) * (g + 1) / G;
+            c1 = static_cast<int>(std::lower_bound(cell_node_begin.begin(), cell_node_begin.begin() + ncell, target) -
+                                  cell_node_begin.begin());
+            c1 = std::max(c1, c0 + 1);
+        }
+        cg.cell0 = c0;
+        cg.cell1 = c1;
+        cg.node0 = cell_node_begin[c0];
+        cg.node1 = cell_node_begin[c1];
+        c0 = c1;
+        auto range = [&](const std::vector<int>& nodes, int& b, int& e) {
+            b = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node0) - nodes.begin());
+            e = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node1) - nodes.begin());
+        };
+        range(h_pre_node_dev, cg.pre0, cg.pre1);
+        range(syn_node[0], cg.es0, cg.es1);
+        range(syn_node[1], cg.e20, cg.e21);
+        for (int id = 0; id < M_COUNT; ++id) range(inst_node[id], cg.inst0[id], cg.inst1[id]);
+        // synapse fold tables over the group's node blocks
+        auto fold_table = [&](const std::vector<int>& nodes) {
+            const int nb = (cg.node1 - cg.node0 + kBlock - 1) / kBlock;
+            std::vector<int> bb(nb + 1);
+            for (int b = 0; b < nb; ++b)
+                bb[b] = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node0 + b * kBlock) -
+                                         nodes.begin());
+            bb[nb] = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node1) - nodes.begin());
+            return dupload(owned, bb);
+        };
+        if (!syn_node[0].empty()) cg.d_blk_es = fold_table(syn_node[0]);
+        if (!syn_node[1].empty()) cg.d_blk_e2 = fold_table(syn_node[1]);
+        // VecStim fan-out restricted to the group's synapses
+        std::vector<int> b(vs_fo.size() + 1, 0), tg;
+        std::vector<double> de;
+        cg.vs_used.assign(vs_fo.size(), 0);
+        for (size_t i = 0; i < vs_fo.size(); ++i) {
+            for (auto& pr : vs_fo[i]) {
+                const int type = pr.first >> 30, inst = pr.first & ((1 << 30) - 1);
+                const int node = syn_node[type][inst];
+                if (G > 1 && (node < cg.node0 || node >= cg.node1)) continue;
+                tg.push_back(pr.first);
+                de.push_back(pr.second);
+                cg.vs_used[i] = 1;
+            }
+            b[i + 1] = static_cast<int>(tg.size());
+        }
+        cg.d_vs_fo_begin = dupload(owned, b);
+        cg.d_vs_fo_target = dupload(owned, tg);
+        cg.d_vs_fo_delay = dupload(owned, de);
+        const long long ng = static_cast<long long>(tg.size()) + (g == 0 ? ntgt : 0);
+        const long long cap =
+            event_cap_request > 0 ? event_cap_request : std::max<long long>(4096, std::min<long long>(ng, 1 << 20));
+        cg.ring.nslot = nslot;
+        cg.ring.cap = static_cast<int>(cap);
+        cg.ring.count = dalloc<int>(owned, nslot);
+        cg.ring.entry = dalloc<int>(owned, static_cast<size_t>(nslot) * cap);
+        cg.ring.overflow = dalloc<int>(owned, 1);
+        HXC(hipMemset(cg.ring.count, 0, sizeof(int) * nslot));
+        HXC(hipMemset(cg.ring.overflow, 0, sizeof(int)));
+        cg.d_in_cursor = dalloc<int>(owned, 1);
+        HXC(hipMemset(cg.d_in_cursor, 0, sizeof(int)));
+        if (G > 1) {
+            HXC(hipStreamCreate(&cg.s));
+            HXC(hipEventCreateWithFlags(&cg.done, hipEventDisableTiming));
+        }
+    }
+    if (G > 1 && !ev_main) HXC(hipEventCreateWithFlags(&ev_main, hipEventDisableTiming));
 }
 
 // VecStim trains -> globally sorted effective event times.  A train element is
@@ -689,12 +836,19 @@ void hx_sim::upload_inputs() {
         }
     }
     std::stable_sort(ev.begin(), ev.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
-    std::vector<double> tt(ev.size());
-    std::vector<int> ii(ev.size());
-    for (size_t i = 0; i < ev.size(); ++i) { tt[i] = ev[i].first; ii[i] = ev[i].second; }
-    n_in = static_cast<int>(ev.size());
-    d_in_time = dupload(owned, tt);
-    d_in_inst = dupload(owned, ii);
+    for (auto& cg : groups) {
+        // each group keeps the events of the VecStims that drive its synapses
+        std::vector<double> tt;
+        std::vector<int> ii;
+        for (auto& e : ev)
+            if (e.second < static_cast<int>(cg.vs_used.size()) && cg.vs_used[e.second]) {
+                tt.push_back(e.first);
+                ii.push_back(e.second);
+            }
+        cg.n_in = static_cast<int>(tt.size());
+        cg.d_in_time = dupload(owned, tt);
+        cg.d_in_inst = dupload(owned, ii);
+    }
     inputs_dirty = false;
 }
 
@@ -735,8 +889,37 @@ void hx_sim::upload_vecplay() {
 }
 
 void hx_sim::upload_monitors() {
-    std::vector<double*> ptrs;
-    for (auto& r : mon_ref) ptrs.push_back(r.dev);
+    // sample-buffer columns are ordered by cell group (voltage monitors; the
+    // rest last) so a group records its columns as one contiguous range
+    const int nm = static_cast<int>(mon_ref.size());
+    const int G = static_cast<int>(groups.size());
+    std::vector<int> grp(nm, G);
+    mon_all_v = true;
+    for (int i = 0; i < nm; ++i) {
+        const double* p = mon_ref[i].dev;
+        if (p >= d_v && p < d_v + nnode) {
+            const int node = static_cast<int>(p - d_v);
+            for (int g = 0; g < G; ++g)
+                if (node >= groups[g].node0 && node < groups[g].node1) grp[i] = g;
+        } else {
+            mon_all_v = false;
+        }
+    }
+    std::vector<int> order(nm);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return grp[x] < grp[y]; });
+    mon_col.assign(nm, 0);
+    std::vector<double*> ptrs(nm);
+    for (int q = 0; q < nm; ++q) {
+        mon_col[order[q]] = q;
+        ptrs[q] = mon_ref[order[q]].dev;
+    }
+    for (int g = 0; g < G; ++g) {
+        groups[g].mon0 = static_cast<int>(std::lower_bound(order.begin(), order.end(), g,
+                                                           [&](int m, int gg) { return grp[m] < gg; }) - order.begin());
+        groups[g].mon1 = static_cast<int>(std::lower_bound(order.begin(), order.end(), g + 1,
+                                                           [&](int m, int gg) { return grp[m] < gg; }) - order.begin());
+    }
     d_mon_ptr = dupload(owned, ptrs);
     mon_dirty = false;
 }
@@ -816,6 +999,9 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
 StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     StepArgs A{};
     A.N = nnode;
+    A.node0 = 0;
+    A.pt0 = 0;
+    A.pt1 = std::numeric_limits<int>::max();
     A.v = d_v;
     A.d = d_d;
     A.rhs = d_rhs;
@@ -874,29 +1060,47 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
 // ===========================================================================
 static const int kSparseOrder[] = {M_PAS, M_NA_ION, M_K_ION, M_HH, M_CA_ION, M_CADYN, M_CAHVA, M_HDLA};
 
-void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur) {
+// The mechanism pass over the whole model, or over one cell group (nodes,
+// synapse fold tables and instance ranges of that group) on stream `on`.
+void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp, hipStream_t on) {
     StepArgs A = step_args(tcur, do_state, do_current);
-    tbegin(T_MECH);
-    if (do_current) {
-        launch_dense(A, stream);
-    } else if (dense_mask) {
-        launch_dense(A, stream);
+    const CellGroup* cg = grp >= 0 ? &groups[grp] : nullptr;
+    hipStream_t s = on ? on : stream;
+    if (cg) {
+        A.node0 = cg->node0;
+        A.N = cg->node1;
+        A.m[M_EXPSYN].blk_begin = cg->d_blk_es;
+        A.m[M_EXP2SYN].blk_begin = cg->d_blk_e2;
     }
-    tend(T_MECH);
+    tbegin(T_MECH, s);
+    if (do_current) {
+        launch_dense(A, s);
+    } else if (dense_mask) {
+        launch_dense(A, s);
+    }
+    tend(T_MECH, s);
     bool any_sparse = false;
     for (int id : kSparseOrder) any_sparse |= mech[id].present && !(dense_mask & (1u << id));
     if (!any_sparse) return;
-    tbegin(T_SPARSE);
+    auto sparse = [&](int id) {
+        StepArgs B = A;
+        if (cg) {
+            B.pt0 = cg->inst0[id];
+            B.pt1 = cg->inst1[id];
+        }
+        launch_sparse(id, B, s);
+    };
+    tbegin(T_SPARSE, s);
     if (do_state && !do_current) {
         // ion writers first (simulate.cpp:822-834)
-        if (mech[M_CADYN].present && !(dense_mask & (1u << M_CADYN))) launch_sparse(M_CADYN, A, stream);
+        if (mech[M_CADYN].present && !(dense_mask & (1u << M_CADYN))) sparse(M_CADYN);
         for (int id : kSparseOrder)
-            if (id != M_CADYN && mech[id].present && !(dense_mask & (1u << id))) launch_sparse(id, A, stream);
+            if (id != M_CADYN && mech[id].present && !(dense_mask & (1u << id))) sparse(id);
     } else {
         for (int id : kSparseOrder)
-            if (mech[id].present && !(dense_mask & (1u << id))) launch_sparse(id, A, stream);
+            if (mech[id].present && !(dense_mask & (1u << id))) sparse(id);
     }
-    tend(T_SPARSE);
+    tend(T_SPARSE, s);
 }
 
 void hx_sim::launch_point_currents(double tcur) {
@@ -912,26 +1116,32 @@ void hx_sim::launch_point_currents(double tcur) {
 }
 
 void hx_sim::launch_events(int kk, double tk) {
+    for (int g = 0; g < static_cast<int>(groups.size()); ++g) launch_events_group(g, kk, tk, stream);
+}
+
+// VecStim input and delivery of step kk for one cell group's synapses.
+void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     if (!(mech[M_EXPSYN].present || mech[M_EXP2SYN].present)) return;
-    tbegin(T_EVENTS);
-    if (n_in > 0) {
+    CellGroup& cg = groups[g];
+    tbegin(T_EVENTS, on);
+    if (cg.n_in > 0) {
         InputArgs I{};
-        I.eff_time = d_in_time;
-        I.inst = d_in_inst;
-        I.n = n_in;
-        I.cursor = d_in_cursor;
+        I.eff_time = cg.d_in_time;
+        I.inst = cg.d_in_inst;
+        I.n = cg.n_in;
+        I.cursor = cg.d_in_cursor;
         I.tcut = tk + dt / 2;
         I.t = tk;
         I.k = kk;
-        I.fo = FanOut{d_vs_fo_begin, d_vs_fo_target, d_vs_fo_delay};
-        I.ring = ring;
+        I.fo = FanOut{cg.d_vs_fo_begin, cg.d_vs_fo_target, cg.d_vs_fo_delay};
+        I.ring = cg.ring;
         I.ttab = d_ttab;
         I.kmax = static_cast<int>(ttab.size()) - 1;
         I.half_dt = dt / 2;
-        launch_input(I, stream);
+        launch_input(I, on);
     }
     DeliverArgs D{};
-    D.ring = ring;
+    D.ring = cg.ring;
     D.k = kk;
     D.es = mech[M_EXPSYN].dev;
     D.e2 = mech[M_EXP2SYN].dev;
@@ -940,9 +1150,10 @@ void hx_sim::launch_events(int kk, double tk) {
     if (tape_on && tape_n < tape_cap) {
         D.log_count = d_tape_evn + tape_n;
         D.log = d_tape_ev + static_cast<size_t>(tape_n) * tape_evcap;
+        D.log_cap = tape_evcap;
     }
-    launch_deliver(D, stream);
-    tend(T_EVENTS);
+    launch_deliver(D, on);
+    tend(T_EVENTS, on);
 }
 
 void hx_sim::launch_detect(int kk, double tk) {
@@ -962,7 +1173,7 @@ void hx_sim::launch_detect(int kk, double tk) {
     S.log_count = d_spk_count;
     S.log_cap = spk_cap;
     S.fo = FanOut{d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay};
-    S.ring = ring;
+    S.ring = groups[0].ring;   // detector netcons exist only with a single group
     S.ttab = d_ttab;
     S.kmax = static_cast<int>(ttab.size()) - 1;
     S.half_dt = dt / 2;
@@ -1012,7 +1223,93 @@ void hx_sim::tape_record() {
     ++tape_n;
 }
 
+bool hx_sim::want_multi_stream() const {
+    return groups.size() > 1 && fused && vecplay.empty() && !tape_on && !(learn && learn->capturing()) &&
+           (mon_ref.empty() || mon_all_v);
+}
+
+// One fadvance with each cell group's chain on its own stream: the same
+// launches as step_once, restricted to the group's nodes, cells, detectors and
+// synapses, in the same order.
+void hx_sim::step_once_groups() {
+    const double tk = t;
+    const double tmid = tk + 0.5 * dt;
+    double tn = tk;
+    tn += 0.5 * dt;
+    tn += 0.5 * dt;
+    const bool pending = state_pending;
+    const StepArgs post = step_args(tn, 1, 0);
+    const size_t nm = mon_ref.size();
+    if (pending && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
+        CellGroup& cg = groups[g];
+        hipStream_t s = cg.s;
+        launch_events_group(g, k, tk, s);
+        launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+        if (pending && cg.mon1 > cg.mon0)
+            hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
+        SolveArgs S{};
+        S.ncell = cg.cell1 - cg.cell0;
+        S.cell_node_begin = d_cell_node_begin + cg.cell0;
+        S.cell_desc_begin = d_cell_desc_begin + cg.cell0;
+        S.cell_round_begin = d_cell_round_begin + cg.cell0;
+        S.rounds = d_rounds;
+        S.desc = d_desc;
+        S.v = d_v;
+        S.d = d_d;
+        S.rhs = d_rhs;
+        S.w = d_w;
+        S.a = d_a;
+        S.b = d_b;
+        tbegin(T_SOLVE, s);
+        launch_solve(S, max_slots, s);
+        tend(T_SOLVE, s);
+        if (cg.pre1 > cg.pre0) {
+            tbegin(T_SPIKE, s);
+            SpikeArgs P{};
+            P.npre = cg.pre1 - cg.pre0;
+            P.v = d_v;
+            P.node = d_pre_node + cg.pre0;
+            P.thr = d_pre_thr + cg.pre0;
+            P.flag = d_pre_flag + cg.pre0;
+            P.gid = d_pre_gid + cg.pre0;
+            P.t = tn;
+            P.k = k + 1;
+            P.log_t = d_spk_t;
+            P.log_gid = d_spk_gid;
+            P.log_count = d_spk_count;
+            P.log_cap = spk_cap;
+            P.fo = FanOut{d_pre_fo_begin + cg.pre0, d_pre_fo_target, d_pre_fo_delay};
+            P.ring = cg.ring;
+            P.ttab = d_ttab;
+            P.kmax = static_cast<int>(ttab.size()) - 1;
+            P.half_dt = dt / 2;
+            launch_spike(P, s);
+            tend(T_SPIKE, s);
+        }
+        if (mech[M_EXPSYN].present || mech[M_EXP2SYN].present) {
+            tbegin(T_POINT, s);
+            StepArgs D = post;
+            D.pt0 = cg.es0;
+            D.pt1 = cg.es1;
+            launch_point_state(M_EXPSYN, D, s);
+            D.pt0 = cg.e20;
+            D.pt1 = cg.e21;
+            launch_point_state(M_EXP2SYN, D, s);
+            tend(T_POINT, s);
+        }
+    }
+    if (pending && nm) mon_buf_fill++;
+    t = tn;
+    k += 1;
+    state_pending = true;
+}
+
 void hx_sim::step_once() {
+    if (multi_stream) {
+        step_once_groups();
+        return;
+    }
     const double tk = t;
     const double tmid = tk + 0.5 * dt;
     const bool has_vp = !vecplay.empty();
@@ -1079,6 +1376,20 @@ void hx_sim::step_once() {
 
 void hx_sim::finish_pending() {
     if (!state_pending) return;
+    if (multi_stream) {
+        const size_t nm = mon_ref.size();
+        if (nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+        for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
+            CellGroup& cg = groups[g];
+            launch_mech_pass(1, 0, t, g, cg.s);
+            if (cg.mon1 > cg.mon0)
+                hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0,
+                                  cg.s);
+        }
+        if (nm) mon_buf_fill++;
+        state_pending = false;
+        return;
+    }
     launch_mech_pass(1, 0, t);
     launch_record();
     state_pending = false;
@@ -1087,9 +1398,11 @@ void hx_sim::finish_pending() {
 void hx_sim::sync_outputs() {
     HXC(hipStreamSynchronize(stream));
     if (profiling) tcollect();
-    int ov = 0;
-    HXC(hipMemcpy(&ov, ring.overflow, sizeof(int), hipMemcpyDeviceToHost));
-    if (ov) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
+    for (auto& cg : groups) {
+        int ov = 0;
+        HXC(hipMemcpy(&ov, cg.ring.overflow, sizeof(int), hipMemcpyDeviceToHost));
+        if (ov) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
+    }
     int ns = 0;
     HXC(hipMemcpy(&ns, d_spk_count, sizeof(int), hipMemcpyDeviceToHost));
     if (ns > spk_cap) throw std::runtime_error("spike log overflow");
@@ -1109,7 +1422,7 @@ void hx_sim::sync_outputs() {
         std::vector<double> buf(static_cast<size_t>(mon_buf_fill) * nm);
         HXC(hipMemcpy(buf.data(), d_mon_buf, sizeof(double) * buf.size(), hipMemcpyDeviceToHost));
         for (long long s = 0; s < mon_buf_fill; ++s)
-            for (size_t i = 0; i < nm; ++i) mon_data[i].push_back(buf[s * nm + i]);
+            for (size_t i = 0; i < nm; ++i) mon_data[i].push_back(buf[s * nm + mon_col[i]]);
         mon_buf_fill = 0;
     }
 }
@@ -1129,11 +1442,34 @@ int hx_sim::run_steps(int nstep) {
     // last step of the call stores them all, so they read back as after the
     // reference's last step.
     final_step = false;
-    for (int s = 0; s < nstep; ++s) {
-        final_step = s == nstep - 1;
-        step_once();
+    // cell groups on their own streams: they start after everything already on
+    // the library stream, and the library stream waits for all of them
+    multi_stream = want_multi_stream();
+    last_multi_stream = multi_stream;
+    if (multi_stream) {
+        HXC(hipEventRecord(ev_main, stream));
+        for (auto& cg : groups) HXC(hipStreamWaitEvent(cg.s, ev_main, 0));
     }
-    finish_pending();
+    try {
+        for (int s = 0; s < nstep; ++s) {
+            final_step = s == nstep - 1;
+            step_once();
+        }
+        finish_pending();
+    } catch (...) {
+        if (multi_stream) {
+            for (auto& cg : groups) (void)hipStreamSynchronize(cg.s);
+            multi_stream = false;
+        }
+        throw;
+    }
+    if (multi_stream) {
+        for (auto& cg : groups) {
+            HXC(hipEventRecord(cg.done, cg.s));
+            HXC(hipStreamWaitEvent(stream, cg.done, 0));
+        }
+        multi_stream = false;
+    }
     final_step = false;
     sync_outputs();
     return 0;
@@ -1161,11 +1497,13 @@ void hx_sim::finitialize(double v_init) {
         launch_vecplay_reset(d_vecplay, nvp, stream);
         launch_vecplay(d_vecplay, nvp, 0.0, 1, stream);
     }
-    launch_clear_ints(ring.count, ring.nslot, stream);
-    launch_clear_ints(ring.overflow, 1, stream);
+    for (auto& cg : groups) {
+        launch_clear_ints(cg.ring.count, cg.ring.nslot, stream);
+        launch_clear_ints(cg.ring.overflow, 1, stream);
+        launch_clear_ints(cg.d_in_cursor, 1, stream);
+    }
     launch_clear_ints(d_pre_flag, npre, stream);
     launch_clear_ints(d_spk_count, 1, stream);
-    launch_clear_ints(d_in_cursor, 1, stream);
     if (tape_on) {
         tape_n = 0;
         launch_clear_ints(d_tape_evn, tape_cap, stream);
@@ -1680,6 +2018,13 @@ int hx_set_event_capacity(hx_sim* sim, int per_step) {
     return 0;
 }
 
+int hx_set_cell_groups(hx_sim* sim, int ngroup) {
+    if (sim->loaded) return sim->fail("set the cell groups before hx_load_model");
+    if (ngroup < 0) return sim->fail("group count must be >= 0");
+    sim->group_request = ngroup;
+    return 0;
+}
+
 int hx_set_fusion(hx_sim* sim, int enable) {
     sim->fusion_allowed = enable ? 1 : 0;
     if (sim->loaded) {
@@ -1840,8 +2185,10 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "fused") return sim->fused ? 1 : 0;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
-    if (k == "event_slots") return sim->ring.nslot;
-    if (k == "event_cap") return sim->ring.cap;
+    if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
+    if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
+    if (k == "cell_groups") return static_cast<long long>(sim->groups.size());
+    if (k == "multi_stream") return sim->last_multi_stream ? 1 : 0;
     return -1;
 }
 
@@ -1878,7 +2225,9 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
         HXC(hipMalloc(&sim->d_tape_x, sizeof(double) * cap * 3 * sim->mech[M_HH].dev.stride));
     if (sim->mech[M_EXPSYN].present && sim->mech[M_EXPSYN].n > 0)
         HXC(hipMalloc(&sim->d_tape_g, sizeof(double) * cap * sim->mech[M_EXPSYN].n));
-    sim->tape_evcap = std::max(sim->ring.cap, 1);
+    sim->tape_evcap = 0;
+    for (auto& cg : sim->groups) sim->tape_evcap += cg.ring.cap;   // every group appends to one row per step
+    sim->tape_evcap = std::max(sim->tape_evcap, 1);
     HXC(hipMalloc(&sim->d_tape_evn, sizeof(int) * cap));
     HXC(hipMalloc(&sim->d_tape_ev, sizeof(int) * cap * sim->tape_evcap));
     HXC(hipMemsetAsync(sim->d_tape_evn, 0, sizeof(int) * cap, sim->stream));

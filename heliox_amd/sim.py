@@ -118,6 +118,7 @@ SIGNATURES = {
                   _I, _F, C.c_int, _I, _I, _F, C.c_double, C.c_int, C.c_int, C.c_double, C.c_double, C.c_double,
                   C.c_double, C.c_double, C.c_int, C.c_int]),
     "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
+    "hx_set_cell_groups": (C.c_int, [_P, C.c_int]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
 
@@ -652,6 +653,11 @@ class Sim:
             self._h, _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, pre.size, _ip(pre), _fp(dw),
             _fp(dx), *args, tstop_ms, int(k_mul), int(bool(percise)), v_init, dt_ms, grad_scale, eps,
             grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))
+
+    def set_cell_groups(self, ngroup: int) -> None:
+        """Cell groups issued on separate streams when nothing couples them (0 automatic, 1 off).
+        Call before loading the model."""
+        self._chk(lib().hx_set_cell_groups(self._h, int(ngroup)), "set_cell_groups")
 
     def set_replay_timing(self, enable: bool) -> None:
         self._chk(lib().hx_set_replay_timing(self._h, int(bool(enable))), "set_replay_timing")

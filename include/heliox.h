@@ -125,7 +125,17 @@ int hx_set_profiling(hx_sim* sim, int enable);
  * Fewer timed classes means fewer events on the stream, so less perturbation. */
 int hx_set_profiling_classes(hx_sim* sim, const char* classes);
 int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches);
-/* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused". */
+/* Cell groups (no counterpart in the reference; an MI355X scheduling choice).  When
+ * nothing couples cells across groups -- no detector-driven netcons, gaps or point
+ * currents outside the node kernel, every density mechanism in the node kernel -- the
+ * cells are split into ngroup contiguous groups and, in runs without VecPlay, taping,
+ * capture or non-voltage monitors, each group's step chain is issued on its own HIP
+ * stream, so one group's latency-bound tree solve overlaps another group's HBM-bound
+ * node pass.  Results are identical to a single group.  0 (default) picks 2; 1 turns
+ * it off.  Call before hx_load_model. */
+int hx_set_cell_groups(hx_sim* sim, int ngroup);
+/* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused",
+ * "cell_groups", "multi_stream" (1 if the last run used per-group streams). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the
