@@ -40,12 +40,13 @@ MECH_BYTES_PER_COMP = 280
 
 
 def _traffic_from_profiles():
-    """HBM bytes per launch of the mechanism kernel from the committed rocprof counter summary."""
+    """HBM bytes of one node-kernel pass over the whole model, from the committed rocprof
+    counter summary (copy-calibrated FETCH_SIZE + WRITE_SIZE)."""
     path = os.path.join(ROOT, "profiles", "k_dense_config3_counters.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith("traffic_bytes_per_full_pass:"):
             try:
                 return float(line.split(":", 1)[1].strip())
             except ValueError:
@@ -296,22 +297,43 @@ def main():
 
     value = nnode * args.steps / wall
     ms_per_step = wall * 1e3 / args.steps
+    multi = sim.info("multi_stream")
     kernels = {}
     for k in ("mech", "sparse", "point", "solve", "spike", "events", "other"):
         ms, n = sim.kernel_time(k)
         if n:
             kernels[k] = {"ms_total": ms, "launches": n, "us_per_launch": ms * 1e3 / n}
-    roofline = None
-    if "mech" in kernels:
-        # each step runs the node kernel once per cell group; a launch covers
-        # nnode / groups compartments on average
-        per_launch_s = kernels["mech"]["ms_total"] / kernels["mech"]["launches"] / 1e3
-        alg = MECH_BYTES_PER_COMP * nnode / groups
+
+    def node_kernel_roofline(mech, parts):
+        # a step runs the node kernel once per part (cell group); a launch covers
+        # nnode / parts compartments
+        per_launch_s = mech["ms_total"] / mech["launches"] / 1e3
+        alg = MECH_BYTES_PER_COMP * nnode / parts
         achieved = alg / per_launch_s / 1e9
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic_from_profiles(),
-                    "kernel": "k_dense (fused hh/pas/Ih/Ca_HVA/CaDynamics_E2 state+current)",
-                    "alg_bytes_per_launch": alg}
+        traffic = _traffic_from_profiles()
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": None if traffic is None else traffic / parts,
+                "kernel": "k_dense (fused hh/pas/Ih/Ca_HVA/CaDynamics_E2 state+current)",
+                "alg_bytes_per_launch": alg}
+
+    roofline = None
+    alone = None
+    if "mech" in kernels:
+        parts = groups if multi else 1
+        roofline = node_kernel_roofline(kernels["mech"], parts)
+        if multi:
+            # the same kernel with the whole GPU to itself: a short single-stream
+            # segment after the timed region (its launches cover the whole model)
+            roofline["note"] = ("launch time measured while the other cell group's tree solve runs "
+                                "beside it on its own stream")
+            sim.set_group_streams(False)
+            sim.set_profiling(True, classes=["mech"])
+            sim.continue_run(100.5 * dt)
+            ms, n = sim.kernel_time("mech")
+            sim.set_group_streams(True)
+            if n:
+                alone = node_kernel_roofline({"ms_total": ms, "launches": n}, 1)
     print(json.dumps({"kernel_times": kernels, "build_s": round(t_build, 2), "nnode": nnode,
                       "cell_groups": groups, "multi_stream": sim.info("multi_stream"),
                       "spikes": sim.spikes()[0].size, "t_end": sim.get_t()}), file=sys.stderr)
@@ -339,6 +361,7 @@ def main():
                    "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "roofline": roofline,
+        "roofline_single_stream": alone,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -265,6 +265,7 @@ struct hx_sim {
     bool groups_coupled = true;                   // structural: something couples the groups
     bool multi_stream = false;                    // the current run issues groups on their streams
     bool last_multi_stream = false;
+    bool group_streams_allowed = true;            // hx_set_group_streams
     hipEvent_t ev_main = nullptr;
     // time table
     std::vector<double> ttab;
@@ -1224,8 +1225,8 @@ void hx_sim::tape_record() {
 }
 
 bool hx_sim::want_multi_stream() const {
-    return groups.size() > 1 && fused && vecplay.empty() && !tape_on && !(learn && learn->capturing()) &&
-           (mon_ref.empty() || mon_all_v);
+    return group_streams_allowed && groups.size() > 1 && fused && vecplay.empty() && !tape_on &&
+           !(learn && learn->capturing()) && (mon_ref.empty() || mon_all_v);
 }
 
 // One fadvance with each cell group's chain on its own stream: the same
@@ -2022,6 +2023,11 @@ int hx_set_cell_groups(hx_sim* sim, int ngroup) {
     if (sim->loaded) return sim->fail("set the cell groups before hx_load_model");
     if (ngroup < 0) return sim->fail("group count must be >= 0");
     sim->group_request = ngroup;
+    return 0;
+}
+
+int hx_set_group_streams(hx_sim* sim, int enable) {
+    sim->group_streams_allowed = enable != 0;
     return 0;
 }
 

@@ -119,6 +119,7 @@ SIGNATURES = {
                   C.c_double, C.c_double, C.c_int, C.c_int]),
     "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
     "hx_set_cell_groups": (C.c_int, [_P, C.c_int]),
+    "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
 
@@ -658,6 +659,10 @@ class Sim:
         """Cell groups issued on separate streams when nothing couples them (0 automatic, 1 off).
         Call before loading the model."""
         self._chk(lib().hx_set_cell_groups(self._h, int(ngroup)), "set_cell_groups")
+
+    def set_group_streams(self, enable: bool) -> None:
+        """Allow the cell groups' own streams in the following runs (same results either way)."""
+        self._chk(lib().hx_set_group_streams(self._h, int(bool(enable))), "set_group_streams")
 
     def set_replay_timing(self, enable: bool) -> None:
         self._chk(lib().hx_set_replay_timing(self._h, int(bool(enable))), "set_replay_timing")

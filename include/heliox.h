@@ -131,9 +131,13 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
  * cells are split into ngroup contiguous groups and, in runs without VecPlay, taping,
  * capture or non-voltage monitors, each group's step chain is issued on its own HIP
  * stream, so one group's latency-bound tree solve overlaps another group's HBM-bound
- * node pass.  Results are identical to a single group.  0 (default) picks 2; 1 turns
- * it off.  Call before hx_load_model. */
+ * node pass.  Results are identical to a single group.  0 (default) picks 2 (the
+ * fastest on config 3: 3 and 4 groups are slower); 1 turns it off.  Call before
+ * hx_load_model. */
 int hx_set_cell_groups(hx_sim* sim, int ngroup);
+/* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
+ * following runs; with 0 every launch goes to the library stream.  Same results. */
+int hx_set_group_streams(hx_sim* sim, int enable);
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused",
  * "cell_groups", "multi_stream" (1 if the last run used per-group streams). */
 long long hx_get_info(hx_sim* sim, const char* key);
