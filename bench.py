@@ -244,6 +244,8 @@ def main():
     ap.add_argument("--train-cells", type=int, default=1000)
     ap.add_argument("--cell-groups", type=int, default=0,
                     help="cell groups issued on separate streams (0: the library's choice, 1: one stream)")
+    ap.add_argument("--model-root", action="store_true",
+                    help="solve each cell toward its model root instead of its centre")
     ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
     ap.add_argument("--lrds-n", type=int, default=2048)
     ap.add_argument("--lrds-ticks", type=int, default=256)
@@ -277,6 +279,7 @@ def main():
     spec = build_config(3, args.ncell, tstop_needed)
     sim = Sim()
     sim.set_cell_groups(args.cell_groups)
+    sim.set_solver_root(not args.model_root)
     sim.load_model_from_spec(spec)
     t_build = time.perf_counter() - t_build
     groups = sim.info("cell_groups")

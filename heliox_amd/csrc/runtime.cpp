@@ -162,7 +162,13 @@ struct VecPlayHost {
 
 // klass 0 param/state, 1 assigned; point: a point-process column (its values
 // change at event delivery, which the fused schedule runs before the record)
-struct Ref { double* dev = nullptr; int klass = 0; bool point = false; };
+struct Ref {
+    double* dev = nullptr;
+    int klass = 0;
+    bool point = false;
+    int ab = 0;           // 1: node coefficient a, 2: b (the solver keeps its own copy)
+    int node = -1;        // user node of an a / b reference
+};
 
 struct Timer {
     std::vector<hipEvent_t> pool;
@@ -200,6 +206,10 @@ struct hx_sim {
     // layout
     std::vector<int> node_perm, node_iperm;    // user <-> solver order
     std::vector<int> cell_node_begin, cell_desc_begin, cell_round_begin;
+    // the solver's tree (user node indices) and its coupling coefficients
+    std::vector<int> solve_parent;
+    std::vector<double> solve_a, solve_b;
+    bool solve_root_centre = true;
     std::vector<RoundInfo> rounds;       // all cells' rounds, cell by cell
     std::vector<ChunkDesc> descs;
     int max_slots = 0, max_rounds = 0;
@@ -212,6 +222,7 @@ struct hx_sim {
     // device
     std::vector<void*> owned;
     hipStream_t stream = nullptr;
+    double *d_sa = nullptr, *d_sb = nullptr;   // solver coefficients (solver tree), node order
     double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
            *d_area = nullptr, *d_w = nullptr;
     int *d_cell_node_begin = nullptr, *d_cell_desc_begin = nullptr, *d_cell_round_begin = nullptr;
@@ -313,6 +324,7 @@ struct hx_sim {
            *d_dT = nullptr, *d_rhsT = nullptr, *d_vT = nullptr, *d_wT = nullptr;
     double *d_grad_gnabar = nullptr, *d_grad_gkbar = nullptr, *d_grad_gpas = nullptr, *d_grad_w = nullptr;
     bool have_grad = false;
+    bool adj_delta_dirty = true;
     struct AdamHost {
         double beta1 = 0.9, beta2 = 0.999, eps = 1e-8;
         long long step = 0;
@@ -348,6 +360,7 @@ struct hx_sim {
         return *learn;
     }
     void require_sample_point(const Ref& r);
+    void mirror_ab(const Ref& r, double value);
 
     ~hx_sim() {
         learn.reset();
@@ -434,6 +447,69 @@ struct hx_sim {
 // ===========================================================================
 // layout
 // ===========================================================================
+namespace {
+
+// Midpoint of the longest path of a tree given by parent links (parent < child).
+int tree_centre(const std::vector<int>& lp) {
+    const int n = static_cast<int>(lp.size());
+    if (n <= 2) return 0;
+    std::vector<std::vector<int>> adj(n);
+    for (int j = 1; j < n; ++j) {
+        adj[j].push_back(lp[j]);
+        adj[lp[j]].push_back(j);
+    }
+    std::vector<int> dist(n), prev(n);
+    auto bfs = [&](int s) {
+        std::fill(dist.begin(), dist.end(), -1);
+        std::vector<int> q{s};
+        dist[s] = 0;
+        prev[s] = -1;
+        int far = s;
+        for (size_t h = 0; h < q.size(); ++h) {
+            const int u = q[h];
+            if (dist[u] > dist[far]) far = u;
+            for (int w : adj[u])
+                if (dist[w] < 0) {
+                    dist[w] = dist[u] + 1;
+                    prev[w] = u;
+                    q.push_back(w);
+                }
+        }
+        return far;
+    };
+    const int x = bfs(0);
+    const int y = bfs(x);
+    std::vector<int> path;
+    for (int u = y; u >= 0; u = prev[u]) path.push_back(u);
+    return path[path.size() / 2];
+}
+
+// Re-root a tree at `root`: bfs lists the nodes in BFS order, and spl[j] is
+// the parent of bfs[j] as an index into bfs (-1 for the root), so parent < child.
+void reroot_tree(const std::vector<int>& lp, int root, std::vector<int>& bfs, std::vector<int>& spl) {
+    const int n = static_cast<int>(lp.size());
+    std::vector<std::vector<int>> adj(n);
+    for (int j = 1; j < n; ++j) {
+        adj[j].push_back(lp[j]);
+        adj[lp[j]].push_back(j);
+    }
+    std::vector<int> label(n, -1);
+    bfs.assign(1, root);
+    spl.assign(1, -1);
+    label[root] = 0;
+    for (size_t h = 0; h < bfs.size(); ++h) {
+        const int u = bfs[h];
+        for (int w : adj[u])
+            if (label[w] < 0) {
+                label[w] = static_cast<int>(bfs.size());
+                bfs.push_back(w);
+                spl.push_back(static_cast<int>(h));
+            }
+    }
+}
+
+}  // namespace
+
 void hx_sim::build_layout() {
     const auto& R = registry();
     // per-cell node lists (user order, increasing)
@@ -457,6 +533,14 @@ void hx_sim::build_layout() {
     max_slots = 0;
     max_rounds = 0;
     int pos = 0;
+    // The solve may eliminate toward any node of a cell: the matrix and its
+    // solution do not depend on the root, and the axial assembly is the same
+    // once a and b trade places on every reversed edge.  Each cell is rooted at
+    // the midpoint of its longest path, which shortens the chain of rounds
+    // (config 3: 62 -> about 48).
+    solve_parent.assign(nnode, -1);
+    solve_a.assign(nnode, 0.0);
+    solve_b.assign(nnode, 0.0);
     for (int c = 0; c < ncell; ++c) {
         const int n = cnt[c];
         std::vector<int> lp(n);
@@ -465,13 +549,30 @@ void hx_sim::build_layout() {
             const int u = cnodes[cbeg[c] + j];
             lp[j] = (j == 0) ? -1 : local[parent[u]];
         }
+        // solver tree: BFS from the root, relabelled so that parent < child
+        const int root = solve_root_centre ? tree_centre(lp) : 0;
+        std::vector<int> bfs, spl;   // BFS order (original local ids), solver-local parents
+        reroot_tree(lp, root, bfs, spl);
         CellSchedule cs;
-        build_cell_schedule(lp, kChunk, kWave, kRoundMax, cs);
+        build_cell_schedule(spl, kChunk, kWave, kRoundMax, cs);
         cell_node_begin[c] = pos;
         for (int s = 0; s < n; ++s) {
-            const int u = cnodes[cbeg[c] + cs.order[s]];
+            const int u = cnodes[cbeg[c] + bfs[cs.order[s]]];
             node_perm[u] = pos + s;
             node_iperm[pos + s] = u;
+        }
+        for (int j = 0; j < n; ++j) {
+            if (spl[j] < 0) continue;
+            const int u = cnodes[cbeg[c] + bfs[j]];
+            const int q = cnodes[cbeg[c] + bfs[spl[j]]];
+            solve_parent[u] = q;
+            if (parent[u] == q) {          // same orientation as the model's tree
+                solve_a[u] = a[u];
+                solve_b[u] = b[u];
+            } else {                       // reversed edge: the coefficients of q's old link trade places
+                solve_a[u] = b[q];
+                solve_b[u] = a[q];
+            }
         }
         pos += n;
         cell_desc_begin[c] = static_cast<int>(descs.size());
@@ -550,6 +651,8 @@ void hx_sim::upload() {
     d_w = dalloc<double>(owned, nnode);
     d_a = dupload(owned, perm_nodes(a));
     d_b = dupload(owned, perm_nodes(b));
+    d_sa = dupload(owned, perm_nodes(solve_a));
+    d_sb = dupload(owned, perm_nodes(solve_b));
     d_cm = dupload(owned, perm_nodes(cm));
     d_area = dupload(owned, perm_nodes(area));
     d_cell_node_begin = dupload(owned, cell_node_begin);
@@ -956,8 +1059,8 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
         if (var == "v") r.dev = d_v + g;
         else if (var == "d") { r.dev = d_d + g; r.klass = 1; }
         else if (var == "rhs") { r.dev = d_rhs + g; r.klass = 1; }
-        else if (var == "a") r.dev = d_a + g;
-        else if (var == "b") r.dev = d_b + g;
+        else if (var == "a") { r.dev = d_a + g; r.ab = 1; r.node = idx; }
+        else if (var == "b") { r.dev = d_b + g; r.ab = 2; r.node = idx; }
         else if (var == "area") r.dev = d_area + g;
         return r;
     }
@@ -1192,6 +1295,29 @@ void hx_sim::launch_record() {
     mon_buf_fill++;
 }
 
+// A write to a node's a or b also reaches the solver's copy: at the same node
+// when the solver's tree keeps the link's orientation, else, with a and b
+// trading places, at the node's parent (which the solver hangs below it).
+void hx_sim::mirror_ab(const Ref& r, double value) {
+    if (!r.ab || r.node < 0) return;
+    const int u = r.node;
+    (r.ab == 1 ? a : b)[u] = value;
+    const int p = parent[u];
+    if (p < 0) return;
+    int at;
+    bool a_side;
+    if (solve_parent[u] == p) {
+        at = u;
+        a_side = r.ab == 1;
+    } else {
+        at = p;
+        a_side = r.ab == 2;
+    }
+    (a_side ? solve_a : solve_b)[at] = value;
+    HXC(hipMemcpy((a_side ? d_sa : d_sb) + node_perm[at], &value, sizeof(double), hipMemcpyHostToDevice));
+    adj_delta_dirty = true;   // rebuilt by the next adjoint
+}
+
 // A sampled assigned variable (klass 1) or point-process variable is only
 // valid at the reference's record point under the split schedule.
 void hx_sim::require_sample_point(const Ref& r) {
@@ -1260,8 +1386,8 @@ void hx_sim::step_once_groups() {
         S.d = d_d;
         S.rhs = d_rhs;
         S.w = d_w;
-        S.a = d_a;
-        S.b = d_b;
+        S.a = d_sa;
+        S.b = d_sb;
         tbegin(T_SOLVE, s);
         launch_solve(S, max_slots, s);
         tend(T_SOLVE, s);
@@ -1341,8 +1467,8 @@ void hx_sim::step_once() {
     S.d = d_d;
     S.rhs = d_rhs;
     S.w = d_w;
-    S.a = d_a;
-    S.b = d_b;
+    S.a = d_sa;
+    S.b = d_sb;
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
@@ -1846,6 +1972,7 @@ int hx_set_variable_by_handle(hx_sim* sim, int h, double value) {
     API_BEGIN
     HXC(hipStreamSynchronize(sim->stream));
     HXC(hipMemcpy(sim->handles[h].dev, &value, sizeof(double), hipMemcpyHostToDevice));
+    sim->mirror_ab(sim->handles[h], value);
     return 0;
     API_END
 }
@@ -1889,6 +2016,7 @@ int hx_set_variable_value(hx_sim* sim, double value, const char* mech, const cha
     if (!r.dev) return sim->fail("variable %s.%s[%d] not found", mech, var, idx);
     HXC(hipStreamSynchronize(sim->stream));
     HXC(hipMemcpy(r.dev, &value, sizeof(double), hipMemcpyHostToDevice));
+    sim->mirror_ab(r, value);
     return 0;
     API_END
 }
@@ -2026,6 +2154,12 @@ int hx_set_cell_groups(hx_sim* sim, int ngroup) {
     return 0;
 }
 
+int hx_set_solver_root(hx_sim* sim, int centre) {
+    if (sim->loaded) return sim->fail("set the solver root before hx_load_model");
+    sim->solve_root_centre = centre != 0;
+    return 0;
+}
+
 int hx_set_group_streams(hx_sim* sim, int enable) {
     sim->group_streams_allowed = enable != 0;
     return 0;
@@ -2102,8 +2236,8 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
             const int g = tmp.node_perm[i];
             arr[SA_DB][g] = d[i] + cfac * cm[i];
             arr[SA_RM][g] = rhs[i];
-            arr[SA_A][g] = a[i];
-            arr[SA_B][g] = b[i];
+            arr[SA_A][g] = tmp.solve_a[i];   // the solver's tree and coefficients, as uploaded
+            arr[SA_B][g] = tmp.solve_b[i];
             arr[SA_V][g] = v[i];
         }
         const double neutral[kStageArrays] = {1.0, 0.0, 0.0, 0.0, 0.0};
@@ -2276,14 +2410,8 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     // diagonal correction of the transposed solve: the tree kernel assembles
     // d - b_i - sum_c a_c from the (swapped) coefficients, M^T needs the original
     if (!sim->d_adj_delta) {
-        std::vector<double> delta(N, 0.0);
-        for (int i = sim->ncell; i < N; ++i) {
-            delta[i] += sim->a[i] - sim->b[i];
-            delta[sim->parent[i]] += sim->b[i] - sim->a[i];
-        }
-        std::vector<double> g(N);
-        for (int i = 0; i < N; ++i) g[sim->node_perm[i]] = delta[i];
-        sim->d_adj_delta = dupload(owned, g);
+        sim->d_adj_delta = dalloc<double>(owned, N);
+        sim->adj_delta_dirty = true;
         for (double** p : {&sim->d_lv, &sim->d_lv2, &sim->d_dT, &sim->d_rhsT, &sim->d_vT, &sim->d_wT})
             *p = dalloc<double>(owned, N);
         const HostMech& hh = sim->mech[M_HH];
@@ -2295,6 +2423,20 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         sim->d_grad_gkbar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
         sim->d_grad_gpas = dalloc<double>(owned, std::max(1, pas.present ? pas.n : 0));
         sim->d_grad_w = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+    }
+    if (!sim->d_adj_delta || sim->adj_delta_dirty) {
+        // diagonal correction on the solver's tree, with the solver's coefficients
+        std::vector<double> delta(N, 0.0);
+        for (int i = 0; i < N; ++i) {
+            const int q = sim->solve_parent[i];
+            if (q < 0) continue;
+            delta[i] += sim->solve_a[i] - sim->solve_b[i];
+            delta[q] += sim->solve_b[i] - sim->solve_a[i];
+        }
+        std::vector<double> g(N);
+        for (int i = 0; i < N; ++i) g[sim->node_perm[i]] = delta[i];
+        HXC(hipMemcpy(sim->d_adj_delta, g.data(), sizeof(double) * N, hipMemcpyHostToDevice));
+        sim->adj_delta_dirty = false;
     }
     const HostMech& hh = sim->mech[M_HH];
     const HostMech& es = sim->mech[M_EXPSYN];
@@ -2339,8 +2481,8 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     S.d = sim->d_dT;
     S.rhs = sim->d_rhsT;
     S.w = sim->d_wT;
-    S.a = sim->d_b;       // M^T: the coefficients trade places
-    S.b = sim->d_a;
+    S.a = sim->d_sb;      // M^T: the coefficients trade places
+    S.b = sim->d_sa;
     double* lv = sim->d_lv;
     double* lv2 = sim->d_lv2;
     const size_t row = static_cast<size_t>(N);

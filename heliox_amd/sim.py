@@ -120,6 +120,7 @@ SIGNATURES = {
     "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
     "hx_set_cell_groups": (C.c_int, [_P, C.c_int]),
     "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
+    "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
 
@@ -659,6 +660,11 @@ class Sim:
         """Cell groups issued on separate streams when nothing couples them (0 automatic, 1 off).
         Call before loading the model."""
         self._chk(lib().hx_set_cell_groups(self._h, int(ngroup)), "set_cell_groups")
+
+    def set_solver_root(self, centre: bool) -> None:
+        """Root each cell's tree solve at the midpoint of its longest path (default) or at
+        the model root.  Call before loading the model."""
+        self._chk(lib().hx_set_solver_root(self._h, int(bool(centre))), "set_solver_root")
 
     def set_group_streams(self, enable: bool) -> None:
         """Allow the cell groups' own streams in the following runs (same results either way)."""

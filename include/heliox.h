@@ -135,6 +135,12 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
  * fastest on config 3: 3 and 4 groups are slower); 1 turns it off.  Call before
  * hx_load_model. */
 int hx_set_cell_groups(hx_sim* sim, int ngroup);
+/* Root of each cell's tree solve (no counterpart in the reference: its solve always
+ * eliminates toward the model root).  centre != 0 (default): the midpoint of the cell's
+ * longest path, which shortens the solve's chain of dependent rounds; 0: the model's
+ * root.  The solution is the same up to rounding; after a step, d holds the pivots of
+ * the order used.  Call before hx_load_model. */
+int hx_set_solver_root(hx_sim* sim, int centre);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
