@@ -176,3 +176,28 @@ def test_full_size_prefix(gpu_lib, config, ncell, nref):
     assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
     v = g.get_array("global", "v")
     assert np.all(np.isfinite(v))
+
+
+def test_axial_coefficient_writes_reach_the_solver(gpu_lib):
+    """a and b written through handles mid-run: the solve runs on each cell's
+    centre-rooted tree, where the links between the model root and the centre
+    are reversed, so the writes must reach the solver's own coefficients."""
+    spec = build_config(2, 2, 30.0)
+    mons = [("global", "v", i) for i in range(2)]
+    o, g = run_both(spec, 10.0, monitors=mons)
+    cell = spec.cell_of_node()
+    rng = np.random.default_rng(7)
+    # every link of cell 0, which includes the reversed ones; a few of cell 1
+    nodes = [int(i) for i in np.nonzero(cell == 0)[0][1:]] + [int(i) for i in np.nonzero(cell == 1)[0][1:6]]
+    for i in nodes:
+        for var in ("a", "b"):
+            x = o.get("global", var, i) * float(rng.uniform(0.5, 2.0))
+            o.set("global", var, i, x)
+            h = g.get_variable_handle("global", var, i)
+            g.set_variable_by_handle(h, x)
+            assert g.get_variable_by_handle(h) == x
+    o.continue_run(20.0)
+    g.continue_run(20.0)
+    err = float(np.max(np.abs(o.traces() - g.traces())))
+    print(f"  max |dv| after a/b writes {err:.3e}", flush=True)
+    assert err < V_TOL
