@@ -249,7 +249,7 @@ def main():
     ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
     ap.add_argument("--lrds-n", type=int, default=2048)
     ap.add_argument("--lrds-ticks", type=int, default=256)
-    ap.add_argument("--lrds-cpu-rows", type=int, default=6)
+    ap.add_argument("--lrds-cpu-rows", type=int, default=1)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:

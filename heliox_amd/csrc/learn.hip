@@ -75,27 +75,38 @@ __global__ void k_rp_base(ReplayBaseArgs A) {
 }
 
 // ---------------------------------------------------------------- correction GEMM
-// Workgroup tile: 128 rows x TJ columns of one block (TJ = 64 or 128), 8 waves
-// as 4 row groups x 2 column groups; a wave owns 32 rows x TJ/2 columns, i.e.
-// TJ/64 accumulators of v_mfma_f32_32x32x2f32.  The reduction runs over
-// (tap u, chunk of 32 columns k).  Each chunk stages X -- formed from the
-// history slice D and its column-gathered copy G, both read as contiguous row
-// segments -- and the K taps through LDS, double-buffered, with the next
-// chunk's global loads in flight while the MFMAs run.
+// Workgroup tile: 128 rows x TJ columns of one block (TJ = 64 or 128) with NT
+// threads, the waves arranged as WR row groups x (NT/64/WR) column groups; a
+// wave owns a (128/WR) x (TJ/WC) sub-tile, held as 32 x 32 accumulators of
+// v_mfma_f32_32x32x2f32.  The reduction runs over (tap u, chunk of KC columns
+// k).  Each chunk stages X -- formed from the history slice D and its
+// column-gathered copy G, both read as contiguous row segments -- and the K
+// taps through LDS, double-buffered, with the next chunk's global loads in
+// flight while the MFMAs run.
+// Measured on MI355X (N = 2048, 16 blocks of 128, K_len 64): 64-tap chunks
+// (one 130 KB workgroup per CU) beat 32- and 16-tap chunks, and 8 waves of
+// 32 x 64 sub-tiles beat 4 waves of 64 x 64.
 constexpr int kCorrThreads = 512;
 constexpr int kTI = 128;
-constexpr int kKC = 32;
+constexpr int kKC = 64;
+constexpr int kWR = 4;
 constexpr int kAPad = kTI + 1;
 
 template <int TJ>
 __global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
-    constexpr int NACC = TJ / 64;                       // 32-column accumulators per wave
-    constexpr int BSTEP = kCorrThreads / TJ;            // B rows covered per pass
+    constexpr int NW = kCorrThreads / 64;               // waves
+    constexpr int WC = NW / kWR;                        // column groups of waves
+    constexpr int WTI = kTI / kWR, WTJ = TJ / WC;       // wave sub-tile
+    constexpr int MR = WTI / 32, NC = WTJ / 32;         // accumulators per wave
+    static_assert(MR >= 1 && NC >= 1 && WTI % 32 == 0 && WTJ % 32 == 0, "wave sub-tile must be 32-aligned");
+    constexpr int ASTEP = kCorrThreads / kKC;           // A rows covered per pass
+    constexpr int RA = kTI / ASTEP;                     // A elements per thread and array
+    constexpr int BSTEP = kCorrThreads / TJ;            // B taps covered per pass
     constexpr int BR = kKC / BSTEP;                     // B elements per thread
     __shared__ float As[2][kKC][kAPad];                 // X chunk, [k][i]
     __shared__ float Bs[2][kKC][TJ];                    // K chunk, [k][j]
-    __shared__ double red_s[kCorrThreads / 64];
-    __shared__ int red_f[kCorrThreads / 64];
+    __shared__ double red_s[NW];
+    __shared__ int red_f[NW];
 
     const int2 tl = A.tiles[blockIdx.x];
     const int b = tl.x, j0 = tl.y;
@@ -103,16 +114,16 @@ __global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
     const int N = A.N;
     const int i0 = blockIdx.y * kTI;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
+    const int wr = wave / WC, wc = wave % WC;
     const float* Kb = A.kt2 + A.koff[b];
     const size_t plane = static_cast<size_t>(bn) * bn;
     const int nkc = (bn + kKC - 1) / kKC;
     const int nchunk = A.tw * nkc;
 
-    // staging coordinates: A element (row ai + 16r, tap ak), B element (tap bk + BSTEP r, column bj)
-    const int ak = tid & 31, ai = tid >> 5;
+    // staging coordinates: A element (row ai + ASTEP r, tap ak), B element (tap bk + BSTEP r, column bj)
+    const int ak = tid % kKC, ai = tid / kKC;
     const int bj = tid % TJ, bk = tid / TJ;
-    float rd[8], rg[8], rb[BR];
+    float rd[RA], rg[RA], rb[BR];
     float ca = 0.f, cp = 0.f;
 
     auto fetch = [&](int c) {
@@ -134,13 +145,15 @@ __global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
             cp = sig * A.dp[tau * N + col];
         }
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int i = i0 + ai + 16 * r;
+        for (int r = 0; r < RA; ++r) {
+            const int i = i0 + ai + ASTEP * r;
             float x = 0.f, y = 0.f;
             if (kin && i < N) {
                 const size_t o = static_cast<size_t>(i) * N + col;
-                x = D[o];
-                y = G[o];
+                // the history window streams through once per tick: keep it out of
+                // the caches so the K taps, reused by every row tile, stay in L2
+                x = __builtin_nontemporal_load(D + o);
+                y = __builtin_nontemporal_load(G + o);
             }
             rd[r] = x;
             rg[r] = y;
@@ -155,65 +168,73 @@ __global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
     };
     auto stage = [&](int buf) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r) As[buf][ak][ai + 16 * r] = rd[r] * ca + rg[r] * cp;
+        for (int r = 0; r < RA; ++r) As[buf][ak][ai + ASTEP * r] = rd[r] * ca + rg[r] * cp;
 #pragma unroll
         for (int r = 0; r < BR; ++r) Bs[buf][bk + BSTEP * r][bj] = rb[r];
     };
 
-    f16v acc[NACC];
+    f16v acc[MR][NC];
 #pragma unroll
-    for (int n = 0; n < NACC; ++n)
+    for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+        for (int n = 0; n < NC; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
 
     if (nchunk > 0) {
         fetch(0);
         stage(0);
         __syncthreads();
         const int kr = lane >> 5;
-        const int ia = wr * 32 + (lane & 31);
-        const int jb = wc * (TJ / 2) + (lane & 31);
+        const int ia = wr * WTI + (lane & 31);
+        const int jb = wc * WTJ + (lane & 31);
         for (int c = 0; c < nchunk; ++c) {
             const int buf = c & 1;
             if (c + 1 < nchunk) fetch(c + 1);
 #pragma unroll
             for (int q = 0; q < kKC / 2; ++q) {
-                const float a = As[buf][2 * q + kr][ia];
+                float av[MR], bv[NC];
 #pragma unroll
-                for (int n = 0; n < NACC; ++n) {
-                    const float bb = Bs[buf][2 * q + kr][jb + 32 * n];
-                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bb, acc[n], 0, 0, 0);
-                }
+                for (int m = 0; m < MR; ++m) av[m] = As[buf][2 * q + kr][ia + 32 * m];
+#pragma unroll
+                for (int n = 0; n < NC; ++n) bv[n] = Bs[buf][2 * q + kr][jb + 32 * n];
+#pragma unroll
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int n = 0; n < NC; ++n)
+                        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[m], bv[n], acc[m][n], 0, 0, 0);
             }
             if (c + 1 < nchunk) stage(buf ^ 1);
             __syncthreads();
         }
     }
 
-    // epilogue: accumulator n of a lane holds rows 8(r/4) + 4(lane/32) + r%4 and
-    // column 32n + lane%32 of its wave's sub-tile
+    // epilogue: accumulator (m, n) of a lane holds rows 32m + 8(r/4) + 4(lane/32) + r%4
+    // and column 32n + lane%32 of its wave's sub-tile
     double sq = 0.0;
     int bad = 0;
     const float* base = A.base + A.boff[b];
 #pragma unroll
-    for (int n = 0; n < NACC; ++n) {
-        const int jw = j0 + wc * (TJ / 2) + 32 * n + (lane & 31);
+    for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = i0 + wr * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (row >= N || jw >= bn) continue;
-            float v = acc[n][r] * A.dt;
-            if (row >= s && row < s + bn) v = base[static_cast<size_t>(row - s) * bn + jw] + v;
-            if (A.sanitize) {
-                if (!isfinite(v)) {
-                    v = 0.f;
-                    bad = 1;
+        for (int n = 0; n < NC; ++n) {
+            const int jw = j0 + wc * WTJ + 32 * n + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = i0 + wr * WTI + 32 * m + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row >= N || jw >= bn) continue;
+                float v = acc[m][n][r] * A.dt;
+                if (row >= s && row < s + bn) v = base[static_cast<size_t>(row - s) * bn + jw] + v;
+                if (A.sanitize) {
+                    if (!isfinite(v)) {
+                        v = 0.f;
+                        bad = 1;
+                    }
+                    sq += static_cast<double>(v) * v;
                 }
-                sq += static_cast<double>(v) * v;
+                A.out[static_cast<size_t>(row) * N + s + jw] = v;
             }
-            A.out[static_cast<size_t>(row) * N + s + jw] = v;
         }
-    }
     if (A.sanitize) {
         for (int o = 32; o > 0; o >>= 1) {
             sq += __shfl_xor(sq, o);
@@ -227,7 +248,7 @@ __global__ __launch_bounds__(kCorrThreads) void k_rp_corr(ReplayCorrArgs A) {
         if (tid == 0) {
             double t = 0.0;
             int f = 0;
-            for (int w = 0; w < kCorrThreads / 64; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 t += red_s[w];
                 f |= red_f[w];
             }
