@@ -46,10 +46,20 @@ __device__ __forceinline__ int ion_index(const MechDev& m, int which, int j) {
 struct HHState { double m, h, n; };
 struct CaHVAState { double m, h; };
 
+// Per-compartment parameters and states are touched once per step, and a step
+// moves far more data than L2 and the Infinity Cache hold: they are read and
+// written with the non-temporal hint, which leaves the caches to the node
+// arrays (v, d, rhs) that the tree solve reads right after the node kernel
+// (config 3: 0.84 -> 0.80 ms per step).
+__device__ __forceinline__ double lds_(const double* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void sts_(double* p, double v) { __builtin_nontemporal_store(v, p); }
+
 __device__ __forceinline__ HHState hh_load(const MechDev& m, int j) {
-    return {m.col(HH_M)[j], m.col(HH_H)[j], m.col(HH_N)[j]};
+    return {lds_(m.col(HH_M) + j), lds_(m.col(HH_H) + j), lds_(m.col(HH_N) + j)};
 }
-__device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) { return {m.col(CH_M)[j], m.col(CH_H)[j]}; }
+__device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) {
+    return {lds_(m.col(CH_M) + j), lds_(m.col(CH_H) + j)};
+}
 
 __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s) {
     double minf, mtau, hinf, htau, ninf, ntau;
@@ -57,9 +67,9 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
     s.m = hh_cnexp(s.m, minf, mtau, A.dt);
     s.h = hh_cnexp(s.h, hinf, htau, A.dt);
     s.n = hh_cnexp(s.n, ninf, ntau, A.dt);
-    m.col(HH_M)[j] = s.m;
-    m.col(HH_H)[j] = s.h;
-    m.col(HH_N)[j] = s.n;
+    sts_(m.col(HH_M) + j, s.m);
+    sts_(m.col(HH_H) + j, s.h);
+    sts_(m.col(HH_N) + j, s.n);
     if (A.write_assigned) {
         m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
         m.col(HH_HINF)[j] = hinf; m.col(HH_HTAU)[j] = htau;
@@ -74,8 +84,8 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
     cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
     s.m = s.m + (1.0 - exp(-A.dt / mTau)) * (mInf - s.m);
     s.h = s.h + (1.0 - exp(-A.dt / hTau)) * (hInf - s.h);
-    m.col(CH_M)[j] = s.m;
-    m.col(CH_H)[j] = s.h;
+    sts_(m.col(CH_M) + j, s.m);
+    sts_(m.col(CH_H) + j, s.h);
     if (A.write_assigned) {
         m.col(CH_ECA)[j] = ca_erev[ci];
         m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
@@ -86,17 +96,17 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
 
 __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l) {
     double linf, taul;
-    hdla_rate(v, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
+    hdla_rate(v, lds_(m.col(HD_VHALFL) + j), lds_(m.col(HD_TAU) + j), A.c, linf, taul);
     l = l + (1.0 - exp(-A.dt / taul)) * (linf - l);
-    m.col(HD_L)[j] = l;
+    sts_(m.col(HD_L) + j, l);
     if (A.write_assigned) { m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul; }
     return l;
 }
 
 // returns the new cai (the caller stores it)
 __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& m, int j, double cai, double ica) {
-    return cadyn_step(cai, ica, m.col(CD_GAMMA)[j], m.col(CD_DECAY)[j], m.col(CD_DEPTH)[j], m.col(CD_MINCAI)[j],
-                      A.dt);
+    return cadyn_step(cai, ica, lds_(m.col(CD_GAMMA) + j), lds_(m.col(CD_DECAY) + j), lds_(m.col(CD_DEPTH) + j),
+                      lds_(m.col(CD_MINCAI) + j), A.dt);
 }
 
 // ---------------------------------------------------------------------------
@@ -105,7 +115,7 @@ __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& 
 // returned for the caller to accumulate
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
-    double gp = m.col(PAS_G)[j], ep = m.col(PAS_E)[j];
+    double gp = lds_(m.col(PAS_G) + j), ep = lds_(m.col(PAS_E) + j);
     double v1 = v + 0.001;
     double i1 = gp * (v1 - ep);
     double i0 = gp * (v - ep);
@@ -116,8 +126,8 @@ __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, i
 
 __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, const HHState& s,
                                          double ena, double ek, double& g, double& ina, double& ik) {
-    double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
-    double gl = m.col(HH_GL)[j], el = m.col(HH_EL)[j];
+    double gnabar = lds_(m.col(HH_GNABAR) + j), gkbar = lds_(m.col(HH_GKBAR) + j);
+    double gl = lds_(m.col(HH_GL) + j), el = lds_(m.col(HH_EL) + j);
     double gna, gk, il;
     double v1 = v + 0.001;
     double i1 = hh_current(v1, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
@@ -132,7 +142,7 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
 
 __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v,
                                             const CaHVAState& s, double eca, double& g) {
-    double gbar = m.col(CH_GBAR)[j];
+    double gbar = lds_(m.col(CH_GBAR) + j);
     double v1 = v + 0.001;
     double gg = gbar * s.m * s.m * s.h;
     double i1 = gg * (v1 - eca);
@@ -146,7 +156,7 @@ __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m,
 
 __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double l,
                                            double& g) {
-    double ghd = m.col(HD_GHDBAR)[j] * l;
+    double ghd = lds_(m.col(HD_GHDBAR) + j) * l;
     double v1 = v + 0.001;
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);
@@ -171,15 +181,15 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
                                                  bool have_ci, double ci) {
     const int type = A.ion_type[x] >= 0 ? A.ion_type[x] : ion.iontype[i];
     if (type & 0100) {
-        const double e = nernst(have_ci ? ci : ion.col(ION_CONCI)[i], ion.col(ION_CONCO)[i], z, A.c.ktf);
-        if (A.ion_store & (2u << (2 * x))) ion.col(ION_EREV)[i] = e;
+        const double e = nernst(have_ci ? ci : lds_(ion.col(ION_CONCI) + i), lds_(ion.col(ION_CONCO) + i), z, A.c.ktf);
+        if (A.ion_store & (2u << (2 * x))) sts_(ion.col(ION_EREV) + i, e);
         return e;
     }
-    return ion.col(ION_EREV)[i];
+    return lds_(ion.col(ION_EREV) + i);
 }
 
 __device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {
-    if (A.ion_store & (1u << (2 * x))) ion.col(ION_CUR)[i] = cur;
+    if (A.ion_store & (1u << (2 * x))) sts_(ion.col(ION_CUR) + i, cur);
     if (A.write_assigned) ion.col(ION_DCURDV)[i] = 0.;
 }
 
@@ -215,17 +225,17 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
         if (A.do_state) {
             if (HAS(M_CADYN)) {
                 double* conci = ca.col(ION_CONCI);
-                cai = cadyn_state(A, A.m[M_CADYN], i, conci[i], ca.col(ION_CUR)[i]);
-                conci[i] = cai;
+                cai = cadyn_state(A, A.m[M_CADYN], i, lds_(conci + i), lds_(ca.col(ION_CUR) + i));
+                sts_(conci + i, cai);
             }
             if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, hh_load(A.m[M_HH], i));
             if (HAS(M_CAHVA))
                 cs = cahva_state(A, A.m[M_CAHVA], i, v, cahva_load(A.m[M_CAHVA], i), ca.col(ION_EREV), i);
-            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, A.m[M_HDLA].col(HD_L)[i]);
+            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, lds_(A.m[M_HDLA].col(HD_L) + i));
         } else if (A.do_current) {
             if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
             if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
-            if (HAS(M_HDLA)) hl = A.m[M_HDLA].col(HD_L)[i];
+            if (HAS(M_HDLA)) hl = lds_(A.m[M_HDLA].col(HD_L) + i);
         }
     }
     if (!A.do_current) return;
