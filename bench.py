@@ -39,6 +39,30 @@ METRIC = "compartment-steps/s (2000×5000-comp fp64) + achieved HBM GB/s"
 MECH_BYTES_PER_COMP = 280
 
 
+# Algorithmic bytes per instance and step over the whole step (node kernel and tree
+# solve), following the compulsory-traffic accounting of the workload definition:
+# states read and written once, parameters and ion inputs read once, plus index,
+# area and scattered rhs/d read-modify-write for point processes.  hh reads gl and
+# el per instance here (96 rather than 80); CaDynamics_E2 includes its ca_ion.
+STEP_BYTES_PER_INSTANCE = {"pas": 16, "hh": 96, "hd_la": 40, "Ca_HVA": 40, "CaDynamics_E2": 56,
+                           "Exp2Syn": 108, "ExpSyn": 76, "IClamp": 52}
+# per node: node kernel reads v, cm and writes rhs, d (32); the solve reads rhs, d,
+# a, b, v and the parent index and writes v (52)
+STEP_BYTES_PER_NODE = 84
+
+
+def step_bytes(spec, ms_per_step: float):
+    """Algorithmic HBM bytes of one whole step and the rate they imply at the measured
+    step time (against the HBM peak): an end-to-end figure beside the node kernel's."""
+    total = STEP_BYTES_PER_NODE * spec.nnode
+    for name, m in spec.mechs.items():
+        total += STEP_BYTES_PER_INSTANCE.get(name, 0) * m.n
+    gbs = total / (ms_per_step * 1e-3) / 1e9
+    return {"alg_bytes_per_step": total, "alg_bytes_per_compartment": round(total / spec.nnode, 2),
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def _traffic_from_profiles():
     """HBM bytes of one node-kernel pass over the whole model, from the committed rocprof
     counter summary (copy-calibrated FETCH_SIZE + WRITE_SIZE)."""
@@ -68,6 +92,40 @@ def cpu_baseline(ncell: int, nstep: int):
     return {"value": rate, "unit": "compartment-steps/s", "cores": 1, "kind": "port",
             "sample": f"config 3, first {ncell} cells x 5000 compartments, {nstep} steps "
                       f"({spec.nnode * nstep:.3g} compartment-steps, {el:.1f} s on one core)"}
+
+
+def cpu_baseline_all_cores(ncell: int, nstep: int, threads: int):
+    """The same port on every host core: the cells of config 3 are independent (VecStim
+    input only), so each thread steps its own range of ``ncell`` cells; ctypes releases
+    the GIL for the duration of each oracle call."""
+    import oracle
+    from concurrent.futures import ThreadPoolExecutor
+    from heliox_amd import build_config
+
+    sims, nnode = [], 0
+    for k in range(threads):
+        spec = build_config(3, ncell, nstep * 0.025 + 1.0, first_cell=k * ncell)
+        o = oracle.OracleSim(spec, monitors=[])
+        o.finitialize(-65.0)
+        sims.append(o)
+        nnode += spec.nnode
+    with ThreadPoolExecutor(threads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(lambda o: o.nsteps(nstep), sims))
+        el = time.perf_counter() - t0
+    return {"value": nnode * nstep / el, "unit": "compartment-steps/s", "cores": threads, "kind": "port",
+            "sample": f"config 3, cells 0..{threads * ncell - 1} ({ncell} per thread) x 5000 compartments, "
+                      f"{nstep} steps ({nnode * nstep:.3g} compartment-steps, {el:.1f} s on {threads} threads)"}
+
+
+def host_threads() -> int:
+    """Threads for the all-core baseline: the process's CPU affinity, capped by
+    OMP_NUM_THREADS when that is set (the share of a shared host this job owns)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def train_bench(args):
@@ -341,9 +399,10 @@ def main():
                       "cell_groups": groups, "multi_stream": sim.info("multi_stream"),
                       "spikes": sim.spikes()[0].size, "t_end": sim.get_t()}), file=sys.stderr)
 
-    cpu = None
+    cpu = cpu_all = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_cells, args.cpu_steps)
+        cpu_all = cpu_baseline_all_cores(args.cpu_cells, args.cpu_steps // 2, host_threads())
 
     out = {
         "metric": METRIC,
@@ -365,7 +424,9 @@ def main():
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "roofline": roofline,
         "roofline_single_stream": alone,
+        "step_bytes": step_bytes(spec, ms_per_step),
         "cpu_baseline": cpu,
+        "cpu_baseline_all_cores": cpu_all,
     }
     print(json.dumps(out))
 

@@ -265,15 +265,22 @@ def _poisson_trains(rng, n: int, rate_hz: float, tstop: float):
     return [t[i, : counts[i]] for i in range(n)]
 
 
-def build_config(config: int, ncell: Optional[int] = None, tstop: Optional[float] = None) -> ModelSpec:
-    """Build configuration ``config`` (1..5) with ``ncell`` cells (default: full size)."""
+def build_config(config: int, ncell: Optional[int] = None, tstop: Optional[float] = None,
+                 first_cell: int = 0) -> ModelSpec:
+    """Build configuration ``config`` (1..5) with ``ncell`` cells (default: full size).
+
+    ``first_cell`` selects cells ``first_cell .. first_cell + ncell - 1`` of the full
+    configuration (each cell has its own random stream); configuration 4 wires cells to
+    each other and only accepts 0."""
     full = {1: 1000, 2: 10000, 3: 2000, 4: 10000, 5: 1000}
     tdef = {1: 100.0, 2: 500.0, 3: 1000.0, 4: 1000.0, 5: 200.0}
     if config not in full:
         raise ValueError("config must be 1..5")
     ncell = full[config] if ncell is None else int(ncell)
     tstop = tdef[config] if tstop is None else float(tstop)
-    rngs = [cell_rng(config, c) for c in range(ncell)]
+    if first_cell and config == 4:
+        raise ValueError("configuration 4 connects its cells: first_cell must be 0")
+    rngs = [cell_rng(config, first_cell + c) for c in range(ncell)]
     if config == 1:
         cells = [_cell_c1(r) for r in rngs]
     elif config in (2, 5):
