@@ -123,7 +123,9 @@ struct alignas(16) RoundInfo {
     uint16_t node_base;
     uint16_t node_count;
     uint8_t off[kChunk];
-    uint32_t pad[2];
+    uint8_t maxlen;        // longest chunk of the round (0 for a padding round)
+    uint8_t pad8[3];
+    uint32_t pad;
 };
 static_assert(sizeof(RoundInfo) == 32, "RoundInfo must stay 32 bytes");
 

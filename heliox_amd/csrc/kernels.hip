@@ -544,7 +544,7 @@ struct RoundV {
     uint4 lo, hi;
 };
 struct RoundU {
-    int desc_begin, desc_count, node_base, node_count;
+    int desc_begin, desc_count, node_base, node_count, maxlen;
     uint32_t off[4];      // off[k] in byte k % 4 of off[k / 4]
     __device__ __forceinline__ int offset(int k) const { return (off[k >> 2] >> (8 * (k & 3))) & 0xFF; }
 };
@@ -564,6 +564,7 @@ __device__ __forceinline__ RoundU uniform_round(const RoundV& v) {
     u.off[1] = __builtin_amdgcn_readfirstlane(v.lo.w);
     u.off[2] = __builtin_amdgcn_readfirstlane(v.hi.x);
     u.off[3] = __builtin_amdgcn_readfirstlane(v.hi.y);
+    u.maxlen = __builtin_amdgcn_readfirstlane(v.hi.z) & 0xFF;
     return u;
 }
 
@@ -691,7 +692,7 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
             st[SA_RM * kStageStride + wp[k]] = u;
             st[SA_B * kStageStride + wp[k]] = w;
         },
-        rcp_nr, cd, ce);
+        rcp_nr, cd, ce, ri.maxlen);
     if (act && has_parent) {
         C.slots[2 * slot] = cd;
         C.slots[2 * slot + 1] = ce;
@@ -751,7 +752,7 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, 
                         st[SA_V * kStageStride + wp[k]] = vn;
                         st[SA_RM * kStageStride + wp[k]] = x;
                     },
-                    vpar);
+                    vpar, ri.maxlen);
     if (act) C.slots[2 * slot] = st[SA_V * kStageStride + tp];   // the tail's new voltage
     round_boundary();
     const int base = C.nb + ri.node_base;

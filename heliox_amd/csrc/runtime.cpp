@@ -2242,6 +2242,7 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
         }
         const double neutral[kStageArrays] = {1.0, 0.0, 0.0, 0.0, 0.0};
         std::vector<double> slots(2 * static_cast<size_t>(std::max(tmp.max_slots, 1)));
+        bool bound_mismatch = false;
         auto rcp = [](double x) { return 1.0 / x; };
         for (int c = 0; c < ncell; ++c) {
             const int nb = tmp.cell_node_begin[c];
@@ -2280,7 +2281,21 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     chunk_forward_math(
                         q.parent_slot != kNone, in,
                         [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp, cdd,
-                        cee);
+                        cee, ri[r].maxlen);
+                    {
+                        // the round's length bound skips padding iterations only:
+                        // the full-length recurrence gives the same bits
+                        double D2[kChunk], U2[kChunk], W2[kChunk], cd2, ce2;
+                        chunk_forward_math(
+                            q.parent_slot != kNone, in,
+                            [&](int k, double Dk, double uk, double wk) { D2[k] = Dk; U2[k] = uk; W2[k] = wk; }, rcp,
+                            cd2, ce2);
+                        bool same = std::memcmp(&cd2, &cdd, sizeof cdd) == 0 && std::memcmp(&ce2, &cee, sizeof cee) == 0;
+                        for (int k = 0; k < q.len; ++k)
+                            same = same && std::memcmp(&D2[k], &D[k], 8) == 0 && std::memcmp(&U2[k], &U[k], 8) == 0 &&
+                                   std::memcmp(&W2[k], &W[k], 8) == 0;
+                        if (!same || q.len > ri[r].maxlen) bound_mismatch = true;
+                    }
                     for (int k = 0; k < q.len; ++k) {
                         arr[SA_DB][idx[k]] = D[k];
                         arr[SA_RM][idx[k]] = U[k];
@@ -2296,8 +2311,13 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     const ChunkDesc& q = cd[ri[r].desc_begin + l];
                     positions(r, l, q.len);
                     const double vpar = q.parent_slot != kNone ? slots[2 * q.parent_slot] : 0.0;
-                    double VN[kChunk], X[kChunk];
-                    chunk_back_math(in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
+                    double VN[kChunk], X[kChunk], VN2[kChunk], X2[kChunk];
+                    chunk_back_math(in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar,
+                                    ri[r].maxlen);
+                    chunk_back_math(in, [&](int k, double vn, double x) { VN2[k] = vn; X2[k] = x; }, vpar);
+                    for (int k = 0; k < q.len; ++k)
+                        if (std::memcmp(&VN[k], &VN2[k], 8) != 0 || std::memcmp(&X[k], &X2[k], 8) != 0)
+                            bound_mismatch = true;
                     for (int k = 0; k < q.len; ++k) {
                         arr[SA_V][idx[k]] = VN[k];
                         arr[SA_RM][idx[k]] = X[k];
@@ -2305,6 +2325,7 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     slots[2 * q.slot] = VN[q.len - 1];
                 }
         }
+        if (bound_mismatch) return -2;
         std::vector<double>& gv = arr[SA_V];
         for (int i = 0; i < N; ++i) v[i] = gv[tmp.node_perm[i]];
         if (nchunk_max) *nchunk_max = tmp.max_slots;

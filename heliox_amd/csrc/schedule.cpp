@@ -112,8 +112,9 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         info.desc_begin = static_cast<uint16_t>(out.desc.size());
         info.desc_count = static_cast<uint16_t>(rounds[ri].size());
         info.node_base = static_cast<uint16_t>(round_base[ri]);
-        int cnt = 0;
+        int cnt = 0, maxlen = 0;
         for (int q : rounds[ri]) {
+            maxlen = std::max(maxlen, chunks[q].len);
             ChunkDesc d{};
             d.len = static_cast<uint8_t>(chunks[q].len);
             d.slot = static_cast<uint16_t>(q);
@@ -125,6 +126,7 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
             cnt += chunks[q].len;
         }
         info.node_count = static_cast<uint16_t>(cnt);
+        info.maxlen = static_cast<uint8_t>(maxlen);
         // off[k] = number of the round's nodes at positions < k (chunks sorted by length)
         int off = 0;
         for (int k = 0; k < kChunk; ++k) {

@@ -66,15 +66,24 @@ __host__ __device__ __forceinline__ void tail_inject(double& db, double& rm, dou
 // the caller for k >= len).  cd, ce: this chunk's pair for its parent.
 // Node k-1's inputs are fetched before node k's results are handed out, so a
 // caller reading and writing one buffer overlaps the read with the math.
+// kmax (<= kChunk, the same on every lane of a round) bounds the chunk
+// lengths: nodes k >= kmax are padding on every lane, and a padding node maps
+// the recurrence state (P1 = 1, r1 = 1, a1 = ab1 = accr = 0) onto itself, so
+// those iterations are skipped without changing any result.
 template <class In, class Out, class Rcp>
 __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, const In& in, Out&& out, Rcp rcp,
-                                                            double& cd, double& ce) {
+                                                            double& cd, double& ce, int kmax = kChunk) {
     double P1 = 1.0, P2 = 0.0, r1 = 1.0, a1 = 0.0, ab1 = 0.0, accr = 0.0;
     cd = 0.0;
     ce = 0.0;
-    FwdNode cur = in.fwd(kChunk - 1);
+    FwdNode cur{};
+    if (kmax == kChunk) cur = in.fwd(kChunk - 1);
 #pragma unroll
     for (int k = kChunk - 1; k >= 0; --k) {
+        if (k >= kmax) {
+            if (k == kmax) cur = in.fwd(k - 1);
+            continue;
+        }
         FwdNode nxt{};
         if (k > 0) nxt = in.fwd(k - 1);
         double a = cur.a, b = cur.b;
@@ -107,15 +116,18 @@ __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, con
 
 // in.back(k): node k's (u, w, v) (neutral for k >= len); vpar_new: updated
 // voltage of the head's parent (0 for the root chunk, whose w_0 is 0).
-// out(k, v_new, x).
+// out(k, v_new, x).  kmax as for the elimination: nodes k >= kmax are padding
+// on every lane and are skipped.
 template <class In, class Out>
-__host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new) {
+__host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new, int kmax = kChunk) {
     double x = vpar_new;
+    if (kmax <= 0) return;
     BackNode cur = in.back(0);
 #pragma unroll
     for (int k = 0; k < kChunk; ++k) {
+        if (k >= kmax) break;
         BackNode nxt{};
-        if (k + 1 < kChunk) nxt = in.back(k + 1);
+        if (k + 1 < kChunk && k + 1 < kmax) nxt = in.back(k + 1);
         x = fma(-cur.w, x, cur.u);
         out(k, cur.v + x, x);
         cur = nxt;

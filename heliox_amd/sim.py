@@ -696,6 +696,8 @@ def emulate_tree_solve(ncell, parent, a, b, cm, cfac, v, d, rhs):
     nr = C.c_int()
     rc = L.hx_emulate_tree_solve(int(ncell), parent.size, _ip(parent), _dp(a), _dp(b), _dp(cm), float(cfac),
                                  _dp(vv), _dp(d), _dp(rhs), C.byref(nc), C.byref(nr))
+    if rc == -2:
+        raise HelioxError("hx_emulate_tree_solve: the round length bound changed a result")
     if rc != 0:
         raise HelioxError("hx_emulate_tree_solve failed")
     return vv, nc.value, nr.value

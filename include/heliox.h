@@ -258,7 +258,9 @@ int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches);
  * a diagnostic for CPU-only checks of the solver schedule): capacitance and
  * axial assembly, elimination and back substitution over the same chunk
  * schedule the kernel uses, then v += dv.  Arrays are in node order; d and rhs
- * hold the membrane-mechanism diagonal and right-hand side. */
+ * hold the membrane-mechanism diagonal and right-hand side.  Every chunk is
+ * also solved without its round's length bound; returns -2 if the two differ
+ * in any bit (the bound may only skip padding). */
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max);
