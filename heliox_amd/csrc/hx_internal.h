@@ -2,7 +2,8 @@
 //
 // HBM layout (one model per handle):
 //   * node arrays (v, d, rhs, a, b, cm, area) are stored in solver order:
-//     cells are contiguous, and inside a cell nodes are grouped in chunks
+//     cells are gathered into solve units of a few consecutive cells, units
+//     are contiguous, and inside a unit its cells' nodes are grouped in chunks
 //     (unbranched runs of at most kChunk nodes) ordered root-round first;
 //   * every mechanism is a structure of arrays: column c of mechanism m lives
 //     at base + c * stride (stride = instance count rounded up to 64), and
@@ -93,15 +94,16 @@ struct StepArgs {
     MechConsts c;
 };
 
-// Chunked tree-solve schedule (one wavefront per cell).  Indices are relative
-// to the cell (cells are limited to 65535 nodes and 65535 chunks), so a
-// descriptor packs into 8 bytes.
+// Chunked tree-solve schedule (one wavefront per solve unit: a few
+// consecutive cells solved as one forest).  Indices are relative to the unit
+// (units are limited to 65535 nodes and 65535 chunks), so a descriptor packs
+// into 8 bytes.
 constexpr int kBlock = 256;       // threads per block of the node-parallel kernels
 constexpr uint16_t kNone = 0xFFFF;
 constexpr int kChunk = 16;        // max nodes per chunk (one lane's serial run)
 constexpr int kWave = 64;
 constexpr int kMaxCellNodes = 65535;
-constexpr int kRoundMax = 192;    // max nodes per round (one LDS stage)
+constexpr int kRoundMax = 384;    // max nodes per round (one LDS stage)
 constexpr int kPer = kRoundMax / kWave;   // stage elements per lane per array
 
 struct ChunkDesc {
@@ -113,8 +115,8 @@ struct ChunkDesc {
 };
 static_assert(sizeof(ChunkDesc) == 8, "ChunkDesc must stay 8 bytes");
 
-// One round of a cell's schedule: its descriptors and its contiguous,
-// position-major block of nodes (all cell-relative).  Node k of the chunk on
+// One round of a unit's schedule: its descriptors and its contiguous,
+// position-major block of nodes (all unit-relative).  Node k of the chunk on
 // lane l sits at node_base + off[k] + l, where off[k] = sum_{j<k} W_j and W_j
 // is the number of the round's chunks longer than j.
 struct alignas(16) RoundInfo {
@@ -122,18 +124,18 @@ struct alignas(16) RoundInfo {
     uint16_t desc_count;
     uint16_t node_base;
     uint16_t node_count;
-    uint8_t off[kChunk];
+    uint16_t off[kChunk];
     uint8_t maxlen;        // longest chunk of the round (0 for a padding round)
     uint8_t pad8[3];
     uint32_t pad;
 };
-static_assert(sizeof(RoundInfo) == 32, "RoundInfo must stay 32 bytes");
+static_assert(sizeof(RoundInfo) == 48, "RoundInfo must stay 48 bytes");
 
 struct SolveArgs {
-    int ncell;
-    const int* cell_node_begin;   // [ncell+1] first solver-order node of each cell
-    const int* cell_desc_begin;   // [ncell+1] first descriptor of each cell
-    const int* cell_round_begin;  // [ncell+1] first round of each cell
+    int nunit;
+    const int* unit_node_begin;   // [nunit+1] first solver-order node of each solve unit
+    const int* unit_desc_begin;   // [nunit+1] first descriptor of each unit
+    const int* unit_round_begin;  // [nunit+1] first round of each unit
     const RoundInfo* rounds;
     const ChunkDesc* desc;
     double* v;
@@ -262,12 +264,15 @@ struct VecPlayDev {
 };
 
 // LDS of the solve kernel: two junction values per chunk, then one round
-// stage of kStageArrays arrays, each with a neutral entry and kSinkWays write
-// sinks after its kRoundMax nodes (padding writes of a 16-lane LDS access group
-// land on 16 different banks pairs instead of one address).
+// stage of kStageArrays arrays, each with a neutral entry after its kRoundMax
+// nodes.
 constexpr int kStageArrays = 5;
-constexpr int kSinkWays = 16;
-constexpr int kStageStride = kRoundMax + 1 + kSinkWays;
+constexpr int kStageStride = kRoundMax + 1;
+// Solve units: the default unit size aims at about kSolveUnitTarget units in
+// all (one wavefront per SIMD of the chip), and a unit's LDS stays within
+// kUnitLdsBudget so that four units fit in a CU's 160 KB.
+constexpr int kSolveUnitTarget = 1024;
+constexpr size_t kUnitLdsBudget = 40 * 1024;
 inline size_t solve_lds_bytes(int max_chunks) {
     const int mc = max_chunks > 0 ? max_chunks : 1;
     return static_cast<size_t>(mc) * 2 * sizeof(double) +

@@ -13,7 +13,8 @@
 //                    nodes (instance-parallel, gather v / update d, rhs)
 //   k_point<M> ..... point-process currents (IClamp, ExpSyn, Exp2Syn, HalfGap),
 //                    scaled by 1e2/area and accumulated with fp64 atomics
-//   k_solve ........ one wavefront per cell: capacitance + axial assembly, the
+//   k_solve ........ one wavefront per solve unit (a few consecutive cells):
+//                    capacitance + axial assembly, the
 //                    Hines elimination over chunked unbranched runs, back
 //                    substitution and v update; junction values through LDS
 //   k_spike ........ threshold detection, wave-ballot compaction into the spike
@@ -507,7 +508,10 @@ __global__ void k_set_v(double* v, int n, double val) {
 }
 
 // ---------------------------------------------------------------------------
-// Tree solve: one wavefront per cell.  Forward rounds run leaves -> root, each
+// Tree solve: one wavefront per solve unit, a forest of a few consecutive
+// cells (a wavefront issues the same instructions however many of its lanes
+// carry a chunk, so packing cells into one wavefront divides the issue work
+// of the whole solve).  Forward rounds run leaves -> root, each
 // lane eliminating one chunk (an unbranched run of <= kChunk nodes) into its
 // parent; the head's contribution to the parent chunk's tail is passed through
 // an LDS slot.  Back substitution runs the rounds in reverse.
@@ -524,7 +528,6 @@ __device__ __forceinline__ void round_boundary() {
 }
 
 constexpr int kNeutral = kRoundMax;       // stage entry holding the padding value
-constexpr int kSink = kRoundMax + 1;      // first of the kSinkWays entries absorbing padding writes
 
 // 1/x: hardware reciprocal estimate refined by two Newton-Raphson steps
 // (each step squares the relative error), correct to about an ulp.
@@ -541,30 +544,35 @@ __device__ __forceinline__ double rcp_nr(double x) {
 // to wait for the round's vector stores), then moves them to uniform
 // registers.
 struct RoundV {
-    uint4 lo, hi;
+    uint4 x0, x1, x2;
 };
+static_assert(sizeof(RoundV) == sizeof(RoundInfo), "RoundV mirrors RoundInfo");
 struct RoundU {
     int desc_begin, desc_count, node_base, node_count, maxlen;
-    uint32_t off[4];      // off[k] in byte k % 4 of off[k / 4]
-    __device__ __forceinline__ int offset(int k) const { return (off[k >> 2] >> (8 * (k & 3))) & 0xFF; }
+    uint32_t off[kChunk / 2];      // off[k] in half k % 2 of off[k / 2]
+    __device__ __forceinline__ int offset(int k) const { return (off[k >> 1] >> (16 * (k & 1))) & 0xFFFF; }
 };
 __device__ __forceinline__ RoundV load_round(const RoundInfo* rounds, int r) {
     const uint4* p = reinterpret_cast<const uint4*>(rounds + r);
-    return {p[0], p[1]};
+    return {p[0], p[1], p[2]};
 }
 __device__ __forceinline__ RoundU uniform_round(const RoundV& v) {
     RoundU u;
-    const uint32_t w0 = __builtin_amdgcn_readfirstlane(v.lo.x);
-    const uint32_t w1 = __builtin_amdgcn_readfirstlane(v.lo.y);
+    const uint32_t w0 = __builtin_amdgcn_readfirstlane(v.x0.x);
+    const uint32_t w1 = __builtin_amdgcn_readfirstlane(v.x0.y);
     u.desc_begin = w0 & 0xFFFF;
     u.desc_count = w0 >> 16;
     u.node_base = w1 & 0xFFFF;
     u.node_count = w1 >> 16;
-    u.off[0] = __builtin_amdgcn_readfirstlane(v.lo.z);
-    u.off[1] = __builtin_amdgcn_readfirstlane(v.lo.w);
-    u.off[2] = __builtin_amdgcn_readfirstlane(v.hi.x);
-    u.off[3] = __builtin_amdgcn_readfirstlane(v.hi.y);
-    u.maxlen = __builtin_amdgcn_readfirstlane(v.hi.z) & 0xFF;
+    u.off[0] = __builtin_amdgcn_readfirstlane(v.x0.z);
+    u.off[1] = __builtin_amdgcn_readfirstlane(v.x0.w);
+    u.off[2] = __builtin_amdgcn_readfirstlane(v.x1.x);
+    u.off[3] = __builtin_amdgcn_readfirstlane(v.x1.y);
+    u.off[4] = __builtin_amdgcn_readfirstlane(v.x1.z);
+    u.off[5] = __builtin_amdgcn_readfirstlane(v.x1.w);
+    u.off[6] = __builtin_amdgcn_readfirstlane(v.x2.x);
+    u.off[7] = __builtin_amdgcn_readfirstlane(v.x2.y);
+    u.maxlen = __builtin_amdgcn_readfirstlane(v.x2.z) & 0xFF;
     return u;
 }
 
@@ -585,26 +593,51 @@ struct BackBuf {
 
 struct SolveCtx {
     const SolveArgs& S;
-    const RoundInfo* __restrict__ rounds;   // this cell's rounds
-    const uint2* __restrict__ desc;         // this cell's descriptors
-    int nb;                                 // first node of the cell
+    // Not __restrict__: with it the compiler proves the tables unwritten and turns
+    // their uniform reads into scalar loads, whose waits share the LDS counter
+    // and drain it; as vector loads they are requested a round ahead.
+    const RoundInfo* rounds;                // this unit's rounds
+    const uint2* desc;                      // this unit's descriptors
+    int nb;                                 // first node of the unit
+    int nn;                                 // nodes of the unit
     double* slots;                          // LDS, 2 per chunk
     double* stage;                          // LDS, kStageArrays x kStageStride
     int lane;
 };
 
-// Stage positions of the lane's chunk: read from the neutral entry and write
-// to a sink past the chunk's length; tp = position of the tail.
-__device__ __forceinline__ void round_positions(const RoundU& ri, int len, int lane, int* rp, int* wp, int& tp) {
+// Results leave the solve as raw buffer stores on a descriptor that spans the
+// unit's nodes; a store whose offset lies past the descriptor's range is
+// dropped by the hardware, which is how padding slots are masked without a
+// branch (kDrop is far past any unit: units hold at most 65535 nodes).
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kBufferConfig = 0x00020000;   // raw buffer, 32-bit data format (CDNA)
+constexpr int kDrop = static_cast<int>(0x80000000u);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cell_buffer(double* base, int nnode) {
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, nnode * static_cast<int>(sizeof(double)), kBufferConfig);
+}
+__device__ __forceinline__ void store_f64(__amdgpu_buffer_rsrc_t r, int byte_offset, double x) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, x), r, byte_offset, 0, 0);
+}
+
+// Stage positions of the first KM slots of the lane's chunk (the neutral
+// entry past the chunk's length), byte offsets of its nodes in the unit (kDrop
+// past the length) and tp, the position of the tail.
+template <int KM>
+__device__ __forceinline__ void round_positions(const RoundU& ri, int len, int lane, int* rp, int* wo, int& tp) {
     tp = kNeutral;
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) {
+    for (int k = 0; k < KM; ++k) {
         const int p = ri.offset(k) + lane;
         rp[k] = k < len ? p : kNeutral;
-        wp[k] = k < len ? p : kSink + (lane & (kSinkWays - 1));
+        wo[k] = k < len ? (ri.node_base + p) * static_cast<int>(sizeof(double)) : kDrop;
         if (k == len - 1) tp = p;
     }
 }
+
+// A chunk hands its parent the pair (cd, ce) through one 16-byte LDS slot.
+struct SlotPair {
+    double cd, ce;
+};
 
 struct StageIn {
     const double* st;
@@ -671,42 +704,48 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
     const int child_begin = q.y & 0xFFFF;
     const int len = act ? (q.y >> 16) & 0xFF : 0;
     const int nchild = act ? q.y >> 24 : 0;
-    int rp[kChunk], wp[kChunk], tp;
-    round_positions(ri, len, C.lane, rp, wp, tp);
+    SlotPair* pairs = reinterpret_cast<SlotPair*>(C.slots);
+    // the children's terms, summed in child order (the first two unrolled)
+    double acd = 0.0, ace = 0.0;
     if (nchild > 0) {
-        double acd = 0.0, ace = 0.0;
-        for (int ch = 0; ch < nchild; ++ch) {
-            acd += C.slots[2 * (child_begin + ch)];
-            ace += C.slots[2 * (child_begin + ch) + 1];
+        const SlotPair p0 = pairs[child_begin];
+        acd = p0.cd;
+        ace = p0.ce;
+        if (nchild > 1) {
+            const SlotPair p1 = pairs[child_begin + 1];
+            acd += p1.cd;
+            ace += p1.ce;
+            for (int ch = 2; ch < nchild; ++ch) {
+                const SlotPair pc = pairs[child_begin + ch];
+                acd += pc.cd;
+                ace += pc.ce;
+            }
         }
-        double db = st[SA_DB * kStageStride + tp], rm = st[SA_RM * kStageStride + tp];
-        tail_inject(db, rm, st[SA_V * kStageStride + tp], acd, ace);
-        st[SA_DB * kStageStride + tp] = db;
-        st[SA_RM * kStageStride + tp] = rm;
     }
+    // results go straight to HBM: node k of the lane's chunk sits at offset(k) + lane
+    // of the round's block, so each store instruction writes contiguous memory
+    const __amdgpu_buffer_rsrc_t rd = cell_buffer(C.S.d + C.nb, C.nn);
+    const __amdgpu_buffer_rsrc_t ru = cell_buffer(C.S.rhs + C.nb, C.nn);
+    const __amdgpu_buffer_rsrc_t rw = cell_buffer(C.S.w + C.nb, C.nn);
     double cd, ce;
-    chunk_forward_math(
-        has_parent, StageIn{st, rp},
-        [&](int k, double D, double u, double w) {
-            st[SA_DB * kStageStride + wp[k]] = D;
-            st[SA_RM * kStageStride + wp[k]] = u;
-            st[SA_B * kStageStride + wp[k]] = w;
-        },
-        rcp_nr, cd, ce, ri.maxlen);
-    if (act && has_parent) {
-        C.slots[2 * slot] = cd;
-        C.slots[2 * slot + 1] = ce;
-    }
-    round_boundary();
-    // a padding round writes back node 0's staged values unchanged
-    const int base = C.nb + ri.node_base;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const unsigned e = clamp_index(C.lane, j, ri.node_count);
-        C.S.d[base + e] = st[SA_DB * kStageStride + e];
-        C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
-        C.S.w[base + e] = st[SA_B * kStageStride + e];
-    }
+    dispatch_chunk_bound(ri.maxlen, [&](auto km) {
+        constexpr int KM = decltype(km)::value;
+        int rp[KM], wo[KM], tp;
+        round_positions<KM>(ri, len, C.lane, rp, wo, tp);
+        if (nchild > 0) {
+            double db = st[SA_DB * kStageStride + tp], rm = st[SA_RM * kStageStride + tp];
+            tail_inject(db, rm, st[SA_V * kStageStride + tp], acd, ace);
+            st[SA_DB * kStageStride + tp] = db;
+            st[SA_RM * kStageStride + tp] = rm;
+        }
+        auto out = [&](int k, double D, double u, double w) {
+            store_f64(rd, wo[k], D);
+            store_f64(ru, wo[k], u);
+            store_f64(rw, wo[k], w);
+        };
+        chunk_forward_math<KM>(has_parent, StageIn{st, rp}, out, rcp_nr, cd, ce);
+    });
+    if (act && has_parent) pairs[slot] = SlotPair{cd, ce};
     round_boundary();
 }
 
@@ -745,23 +784,21 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, 
     const int parent_slot = q.x >> 16;
     const int len = act ? (q.y >> 16) & 0xFF : 0;
     const double vpar = (act && parent_slot != kNone) ? C.slots[2 * parent_slot] : 0.0;
-    int rp[kChunk], wp[kChunk], tp;
-    round_positions(ri, len, C.lane, rp, wp, tp);
-    chunk_back_math(StageIn{st, rp},
-                    [&](int k, double vn, double x) {
-                        st[SA_V * kStageStride + wp[k]] = vn;
-                        st[SA_RM * kStageStride + wp[k]] = x;
-                    },
-                    vpar, ri.maxlen);
-    if (act) C.slots[2 * slot] = st[SA_V * kStageStride + tp];   // the tail's new voltage
-    round_boundary();
-    const int base = C.nb + ri.node_base;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const unsigned e = clamp_index(C.lane, j, ri.node_count);
-        C.S.v[base + e] = st[SA_V * kStageStride + e];
-        C.S.rhs[base + e] = st[SA_RM * kStageStride + e];
-    }
+    const __amdgpu_buffer_rsrc_t rv = cell_buffer(C.S.v + C.nb, C.nn);
+    const __amdgpu_buffer_rsrc_t rx = cell_buffer(C.S.rhs + C.nb, C.nn);
+    double vtail = 0.0;
+    dispatch_chunk_bound(ri.maxlen, [&](auto km) {
+        constexpr int KM = decltype(km)::value;
+        int rp[KM], wo[KM], tp;
+        round_positions<KM>(ri, len, C.lane, rp, wo, tp);
+        auto out = [&](int k, double vn, double x) {
+            store_f64(rv, wo[k], vn);
+            store_f64(rx, wo[k], x);
+            if (k == len - 1) vtail = vn;
+        };
+        chunk_back_math<KM>(StageIn{st, rp}, out, vpar);
+    });
+    if (act) C.slots[2 * slot] = vtail;   // the tail's new voltage
     round_boundary();
 }
 
@@ -771,29 +808,36 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, 
 // steady state (one round's stores after the buffer's loads).
 __device__ __forceinline__ void drain_vector_memory() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// One wavefront per cell.  Elimination walks the rounds from the leaves
+// One wavefront per unit.  Elimination walks the rounds from the leaves
 // (round nround-1) to the root, back substitution from the root out.  While a
 // round is solved from one register buffer, the next round's data is loaded
 // into the other (a round takes longer than an HBM round trip); the round-table
-// entry is fetched a round earlier still.  A cell's round count is even (the
+// entry is fetched a round earlier still.  A unit's round count is even (the
 // schedule appends a padding round with no chunks when needed), so each loop
 // trip solves two rounds and the buffers never trade registers.  Round indices
 // past either end are clamped to a real round, whose loads are issued but
 // never used.
-__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* __restrict__ rounds_all,
-                                                 const uint2* __restrict__ desc, int max_chunks) {
+__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* rounds_all, const uint2* desc,
+                                                 int max_chunks) {
     extern __shared__ double lds[];
     const int c = blockIdx.x;
     const int lane = threadIdx.x;
-    const int rb = S.cell_round_begin[c];
-    const int nround = S.cell_round_begin[c + 1] - rb;
+    const int rb = S.unit_round_begin[c];
+    const int nround = S.unit_round_begin[c + 1] - rb;
     const int last = nround - 1;
     double* slots = lds;
     double* stage = slots + 2 * max_chunks;
     if (lane < kStageArrays) stage[lane * kStageStride + kNeutral] = lane == SA_DB ? 1.0 : 0.0;
     round_boundary();
     const RoundInfo* rounds = rounds_all + rb;
-    const SolveCtx C{S, rounds, desc + S.cell_desc_begin[c], S.cell_node_begin[c], slots, stage, lane};
+    const SolveCtx C{S,
+                     rounds,
+                     desc + S.unit_desc_begin[c],
+                     S.unit_node_begin[c],
+                     S.unit_node_begin[c + 1] - S.unit_node_begin[c],
+                     slots,
+                     stage,
+                     lane};
     auto fwd_idx = [&](int r) { return r > 0 ? r : 0; };
     auto back_idx = [&](int r) { return r < last ? r : last; };
 
@@ -1060,9 +1104,9 @@ void launch_set_v(double* v, int n, double val, hipStream_t s) {
 }
 
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
-    if (a.ncell <= 0) return;
+    if (a.nunit <= 0) return;
     const size_t lds = solve_lds_bytes(max_chunks);
-    hipLaunchKernelGGL(k_solve, dim3(a.ncell), dim3(kWave), lds, s, a, a.rounds,
+    hipLaunchKernelGGL(k_solve, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
                        reinterpret_cast<const uint2*>(a.desc), max_chunks);
 }
 

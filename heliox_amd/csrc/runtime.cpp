@@ -205,12 +205,16 @@ struct hx_sim {
 
     // layout
     std::vector<int> node_perm, node_iperm;    // user <-> solver order
-    std::vector<int> cell_node_begin, cell_desc_begin, cell_round_begin;
+    // solve units: runs of consecutive cells, each solved by one wavefront
+    std::vector<int> unit_cell_begin, unit_node_begin, unit_desc_begin, unit_round_begin;
+    int nunit = 0;
+    int unit_cells = 1;                  // cells per unit of the current layout
+    int unit_request = 0;                // 0: the library's choice
     // the solver's tree (user node indices) and its coupling coefficients
     std::vector<int> solve_parent;
     std::vector<double> solve_a, solve_b;
     bool solve_root_centre = true;
-    std::vector<RoundInfo> rounds;       // all cells' rounds, cell by cell
+    std::vector<RoundInfo> rounds;       // all units' rounds, unit by unit
     std::vector<ChunkDesc> descs;
     int max_slots = 0, max_rounds = 0;
     int ion_type_uniform[3] = {-1, -1, -1};
@@ -225,7 +229,7 @@ struct hx_sim {
     double *d_sa = nullptr, *d_sb = nullptr;   // solver coefficients (solver tree), node order
     double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
            *d_area = nullptr, *d_w = nullptr;
-    int *d_cell_node_begin = nullptr, *d_cell_desc_begin = nullptr, *d_cell_round_begin = nullptr;
+    int *d_unit_node_begin = nullptr, *d_unit_desc_begin = nullptr, *d_unit_round_begin = nullptr;
     RoundInfo* d_rounds = nullptr;
     ChunkDesc* d_desc = nullptr;
     // spikes / events
@@ -253,7 +257,7 @@ struct hx_sim {
     // detection, synapse decay -- is issued on a stream of its own, so one
     // group's latency-bound solve overlaps another group's HBM-bound node pass.
     struct CellGroup {
-        int node0 = 0, node1 = 0, cell0 = 0, cell1 = 0;
+        int node0 = 0, node1 = 0, cell0 = 0, cell1 = 0, unit0 = 0, unit1 = 0;
         int pre0 = 0, pre1 = 0;                   // detectors (sorted by node)
         int es0 = 0, es1 = 0, e20 = 0, e21 = 0;   // ExpSyn / Exp2Syn instances
         int inst0[M_COUNT] = {}, inst1[M_COUNT] = {};   // instances of mechanisms outside the node kernel
@@ -523,16 +527,6 @@ void hx_sim::build_layout() {
     std::vector<int> cnodes(nnode), fill(cbeg.begin(), cbeg.end() - 1);
     for (int i = 0; i < nnode; ++i) cnodes[fill[cell_of[i]]++] = i;   // increasing user index per cell
     std::vector<int> local(nnode);
-    node_perm.assign(nnode, -1);
-    node_iperm.assign(nnode, -1);
-    cell_node_begin.assign(ncell + 1, 0);
-    cell_desc_begin.assign(ncell + 1, 0);
-    cell_round_begin.assign(ncell + 1, 0);
-    rounds.clear();
-    descs.clear();
-    max_slots = 0;
-    max_rounds = 0;
-    int pos = 0;
     // The solve may eliminate toward any node of a cell: the matrix and its
     // solution do not depend on the root, and the axial assembly is the same
     // once a and b trade places on every reversed edge.  Each cell is rooted at
@@ -541,6 +535,7 @@ void hx_sim::build_layout() {
     solve_parent.assign(nnode, -1);
     solve_a.assign(nnode, 0.0);
     solve_b.assign(nnode, 0.0);
+    std::vector<std::vector<int>> cbfs(ncell), cspl(ncell);   // per cell: BFS order, solver-local parents
     for (int c = 0; c < ncell; ++c) {
         const int n = cnt[c];
         std::vector<int> lp(n);
@@ -551,16 +546,9 @@ void hx_sim::build_layout() {
         }
         // solver tree: BFS from the root, relabelled so that parent < child
         const int root = solve_root_centre ? tree_centre(lp) : 0;
-        std::vector<int> bfs, spl;   // BFS order (original local ids), solver-local parents
+        std::vector<int>& bfs = cbfs[c];
+        std::vector<int>& spl = cspl[c];
         reroot_tree(lp, root, bfs, spl);
-        CellSchedule cs;
-        build_cell_schedule(spl, kChunk, kWave, kRoundMax, cs);
-        cell_node_begin[c] = pos;
-        for (int s = 0; s < n; ++s) {
-            const int u = cnodes[cbeg[c] + bfs[cs.order[s]]];
-            node_perm[u] = pos + s;
-            node_iperm[pos + s] = u;
-        }
         for (int j = 0; j < n; ++j) {
             if (spl[j] < 0) continue;
             const int u = cnodes[cbeg[c] + bfs[j]];
@@ -574,17 +562,70 @@ void hx_sim::build_layout() {
                 solve_b[u] = a[q];
             }
         }
-        pos += n;
-        cell_desc_begin[c] = static_cast<int>(descs.size());
-        cell_round_begin[c] = static_cast<int>(rounds.size());
-        for (auto& d : cs.desc) descs.push_back(d);
-        for (auto& r : cs.rounds) rounds.push_back(r);
-        max_slots = std::max(max_slots, cs.nchunk);
-        max_rounds = std::max(max_rounds, cs.nround);
     }
-    cell_node_begin[ncell] = pos;
-    cell_desc_begin[ncell] = static_cast<int>(descs.size());
-    cell_round_begin[ncell] = static_cast<int>(rounds.size());
+    // Solve units: runs of consecutive cells, each solved by one wavefront as
+    // a forest.  By default a unit holds about ncell / kSolveUnitTarget cells,
+    // so the whole solve runs about one wavefront per SIMD; a unit whose
+    // schedule would need more than kUnitLdsBudget of LDS is split further.
+    auto build_units = [&](int U) {
+        node_perm.assign(nnode, -1);
+        node_iperm.assign(nnode, -1);
+        nunit = (ncell + U - 1) / U;
+        unit_cell_begin.assign(nunit + 1, 0);
+        unit_node_begin.assign(nunit + 1, 0);
+        unit_desc_begin.assign(nunit + 1, 0);
+        unit_round_begin.assign(nunit + 1, 0);
+        rounds.clear();
+        descs.clear();
+        max_slots = 0;
+        max_rounds = 0;
+        int pos = 0;
+        for (int k = 0; k < nunit; ++k) {
+            const int c0 = k * U, c1 = std::min(ncell, c0 + U);
+            std::vector<int> fp;                 // forest parents, cells one after another
+            std::vector<int> fnode;              // forest index -> user node
+            for (int c = c0; c < c1; ++c) {
+                const int off = static_cast<int>(fp.size());
+                for (size_t j = 0; j < cbfs[c].size(); ++j) {
+                    fp.push_back(cspl[c][j] < 0 ? -1 : off + cspl[c][j]);
+                    fnode.push_back(cnodes[cbeg[c] + cbfs[c][j]]);
+                }
+            }
+            UnitSchedule us;
+            build_unit_schedule(fp, kChunk, kWave, kRoundMax, us);
+            if (U > 1 && solve_lds_bytes(us.nchunk) > kUnitLdsBudget) return false;
+            unit_cell_begin[k] = c0;
+            unit_node_begin[k] = pos;
+            unit_desc_begin[k] = static_cast<int>(descs.size());
+            unit_round_begin[k] = static_cast<int>(rounds.size());
+            const int n = static_cast<int>(fp.size());
+            for (int s = 0; s < n; ++s) {
+                const int u = fnode[us.order[s]];
+                node_perm[u] = pos + s;
+                node_iperm[pos + s] = u;
+            }
+            pos += n;
+            for (auto& d : us.desc) descs.push_back(d);
+            for (auto& r : us.rounds) rounds.push_back(r);
+            max_slots = std::max(max_slots, us.nchunk);
+            max_rounds = std::max(max_rounds, us.nround);
+        }
+        unit_cell_begin[nunit] = ncell;
+        unit_node_begin[nunit] = pos;
+        unit_desc_begin[nunit] = static_cast<int>(descs.size());
+        unit_round_begin[nunit] = static_cast<int>(rounds.size());
+        return true;
+    };
+    int U = unit_request > 0 ? unit_request
+                             : std::max(1, static_cast<int>(std::lround(static_cast<double>(ncell) / kSolveUnitTarget)));
+    U = std::max(1, std::min(U, ncell));
+    while (!build_units(U)) {
+        if (unit_request > 0)
+            throw std::runtime_error("solve units of " + std::to_string(U) + " cells need more than " +
+                                     std::to_string(kUnitLdsBudget) + " B of LDS; use fewer cells per unit");
+        U = std::max(1, U / 2);
+    }
+    unit_cells = U;
 
     // mechanism instance order: by solver-order node (stable)
     for (int id = 0; id < M_COUNT; ++id) {
@@ -655,9 +696,9 @@ void hx_sim::upload() {
     d_sb = dupload(owned, perm_nodes(solve_b));
     d_cm = dupload(owned, perm_nodes(cm));
     d_area = dupload(owned, perm_nodes(area));
-    d_cell_node_begin = dupload(owned, cell_node_begin);
-    d_cell_desc_begin = dupload(owned, cell_desc_begin);
-    d_cell_round_begin = dupload(owned, cell_round_begin);
+    d_unit_node_begin = dupload(owned, unit_node_begin);
+    d_unit_desc_begin = dupload(owned, unit_desc_begin);
+    d_unit_round_begin = dupload(owned, unit_round_begin);
     d_rounds = dupload(owned, rounds);
     d_desc = dupload(owned, descs);
     {
@@ -667,7 +708,7 @@ void hx_sim::upload() {
         HXC(hipGetDeviceProperties(&prop, dev));
         const size_t lds = solve_lds_bytes(max_slots);
         if (lds > prop.sharedMemPerBlock)
-            throw std::runtime_error("a cell has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
+            throw std::runtime_error("a solve unit has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
                                      " B solver schedule exceeds the " + std::to_string(prop.sharedMemPerBlock) +
                                      " B of LDS per workgroup");
     }
@@ -845,28 +886,31 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
     int G = 1;
     if (!coupled) {
         G = group_request > 0 ? group_request : 2;
-        G = std::min(G, std::max(1, ncell / 8));
+        G = std::min(G, std::max(1, std::min(ncell / 8, nunit)));
     }
     // event ring geometry: one slot per step, enough slots to cover the longest delay
     const int steps = static_cast<int>(std::ceil(max_delay / dt)) + 4;
     int nslot = 8;
     while (nslot < steps) nslot <<= 1;
     groups.resize(G);
-    int c0 = 0;
+    // groups are runs of whole solve units of about equal node count
+    int u0 = 0;
     for (int g = 0; g < G; ++g) {
         CellGroup& cg = groups[g];
-        int c1 = ncell;
+        int u1 = nunit;
         if (g < G - 1) {
             const long long target = static_cast<long long>(nnode) * (g + 1) / G;
-            c1 = static_cast<int>(std::lower_bound(cell_node_begin.begin(), cell_node_begin.begin() + ncell, target) -
-                                  cell_node_begin.begin());
-            c1 = std::max(c1, c0 + 1);
+            u1 = static_cast<int>(std::lower_bound(unit_node_begin.begin(), unit_node_begin.begin() + nunit, target) -
+                                  unit_node_begin.begin());
+            u1 = std::min(std::max(u1, u0 + 1), nunit - (G - 1 - g));
         }
-        cg.cell0 = c0;
-        cg.cell1 = c1;
-        cg.node0 = cell_node_begin[c0];
-        cg.node1 = cell_node_begin[c1];
-        c0 = c1;
+        cg.unit0 = u0;
+        cg.unit1 = u1;
+        cg.cell0 = unit_cell_begin[u0];
+        cg.cell1 = unit_cell_begin[u1];
+        cg.node0 = unit_node_begin[u0];
+        cg.node1 = unit_node_begin[u1];
+        u0 = u1;
         auto range = [&](const std::vector<int>& nodes, int& b, int& e) {
             b = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node0) - nodes.begin());
             e = static_cast<int>(std::lower_bound(nodes.begin(), nodes.end(), cg.node1) - nodes.begin());
@@ -1376,10 +1420,10 @@ void hx_sim::step_once_groups() {
         if (pending && cg.mon1 > cg.mon0)
             hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
         SolveArgs S{};
-        S.ncell = cg.cell1 - cg.cell0;
-        S.cell_node_begin = d_cell_node_begin + cg.cell0;
-        S.cell_desc_begin = d_cell_desc_begin + cg.cell0;
-        S.cell_round_begin = d_cell_round_begin + cg.cell0;
+        S.nunit = cg.unit1 - cg.unit0;
+        S.unit_node_begin = d_unit_node_begin + cg.unit0;
+        S.unit_desc_begin = d_unit_desc_begin + cg.unit0;
+        S.unit_round_begin = d_unit_round_begin + cg.unit0;
         S.rounds = d_rounds;
         S.desc = d_desc;
         S.v = d_v;
@@ -1457,10 +1501,10 @@ void hx_sim::step_once() {
     }
     launch_point_currents(tmid);
     SolveArgs S{};
-    S.ncell = ncell;
-    S.cell_node_begin = d_cell_node_begin;
-    S.cell_desc_begin = d_cell_desc_begin;
-    S.cell_round_begin = d_cell_round_begin;
+    S.nunit = nunit;
+    S.unit_node_begin = d_unit_node_begin;
+    S.unit_desc_begin = d_unit_desc_begin;
+    S.unit_round_begin = d_unit_round_begin;
     S.rounds = d_rounds;
     S.desc = d_desc;
     S.v = d_v;
@@ -2160,6 +2204,13 @@ int hx_set_solver_root(hx_sim* sim, int centre) {
     return 0;
 }
 
+int hx_set_solve_unit_cells(hx_sim* sim, int cells) {
+    if (sim->loaded) return sim->fail("set the solve unit size before hx_load_model");
+    if (cells < 0) return sim->fail("solve unit size must be >= 0 (0: the library's choice)");
+    sim->unit_request = cells;
+    return 0;
+}
+
 int hx_set_group_streams(hx_sim* sim, int enable) {
     sim->group_streams_allowed = enable != 0;
     return 0;
@@ -2224,9 +2275,16 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max) {
+    return hx_emulate_tree_solve_units(ncell, nnode, parent, a, b, cm, cfac, v, d, rhs, 0, nchunk_max, nround_max);
+}
+
+int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const double* a, const double* b,
+                                const double* cm, double cfac, double* v, const double* d, const double* rhs,
+                                int unit_cells, int* nchunk_max, int* nround_max) {
     try {
         hx_sim tmp;
         if (hx_model_set_nodes(&tmp, ncell, nnode, parent, a, b, a) != 0) return -1;
+        tmp.unit_request = std::max(0, unit_cells);
         tmp.build_layout();
         const int N = nnode;
         // solver-order arrays: DB RM A B V (the kernel's stage arrays) and w
@@ -2244,11 +2302,11 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
         std::vector<double> slots(2 * static_cast<size_t>(std::max(tmp.max_slots, 1)));
         bool bound_mismatch = false;
         auto rcp = [](double x) { return 1.0 / x; };
-        for (int c = 0; c < ncell; ++c) {
-            const int nb = tmp.cell_node_begin[c];
-            const ChunkDesc* cd = tmp.descs.data() + tmp.cell_desc_begin[c];
-            const RoundInfo* ri = tmp.rounds.data() + tmp.cell_round_begin[c];
-            const int nround = tmp.cell_round_begin[c + 1] - tmp.cell_round_begin[c];
+        for (int c = 0; c < tmp.nunit; ++c) {
+            const int nb = tmp.unit_node_begin[c];
+            const ChunkDesc* cd = tmp.descs.data() + tmp.unit_desc_begin[c];
+            const RoundInfo* ri = tmp.rounds.data() + tmp.unit_round_begin[c];
+            const int nround = tmp.unit_round_begin[c + 1] - tmp.unit_round_begin[c];
             int idx[kChunk];
             auto positions = [&](int r, int l, int len) {
                 for (int k = 0; k < kChunk; ++k) idx[k] = k < len ? nb + ri[r].node_base + ri[r].off[k] + l : -1;
@@ -2278,15 +2336,17 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     // results are written after the chunk is done (the kernel writes
                     // in place; a node's inputs are read before its outputs exist)
                     double D[kChunk], U[kChunk], W[kChunk], cdd, cee;
-                    chunk_forward_math(
-                        q.parent_slot != kNone, in,
-                        [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp, cdd,
-                        cee, ri[r].maxlen);
+                    dispatch_chunk_bound(ri[r].maxlen, [&](auto km) {
+                        chunk_forward_math<decltype(km)::value>(
+                            q.parent_slot != kNone, in,
+                            [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp,
+                            cdd, cee);
+                    });
                     {
                         // the round's length bound skips padding iterations only:
                         // the full-length recurrence gives the same bits
                         double D2[kChunk], U2[kChunk], W2[kChunk], cd2, ce2;
-                        chunk_forward_math(
+                        chunk_forward_math<kChunk>(
                             q.parent_slot != kNone, in,
                             [&](int k, double Dk, double uk, double wk) { D2[k] = Dk; U2[k] = uk; W2[k] = wk; }, rcp,
                             cd2, ce2);
@@ -2312,9 +2372,11 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
                     positions(r, l, q.len);
                     const double vpar = q.parent_slot != kNone ? slots[2 * q.parent_slot] : 0.0;
                     double VN[kChunk], X[kChunk], VN2[kChunk], X2[kChunk];
-                    chunk_back_math(in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar,
-                                    ri[r].maxlen);
-                    chunk_back_math(in, [&](int k, double vn, double x) { VN2[k] = vn; X2[k] = x; }, vpar);
+                    dispatch_chunk_bound(ri[r].maxlen, [&](auto km) {
+                        chunk_back_math<decltype(km)::value>(
+                            in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
+                    });
+                    chunk_back_math<kChunk>(in, [&](int k, double vn, double x) { VN2[k] = vn; X2[k] = x; }, vpar);
                     for (int k = 0; k < q.len; ++k)
                         if (std::memcmp(&VN[k], &VN2[k], 8) != 0 || std::memcmp(&X[k], &X2[k], 8) != 0)
                             bound_mismatch = true;
@@ -2331,6 +2393,9 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
         if (nchunk_max) *nchunk_max = tmp.max_slots;
         if (nround_max) *nround_max = tmp.max_rounds;
         return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "hx_emulate_tree_solve: %s\n", e.what());
+        return -1;
     } catch (...) {
         return -1;
     }
@@ -2345,6 +2410,8 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "dense_mask") return sim->dense_mask;
     if (k == "fused") return sim->fused ? 1 : 0;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());
+    if (k == "solve_units") return sim->nunit;
+    if (k == "solve_unit_cells") return sim->unit_cells;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
@@ -2492,10 +2559,10 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.grad_gpas = sim->d_grad_gpas;
     A.grad_w = sim->d_grad_w;
     SolveArgs S{};
-    S.ncell = sim->ncell;
-    S.cell_node_begin = sim->d_cell_node_begin;
-    S.cell_desc_begin = sim->d_cell_desc_begin;
-    S.cell_round_begin = sim->d_cell_round_begin;
+    S.nunit = sim->nunit;
+    S.unit_node_begin = sim->d_unit_node_begin;
+    S.unit_desc_begin = sim->d_unit_desc_begin;
+    S.unit_round_begin = sim->d_unit_round_begin;
     S.rounds = sim->d_rounds;
     S.desc = sim->d_desc;
     S.v = sim->d_vT;

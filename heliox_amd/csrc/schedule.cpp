@@ -3,9 +3,12 @@
 // dynamic_interleave2 / admin_dynamic2), which packs cells into 32-lane groups
 // that rely on implicit warp lockstep (simulate.cu:119-189).
 //
-// Here every cell is solved by one 64-lane wavefront.  The cell's tree is cut
-// into chunks: unbranched runs of at most kChunk nodes (a node with exactly
-// one child continues its chunk).  A chunk's height is 0 for a leaf chunk and
+// Here a solve unit -- a few consecutive cells -- is solved by one 64-lane
+// wavefront: a unit is a forest, one tree per cell, and since a wavefront
+// issues the same instructions however many of its lanes have a chunk, a
+// unit of several cells costs little more per round than one cell.  Each
+// tree is cut into chunks: unbranched runs of at most kChunk nodes (a node
+// with exactly one child continues its chunk).  A chunk's height is 0 for a leaf chunk and
 // 1 + the largest child height otherwise; chunks of equal height are
 // independent, so they form rounds of up to 64 lanes.  Elimination walks the
 // rounds by increasing height, back substitution by decreasing height, with a
@@ -22,30 +25,37 @@
 
 namespace hx {
 
-void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, int lanes, int round_max,
-                         CellSchedule& out) {
-    const int n = static_cast<int>(local_parent.size());
-    out = CellSchedule();
+void build_unit_schedule(const std::vector<int>& forest_parent, int chunk_max, int lanes, int round_max,
+                         UnitSchedule& out) {
+    const int n = static_cast<int>(forest_parent.size());
+    out = UnitSchedule();
     if (n == 0) return;
-    if (local_parent[0] != -1) throw std::runtime_error("cell root must be local node 0");
-    if (chunk_max < 1 || chunk_max > kChunk || round_max < chunk_max || round_max > 255)
+    if (forest_parent[0] != -1) throw std::runtime_error("a solve unit must start with a cell root");
+    if (chunk_max < 1 || chunk_max > kChunk || round_max < chunk_max || round_max > kRoundMax)
         throw std::runtime_error("solver schedule: chunk or round size out of range");
-    std::vector<int> nchild(n, 0);
-    for (int i = 1; i < n; ++i) {
-        const int p = local_parent[i];
-        if (p < 0 || p >= i) throw std::runtime_error("cell nodes must satisfy parent < child");
+    std::vector<int> nchild(n, 0), roots;
+    for (int i = 0; i < n; ++i) {
+        const int p = forest_parent[i];
+        if (p < 0) {
+            roots.push_back(i);
+            continue;
+        }
+        if (p >= i) throw std::runtime_error("cell nodes must satisfy parent < child");
         nchild[p]++;
     }
     std::vector<int> cbeg(n + 1, 0);
     for (int i = 0; i < n; ++i) cbeg[i + 1] = cbeg[i] + nchild[i];
     std::vector<int> cfill(cbeg.begin(), cbeg.end() - 1), clist(std::max(n - 1, 0));
-    for (int i = 1; i < n; ++i) clist[cfill[local_parent[i]]++] = i;
+    for (int i = 0; i < n; ++i)
+        if (forest_parent[i] >= 0) clist[cfill[forest_parent[i]]++] = i;
 
-    // breadth-first chunk construction: children of one chunk get consecutive ids
+    // breadth-first chunk construction from every root: children of one chunk
+    // get consecutive ids, so the child terms of a tail are summed in the same
+    // order whatever else shares the unit
     struct Chunk { int head; int len; int parent; int child_begin; int child_count; std::vector<int> nodes; };
     std::vector<Chunk> chunks;
-    chunks.reserve(n / 2 + 1);
-    chunks.push_back({0, 0, -1, 0, 0, {}});
+    chunks.reserve(n / 2 + roots.size());
+    for (int r : roots) chunks.push_back({r, 0, -1, 0, 0, {}});
     for (size_t q = 0; q < chunks.size(); ++q) {
         int cur = chunks[q].head;
         std::vector<int> nodes{cur};
@@ -67,7 +77,8 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         for (int c = 0; c < chunks[q].child_count; ++c) h = std::max(h, height[chunks[q].child_begin + c] + 1);
         height[q] = h;
     }
-    const int hmax = height[0];
+    int hmax = 0;
+    for (int q = 0; q < static_cast<int>(roots.size()); ++q) hmax = std::max(hmax, height[q]);
     std::vector<std::vector<int>> by_h(hmax + 1);
     for (int q = 0; q < nchunk; ++q) by_h[height[q]].push_back(q);
     // back-substitution order: root height first; within a height, longest chunks first
@@ -89,7 +100,7 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         }
         if (!cur.empty()) rounds.push_back(cur);
     }
-    // solver order of the cell's nodes.  Inside a round the chunks are sorted by
+    // solver order of the unit's nodes.  Inside a round the chunks are sorted by
     // length (longest first) and stored position-major: node k of every chunk
     // that has one, then node k+1, ...  Node k of lane l sits at
     // round_base + sum_{j<k} W_j + l, where W_j = number of chunks longer than j,
@@ -106,7 +117,7 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
                 if (chunks[q].len > k) out.order.push_back(chunks[q].nodes[k]);
     }
     if (n > kMaxCellNodes || nchunk > kMaxCellNodes)
-        throw std::runtime_error("cell too large for the solver schedule (max 65535 nodes)");
+        throw std::runtime_error("solve unit too large for the solver schedule (max 65535 nodes and chunks)");
     for (size_t ri = 0; ri < rounds.size(); ++ri) {
         RoundInfo info{};
         info.desc_begin = static_cast<uint16_t>(out.desc.size());
@@ -130,7 +141,7 @@ void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, in
         // off[k] = number of the round's nodes at positions < k (chunks sorted by length)
         int off = 0;
         for (int k = 0; k < kChunk; ++k) {
-            info.off[k] = static_cast<uint8_t>(off);
+            info.off[k] = static_cast<uint16_t>(off);
             for (int q : rounds[ri]) off += chunks[q].len > k;
         }
         out.rounds.push_back(info);

@@ -1,4 +1,4 @@
-// Tree-solve schedule of one cell (see schedule.cpp).
+// Tree-solve schedule of one solve unit (see schedule.cpp).
 #pragma once
 #include <vector>
 
@@ -6,7 +6,7 @@
 
 namespace hx {
 
-struct CellSchedule {
+struct UnitSchedule {
     std::vector<int> order;          // solver position -> local node
     std::vector<ChunkDesc> desc;     // back-substitution round order
     std::vector<RoundInfo> rounds;   // [nround]
@@ -14,8 +14,9 @@ struct CellSchedule {
     int nround = 0;
 };
 
-// local_parent: parent of each local node (-1 for local node 0, parent < child).
-void build_cell_schedule(const std::vector<int>& local_parent, int chunk_max, int lanes, int round_max,
-                         CellSchedule& out);
+// forest_parent: parent of each unit-local node (-1 for a root; parent < child),
+// the unit's cells one after another, each rooted at its first node.
+void build_unit_schedule(const std::vector<int>& forest_parent, int chunk_max, int lanes, int round_max,
+                         UnitSchedule& out);
 
 }  // namespace hx

@@ -61,37 +61,53 @@ __host__ __device__ __forceinline__ void tail_inject(double& db, double& rm, dou
     rm = rm + (v * acd + ace);
 }
 
+// Prefetch distance of the chunk loops: node k's inputs are requested kAhead
+// nodes before they are used, so a caller reading from a buffer with some
+// latency (LDS) keeps several reads in flight behind the arithmetic.
+constexpr int kAhead = 4;
+
+// The chunk loops walk KM node slots (KM <= kChunk), without branches.  A
+// round whose chunks are all at most KM long runs the KM variant: node slots
+// k >= KM are padding on every lane, and a padding node maps the recurrence
+// state (P1 = 1, r1 = 1, a1 = ab1 = accr = 0) onto itself, so leaving them out
+// changes no result.  dispatch_chunk_bound calls f with the smallest of the
+// compiled bounds that covers maxlen.
+template <int KM>
+struct ChunkBound {
+    static constexpr int value = KM;
+};
+template <class F>
+__host__ __device__ __forceinline__ void dispatch_chunk_bound(int maxlen, F&& f) {
+    if (maxlen <= 8) f(ChunkBound<8>{});
+    else if (maxlen <= 12) f(ChunkBound<12>{});
+    else f(ChunkBound<kChunk>{});
+}
+
 // in.fwd(k): node k's inputs (neutral for k >= len, tail already injected);
-// rcp(x) returns 1/x.  out(k, D, u, w) receives node k's results (ignored by
-// the caller for k >= len).  cd, ce: this chunk's pair for its parent.
-// Node k-1's inputs are fetched before node k's results are handed out, so a
-// caller reading and writing one buffer overlaps the read with the math.
-// kmax (<= kChunk, the same on every lane of a round) bounds the chunk
-// lengths: nodes k >= kmax are padding on every lane, and a padding node maps
-// the recurrence state (P1 = 1, r1 = 1, a1 = ab1 = accr = 0) onto itself, so
-// those iterations are skipped without changing any result.
-template <class In, class Out, class Rcp>
+// rcp(x) returns 1/x.  out(k, D, u, w) receives node k's results for every
+// slot k < KM (the caller drops those of padding nodes).  cd, ce: this
+// chunk's pair for its parent.
+template <int KM, class In, class Out, class Rcp>
 __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, const In& in, Out&& out, Rcp rcp,
-                                                            double& cd, double& ce, int kmax = kChunk) {
+                                                            double& cd, double& ce) {
+    static_assert(KM >= 1 && KM <= kChunk, "chunk bound out of range");
     double P1 = 1.0, P2 = 0.0, r1 = 1.0, a1 = 0.0, ab1 = 0.0, accr = 0.0;
     cd = 0.0;
     ce = 0.0;
-    FwdNode cur{};
-    if (kmax == kChunk) cur = in.fwd(kChunk - 1);
+    FwdNode buf[KM];
+    // the walk runs k = KM-1 down to 0; its first kAhead nodes are requested up front
 #pragma unroll
-    for (int k = kChunk - 1; k >= 0; --k) {
-        if (k >= kmax) {
-            if (k == kmax) cur = in.fwd(k - 1);
-            continue;
-        }
-        FwdNode nxt{};
-        if (k > 0) nxt = in.fwd(k - 1);
+    for (int j = KM - 1; j >= 0 && j >= KM - kAhead; --j) buf[j] = in.fwd(j);
+#pragma unroll
+    for (int k = KM - 1; k >= 0; --k) {
+        if (k - kAhead >= 0) buf[k - kAhead] = in.fwd(k - kAhead);
+        const FwdNode& cur = buf[k];
         double a = cur.a, b = cur.b;
         if (k == 0 && !has_parent) {
             a = 0.0;
             b = 0.0;
         }
-        const double dv = (k > 0 ? nxt.v : 0.0) - cur.v;
+        const double dv = (k > 0 ? buf[k - 1].v : 0.0) - cur.v;
         const double Db = cur.db - b;
         const double Rb = fma(-b, dv, cur.rm);
         const double P = fma(Db - a1, P1, -(ab1 * P2));
@@ -110,27 +126,24 @@ __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, con
         r1 = r;
         a1 = a;
         ab1 = a * b;
-        cur = nxt;
     }
 }
 
 // in.back(k): node k's (u, w, v) (neutral for k >= len); vpar_new: updated
 // voltage of the head's parent (0 for the root chunk, whose w_0 is 0).
-// out(k, v_new, x).  kmax as for the elimination: nodes k >= kmax are padding
-// on every lane and are skipped.
-template <class In, class Out>
-__host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new, int kmax = kChunk) {
+// out(k, v_new, x) for every slot k < KM.
+template <int KM, class In, class Out>
+__host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new) {
+    static_assert(KM >= 1 && KM <= kChunk, "chunk bound out of range");
     double x = vpar_new;
-    if (kmax <= 0) return;
-    BackNode cur = in.back(0);
+    BackNode buf[KM];
 #pragma unroll
-    for (int k = 0; k < kChunk; ++k) {
-        if (k >= kmax) break;
-        BackNode nxt{};
-        if (k + 1 < kChunk && k + 1 < kmax) nxt = in.back(k + 1);
-        x = fma(-cur.w, x, cur.u);
-        out(k, cur.v + x, x);
-        cur = nxt;
+    for (int j = 0; j < kAhead && j < KM; ++j) buf[j] = in.back(j);
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        if (k + kAhead < KM) buf[k + kAhead] = in.back(k + kAhead);
+        x = fma(-buf[k].w, x, buf[k].u);
+        out(k, buf[k].v + x, x);
     }
 }
 

@@ -121,6 +121,9 @@ SIGNATURES = {
     "hx_set_cell_groups": (C.c_int, [_P, C.c_int]),
     "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
     "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
+    "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
+    "hx_emulate_tree_solve_units": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, C.c_int,
+                                              _I, _I]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
 }
 
@@ -666,6 +669,11 @@ class Sim:
         the model root.  Call before loading the model."""
         self._chk(lib().hx_set_solver_root(self._h, int(bool(centre))), "set_solver_root")
 
+    def set_solve_unit_cells(self, cells: int) -> None:
+        """Cells per solve unit (one wavefront each); 0 lets the library choose.  Call
+        before loading the model; results do not depend on it."""
+        self._chk(lib().hx_set_solve_unit_cells(self._h, int(cells)), "set_solve_unit_cells")
+
     def set_group_streams(self, enable: bool) -> None:
         """Allow the cell groups' own streams in the following runs (same results either way)."""
         self._chk(lib().hx_set_group_streams(self._h, int(bool(enable))), "set_group_streams")
@@ -686,16 +694,18 @@ class Sim:
         return ms.value, n.value
 
 
-def emulate_tree_solve(ncell, parent, a, b, cm, cfac, v, d, rhs):
-    """Host emulation of the device tree solve (same chunk schedule); returns (v_new, nchunk_max, nround_max)."""
+def emulate_tree_solve(ncell, parent, a, b, cm, cfac, v, d, rhs, unit_cells=0):
+    """Host emulation of the device tree solve (same chunk schedule); returns (v_new, nchunk_max, nround_max).
+    unit_cells: cells per solve unit (0: the library's choice)."""
     L = lib()
     parent = np.ascontiguousarray(parent, np.int32)
     a, b, cm, d, rhs = (np.ascontiguousarray(x, np.float64) for x in (a, b, cm, d, rhs))
     vv = np.array(v, np.float64)
     nc = C.c_int()
     nr = C.c_int()
-    rc = L.hx_emulate_tree_solve(int(ncell), parent.size, _ip(parent), _dp(a), _dp(b), _dp(cm), float(cfac),
-                                 _dp(vv), _dp(d), _dp(rhs), C.byref(nc), C.byref(nr))
+    rc = L.hx_emulate_tree_solve_units(int(ncell), parent.size, _ip(parent), _dp(a), _dp(b), _dp(cm),
+                                       float(cfac), _dp(vv), _dp(d), _dp(rhs), int(unit_cells), C.byref(nc),
+                                       C.byref(nr))
     if rc == -2:
         raise HelioxError("hx_emulate_tree_solve: the round length bound changed a result")
     if rc != 0:

@@ -141,6 +141,14 @@ int hx_set_cell_groups(hx_sim* sim, int ngroup);
  * root.  The solution is the same up to rounding; after a step, d holds the pivots of
  * the order used.  Call before hx_load_model. */
 int hx_set_solver_root(hx_sim* sim, int centre);
+/* Cells per solve unit (no counterpart in the reference, whose solve packs cells into
+ * 32-thread groups, permute_order.cpp:971-1170): the tree solve runs one wavefront per
+ * unit of `cells` consecutive cells, solved together as a forest.  A wavefront issues
+ * the same instructions however many of its lanes carry work, so fewer, fuller
+ * wavefronts shorten the solve.  0 (default): about ncell / 1024 cells per unit (one
+ * wavefront per SIMD), fewer where a unit's schedule would exceed 40 KB of LDS.  Results
+ * do not depend on it.  Call before hx_load_model. */
+int hx_set_solve_unit_cells(hx_sim* sim, int cells);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
@@ -264,6 +272,12 @@ int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches);
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max);
+
+/* The same with an explicit solve unit size: unit_cells consecutive cells
+ * share one schedule (0: the library's choice, as hx_emulate_tree_solve). */
+int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const double* a, const double* b,
+                                const double* cm, double cfac, double* v, const double* d, const double* rhs,
+                                int unit_cells, int* nchunk_max, int* nround_max);
 
 #ifdef __cplusplus
 }

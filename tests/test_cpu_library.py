@@ -70,6 +70,38 @@ def test_emulated_chunk_solve_matches_serial_hines(config, ncell):
     assert nchunk > 0 and nround > 0
 
 
+@pytest.mark.parametrize("config,ncell,sizes", [(2, 7, (2, 3, 7)), (3, 3, (2,)), (4, 9, (2, 4, 9))])
+def test_solve_units_change_no_bit(config, ncell, sizes):
+    """Cells packed into solve units of several sizes (one schedule per unit, the
+    cells' chunks interleaved in shared rounds) give the same bits as one cell per
+    unit, and the serial Hines solve's values."""
+    spec = build_config(config, ncell, 1.0)
+    rng = np.random.default_rng(10 + config)
+    n = spec.nnode
+    v = rng.uniform(-80, 20, n)
+    dm = rng.uniform(0.5, 2.0, n) * 1e-3
+    rm = rng.normal(0, 1e-3, n)
+    cfac = 1e-3 / 0.025
+    ref = assemble_and_solve_reference(spec, v, dm, rm, cfac)
+    one, _, rounds1 = emulate_tree_solve(spec.ncell, spec.parent, spec.a, spec.b, spec.cm, cfac, v, dm, rm,
+                                         unit_cells=1)
+    assert np.max(np.abs(one - ref)) <= 1e-12 * max(1.0, np.max(np.abs(ref - v)))
+    for u in sizes:
+        got, _, rounds = emulate_tree_solve(spec.ncell, spec.parent, spec.a, spec.b, spec.cm, cfac, v, dm, rm,
+                                            unit_cells=u)
+        assert np.array_equal(got, one), u
+        assert rounds >= rounds1
+
+
+def test_solve_unit_request_beyond_lds_budget_is_refused():
+    # three config-3 cells hold about 1860 chunks: 16 B each plus the stage exceed 40 KB
+    spec = build_config(3, 3, 1.0)
+    n = spec.nnode
+    with pytest.raises(Exception):
+        emulate_tree_solve(spec.ncell, spec.parent, spec.a, spec.b, spec.cm, 40.0, np.zeros(n), np.ones(n),
+                           np.zeros(n), unit_cells=3)
+
+
 @pytest.mark.parametrize("seed", range(8))
 def test_emulated_chunk_solve_random_trees(seed):
     """Random shapes: chains longer than a chunk, bushy nodes, single-node cells."""
