@@ -3,7 +3,7 @@
 synthetic workloads."""
 from .spec import MechSpec, ModelSpec, NetConSpec, VecPlaySpec
 from .synth import build_config
-from .sim import HelioxError, Sim, emulate_tree_solve, lib
+from .sim import HelioxError, Sim, emulate_tree_solve, lib, netstim_train, philox4x32
 
 __all__ = ["MechSpec", "ModelSpec", "NetConSpec", "VecPlaySpec", "build_config", "Sim", "HelioxError",
-           "emulate_tree_solve", "lib"]
+           "emulate_tree_solve", "lib", "netstim_train", "philox4x32"]

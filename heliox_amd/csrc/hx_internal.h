@@ -21,7 +21,7 @@ namespace hx {
 // order (coredat_to_innerdat.cpp:176-181 keeps CoreNEURON's order).
 enum MechId : int {
     M_PAS = 0, M_NA_ION, M_K_ION, M_HH, M_ICLAMP, M_EXPSYN, M_EXP2SYN, M_VECSTIM,
-    M_CA_ION, M_CADYN, M_CAHVA, M_HALFGAP, M_HDLA, M_COUNT
+    M_CA_ION, M_CADYN, M_CAHVA, M_HALFGAP, M_HDLA, M_NETSTIM, M_COUNT
 };
 
 // Column layouts: parameters, then states, then assigned variables.
@@ -41,6 +41,9 @@ enum CaHVACol {
 };
 enum HalfGapCol { HG_G = 0, HG_VGAP, HG_I, HG_NCOL };
 enum HdLaCol { HD_GHDBAR = 0, HD_VHALFL, HD_TAU, HD_L, HD_I, HD_LINF, HD_TAUL, HD_GHD, HD_NCOL };
+// NetStim (src/spike/netstim.cpp): parameters only; its spike trains are made on
+// the host.  id1 < 0 stands for the instance index.
+enum NetStimCol { NS_INTERVAL = 0, NS_NUMBER, NS_START, NS_NOISE, NS_ID1, NS_ID2, NS_ID3, NS_NCOL };
 
 // Per-mechanism device view.
 struct MechDev {

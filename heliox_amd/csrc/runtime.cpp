@@ -20,6 +20,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
 #include <limits>
 #include <map>
 #include <memory>
@@ -33,6 +34,7 @@
 #include "heliox.h"
 #include "hx_internal.h"
 #include "learn.h"
+#include "random123.h"
 #include "schedule.h"
 #include "solve_chunk.h"
 
@@ -88,6 +90,9 @@ const std::vector<MechMeta>& registry() {
         r[M_HALFGAP] = {"HalfGap", HG_NCOL, 2, 0, {"g", "vgap", "i"}, {0, 0, 0}, true, false, false, false, 0, false};
         r[M_HDLA] = {"hd_la", HD_NCOL, 3, 1, {"ghdbar", "vhalfl", "tau", "l", "i", "linf", "taul", "ghd"},
                      {0.0001, -81.0, 1.0, 0, 0, 0, 0, 0}, false, false, false, false, 0, true};
+        // defaults of netstim.cpp reg_node_indices (interval 10, number 10, start 50, noise 0)
+        r[M_NETSTIM] = {"NetStim", NS_NCOL, NS_NCOL, 0, {"interval", "number", "start", "noise", "id1", "id2", "id3"},
+                        {10.0, 10.0, 50.0, 0.0, -1.0, 0.0, 0.0}, true, false, true, false, 0, false};
         return r;
     }();
     return R;
@@ -168,6 +173,8 @@ struct Ref {
     bool point = false;
     int ab = 0;           // 1: node coefficient a, 2: b (the solver keeps its own copy)
     int node = -1;        // user node of an a / b reference
+    int ns_col = -1;      // NetStim parameter (the host keeps the copy its trains come from)
+    int ns_inst = -1;
 };
 
 struct Timer {
@@ -196,6 +203,10 @@ struct hx_sim {
     std::vector<int> pre_gid, pre_node;
     std::vector<double> pre_thr;
     std::vector<std::vector<double>> vecstim;
+    // NetStim trains (self-event times), made on the host up to step ns_horizon
+    std::vector<std::vector<double>> netstim;
+    int ns_horizon = 0;
+    void make_netstim_trains(int horizon);
     std::vector<NetCon> netcons;
     std::vector<std::pair<int, int>> gaps;     // (src node, halfgap inst)
     std::vector<VecPlayHost> vecplay;
@@ -815,8 +826,10 @@ void hx_sim::upload() {
     // netcons: the last one per synapse instance wins (coredat_to_innerdat.cpp:356-364)
     std::map<std::pair<int, int>, NetCon> by_syn;
     for (auto& nc : netcons) by_syn[{nc.mech, nc.inst}] = nc;
+    // input sources: VecStim instances, then NetStim instances
     const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
-    std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs);
+    const int nns = mech[M_NETSTIM].present ? mech[M_NETSTIM].n : 0;
+    std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs + nns);
     std::vector<double> esw(mech[M_EXPSYN].present ? mech[M_EXPSYN].n : 0, 0.0);
     std::vector<double> e2w(mech[M_EXP2SYN].present ? mech[M_EXP2SYN].n : 0, 0.0);
     max_delay = 0;
@@ -827,7 +840,8 @@ void hx_sim::upload() {
         if (nc.mech == M_EXPSYN) esw[dinst] = nc.weight;
         else e2w[dinst] = nc.weight;
         if (nc.src_kind == 0) pre_fo[pre_dev[nc.src]].push_back({packed, nc.delay});
-        else vs_fo[nc.src].push_back({packed, nc.delay});
+        else if (nc.src_kind == 1) vs_fo[nc.src].push_back({packed, nc.delay});
+        else vs_fo[nvs + nc.src].push_back({packed, nc.delay});
         max_delay = std::max(max_delay, nc.delay);
     }
     long long ntgt = 0;
@@ -969,6 +983,103 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
     if (G > 1 && !ev_main) HXC(hipEventCreateWithFlags(&ev_main, hipEventDisableTiming));
 }
 
+// NetStim (netstim.cpp:211-330, one random stream per instance) as a train of
+// self-event times, for instances that receive no events.  INITIAL schedules
+// the init event at start + invl - interval (1 - noise) (0 if negative); that
+// event starts the sequence with a self event at the same time, and every self
+// event emits a spike at the step time t_m of the step that delivers it, draws
+// the next interval and, until `number` spikes are out, schedules the next self
+// event at t_m + interval.  A train element is therefore delivered exactly as
+// a VecStim element: at the first step whose window t_m + dt/2 reaches it.
+// Each instance draws from its own stream, ids (id1, id2, id3) with id1 < 0
+// meaning the instance index, sequence 0 at every finitialize (the reference
+// shares one stream among all instances and redraws every instance's interval
+// on any event, netstim.cpp:118-161; each instance's draws here are the ones
+// it would make alone).  Elements past step `horizon` are left for later.
+constexpr int kNetStimHorizon0 = 4096;   // steps of NetStim train made at finitialize
+
+namespace {
+
+struct NetStimParams {
+    double interval, number, start, noise;
+    uint32_t id1, id2, id3;
+};
+
+// The train of one instance up to step `horizon` of the step-time table ttab.
+void netstim_train(const std::vector<double>& ttab, int horizon, double dt, const NetStimParams& P,
+                   std::vector<double>& train) {
+    train.clear();
+    const double half = dt / 2;
+    const double t_end = ttab[horizon];
+    const double interval = P.interval, number = P.number, start = P.start;
+    const double noise = std::min(1.0, std::max(0.0, P.noise));
+    Stream123 rng;
+    rng.set_ids(P.id1, P.id2, P.id3);
+    rng.set_seq(0, 0);
+    auto invl = [&](double mean) {   // netstim.cpp:140-155
+        if (mean <= 0.0) mean = 0.01;
+        if (noise == 0) return mean;
+        return (1.0 - noise) * mean + noise * mean * rng.negexp();
+    };
+    if (!(start >= 0.0 && number > 0)) return;
+    double T = start + invl(interval) - interval * (1.0 - noise);
+    if (T < 0.0) T = 0.0;
+    int mstep = 0;
+    double ispike = 0.0;
+    while (T <= t_end) {
+        while (ttab[mstep] + half < T) ++mstep;   // delivering step
+        train.push_back(T);
+        if (train.size() > 64 * static_cast<size_t>(horizon + 1))
+            throw std::runtime_error("a NetStim fires more than 64 times per step (interval too small)");
+        ispike += 1.0;
+        const double e = invl(interval);
+        if (ispike >= number) break;
+        T = ttab[mstep] + e;
+    }
+}
+
+// t of every step since finitialize, accumulated exactly as Simulate::fadvance
+// does (t += 0.5*dt twice, simulate.cpp:417,774).
+void extend_step_times(std::vector<double>& ttab, int n, double dt) {
+    if (ttab.empty()) ttab.push_back(0.0);
+    while (static_cast<int>(ttab.size()) < n) {
+        double x = ttab.back();
+        x += 0.5 * dt;
+        x += 0.5 * dt;
+        ttab.push_back(x);
+    }
+}
+
+}  // namespace
+
+// NetStim (netstim.cpp:211-330, one random stream per instance) as a train of
+// self-event times, for instances that receive no events.  INITIAL schedules
+// the init event at start + invl - interval (1 - noise) (0 if negative); that
+// event starts the sequence with a self event at the same time, and every self
+// event emits a spike at the step time t_m of the step that delivers it, draws
+// the next interval and, until `number` spikes are out, schedules the next self
+// event at t_m + interval.  A train element is therefore delivered exactly as
+// a VecStim element: at the first step whose window t_m + dt/2 reaches it.
+// Each instance draws from its own stream, ids (id1, id2, id3) with id1 < 0
+// meaning the instance index, sequence 0 at every finitialize (the reference
+// shares one stream among all instances and redraws every instance's interval
+// on any event, netstim.cpp:118-161; each instance's draws here are the ones
+// it would make alone).  Elements past step `horizon` are left for later.
+void hx_sim::make_netstim_trains(int horizon) {
+    const HostMech& m = mech[M_NETSTIM];
+    const int nns = m.present ? m.n : 0;
+    netstim.assign(nns, {});
+    ensure_ttab(horizon + 1);
+    for (int j = 0; j < nns; ++j) {
+        const double id1 = m.col[NS_ID1][j];
+        const NetStimParams P{m.col[NS_INTERVAL][j], m.col[NS_NUMBER][j], m.col[NS_START][j], m.col[NS_NOISE][j],
+                              id1 < 0 ? static_cast<uint32_t>(j) : static_cast<uint32_t>(id1),
+                              static_cast<uint32_t>(m.col[NS_ID2][j]), static_cast<uint32_t>(m.col[NS_ID3][j])};
+        netstim_train(ttab, horizon, dt, P, netstim[j]);
+    }
+    ns_horizon = horizon;
+}
+
 // VecStim trains -> globally sorted effective event times.  A train element is
 // processed at the first step whose window t+dt/2 reaches it, but never before
 // the previous element of the same train (vecevent.cpp:172-199 chains the
@@ -976,13 +1087,16 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
 void hx_sim::upload_inputs() {
     std::vector<std::pair<double, int>> ev;
     const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
-    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) {
+    const int nns = mech[M_NETSTIM].present ? mech[M_NETSTIM].n : 0;
+    auto add_train = [&](const std::vector<double>& train, int s) {
         double run_max = -INFINITY;
-        for (double e : vecstim[s]) {
+        for (double e : train) {
             run_max = std::max(run_max, e);
             ev.push_back({run_max, s});
         }
-    }
+    };
+    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) add_train(vecstim[s], s);
+    for (int j = 0; j < nns && j < static_cast<int>(netstim.size()); ++j) add_train(netstim[j], nvs + j);
     std::stable_sort(ev.begin(), ev.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
     for (auto& cg : groups) {
         // each group keeps the events of the VecStims that drive its synapses
@@ -1072,19 +1186,12 @@ void hx_sim::upload_monitors() {
     mon_dirty = false;
 }
 
-// t of every step since finitialize, accumulated exactly as Simulate::fadvance
-// does (t += 0.5*dt twice, simulate.cpp:417,774).
+// Step-time table long enough for kneed steps plus the longest netcon delay.
 void hx_sim::ensure_ttab(int kneed) {
     const int margin = static_cast<int>(std::ceil(max_delay / dt)) + 8;
     const int want = kneed + margin;
     if (static_cast<int>(ttab.size()) < want + 1) {
-        if (ttab.empty()) ttab.push_back(0.0);
-        while (static_cast<int>(ttab.size()) < want + 1) {
-            double x = ttab.back();
-            x += 0.5 * dt;
-            x += 0.5 * dt;
-            ttab.push_back(x);
-        }
+        extend_step_times(ttab, want + 1, dt);
     }
     if (ttab_cap < static_cast<int>(ttab.size())) {
         ttab_cap = static_cast<int>(ttab.size()) * 2;
@@ -1139,6 +1246,11 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     r.dev = m.dev.col(c) + m.perm[idx];
     r.klass = c >= M.nparam + M.nstate ? 1 : 0;
     r.point = M.point;
+    if (id == M_NETSTIM) {           // parameters only: nothing changes them during a step
+        r.point = false;
+        r.ns_col = c;
+        r.ns_inst = idx;
+    }
     if (id == M_EXP2SYN && c == E2_FACTOR) r.klass = 0;   // written by INITIAL
     if (id == M_HALFGAP && c == HG_VGAP) r.klass = 0;     // written by the gap transfer
     return r;
@@ -1343,6 +1455,10 @@ void hx_sim::launch_record() {
 // when the solver's tree keeps the link's orientation, else, with a and b
 // trading places, at the node's parent (which the solver hangs below it).
 void hx_sim::mirror_ab(const Ref& r, double value) {
+    if (r.ns_col >= 0) {   // NetStim trains are made from the host copy at the next finitialize
+        mech[M_NETSTIM].col[r.ns_col][r.ns_inst] = value;
+        return;
+    }
     if (!r.ab || r.node < 0) return;
     const int u = r.node;
     (r.ab == 1 ? a : b)[u] = value;
@@ -1601,6 +1717,12 @@ void hx_sim::sync_outputs() {
 int hx_sim::run_steps(int nstep) {
     if (!initialized) throw std::runtime_error("finitialize must be called before stepping");
     ensure_ttab(k + nstep + 1);
+    if (mech[M_NETSTIM].present && mech[M_NETSTIM].n > 0 && k + nstep + 2 > ns_horizon) {
+        // longer trains: the streams restart, so the events already delivered come
+        // out the same and only events past the old horizon are added
+        make_netstim_trains(std::max(2 * ns_horizon, k + nstep + 2 + kNetStimHorizon0));
+        upload_inputs();
+    }
     if (mon_dirty) upload_monitors();
     if (vecplay_dirty) upload_vecplay();
     if (!mon_ref.empty() && mon_buf_cap < nstep + 2) {
@@ -1648,6 +1770,10 @@ int hx_sim::run_steps(int nstep) {
 
 // Simulate::finitialize (simulate.cpp:106-141, 271-339)
 void hx_sim::finitialize(double v_init) {
+    if (mech[M_NETSTIM].present && mech[M_NETSTIM].n > 0) {
+        make_netstim_trains(std::max(ns_horizon, kNetStimHorizon0));
+        inputs_dirty = true;
+    }
     if (inputs_dirty) upload_inputs();
     if (vecplay_dirty) upload_vecplay();
     if (mon_dirty) upload_monitors();
@@ -1866,7 +1992,9 @@ int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, 
         return sim->fail("netcon source detector out of range");
     if (src_kind == 1 && (!sim->mech[M_VECSTIM].present || src < 0 || src >= sim->mech[M_VECSTIM].n))
         return sim->fail("netcon source VecStim out of range");
-    if (src_kind != 0 && src_kind != 1) return sim->fail("src_kind must be 0 or 1");
+    if (src_kind == 2 && (!sim->mech[M_NETSTIM].present || src < 0 || src >= sim->mech[M_NETSTIM].n))
+        return sim->fail("netcon source NetStim out of range");
+    if (src_kind < 0 || src_kind > 2) return sim->fail("src_kind must be 0, 1 or 2");
     if (!(delay >= 0)) return sim->fail("netcon delay must be >= 0");
     sim->netcons.push_back({src_kind, src, id, inst, w, delay});
     return 0;
@@ -2176,6 +2304,26 @@ int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap) {
     return n;
 }
 
+// Simulate::output_spikes (simulate.cpp:892-909): <folder>/spk.dat, one "%.8g\t%d" line per
+// spike, ordered by time and then gid, spikes of negative gids left out.
+int hx_output_spikes(hx_sim* sim, const char* folder) {
+    if (!folder || !*folder) return sim->fail("output_spikes: no folder given");
+    std::error_code ec;
+    std::filesystem::create_directories(folder, ec);
+    if (ec) return sim->fail("output_spikes: cannot create %s: %s", folder, ec.message().c_str());
+    std::vector<std::pair<double, int>> s = sim->spikes;
+    std::sort(s.begin(), s.end(), [](const auto& x, const auto& y) {
+        return x.first == y.first ? x.second < y.second : x.first < y.first;
+    });
+    const std::string path = std::string(folder) + "/spk.dat";
+    FILE* fp = std::fopen(path.c_str(), "w");
+    if (!fp) return sim->fail("output_spikes: cannot open %s", path.c_str());
+    for (auto& e : s)
+        if (e.second > -1) std::fprintf(fp, "%.8g\t%d\n", e.first, e.second);
+    if (std::fclose(fp) != 0) return sim->fail("output_spikes: write to %s failed", path.c_str());
+    return 0;
+}
+
 int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap) {
     auto it = sim->spk_by_gid.find(gid);
     if (it == sim->spk_by_gid.end()) return 0;
@@ -2272,6 +2420,30 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
 // kernel's per-chunk arithmetic (reciprocals here are plain divisions).  Lanes
 // of a round touch disjoint nodes and slots, so running them one after the
 // other is what the wavefront computes.
+int hx_random123_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
+    if (!ctr || !key || !out) return -1;
+    Philox4x32::block(ctr, key, out);
+    return 0;
+}
+
+int hx_netstim_train(double dt, double t_end, double interval, double number, double start, double noise,
+                     unsigned id1, unsigned id2, unsigned id3, double* out, int cap) {
+    try {
+        if (!(dt > 0) || !(t_end >= 0) || cap < 0 || (cap > 0 && !out)) return -1;
+        std::vector<double> ttab;
+        const int horizon = static_cast<int>(std::ceil(t_end / dt));
+        extend_step_times(ttab, horizon + 1, dt);
+        std::vector<double> train;
+        netstim_train(ttab, horizon, dt, NetStimParams{interval, number, start, noise, id1, id2, id3}, train);
+        const int n = static_cast<int>(train.size());
+        for (int i = 0; i < std::min(n, cap); ++i) out[i] = train[i];
+        return n;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "hx_netstim_train: %s\n", e.what());
+        return -1;
+    }
+}
+
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max) {
@@ -2436,8 +2608,8 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
     for (int id = 0; id < M_COUNT; ++id) {
         if (!sim->mech[id].present) continue;
         if (id != M_PAS && id != M_NA_ION && id != M_K_ION && id != M_HH && id != M_ICLAMP && id != M_EXPSYN &&
-            id != M_VECSTIM)
-            return sim->fail("the adjoint supports pas, hh, ExpSyn, IClamp, VecStim and the na/k ions; "
+            id != M_VECSTIM && id != M_NETSTIM)
+            return sim->fail("the adjoint supports pas, hh, ExpSyn, IClamp, VecStim, NetStim and the na/k ions; "
                              "the model has %s", R[id].name);
     }
     for (int x : {M_NA_ION, M_K_ION})

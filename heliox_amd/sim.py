@@ -122,6 +122,10 @@ SIGNATURES = {
     "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
     "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
+    "hx_output_spikes": (C.c_int, [_P, C.c_char_p]),
+    "hx_random123_philox4x32": (C.c_int, [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    "hx_netstim_train": (C.c_int, [C.c_double, C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
+                                   C.c_uint, C.c_uint, C.c_uint, _D, C.c_int]),
     "hx_emulate_tree_solve_units": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, C.c_int,
                                               _I, _I]),
     "hx_get_replay_kernel_time": (C.c_int, [_P, _D, C.POINTER(C.c_longlong)]),
@@ -425,6 +429,12 @@ class Sim:
         L.hx_get_spikes(self._h, _dp(t), _ip(g), n)
         return t, g
 
+    def output_spikes(self, folder: str) -> str:
+        """Write ``<folder>/spk.dat`` in the reference's format (Simulate::output_spikes);
+        returns the file's path."""
+        self._chk(lib().hx_output_spikes(self._h, _b(folder)), "output_spikes")
+        return os.path.join(folder, "spk.dat")
+
     def get_spk_by_gid(self, gid: int) -> List[float]:
         L = lib()
         n = L.hx_get_spike_count(self._h)
@@ -692,6 +702,29 @@ class Sim:
         n = C.c_longlong()
         self._chk(lib().hx_get_kernel_time(self._h, _b(kernel), C.byref(ms), C.byref(n)), "kernel_time")
         return ms.value, n.value
+
+
+def philox4x32(ctr, key):
+    """One Philox4x32-10 block of the library's NetStim streams (diagnostic)."""
+    c = (C.c_uint32 * 4)(*[int(x) for x in ctr])
+    k = (C.c_uint32 * 2)(*[int(x) for x in key])
+    out = (C.c_uint32 * 4)()
+    if lib().hx_random123_philox4x32(c, k, out) != 0:
+        raise HelioxError("hx_random123_philox4x32 failed")
+    return [int(x) for x in out]
+
+
+def netstim_train(dt, t_end, interval=10.0, number=10.0, start=50.0, noise=0.0, ids=(0, 0, 0)):
+    """Self-event times of one NetStim instance as the library makes them (diagnostic)."""
+    L = lib()
+    args = (float(dt), float(t_end), float(interval), float(number), float(start), float(noise),
+            int(ids[0]), int(ids[1]), int(ids[2]))
+    n = L.hx_netstim_train(*args, None, 0)
+    if n < 0:
+        raise HelioxError("hx_netstim_train failed")
+    out = np.empty(max(n, 1))
+    L.hx_netstim_train(*args, _dp(out), n)
+    return out[:n]
 
 
 def emulate_tree_solve(ncell, parent, a, b, cm, cfac, v, d, rhs, unit_cells=0):

@@ -34,12 +34,13 @@ MECH_PARAMS: Dict[str, Tuple[str, ...]] = {
     "ExpSyn": ("tau", "e"),
     "Exp2Syn": ("tau1", "tau2", "e"),
     "VecStim": (),
+    "NetStim": ("interval", "number", "start", "noise", "id1", "id2", "id3"),
     "na_ion": ("erev", "conci", "conco"),
     "k_ion": ("erev", "conci", "conco"),
     "ca_ion": ("erev", "conci", "conco"),
 }
 ION_NAMES = ("na_ion", "k_ion", "ca_ion")
-POINT_PROCESSES = ("IClamp", "HalfGap", "ExpSyn", "Exp2Syn", "VecStim")
+POINT_PROCESSES = ("IClamp", "HalfGap", "ExpSyn", "Exp2Syn", "VecStim", "NetStim")
 
 
 @dataclass
@@ -58,7 +59,7 @@ class MechSpec:
 class NetConSpec:
     """Netcons into one synapse mechanism: one source per synapse instance."""
     inst: np.ndarray      # int32 target instance
-    src_kind: np.ndarray  # int8: 0 = real presyn index, 1 = VecStim instance
+    src_kind: np.ndarray  # int8: 0 = real presyn index, 1 = VecStim instance, 2 = NetStim instance
     src: np.ndarray       # int32
     weight: np.ndarray    # float64 (uS)
     delay: np.ndarray     # float64 (ms)

@@ -24,6 +24,8 @@
 #ifndef HELIOX_AMD_H
 #define HELIOX_AMD_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -63,8 +65,16 @@ int hx_model_add_presyn(hx_sim* sim, int gid, int node, double threshold);
 /* VecStim spike times of one instance (VecEvent::update_sequence, vecevent.cpp:292-309). */
 int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times);
 /* NetCon into synapse `target` instance `inst` (ExpSyn / Exp2Syn).  src_kind 0: detector index,
- * 1: VecStim instance.  One source per synapse instance; a later netcon replaces an earlier one
- * (coredat_to_innerdat.cpp:356-364). */
+ * 1: VecStim instance, 2: NetStim instance.  One source per synapse instance; a later netcon
+ * replaces an earlier one (coredat_to_innerdat.cpp:356-364).
+ * NetStim (netstim.cpp:211-330) is inserted like any mechanism, with parameters interval,
+ * number, start, noise (defaults 10, 10, 50, 0) and id1, id2, id3, the ids of its own
+ * Random123 Philox4x32 stream (id1 < 0, the default: the instance index).  Its trains are
+ * made on the host at finitialize and as runs need them; it takes no incoming events.  The
+ * reference draws every instance from one shared stream and redraws all instances' intervals
+ * on any event (netstim.cpp:118-161); here each instance draws only its own intervals from
+ * its own stream, restarted at sequence 0 by every finitialize.  Parameter writes through
+ * handles take effect at the next finitialize. */
 int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double weight,
                         double delay);
 /* Gap-junction transfer after each update: HalfGap[halfgap_inst].vgap = v[src_node]
@@ -110,6 +120,10 @@ int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
 int hx_get_spike_count(hx_sim* sim);
 int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap);
 int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap);
+/* Simulate::output_spikes (simulate.cpp:892-909): writes <folder>/spk.dat (the folder is
+ * created if needed) with one "%.8g<TAB>%d" line per spike of the spikes recorded so far,
+ * ordered by time and then gid; spikes of negative gids are left out. */
+int hx_output_spikes(hx_sim* sim, const char* folder);
 
 /* ---- capacity and diagnostics ---- */
 /* Event-ring capacity per delivery step (default sized from the model). */
@@ -272,6 +286,16 @@ int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches);
 int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double* a, const double* b,
                           const double* cm, double cfac, double* v, const double* d, const double* rhs,
                           int* nchunk_max, int* nround_max);
+
+/* Philox4x32-10 block (no counterpart in the reference's API; the generator of its vendored
+ * Random123, src/third_party/Random123/philox.h, as published by Salmon et al., SC11): out =
+ * philox(ctr[4], key[2]).  A diagnostic for known-answer checks of the NetStim streams. */
+int hx_random123_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out);
+/* The self-event times of one NetStim instance up to t_end with step dt, as the library makes
+ * them at finitialize (see hx_model_add_netcon): a diagnostic of the host-side generator.
+ * Writes up to cap times to out and returns their total count (-1 on error). */
+int hx_netstim_train(double dt, double t_end, double interval, double number, double start, double noise,
+                     unsigned id1, unsigned id2, unsigned id3, double* out, int cap);
 
 /* The same with an explicit solve unit size: unit_cells consecutive cells
  * share one schedule (0: the library's choice, as hx_emulate_tree_solve). */

@@ -16,6 +16,10 @@ Parity status of each oracle function (see ``tests/test_oracle_*.py``):
   VecPlay .............. pinned: closed-form linear interpolation
   hd_la, Ca_HVA rates .. pinned: steady-state (linf / mInf) invariants at clamp
   Adam ................. pinned: Kingma-Ba closed form
+  NetStim .............. pinned: Philox4x32-10 against Random123's published
+                         known-answer vectors, the stream's id/draw layout against
+                         those blocks, noiseless trains against start + k interval,
+                         noisy intervals against the exponential law
 """
 from __future__ import annotations
 
@@ -80,8 +84,19 @@ def lib():
         L.hxo_solve_serial.argtypes = [C.c_int, C.c_int, _I, _D, _D, _D, _D]
         L.hxo_adam_step.argtypes = [_D, _D, _I, C.c_int, _D, _D, C.c_longlong, C.c_double, C.c_double,
                                     C.c_double, C.c_double, C.c_double, C.c_double]
+        L.hxo_philox4x32.argtypes = [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]
+        L.hxo_netstim_spikes.argtypes = [C.c_void_p, _D, _I, C.c_int]
         _lib = L
     return _lib
+
+
+def philox4x32(ctr, key):
+    """The oracle's Philox4x32-10 block (known-answer checks)."""
+    c = (C.c_uint32 * 4)(*[int(x) for x in ctr])
+    k = (C.c_uint32 * 2)(*[int(x) for x in key])
+    out = (C.c_uint32 * 4)()
+    lib().hxo_philox4x32(c, k, out)
+    return [int(x) for x in out]
 
 
 def _dp(a):
@@ -184,6 +199,15 @@ class OracleSim:
 
     def traces(self) -> np.ndarray:
         return np.stack([self.monitor(h) for h in self.monitors]) if self.monitors else np.zeros((0, 0))
+
+    def netstim_spikes(self):
+        """(time, instance) of every NetStim spike since finitialize, in emission order."""
+        L = lib()
+        n = L.hxo_netstim_spikes(self.h, None, None, 0)
+        t = np.empty(max(n, 1))
+        i = np.empty(max(n, 1), np.int32)
+        L.hxo_netstim_spikes(self.h, _dp(t), _ip(i), n)
+        return t[:n], i[:n]
 
     def spikes(self):
         L = lib()

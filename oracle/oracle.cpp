@@ -29,6 +29,9 @@
 //   ExpSyn ............... src/spike/postsyn_mech/expsyn.cpp (current/state/net_receive)
 //   Exp2Syn .............. src/spike/user_postsyn_mech/exp2syn_temp.cuh:29-67
 //   VecStim .............. src/spike/vecevent.cpp:94-217, src/spike/articell.cpp:18-35
+//   NetStim .............. src/spike/netstim.cpp:211-330 with one stream per instance
+//                          (src/utils/nrnran123.cpp:23-110; Philox4x32-10 as published
+//                          by Salmon et al., SC11)
 //   VecPlay .............. src/vecplay.cu:19-111
 //   Adam ................. src/optimizer/optimizer.cpp:351-413
 //
@@ -151,7 +154,7 @@ struct Model {
         }
     };
     using SpikeBuffer = std::priority_queue<Spike, std::vector<Spike>, Cmp>;
-    enum { INVALID = -1, NORMAL_EVENT = 0, SELF_EVENT = 1 };
+    enum { INVALID = -1, NORMAL_EVENT = 0, SELF_EVENT = 1, NETSTIM_INIT_EVENT = 2 };
 
     // real presyns occupy spike slots [0, npre); VecStim instance k occupies npre + k
     std::vector<int> pre_node, pre_gid;
@@ -180,6 +183,12 @@ struct Model {
     std::vector<int> vs_index;
     std::vector<double> vs_etime;
     int vs_postsyn = -1;
+    // NetStim (netstim.cpp): spike slots after the VecStim ones
+    int ns_postsyn = -1;
+    std::vector<std::pair<double, int>> ns_spikes;   // (time, instance) of every NetStim spike
+    void net_send_netstim(uint32_t idx, double tt, int flag);
+    void netstim_init();
+    bool netstim_receive(int isyn, int flag);
 
     // VecPlay (vecplay.cu)
     struct VecPlayItem {
@@ -696,8 +705,66 @@ struct VecStim : Mech {
     VecStim() { name = "VecStim"; point_process = true; }
 };
 
+// nrnran123 stream (nrnran123.cpp: setids, setseq, ipick, dblpick, negexp) over
+// Philox4x32-10: 10 rounds with multipliers 0xD2511F53 / 0xCD9E8D57 on counter
+// words 0 / 2 and key increments 0x9E3779B9 / 0xBB67AE85 (Salmon et al., SC11).
+struct Ran123 {
+    uint32_t c[4] = {0, 0, 0, 0}, r[4] = {0, 0, 0, 0};
+    int which = 0;
+    static void philox(const uint32_t in[4], uint32_t out[4]) {
+        uint32_t x0 = in[0], x1 = in[1], x2 = in[2], x3 = in[3], k0 = 0, k1 = 0;   // global index 0
+        for (int rnd = 0; rnd < 10; ++rnd) {
+            if (rnd > 0) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+            uint64_t a = (uint64_t)0xD2511F53u * x0, b = (uint64_t)0xCD9E8D57u * x2;
+            uint32_t y0 = (uint32_t)(b >> 32) ^ x1 ^ k0, y1 = (uint32_t)b;
+            uint32_t y2 = (uint32_t)(a >> 32) ^ x3 ^ k1, y3 = (uint32_t)a;
+            x0 = y0; x1 = y1; x2 = y2; x3 = y3;
+        }
+        out[0] = x0; out[1] = x1; out[2] = x2; out[3] = x3;
+    }
+    void setids(uint32_t id1, uint32_t id2, uint32_t id3) { c[1] = id3; c[2] = id1; c[3] = id2; }
+    void setseq(uint32_t seq, int w) { which = (w > 3 || w < 0) ? 0 : w; c[0] = seq; philox(c, r); }
+    uint32_t ipick() {
+        uint32_t v = r[which++];
+        if (which > 3) {
+            which = 0;
+            if (++c[0] == 0 && ++c[1] == 0 && ++c[2] == 0) ++c[3];
+            philox(c, r);
+        }
+        return v;
+    }
+    double dblpick() { static const double SHIFT32 = 1.0 / 4294967297.0; return ((double)ipick() + 1.0) * SHIFT32; }
+    double negexp() { return -std::log(dblpick()); }
+};
+
+// NetStim: artificial cell driven through the queue (netstim.cpp), each
+// instance with its own stream (ids id1 / id2 / id3, id1 < 0: the instance index).
+struct NetStim : Mech {
+    std::vector<Ran123> rng;
+    NetStim() { name = "NetStim"; point_process = true; }
+    void alloc() override {
+        ensure("interval", 10.0); ensure("number", 10.0); ensure("start", 50.0); ensure("noise", 0.0);
+        ensure("id1", -1.0); ensure("id2", 0.0); ensure("id3", 0.0);
+        ensure("event", 0.0); ensure("on", 0.0); ensure("ispike", 0.0);
+        rng.assign(n, Ran123());
+    }
+    double invl(int i, double mean) {              // netstim.cpp:140-155
+        if (mean <= 0.0) mean = 0.01;
+        double noise = C("noise")[i];
+        if (noise == 0) return mean;
+        return (1.0 - noise) * mean + noise * mean * rng[i].negexp();
+    }
+    void init_sequence(int i) {                    // netstim.cpp:127-139, this instance only
+        if (C("number")[i] > 0.0) { C("event")[i] = 0.0; C("on")[i] = 1.0; C("ispike")[i] = 0.0; }
+    }
+    void next_invl(int i) {                        // netstim.cpp:156-172, this instance only
+        if (C("number")[i] > 0) C("event")[i] = invl(i, C("interval")[i]);
+        if (C("ispike")[i] >= C("number")[i]) C("on")[i] = 0.0;
+    }
+};
+
 // CoreNEURON type order used by the oracle (NEURON built-ins, then user mechanisms).
-const char* kMechOrder[] = {"pas", "na_ion", "k_ion", "hh", "IClamp", "ExpSyn", "Exp2Syn", "VecStim",
+const char* kMechOrder[] = {"pas", "na_ion", "k_ion", "hh", "IClamp", "ExpSyn", "Exp2Syn", "VecStim", "NetStim",
                             "ca_ion", "CaDynamics_E2", "Ca_HVA", "HalfGap", "hd_la"};
 
 std::unique_ptr<Mech> make_mech(const std::string& nm) {
@@ -714,6 +781,7 @@ std::unique_ptr<Mech> make_mech(const std::string& nm) {
     if (nm == "ExpSyn") return std::make_unique<ExpSyn>();
     if (nm == "Exp2Syn") return std::make_unique<Exp2Syn>();
     if (nm == "VecStim") return std::make_unique<VecStim>();
+    if (nm == "NetStim") return std::make_unique<NetStim>();
     return nullptr;
 }
 
@@ -813,6 +881,64 @@ void Model::vecstim_element(int inode) {      // vecevent.cpp:140-170
     }
 }
 
+void Model::net_send_netstim(uint32_t idx, double tt, int flag) {   // articell.cpp:18-35
+    auto& ps = postsyns[ns_postsyn];
+    if (flag != NORMAL_EVENT) {
+        Spike spk; spk.syn_type = ps.type_id; spk.syn_id = (int)idx; spk.deliver_time = tt; spk.flag = flag;
+        ps.buffer.push(spk);
+    } else {
+        ns_spikes.emplace_back(tt, (int)idx);
+        Spike spk; spk.deliver_time = tt; spk.flag = flag;
+        int nvs = vs_postsyn >= 0 ? postsyns[vs_postsyn].mech->n : 0;
+        uint32_t slot = (uint32_t)(pre_node.size() + nvs) + idx;
+        spk_vec[slot] = spk;
+        spk_flags[slot] = flag;
+    }
+}
+
+void Model::netstim_init() {                  // netstim.cpp:211-246 (initialize_cpu)
+    auto* ns = static_cast<NetStim*>(postsyns[ns_postsyn].mech);
+    ns_spikes.clear();
+    for (int i = 0; i < ns->n; i++) {
+        double id1 = ns->C("id1")[i];
+        ns->rng[i].setids(id1 < 0 ? (uint32_t)i : (uint32_t)id1, (uint32_t)ns->C("id2")[i], (uint32_t)ns->C("id3")[i]);
+        ns->rng[i].setseq(0, 0);
+        double& on = ns->C("on")[i];
+        double& noise = ns->C("noise")[i];
+        on = 0.0;
+        ns->C("ispike")[i] = 0.0;
+        if (noise < 0.0) noise = 0.0;
+        if (noise > 1.0) noise = 1.0;
+        double start = ns->C("start")[i], interval = ns->C("interval")[i];
+        if (start >= 0.0 && ns->C("number")[i] > 0) {
+            on = 1.0;
+            double& event = ns->C("event")[i];
+            event = start + ns->invl(i, interval) - interval * (1.0 - noise);
+            if (event < 0.0) event = 0.0;
+            net_send_netstim(i, event, NETSTIM_INIT_EVENT);
+        }
+    }
+}
+
+bool Model::netstim_receive(int isyn, int flag) {   // netstim.cpp:247-290 (net_receive_cpu)
+    auto* ns = static_cast<NetStim*>(postsyns[ns_postsyn].mech);
+    double& on = ns->C("on")[isyn];
+    bool sent = false;
+    if (flag == NETSTIM_INIT_EVENT && on == 1.0) {
+        ns->init_sequence(isyn);
+        net_send_netstim(isyn, t + 0.0, SELF_EVENT);
+        sent = true;
+    }
+    if (flag == SELF_EVENT && on == 1.0) {
+        ns->C("ispike")[isyn] += 1.0;
+        net_send_netstim(isyn, t, NORMAL_EVENT);
+        ns->next_invl(isyn);
+        if (on == 1.0) net_send_netstim(isyn, t + ns->C("event")[isyn], SELF_EVENT);
+        sent = true;
+    }
+    return sent;
+}
+
 void Model::network_spike_receive() {         // simulate.cpp:916-939
     bool hasSent = false;
     do {
@@ -845,7 +971,12 @@ void Model::network_spike_receive() {         // simulate.cpp:916-939
                 ps.receive_count++;
             }
             // net_receive_cpu(t)
-            if (ps.artificial) {                 // vecevent.cpp:172-199
+            if (ps.artificial && ps.mech->name == "NetStim") {
+                int send_count = 0;
+                for (int i = 0; i < ps.receive_count; i++)
+                    if (netstim_receive((int)ps.receive_idx[i], ps.receive_flag[i])) send_count++;
+                hasSent |= send_count > 0;
+            } else if (ps.artificial) {          // vecevent.cpp:172-199
                 int send_count = 0;
                 for (int i = 0; i < ps.receive_count; i++) {
                     int isyn = (int)ps.receive_idx[i];
@@ -887,7 +1018,9 @@ void Model::finitialize(double v_init) {      // simulate.cpp:106-141, 271-339
     for (int j = 0; j < len; j++) v[j] = v_init;
     gap_transfer();
     for (auto* mm : current_list) {
-        if (mm->name == "VecStim") {           // vecevent.cpp:94-109
+        if (mm->name == "NetStim") {
+            netstim_init();
+        } else if (mm->name == "VecStim") {           // vecevent.cpp:94-109
             for (int inode = 0; inode < mm->n; inode++) {
                 vs_index[inode] = 0;
                 vecstim_element(inode);
@@ -1060,7 +1193,7 @@ static int finalize_model(Model* m) {
         if (mm->write_state_ion) m->state_ion_first.push_back(mm);
         if (!mm->is_ion && !mm->write_state_ion) m->state_rest.push_back(mm);
         std::string s = nm;
-        if (s == "ExpSyn" || s == "Exp2Syn" || s == "VecStim") {
+        if (s == "ExpSyn" || s == "Exp2Syn" || s == "VecStim" || s == "NetStim") {
             Model::PostSynState ps;
             ps.mech = mm;
             ps.type_id = type_id;
@@ -1069,8 +1202,9 @@ static int finalize_model(Model* m) {
             ps.weight.assign(mm->n, 0.0);
             ps.receive_idx.assign(mm->n + 1, 0);
             ps.receive_flag.assign(mm->n + 1, -1);
-            ps.artificial = (s == "VecStim");
-            if (ps.artificial) m->vs_postsyn = (int)m->postsyns.size();
+            ps.artificial = (s == "VecStim" || s == "NetStim");
+            if (s == "VecStim") m->vs_postsyn = (int)m->postsyns.size();
+            if (s == "NetStim") m->ns_postsyn = (int)m->postsyns.size();
             m->postsyns.push_back(std::move(ps));
         }
     }
@@ -1096,8 +1230,9 @@ static int finalize_model(Model* m) {
     }
     int npre = (int)m->pre_node.size();
     int nvs = m->mechs.count("VecStim") ? m->mechs["VecStim"]->n : 0;
-    m->spk_vec.assign(npre + nvs, Model::Spike());
-    m->spk_flags.assign(npre + nvs, Model::INVALID);
+    int nns = m->mechs.count("NetStim") ? m->mechs["NetStim"]->n : 0;
+    m->spk_vec.assign(npre + nvs + nns, Model::Spike());
+    m->spk_flags.assign(npre + nvs + nns, Model::INVALID);
     m->pre_flag.assign(npre, 0);
     m->spk_output.assign(npre, {});
     if ((int)m->vs_times.size() != nvs) m->vs_times.resize(nvs);
@@ -1107,7 +1242,8 @@ static int finalize_model(Model* m) {
     return 0;
 }
 
-// Netcon into a synapse instance.  src_kind 0: real presyn index, 1: VecStim instance.
+// Netcon into a synapse instance.  src_kind 0: real presyn index, 1: VecStim instance,
+// 2: NetStim instance.
 // The reference keeps one source per synapse instance (coredat_to_innerdat.cpp:356-364).
 int hxo_add_netcon(void* h, int src_kind, int src, const char* target, int inst, double weight, double delay) {
     auto* m = static_cast<Model*>(h);
@@ -1116,7 +1252,9 @@ int hxo_add_netcon(void* h, int src_kind, int src, const char* target, int inst,
         if (ps.mech->name != target) continue;
         if (inst < 0 || inst >= ps.mech->n) return -1;
         int npre = (int)m->pre_node.size();
-        uint32_t slot = src_kind == 0 ? (uint32_t)src : (uint32_t)(npre + src);
+        int nvs = m->mechs.count("VecStim") ? m->mechs["VecStim"]->n : 0;
+        uint32_t slot = src_kind == 0 ? (uint32_t)src
+                      : src_kind == 1 ? (uint32_t)(npre + src) : (uint32_t)(npre + nvs + src);
         if (slot >= m->spk_vec.size()) return -1;
         ps.spk_vec_idx[inst] = slot;
         ps.weight[inst] = weight;
@@ -1289,6 +1427,28 @@ int hxo_adam_step(double* w, const double* grads, const int* group_size, int npa
         off += bs;
     }
     return 0;
+}
+
+// Philox4x32-10 with key (key0, key1) (known-answer checks of the NetStim streams).
+int hxo_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
+    uint32_t x0 = ctr[0], x1 = ctr[1], x2 = ctr[2], x3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int rnd = 0; rnd < 10; ++rnd) {
+        if (rnd > 0) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        uint64_t a = (uint64_t)0xD2511F53u * x0, b = (uint64_t)0xCD9E8D57u * x2;
+        uint32_t y0 = (uint32_t)(b >> 32) ^ x1 ^ k0, y1 = (uint32_t)b;
+        uint32_t y2 = (uint32_t)(a >> 32) ^ x3 ^ k1, y3 = (uint32_t)a;
+        x0 = y0; x1 = y1; x2 = y2; x3 = y3;
+    }
+    out[0] = x0; out[1] = x1; out[2] = x2; out[3] = x3;
+    return 0;
+}
+
+// NetStim spikes emitted since finitialize, in emission order.
+int hxo_netstim_spikes(void* h, double* t, int* inst, int cap) {
+    auto* m = static_cast<Model*>(h);
+    int n = (int)m->ns_spikes.size();
+    for (int i = 0; i < n && i < cap; ++i) { t[i] = m->ns_spikes[i].first; inst[i] = m->ns_spikes[i].second; }
+    return n;
 }
 
 }  // extern "C"

@@ -201,3 +201,19 @@ def test_axial_coefficient_writes_reach_the_solver(gpu_lib):
     err = float(np.max(np.abs(o.traces() - g.traces())))
     print(f"  max |dv| after a/b writes {err:.3e}", flush=True)
     assert err < V_TOL
+
+
+def test_spike_file_matches_reference_format(gpu_lib, tmp_path):
+    """spk.dat as Simulate::output_spikes writes it (simulate.cpp:892-909): the oracle's
+    spikes sorted by (time, gid) and printed with "%.8g\\t%d"."""
+    spec = active_network(ncell=30, tstop=40.0)
+    print("case spike file ncell=30", flush=True)
+    o, g = run_both(spec, 40.0)
+    compare_spikes(o, g, spec.dt)
+    path = g.output_spikes(str(tmp_path / "out"))
+    got = open(path).read()
+    ot, og = o.spikes()
+    order = np.lexsort((og, ot))
+    want = "".join("%.8g\t%d\n" % (ot[i], og[i]) for i in order if og[i] > -1)
+    assert len(want) > 0
+    assert got == want
