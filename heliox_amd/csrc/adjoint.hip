@@ -174,13 +174,22 @@ __global__ void k_adam(AdamArgs A) {
     for (int k = b0; k < b1; ++k) sum += *A.grad[k];
     const double avg = sum / static_cast<double>(b1 - b0);
     const double sg = avg * A.impedance[g] * A.inv_record_steps;
-    const double m = A.beta1 * A.m[g] + (1.0 - A.beta1) * sg;
-    const double v = A.beta2 * A.v[g] + (1.0 - A.beta2) * sg * sg;
-    A.m[g] = m;
-    A.v[g] = v;
-    const double mhat = m / (1.0 - pow(A.beta1, static_cast<double>(A.step)));
-    const double vhat = v / (1.0 - pow(A.beta2, static_cast<double>(A.step)));
-    const double w = *A.w[b0] - A.lr * mhat / (sqrt(vhat) + A.eps);
+    double w;
+    if (A.type == 0) {
+        w = *A.w[b0] - A.lr * sg;
+    } else if (A.type == 1) {
+        const double vel = A.momentum * A.m[g] - A.lr * sg;
+        A.m[g] = vel;
+        w = *A.w[b0] + vel;
+    } else {
+        const double m = A.beta1 * A.m[g] + (1.0 - A.beta1) * sg;
+        const double v = A.beta2 * A.v[g] + (1.0 - A.beta2) * sg * sg;
+        A.m[g] = m;
+        A.v[g] = v;
+        const double mhat = m / (1.0 - pow(A.beta1, static_cast<double>(A.step)));
+        const double vhat = v / (1.0 - pow(A.beta2, static_cast<double>(A.step)));
+        w = *A.w[b0] - A.lr * mhat / (sqrt(vhat) + A.eps);
+    }
     for (int k = b0; k < b1; ++k) {
         *A.w[k] = w;
         *A.grad[k] = 0.0;

@@ -243,7 +243,11 @@ struct AdjStep {
 
 // Adam over tied parameter groups (optimizer.cpp:351-393): group g covers
 // entries [begin[g], begin[g+1]) of the weight and gradient pointer lists.
+// Optimizer step over tied parameter groups (optimizer.cpp:102-135 SGD, 190-240
+// momentum, 351-413 Adam): type 0 SGD, 1 momentum (m holds the velocity), 2 Adam.
 struct AdamArgs {
+    int type;
+    double momentum;
     int ngroup;
     const int* begin;
     double* const* w;
@@ -306,5 +310,6 @@ void launch_record(double* const* ptrs, int n, double* out, hipStream_t s);
 void launch_gap(const double* v, const int* src_node, double* vgap_col, const int* halfgap_inst, int n,
                 hipStream_t s);
 void launch_clear_ints(int* p, long long n, hipStream_t s);
+void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t s);
 
 }  // namespace hx

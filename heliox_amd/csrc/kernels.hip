@@ -1027,6 +1027,12 @@ __global__ void k_gap(const double* v, const int* src_node, double* vgap, const 
     if (i < n) vgap[inst[i]] = v[src_node[i]];
 }
 
+// Gap junctions added at run time (simulate.cpp:953-966 gap_transfer): *dst[i] = *src[i].
+__global__ void k_copy_ptrs(double* const* src, double* const* dst, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) *dst[i] = *src[i];
+}
+
 __global__ void k_clear_ints(int* p, long long n) {
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0;
@@ -1137,6 +1143,10 @@ void launch_record(double* const* ptrs, int n, double* out, hipStream_t s) {
 void launch_gap(const double* v, const int* src_node, double* vgap_col, const int* halfgap_inst, int n,
                 hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_gap, grid_for(n), dim3(kBlock), 0, s, v, src_node, vgap_col, halfgap_inst, n);
+}
+
+void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_copy_ptrs, grid_for(n), dim3(kBlock), 0, s, src, dst, n);
 }
 
 void launch_clear_ints(int* p, long long n, hipStream_t s) {

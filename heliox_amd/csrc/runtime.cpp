@@ -341,8 +341,12 @@ struct hx_sim {
     bool have_grad = false;
     bool adj_delta_dirty = true;
     struct AdamHost {
+        int type = 2;        // 0 SGD, 1 momentum, 2 Adam
+        double momentum = 0.9;
         double beta1 = 0.9, beta2 = 0.999, eps = 1e-8;
         long long step = 0;
+        double* d_ext = nullptr;     // external gradients (one per registered weight)
+        int n_ext = 0;
         std::vector<int> begin{0};
         std::vector<double*> w, g;
         std::vector<double> imp, m, v;
@@ -353,6 +357,26 @@ struct hx_sim {
         double *d_imp = nullptr, *d_m = nullptr, *d_v = nullptr;
     };
     std::vector<AdamHost> adams;
+    // gap junctions added at run time (Simulate::add_gap_source/target, simulate.cpp:998-1100)
+    struct GapMeta {
+        std::string mech, var;
+        int idx = 0;
+        std::vector<std::tuple<std::string, std::string, int>> targets;
+    };
+    std::map<int, GapMeta> gap_meta;
+    int next_sid = 0;
+    std::vector<double*> dg_src, dg_dst;
+    double** d_dg_src = nullptr;
+    double** d_dg_dst = nullptr;
+    bool dg_dirty = false;
+    bool static_gaps_on = true;       // cleared by hx_clear_all_gap_junctions
+    void launch_gap_transfers();
+    // spk.dat after each run call (SimWrapper::run / continue_run, SimWrapper.cpp:46-84)
+    bool spike_output = false;
+    std::string output_dir = "output";          // Simulate's default (simulate.cpp:30)
+    int after_run();
+    void ensure_grad_arrays();
+    int opt_add_group(int opt, const std::vector<double*>& w, const std::vector<double*>& g, double impedance);
     void tape_free() {
         for (void* p : {static_cast<void*>(d_tape_v), static_cast<void*>(d_tape_x), static_cast<void*>(d_tape_g),
                         static_cast<void*>(d_tape_evn), static_cast<void*>(d_tape_ev)})
@@ -1236,6 +1260,24 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
         r.klass = (c == ION_CONCI || c == ION_CONCO) ? 0 : 1;
         return r;
     }
+    // gradients of the adjoint (grad_<parameter>) and netcon weights, addressable by
+    // handles so optimizers can be given (weight, gradient) pairs
+    if ((id == M_HH && (var == "grad_gnabar" || var == "grad_gkbar")) || (id == M_PAS && var == "grad_g_pas") ||
+        (id == M_EXPSYN && var == "grad_weight")) {
+        if (idx < 0 || idx >= m.n) return r;
+        ensure_grad_arrays();
+        double* base = var == "grad_gnabar" ? d_grad_gnabar
+                       : var == "grad_gkbar" ? d_grad_gkbar
+                       : var == "grad_g_pas" ? d_grad_gpas
+                                             : d_grad_w;
+        r.dev = base + m.perm[idx];
+        return r;
+    }
+    if ((id == M_EXPSYN || id == M_EXP2SYN) && var == "weight") {
+        if (idx < 0 || idx >= m.n) return r;
+        r.dev = (id == M_EXPSYN ? d_es_weight : d_e2_weight) + m.perm[idx];
+        return r;
+    }
     if (id == M_CADYN && (var == "cai" || var == "ica")) {
         // CaDynamics_E2 keeps cai / ica in the ca_ion columns of its node
         if (idx < 0 || idx >= m.n) return r;
@@ -1510,8 +1552,25 @@ void hx_sim::tape_record() {
     ++tape_n;
 }
 
+// Gap transfers after the update (and at finitialize): the model's HalfGap
+// sources, then the transfers added at run time.
+void hx_sim::launch_gap_transfers() {
+    const bool stat = static_gaps_on && !gaps.empty();
+    if (!stat && dg_src.empty()) return;
+    if (dg_dirty) {
+        d_dg_src = dg_src.empty() ? nullptr : dupload(owned, dg_src);
+        d_dg_dst = dg_dst.empty() ? nullptr : dupload(owned, dg_dst);
+        dg_dirty = false;
+    }
+    tbegin(T_OTHER);
+    if (stat)
+        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
+    launch_copy_ptrs(d_dg_src, d_dg_dst, static_cast<int>(dg_src.size()), stream);
+    tend(T_OTHER);
+}
+
 bool hx_sim::want_multi_stream() const {
-    return group_streams_allowed && groups.size() > 1 && fused && vecplay.empty() && !tape_on &&
+    return group_streams_allowed && groups.size() > 1 && fused && vecplay.empty() && !tape_on && dg_src.empty() &&
            !(learn && learn->capturing()) && (mon_ref.empty() || mon_all_v);
 }
 
@@ -1633,11 +1692,7 @@ void hx_sim::step_once() {
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
     if (tape_on) tape_record();
-    if (!gaps.empty()) {
-        tbegin(T_OTHER);
-        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
-        tend(T_OTHER);
-    }
+    launch_gap_transfers();
     // t += dt/2 twice, exactly as the reference accumulates it
     double tn = tk;
     tn += 0.5 * dt;
@@ -1806,8 +1861,7 @@ void hx_sim::finitialize(double v_init) {
         launch_clear_ints(d_tape_evn, tape_cap, stream);
     }
     launch_set_v(d_v, nnode, v_init, stream);
-    if (!gaps.empty())
-        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
+    launch_gap_transfers();
     StepArgs A = step_args(0.0, 0, 0);
     for (int id = 0; id < M_COUNT; ++id)           // CoreNEURON order, ions before their users
         if (mech[id].present) launch_init(id, A, stream);
@@ -2056,7 +2110,7 @@ int hx_run(hx_sim* sim, double tstop) {
         sim->k = 0;
     }
     if (nstep > 0) sim->run_steps(nstep);
-    return 0;
+    return sim->after_run();
     API_END
 }
 
@@ -2065,8 +2119,114 @@ int hx_continue_run(hx_sim* sim, double runtime) {
     API_BEGIN
     int nstep = static_cast<int>(runtime / sim->dt);
     if (nstep > 0) sim->run_steps(nstep);
+    return sim->after_run();
+    API_END
+}
+
+int hx_sim::after_run() { return spike_output ? hx_output_spikes(this, output_dir.c_str()) : 0; }
+
+int hx_set_spike_output_enabled(hx_sim* sim, int enable) {
+    sim->spike_output = enable != 0;
+    return 0;
+}
+
+int hx_is_spike_output_enabled(hx_sim* sim) { return sim->spike_output ? 1 : 0; }
+
+int hx_set_output_dir(hx_sim* sim, const char* dir) {
+    if (!dir || !*dir) return sim->fail("set_output_dir: empty directory");
+    sim->output_dir = dir;
+    return 0;
+}
+
+// ---- gap junctions at run time (simulate.cpp:998-1100) ----
+int hx_add_gap_source(hx_sim* sim, int sid, const char* mech, const char* var, int idx) {
+    if (!mech || !var) return sim->fail("add_gap_source: null variable name");
+    if (sid < 0) {
+        sid = sim->next_sid++;
+        while (sim->gap_meta.count(sid)) sid = sim->next_sid++;
+    } else {
+        if (sim->gap_meta.count(sid)) return sim->fail("Gap junction with sid %d already exists", sid);
+        if (sid >= sim->next_sid) sim->next_sid = sid + 1;
+    }
+    hx_sim::GapMeta g;
+    g.mech = mech;
+    g.var = var;
+    g.idx = idx;
+    sim->gap_meta[sid] = g;
+    return sid;
+}
+
+int hx_add_gap_target(hx_sim* sim, int sid, const char* mech, const char* var, int idx) {
+    if (!check_loaded(sim)) return -1;
+    auto it = sim->gap_meta.find(sid);
+    if (it == sim->gap_meta.end()) return sim->fail("Gap junction with sid %d does not exist", sid);
+    if (!mech || !var) return sim->fail("add_gap_target: null variable name");
+    API_BEGIN
+    const Ref src = sim->resolve(it->second.mech, it->second.var, it->second.idx);
+    const Ref dst = sim->resolve(mech, var, idx);
+    if (!src.dev || !dst.dev) return sim->fail("Failed to resolve variable pointers");
+    it->second.targets.emplace_back(mech, var, idx);
+    sim->dg_src.push_back(src.dev);
+    sim->dg_dst.push_back(dst.dev);
+    sim->dg_dirty = true;
     return 0;
     API_END
+}
+
+int hx_clear_all_gap_junctions(hx_sim* sim) {
+    sim->gap_meta.clear();
+    sim->next_sid = 0;
+    sim->dg_src.clear();
+    sim->dg_dst.clear();
+    sim->dg_dirty = true;
+    sim->static_gaps_on = false;     // the reference clears the model's transfers too
+    return 0;
+}
+
+int hx_get_next_available_sid(hx_sim* sim) {
+    int sid = sim->next_sid;
+    while (sim->gap_meta.count(sid)) ++sid;
+    return sid;
+}
+
+int hx_get_gap_junction_sids(hx_sim* sim, int* sids, int cap) {
+    int n = 0;
+    for (auto& kv : sim->gap_meta) {
+        if (sids && n < cap) sids[n] = kv.first;
+        ++n;
+    }
+    return n;
+}
+
+int hx_get_gap_junction(hx_sim* sim, int sid, char* mech, int mech_cap, char* var, int var_cap, int* idx,
+                        int* num_targets) {
+    auto it = sim->gap_meta.find(sid);
+    if (it == sim->gap_meta.end()) return -1;
+    auto put = [](char* dst, int cap, const std::string& src) {
+        if (!dst || cap <= 0) return;
+        std::snprintf(dst, static_cast<size_t>(cap), "%s", src.c_str());
+    };
+    put(mech, mech_cap, it->second.mech);
+    put(var, var_cap, it->second.var);
+    if (idx) *idx = it->second.idx;
+    if (num_targets) *num_targets = static_cast<int>(it->second.targets.size());
+    return 0;
+}
+
+// ---- monitor and VecPlay lookups (SimRuntimeCore get_monitor_handle, get_vecplay_keys) ----
+int hx_get_monitor_handle(hx_sim* sim, const char* mech, const char* var, int idx) {
+    if (!mech || !var) return -1;
+    for (size_t i = 0; i < sim->mon_name.size(); ++i)
+        if (sim->mon_name[i].first == mech && sim->mon_name[i].second == var && sim->mon_idx[i] == idx)
+            return static_cast<int>(i);
+    return -1;
+}
+
+int hx_get_vecplay_keys(hx_sim* sim, char* buf, int cap) {
+    std::string all;
+    for (auto& vp : sim->vecplay) all += vp.mech + "\t" + vp.var + "\t" + std::to_string(vp.idx) + "\n";
+    if (buf && cap > 0) std::snprintf(buf, static_cast<size_t>(cap), "%s", all.c_str());
+    return static_cast<int>(all.size()) + 1;
 }
 
 int hx_fadvance(hx_sim* sim) {
@@ -2583,6 +2743,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "fused") return sim->fused ? 1 : 0;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());
     if (k == "solve_units") return sim->nunit;
+    if (k == "handles") return static_cast<long long>(sim->handles.size());
     if (k == "solve_unit_cells") return sim->unit_cells;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
@@ -2643,6 +2804,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (!sim->tape_on || sim->tape_n == 0) return sim->fail("no taped steps (hx_tape_begin, finitialize, run)");
+    if (!sim->dg_src.empty()) return sim->fail("the adjoint does not support gap transfers added at run time");
     if (nsample != sim->tape_n)
         return sim->fail("target has %d samples, the tape holds %d steps", nsample, sim->tape_n);
     if (nloss <= 0) return sim->fail("no loss nodes");
@@ -2679,10 +2841,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         const HostMech& pas = sim->mech[M_PAS];
         sim->d_lx = dalloc<double>(owned, std::max<long long>(1, 3 * (hh.present ? hh.dev.stride : 0)));
         sim->d_lg = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
-        sim->d_grad_gnabar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
-        sim->d_grad_gkbar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
-        sim->d_grad_gpas = dalloc<double>(owned, std::max(1, pas.present ? pas.n : 0));
-        sim->d_grad_w = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+        sim->ensure_grad_arrays();
     }
     if (!sim->d_adj_delta || sim->adj_delta_dirty) {
         // diagonal correction on the solver's tree, with the solver's coefficients
@@ -2808,6 +2967,7 @@ int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, i
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
     if (n <= 0) return sim->fail("empty parameter group");
     const std::string mn = mech ? mech : "", vn = var ? var : "";
+    sim->ensure_grad_arrays();
     double* grad = nullptr;
     int id = -1;
     if (mn == "hh" && vn == "gnabar") { grad = sim->d_grad_gnabar; id = M_HH; }
@@ -2816,21 +2976,15 @@ int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, i
     else if (mn == "ExpSyn" && vn == "weight") { grad = sim->d_grad_w; id = M_EXPSYN; }
     if (id < 0 || !sim->mech[id].present) return sim->fail("no trainable parameter %s.%s", mn.c_str(), vn.c_str());
     if (!grad) return sim->fail("gradients are allocated by the first hx_adjoint call");
-    auto& o = sim->adams[opt];
     const HostMech& m = sim->mech[id];
+    std::vector<double*> w, g;
     for (int k = 0; k < n; ++k) {
         if (inst[k] < 0 || inst[k] >= m.n) return sim->fail("instance %d out of range", inst[k]);
         const int dj = m.perm[inst[k]];
-        double* w = id == M_EXPSYN ? sim->d_es_weight + dj : sim->resolve(mn, vn, inst[k]).dev;
-        o.w.push_back(w);
-        o.g.push_back(grad + dj);
+        w.push_back(id == M_EXPSYN ? sim->d_es_weight + dj : sim->resolve(mn, vn, inst[k]).dev);
+        g.push_back(grad + dj);
     }
-    o.begin.push_back(static_cast<int>(o.w.size()));
-    o.imp.push_back(impedance);
-    o.m.push_back(0.0);
-    o.v.push_back(0.0);
-    o.dirty = true;
-    return static_cast<int>(o.imp.size()) - 1;
+    return sim->opt_add_group(opt, w, g, impedance);
     API_END
 }
 
@@ -2852,6 +3006,8 @@ int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps) {
     }
     ++o.step;
     AdamArgs A{};
+    A.type = o.type;
+    A.momentum = o.momentum;
     A.ngroup = ng;
     A.begin = o.d_begin;
     A.w = o.d_w;
@@ -2878,7 +3034,7 @@ int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* 
     const auto& o = sim->adams[opt];
     const int ng = static_cast<int>(o.imp.size());
     if (step) *step = o.step;
-    if (cap < ng) return sim->fail("output too small");
+    if ((m || v) && cap < ng) return sim->fail("output too small");
     for (int g = 0; g < ng; ++g) {
         if (m) m[g] = o.m[g];
         if (v) v[g] = o.v[g];
@@ -2886,6 +3042,182 @@ int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* 
     return ng;
 }
 
+
+void hx_sim::ensure_grad_arrays() {
+    if (d_grad_gnabar) return;
+    const HostMech& hh = mech[M_HH];
+    const HostMech& es = mech[M_EXPSYN];
+    const HostMech& pas = mech[M_PAS];
+    d_grad_gnabar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
+    d_grad_gkbar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
+    d_grad_gpas = dalloc<double>(owned, std::max(1, pas.present ? pas.n : 0));
+    d_grad_w = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+    HXC(hipMemset(d_grad_gnabar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0)));
+    HXC(hipMemset(d_grad_gkbar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0)));
+    HXC(hipMemset(d_grad_gpas, 0, sizeof(double) * std::max(1, pas.present ? pas.n : 0)));
+    HXC(hipMemset(d_grad_w, 0, sizeof(double) * std::max(1, es.present ? es.n : 0)));
+}
+
+int hx_sim::opt_add_group(int opt, const std::vector<double*>& w, const std::vector<double*>& g, double impedance) {
+    auto& o = adams[opt];
+    for (size_t k = 0; k < w.size(); ++k) {
+        o.w.push_back(w[k]);
+        o.g.push_back(g[k]);
+    }
+    o.begin.push_back(static_cast<int>(o.w.size()));
+    o.imp.push_back(impedance);
+    o.m.push_back(0.0);
+    o.v.push_back(0.0);
+    o.dirty = true;
+    return static_cast<int>(o.imp.size()) - 1;
+}
+
+// ---------------------------------------------------------------------------
+// optimizers with the reference's interface (SimWrapper.cpp:159-460,
+// simulate.cpp:1150-1260): parameters are (weight, gradient) variable handles,
+// a batch is one tied group (mean gradient, one update broadcast to every
+// weight), gradients are zeroed after each step
+// ---------------------------------------------------------------------------
+int hx_create_optimizer(hx_sim* sim, const char* type) {
+    if (!check_loaded(sim)) return -1;
+    std::string t = type ? type : "";
+    std::transform(t.begin(), t.end(), t.begin(), [](unsigned char c) { return std::tolower(c); });
+    hx_sim::AdamHost o;
+    if (t == "sgd") o.type = 0;
+    else if (t == "momentum" || t == "sgdmomentum" || t == "sgd_momentum") o.type = 1;
+    else if (t == "adam") o.type = 2;
+    else return sim->fail("Unsupported optimizer type: %s", type ? type : "");
+    sim->adams.push_back(o);
+    return static_cast<int>(sim->adams.size()) - 1;
+}
+
+int hx_configure_optimizer(hx_sim* sim, int opt, double momentum, double beta1, double beta2, double eps) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    auto& o = sim->adams[opt];
+    o.momentum = momentum;
+    o.beta1 = beta1;
+    o.beta2 = beta2;
+    o.eps = eps;
+    return 0;
+}
+
+int hx_optimizer_add_param_batch(hx_sim* sim, int opt, int n, const int* weight_handles, const int* grad_handles,
+                                 double impedance) {
+    if (!check_loaded(sim)) return -1;
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    if (n <= 0 || !weight_handles || !grad_handles)
+        return sim->fail("optimizer_add_param_batch: handle lists must be non-empty and have equal length");
+    std::vector<double*> w(n), g(n);
+    const int nh = static_cast<int>(sim->handles.size());
+    for (int i = 0; i < n; ++i) {
+        if (weight_handles[i] < 0 || weight_handles[i] >= nh)
+            return sim->fail("optimizer_add_param_batch: invalid weight handle %d", weight_handles[i]);
+        if (grad_handles[i] < 0 || grad_handles[i] >= nh)
+            return sim->fail("optimizer_add_param_batch: invalid grad handle %d", grad_handles[i]);
+        w[i] = sim->handles[weight_handles[i]].dev;
+        g[i] = sim->handles[grad_handles[i]].dev;
+    }
+    return sim->opt_add_group(opt, w, g, impedance);
+}
+
+int hx_optimizer_add_param(hx_sim* sim, int opt, int weight_handle, int grad_handle, double impedance) {
+    return hx_optimizer_add_param_batch(sim, opt, 1, &weight_handle, &grad_handle, impedance);
+}
+
+int hx_optimizer_step_with_inv_record_steps(hx_sim* sim, int opt, double lr, double inv_record_steps) {
+    return hx_adam_step(sim, opt, lr, inv_record_steps);
+}
+
+int hx_optimizer_step(hx_sim* sim, int opt, double lr, double record_time, double dt) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer_step: optimizer %d not found", opt);
+    if (record_time <= 0.0 || dt <= 0.0)
+        return sim->fail("optimizer_step: invalid record_time (%f) or dt (%f)", record_time, dt);
+    return hx_adam_step(sim, opt, lr, dt / record_time);   // simulate.cpp:1198-1211
+}
+
+int hx_optimizer_add_external_grads(hx_sim* sim, int opt, int n, const int* weight_handles, double impedance) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    if (n <= 0 || !weight_handles) return sim->fail("optimizer_add_external_grads: empty weight_handles");
+    if (!(impedance > 0.0)) return sim->fail("optimizer_add_external_grads: invalid impedance (%f)", impedance);
+    auto& o = sim->adams[opt];
+    const int nh = static_cast<int>(sim->handles.size());
+    for (int i = 0; i < n; ++i)
+        if (weight_handles[i] < 0 || weight_handles[i] >= nh)
+            return sim->fail("optimizer_add_external_grads: invalid weight handle %d", weight_handles[i]);
+    o.d_ext = dalloc<double>(sim->owned, n);
+    o.n_ext = n;
+    HXC(hipMemset(o.d_ext, 0, sizeof(double) * n));
+    for (int i = 0; i < n; ++i)      // one group per weight (SimWrapper.cpp:284-353)
+        sim->opt_add_group(opt, {sim->handles[weight_handles[i]].dev}, {o.d_ext + i}, impedance);
+    return 0;
+    API_END
+}
+
+int hx_optimizer_set_external_grads_f32(hx_sim* sim, int opt, int n, const float* grads) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    auto& o = sim->adams[opt];
+    if (!o.d_ext) return sim->fail("optimizer_set_external_grads_f32: optimizer %d has no external grads binding", opt);
+    if (n != o.n_ext || !grads)
+        return sim->fail("optimizer_set_external_grads_f32: grads shape mismatch (got %d expected %d)", n, o.n_ext);
+    API_BEGIN
+    std::vector<double> g(grads, grads + n);
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemcpy(o.d_ext, g.data(), sizeof(double) * n, hipMemcpyHostToDevice));
+    return 0;
+    API_END
+}
+
+int hx_optimizer_clear_external_grads(hx_sim* sim, int opt) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    auto& o = sim->adams[opt];
+    if (!o.d_ext) return 0;
+    API_BEGIN
+    HXC(hipStreamSynchronize(sim->stream));
+    HXC(hipMemset(o.d_ext, 0, sizeof(double) * o.n_ext));
+    return 0;
+    API_END
+}
+
+int hx_optimizer_reset_state(hx_sim* sim, int opt) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    auto& o = sim->adams[opt];
+    if (o.type == 2) o.step = 0;
+    std::fill(o.m.begin(), o.m.end(), 0.0);
+    std::fill(o.v.begin(), o.v.end(), 0.0);
+    o.dirty = true;
+    return 0;
+}
+
+int hx_optimizer_get_adam_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap, double* beta1,
+                                double* beta2, double* eps) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    const auto& o = sim->adams[opt];
+    if (o.type != 2) return sim->fail("optimizer %d is not Adam", opt);
+    if (beta1) *beta1 = o.beta1;
+    if (beta2) *beta2 = o.beta2;
+    if (eps) *eps = o.eps;
+    return hx_adam_get_state(sim, opt, step, m, v, cap);
+}
+
+int hx_optimizer_set_adam_state(hx_sim* sim, int opt, long long step, int n, const double* m, const double* v,
+                                double beta1, double beta2, double eps) {
+    if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
+    auto& o = sim->adams[opt];
+    if (o.type != 2) return sim->fail("optimizer %d is not Adam", opt);
+    if (n != static_cast<int>(o.imp.size()) || (n > 0 && (!m || !v)))
+        return sim->fail("optimizer_set_adam_state: state size %d does not match %zu parameters", n, o.imp.size());
+    if (step < 0) return sim->fail("optimizer_set_adam_state: negative step count");
+    o.step = step;
+    o.m.assign(m, m + n);
+    o.v.assign(v, v + n);
+    o.beta1 = beta1;
+    o.beta2 = beta2;
+    o.eps = eps;
+    o.dirty = true;
+    return 0;
+}
 
 // ---------------------------------------------------------------------------
 // learn gradient surface (LearnRuntime.cpp:197-2457)

@@ -123,6 +123,30 @@ SIGNATURES = {
     "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
     "hx_output_spikes": (C.c_int, [_P, C.c_char_p]),
+    "hx_set_spike_output_enabled": (C.c_int, [_P, C.c_int]),
+    "hx_is_spike_output_enabled": (C.c_int, [_P]),
+    "hx_set_output_dir": (C.c_int, [_P, C.c_char_p]),
+    "hx_add_gap_source": (C.c_int, [_P, C.c_int, C.c_char_p, C.c_char_p, C.c_int]),
+    "hx_add_gap_target": (C.c_int, [_P, C.c_int, C.c_char_p, C.c_char_p, C.c_int]),
+    "hx_clear_all_gap_junctions": (C.c_int, [_P]),
+    "hx_get_next_available_sid": (C.c_int, [_P]),
+    "hx_get_gap_junction_sids": (C.c_int, [_P, _I, C.c_int]),
+    "hx_get_gap_junction": (C.c_int, [_P, C.c_int, C.c_char_p, C.c_int, C.c_char_p, C.c_int, _I, _I]),
+    "hx_get_monitor_handle": (C.c_int, [_P, C.c_char_p, C.c_char_p, C.c_int]),
+    "hx_get_vecplay_keys": (C.c_int, [_P, C.c_char_p, C.c_int]),
+    "hx_create_optimizer": (C.c_int, [_P, C.c_char_p]),
+    "hx_configure_optimizer": (C.c_int, [_P, C.c_int, C.c_double, C.c_double, C.c_double, C.c_double]),
+    "hx_optimizer_add_param": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_double]),
+    "hx_optimizer_add_param_batch": (C.c_int, [_P, C.c_int, C.c_int, _I, _I, C.c_double]),
+    "hx_optimizer_step": (C.c_int, [_P, C.c_int, C.c_double, C.c_double, C.c_double]),
+    "hx_optimizer_step_with_inv_record_steps": (C.c_int, [_P, C.c_int, C.c_double, C.c_double]),
+    "hx_optimizer_add_external_grads": (C.c_int, [_P, C.c_int, C.c_int, _I, C.c_double]),
+    "hx_optimizer_set_external_grads_f32": (C.c_int, [_P, C.c_int, C.c_int, _F]),
+    "hx_optimizer_clear_external_grads": (C.c_int, [_P, C.c_int]),
+    "hx_optimizer_reset_state": (C.c_int, [_P, C.c_int]),
+    "hx_optimizer_get_adam_state": (C.c_int, [_P, C.c_int, C.POINTER(C.c_longlong), _D, _D, C.c_int, _D, _D, _D]),
+    "hx_optimizer_set_adam_state": (C.c_int, [_P, C.c_int, C.c_longlong, C.c_int, _D, _D, C.c_double, C.c_double,
+                                              C.c_double]),
     "hx_random123_philox4x32": (C.c_int, [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
     "hx_netstim_train": (C.c_int, [C.c_double, C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
                                    C.c_uint, C.c_uint, C.c_uint, _D, C.c_int]),
@@ -335,6 +359,20 @@ class Sim:
             self.monitor_handles.append(h)
         return h
 
+    def add_monitor_with_array(self, mech: str, var: str, idx: int, array_index: int) -> int:
+        """Variables here are scalars: array_index must be 0."""
+        if int(array_index) != 0:
+            return self._pyfail(f"{mech}.{var} is not an array variable (array_index {array_index})")
+        return self.add_monitor(mech, var, idx)
+
+    def get_monitor_handle(self, mech: str, var: str, idx: int) -> int:
+        return lib().hx_get_monitor_handle(self._h, _b(mech), _b(var), int(idx))
+
+    def get_monitor_handle_with_array(self, mech: str, var: str, idx: int, array_index: int) -> int:
+        if int(array_index) != 0:
+            return self._pyfail(f"{mech}.{var} is not an array variable (array_index {array_index})")
+        return self.get_monitor_handle(mech, var, idx)
+
     def flush_recorders(self) -> int:
         return self._rc(lib().hx_flush_recorders(self._h))
 
@@ -360,6 +398,21 @@ class Sim:
     # --------------------------------------------------------------- variables
     def get_variable_handle(self, mech: str, var: str, idx: int) -> int:
         return lib().hx_get_variable_handle(self._h, _b(mech), _b(var), int(idx))
+
+    def get_variable_handle_with_array(self, mech: str, var: str, idx: int, array_index: int) -> int:
+        if int(array_index) != 0:
+            return self._pyfail(f"{mech}.{var} is not an array variable (array_index {array_index})")
+        return self.get_variable_handle(mech, var, idx)
+
+    def get_variable_value_with_array(self, mech: str, var: str, idx: int, array_index: int) -> float:
+        if int(array_index) != 0:
+            raise HelioxError(f"{mech}.{var} is not an array variable (array_index {array_index})")
+        return self.get_variable_value(mech, var, idx)
+
+    def set_variable_value_with_array(self, val: float, mech: str, var: str, idx: int, array_index: int) -> int:
+        if int(array_index) != 0:
+            return self._pyfail(f"{mech}.{var} is not an array variable (array_index {array_index})")
+        return self.set_variable_value(val, mech, var, idx)
 
     def get_variable_by_handle(self, handle: int) -> float:
         out = np.zeros(1)
@@ -417,6 +470,13 @@ class Sim:
     def remove_vecplay(self, mech: str, var: str, idx: int) -> int:
         return self._rc(lib().hx_remove_vecplay(self._h, _b(mech), _b(var), int(idx)))
 
+    def get_all_vecplay_keys(self) -> List[List[str]]:
+        L = lib()
+        n = L.hx_get_vecplay_keys(self._h, None, 0)
+        buf = C.create_string_buffer(max(n, 1))
+        L.hx_get_vecplay_keys(self._h, buf, len(buf))
+        return [line.split("\t") for line in buf.value.decode().splitlines() if line]
+
     def has_vecplay(self, mech: str, var: str, idx: int) -> bool:
         return lib().hx_has_vecplay(self._h, _b(mech), _b(var), int(idx)) == 1
 
@@ -434,6 +494,16 @@ class Sim:
         returns the file's path."""
         self._chk(lib().hx_output_spikes(self._h, _b(folder)), "output_spikes")
         return os.path.join(folder, "spk.dat")
+
+    def set_spike_output_enabled(self, enable: bool) -> int:
+        """Write spk.dat into the output directory after every run / continue_run."""
+        return self._rc(lib().hx_set_spike_output_enabled(self._h, int(bool(enable))))
+
+    def is_spike_output_enabled(self) -> bool:
+        return bool(lib().hx_is_spike_output_enabled(self._h))
+
+    def set_output_dir(self, dir: str) -> int:
+        return self._rc(lib().hx_set_output_dir(self._h, _b(dir)))
 
     def get_spk_by_gid(self, gid: int) -> List[float]:
         L = lib()
@@ -501,6 +571,200 @@ class Sim:
 
     # ---- learn gradient surface (SimWrapper.cpp:533-1183; PyBindings.cpp:88-200).
     # Like the reference's bindings these return 0 / -1; last_error() holds the message.
+    # --------------------------------------------------------------- optimizers
+    def create_optimizer(self, optimizer_type: str) -> int:
+        """"sgd", "momentum" or "adam"; returns the optimizer id (-1 on error)."""
+        return lib().hx_create_optimizer(self._h, _b(optimizer_type))
+
+    def configure_optimizer(self, optimizer_id: int, momentum: float = 0.9, beta1: float = 0.9,
+                            beta2: float = 0.999, epsilon: float = 1e-8) -> int:
+        return self._rc(lib().hx_configure_optimizer(self._h, int(optimizer_id), float(momentum), float(beta1),
+                                                     float(beta2), float(epsilon)))
+
+    def optimizer_add_param(self, optimizer_id: int, weight_handle: int, grad_handle: int,
+                            impedance: float = 1.0) -> int:
+        return lib().hx_optimizer_add_param(self._h, int(optimizer_id), int(weight_handle), int(grad_handle),
+                                            float(impedance))
+
+    def optimizer_add_param_batch(self, optimizer_id: int, weight_handles: Sequence[int],
+                                  grad_handles: Sequence[int], impedance: float = 1.0) -> int:
+        w = np.ascontiguousarray(weight_handles, np.int32)
+        g = np.ascontiguousarray(grad_handles, np.int32)
+        if w.size != g.size or w.size == 0:
+            return self._pyfail("optimizer_add_param_batch: handle lists must be non-empty and have equal length")
+        return lib().hx_optimizer_add_param_batch(self._h, int(optimizer_id), w.size, _ip(w), _ip(g),
+                                                  float(impedance))
+
+    def optimizer_step(self, optimizer_id: int, learning_rate: float, record_time: float, dt: float) -> int:
+        return self._rc(lib().hx_optimizer_step(self._h, int(optimizer_id), float(learning_rate),
+                                                float(record_time), float(dt)))
+
+    def optimizer_step_with_inv_record_steps(self, optimizer_id: int, learning_rate: float,
+                                             inv_record_steps: float) -> int:
+        return self._rc(lib().hx_optimizer_step_with_inv_record_steps(self._h, int(optimizer_id),
+                                                                      float(learning_rate),
+                                                                      float(inv_record_steps)))
+
+    def optimizer_add_external_grads(self, optimizer_id: int, weight_handles: Sequence[int],
+                                     impedance: float = 1.0) -> int:
+        w = np.ascontiguousarray(weight_handles, np.int32)
+        return self._rc(lib().hx_optimizer_add_external_grads(self._h, int(optimizer_id), w.size, _ip(w),
+                                                              float(impedance)))
+
+    def optimizer_set_external_grads_f32(self, optimizer_id: int, grads: np.ndarray) -> int:
+        g = np.asarray(grads)
+        if g.dtype != np.float32 or g.ndim != 1 or not g.flags.c_contiguous:
+            raise TypeError("grads must be a 1-D C-contiguous float32 array")
+        return self._rc(lib().hx_optimizer_set_external_grads_f32(self._h, int(optimizer_id), g.size,
+                                                                  g.ctypes.data_as(_F)))
+
+    def optimizer_clear_external_grads(self, optimizer_id: int) -> int:
+        return self._rc(lib().hx_optimizer_clear_external_grads(self._h, int(optimizer_id)))
+
+    def optimizer_reset_state(self, optimizer_id: int) -> int:
+        return self._rc(lib().hx_optimizer_reset_state(self._h, int(optimizer_id)))
+
+    def optimizer_get_adam_state(self, optimizer_id: int):
+        """(step_count, m, v, beta1, beta2, epsilon); the defaults with empty m, v if the
+        optimizer is not Adam (as SimWrapper::optimizer_get_adam_state)."""
+        L = lib()
+        step = C.c_longlong(0)
+        b1, b2, ep = np.zeros(1), np.zeros(1), np.zeros(1)
+        n = L.hx_optimizer_get_adam_state(self._h, int(optimizer_id), C.byref(step), None, None, 0,
+                                          _dp(b1), _dp(b2), _dp(ep))
+        if n < 0:
+            return 0, [], [], 0.9, 0.999, 1e-8
+        m, v = np.zeros(max(n, 1)), np.zeros(max(n, 1))
+        L.hx_optimizer_get_adam_state(self._h, int(optimizer_id), C.byref(step), _dp(m), _dp(v), n,
+                                      _dp(b1), _dp(b2), _dp(ep))
+        return int(step.value), m[:n].tolist(), v[:n].tolist(), float(b1[0]), float(b2[0]), float(ep[0])
+
+    def optimizer_set_adam_state(self, optimizer_id: int, step_count: int, m: Sequence[float], v: Sequence[float],
+                                 beta1: float = 0.9, beta2: float = 0.999, epsilon: float = 1e-8) -> int:
+        mm = np.ascontiguousarray(m, np.float64)
+        vv = np.ascontiguousarray(v, np.float64)
+        if mm.size != vv.size:
+            return self._pyfail("optimizer_set_adam_state: m and v differ in length")
+        return self._rc(lib().hx_optimizer_set_adam_state(self._h, int(optimizer_id), int(step_count), mm.size,
+                                                          _dp(mm), _dp(vv), float(beta1), float(beta2),
+                                                          float(epsilon)))
+
+    # --------------------------------------------------------------- gap junctions
+    def add_gap_source(self, sid: int, src_mech: str, src_var: str, src_idx: int) -> int:
+        return lib().hx_add_gap_source(self._h, int(sid), _b(src_mech), _b(src_var), int(src_idx))
+
+    def add_gap_target(self, sid: int, tgt_mech: str, tgt_var: str, tgt_idx: int) -> int:
+        return self._rc(lib().hx_add_gap_target(self._h, int(sid), _b(tgt_mech), _b(tgt_var), int(tgt_idx)))
+
+    def clear_all_gap_junctions(self) -> int:
+        return self._rc(lib().hx_clear_all_gap_junctions(self._h))
+
+    def get_next_available_sid(self) -> int:
+        return lib().hx_get_next_available_sid(self._h)
+
+    def get_gap_junction(self, sid: int) -> Dict[str, object]:
+        mech = C.create_string_buffer(256)
+        var = C.create_string_buffer(256)
+        idx = C.c_int(0)
+        nt = C.c_int(0)
+        if lib().hx_get_gap_junction(self._h, int(sid), mech, 256, var, 256, C.byref(idx), C.byref(nt)) != 0:
+            return {}
+        return {"src_mech": mech.value.decode(), "src_var": var.value.decode(), "src_idx": idx.value,
+                "num_targets": nt.value, "is_dynamic": True}
+
+    def get_all_gap_junctions(self) -> Dict[int, Dict[str, object]]:
+        L = lib()
+        n = L.hx_get_gap_junction_sids(self._h, None, 0)
+        sids = np.zeros(max(n, 1), np.int32)
+        L.hx_get_gap_junction_sids(self._h, _ip(sids), n)
+        return {int(s): self.get_gap_junction(int(s)) for s in sids[:n]}
+
+    # --------------------------------------------------------------- input batches
+    def register_netstim_batch(self, handle_triplets, interval_scale: float = 1.0, start_base: float = 0.0,
+                               epsilon: float = 1e-6, number: float = 1.0) -> int:
+        """NetStim inputs driven by pixel values (SimRuntimeCore.cpp:694-790): triplets of
+        (interval, start, number) variable handles; see set_input_batch_pixels."""
+        trip = [tuple(int(x) for x in t) for t in handle_triplets]
+        if not trip:
+            return self._pyfail("register_netstim_batch: handle list is empty")
+        nh = lib().hx_get_info(self._h, b"handles")
+        if any(h < 0 or h >= nh for t in trip for h in t):
+            return self._pyfail("register_netstim_batch: invalid handle")
+        return self._add_batch(("NetStim", trip, float(interval_scale), float(start_base), float(epsilon),
+                                float(number)))
+
+    def register_vecstim_batch(self, mech_indices, spike_scale: float = 1.0, start_base: float = 0.0,
+                               epsilon: float = 1e-6, spike_count: int = 1) -> int:
+        """VecStim inputs driven by pixel values (SimRuntimeCore.cpp:791-826): one VecStim
+        instance per pixel."""
+        idx = [int(i) for i in mech_indices]
+        if not idx:
+            return self._pyfail("register_vecstim_batch: mech list is empty")
+        if any(i < 0 for i in idx):
+            return self._pyfail("register_vecstim_batch: invalid mech index")
+        return self._add_batch(("VecStim", idx, float(spike_scale), float(start_base), float(epsilon),
+                                int(spike_count)))
+
+    def _add_batch(self, b) -> int:
+        if not hasattr(self, "_batches"):
+            self._batches = []
+        self._batches.append(b)
+        return len(self._batches) - 1
+
+    def set_input_batch_pixels(self, batch_id: int, pixels) -> int:
+        """Encode one input image (SimRuntimeCore.cpp:827-915): with d = max(pixel + eps, eps),
+        NetStim interval = interval_scale / d, start = start_base + interval, number as given;
+        VecStim spikes at start_base + k * spike_scale / d for k = 1..spike_count.  NetStim
+        and VecStim inputs take the new values at the next finitialize."""
+        bs = getattr(self, "_batches", [])
+        if not 0 <= int(batch_id) < len(bs):
+            return self._pyfail(f"set_input_batch_pixels: batch {batch_id} not found")
+        kind, items, scale, base, eps, count = bs[int(batch_id)]
+        px = np.asarray(pixels, np.float64).ravel()
+        if px.size != len(items):
+            return self._pyfail(f"set_input_batch_pixels: size mismatch batch={len(items)}, got={px.size}")
+        d = np.maximum(px + eps, eps)
+        if kind == "NetStim":
+            for (hi, hs, hn), dv in zip(items, d):
+                interval = scale / dv
+                for h, val in ((hi, interval), (hs, base + interval), (hn, count)):
+                    if self.set_variable_by_handle(h, val) != 0:
+                        return -1
+            return 0
+        L = lib()
+        for mi, dv in zip(items, d):
+            step = scale / dv
+            times = np.ascontiguousarray(base + step * np.arange(1, count + 1, dtype=np.float64))
+            if L.hx_model_set_vecstim(self._h, mi, times.size, _dp(times)) != 0:
+                return -1
+        return 0
+
+    # --------------------------------------------------------------- not provided
+    def set_data_path(self, path: str) -> int:
+        """CoreNEURON export directories are not read here: build the model with
+        load_model_from_spec (node arrays, mechanism columns, netcons)."""
+        return self._pyfail("set_data_path: CoreNEURON exports are not read; use load_model_from_spec")
+
+    def load_model(self, *args, **kwargs) -> int:
+        return self._pyfail("load_model: CoreNEURON exports are not read; use load_model_from_spec")
+
+    def set_permute_type(self, permute_type: int) -> int:
+        """Accepted for compatibility: the solver uses its own node order (solve units)."""
+        if int(permute_type) not in (0, 1, 2, 3):
+            return self._pyfail(f"set_permute_type: unknown type {permute_type}")
+        self._permute_type = int(permute_type)
+        return 0
+
+    def set_user_mod_num(self, num: int) -> None:
+        """Accepted for compatibility (user mechanisms are compiled into the library)."""
+        self._user_mod_num = int(num)
+
+    def call_mech_func(self, mech_name: str, func_name: str, *args) -> float:
+        """The reference's FunctionRegistry calls belong to mechanism families outside this
+        library; none is registered."""
+        self._pyfail(f"call_mech_func: no function {mech_name}.{func_name}")
+        return -1.0
+
     def set_dense_blocks_f32(self, blocks) -> int:
         """Upload (bn, bn, K_len) float32 blocks; returns K_len or -1 (SimWrapper.cpp:533-572)."""
         self._py_err = None

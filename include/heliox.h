@@ -125,6 +125,63 @@ int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap);
  * ordered by time and then gid; spikes of negative gids are left out. */
 int hx_output_spikes(hx_sim* sim, const char* folder);
 
+/* spk.dat after every hx_run / hx_continue_run (SimWrapper::run, continue_run,
+ * SimWrapper.cpp:46-84; set_spike_output_enabled, set_output_dir).  Default: off, folder
+ * "output" (simulate.cpp:30). */
+int hx_set_spike_output_enabled(hx_sim* sim, int enable);
+int hx_is_spike_output_enabled(hx_sim* sim);
+int hx_set_output_dir(hx_sim* sim, const char* dir);
+
+/* ---- gap junctions added at run time (Simulate::add_gap_source / add_gap_target /
+ *      clear_all_gap_junctions / get_gap_junction / get_next_available_sid,
+ *      simulate.cpp:998-1100).  After each update (and at finitialize) every target
+ *      variable receives its source variable's value.  sid < 0 picks the next free id;
+ *      the call returns the sid.  Clearing also stops the model's own HalfGap transfers,
+ *      as the reference's does.  Runs with such transfers stay on one stream, and the
+ *      adjoint refuses them. ---- */
+int hx_add_gap_source(hx_sim* sim, int sid, const char* mech, const char* var, int idx);
+int hx_add_gap_target(hx_sim* sim, int sid, const char* mech, const char* var, int idx);
+int hx_clear_all_gap_junctions(hx_sim* sim);
+int hx_get_next_available_sid(hx_sim* sim);
+/* Ids of all gap junctions (up to cap written); returns their count. */
+int hx_get_gap_junction_sids(hx_sim* sim, int* sids, int cap);
+/* Source of gap junction sid and its number of targets; -1 if there is no such sid. */
+int hx_get_gap_junction(hx_sim* sim, int sid, char* mech, int mech_cap, char* var, int var_cap, int* idx,
+                        int* num_targets);
+
+/* Handle of the monitor on (mech, var, idx), -1 if none (SimRuntimeCore get_monitor_handle). */
+int hx_get_monitor_handle(hx_sim* sim, const char* mech, const char* var, int idx);
+/* All VecPlay keys as "mech\tvar\tidx\n" lines into buf; returns the size needed. */
+int hx_get_vecplay_keys(hx_sim* sim, char* buf, int cap);
+
+/* ---- optimizers (SimWrapper.cpp:159-460, simulate.cpp:1150-1260, optimizer.cpp:102-457).
+ * type "sgd", "momentum" (or "sgdmomentum", "sgd_momentum") or "adam"; returns the id.
+ * A parameter batch is one tied group: the update uses the mean of its gradients times
+ * impedance times inv_record_steps and writes the same value to all its weights; the
+ * gradients are zeroed after each step.  Weights and gradients are variable handles: any
+ * variable, including ExpSyn/Exp2Syn "weight" (netcon weights) and the adjoint's gradients
+ * hh "grad_gnabar" / "grad_gkbar", pas "grad_g_pas" and ExpSyn "grad_weight". ---- */
+int hx_create_optimizer(hx_sim* sim, const char* type);
+int hx_configure_optimizer(hx_sim* sim, int opt, double momentum, double beta1, double beta2, double eps);
+int hx_optimizer_add_param(hx_sim* sim, int opt, int weight_handle, int grad_handle, double impedance);
+int hx_optimizer_add_param_batch(hx_sim* sim, int opt, int n, const int* weight_handles, const int* grad_handles,
+                                 double impedance);
+/* inv_record_steps = dt / record_time (simulate.cpp:1198-1211). */
+int hx_optimizer_step(hx_sim* sim, int opt, double lr, double record_time, double dt);
+int hx_optimizer_step_with_inv_record_steps(hx_sim* sim, int opt, double lr, double inv_record_steps);
+/* One group per weight handle with a library-owned gradient, set by
+ * hx_optimizer_set_external_grads_f32 (n values, the handles' order). */
+int hx_optimizer_add_external_grads(hx_sim* sim, int opt, int n, const int* weight_handles, double impedance);
+int hx_optimizer_set_external_grads_f32(hx_sim* sim, int opt, int n, const float* grads);
+int hx_optimizer_clear_external_grads(hx_sim* sim, int opt);
+int hx_optimizer_reset_state(hx_sim* sim, int opt);
+/* Adam only: step count, per-group m and v (up to cap), and the hyperparameters; returns the
+ * group count. */
+int hx_optimizer_get_adam_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap, double* beta1,
+                                double* beta2, double* eps);
+int hx_optimizer_set_adam_state(hx_sim* sim, int opt, long long step, int n, const double* m, const double* v,
+                                double beta1, double beta2, double eps);
+
 /* ---- capacity and diagnostics ---- */
 /* Event-ring capacity per delivery step (default sized from the model). */
 int hx_set_event_capacity(hx_sim* sim, int per_step);
