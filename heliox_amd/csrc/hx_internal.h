@@ -87,6 +87,9 @@ struct StepArgs {
     MechDev m[M_COUNT];
     unsigned dense_mask;          // mechanisms processed by the fused node kernel
     int do_state;                 // finish the previous step's state update first
+    int cadyn_skip;               // ... except CaDynamics_E2, already updated by the last current pass
+    int cadyn_after;              // update CaDynamics_E2 right after this pass's ica (its state
+                                  // depends on ica and cai only, so this is the step's own update)
     int do_current;
     int write_assigned;           // also store assigned outputs (i, ina, gna, minf, ...)
     unsigned ion_store;           // ion x (0 na, 1 k, 2 ca): bit 2x stores cur, bit 2x+1 stores erev

@@ -221,10 +221,10 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     HHState hs{};
     CaHVAState cs{};
     double hl = 0.0, cai = 0.0;
-    const bool have_cai = A.do_state && HAS(M_CADYN);
+    const bool have_cai = A.do_state && HAS(M_CADYN) && !A.cadyn_skip;
     if (live) {
         if (A.do_state) {
-            if (HAS(M_CADYN)) {
+            if (HAS(M_CADYN) && !A.cadyn_skip) {
                 double* conci = ca.col(ION_CONCI);
                 cai = cadyn_state(A, A.m[M_CADYN], i, lds_(conci + i), lds_(ca.col(ION_CUR) + i));
                 sts_(conci + i, cai);
@@ -260,7 +260,10 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     }
     rhs += prhs;   // ExpSyn, Exp2Syn (mechanism types 5, 6)
     d += pd;
-    if (HAS(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai, cai);
+    // cai for the Nernst potential and, when CaDynamics_E2 runs after this pass, for its update
+    const bool need_ci = HAS(M_CADYN) && A.cadyn_after;
+    const double ci = have_cai ? cai : (need_ci ? lds_(ca.col(ION_CONCI) + i) : 0.0);
+    if (HAS(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai || need_ci, ci);
     if (HAS(M_CAHVA)) {
         cur = cahva_cur(A, A.m[M_CAHVA], i, v, cs, eca, g);
         ica += cur;
@@ -272,6 +275,7 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     if (HAS(M_NA_ION)) dense_ion_store(A, na, 0, i, ina);
     if (HAS(M_K_ION)) dense_ion_store(A, kk, 1, i, ik);
     if (HAS(M_CA_ION)) dense_ion_store(A, ca, 2, i, ica);
+    if (need_ci) sts_(ca.col(ION_CONCI) + i, cadyn_state(A, A.m[M_CADYN], i, ci, ica));
 }
 
 // ---------------------------------------------------------------------------

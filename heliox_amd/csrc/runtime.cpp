@@ -231,6 +231,12 @@ struct hx_sim {
     int ion_type_uniform[3] = {-1, -1, -1};
     unsigned dense_mask = 0;
     bool fused = false;
+    // CaDynamics_E2 updated by the current pass that computes its ica (see k_dense):
+    // allowed when nothing samples calcium between the two passes
+    bool cadyn_eager = false;
+    bool cadyn_done = false;      // the last current pass already did this step's update
+    int pass_cadyn_skip = 0, pass_cadyn_after = 0;
+    void refresh_cadyn_eager();
     bool write_assigned = false;
     bool need_split_for_monitor = false;
 
@@ -708,6 +714,19 @@ void hx_sim::recompute_fused() {
     }
     if (need_split_for_monitor) fuse = false;
     fused = fuse;
+}
+
+// CaDynamics_E2's state depends on ica and cai only, so in the fused schedule
+// the current pass that computes ica can apply the step's update at once (one
+// calcium read and write per step instead of also storing and reloading ica).
+// Exact unless something samples calcium between the current and state passes:
+// a monitor on ca_ion or CaDynamics_E2, taping or signal capture.
+void hx_sim::refresh_cadyn_eager() {
+    bool ok = fused && mech[M_CADYN].present && (dense_mask & (1u << M_CADYN)) && !tape_on &&
+              !(learn && learn->capturing());
+    for (size_t i = 0; ok && i < mon_name.size(); ++i)
+        if (mon_name[i].first == "ca_ion" || mon_name[i].first == "CaDynamics_E2") ok = false;
+    cadyn_eager = ok;
 }
 
 void hx_sim::upload() {
@@ -1313,6 +1332,8 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     for (int id = 0; id < M_COUNT; ++id) A.m[id] = mech[id].dev;
     A.dense_mask = dense_mask;
     A.do_state = do_state;
+    A.cadyn_skip = do_state ? pass_cadyn_skip : 0;
+    A.cadyn_after = do_current ? pass_cadyn_after : 0;
     A.do_current = do_current;
     const bool assigned = write_assigned || final_step;
     A.write_assigned = assigned ? 1 : 0;
@@ -1327,7 +1348,7 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
         A.ion_store = 0;
         for (int x = 0; x < 3; ++x) {
             const bool ext = assigned || (need & (1u << x));
-            if (ext || (x == 2 && mech[M_CADYN].present)) A.ion_store |= 1u << (2 * x);
+            if (ext || (x == 2 && mech[M_CADYN].present && !pass_cadyn_after)) A.ion_store |= 1u << (2 * x);
             if (ext) A.ion_store |= 2u << (2 * x);
             A.ion_type[x] = ion_type_uniform[x];
         }
@@ -1587,6 +1608,8 @@ void hx_sim::step_once_groups() {
     const StepArgs post = step_args(tn, 1, 0);
     const size_t nm = mon_ref.size();
     if (pending && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    pass_cadyn_skip = cadyn_done ? 1 : 0;
+    pass_cadyn_after = cadyn_eager ? 1 : 0;
     for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
         CellGroup& cg = groups[g];
         hipStream_t s = cg.s;
@@ -1646,6 +1669,8 @@ void hx_sim::step_once_groups() {
         }
     }
     if (pending && nm) mon_buf_fill++;
+    cadyn_done = cadyn_eager;
+    pass_cadyn_skip = pass_cadyn_after = 0;
     t = tn;
     k += 1;
     state_pending = true;
@@ -1667,7 +1692,11 @@ void hx_sim::step_once() {
         // currents with this step's deliveries in place
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        pass_cadyn_skip = cadyn_done ? 1 : 0;
+        pass_cadyn_after = cadyn_eager ? 1 : 0;
         launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
+        cadyn_done = cadyn_eager;
+        pass_cadyn_skip = pass_cadyn_after = 0;
         if (state_pending) launch_record();
     } else {
         launch_events(k, tk);
@@ -1718,6 +1747,11 @@ void hx_sim::step_once() {
 
 void hx_sim::finish_pending() {
     if (!state_pending) return;
+    pass_cadyn_skip = cadyn_done ? 1 : 0;
+    struct Reset {   // the pending pass completes this step's updates
+        hx_sim* s;
+        ~Reset() { s->pass_cadyn_skip = 0; s->cadyn_done = false; }
+    } reset{this};
     if (multi_stream) {
         const size_t nm = mon_ref.size();
         if (nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
@@ -1772,6 +1806,7 @@ void hx_sim::sync_outputs() {
 int hx_sim::run_steps(int nstep) {
     if (!initialized) throw std::runtime_error("finitialize must be called before stepping");
     ensure_ttab(k + nstep + 1);
+    refresh_cadyn_eager();
     if (mech[M_NETSTIM].present && mech[M_NETSTIM].n > 0 && k + nstep + 2 > ns_horizon) {
         // longer trains: the streams restart, so the events already delivered come
         // out the same and only events past the old horizon are added
@@ -1835,6 +1870,8 @@ void hx_sim::finitialize(double v_init) {
     t = 0.0;
     k = 0;
     state_pending = false;
+    cadyn_done = false;
+    pass_cadyn_skip = pass_cadyn_after = 0;
     ensure_ttab(1);
     if (!mon_ref.empty() && mon_buf_cap < 2) {
         mon_buf_cap = 2;
