@@ -217,3 +217,24 @@ def test_spike_file_matches_reference_format(gpu_lib, tmp_path):
     want = "".join("%.8g\t%d\n" % (ot[i], og[i]) for i in order if og[i] > -1)
     assert len(want) > 0
     assert got == want
+
+
+@pytest.mark.parametrize("groups", [1, 0])
+def test_calcium_update_in_the_current_pass_is_exact(gpu_lib, groups):
+    """CaDynamics_E2 updated right after its ica (the default) against the separate state
+    pass (selected by a monitor on ca_ion): the same bits."""
+    spec = build_config(3, 16, 10.0)
+    vm = [("global", "v", c) for c in range(0, 16, 3)]
+    runs = []
+    for extra in ([], [("ca_ion", "conci", 7)]):
+        g = Sim()
+        g.set_cell_groups(groups)
+        g.load_model_from_spec(dataclasses.replace(spec, monitors=vm + extra))
+        g.finitialize(-65.0)
+        g.continue_run(4.0)
+        g.continue_run(6.0)
+        runs.append(g)
+    a, b = runs
+    assert np.array_equal(a.traces(), b.traces()[: len(vm)])
+    assert np.array_equal(a.get_array("ca_ion", "conci"), b.get_array("ca_ion", "conci"))
+    assert np.array_equal(a.get_array("ca_ion", "cur"), b.get_array("ca_ion", "cur"))
