@@ -71,6 +71,7 @@ struct MechConsts {
     double hh_q10;                // pow(3, (celsius - 6.3) / 10)            hh_templated.cu:87
     double hd_qt;                 // pow(q10, (celsius - 33) / 10)           hd_la.cu:94
     double hd_ehd, hd_kl, hd_vhalft, hd_a0t, hd_zetat, hd_gmt, hd_qtl;
+    double hd_inv_kl;             // 1 / hd_kl
     double ktf;                   // 1000 R (celsius + 273.15) / F           eion.cuh:33-36
 };
 

@@ -63,15 +63,13 @@ __device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) {
 }
 
 __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s) {
-    double minf, mtau, hinf, htau, ninf, ntau;
-    hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
-    s.m = hh_cnexp(s.m, minf, mtau, A.dt);
-    s.h = hh_cnexp(s.h, hinf, htau, A.dt);
-    s.n = hh_cnexp(s.n, ninf, ntau, A.dt);
+    hh_gates_r(v, A.c.hh_q10, A.dt, s.m, s.h, s.n);
     sts_(m.col(HH_M) + j, s.m);
     sts_(m.col(HH_H) + j, s.h);
     sts_(m.col(HH_N) + j, s.n);
     if (A.write_assigned) {
+        double minf, mtau, hinf, htau, ninf, ntau;
+        hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
         m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
         m.col(HH_HINF)[j] = hinf; m.col(HH_HTAU)[j] = htau;
         m.col(HH_NINF)[j] = ninf; m.col(HH_NTAU)[j] = ntau;
@@ -81,13 +79,12 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
 
 __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
                                                   CaHVAState s, const double* ca_erev, int ci) {
-    double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
-    cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
-    s.m = s.m + (1.0 - exp(-A.dt / mTau)) * (mInf - s.m);
-    s.h = s.h + (1.0 - exp(-A.dt / hTau)) * (hInf - s.h);
+    cahva_gates_r(v, A.dt, s.m, s.h);
     sts_(m.col(CH_M) + j, s.m);
     sts_(m.col(CH_H) + j, s.h);
     if (A.write_assigned) {
+        double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
+        cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
         m.col(CH_ECA)[j] = ca_erev[ci];
         m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
         m.col(CH_HINF)[j] = hInf; m.col(CH_HTAU)[j] = hTau; m.col(CH_HALPHA)[j] = hAlpha; m.col(CH_HBETA)[j] = hBeta;
@@ -96,18 +93,21 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
 }
 
 __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l) {
-    double linf, taul;
-    hdla_rate(v, lds_(m.col(HD_VHALFL) + j), lds_(m.col(HD_TAU) + j), A.c, linf, taul);
-    l = l + (1.0 - exp(-A.dt / taul)) * (linf - l);
+    const double vhalfl = lds_(m.col(HD_VHALFL) + j), tau = lds_(m.col(HD_TAU) + j);
+    l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
     sts_(m.col(HD_L) + j, l);
-    if (A.write_assigned) { m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul; }
+    if (A.write_assigned) {
+        double linf, taul;
+        hdla_rate(v, vhalfl, tau, A.c, linf, taul);
+        m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul;
+    }
     return l;
 }
 
 // returns the new cai (the caller stores it)
 __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& m, int j, double cai, double ica) {
-    return cadyn_step(cai, ica, lds_(m.col(CD_GAMMA) + j), lds_(m.col(CD_DECAY) + j), lds_(m.col(CD_DEPTH) + j),
-                      lds_(m.col(CD_MINCAI) + j), A.dt);
+    return cadyn_step_r(cai, ica, lds_(m.col(CD_GAMMA) + j), lds_(m.col(CD_DECAY) + j), lds_(m.col(CD_DEPTH) + j),
+                        lds_(m.col(CD_MINCAI) + j), A.dt);
 }
 
 // ---------------------------------------------------------------------------
@@ -120,7 +120,7 @@ __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, i
     double v1 = v + 0.001;
     double i1 = gp * (v1 - ep);
     double i0 = gp * (v - ep);
-    g = (i1 - i0) / 0.001;
+    g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) m.col(PAS_I)[j] = i0;
     return i0;
 }
@@ -133,7 +133,7 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
     double v1 = v + 0.001;
     double i1 = hh_current(v1, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
     double i0 = hh_current(v, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
-    g = (i1 - i0) / 0.001;
+    g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) {
         m.col(HH_ENA)[j] = ena; m.col(HH_EK)[j] = ek; m.col(HH_INA)[j] = ina; m.col(HH_IK)[j] = ik;
         m.col(HH_IL)[j] = il; m.col(HH_GNA)[j] = gna; m.col(HH_GK)[j] = gk;
@@ -148,7 +148,7 @@ __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m,
     double gg = gbar * s.m * s.m * s.h;
     double i1 = gg * (v1 - eca);
     double i0 = gg * (v - eca);
-    g = (i1 - i0) / 0.001;
+    g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) {
         m.col(CH_ECA)[j] = eca; m.col(CH_G)[j] = gg; m.col(CH_ICA)[j] = i0; m.col(CH_IMECH)[j] = i0;
     }
@@ -161,7 +161,7 @@ __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, 
     double v1 = v + 0.001;
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);
-    g = (i1 - i0) / 0.001;
+    g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) { m.col(HD_GHD)[j] = ghd; m.col(HD_I)[j] = i0; }
     return i0;
 }
@@ -368,7 +368,7 @@ __device__ __forceinline__ void point_current(const StepArgs& A, const MechDev& 
         i0 = gg * (v - e);
         if (A.write_assigned) { m.col(E2_G)[j] = gg; m.col(E2_I)[j] = i0; }
     }
-    g = (i1 - i0) / 0.001;
+    g = (i1 - i0) * 1000.0;   // / 0.001
 }
 
 template <int MECH>

@@ -1,8 +1,9 @@
 // Device-side mechanism arithmetic.
 //
-// Every expression keeps the algebraic form of the reference mechanism so that
-// the fp64 results track the reference CPU path to rounding (the reference is
-// compiled with -ffp-contract=off on the host; this library uses the same flag):
+// The reference forms below keep the algebraic form of the reference mechanism
+// (the reference is compiled with -ffp-contract=off on the host; this library
+// uses the same flag); the forward step uses the rearranged forms further down,
+// which differ from them by a few ulps:
 //   hh ............ src/mech/user-mech/hh_templated.cu:76-164
 //   pas ........... src/mech/user-mech/pas_templated.cu:27-31
 //   IClamp ........ src/mech/user-mech/iclamp_templated.cu:29-40
@@ -137,6 +138,70 @@ __device__ __forceinline__ double cadyn_step(double cai, double ica, double gamm
     double drive_ica = -(10000.0) * (ica * gamma) / (2.0 * kFaradayCaDyn * depth);
     double exp_factor = exp(dt * (-1.0 / decay));
     double steady_term = -(drive_ica - (-minCai) / decay) / (-1.0 / decay);
+    return cai + (1.0 - exp_factor) * (steady_term - cai);
+}
+
+// ---------------- rearranged forms for the forward step ----------------
+// The same mathematics as the reference forms above, with the divisions that the
+// reference's expressions spell out but the algebra does not need taken out (an
+// fp64 division costs about ten instructions, a multiplication one; the node
+// kernel is close to its instruction-issue limit).  The cnexp update with
+// tau = 1/(k (a+b)) and inf = a/(a+b),
+//     x + (1 - exp(dt (-1/tau))) ((inf/tau)/(1/tau) - x),
+// is x + (1 - exp(-dt k (a+b))) (a/(a+b) - x); divisions by constants become
+// multiplications by their reciprocals.  Results differ from the reference
+// forms by a few ulps.  The reference forms stay in use where their
+// intermediate values are outputs (assigned variables) and in the adjoint.
+__device__ __forceinline__ double vtrap_r(double x, double y, double inv_y) {
+    const double r = x * inv_y;                      // x / y
+    if (fabs(r) < 1e-6) return y * (1 - r * 0.5);
+    return x / (exp(r) - 1);
+}
+
+__device__ __forceinline__ double gate_step(double x, double a, double b, double k, double dt) {
+    const double sum = a + b;
+    return x + (1.0 - exp(-dt * (k * sum))) * (a / sum - x);
+}
+
+// hh: the three gates of one compartment
+__device__ __forceinline__ void hh_gates_r(double v, double q10, double dt, double& m, double& h, double& n) {
+    const double am = 0.1 * vtrap_r(-(v + 40), 10.0, 0.1);
+    const double bm = 4 * exp(-(v + 65) * (1.0 / 18));
+    const double ah = 0.07 * exp(-(v + 65) * 0.05);
+    const double bh = 1.0 / (exp(-(v + 35) * 0.1) + 1);
+    const double an = 0.01 * vtrap_r(-(v + 55), 10.0, 0.1);
+    const double bn = 0.125 * exp(-(v + 65) * 0.0125);
+    m = gate_step(m, am, bm, q10, dt);
+    h = gate_step(h, ah, bh, q10, dt);
+    n = gate_step(n, an, bn, q10, dt);
+}
+
+// Ca_HVA: m, h
+__device__ __forceinline__ void cahva_gates_r(double v, double dt, double& m, double& h) {
+    const double ma = 0.055 * vtrap_r(-27.0 - v, 3.8, 1.0 / 3.8);
+    const double mb = 0.94 * exp((-75.0 - v) * (1.0 / 17.0));
+    const double ha = 0.000457 * exp((-13.0 - v) * 0.02);
+    const double hb = 0.0065 / (exp((-v - 15.0) * (1.0 / 28.0)) + 1.0);
+    m = gate_step(m, ma, mb, 1.0, dt);
+    h = gate_step(h, ha, hb, 1.0, dt);
+}
+
+// hd_la: l + (1 - exp(-dt / taul)) (linf - l) with -dt / taul folded into one division
+__device__ __forceinline__ double hdla_gate_r(double v, double l, double vhalfl, double tau, const MechConsts& c,
+                                              double dt) {
+    const double a = exp(0.0378 * c.hd_zetat * (v - c.hd_vhalft));
+    const double linf = 1.0 / (1.0 + exp(-(v - vhalfl) * c.hd_inv_kl));
+    const double bett = exp(0.0378 * c.hd_zetat * c.hd_gmt * (v - c.hd_vhalft));
+    const double rate = (c.hd_qtl * c.hd_qt * c.hd_a0t * (1.0 + a)) / (tau * bett);   // 1 / taul
+    return l + (1.0 - exp(-dt * rate)) * (linf - l);
+}
+
+// CaDynamics_E2: steady_term = -(drive - (-minCai)/decay) / (-1/decay) = drive decay + minCai
+__device__ __forceinline__ double cadyn_step_r(double cai, double ica, double gamma, double decay, double depth,
+                                               double minCai, double dt) {
+    const double drive_ica = -(10000.0) * (ica * gamma) / (2.0 * kFaradayCaDyn * depth);
+    const double exp_factor = exp(-dt / decay);
+    const double steady_term = drive_ica * decay + minCai;
     return cai + (1.0 - exp_factor) * (steady_term - cai);
 }
 

@@ -1368,6 +1368,7 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.c.hd_qt = std::pow(G(M_HDLA, "q10", 4.5), ((hd_cel - 33.0) / 10.0));
     A.c.hd_ehd = G(M_HDLA, "ehd", -30.0);
     A.c.hd_kl = G(M_HDLA, "kl", -8.0);
+    A.c.hd_inv_kl = 1.0 / A.c.hd_kl;
     A.c.hd_vhalft = G(M_HDLA, "vhalft", -75.0);
     A.c.hd_a0t = G(M_HDLA, "a0t", 0.011);
     A.c.hd_zetat = G(M_HDLA, "zetat", 2.2);
