@@ -164,13 +164,29 @@ __device__ __forceinline__ double gate_step(double x, double a, double b, double
 }
 
 // hh: the three gates of one compartment
+// The rates hold six exponentials of v; three of them are the others times
+// constants: with E = exp(-(v + 40) / 10) and F = exp(-(v + 65) / 80),
+//     exp(-(v + 35) / 10) = E e^(1/2),  exp(-(v + 55) / 10) = E e^(-3/2),
+//     exp(-(v + 65) / 20) = F^4,
+// which leaves three exp calls (a few ulps from the six-call form).
+__device__ __forceinline__ double vtrap_e(double x, double y, double inv_y, double ex) {   // ex = exp(x / y)
+    const double r = x * inv_y;
+    if (fabs(r) < 1e-6) return y * (1 - r * 0.5);
+    return x / (ex - 1);
+}
+
 __device__ __forceinline__ void hh_gates_r(double v, double q10, double dt, double& m, double& h, double& n) {
-    const double am = 0.1 * vtrap_r(-(v + 40), 10.0, 0.1);
+    constexpr double kExpHalf = 1.6487212707001282;        // e^(1/2)
+    constexpr double kExpMinus3Half = 0.22313016014842982; // e^(-3/2)
+    const double E = exp(-(v + 40) * 0.1);
+    const double F = exp(-(v + 65) * 0.0125);
+    const double F2 = F * F;
+    const double am = 0.1 * vtrap_e(-(v + 40), 10.0, 0.1, E);
     const double bm = 4 * exp(-(v + 65) * (1.0 / 18));
-    const double ah = 0.07 * exp(-(v + 65) * 0.05);
-    const double bh = 1.0 / (exp(-(v + 35) * 0.1) + 1);
-    const double an = 0.01 * vtrap_r(-(v + 55), 10.0, 0.1);
-    const double bn = 0.125 * exp(-(v + 65) * 0.0125);
+    const double ah = 0.07 * (F2 * F2);
+    const double bh = 1.0 / (E * kExpHalf + 1);
+    const double an = 0.01 * vtrap_e(-(v + 55), 10.0, 0.1, E * kExpMinus3Half);
+    const double bn = 0.125 * F;
     m = gate_step(m, am, bm, q10, dt);
     h = gate_step(h, ah, bh, q10, dt);
     n = gate_step(n, an, bn, q10, dt);
