@@ -17,7 +17,8 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libheliox_amd.so")
 ARCH = os.environ.get("HELIOX_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["kernels.hip", "adjoint.hip", "learn.hip", "learn_runtime.cpp", "runtime.cpp", "schedule.cpp"]
+SOURCES = ["kernels.hip", "adjoint.hip", "learn.hip", "learn_runtime.cpp", "runtime.cpp", "schedule.cpp",
+           "coredat.cpp"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 DEVICE = [f"--offload-arch={ARCH}", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

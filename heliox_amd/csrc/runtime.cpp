@@ -193,7 +193,10 @@ enum TimerId { T_MECH = 0, T_SPARSE, T_POINT, T_SOLVE, T_SPIKE, T_EVENTS, T_OTHE
 struct hx_sim {
     std::string err;
     double dt = 0.025;
+    bool dt_set = false;                 // set by the caller (else a CoreNEURON export's dt is taken)
     double celsius = 6.3;
+    std::string data_path;               // CoreNEURON export read by hx_load_model
+    int user_mod_num = 1000;             // artificial presyns are -(type + index * user_mod_num)
     // nodes (user order)
     int ncell = 0, nnode = 0;
     std::vector<int> parent;
@@ -419,6 +422,21 @@ struct hx_sim {
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
         if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    // drops what the model builder holds (a failed read of an export)
+    void reset_model(size_t keep_vecplay) {
+        ncell = nnode = 0;
+        parent.clear(); a.clear(); b.clear(); area.clear(); cm.clear();
+        for (int k = 0; k < M_COUNT; ++k) {
+            mech[k] = HostMech();
+            globals[k].clear();
+        }
+        pre_gid.clear(); pre_node.clear(); pre_thr.clear();
+        vecstim.clear();
+        netcons.clear();
+        gaps.clear();
+        if (vecplay.size() > keep_vecplay) vecplay.resize(keep_vecplay);
     }
 
     int fail(const char* fmt, ...) {
@@ -668,13 +686,16 @@ void hx_sim::build_layout() {
     }
     unit_cells = U;
 
-    // mechanism instance order: by solver-order node (stable)
+    // mechanism instance order: by solver-order node (stable); artificial cells
+    // sit on no node and keep their own order
     for (int id = 0; id < M_COUNT; ++id) {
         HostMech& m = mech[id];
         if (!m.present) continue;
         std::vector<int> idx(m.n);
         std::iota(idx.begin(), idx.end(), 0);
-        std::stable_sort(idx.begin(), idx.end(), [&](int x, int y) { return node_perm[m.node[x]] < node_perm[m.node[y]]; });
+        if (!R[id].artificial)
+            std::stable_sort(idx.begin(), idx.end(),
+                             [&](int x, int y) { return node_perm[m.node[x]] < node_perm[m.node[y]]; });
         m.iperm = idx;
         m.perm.assign(m.n, 0);
         for (int j = 0; j < m.n; ++j) m.perm[idx[j]] = j;
@@ -1924,6 +1945,20 @@ void hx_sim::finitialize(double v_init) {
         return sim->fail("%s", e.what());               \
     }
 
+namespace hx {
+int read_coredat(hx_sim* sim, const std::string& dir, int user_mod_num, bool take_dt, std::string& err);
+}
+
+namespace {
+uint64_t fnv1a(const void* p, size_t n, uint64_t h = 1469598103934665603ull) {
+    const unsigned char* c = static_cast<const unsigned char*>(p);
+    for (size_t i = 0; i < n; ++i) h = (h ^ c[i]) * 1099511628211ull;
+    return h;
+}
+template <class T>
+uint64_t fnv_vec(const std::vector<T>& v) { return fnv1a(v.data(), v.size() * sizeof(T)); }
+}  // namespace
+
 static bool check_loaded(hx_sim* sim) {
     if (!sim->loaded) { sim->fail("model not loaded (call hx_load_model)"); return false; }
     return true;
@@ -1955,6 +1990,7 @@ int hx_set_device(hx_sim* sim, const char* dev) {
 
 int hx_set_dt(hx_sim* sim, double dt) {
     if (!(dt > 0)) return sim->fail("dt must be positive");
+    sim->dt_set = true;
     if (sim->loaded && dt != sim->dt) {
         sim->dt = dt;
         sim->ttab.clear();
@@ -1969,6 +2005,19 @@ double hx_get_dt(hx_sim* sim) { return sim->dt; }
 
 int hx_set_celsius(hx_sim* sim, double c) {
     sim->celsius = c;
+    return 0;
+}
+
+int hx_set_data_path(hx_sim* sim, const char* path) {
+    if (sim->loaded) return sim->fail("cannot set the data path after the model is loaded");
+    if (!path || !*path) return sim->fail("empty data path");
+    sim->data_path = path;
+    return 0;
+}
+
+int hx_set_user_mod_num(hx_sim* sim, int num) {
+    if (num <= 0) return sim->fail("user_mod_num must be positive");
+    sim->user_mod_num = num;
     return 0;
 }
 
@@ -2101,8 +2150,95 @@ int hx_model_add_gap(hx_sim* sim, int src_node, int hg) {
     return 0;
 }
 
+int hx_model_digest(hx_sim* sim, char* out, int cap) {
+    std::string d;
+    char buf[512];
+    auto add = [&](const char* fmt, auto... args) {
+        snprintf(buf, sizeof(buf), fmt, args...);
+        d += buf;
+    };
+    add("ncell %d nnode %d dt %.17g celsius %.17g\n", sim->ncell, sim->nnode, sim->dt, sim->celsius);
+    add("nodes parent %016llx a %016llx b %016llx area %016llx cm %016llx\n",
+        (unsigned long long)fnv_vec(sim->parent), (unsigned long long)fnv_vec(sim->a),
+        (unsigned long long)fnv_vec(sim->b), (unsigned long long)fnv_vec(sim->area),
+        (unsigned long long)fnv_vec(sim->cm));
+    const auto& R = registry();
+    for (int id = 0; id < M_COUNT; ++id) {
+        const HostMech& m = sim->mech[id];
+        if (!m.present) continue;
+        // artificial cells sit on no node: their node list is not part of the model
+        add("mech %s n %d node %016llx", R[id].name, m.n,
+            (unsigned long long)(R[id].artificial ? 0 : fnv_vec(m.node)));
+        for (size_t c = 0; c < m.col.size(); ++c) add(" c%zu %016llx", c, (unsigned long long)fnv_vec(m.col[c]));
+        if (!m.iontype.empty()) add(" style %016llx", (unsigned long long)fnv_vec(m.iontype));
+        for (const auto& g : sim->globals[id]) add(" %s=%.17g", g.first.c_str(), g.second);
+        d += "\n";
+    }
+    add("presyn %zu gid %016llx node %016llx thr %016llx\n", sim->pre_node.size(),
+        (unsigned long long)fnv_vec(sim->pre_gid), (unsigned long long)fnv_vec(sim->pre_node),
+        (unsigned long long)fnv_vec(sim->pre_thr));
+    uint64_t h = 1469598103934665603ull;
+    size_t nt = 0;
+    for (const auto& v : sim->vecstim) {
+        const size_t n = v.size();
+        h = fnv1a(&n, sizeof(n), h);
+        h = fnv1a(v.data(), n * sizeof(double), h);
+        nt += n;
+    }
+    add("vecstim %zu times %zu %016llx\n", sim->vecstim.size(), nt, (unsigned long long)h);
+    // netcons in (target, instance) order: only the last one per instance acts
+    std::map<std::pair<int, int>, NetCon> last;
+    for (const auto& nc : sim->netcons) last[{nc.mech, nc.inst}] = nc;
+    h = 1469598103934665603ull;
+    for (const auto& e : last) {
+        const NetCon& nc = e.second;
+        const int iv[4] = {nc.src_kind, nc.src, nc.mech, nc.inst};
+        const double dv[2] = {nc.weight, nc.delay};
+        h = fnv1a(iv, sizeof(iv), h);
+        h = fnv1a(dv, sizeof(dv), h);
+    }
+    add("netcon %zu %016llx\n", last.size(), (unsigned long long)h);
+    // one transfer per HalfGap instance: their order does not matter
+    auto gaps = sim->gaps;
+    std::sort(gaps.begin(), gaps.end(), [](const auto& x, const auto& y) {
+        return x.second != y.second ? x.second < y.second : x.first < y.first;
+    });
+    h = fnv1a(gaps.data(), gaps.size() * sizeof(gaps[0]));
+    add("gap %zu %016llx\n", sim->gaps.size(), (unsigned long long)h);
+    for (const auto& vp : sim->vecplay)
+        add("vecplay %s.%s[%d] %zu t %016llx y %016llx\n", vp.mech.c_str(), vp.var.c_str(), vp.idx, vp.tvec.size(),
+            (unsigned long long)fnv_vec(vp.tvec), (unsigned long long)fnv_vec(vp.yvec));
+    if (out && cap > 0) {
+        const size_t n = std::min(d.size(), static_cast<size_t>(cap - 1));
+        memcpy(out, d.data(), n);
+        out[n] = 0;
+    }
+    return static_cast<int>(d.size()) + 1;
+}
+
+int hx_model_read_export(hx_sim* sim) {
+    if (sim->loaded) return sim->fail("model already loaded");
+    if (sim->data_path.empty()) return sim->fail("no data path set");
+    if (sim->nnode != 0) return sim->fail("the model already has nodes");
+    std::string err;
+    const bool dt_set = sim->dt_set;
+    const double dt = sim->dt, celsius = sim->celsius;
+    const size_t nvp = sim->vecplay.size();
+    if (hx::read_coredat(sim, sim->data_path, sim->user_mod_num, !dt_set, err) != 0) {
+        const std::string msg = sim->data_path + ": " + err;
+        sim->reset_model(nvp);
+        sim->dt_set = dt_set;
+        sim->dt = dt;
+        sim->celsius = celsius;
+        return sim->fail("%s", msg.c_str());
+    }
+    sim->data_path.clear();     // read: hx_load_model builds from what is now in the builder
+    return 0;
+}
+
 int hx_load_model(hx_sim* sim) {
     if (sim->loaded) return sim->fail("model already loaded");
+    if (!sim->data_path.empty() && hx_model_read_export(sim) != 0) return -1;
     if (sim->nnode == 0) return sim->fail("no nodes");
     API_BEGIN
     sim->build_layout();

@@ -55,6 +55,10 @@ SIGNATURES = {
     "hx_model_add_netcon": (C.c_int, [_P, C.c_int, C.c_int, _S, C.c_int, C.c_double, C.c_double]),
     "hx_model_add_gap": (C.c_int, [_P, C.c_int, C.c_int]),
     "hx_load_model": (C.c_int, [_P]),
+    "hx_set_data_path": (C.c_int, [_P, _S]),
+    "hx_set_user_mod_num": (C.c_int, [_P, C.c_int]),
+    "hx_model_read_export": (C.c_int, [_P]),
+    "hx_model_digest": (C.c_int, [_P, C.c_char_p, C.c_int]),
     "hx_finitialize": (C.c_int, [_P, C.c_double]),
     "hx_run": (C.c_int, [_P, C.c_double]),
     "hx_continue_run": (C.c_int, [_P, C.c_double]),
@@ -279,7 +283,15 @@ class Sim:
 
     # --------------------------------------------------------------- model
     def load_model_from_spec(self, spec: ModelSpec, add_monitors: bool = True) -> int:
-        """Build the model of ``spec`` and upload it (replaces set_data_path + load_model)."""
+        """Build the model of ``spec`` and upload it (set_data_path + load_model with
+        in-memory arrays instead of an export)."""
+        self.build_model_from_spec(spec, add_monitors)
+        self._chk(lib().hx_load_model(self._h), "load_model")
+        self.spec = spec
+        return 0
+
+    def build_model_from_spec(self, spec: ModelSpec, add_monitors: bool = True) -> int:
+        """The model builder's calls for ``spec`` (no GPU); load_model uploads it."""
         spec.validate()
         L = lib()
         h = self._h
@@ -327,8 +339,6 @@ class Sim:
             for mech, var, idx in spec.monitors:
                 self.monitor_handles.append(self._chk(L.hx_add_monitor(h, _b(mech), _b(var), int(idx)),
                                                       f"monitor {mech}.{var}[{idx}]"))
-        self._chk(L.hx_load_model(h), "load_model")
-        self.spec = spec
         return 0
 
     def info(self, key: str) -> int:
@@ -739,14 +749,29 @@ class Sim:
                 return -1
         return 0
 
-    # --------------------------------------------------------------- not provided
+    # --------------------------------------------------------------- CoreNEURON exports
     def set_data_path(self, path: str) -> int:
-        """CoreNEURON export directories are not read here: build the model with
-        load_model_from_spec (node arrays, mechanism columns, netcons)."""
-        return self._pyfail("set_data_path: CoreNEURON exports are not read; use load_model_from_spec")
+        """Directory of a CoreNEURON export read by the next load_model (SimWrapper.cpp:18)."""
+        return self._rc(lib().hx_set_data_path(self._h, _b(str(path))))
 
-    def load_model(self, *args, **kwargs) -> int:
-        return self._pyfail("load_model: CoreNEURON exports are not read; use load_model_from_spec")
+    def load_model(self) -> int:
+        """Read the export at the data path and upload the model (SimWrapper.cpp:26-31).
+        Monitors added before the call are resolved against the loaded model."""
+        rc = lib().hx_load_model(self._h)
+        if rc >= 0:
+            self.spec = None
+        return self._rc(rc)
+
+    def read_export(self) -> int:
+        """Only the read half of load_model: the export into the model builder (no GPU)."""
+        return self._rc(lib().hx_model_read_export(self._h))
+
+    def model_digest(self) -> str:
+        """Counts and hashes of what the model builder holds (no reference counterpart)."""
+        n = lib().hx_model_digest(self._h, None, 0)
+        buf = C.create_string_buffer(n)
+        lib().hx_model_digest(self._h, buf, n)
+        return buf.value.decode()
 
     def set_permute_type(self, permute_type: int) -> int:
         """Accepted for compatibility: the solver uses its own node order (solve units)."""
@@ -756,8 +781,10 @@ class Sim:
         return 0
 
     def set_user_mod_num(self, num: int) -> None:
-        """Accepted for compatibility (user mechanisms are compiled into the library)."""
+        """Numbering of artificial presyns in an export: -(type + index * num) (SimWrapper.cpp:481)."""
         self._user_mod_num = int(num)
+        if lib().hx_set_user_mod_num(self._h, int(num)) < 0:
+            raise HelioxError(f"set_user_mod_num: {self.last_error()}")
 
     def call_mech_func(self, mech_name: str, func_name: str, *args) -> float:
         """The reference's FunctionRegistry calls belong to mechanism families outside this

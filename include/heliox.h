@@ -80,7 +80,27 @@ int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, 
 /* Gap-junction transfer after each update: HalfGap[halfgap_inst].vgap = v[src_node]
  * (Simulate::add_gap_source/add_gap_target, simulate.cpp:953-966). */
 int hx_model_add_gap(hx_sim* sim, int src_node, int halfgap_inst);
-/* SimWrapper::load_model: builds the solver layout and uploads the model to HBM. */
+/* SimWrapper::set_data_path (SimWrapper.cpp:18, SimRuntime.cpp:28-36): a directory holding
+ * a CoreNEURON export (files.dat, bbcore_mech.dat, <id>_1.dat, <id>_2.dat, optional
+ * <id>_gap.dat, globals.dat), read by the next hx_load_model.  Formats 1.8 and older,
+ * one group, as read_coredat.cpp:36-1141 reads them. */
+int hx_set_data_path(hx_sim* sim, const char* path);
+/* SimWrapper::set_user_mod_num (SimWrapper.cpp:481): artificial presyns of the export are
+ * numbered -(type + index * num); 1000 by default (100 for older HelioX test models). */
+int hx_set_user_mod_num(hx_sim* sim, int num);
+/* The read half of load_model (read_coredat + data_format_trans,
+ * SimRuntimeCore.cpp:109-147): reads the export at the data path into the model builder,
+ * as the hx_model_* calls would build it, without building the layout or touching the
+ * GPU.  hx_load_model calls it when a data path is set.  On an error the builder is left
+ * empty and the message names the file and the record. */
+int hx_model_read_export(hx_sim* sim);
+/* No reference counterpart: a text summary of the model builder (counts and FNV-1a
+ * hashes of every array; netcons reduced to the last one per synapse instance), for
+ * comparing two ways of building one model.  Writes up to cap bytes (NUL-terminated)
+ * and returns the length needed including the NUL. */
+int hx_model_digest(hx_sim* sim, char* out, int cap);
+/* SimWrapper::load_model: reads the export at the data path when one is set, then builds
+ * the solver layout and uploads the model to HBM. */
 int hx_load_model(hx_sim* sim);
 
 /* ---- step API (Simulate::finitialize/run/continue_run/fadvance, simulate.h:17-76) ---- */

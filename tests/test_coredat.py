@@ -1,0 +1,242 @@
+"""CoreNEURON export reader (read_coredat.cpp:36-1141, coredat_to_innerdat.cpp:42-603):
+an export written from a model gives the model builder the same arrays as the model's
+in-memory build (compared through the builder digest), across format versions,
+user_mod_num numberings, optional arrays and netcon orders; the reader's errors name
+the file and the record and leave the builder empty.  No GPU is used.
+
+No CoreNEURON export ships with the reference and NEURON is absent from the image, so
+the files are written by tests/coredat_writer.py, which lays them out in the order the
+reference's reader takes them apart; real NEURON exports are not read here."""
+import os
+
+import numpy as np
+import pytest
+
+from coredat_writer import HD_LA_GLOBALS, write_export
+from heliox_amd import Sim, build_config
+from heliox_amd.sim import HelioxError
+from heliox_amd.spec import MechSpec, NetConSpec
+
+HD_DEFAULTS = dict(zip(HD_LA_GLOBALS, (-30.0, -8.0, -75.0, 0.011, 2.2, 0.4, 4.5, 1.0)))
+FILL = {
+    "pas": {"g_pas": 1e-4, "e_pas": -65.0},
+    "hh": {"gnabar": 0.12, "gkbar": 0.036, "gl": 3e-4, "el": -54.3},
+    "IClamp": {"delay": 1.0, "dur": 5.0, "amp": 0.1},
+    "ExpSyn": {"tau": 2.0, "e": 0.0},
+    "Exp2Syn": {"tau1": 0.5, "tau2": 2.0, "e": 0.0},
+    "NetStim": {"interval": 10.0, "number": 10.0, "start": 50.0, "noise": 0.0},
+    "Ca_HVA": {"gbar": 5e-5},
+    "CaDynamics_E2": {"gamma": 0.05, "decay": 80.0, "depth": 0.1, "minCai": 1e-4},
+    "hd_la": {"ghdbar": 1e-4, "vhalfl": -81.0, "tau": 1.0},
+    "HalfGap": {"g": 1e-3},
+    "na_ion": {"erev": 50.0, "conci": 10.0, "conco": 140.0},
+    "k_ion": {"erev": -77.0, "conci": 140.0, "conco": 4.0},
+    "ca_ion": {"erev": 132.0, "conci": 5e-5, "conco": 2.0},
+}
+
+
+def complete(spec):
+    """Every variable the export carries set explicitly (the export has no 'unset')."""
+    for name, m in spec.mechs.items():
+        for k, v in FILL.get(name, {}).items():
+            if k not in m.params:
+                m.params[k] = np.full(m.n, v)
+        if name == "hd_la":
+            for k, v in HD_DEFAULTS.items():
+                m.globals.setdefault(k, v)
+    return spec
+
+
+def spec_digest(spec, dt=None):
+    s = Sim()
+    if dt is not None:
+        s.set_dt(dt)
+    s.build_model_from_spec(spec, add_monitors=False)
+    return s.model_digest()
+
+
+def export_digest(path, mod_num=None, dt=None):
+    s = Sim()
+    if mod_num is not None:
+        s.set_user_mod_num(mod_num)
+    if dt is not None:
+        s.set_dt(dt)
+    assert s.set_data_path(str(path)) == 0
+    rc = s.read_export()
+    return rc, s.model_digest(), s.last_error()
+
+
+def netstim_spec(ncell=4, tstop=20.0):
+    spec = build_config(2, ncell, tstop)
+    n = spec.n_vecstim
+    rng = np.random.default_rng(5)
+    spec.mechs.pop("VecStim")
+    spec.mechs["NetStim"] = MechSpec(np.zeros(n, np.int32), {
+        "interval": np.full(n, 25.0), "number": np.full(n, 1e9), "start": rng.uniform(0, 10, n),
+        "noise": np.where(np.arange(n) % 2 == 0, 1.0, 0.0)})
+    spec.vecstim_offsets = np.zeros(1, np.int64)
+    spec.vecstim_times = np.zeros(0)
+    nc = spec.netcons["ExpSyn"]
+    kind = nc.src_kind.copy()
+    kind[kind == 1] = 2
+    spec.netcons["ExpSyn"] = NetConSpec(nc.inst, kind, nc.src, nc.weight * 20, nc.delay)
+    return spec
+
+
+CASES = {
+    "config1": lambda: build_config(1, 3, 20.0),
+    "config2": lambda: build_config(2, 3, 20.0),
+    "config3": lambda: build_config(3, 2, 5.0),
+    "config4": lambda: build_config(4, 8, 20.0),
+    "config5": lambda: build_config(5, 2, 20.0),
+    "netstim": lambda: netstim_spec(),
+}
+
+
+@pytest.mark.parametrize("case", sorted(CASES))
+def test_export_builds_the_same_model(case, tmp_path):
+    spec = complete(CASES[case]())
+    write_export(spec, tmp_path, seed=len(case))
+    rc, got, err = export_digest(tmp_path)
+    assert rc == 0, err
+    assert got == spec_digest(spec)
+    # the digest sees what it should: a changed value or a dropped netcon changes it
+    assert "mech " in got and "netcon " in got and "presyn " in got
+
+
+def test_config4_has_gaps_vecplay_and_iclamp(tmp_path):
+    spec = complete(build_config(4, 8, 20.0))
+    assert len(spec.gap_src_node) > 0 and spec.vecplay and "IClamp" in spec.mechs
+    write_export(spec, tmp_path)
+    rc, got, err = export_digest(tmp_path)
+    assert rc == 0, err
+    assert f"gap {len(spec.gap_src_node)} " in got
+    assert got.count("vecplay IClamp.amp") == len(spec.vecplay)
+
+
+def test_older_format_and_user_mod_num(tmp_path):
+    spec = complete(build_config(2, 3, 20.0))
+    want = spec_digest(spec)
+    write_export(spec, tmp_path / "v17", version="1.7", mod_num=100)
+    rc, got, err = export_digest(tmp_path / "v17", mod_num=100)
+    assert rc == 0, err
+    assert got == want
+    # the same files read with the default numbering: artificial presyns decode to other types
+    rc, got, err = export_digest(tmp_path / "v17")
+    assert rc == -1 and "user_mod_num 1000" in err
+    assert got.startswith("ncell 0 nnode 0")
+
+
+def test_pointer2type_arrays_and_unshuffled_netcons(tmp_path):
+    spec = complete(build_config(4, 6, 20.0))
+    write_export(spec, tmp_path, pointer2type=True, shuffle_netcons=False)
+    rc, got, err = export_digest(tmp_path)
+    assert rc == 0, err
+    assert got == spec_digest(spec)
+
+
+def test_netcons_apply_in_presyn_order(tmp_path):
+    """Netcons apply presyn by presyn, so into a synapse instance the netcon from the
+    latest presyn wins, whatever the file order.  A real-cell presyn without a detector
+    (output_vindex -1) sits after the other real cells and before the artificial ones:
+    its netcon overrides a netcon from a cell (config 4: the instance then receives no
+    events) but not one from a VecStim (config 2)."""
+    spec = complete(build_config(4, 6, 20.0))
+    write_export(spec, tmp_path / "c4", dead_netcons=[("ExpSyn", 0), ("ExpSyn", 5)])
+    rc, got, err = export_digest(tmp_path / "c4")
+    assert rc == 0, err
+    nc = spec.netcons["ExpSyn"]
+    keep = ~np.isin(nc.inst, [0, 5])
+    assert keep.sum() == nc.inst.size - 2
+    spec.netcons["ExpSyn"] = NetConSpec(nc.inst[keep], nc.src_kind[keep], nc.src[keep], nc.weight[keep],
+                                        nc.delay[keep])
+    assert got == spec_digest(spec)
+    spec = complete(build_config(2, 3, 20.0))
+    write_export(spec, tmp_path / "c2", dead_netcons=[("ExpSyn", 0), ("ExpSyn", 4)])
+    rc, got, err = export_digest(tmp_path / "c2")
+    assert rc == 0, err
+    assert got == spec_digest(spec)
+
+
+def test_dt_from_globals_unless_set(tmp_path):
+    spec = complete(build_config(1, 2, 20.0))
+    write_export(spec, tmp_path, dt=0.0125, extra_globals={"celsius_unused_copy": 1.0})
+    rc, got, _ = export_digest(tmp_path)
+    assert rc == 0 and float(got.split()[5]) == 0.0125
+    rc, got, _ = export_digest(tmp_path, dt=0.025)
+    assert rc == 0 and float(got.split()[5]) == 0.025
+    assert got == spec_digest(spec, dt=0.025)
+
+
+def _rewrite(path, old: bytes, new: bytes):
+    b = open(path, "rb").read()
+    assert old in b
+    open(path, "wb").write(b.replace(old, new, 1))
+
+
+def test_errors_name_the_file_and_leave_the_builder_empty(tmp_path):
+    spec = complete(build_config(2, 2, 20.0))
+
+    def fresh(name, **kw):
+        d = tmp_path / name
+        write_export(spec, d, **kw)
+        return d
+
+    rc, dig, err = export_digest(tmp_path / "nothing_here")
+    assert rc == -1 and "files.dat" in err and dig.startswith("ncell 0 nnode 0")
+    d = fresh("chk")
+    _rewrite(d / "7_2.dat", b"chkpnt 5\n", b"chkpnt 9\n")
+    rc, dig, err = export_digest(d)
+    assert rc == -1 and "7_2.dat" in err and "chkpnt 9 where 5" in err and dig.startswith("ncell 0 nnode 0")
+    d = fresh("groups")
+    open(d / "files.dat", "w").write("1.8\n2\n7\n8\n")
+    rc, _, err = export_digest(d)
+    assert rc == -1 and "one group" in err
+    d = fresh("unknown")
+    _rewrite(d / "bbcore_mech.dat", b"\nhd_la ", b"\nNap_Et2 ")
+    spec3 = complete(build_config(3, 1, 5.0))
+    write_export(spec3, d)
+    _rewrite(d / "bbcore_mech.dat", b"\nhd_la ", b"\nNap_Et2 ")
+    rc, _, err = export_digest(d)
+    assert rc == -1 and "not provided by this library: Nap_Et2" in err
+    d = fresh("cut")
+    b = open(d / "7_2.dat", "rb").read()
+    open(d / "7_2.dat", "wb").write(b[: len(b) // 2])
+    rc, _, err = export_digest(d)
+    assert rc == -1 and "7_2.dat" in err
+    d = fresh("noglobals")
+    os.remove(d / "globals.dat")
+    rc, dig, err = export_digest(d)
+    assert rc == -1 and "globals.dat" in err and dig.startswith("ncell 0 nnode 0")
+
+
+def test_weight_count_follows_receive_sizes(tmp_path):
+    """Netcon weights sit at a running index that grows by the target's receive size
+    (ExpSyn 1, Exp2Syn 1, other point processes 0, no target 1); a file whose weight
+    count disagrees is refused.  Here one netcon is retargeted to NetStim."""
+    from coredat_writer import TYPE
+    spec = complete(netstim_spec())
+    d = tmp_path / "a"
+    write_export(spec, d)
+    b = bytearray(open(d / "7_2.dat", "rb").read())
+    # the pnttype array: every netcon targets ExpSyn
+    nc_types = np.full(spec.netcons["ExpSyn"].inst.size, TYPE["ExpSyn"], np.int32).tobytes()
+    k = bytes(b).find(nc_types)
+    assert k > 0
+    b[k: k + 4] = np.int32(TYPE["NetStim"]).tobytes()
+    open(d / "7_2.dat", "wb").write(bytes(b))
+    rc, _, err = export_digest(d)
+    assert rc == -1 and "netcon weights" in err
+
+
+def test_load_model_without_data_path_or_twice(tmp_path):
+    s = Sim()
+    assert s.load_model() == -1 and "no nodes" in s.last_error()
+    spec = complete(build_config(1, 2, 20.0))
+    write_export(spec, tmp_path)
+    s = Sim()
+    s.build_model_from_spec(spec, add_monitors=False)
+    assert s.set_data_path(str(tmp_path)) == 0
+    assert s.read_export() == -1 and "already has nodes" in s.last_error()
+    with pytest.raises(HelioxError):
+        Sim().set_user_mod_num(0)
