@@ -51,10 +51,11 @@ STEP_BYTES_PER_INSTANCE = {"pas": 16, "hh": 96, "hd_la": 40, "Ca_HVA": 40, "CaDy
 STEP_BYTES_PER_NODE = 84
 
 
-def step_bytes(spec, ms_per_step: float):
+def step_bytes(spec, ms_per_step: float, not_read: int = 0):
     """Algorithmic HBM bytes of one whole step and the rate they imply at the measured
-    step time (against the HBM peak): an end-to-end figure beside the node kernel's."""
-    total = STEP_BYTES_PER_NODE * spec.nnode
+    step time (against the HBM peak): an end-to-end figure beside the node kernel's.
+    not_read: bytes of parameter columns served as one value (not read per instance)."""
+    total = STEP_BYTES_PER_NODE * spec.nnode - not_read
     for name, m in spec.mechs.items():
         total += STEP_BYTES_PER_INSTANCE.get(name, 0) * m.n
     gbs = total / (ms_per_step * 1e-3) / 1e9
@@ -295,6 +296,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--no-streamed-segment", action="store_true",
+                    help="skip the segment timed with every parameter column read per instance")
     ap.add_argument("--all-kernel-timing", action="store_true",
                     help="time every kernel class (adds event records to the timed region)")
     ap.add_argument("--calibrate-copy", action="store_true")
@@ -343,6 +346,9 @@ def main():
     groups = sim.info("cell_groups")
     nnode = spec.nnode
     dt = spec.dt
+    # parameter columns with one value over the model are read as that value
+    uniform_cols = sim.info("uniform_columns")
+    uniform_bytes = sim.info("uniform_bytes")
 
     sim.finitialize(-65.0)
     if args.warmup:
@@ -365,11 +371,11 @@ def main():
         if n:
             kernels[k] = {"ms_total": ms, "launches": n, "us_per_launch": ms * 1e3 / n}
 
-    def node_kernel_roofline(mech, parts):
+    def node_kernel_roofline(mech, parts, not_read=uniform_bytes):
         # a step runs the node kernel once per part (cell group); a launch covers
-        # nnode / parts compartments
+        # nnode / parts compartments and reads no uniform parameter column per instance
         per_launch_s = mech["ms_total"] / mech["launches"] / 1e3
-        alg = MECH_BYTES_PER_COMP * nnode / parts
+        alg = (MECH_BYTES_PER_COMP * nnode - not_read) / parts
         achieved = alg / per_launch_s / 1e9
         traffic = _traffic_from_profiles()
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -395,6 +401,26 @@ def main():
             sim.set_group_streams(True)
             if n:
                 alone = node_kernel_roofline({"ms_total": ms, "launches": n}, 1)
+    # the same model with every parameter column read per instance (as the reference
+    # reads them): a shorter timed segment after the main one
+    streamed = None
+    if uniform_cols and not args.no_streamed_segment:
+        nseg = max(50, args.steps // 4)
+        sim.set_uniform_columns(False)
+        sim.set_profiling(not args.no_kernel_timing, classes=["mech"])
+        sim.continue_run(20.5 * dt)
+        torch.cuda.synchronize()
+        sim.set_profiling(not args.no_kernel_timing, classes=["mech"])
+        t1 = time.perf_counter()
+        sim.continue_run((nseg + 0.5) * dt)
+        torch.cuda.synchronize()
+        w1 = time.perf_counter() - t1
+        sim.set_uniform_columns(True)
+        ms1, n1 = sim.kernel_time("mech")
+        streamed = {"steps": nseg, "ms_per_step": w1 * 1e3 / nseg, "value": nnode * nseg / w1}
+        if n1:
+            streamed["roofline"] = node_kernel_roofline({"ms_total": ms1, "launches": n1},
+                                                        groups if multi else 1, not_read=0)
     print(json.dumps({"kernel_times": kernels, "build_s": round(t_build, 2), "nnode": nnode,
                       "cell_groups": groups, "multi_stream": sim.info("multi_stream"),
                       "spikes": sim.spikes()[0].size, "t_end": sim.get_t()}), file=sys.stderr)
@@ -424,7 +450,9 @@ def main():
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "roofline": roofline,
         "roofline_single_stream": alone,
-        "step_bytes": step_bytes(spec, ms_per_step),
+        "step_bytes": step_bytes(spec, ms_per_step, uniform_bytes),
+        "uniform_columns": {"columns": uniform_cols, "bytes_per_step_not_read": uniform_bytes,
+                            "all_columns_read": streamed},
         "cpu_baseline": cpu,
         "cpu_baseline_all_cores": cpu_all,
     }

@@ -46,6 +46,8 @@ enum HdLaCol { HD_GHDBAR = 0, HD_VHALFL, HD_TAU, HD_L, HD_I, HD_LINF, HD_TAUL, H
 enum NetStimCol { NS_INTERVAL = 0, NS_NUMBER, NS_START, NS_NOISE, NS_ID1, NS_ID2, NS_ID3, NS_NCOL };
 
 // Per-mechanism device view.
+constexpr int kUniformCols = 32;   // parameter columns a mechanism may serve as one value
+
 struct MechDev {
     double* base = nullptr;       // column c at base + c * stride
     long long stride = 0;
@@ -62,6 +64,10 @@ struct MechDev {
     // synapses folded into the node kernel: instances on the nodes of node-kernel
     // block b are [blk_begin[b], blk_begin[b+1])
     const int* blk_begin = nullptr;
+    // parameter columns that hold one value for every instance: bit c set means
+    // column c is uval[c] everywhere (the full column in HBM holds the same values)
+    unsigned umask = 0;
+    const double* uval = nullptr;
     __host__ __device__ double* col(int c) const { return base + c * stride; }
 };
 

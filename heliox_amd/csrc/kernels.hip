@@ -55,6 +55,14 @@ struct CaHVAState { double m, h; };
 __device__ __forceinline__ double lds_(const double* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void sts_(double* p, double v) { __builtin_nontemporal_store(v, p); }
 
+// Parameter column c of instance j.  A column with one value for every instance
+// is read once per wave from uval (a scalar load) instead of once per instance
+// from HBM; the mask is uniform, so the choice is a scalar branch.
+__device__ __forceinline__ double ldp(const MechDev& m, int c, int j) {
+    if ((m.umask >> c) & 1u) return m.uval[c];
+    return lds_(m.col(c) + j);
+}
+
 __device__ __forceinline__ HHState hh_load(const MechDev& m, int j) {
     return {lds_(m.col(HH_M) + j), lds_(m.col(HH_H) + j), lds_(m.col(HH_N) + j)};
 }
@@ -93,7 +101,7 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
 }
 
 __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l) {
-    const double vhalfl = lds_(m.col(HD_VHALFL) + j), tau = lds_(m.col(HD_TAU) + j);
+    const double vhalfl = ldp(m, HD_VHALFL, j), tau = ldp(m, HD_TAU, j);
     l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
     sts_(m.col(HD_L) + j, l);
     if (A.write_assigned) {
@@ -106,8 +114,8 @@ __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m
 
 // returns the new cai (the caller stores it)
 __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& m, int j, double cai, double ica) {
-    return cadyn_step_r(cai, ica, lds_(m.col(CD_GAMMA) + j), lds_(m.col(CD_DECAY) + j), lds_(m.col(CD_DEPTH) + j),
-                        lds_(m.col(CD_MINCAI) + j), A.dt);
+    return cadyn_step_r(cai, ica, ldp(m, CD_GAMMA, j), ldp(m, CD_DECAY, j), ldp(m, CD_DEPTH, j),
+                        ldp(m, CD_MINCAI, j), A.dt);
 }
 
 // ---------------------------------------------------------------------------
@@ -116,7 +124,7 @@ __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& 
 // returned for the caller to accumulate
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
-    double gp = lds_(m.col(PAS_G) + j), ep = lds_(m.col(PAS_E) + j);
+    double gp = ldp(m, PAS_G, j), ep = ldp(m, PAS_E, j);
     double v1 = v + 0.001;
     double i1 = gp * (v1 - ep);
     double i0 = gp * (v - ep);
@@ -127,8 +135,8 @@ __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, i
 
 __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, const HHState& s,
                                          double ena, double ek, double& g, double& ina, double& ik) {
-    double gnabar = lds_(m.col(HH_GNABAR) + j), gkbar = lds_(m.col(HH_GKBAR) + j);
-    double gl = lds_(m.col(HH_GL) + j), el = lds_(m.col(HH_EL) + j);
+    double gnabar = ldp(m, HH_GNABAR, j), gkbar = ldp(m, HH_GKBAR, j);
+    double gl = ldp(m, HH_GL, j), el = ldp(m, HH_EL, j);
     double gna, gk, il;
     double v1 = v + 0.001;
     double i1 = hh_current(v1, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
@@ -143,7 +151,7 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
 
 __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v,
                                             const CaHVAState& s, double eca, double& g) {
-    double gbar = lds_(m.col(CH_GBAR) + j);
+    double gbar = ldp(m, CH_GBAR, j);
     double v1 = v + 0.001;
     double gg = gbar * s.m * s.m * s.h;
     double i1 = gg * (v1 - eca);
@@ -157,7 +165,7 @@ __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m,
 
 __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double l,
                                            double& g) {
-    double ghd = lds_(m.col(HD_GHDBAR) + j) * l;
+    double ghd = ldp(m, HD_GHDBAR, j) * l;
     double v1 = v + 0.001;
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);

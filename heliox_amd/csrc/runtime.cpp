@@ -215,6 +215,7 @@ struct hx_sim {
     std::vector<VecPlayHost> vecplay;
     int event_cap_request = 0;
     int fusion_allowed = 1;
+    bool uniform_on = true;              // parameter columns with one value read as scalars
     bool loaded = false;
 
     // layout
@@ -797,6 +798,7 @@ void hx_sim::upload() {
         if (!im.present) continue;
         for (int j = 0; j < im.n; ++j) ion_at[x][node_perm[im.node[im.iperm[j]]]] = j;
     }
+    std::vector<double> uval_host(static_cast<size_t>(M_COUNT) * kUniformCols, 0.0);
     for (int id = 0; id < M_COUNT; ++id) {
         HostMech& m = mech[id];
         MechDev& d = m.dev;
@@ -812,6 +814,21 @@ void hx_sim::upload() {
                 for (int j = 0; j < m.n; ++j) blk[c * d.stride + j] = m.col[c][m.iperm[j]];
             d.base = dupload(owned, blk);
         }
+        // parameters holding one value, for the mechanisms whose parameters the node
+        // kernels read through ldp (ion columns may be written by kernels; point
+        // processes read theirs elsewhere): compared bit for bit, so a uniform
+        // column is exactly its value
+        const bool scalar_reads = id == M_PAS || id == M_HH || id == M_HDLA || id == M_CAHVA || id == M_CADYN;
+        if (scalar_reads && m.n > 0)
+            for (int c = 0; c < std::min(R[id].nparam, kUniformCols); ++c) {
+                const double x0 = m.col[c][0];
+                bool same = true;
+                for (int j = 1; j < m.n && same; ++j) same = std::memcmp(&m.col[c][j], &x0, sizeof(double)) == 0;
+                if (same) {
+                    d.umask |= 1u << c;
+                    uval_host[static_cast<size_t>(id) * kUniformCols + c] = x0;
+                }
+            }
         std::vector<int> nodes(m.n);
         for (int j = 0; j < m.n; ++j) nodes[j] = node_perm[m.node[m.iperm[j]]];
         d.node = dupload(owned, nodes);
@@ -860,6 +877,10 @@ void hx_sim::upload() {
             }
             if (!ident) d.ion[x] = dupload(owned, map);
         }
+    }
+    {
+        const double* d_uval = dupload(owned, uval_host);
+        for (int id = 0; id < M_COUNT; ++id) mech[id].dev.uval = d_uval + static_cast<size_t>(id) * kUniformCols;
     }
 
     // spike detectors, in solver-node order so a cell group's detectors are a
@@ -1326,6 +1347,8 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     const int c = col_id(id, var);
     if (c < 0 || idx < 0 || idx >= m.n) return r;
     r.dev = m.dev.col(c) + m.perm[idx];
+    // a handle may write the column: from now on the kernels read it per instance
+    if (c < 32) m.dev.umask &= ~(1u << c);
     r.klass = c >= M.nparam + M.nstate ? 1 : 0;
     r.point = M.point;
     if (id == M_NETSTIM) {           // parameters only: nothing changes them during a step
@@ -1350,7 +1373,10 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.area = d_area;
     A.cm = d_cm;
     A.cfac = 0.001 * (1.0 / dt);
-    for (int id = 0; id < M_COUNT; ++id) A.m[id] = mech[id].dev;
+    for (int id = 0; id < M_COUNT; ++id) {
+        A.m[id] = mech[id].dev;
+        if (!uniform_on) A.m[id].umask = 0;
+    }
     A.dense_mask = dense_mask;
     A.do_state = do_state;
     A.cadyn_skip = do_state ? pass_cadyn_skip : 0;
@@ -2698,6 +2724,11 @@ int hx_set_group_streams(hx_sim* sim, int enable) {
     return 0;
 }
 
+int hx_set_uniform_columns(hx_sim* sim, int enable) {
+    sim->uniform_on = enable != 0;
+    return 0;
+}
+
 int hx_set_fusion(hx_sim* sim, int enable) {
     sim->fusion_allowed = enable ? 1 : 0;
     if (sim->loaded) {
@@ -2924,6 +2955,16 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
     if (k == "cell_groups") return static_cast<long long>(sim->groups.size());
     if (k == "multi_stream") return sim->last_multi_stream ? 1 : 0;
+    if (k == "uniform_columns" || k == "uniform_bytes") {
+        long long cols = 0, bytes = 0;
+        for (int id = 0; id < M_COUNT; ++id) {
+            if (!sim->mech[id].present || !sim->uniform_on) continue;
+            const int nb = __builtin_popcount(sim->mech[id].dev.umask);
+            cols += nb;
+            bytes += 8LL * nb * sim->mech[id].n;
+        }
+        return k == "uniform_columns" ? cols : bytes;
+    }
     return -1;
 }
 

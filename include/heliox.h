@@ -208,6 +208,12 @@ int hx_set_event_capacity(hx_sim* sim, int per_step);
 /* enable = 1 (default): fold each step's state update into the next step's current pass when that is
  * exact; 0: always run the reference's separate current and state passes. */
 int hx_set_fusion(hx_sim* sim, int enable);
+/* No reference counterpart.  enable = 1 (default): a mechanism parameter column that holds
+ * one value for every instance at hx_load_model is read by the node kernels as that value
+ * instead of once per instance from HBM (the full column stays in HBM and is what handles,
+ * get_array and the other kernels use; any handle into a column ends its scalar reading).
+ * 0: every column is read per instance.  Takes effect from the next step. */
+int hx_set_uniform_columns(hx_sim* sim, int enable);
 /* Per-kernel timing with HIP events on the library's stream: enable, then read
  * accumulated milliseconds and launch counts for a kernel class
  * ("mech", "sparse", "point", "solve", "spike", "events", "other"). */

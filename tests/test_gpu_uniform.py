@@ -1,0 +1,70 @@
+"""Parameter columns holding one value are read by the node kernels as that value: the
+same bits as reading every instance's copy, and a handle into such a column (a write
+through set_variable_value here) returns the column to per-instance reads before the
+next step, so the written value takes effect (checked against the oracle with the same
+change)."""
+import dataclasses
+
+import numpy as np
+import pytest
+
+import oracle
+from heliox_amd import Sim, build_config
+from parity_util import V_TOL
+
+pytestmark = pytest.mark.gpu
+
+
+def run(spec, tstop, uniform=True, mons=None, edit=None):
+    g = Sim()
+    g.set_cell_groups(1)
+    g.load_model_from_spec(dataclasses.replace(spec, monitors=list(mons or spec.monitors)))
+    g.set_uniform_columns(uniform)
+    if edit:
+        edit(g)
+    g.finitialize(-65.0)
+    g.run(tstop)
+    return g
+
+
+def test_scalar_reads_give_the_same_bits(gpu_lib):
+    spec = build_config(3, 2, 5.0)
+    mons = [("global", "v", 0), ("global", "v", spec.nnode - 1), ("hh", "m", 7), ("CaDynamics_E2", "cai", 9)]
+    print("case uniform columns config3 2 cells", flush=True)
+    a = run(spec, 5.0, True, mons)
+    b = run(spec, 5.0, False, mons)
+    # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2 gamma/decay/depth/minCai
+    assert a.info("uniform_columns") == 11
+    assert b.info("uniform_columns") == 0
+    assert a.info("uniform_bytes") == 11 * 8 * spec.nnode
+    assert np.array_equal(a.traces(), b.traces())
+
+
+def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
+    spec = build_config(2, 3, 40.0)
+    n_pas = spec.mechs["pas"].n
+    mons = [("global", "v", c) for c in range(3)] + [("global", "v", 100)]
+    node = int(spec.mechs["pas"].nodes[100])
+    print("case uniform column written through a handle", flush=True)
+
+    def edit(g):
+        before = g.info("uniform_columns")
+        assert g.set_variable_value(3e-3, "pas", "g_pas", 100) == 0
+        assert g.info("uniform_columns") == before - 1
+
+    g = run(spec, 40.0, True, mons, edit)
+    ref = dataclasses.replace(spec, mechs=dict(spec.mechs))
+    ref.mechs["pas"] = dataclasses.replace(spec.mechs["pas"], params=dict(spec.mechs["pas"].params))
+    gp = ref.mechs["pas"].params["g_pas"].copy()
+    gp[100] = 3e-3
+    ref.mechs["pas"].params["g_pas"] = gp
+    o = oracle.OracleSim(ref, monitors=mons)
+    o.finitialize(-65.0)
+    o.run(40.0)
+    err = float(np.max(np.abs(o.traces() - g.traces())))
+    print(f"  max |dv| vs oracle {err:.3e} (node {node})", flush=True)
+    assert err < V_TOL
+    # and the change is visible: the untouched model differs at that node
+    u = run(spec, 40.0, True, mons)
+    assert np.max(np.abs(u.traces()[3] - g.traces()[3])) > 1e-3
+    assert n_pas > 100
