@@ -190,11 +190,11 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
                                                  bool have_ci, double ci) {
     const int type = A.ion_type[x] >= 0 ? A.ion_type[x] : ion.iontype[i];
     if (type & 0100) {
-        const double e = nernst(have_ci ? ci : lds_(ion.col(ION_CONCI) + i), lds_(ion.col(ION_CONCO) + i), z, A.c.ktf);
+        const double e = nernst(have_ci ? ci : lds_(ion.col(ION_CONCI) + i), ldp(ion, ION_CONCO, i), z, A.c.ktf);
         if (A.ion_store & (2u << (2 * x))) sts_(ion.col(ION_EREV) + i, e);
         return e;
     }
-    return lds_(ion.col(ION_EREV) + i);
+    return ldp(ion, ION_EREV, i);
 }
 
 __device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {

@@ -819,6 +819,26 @@ void hx_sim::upload() {
         // processes read theirs elsewhere): compared bit for bit, so a uniform
         // column is exactly its value
         const bool scalar_reads = id == M_PAS || id == M_HH || id == M_HDLA || id == M_CAHVA || id == M_CADYN;
+        if (R[id].ion && m.n > 0) {
+            // the node kernel reads an ion's erev, or its conco when the style has 0100
+            // (Nernst each step); erev is written by kernels under styles 040 (init) and
+            // 0100, conco under 04 (init); conci is a state of calcium dynamics
+            int any = 0;
+            for (int t : m.iontype) any |= t;
+            const int cols[2] = {ION_EREV, ION_CONCO};
+            const bool ok[2] = {!(any & (040 | 0100)), (any & 0100) && !(any & 04)};
+            for (int k = 0; k < 2; ++k) {
+                if (!ok[k]) continue;
+                const int c = cols[k];
+                const double x0 = m.col[c][0];
+                bool same = true;
+                for (int j = 1; j < m.n && same; ++j) same = std::memcmp(&m.col[c][j], &x0, sizeof(double)) == 0;
+                if (same) {
+                    d.umask |= 1u << c;
+                    uval_host[static_cast<size_t>(id) * kUniformCols + c] = x0;
+                }
+            }
+        }
         if (scalar_reads && m.n > 0)
             for (int c = 0; c < std::min(R[id].nparam, kUniformCols); ++c) {
                 const double x0 = m.col[c][0];
@@ -1318,6 +1338,7 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
         const int c = col_id(id, var);
         if (inst < 0 || c < 0) return r;
         r.dev = m.dev.col(c) + inst;
+        m.dev.umask &= ~(1u << c);       // a handle may write the column
         r.klass = (c == ION_CONCI || c == ION_CONCO) ? 0 : 1;
         return r;
     }

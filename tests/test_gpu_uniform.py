@@ -33,10 +33,12 @@ def test_scalar_reads_give_the_same_bits(gpu_lib):
     print("case uniform columns config3 2 cells", flush=True)
     a = run(spec, 5.0, True, mons)
     b = run(spec, 5.0, False, mons)
-    # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2 gamma/decay/depth/minCai
-    assert a.info("uniform_columns") == 11
+    # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2
+    # gamma/decay/depth/minCai, and the erev of na and k (style 0: no kernel writes it);
+    # ca's conco is rewritten at finitialize (style 04) and stays per instance
+    assert a.info("uniform_columns") == 13
     assert b.info("uniform_columns") == 0
-    assert a.info("uniform_bytes") == 11 * 8 * spec.nnode
+    assert a.info("uniform_bytes") == 13 * 8 * spec.nnode
     assert np.array_equal(a.traces(), b.traces())
 
 
@@ -44,13 +46,20 @@ def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
     spec = build_config(2, 3, 40.0)
     n_pas = spec.mechs["pas"].n
     mons = [("global", "v", c) for c in range(3)] + [("global", "v", 100)]
+    assert int(spec.mechs["na_ion"].iontype.max()) == 0
     node = int(spec.mechs["pas"].nodes[100])
     print("case uniform column written through a handle", flush=True)
+
+    na_nodes = spec.mechs["na_ion"].nodes
+    k_na = 1
+    na_node = int(na_nodes[k_na])
 
     def edit(g):
         before = g.info("uniform_columns")
         assert g.set_variable_value(3e-3, "pas", "g_pas", 100) == 0
         assert g.info("uniform_columns") == before - 1
+        assert g.set_variable_value(65.0, "na_ion", "erev", na_node) == 0     # ions: by node
+        assert g.info("uniform_columns") == before - 2
 
     g = run(spec, 40.0, True, mons, edit)
     ref = dataclasses.replace(spec, mechs=dict(spec.mechs))
@@ -58,6 +67,10 @@ def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
     gp = ref.mechs["pas"].params["g_pas"].copy()
     gp[100] = 3e-3
     ref.mechs["pas"].params["g_pas"] = gp
+    ref.mechs["na_ion"] = dataclasses.replace(spec.mechs["na_ion"], params=dict(spec.mechs["na_ion"].params))
+    ena = ref.mechs["na_ion"].params["erev"].copy()
+    ena[k_na] = 65.0
+    ref.mechs["na_ion"].params["erev"] = ena
     o = oracle.OracleSim(ref, monitors=mons)
     o.finitialize(-65.0)
     o.run(40.0)
