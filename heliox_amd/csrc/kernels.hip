@@ -232,15 +232,26 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     const bool have_cai = A.do_state && HAS(M_CADYN) && !A.cadyn_skip;
     if (live) {
         if (A.do_state) {
-            if (HAS(M_CADYN) && !A.cadyn_skip) {
-                double* conci = ca.col(ION_CONCI);
-                cai = cadyn_state(A, A.m[M_CADYN], i, lds_(conci + i), lds_(ca.col(ION_CUR) + i));
+            // every state load ahead of the first state store: a load written after a
+            // store (which may alias it, as far as the compiler can tell) waits for it
+            double* conci = ca.col(ION_CONCI);
+            double ci0 = 0.0, ica0 = 0.0, l0 = 0.0;
+            HHState h0{};
+            CaHVAState c0{};
+            if (have_cai) {
+                ci0 = lds_(conci + i);
+                ica0 = lds_(ca.col(ION_CUR) + i);
+            }
+            if (HAS(M_HH)) h0 = hh_load(A.m[M_HH], i);
+            if (HAS(M_CAHVA)) c0 = cahva_load(A.m[M_CAHVA], i);
+            if (HAS(M_HDLA)) l0 = lds_(A.m[M_HDLA].col(HD_L) + i);
+            if (have_cai) {
+                cai = cadyn_state(A, A.m[M_CADYN], i, ci0, ica0);
                 sts_(conci + i, cai);
             }
-            if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, hh_load(A.m[M_HH], i));
-            if (HAS(M_CAHVA))
-                cs = cahva_state(A, A.m[M_CAHVA], i, v, cahva_load(A.m[M_CAHVA], i), ca.col(ION_EREV), i);
-            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, lds_(A.m[M_HDLA].col(HD_L) + i));
+            if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, h0);
+            if (HAS(M_CAHVA)) cs = cahva_state(A, A.m[M_CAHVA], i, v, c0, ca.col(ION_EREV), i);
+            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, l0);
         } else if (A.do_current) {
             if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
             if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
