@@ -378,6 +378,8 @@ def main():
         alg = (MECH_BYTES_PER_COMP * nnode - not_read) / parts
         achieved = alg / per_launch_s / 1e9
         traffic = _traffic_from_profiles()
+        if not_read != uniform_bytes:
+            traffic = None      # the committed counter summary is of the default (uniform-column) reads
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else traffic / parts,
