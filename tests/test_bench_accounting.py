@@ -15,6 +15,16 @@ def test_step_bytes_config3_per_compartment():
     assert abs(out["achieved"] - 3363200 / 1e-3 / 1e9) < 0.1
 
 
+def test_step_bytes_less_uniform_columns():
+    """Columns served as one value are taken out of the step's algorithmic bytes: config 3's
+    13 uniform columns (pas 2, hh gl/el, hd_la 2, Ca_HVA 1, CaDynamics_E2 4, na/k erev) are
+    104 B per compartment, which leaves 232.32."""
+    spec = build_config(3, 2, 1.0)
+    out = bench.step_bytes(spec, 1.0, not_read=13 * 8 * spec.nnode)
+    assert out["alg_bytes_per_compartment"] == 232.32
+    assert out["alg_bytes_per_step"] == 3363200 - 1040000
+
+
 def test_first_cell_selects_disjoint_cells():
     whole = build_config(3, 3, 1.0)
     tail = build_config(3, 1, 1.0, first_cell=2)
