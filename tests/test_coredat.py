@@ -127,6 +127,17 @@ def test_older_format_and_user_mod_num(tmp_path):
     assert got.startswith("ncell 0 nnode 0")
 
 
+@pytest.mark.parametrize("version", ["1.7", "1.8", "1.9"])
+def test_versions_with_gaps_vecplay_and_cells(version, tmp_path):
+    """Before 1.8 there are no array_dims, n_real_cell line or pointer2type/nmodlrandom
+    counts; 1.8 and later have them (compared part by part, utils.cpp:18-33)."""
+    spec = complete(build_config(4, 6, 20.0))
+    write_export(spec, tmp_path, version=version, pointer2type=version != "1.7")
+    rc, got, err = export_digest(tmp_path)
+    assert rc == 0, err
+    assert got == spec_digest(spec)
+
+
 def test_pointer2type_arrays_and_unshuffled_netcons(tmp_path):
     spec = complete(build_config(4, 6, 20.0))
     write_export(spec, tmp_path, pointer2type=True, shuffle_netcons=False)
