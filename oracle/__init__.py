@@ -4,22 +4,37 @@ Python binding over ``liboracle.so`` (built from ``oracle.cpp`` by the Makefile
 in this directory), the C++ restatement of the reference's CPU step loop.
 Only tests, the smoke check and the CPU-baseline leg of the benchmark use it.
 
-Parity status of each oracle function (see ``tests/test_oracle_*.py``):
-  solve_serial ......... pinned: dense-solve equality, single-node closed form
+Parity status of each oracle function (``tests/test_oracle_pinning.py`` unless named):
+  solve_serial ......... pinned: dense-solve equality, relabel invariance,
+                         single-node closed form
   passive + IClamp ..... pinned: one-compartment backward-Euler closed form,
                          sealed-cable steady state
-  hh ................... pinned: resting fixed point, FD Jacobian vs analytic g
-  cnexp states ......... pinned: ExpSyn/Exp2Syn decay closed forms, Exp2Syn peak 1
+  hh ................... pinned: textbook rates at init (two temperatures), gate
+                         relaxation x_inf + (x0 - x_inf) exp(-t/tau) under a voltage
+                         clamp at four voltages and two temperatures, ina/ik into
+                         the ion currents, FD Jacobian vs analytic g
+  Ca_HVA ............... pinned: m/h relaxation with the published mTau/hTau under
+                         clamp; ica = gbar m^2 h (v - eca) in ca_ion.cur, with a
+                         fixed eca and with eca from the per-step Nernst
+  hd_la (Ih) ........... pinned: l relaxation with taul under clamp (two
+                         temperatures, per-instance vhalfl and tau)
+  CaDynamics_E2 ........ pinned: cai under a constant non-zero ica against the
+                         linear-ODE solution c_inf + (c0 - c_inf) exp(-t/decay),
+                         c_inf = minCai - decay 1e4 ica gamma / (2 F depth); and
+                         relaxation to minCai with no current
   Nernst ............... pinned: closed form with CODATA constants
-  CaDynamics_E2 ........ pinned: linear-ODE closed form for a clamped ica
+  ExpSyn / Exp2Syn ..... pinned: decay closed forms, Exp2Syn peak = weight, the
+                         synaptic current in a backward-Euler compartment
+  HalfGap .............. pinned: a two-compartment pair against the lagged
+                         coupling recurrence
   spikes / delivery .... pinned: brute-force delivery-step rule on tiny inputs
   VecPlay .............. pinned: closed-form linear interpolation
-  hd_la, Ca_HVA rates .. pinned: steady-state (linf / mInf) invariants at clamp
   Adam ................. pinned: Kingma-Ba closed form
-  NetStim .............. pinned: Philox4x32-10 against Random123's published
-                         known-answer vectors, the stream's id/draw layout against
-                         those blocks, noiseless trains against start + k interval,
-                         noisy intervals against the exponential law
+  NetStim .............. pinned (tests/test_netstim.py): Philox4x32-10 against
+                         Random123's published known-answer vectors, the stream's
+                         id/draw layout against those blocks, noiseless trains
+                         against start + k interval, noisy intervals against the
+                         exponential law
 """
 from __future__ import annotations
 

@@ -208,6 +208,177 @@ def test_hh_gates_fixed_point_at_clamp():
     assert np.max(np.abs(m - m[0])) < 1e-9 and np.max(np.abs(n - n[0])) < 1e-9
 
 
+# A capacitance of 1e15 uF/cm2 holds v: the largest membrane current here moves it by
+# about 1e-12 mV per step, so gates see a constant voltage and cnexp is exact.
+CLAMP_CM = 1e15
+
+
+def relaxation(x0, xinf, tau, nsamp, dt=0.025):
+    """Sample k of a first-order relaxation started at x0 (sample 0 = x0)."""
+    k = np.arange(nsamp)
+    return xinf + (x0 - xinf) * np.exp(-k * dt / tau)
+
+
+def clamp_step(o, v0, v1, tstop):
+    """finitialize at v0 (gates at x_inf(v0)), then hold v at v1 for tstop ms."""
+    o.finitialize(v0)
+    o.set("global", "v", 0, v1)
+    o.run(tstop)
+
+
+@pytest.mark.parametrize("v1", [-90.0, -55.0, -30.0, 5.0])
+@pytest.mark.parametrize("celsius", [6.3, 16.3])
+def test_hh_gate_relaxation_under_clamp(v1, celsius):
+    """Gates started at x_inf(v0) and held at v1 follow x_inf + (x0 - x_inf) exp(-t/tau)
+    with x_inf and tau of the textbook rates at v1 and the temperature's q10
+    (hh_templated.cu:151-164).  A wrong tau, q10, sign or rate fails."""
+    v0 = -65.0
+    spec = hh_cell(v0, celsius)
+    spec.cm[:] = CLAMP_CM
+    o = oracle.OracleSim(spec, monitors=[("hh", "m", 0), ("hh", "h", 0), ("hh", "n", 0), ("global", "v", 0)])
+    clamp_step(o, v0, v1, 6.0)
+    v = o.monitor(3)
+    assert np.max(np.abs(v[1:] - v1)) < 1e-9
+    r0 = hh_textbook(v0, celsius)
+    r1 = hh_textbook(v1, celsius)
+    for j, name in enumerate("mhn"):
+        x = o.monitor(j)
+        ref = relaxation(r0[2 * j], r1[2 * j], r1[2 * j + 1], x.size)
+        assert np.max(np.abs(x - ref)) < 1e-10, name
+        # the relaxation is visible: it moved the gate by more than the tolerance
+        assert abs(x[-1] - x[0]) > 1e-4 or abs(r0[2 * j] - r1[2 * j]) < 1e-4
+
+
+def test_hh_ion_currents_under_clamp():
+    """ina = gnabar m^3 h (v - ena) and ik = gkbar n^4 (v - ek) accumulate into the ions'
+    cur (hh_templated.cu:120-140)."""
+    v0, v1 = -65.0, -20.0
+    spec = hh_cell(v0)
+    spec.cm[:] = CLAMP_CM
+    o = oracle.OracleSim(spec, monitors=[("hh", "m", 0), ("hh", "h", 0), ("hh", "n", 0),
+                                         ("na_ion", "cur", 0), ("k_ion", "cur", 0)])
+    clamp_step(o, v0, v1, 1.0)
+    m, h, n, ina, ik = (o.monitor(j) for j in range(5))
+    # the current of step k uses the gates of sample k-1 (states update after the solve)
+    assert np.allclose(ina[1:], 0.12 * m[:-1] ** 3 * h[:-1] * (v1 - 50.0), rtol=1e-9, atol=0)
+    assert np.allclose(ik[1:], 0.036 * n[:-1] ** 4 * (v1 + 77.0), rtol=1e-9, atol=0)
+
+
+def cahva_textbook(v):
+    """Ca_HVA rates of Reuveni et al. (1993) as distributed with the BBP models:
+    (mInf, mTau, hInf, hTau)."""
+    x = -27.0 - v
+    ma = 0.055 * (3.8 if abs(x) < 1e-9 else x / (math.exp(x / 3.8) - 1))
+    mb = 0.94 * math.exp((-75.0 - v) / 17.0)
+    ha = 0.000457 * math.exp((-13.0 - v) / 50.0)
+    hb = 0.0065 / (math.exp((-v - 15.0) / 28.0) + 1.0)
+    return ma / (ma + mb), 1 / (ma + mb), ha / (ha + hb), 1 / (ha + hb)
+
+
+def hdla_textbook(v, celsius, vhalfl=-81.0, tau=1.0):
+    """Ih of Larkum (hd_la): linf and taul with the mechanism's default globals
+    (kl -8, vhalft -75, a0t 0.011, zetat 2.2, gmt 0.4, q10 4.5, qtl 1)."""
+    qt = 4.5 ** ((celsius - 33.0) / 10.0)
+    a = math.exp(0.0378 * 2.2 * (v + 75.0))
+    b = math.exp(0.0378 * 2.2 * 0.4 * (v + 75.0))
+    linf = 1.0 / (1.0 + math.exp((v - vhalfl) / 8.0))
+    return linf, tau * b / (1.0 * qt * 0.011 * (1.0 + a))
+
+
+def calcium_cell(gbar, iontype, cadyn_params, celsius=6.3, hd=None):
+    spec = single_compartment(celsius=celsius)
+    spec.cm[:] = CLAMP_CM
+    n = np.array([0], np.int32)
+    spec.mechs["ca_ion"] = MechSpec(n, {"conci": np.array([5e-5]), "conco": np.array([2.0])},
+                                    iontype=np.array([iontype], np.int32))
+    spec.mechs["Ca_HVA"] = MechSpec(n.copy(), {"gbar": np.array([gbar])})
+    if cadyn_params is not None:
+        spec.mechs["CaDynamics_E2"] = MechSpec(n.copy(), {k: np.array([v]) for k, v in cadyn_params.items()})
+    if hd is not None:
+        spec.mechs["hd_la"] = MechSpec(n.copy(), {k: np.array([v]) for k, v in hd.items()})
+    return spec
+
+
+@pytest.mark.parametrize("v1", [-70.0, -35.0, -10.0, 20.0])
+def test_cahva_gate_relaxation_under_clamp(v1):
+    """Ca_HVA m and h relax with mTau, hTau of the published rates (CA_HVA.cu:97-178)."""
+    v0 = -65.0
+    spec = calcium_cell(1e-4, 0o4 | 0o40 | 0o100, None)
+    o = oracle.OracleSim(spec, monitors=[("Ca_HVA", "m", 0), ("Ca_HVA", "h", 0)])
+    clamp_step(o, v0, v1, 20.0)
+    r0 = cahva_textbook(v0)
+    r1 = cahva_textbook(v1)
+    m, h = o.monitor(0), o.monitor(1)
+    assert np.max(np.abs(m - relaxation(r0[0], r1[0], r1[1], m.size))) < 1e-10
+    assert np.max(np.abs(h - relaxation(r0[2], r1[2], r1[3], h.size))) < 1e-10
+    # both gates moved by at least 1e4 times the tolerance
+    assert abs(m[-1] - m[0]) > 1e-6
+    assert abs(h[-1] - h[0]) > 1e-6
+    # the assigned time constants are the rates' own
+    assert abs(o.get("Ca_HVA", "mTau", 0) / r1[1] - 1) < 1e-9
+    assert abs(o.get("Ca_HVA", "hTau", 0) / r1[3] - 1) < 1e-9
+
+
+@pytest.mark.parametrize("v1", [-100.0, -81.0, -60.0])
+@pytest.mark.parametrize("celsius", [6.3, 34.0])
+def test_hdla_gate_relaxation_under_clamp(v1, celsius):
+    """Ih's l relaxes with taul = tau bett / (qtl qt a0t (1 + alpt)) (hd_la.cu:80-128),
+    here with a per-instance vhalfl and tau away from their defaults."""
+    v0 = -65.0
+    spec = calcium_cell(0.0, 0o4 | 0o40 | 0o100, None, celsius=celsius,
+                        hd={"ghdbar": 1e-4, "vhalfl": -78.0, "tau": 1.7})
+    o = oracle.OracleSim(spec, monitors=[("hd_la", "l", 0)])
+    clamp_step(o, v0, v1, 100.0)
+    l0, _ = hdla_textbook(v0, celsius, -78.0, 1.7)
+    l1, t1 = hdla_textbook(v1, celsius, -78.0, 1.7)
+    x = o.monitor(0)
+    assert np.max(np.abs(x - relaxation(l0, l1, t1, x.size))) < 1e-10
+    assert abs(x[-1] - x[0]) > 1e-3
+
+
+@pytest.mark.parametrize("v0,gbar", [(-10.0, 1e-3), (-30.0, 5e-4), (10.0, 2e-3)])
+def test_cadynamics_drive_under_constant_ica(v0, gbar):
+    """With v held and eca fixed at its initial Nernst value (ion style 04|040, no
+    per-step Nernst), Ca_HVA's ica is constant and lands in ca_ion.cur as
+    gbar m^2 h (v - eca); cai then follows the linear ODE
+    dcai/dt = -1e4 ica gamma / (2 F depth) - (cai - minCai) / decay, whose solution is
+    c_inf + (c0 - c_inf) exp(-t/decay) with c_inf = minCai - decay 1e4 ica gamma / (2 F depth)
+    (CaDynamics_E2.cu:101-139, CA_HVA.cu:150-165)."""
+    gamma, decay, depth, minCai = 0.07, 60.0, 0.2, 2e-4
+    celsius = 6.3
+    spec = calcium_cell(gbar, 0o4 | 0o40, {"gamma": gamma, "decay": decay, "depth": depth, "minCai": minCai})
+    o = oracle.OracleSim(spec, monitors=[("ca_ion", "conci", 0), ("ca_ion", "cur", 0), ("ca_ion", "erev", 0)])
+    o.finitialize(v0)
+    o.run(150.0)
+    cai, cur, erev = o.monitor(0), o.monitor(1), o.monitor(2)
+    eca = 1000 * R * (celsius + 273.15) / F / 2 * math.log(2.0 / 5e-5)
+    assert np.max(np.abs(erev - eca)) < 1e-12
+    minf, _, hinf, _ = cahva_textbook(v0)
+    ica = gbar * minf ** 2 * hinf * (v0 - eca)
+    assert np.max(np.abs(cur[1:] - ica)) < 1e-12 * abs(ica) + 1e-15
+    cinf = minCai - decay * 1e4 * ica * gamma / (2 * F * depth)
+    ref = relaxation(5e-5, cinf, decay, cai.size)
+    assert np.max(np.abs(cai - ref)) < 1e-10 * abs(cinf)
+    assert cai[-1] > 10 * 5e-5          # the drive moved calcium far from its start
+
+
+def test_cahva_ica_follows_nernst_each_step():
+    """With style 0100 eca is recomputed from cai every step, and ica in ca_ion.cur is
+    gbar m^2 h (v - eca) with that step's eca (eion.cuh:155-166, CA_HVA.cu:150-165)."""
+    v0, gbar = -10.0, 1e-3
+    spec = calcium_cell(gbar, 0o4 | 0o40 | 0o100, {"decay": 80.0})
+    o = oracle.OracleSim(spec, monitors=[("ca_ion", "conci", 0), ("ca_ion", "cur", 0), ("ca_ion", "erev", 0)])
+    o.finitialize(v0)
+    o.run(20.0)
+    cai, cur, erev = o.monitor(0), o.monitor(1), o.monitor(2)
+    minf, _, hinf, _ = cahva_textbook(v0)
+    nernst = 1000 * R * (6.3 + 273.15) / F / 2 * np.log(2.0 / cai)
+    # the erev sampled after step k is Nernst of the cai that step k's current phase saw
+    assert np.allclose(erev[1:], nernst[:-1], rtol=1e-12)
+    assert np.allclose(cur[1:], gbar * minf ** 2 * hinf * (v0 - erev[1:]), rtol=1e-12)
+    assert erev[-1] < erev[0] - 1.0
+
+
 # ---------------------------------------------------------------------------
 # synapses: cnexp decays are exact exponentials; Exp2Syn peak is normalised
 # ---------------------------------------------------------------------------
@@ -237,6 +408,81 @@ def test_expsyn_decay_closed_form():
     assert np.allclose(g[k0:], ref, rtol=1e-12)
     # the event (weight w) lands before the first state update of its step
     assert abs(g[k0] - w * math.exp(-0.025 / tau)) < 1e-15
+
+
+def backward_euler_pas_syn(v0, gsyn_per_step, esyn, gp=1e-4, ep=-65.0, area=1000.0, cm=1.0, dt=0.025):
+    """Backward Euler of one compartment with pas and a synaptic conductance (uS) that is
+    constant within each step: v' = (C v + gp ep + G esyn) / (C + gp + G), C = 1e-3 cm / dt,
+    G = gsyn * 1e2 / area (a point process's nA -> mA/cm2)."""
+    c = 1e-3 * cm / dt
+    v = [v0]
+    for gs in gsyn_per_step:
+        G = gs * 1e2 / area
+        v.append((c * v[-1] + gp * ep + G * esyn) / (c + gp + G))
+    return np.array(v)
+
+
+def test_expsyn_current_backward_euler():
+    """ExpSyn's current g (v - e) enters the membrane as a point process: its conductance
+    during step k is the sampled g undone by one decay factor (the event lands before
+    the current, the decay after the solve) (expsyn.cu:40-70)."""
+    tau, w, esyn = 3.0, 0.004, -10.0
+    spec = synapse_cell("ExpSyn", {"tau": tau, "e": esyn}, [0.5, 3.0], w)
+    o = oracle.OracleSim(spec, monitors=[("ExpSyn", "g", 0), ("global", "v", 0)])
+    o.finitialize(-65.0)
+    o.run(15.0)
+    g, v = o.monitor(0), o.monitor(1)
+    gstep = g[1:] * math.exp(0.025 / tau)
+    ref = backward_euler_pas_syn(-65.0, gstep, esyn)
+    assert np.max(np.abs(v - ref)) < 1e-9
+    assert v.max() > -60.0            # the synapse moved v by several mV
+
+
+def test_exp2syn_current_backward_euler():
+    """Exp2Syn's conductance is B - A, each undone by its own decay factor (exp2syn_temp.cuh:46-67)."""
+    t1, t2, w, esyn = 0.5, 5.0, 0.003, 0.0
+    spec = synapse_cell("Exp2Syn", {"tau1": t1, "tau2": t2, "e": esyn}, [0.5], w)
+    o = oracle.OracleSim(spec, monitors=[("Exp2Syn", "A", 0), ("Exp2Syn", "B", 0), ("global", "v", 0)])
+    o.finitialize(-65.0)
+    o.run(15.0)
+    A, B, v = o.monitor(0), o.monitor(1), o.monitor(2)
+    gstep = B[1:] * math.exp(0.025 / t2) - A[1:] * math.exp(0.025 / t1)
+    ref = backward_euler_pas_syn(-65.0, gstep, esyn)
+    assert np.max(np.abs(v - ref)) < 1e-9
+    assert v.max() > -60.0
+
+
+def test_halfgap_pair_lagged_coupling():
+    """Two compartments joined by a HalfGap pair: each step the ELECTRODE current
+    (vgap - v) g, with g implicit in v and vgap the partner's voltage after the
+    previous update (simulate.cpp:436-438, 953-966; HalfGap.cu:61-68), gives
+    v' = v + [G (vgap - v) - gp (v - e)] / (C + gp + G)."""
+    area, g, gp, dt = 1000.0, 1e-3, 1e-4, 0.025
+    e = np.array([-65.0, -40.0])
+    spec = ModelSpec(ncell=2, parent=np.array([-1, -1], np.int32), a=np.zeros(2), b=np.zeros(2),
+                     area=np.full(2, area), cm=np.ones(2), dt=dt)
+    nodes = np.array([0, 1], np.int32)
+    spec.mechs["pas"] = MechSpec(nodes, {"g_pas": np.full(2, gp), "e_pas": e.copy()})
+    spec.mechs["HalfGap"] = MechSpec(nodes.copy(), {"g": np.full(2, g)})
+    spec.gap_src_node = np.array([1, 0], np.int32)       # HalfGap 0 (on cell 0) sees cell 1
+    spec.gap_halfgap = np.array([0, 1], np.int32)
+    o = oracle.OracleSim(spec, monitors=[("global", "v", 0), ("global", "v", 1), ("HalfGap", "vgap", 0)])
+    o.finitialize(-65.0)
+    o.run(30.0)
+    v0, v1, vg = o.monitor(0), o.monitor(1), o.monitor(2)
+    c = 1e-3 / dt
+    G = g * 1e2 / area
+    ref = np.zeros((v0.size, 2))
+    ref[0] = -65.0
+    for k in range(1, v0.size):
+        v = ref[k - 1]
+        vgap = v[::-1]
+        ref[k] = v + (G * (vgap - v) - gp * (v - e)) / (c + gp + G)
+    assert np.max(np.abs(v0 - ref[:, 0])) < 1e-10
+    assert np.max(np.abs(v1 - ref[:, 1])) < 1e-10
+    assert np.array_equal(vg, v1)                 # the transfer after each update
+    # the coupling is visible: without it cell 0 would stay at its rest
+    assert v0[-1] > -64.0
 
 
 def test_exp2syn_peak_is_weight():
