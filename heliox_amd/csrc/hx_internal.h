@@ -152,11 +152,12 @@ struct SolveArgs {
     const RoundInfo* rounds;
     const ChunkDesc* desc;
     double* v;
-    double* d;                    // in: membrane + capacitance diagonal; out: eliminated diagonal D
-    double* rhs;                  // in: membrane right-hand side; out: solution x (v += x)
+    double* d;                    // in: membrane + capacitance diagonal; out (store_dx): eliminated diagonal D
+    double* rhs;                  // in: membrane right-hand side; between the sweeps s; out (store_dx): solution x
     double* w;                    // scratch: b / D per node, written by elimination
     const double* a;
     const double* b;
+    int store_dx;                 // 1: leave D in d and x = vn - v in rhs (as the reference does); 0: neither
 };
 
 // Event ring: one slot per delivery step (mod nslot), fixed capacity per slot.

@@ -608,8 +608,9 @@ struct FwdBuf {
     uint2 q;              // ChunkDesc
     RoundU ri;
 };
+template <int kX>
 struct BackBuf {
-    double x[3][kPer];    // u (rhs) w v
+    double x[2 + kX][kPer];   // s (in rhs), w [, the old v]
     uint2 q;
     RoundU ri;
 };
@@ -669,6 +670,10 @@ struct StageIn {
     __device__ __forceinline__ FwdNode fwd(int k) const {
         return {at(SA_DB, k), at(SA_RM, k), at(SA_A, k), at(SA_B, k), at(SA_V, k)};
     }
+    __device__ __forceinline__ BackNode back(int k) const { return {at(SA_RM, k), at(SA_A, k), 0.0}; }
+};
+// back substitution that also reports x = vn - v: the old voltages are staged too
+struct StageInX : StageIn {
     __device__ __forceinline__ BackNode back(int k) const { return {at(SA_RM, k), at(SA_A, k), at(SA_V, k)}; }
 };
 
@@ -705,7 +710,9 @@ __device__ __forceinline__ void fwd_load(const SolveCtx& C, FwdBuf& B, const Rou
 }
 
 // Solves the round held in B; once B is staged, the next round (table entry
-// `next`, already loaded) is requested into N.
+// `next`, already loaded) is requested into N.  kX: the pivots D go to d (the
+// reference leaves them there; only read back through the API).
+template <int kX>
 __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, FwdBuf& N, const RoundV& next) {
     const RoundU& ri = B.ri;
     const uint2 q = B.q;
@@ -761,9 +768,9 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
             st[SA_DB * kStageStride + tp] = db;
             st[SA_RM * kStageStride + tp] = rm;
         }
-        auto out = [&](int k, double D, double u, double w) {
-            store_f64(rd, wo[k], D);
-            store_f64(ru, wo[k], u);
+        auto out = [&](int k, double D, double sv, double w) {
+            if constexpr (kX != 0) store_f64(rd, wo[k], D);
+            store_f64(ru, wo[k], sv);
             store_f64(rw, wo[k], w);
         };
         chunk_forward_math<KM>(has_parent, StageIn{st, rp}, out, rcp_nr, cd, ce);
@@ -772,24 +779,28 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
     round_boundary();
 }
 
-__device__ __forceinline__ void back_load(const SolveCtx& C, BackBuf& B, const RoundV& rv) {
+template <int kX>
+__device__ __forceinline__ void back_load(const SolveCtx& C, BackBuf<kX>& B, const RoundV& rv) {
     const RoundU ri = uniform_round(rv);
     const int base = C.nb + ri.node_base;
-    const double* u = C.S.rhs + base;
+    const double* sv = C.S.rhs + base;
     const double* w = C.S.w + base;
     const double* v = C.S.v + base;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const unsigned e = clamp_index(C.lane, j, ri.node_count);
-        B.x[0][j] = u[e];
+        B.x[0][j] = sv[e];
         B.x[1][j] = w[e];
-        B.x[2][j] = v[e];
+        if constexpr (kX != 0) B.x[2][j] = v[e];
     }
     B.q = load_desc(C, ri);
     B.ri = ri;
 }
 
-__device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, BackBuf& N, const RoundV& next) {
+// kX: x = vn - v goes to rhs (the reference leaves the solution there).
+template <int kX>
+__device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>& B, BackBuf<kX>& N,
+                                           const RoundV& next) {
     const RoundU& ri = B.ri;
     const uint2 q = B.q;
     double* st = C.stage;
@@ -798,10 +809,10 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, 
         const int e = C.lane + kWave * j;
         st[SA_RM * kStageStride + e] = B.x[0][j];
         st[SA_A * kStageStride + e] = B.x[1][j];
-        st[SA_V * kStageStride + e] = B.x[2][j];
+        if constexpr (kX != 0) st[SA_V * kStageStride + e] = B.x[2][j];
     }
     round_boundary();
-    back_load(C, N, next);
+    back_load<kX>(C, N, next);
     const bool act = C.lane < ri.desc_count;
     const int slot = q.x & 0xFFFF;
     const int parent_slot = q.x >> 16;
@@ -814,12 +825,13 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf& B, 
         constexpr int KM = decltype(km)::value;
         int rp[KM], wo[KM], tp;
         round_positions<KM>(ri, len, C.lane, rp, wo, tp);
-        auto out = [&](int k, double vn, double x) {
+        auto out = [&](int k, double vn, double vo) {
             store_f64(rv, wo[k], vn);
-            store_f64(rx, wo[k], x);
+            if constexpr (kX != 0) store_f64(rx, wo[k], vn - vo);
             if (k == len - 1) vtail = vn;
         };
-        chunk_back_math<KM>(StageIn{st, rp}, out, vpar);
+        if constexpr (kX != 0) chunk_back_math<KM>(StageInX{{st, rp}}, out, vpar);
+        else chunk_back_math<KM>(StageIn{st, rp}, out, vpar);
     });
     if (act) C.slots[2 * slot] = vtail;   // the tail's new voltage
     round_boundary();
@@ -840,6 +852,7 @@ __device__ __forceinline__ void drain_vector_memory() { __builtin_amdgcn_s_waitc
 // trip solves two rounds and the buffers never trade registers.  Round indices
 // past either end are clamped to a real round, whose loads are issued but
 // never used.
+template <int kX>
 __global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* rounds_all, const uint2* desc,
                                                  int max_chunks) {
     extern __shared__ double lds[];
@@ -871,21 +884,21 @@ __global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* r
         drain_vector_memory();
         for (int r = last; r > 0; r -= 2) {
             RoundV n = load_round(rounds, fwd_idx(r - 2));
-            fwd_round(C, x, y, nx);
+            fwd_round<kX>(C, x, y, nx);
             nx = load_round(rounds, fwd_idx(r - 3));
-            fwd_round(C, y, x, n);
+            fwd_round<kX>(C, y, x, n);
         }
     }
     {
-        BackBuf x, y;
-        back_load(C, x, load_round(rounds, 0));
+        BackBuf<kX> x, y;
+        back_load<kX>(C, x, load_round(rounds, 0));
         RoundV nx = load_round(rounds, 1);
         drain_vector_memory();
         for (int r = 0; r < last; r += 2) {
             RoundV n = load_round(rounds, back_idx(r + 2));
-            back_round(C, x, y, nx);
+            back_round<kX>(C, x, y, nx);
             nx = load_round(rounds, back_idx(r + 3));
-            back_round(C, y, x, n);
+            back_round<kX>(C, y, x, n);
         }
     }
 }
@@ -1135,8 +1148,12 @@ void launch_set_v(double* v, int n, double val, hipStream_t s) {
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
     if (a.nunit <= 0) return;
     const size_t lds = solve_lds_bytes(max_chunks);
-    hipLaunchKernelGGL(k_solve, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
-                       reinterpret_cast<const uint2*>(a.desc), max_chunks);
+    if (a.store_dx)
+        hipLaunchKernelGGL(k_solve<1>, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
+                           reinterpret_cast<const uint2*>(a.desc), max_chunks);
+    else
+        hipLaunchKernelGGL(k_solve<0>, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
+                           reinterpret_cast<const uint2*>(a.desc), max_chunks);
 }
 
 void launch_spike(const SpikeArgs& a, hipStream_t s) {

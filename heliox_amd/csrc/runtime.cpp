@@ -220,6 +220,7 @@ struct hx_sim {
 
     // layout
     std::vector<int> node_perm, node_iperm;    // user <-> solver order
+    std::vector<int> ion_at[3];                // na/k/ca: solver-order node -> device ion instance (-1: none)
     // solve units: runs of consecutive cells, each solved by one wavefront
     std::vector<int> unit_cell_begin, unit_node_begin, unit_desc_begin, unit_round_begin;
     int nunit = 0;
@@ -303,6 +304,9 @@ struct hx_sim {
     bool last_multi_stream = false;
     bool group_streams_allowed = true;            // hx_set_group_streams
     hipEvent_t ev_main = nullptr;
+    hipEvent_t ev_stagger = nullptr;     // group g's first node pass of a run, awaited by group g+1
+    bool stagger_next = false;           // the next grouped step starts the groups half a step apart
+    int stagger_groups = 1;              // 0: all groups start together
     // time table
     std::vector<double> ttab;
     double* d_ttab = nullptr;
@@ -419,6 +423,7 @@ struct hx_sim {
             if (g.s) (void)hipStreamDestroy(g.s);
         }
         if (ev_main) (void)hipEventDestroy(ev_main);
+        if (ev_stagger) (void)hipEventDestroy(ev_stagger);
         for (auto& tm : timers)
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
@@ -500,6 +505,10 @@ struct hx_sim {
     void launch_record();
     void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
     bool want_multi_stream() const;
+    // The tree solve leaves the pivots in d and the solution x in rhs, as the reference
+    // does, on the last step of a call (read back through the API) and on every step
+    // when a handle, monitor or transfer may read them; otherwise neither is stored.
+    bool store_dx() const { return final_step || write_assigned || !dg_src.empty(); }
     void step_once_groups();
     void step_once();
     void finish_pending();
@@ -790,7 +799,6 @@ void hx_sim::upload() {
     }
 
     // ion node -> device instance maps
-    std::vector<int> ion_at[3];
     const int ion_ids[3] = {M_NA_ION, M_K_ION, M_CA_ION};
     for (int x = 0; x < 3; ++x) {
         ion_at[x].assign(nnode, -1);
@@ -1086,6 +1094,7 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
         }
     }
     if (G > 1 && !ev_main) HXC(hipEventCreateWithFlags(&ev_main, hipEventDisableTiming));
+    if (G > 1 && !ev_stagger) HXC(hipEventCreateWithFlags(&ev_stagger, hipEventDisableTiming));
 }
 
 // NetStim (netstim.cpp:211-330, one random stream per instance) as a train of
@@ -1331,10 +1340,8 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     HostMech& m = mech[id];
     if (M.ion) {
         if (idx < 0 || idx >= nnode) return r;
-        const int g = node_perm[idx];
-        int inst = -1;
-        for (int j = 0; j < m.n; ++j)
-            if (node_perm[m.node[m.iperm[j]]] == g) { inst = j; break; }
+        const int x = id == M_NA_ION ? 0 : id == M_K_ION ? 1 : 2;
+        const int inst = ion_at[x][node_perm[idx]];
         const int c = col_id(id, var);
         if (inst < 0 || c < 0) return r;
         r.dev = m.dev.col(c) + inst;
@@ -1679,11 +1686,19 @@ void hx_sim::step_once_groups() {
     if (pending && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
     pass_cadyn_skip = cadyn_done ? 1 : 0;
     pass_cadyn_after = cadyn_eager ? 1 : 0;
+    // First step of a run: each group starts once the previous group's node pass is
+    // done, so from then on one group's tree solve (latency-bound) runs beside the
+    // other's node pass (HBM-bound) instead of two node passes and then two solves
+    // running together.  The ordering is through events only: results are unchanged.
+    const bool stagger = stagger_next;
+    stagger_next = false;
     for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
         CellGroup& cg = groups[g];
         hipStream_t s = cg.s;
+        if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
         launch_events_group(g, k, tk, s);
         launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+        if (stagger && g + 1 < static_cast<int>(groups.size())) HXC(hipEventRecord(ev_stagger, s));
         if (pending && cg.mon1 > cg.mon0)
             hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
         SolveArgs S{};
@@ -1699,6 +1714,7 @@ void hx_sim::step_once_groups() {
         S.w = d_w;
         S.a = d_sa;
         S.b = d_sb;
+        S.store_dx = store_dx() ? 1 : 0;
         tbegin(T_SOLVE, s);
         launch_solve(S, max_slots, s);
         tend(T_SOLVE, s);
@@ -1786,6 +1802,7 @@ void hx_sim::step_once() {
     S.w = d_w;
     S.a = d_sa;
     S.b = d_sb;
+    S.store_dx = store_dx() ? 1 : 0;
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
@@ -1901,6 +1918,7 @@ int hx_sim::run_steps(int nstep) {
     if (multi_stream) {
         HXC(hipEventRecord(ev_main, stream));
         for (auto& cg : groups) HXC(hipStreamWaitEvent(cg.s, ev_main, 0));
+        stagger_next = stagger_groups != 0;
     }
     try {
         for (int s = 0; s < nstep; ++s) {
@@ -2598,11 +2616,19 @@ int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, in
     int id = mech_id(mn);
     if (id < 0 || !sim->mech[id].present) return sim->fail("mechanism '%s' not present", mn.c_str());
     if (id == M_CADYN && (vn == "cai" || vn == "ica")) {
+        // CaDynamics_E2 keeps cai / ica in the ca_ion column of its node: one copy of
+        // that column, then a gather through the node -> ion instance map
         HostMech& m = sim->mech[id];
+        HostMech& ca = sim->mech[M_CA_ION];
         if (cap < m.n) return sim->fail("output too small");
+        std::vector<double> col(ca.n);
+        if (ca.n)
+            HXC(hipMemcpy(col.data(), ca.dev.col(vn == "cai" ? ION_CONCI : ION_CUR), sizeof(double) * ca.n,
+                          hipMemcpyDeviceToHost));
         for (int j = 0; j < m.n; ++j) {
-            Ref r = sim->resolve("ca_ion", vn == "cai" ? "conci" : "cur", m.node[j]);
-            HXC(hipMemcpy(out + j, r.dev, sizeof(double), hipMemcpyDeviceToHost));
+            const int inst = sim->ion_at[2][sim->node_perm[m.node[j]]];
+            if (inst < 0) return sim->fail("CaDynamics_E2 instance %d has no ca_ion on its node", j);
+            out[j] = col[inst];
         }
         return m.n;
     }
@@ -2869,7 +2895,7 @@ int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const d
             auto positions = [&](int r, int l, int len) {
                 for (int k = 0; k < kChunk; ++k) idx[k] = k < len ? nb + ri[r].node_base + ri[r].off[k] + l : -1;
             };
-            // kernel stage arrays: DB RM A B V; back substitution reads u from RM, w from w, v from V
+            // kernel stage arrays: DB RM A B V; back substitution reads s from RM, w from w, v from V
             auto val = [&](int x, int k) { return idx[k] >= 0 ? arr[x][idx[k]] : neutral[x]; };
             struct In {
                 std::function<double(int, int)> f;
@@ -2897,7 +2923,7 @@ int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const d
                     dispatch_chunk_bound(ri[r].maxlen, [&](auto km) {
                         chunk_forward_math<decltype(km)::value>(
                             q.parent_slot != kNone, in,
-                            [&](int k, double Dk, double uk, double wk) { D[k] = Dk; U[k] = uk; W[k] = wk; }, rcp,
+                            [&](int k, double Dk, double sk, double wk) { D[k] = Dk; U[k] = sk; W[k] = wk; }, rcp,
                             cdd, cee);
                     });
                     {
@@ -2906,7 +2932,7 @@ int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const d
                         double D2[kChunk], U2[kChunk], W2[kChunk], cd2, ce2;
                         chunk_forward_math<kChunk>(
                             q.parent_slot != kNone, in,
-                            [&](int k, double Dk, double uk, double wk) { D2[k] = Dk; U2[k] = uk; W2[k] = wk; }, rcp,
+                            [&](int k, double Dk, double sk, double wk) { D2[k] = Dk; U2[k] = sk; W2[k] = wk; }, rcp,
                             cd2, ce2);
                         bool same = std::memcmp(&cd2, &cdd, sizeof cdd) == 0 && std::memcmp(&ce2, &cee, sizeof cee) == 0;
                         for (int k = 0; k < q.len; ++k)
@@ -2932,9 +2958,10 @@ int hx_emulate_tree_solve_units(int ncell, int nnode, const int* parent, const d
                     double VN[kChunk], X[kChunk], VN2[kChunk], X2[kChunk];
                     dispatch_chunk_bound(ri[r].maxlen, [&](auto km) {
                         chunk_back_math<decltype(km)::value>(
-                            in, [&](int k, double vn, double x) { VN[k] = vn; X[k] = x; }, vpar);
+                            in, [&](int k, double vn, double vo) { VN[k] = vn; X[k] = vn - vo; }, vpar);
                     });
-                    chunk_back_math<kChunk>(in, [&](int k, double vn, double x) { VN2[k] = vn; X2[k] = x; }, vpar);
+                    chunk_back_math<kChunk>(in, [&](int k, double vn, double vo) { VN2[k] = vn; X2[k] = vn - vo; },
+                                            vpar);
                     for (int k = 0; k < q.len; ++k)
                         if (std::memcmp(&VN[k], &VN2[k], 8) != 0 || std::memcmp(&X[k], &X2[k], 8) != 0)
                             bound_mismatch = true;
@@ -3138,6 +3165,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     S.w = sim->d_wT;
     S.a = sim->d_sb;      // M^T: the coefficients trade places
     S.b = sim->d_sa;
+    S.store_dx = 1;       // mu = M^-T lambda is read from rhs
     double* lv = sim->d_lv;
     double* lv2 = sim->d_lv2;
     const size_t row = static_cast<size_t>(N);

@@ -18,8 +18,11 @@
 //     P_k = (Db_k - a_{k+1}) P_{k+1} - a_{k+1} b_{k+1} P_{k+2}
 //   (P_len = 1), so the chain costs one fma per node and the reciprocals
 //   1/P_k are independent of each other.
-// * Elimination stores u = R/D and w = b/D, so back substitution is
-//   x_k = u_k - w_k x_{k-1}: one fma per node.
+// * Elimination has u = R/D and w = b/D, and back substitution is
+//   x_k = u_k - w_k x_{k-1}.  In terms of the new voltages vn_k = v_k + x_k that is
+//   vn_k = s_k - w_k vn_{k-1} with s_k = v_k + u_k + w_k v_{k-1}, so elimination
+//   stores s and w and back substitution reads just those two (one fma per
+//   node, no reload of v); x is vn - v where a caller needs it.
 // * The head's parent voltage v_p enters R_head only through -b_head v_p.
 //   Leaving it out, the head hands its parent the pair (cd, ce) with
 //   cd = a + (a/D) b and ce = -a v_head - (a/D) R'_head, and the parent's tail
@@ -42,16 +45,15 @@
 
 namespace hx {
 
-// arrays of a round stage; elimination reads DB RM A B V and writes D into
-// DB, u into RM and w into B; back substitution reads u (RM), w (A) and v (V)
-// and writes x into RM and the new v into V
+// arrays of a round stage; elimination reads DB RM A B V and produces D, s and w;
+// back substitution reads s (RM), w (A) and, where x is wanted, the old v (V)
 enum StageArr { SA_DB = 0, SA_RM = 1, SA_A = 2, SA_B = 3, SA_V = 4 };
 
 struct FwdNode {
     double db, rm, a, b, v;    // db = dm + cfac cm
 };
 struct BackNode {
-    double u, w, v;
+    double s, w, v;            // v: the voltage before the step (read only when x is stored)
 };
 
 // The tail's inputs after adding the chunk's children: acd = sum cd,
@@ -84,9 +86,9 @@ __host__ __device__ __forceinline__ void dispatch_chunk_bound(int maxlen, F&& f)
 }
 
 // in.fwd(k): node k's inputs (neutral for k >= len, tail already injected);
-// rcp(x) returns 1/x.  out(k, D, u, w) receives node k's results for every
-// slot k < KM (the caller drops those of padding nodes).  cd, ce: this
-// chunk's pair for its parent.
+// rcp(x) returns 1/x.  out(k, D, s, w) receives node k's results for every
+// slot k < KM (the caller drops those of padding nodes): the pivot D, s and w.
+// cd, ce: this chunk's pair for its parent.
 template <int KM, class In, class Out, class Rcp>
 __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, const In& in, Out&& out, Rcp rcp,
                                                             double& cd, double& ce) {
@@ -116,7 +118,8 @@ __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, con
         const double R = Rb + accr;
         const double p = a * rD;
         accr = fma(a, dv, -(p * R));
-        out(k, P * r1, R * rD, b * rD);
+        const double w = b * rD;
+        out(k, P * r1, fma(w, k > 0 ? buf[k - 1].v : 0.0, cur.v + R * rD), w);
         if (k == 0) {
             cd = fma(p, b, a);
             ce = accr;
@@ -129,21 +132,21 @@ __host__ __device__ __forceinline__ void chunk_forward_math(bool has_parent, con
     }
 }
 
-// in.back(k): node k's (u, w, v) (neutral for k >= len); vpar_new: updated
+// in.back(k): node k's (s, w, v) (neutral for k >= len); vpar_new: updated
 // voltage of the head's parent (0 for the root chunk, whose w_0 is 0).
-// out(k, v_new, x) for every slot k < KM.
+// out(k, v_new, v_old) for every slot k < KM.
 template <int KM, class In, class Out>
 __host__ __device__ __forceinline__ void chunk_back_math(const In& in, Out&& out, double vpar_new) {
     static_assert(KM >= 1 && KM <= kChunk, "chunk bound out of range");
-    double x = vpar_new;
+    double vn = vpar_new;
     BackNode buf[KM];
 #pragma unroll
     for (int j = 0; j < kAhead && j < KM; ++j) buf[j] = in.back(j);
 #pragma unroll
     for (int k = 0; k < KM; ++k) {
         if (k + kAhead < KM) buf[k + kAhead] = in.back(k + kAhead);
-        x = fma(-buf[k].w, x, buf[k].u);
-        out(k, buf[k].v + x, x);
+        vn = fma(-buf[k].w, vn, buf[k].s);
+        out(k, vn, buf[k].v);
     }
 }
 
