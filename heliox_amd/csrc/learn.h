@@ -26,6 +26,8 @@
 namespace hx {
 
 constexpr int kLrMaxChannels = 3;     // pure_i, didv, didvpre
+// Size of the per-device scratch array of the allocation-free replay (64 MiB).
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(64) << 20;
 
 struct CaptureChannel {
     const int* begin = nullptr;       // N + 1: items of column c are [begin[c], begin[c+1])
@@ -152,6 +154,10 @@ public:
     };
     int replay(const ReplayIn& in);
     int load_signals(const float* it_nt, const float* dv_nt, const float* dp_nt, int N, int T, bool percise);
+    // The replay over host (N, T) signals with every device buffer carved from the
+    // library's fixed scratch array (kNoAllocScratchBytes per device): no allocation.
+    int replay_from_host_noalloc(const ReplayIn& in, const float* it_nt, const float* dv_nt, const float* dp_nt, int N,
+                                 int T);
     int capture_N() const { return cap_N_; }
     int capture_T() const { return cap_T_; }
     bool capture_percise() const { return cap_percise_; }
@@ -161,9 +167,17 @@ public:
     double corr_ms = 0;
     long long corr_launches = 0;
 
+    struct Workspace {
+        float *hist = nullptr, *ghist = nullptr, *slot_scale = nullptr, *gs = nullptr, *tick_scale = nullptr,
+              *w_tick = nullptr, *dw_acc = nullptr, *dl = nullptr, *dx = nullptr, *dw_out = nullptr;
+        int *po = nullptr, *pre = nullptr, *pin = nullptr, *flag_part = nullptr;
+        double* norm_part = nullptr;
+    };
+
 private:
     int fail(const char* fmt, ...);
     void free_all(std::vector<void*>& v);
+    int replay_on(const ReplayIn& in, const Workspace& ws, float* const* sig, int N);
 
     hipStream_t stream_;
     // dense blocks
@@ -197,12 +211,7 @@ private:
     // replay workspace, kept while the problem shape is unchanged
     std::vector<void*> ws_mem_;
     std::vector<long long> ws_key_;
-    struct Workspace {
-        float *hist = nullptr, *ghist = nullptr, *slot_scale = nullptr, *gs = nullptr, *tick_scale = nullptr, *w_tick = nullptr,
-              *dw_acc = nullptr, *dl = nullptr, *dx = nullptr, *dw_out = nullptr;
-        int *po = nullptr, *pre = nullptr, *pin = nullptr, *flag_part = nullptr;
-        double* norm_part = nullptr;
-    } ws_;
+    Workspace ws_;
 };
 
 }  // namespace hx

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -279,7 +280,6 @@ int LearnRuntime::replay(const ReplayIn& in) {
     if (N <= 0 || T != in.ksteps + 1) return fail("replay: no signals of %d ticks", in.ksteps);
     const int K_len = k_len_;
     const int ks = in.ksteps;
-    const bool need_dx = in.n_in > 0;
     try {
         // workspace: history ring, base scratch, per-tick vectors, norm partials
         const int R = in.percise ? K_len + 1 : 1;
@@ -307,21 +307,40 @@ int LearnRuntime::replay(const ReplayIn& in) {
             ws_.dw_out = lalloc<float>(ws_mem_, N);
             ws_key_ = key;
         }
-        float* hist = ws_.hist;
-        float* ghist = ws_.ghist;
-        float* slot_scale = ws_.slot_scale;
-        float* gs = ws_.gs;
-        float* tick_scale = ws_.tick_scale;
-        float* w_tick = ws_.w_tick;
-        float* dw_acc = ws_.dw_acc;
-        float* dl = ws_.dl;
-        int* po = ws_.po;
-        int* pre = ws_.pre;
-        int* pin = ws_.pin;
-        float* dx = ws_.dx;
-        double* norm_part = ws_.norm_part;
-        int* flag_part = ws_.flag_part;
-        float* dw_out = ws_.dw_out;
+    } catch (const std::exception& e) {
+        free_all(ws_mem_);
+        ws_key_.clear();
+        return fail("replay: %s", e.what());
+    }
+    return replay_on(in, ws_, sig, N);
+}
+
+// The replay proper over signals sig[c] ((T, N) on the device) with the buffers of ws;
+// it allocates nothing (with timing off).
+int LearnRuntime::replay_on(const ReplayIn& in, const Workspace& ws, float* const* sig, int N) {
+    const int K_len = k_len_;
+    const int ks = in.ksteps;
+    const bool need_dx = in.n_in > 0;
+    try {
+        const int R = in.percise ? K_len + 1 : 1;
+        const size_t slice = static_cast<size_t>(N) * N;
+        const int ntiles = static_cast<int>(tiles_.size());
+        const int nwg = ntiles * rp_corr_row_tiles(N);
+        float* hist = ws.hist;
+        float* ghist = ws.ghist;
+        float* slot_scale = ws.slot_scale;
+        float* gs = ws.gs;
+        float* tick_scale = ws.tick_scale;
+        float* w_tick = ws.w_tick;
+        float* dw_acc = ws.dw_acc;
+        float* dl = ws.dl;
+        int* po = ws.po;
+        int* pre = ws.pre;
+        int* pin = ws.pin;
+        float* dx = ws.dx;
+        double* norm_part = ws.norm_part;
+        int* flag_part = ws.flag_part;
+        float* dw_out = ws.dw_out;
         LRC(hipMemcpyAsync(dl, in.dl, sizeof(float) * static_cast<size_t>(ks) * in.n_out, hipMemcpyHostToDevice,
                            stream_));
         LRC(hipMemcpyAsync(po, in.po, sizeof(int) * in.n_out, hipMemcpyHostToDevice, stream_));
@@ -434,11 +453,107 @@ int LearnRuntime::replay(const ReplayIn& in) {
         if (need_dx)
             LRC(hipMemcpy(in.dx_out, dx, sizeof(float) * static_cast<size_t>(in.n_in) * ks, hipMemcpyDeviceToHost));
     } catch (const std::exception& e) {
-        free_all(ws_mem_);
-        ws_key_.clear();
         return fail("replay: %s", e.what());
     }
     return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Replay without allocation: every device buffer of a host-signal replay is
+// carved from one file-scope device array, `scratch`.  Each device holds its
+// own copy; its address is looked up once per device with hipGetSymbolAddress
+// (the array's name in host code is not a device address).  All calls on one
+// device share it, so calls that overlap on one device race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int kScratchMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex scratch_mu;
+unsigned char* scratch_dev[kScratchMaxDevices] = {};
+
+// 256-byte aligned sub-allocations of the scratch array, in a fixed order; with
+// base == nullptr it only measures.
+struct Carver {
+    unsigned char* base;
+    size_t used = 0;
+    template <class T>
+    T* take(size_t n) {
+        used = (used + 255) & ~static_cast<size_t>(255);
+        T* p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+        used += std::max<size_t>(n, 1) * sizeof(T);
+        return p;
+    }
+};
+}  // namespace
+
+// Address of this device's scratch array (looked up on the first call on each device).
+unsigned char* noalloc_scratch() {
+    int dev = 0;
+    LRC(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kScratchMaxDevices) throw HipFail("device index out of range for the scratch table");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_dev[dev]) {
+        void* p = nullptr;
+        LRC(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        scratch_dev[dev] = static_cast<unsigned char*>(p);
+    }
+    return scratch_dev[dev];
+}
+
+int LearnRuntime::replay_from_host_noalloc(const ReplayIn& in, const float* it_nt, const float* dv_nt,
+                                           const float* dp_nt, int N, int T) {
+    if (N <= 0 || T != in.ksteps + 1) return fail("replay: no signals of %d ticks", in.ksteps);
+    try {
+        const int nch = in.percise ? 3 : 1;
+        const int R = in.percise ? k_len_ + 1 : 1;
+        const size_t slice = static_cast<size_t>(N) * N;
+        const size_t sigsz = static_cast<size_t>(N) * T;
+        const int nwg = static_cast<int>(tiles_.size()) * rp_corr_row_tiles(N);
+        const int ks = in.ksteps;
+        auto carve = [&](Carver& c, Workspace& w, float** sig, float** stage) {
+            *stage = c.take<float>(sigsz);
+            for (int ch = 0; ch < kLrMaxChannels; ++ch) sig[ch] = ch < nch ? c.take<float>(sigsz) : nullptr;
+            w.hist = c.take<float>(slice * R);
+            w.ghist = in.percise ? c.take<float>(slice * R) : nullptr;
+            w.slot_scale = c.take<float>(R);
+            w.gs = c.take<float>(1);
+            w.tick_scale = c.take<float>(1);
+            w.w_tick = c.take<float>(N);
+            w.dw_acc = c.take<float>(N);
+            w.dl = c.take<float>(static_cast<size_t>(ks) * in.n_out);
+            w.po = c.take<int>(in.n_out);
+            w.pre = c.take<int>(N);
+            w.pin = c.take<int>(std::max(in.n_in, 1));
+            w.dx = c.take<float>(static_cast<size_t>(std::max(in.n_in, 1)) * ks);
+            w.norm_part = c.take<double>(nwg);
+            w.flag_part = c.take<int>(nwg);
+            w.dw_out = c.take<float>(N);
+        };
+        Workspace w;
+        float* sig[kLrMaxChannels];
+        float* stage = nullptr;
+        Carver measure{nullptr};
+        carve(measure, w, sig, &stage);
+        if (measure.used > kNoAllocScratchBytes)
+            return fail("replay needs %zu bytes of device scratch for N=%d, T=%d, K_len=%d%s; the allocation-free "
+                        "entry point holds at most %zu bytes (use the allocating one)",
+                        measure.used, N, T, k_len_, in.percise ? " (percise)" : "", kNoAllocScratchBytes);
+        Carver c{noalloc_scratch()};
+        carve(c, w, sig, &stage);
+        // (N, T) host signals -> (T, N) on the device, as load_signals does
+        const float* src[kLrMaxChannels] = {it_nt, dv_nt, dp_nt};
+        for (int ch = 0; ch < nch; ++ch) {
+            LRC(hipMemcpyAsync(stage, src[ch], sigsz * sizeof(float), hipMemcpyHostToDevice, stream_));
+            launch_transpose_nt_tn(stage, sig[ch], N, T, stream_);
+        }
+        const bool was_timing = timing;
+        timing = false;                 // the timing path creates events
+        const int rc = replay_on(in, w, sig, N);
+        timing = was_timing;
+        return rc;
+    } catch (const std::exception& e) {
+        return fail("replay: %s", e.what());
+    }
 }
 
 }  // namespace hx

@@ -3664,7 +3664,8 @@ namespace {
 int replay_common(hx_sim* sim, const char* fn, LearnRuntime::Source src, const float* dL, int ksteps, int n_output,
                   const int* poutput, const int* pinput, int n_input, const int* pre_of_col, int n_pre,
                   float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
-                  double thr, int clip_strategy, int clip_every) {
+                  double thr, int clip_strategy, int clip_every, const float* const* noalloc_sig = nullptr,
+                  int noalloc_T = 0) {
     LearnRuntime& L = sim->learn_rt();
     if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
     const bool cached = src == LearnRuntime::SRC_CACHE;
@@ -3710,7 +3711,11 @@ int replay_common(hx_sim* sim, const char* fn, LearnRuntime::Source src, const f
     in.clip_every = std::max(1, clip_every);
     in.source = src;
     in.cached_clip_rule = src != LearnRuntime::SRC_HOST;
-    if (L.replay(in) != 0) return sim->fail("%s: %s", fn, L.err.c_str());
+    // host signals given here: the allocation-free replay over the library's scratch array
+    const int rc = noalloc_sig
+                       ? L.replay_from_host_noalloc(in, noalloc_sig[0], noalloc_sig[1], noalloc_sig[2], N, noalloc_T)
+                       : L.replay(in);
+    if (rc != 0) return sim->fail("%s: %s", fn, L.err.c_str());
     return 0;
 }
 
@@ -3779,6 +3784,35 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
                          n_input, pre_of_col,
                          N, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps, grad_l2norm_threshold,
                          clip_strategy, clip_check_every);
+    API_END
+}
+
+int hx_replay_compute_dw_dx_from_signals_into_noalloc(
+    hx_sim* sim, const float* it_lr_nt, const float* ditdv_lr_nt, const float* ditdvpre_lr_nt, int N, int T,
+    const float* dLtdv_lr_to, int ksteps_total, int n_output, const int* poutput, const int* pinput, int n_input,
+    const int* pre_of_col, float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
+    double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    static const char* fn = "replay_compute_dw_dx_from_signals_into_noalloc";
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    LearnRuntime& L = sim->learn_rt();
+    // the same checks as the allocating entry point
+    if (L.k_len() <= 0) return sim->fail("%s: dense blocks not set (call set_dense_blocks_f32)", fn);
+    if (!it_lr_nt || !dLtdv_lr_to || !poutput || !pinput || !pre_of_col || !dw_out_n || !dx_lr_it)
+        return sim->fail("%s: null pointer input/output", fn);
+    if (N <= 0 || T < 2) return sim->fail("%s: invalid it_lr_nt shape (%d, %d)", fn, N, T);
+    if (ksteps_total != T - 1) return sim->fail("%s: ksteps_total mismatch (%d vs T-1=%d)", fn, ksteps_total, T - 1);
+    if (n_output <= 0 || n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
+    if (!(dt_ms > 0.0) || !(eps > 0.0)) return sim->fail("%s: invalid dt_ms/eps", fn);
+    if (!(grad_l2norm_threshold > 0.0)) return sim->fail("%s: invalid grad_l2norm_threshold", fn);
+    clip_strategy = std::max(0, clip_strategy);
+    clip_check_every = std::max(1, clip_check_every);
+    if (percise && (!ditdv_lr_nt || !ditdvpre_lr_nt))
+        return sim->fail("%s: percise requested but ditdv buffers are null", fn);
+    const float* sig[3] = {it_lr_nt, ditdv_lr_nt, ditdvpre_lr_nt};
+    return replay_common(sim, fn, LearnRuntime::SRC_HOST, dLtdv_lr_to, ksteps_total, n_output, poutput, pinput,
+                         n_input, pre_of_col, N, dw_out_n, dx_lr_it, dt_ms, percise, grad_scale, eps,
+                         grad_l2norm_threshold, clip_strategy, clip_check_every, sig, T);
     API_END
 }
 

@@ -118,6 +118,9 @@ SIGNATURES = {
     "hx_replay_compute_dw_dx_from_signals_into": (
         C.c_int, [_P, _F, _F, _F, C.c_int, C.c_int, _F, C.c_int, C.c_int, _I, _I, C.c_int, _I, _F, _F, C.c_double,
                   C.c_int, C.c_double, C.c_double, C.c_double, C.c_int, C.c_int]),
+    "hx_replay_compute_dw_dx_from_signals_into_noalloc": (
+        C.c_int, [_P, _F, _F, _F, C.c_int, C.c_int, _F, C.c_int, C.c_int, _I, _I, C.c_int, _I, _F, _F, C.c_double,
+                  C.c_int, C.c_double, C.c_double, C.c_double, C.c_int, C.c_int]),
     "hx_simulate_and_replay_dw_dx_streaming_into": (
         C.c_int, [_P, _F, C.c_int, C.c_int, _I, _I, C.c_int, C.c_int, _I, _F, _F, C.c_int, _I, _I, _F, C.c_int, _I,
                   _I, _F, C.c_int, _I, _I, _F, C.c_double, C.c_int, C.c_int, C.c_double, C.c_double, C.c_double,
@@ -916,7 +919,9 @@ class Sim:
                                                pinput, pre_of_col, dw_out_n, dx_lr_it, dt_ms: float, percise: bool,
                                                grad_scale: float = 1.0, eps: float = 1e-6,
                                                grad_l2norm_threshold: float = 1e6, clip_strategy: int = 1,
-                                               clip_check_every: int = 1) -> int:
+                                               clip_check_every: int = 1, noalloc: bool = False) -> int:
+        """noalloc: the entry point that allocates no device memory (its buffers come from the
+        library's fixed per-GPU scratch array; larger problems are refused)."""
         self._py_err = None
         it = _f32(it_lr_nt, 2)
         dv = _f32(ditdv_lr_nt, 2) if ditdv_lr_nt is not None else None
@@ -932,7 +937,9 @@ class Sim:
         if pre.size != N or dw.size != N or dx.shape != (pin.size, dl.shape[0]):
             return self._pyfail("replay_compute_dw_dx_from_signals_into: output shape mismatch")
         null = C.cast(None, _F)
-        return self._rc(lib().hx_replay_compute_dw_dx_from_signals_into(
+        fn = lib().hx_replay_compute_dw_dx_from_signals_into_noalloc if noalloc else \
+            lib().hx_replay_compute_dw_dx_from_signals_into
+        return self._rc(fn(
             self._h, _fp(it), _fp(dv) if dv is not None else null, _fp(dp) if dp is not None else null, N, T,
             _fp(dl), dl.shape[0], po.size, _ip(po), _ip(pin), pin.size, _ip(pre), _fp(dw), _fp(dx), dt_ms,
             int(bool(percise)), grad_scale, eps, grad_l2norm_threshold, int(clip_strategy), int(clip_check_every)))

@@ -343,6 +343,20 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
                                               int n_input, const int* pre_of_col, float* dw_out_n, float* dx_lr_it,
                                               double dt_ms, int percise, double grad_scale, double eps,
                                               double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
+/* No counterpart in the reference: hx_replay_compute_dw_dx_from_signals_into for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc).  Same arguments, checks and results;
+ * every device buffer (the signals, the dv/dw history ring, the per-tick vectors) is
+ * carved from one fixed 64 MiB device array that the library holds on each GPU it runs
+ * on until the process ends, so the call makes no hipMalloc/hipFree.  A problem whose
+ * buffers do not fit (about 8 (K_len + 1) N^2 + 16 N T bytes with percise) is refused
+ * with an error.  The dense blocks must already be set.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (from several threads) race. */
+int hx_replay_compute_dw_dx_from_signals_into_noalloc(
+    hx_sim* sim, const float* it_lr_nt, const float* ditdv_lr_nt, const float* ditdvpre_lr_nt, int N, int T,
+    const float* dLtdv_lr_to, int ksteps_total, int n_output, const int* poutput, const int* pinput, int n_input,
+    const int* pre_of_col, float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
+    double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
 /* LearnRuntime::simulate_and_replay_dw_dx_streaming_into (LearnRuntime.cpp:729-1288):
  * finitialize(v_init), ksteps_total * k_mul steps with the mapped channels captured every
  * k_mul steps into N columns, then the replay (cached clip schedule) into dw_out_n[N] and
