@@ -18,7 +18,7 @@ LIB = os.path.join(HERE, "libheliox_amd.so")
 ARCH = os.environ.get("HELIOX_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["kernels.hip", "adjoint.hip", "learn.hip", "learn_runtime.cpp", "runtime.cpp", "schedule.cpp",
-           "coredat.cpp"]
+           "coredat.cpp", "h5out.cpp"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 DEVICE = [f"--offload-arch={ARCH}", "-ffp-contract=off",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -52,7 +52,7 @@ def build(verbose: bool = True) -> str:
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp] + objs
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp] + objs + ["-ldl"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}{r.stderr}")

@@ -167,6 +167,7 @@ struct EventRing {
     int nslot;                    // power of two
     int cap;
     int* overflow;                // set to 1 when a slot overflowed
+    unsigned* done;               // workgroups of the delivery launch that have finished (then back to 0)
 };
 
 // Fan-out tables: source -> synapse targets (packed type|instance) with delays.
@@ -314,7 +315,7 @@ void launch_adj_gather(const double* tape_v, long long row, const int* nodes, in
 void launch_adam(const AdamArgs& a, hipStream_t s);
 void launch_spike(const SpikeArgs& a, hipStream_t s);
 void launch_input(const InputArgs& a, hipStream_t s);
-void launch_deliver(const DeliverArgs& a, hipStream_t s);
+void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s);
 void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s);
 void launch_vecplay_reset(VecPlayDev* items, int n, hipStream_t s);
 void launch_record(double* const* ptrs, int n, double* out, hipStream_t s);

@@ -976,29 +976,39 @@ __global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
     if (threadIdx.x == 0) *I.cursor = cur;
 }
 
+// NET_RECEIVE of the events of step k's ring slot (expsyn.cpp net_receive,
+// exp2syn_temp.cuh:62-67): ExpSyn g += w, Exp2Syn A, B += w factor, in any order
+// (fp64 atomics), as on the reference's GPU path.  The workgroups stride over the
+// slot, so a burst spreads over the chip; each counts itself done after its loop (which
+// used the count it read), and the last one empties the slot, so a second launch for
+// the same step (finitialize's, then the first step's) delivers only what was pushed
+// in between.
 __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
     const int slot = D.k & (D.ring.nslot - 1);
     int cnt = D.ring.count[slot];
     if (cnt > D.ring.cap) cnt = D.ring.cap;
     const long long off = static_cast<long long>(slot) * D.ring.cap;
-    for (int e = threadIdx.x; e < cnt; e += blockDim.x) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < cnt; e += gridDim.x * blockDim.x) {
         const int packed = D.ring.entry[off + e];
         const int type = packed >> 30;
         const int inst = packed & 0x3fffffff;
-        if (type == 0) {                        // ExpSyn: g += w (expsyn.cpp net_receive)
+        if (type == 0) {
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
             if (D.log) {
                 const int pos = atomicAdd(D.log_count, 1);
                 if (pos < D.log_cap) D.log[pos] = inst;
             }
-        } else {                                // Exp2Syn: A,B += w * factor
+        } else {
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
             atomicAdd(&D.e2.col(E2_A)[inst], wf);
             atomicAdd(&D.e2.col(E2_B)[inst], wf);
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) D.ring.count[slot] = 0;
+    if (threadIdx.x == 0 && (gridDim.x == 1 || atomicAdd(D.ring.done, 1u) == gridDim.x - 1)) {
+        D.ring.count[slot] = 0;
+        if (gridDim.x > 1) *D.ring.done = 0u;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1164,8 +1174,8 @@ void launch_input(const InputArgs& a, hipStream_t s) {
     if (a.n > 0) hipLaunchKernelGGL(k_input, dim3(1), dim3(kBlock), 0, s, a);
 }
 
-void launch_deliver(const DeliverArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_deliver, dim3(1), dim3(1024), 0, s, a);
+void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s) {
+    hipLaunchKernelGGL(k_deliver, dim3(std::max(1, nblk)), dim3(1024), 0, s, a);
 }
 
 void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s) {

@@ -125,6 +125,8 @@ SIGNATURES = {
         C.c_int, [_P, _F, C.c_int, C.c_int, _I, _I, C.c_int, C.c_int, _I, _F, _F, C.c_int, _I, _I, _F, C.c_int, _I,
                   _I, _F, C.c_int, _I, _I, _F, C.c_double, C.c_int, C.c_int, C.c_double, C.c_double, C.c_double,
                   C.c_double, C.c_double, C.c_int, C.c_int]),
+    "hx_set_hdf5_enabled": (C.c_int, [_P, C.c_int]),
+    "hx_is_hdf5_enabled": (C.c_int, [_P]),
     "hx_set_replay_timing": (C.c_int, [_P, C.c_int]),
     "hx_set_cell_groups": (C.c_int, [_P, C.c_int]),
     "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
@@ -519,6 +521,14 @@ class Sim:
 
     def is_spike_output_enabled(self) -> bool:
         return bool(lib().hx_is_spike_output_enabled(self._h))
+
+    def set_hdf5_enabled(self, enable: bool) -> int:
+        """Monitor samples to <output_dir>/sim_out.h5 at /group_0/<mech>/<var>/<idx>
+        (created at the next finitialize, appended by every run call)."""
+        return self._rc(lib().hx_set_hdf5_enabled(self._h, int(bool(enable))))
+
+    def is_hdf5_enabled(self) -> bool:
+        return bool(lib().hx_is_hdf5_enabled(self._h))
 
     def set_output_dir(self, dir: str) -> int:
         return self._rc(lib().hx_set_output_dir(self._h, _b(dir)))

@@ -145,6 +145,19 @@ int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap);
  * ordered by time and then gid; spikes of negative gids are left out. */
 int hx_output_spikes(hx_sim* sim, const char* folder);
 
+/* Monitor output to <output_dir>/sim_out.h5 (the reference's recorder file:
+ * SimRuntimeCore's enable_hdf5 / main.cpp's watch points select BufferEnable::HDF5,
+ * SimRuntimeCore.cpp:125-128; layout simulate.cpp:185-269; append on flush
+ * variable_recorder.h:142-156).  Enabled, the file is created (truncated) at the next
+ * hx_finitialize with the group /group_0, and every call that brings monitor samples
+ * back (run, continue_run, fadvance, flush_recorders, finitialize) appends them to the
+ * dataset /group_0/<mech>/<var>/<idx> of each monitor: double, one dimension,
+ * unlimited, chunks of 100.  Later hx_finitialize calls keep appending to the same
+ * file, as the reference's recorder does.  The HDF5 C library (1.10 or later) is
+ * loaded at run time; without it enabling fails and nothing else changes.  Default: off. */
+int hx_set_hdf5_enabled(hx_sim* sim, int enable);
+int hx_is_hdf5_enabled(hx_sim* sim);
+
 /* spk.dat after every hx_run / hx_continue_run (SimWrapper::run, continue_run,
  * SimWrapper.cpp:46-84; set_spike_output_enabled, set_output_dir).  Default: off, folder
  * "output" (simulate.cpp:30). */
