@@ -1,7 +1,9 @@
 // Adjoint (vector-Jacobian) backward step of the fixed-step simulation, for
-// models made of pas, hh, ExpSyn (+ ions with fixed reversal potentials and
-// IClamp).  No reference code exists for this; it differentiates the step the
-// forward kernels take (simulate.cpp:410-442 order).
+// models made of pas, hh, Ca_HVA, hd_la (Ih), CaDynamics_E2, ExpSyn, Exp2Syn,
+// IClamp and the ions (na, k with fixed reversal potentials; ca with a fixed
+// eca or eca from cai by the Nernst equation every step).  No reference code
+// exists for this; it differentiates the step the forward kernels take
+// (simulate.cpp:410-442 order).
 //
 // Step n maps (v^n, x^n, g^n) to (v^{n+1}, x^{n+1}, g^{n+1}):
 //   g_eff = g^n + sum of the weights delivered at step n         (ExpSyn)
@@ -19,6 +21,20 @@
 // functions) to lambda_v^{n+1} before the solve.  M^T is solved with the same
 // tree kernel by swapping a and b and correcting the diagonal (the kernel
 // assembles it from a and b).
+//
+// Calcium.  Ca_HVA's current is g (v - eca) with g = gbar m^2 h and eca =
+// (ktf / 2) ln(cao / cai^n) (ion style 0100) or fixed.  CaDynamics_E2 then takes
+//   cai^{n+1} = cai^n + (1 - e)(decay drive(ica^n) + minCai - cai^n),
+//   e = exp(-dt / decay), drive = -1e4 ica gamma / (2 F depth),
+// with ica^n = g (v^n - eca) at the voltage of step n's current pass.  So
+//   lambda_cai^n = e lambda_cai^{n+1} + (terms through eca),
+//   lambda_ica^n = (1 - e) decay (-1e4 gamma / (2 F depth)) lambda_cai^{n+1},
+// and lambda_ica^n reaches v^n, the Ca_HVA gates, gbar and (through eca) cai^n.
+// Through the solve, eca enters like any reversal potential: d/dcai of G E.
+//
+// Exp2Syn: g = B_eff - A_eff (events add w factor to both), A and B decay by
+// exp(-dt / tau1), exp(-dt / tau2) after the solve; a delivered event's weight
+// gets factor (lambda_A + lambda_B).
 #include "hx_internal.h"
 #include "mech_math.h"
 
@@ -59,6 +75,60 @@ __global__ void k_adj_syn_state(AdjStep A) {
     A.lam_g[j] = exp(-A.dt / m.col(ES_TAU)[j]) * A.lam_g[j];
 }
 
+// Ca_HVA gates (cnexp at v^{n+1}): lambda_x <- exp(-dt/tau) lambda_x, lambda_v += dx/dv lambda_x
+__global__ void k_adj_cahva_state(AdjStep A) {
+    const MechDev& m = A.m[M_CAHVA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const Dual v1{A.v1[node], 1.0};
+    Dual mInf, mTau, hInf, hTau;
+    cahva_rates_t(v1, mInf, mTau, hInf, hTau);
+    const Dual mn = cnexp_t(A.c0[j], mInf, mTau, A.dt);
+    const Dual hn = cnexp_t(A.c0[A.cstride + j], hInf, hTau, A.dt);
+    const double lm = A.lam_c[j], lh = A.lam_c[A.cstride + j];
+    A.lam_v[node] += mn.d * lm + hn.d * lh;
+    A.lam_c[j] = exp(-A.dt / mTau.v) * lm;
+    A.lam_c[A.cstride + j] = exp(-A.dt / hTau.v) * lh;
+}
+
+// hd_la gate
+__global__ void k_adj_hdla_state(AdjStep A) {
+    const MechDev& m = A.m[M_HDLA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const Dual v1{A.v1[node], 1.0};
+    Dual linf, taul;
+    hdla_rate_t(v1, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
+    const Dual ln = cnexp_t(A.l0[j], linf, taul, A.dt);
+    const double ll = A.lam_l[j];
+    A.lam_v[node] += ln.d * ll;
+    A.lam_l[j] = exp(-A.dt / taul.v) * ll;
+}
+
+// CaDynamics_E2: lambda_ica^n from lambda_cai^{n+1}, then lambda_cai^n <- e lambda_cai^{n+1}
+__global__ void k_adj_cadyn(AdjStep A) {
+    const MechDev& m = A.m[M_CADYN];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int ci = ion_of(m, 2, j);
+    const double decay = m.col(CD_DECAY)[j];
+    const double e = exp(A.dt * (-1.0 / decay));
+    const double lc = A.lam_cai[ci];
+    A.lam_ica[ci] = (1.0 - e) * decay * (-(10000.0) * m.col(CD_GAMMA)[j] / (2.0 * kFaradayCaDyn * m.col(CD_DEPTH)[j])) * lc;
+    A.lam_cai[ci] = e * lc;
+}
+
+// Exp2Syn decay: lambda_{A,B eff} = exp(-dt/tau_{1,2}) lambda_{A,B}
+__global__ void k_adj_syn2_state(AdjStep A) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    A.lam_ab[j] *= exp(A.dt * (-1.0 / m.col(E2_TAU1)[j]));
+    A.lam_ab[m.n + j] *= exp(A.dt * (-1.0 / m.col(E2_TAU2)[j]));
+}
+
 // transposed system: d = C + delta, rhs = lambda_v, v = 0
 __global__ void k_adj_assemble(AdjStep A) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -83,6 +153,32 @@ __global__ void k_adj_cond_hh(AdjStep A) {
     const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
     A.dT[m.node[j]] += m.col(HH_GNABAR)[j] * mm * mm * mm * hh + m.col(HH_GKBAR)[j] * nn * nn * nn * nn +
                        m.col(HH_GL)[j];
+}
+
+__global__ void k_adj_cond_cahva(AdjStep A) {
+    const MechDev& m = A.m[M_CAHVA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
+    A.dT[m.node[j]] += m.col(CH_GBAR)[j] * mm * mm * hh;
+}
+
+__global__ void k_adj_cond_hdla(AdjStep A) {
+    const MechDev& m = A.m[M_HDLA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    A.dT[m.node[j]] += m.col(HD_GHDBAR)[j] * A.l0[j];
+}
+
+// Exp2Syn grouped by node: sum of (B_eff - A_eff) x 1e2/area
+__global__ void k_adj_cond_syn2(AdjStep A) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= m.ngrp) return;
+    const int node = m.grp_node[q];
+    double g = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.ab0[m.n + j] - A.ab0[j];
+    A.dT[node] += g * (1.e2 / A.area[node]);
 }
 
 // synapses grouped by node: sum of g_eff x 1e2/area
@@ -128,6 +224,74 @@ __global__ void k_adj_pas_param(AdjStep A) {
     A.grad_gpas[j] -= A.mu[node] * (A.v1[node] - m.col(PAS_E)[j]);
 }
 
+// eca of step n at ca_ion instance ci and d eca / d cai (0 where eca is fixed)
+__device__ __forceinline__ double eca_of(const AdjStep& A, int ci, double& deca) {
+    const MechDev& ca = A.m[M_CA_ION];
+    if (ca.iontype[ci] & 0100) {
+        const double c = A.cai0[ci];
+        deca = -A.c.ktf / 2.0 / c;
+        return nernst(c, ca.col(ION_CONCO)[ci], 2.0, A.c.ktf);
+    }
+    deca = 0.0;
+    return ca.col(ION_EREV)[ci];
+}
+
+// Ca_HVA: through the solve (at v^{n+1}) and through the ica CaDynamics_E2 read (at v^n)
+__global__ void k_adj_cahva_param(AdjStep A) {
+    const MechDev& m = A.m[M_CAHVA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const int ci = ion_of(m, 2, j);
+    double deca;
+    const double eca = eca_of(A, ci, deca);
+    const double gbar = m.col(CH_GBAR)[j];
+    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
+    const double g = gbar * mm * mm * hh;
+    // solve: dL/dq += -mu dG/dq (v^{n+1} - eca) + mu G deca/dq
+    const double mu = A.mu[node];
+    const double d1 = A.v1[node] - eca;
+    double lm = -mu * 2.0 * gbar * mm * hh * d1;
+    double lh = -mu * gbar * mm * mm * d1;
+    double gg = -mu * mm * mm * hh * d1;
+    double lcai = mu * g * deca;
+    // ica^n = G (v^n - eca): its adjoint from CaDynamics_E2
+    const double li = A.lam_ica ? A.lam_ica[ci] : 0.0;
+    if (li != 0.0) {
+        const double d0 = A.v0[node] - eca;
+        A.lam_v_new[node] += g * li;
+        lm += 2.0 * gbar * mm * hh * d0 * li;
+        lh += gbar * mm * mm * d0 * li;
+        gg += mm * mm * hh * d0 * li;
+        lcai -= g * deca * li;
+    }
+    A.lam_c[j] += lm;
+    A.lam_c[A.cstride + j] += lh;
+    A.grad_cgbar[j] += gg;
+    if (A.lam_cai) A.lam_cai[ci] += lcai;
+}
+
+__global__ void k_adj_hdla_param(AdjStep A) {
+    const MechDev& m = A.m[M_HDLA];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const double mu = A.mu[node], d1 = A.v1[node] - A.c.hd_ehd;
+    A.lam_l[j] -= mu * m.col(HD_GHDBAR)[j] * d1;
+    A.grad_ghdbar[j] -= mu * A.l0[j] * d1;
+}
+
+// Exp2Syn: lambda_{A,eff} += mu (v^{n+1} - e) 1e2/area, lambda_{B,eff} -= the same
+__global__ void k_adj_syn2_param(AdjStep A) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const double t = A.mu[node] * (A.v1[node] - m.col(E2_E)[j]) * (1.e2 / A.area[node]);
+    A.lam_ab[j] += t;
+    A.lam_ab[m.n + j] -= t;
+}
+
 // lambda_geff += -mu (v^{n+1} - e) 1e2/area
 __global__ void k_adj_syn_param(AdjStep A) {
     const MechDev& m = A.m[M_EXPSYN];
@@ -137,12 +301,19 @@ __global__ void k_adj_syn_param(AdjStep A) {
     A.lam_g[j] -= A.mu[node] * (A.v1[node] - m.col(ES_E)[j]) * (1.e2 / A.area[node]);
 }
 
-// events delivered at step n: dL/dw += lambda_geff (one block)
+// events delivered at step n: ExpSyn dL/dw += lambda_geff, Exp2Syn dL/dw += factor
+// (lambda_A + lambda_B) (one block)
 __global__ void __launch_bounds__(256) k_adj_events(AdjStep A) {
     const int cnt = A.ev_count[0];
     for (int e = threadIdx.x; e < cnt; e += blockDim.x) {
-        const int inst = A.ev[e];
-        atomicAdd(&A.grad_w[inst], A.lam_g[inst]);
+        const int packed = A.ev[e];
+        const int inst = packed & 0x3fffffff;
+        if ((packed >> 30) == 0) {
+            atomicAdd(&A.grad_w[inst], A.lam_g[inst]);
+        } else {
+            const MechDev& m = A.m[M_EXP2SYN];
+            atomicAdd(&A.grad_w2[inst], m.col(E2_FACTOR)[inst] * (A.lam_ab[inst] + A.lam_ab[m.n + inst]));
+        }
     }
 }
 
@@ -203,24 +374,39 @@ inline dim3 grid_of(long long n, int block = kBlock) {
 
 }  // namespace
 
+// Kernels of one mechanism touch only that mechanism's adjoints, except for the
+// per-node lambda_v and d (one density instance per node; point processes go by
+// node groups) and lambda_cai / lambda_ica (one CaDynamics_E2 per ca_ion instance,
+// written by it before the solve and by Ca_HVA after), so no two launches race.
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
     if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_state, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cahva_state, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_hdla_state, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_CADYN].n > 0) hipLaunchKernelGGL(k_adj_cadyn, grid_of(a.m[M_CADYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXP2SYN].n > 0)
+        hipLaunchKernelGGL(k_adj_syn2_state, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
     hipLaunchKernelGGL(k_adj_assemble, grid_of(a.N), dim3(kBlock), 0, s, a);
     if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
     if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_cond_hh, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cond_cahva, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_cond_hdla, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].ngrp > 0)
         hipLaunchKernelGGL(k_adj_cond_syn, grid_of(a.m[M_EXPSYN].ngrp), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXP2SYN].ngrp > 0)
+        hipLaunchKernelGGL(k_adj_cond_syn2, grid_of(a.m[M_EXP2SYN].ngrp), dim3(kBlock), 0, s, a);
 }
 
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
     hipLaunchKernelGGL(k_adj_node, grid_of(a.N), dim3(kBlock), 0, s, a);
     if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
     if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXPSYN].n > 0) {
-        hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
-        hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
-    }
+    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cahva_param, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_hdla_param, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXP2SYN].n > 0)
+        hipLaunchKernelGGL(k_adj_syn2_param, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
+    if (a.m[M_EXPSYN].n > 0 || a.m[M_EXP2SYN].n > 0) hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
 }
 
 void launch_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale, double* lam,

@@ -219,7 +219,7 @@ struct DeliverArgs {
     MechDev e2;                   // Exp2Syn
     const double* es_weight;
     const double* e2_weight;
-    int* log_count;               // when set: ExpSyn instances receiving an event are appended
+    int* log_count;               // when set: every delivered event (packed as in the ring) is appended
     int* log;                     // to log[0 .. *log_count) (capacity log_cap), for the adjoint
     int log_cap;
 };
@@ -229,6 +229,7 @@ struct DeliverArgs {
 struct AdjStep {
     int N;
     double dt, cfac, hh_q10;
+    MechConsts c;
     const double* cm;
     const double* area;
     const double* delta;          // diagonal correction of the transposed solve
@@ -250,7 +251,22 @@ struct AdjStep {
     double* grad_gpas;
     double* grad_w;               // ExpSyn netcon weights
     const int* ev_count;          // events delivered at step n
-    const int* ev;
+    const int* ev;                // packed (type << 30) | instance, as in the event ring
+    // Ca_HVA, hd_la, CaDynamics_E2 (+ ca_ion) and Exp2Syn
+    const double* v0;             // v^n, the voltage of step n's current pass (ica uses it)
+    const double* c0;             // Ca_HVA m^n, h^n (2 columns of cstride)
+    long long cstride;
+    double* lam_c;                // adjoint of the Ca_HVA gates
+    const double* l0;             // hd_la l^n
+    double* lam_l;
+    const double* cai0;           // cai^n per ca_ion instance
+    double* lam_cai;              // adjoint of cai (cai^{n+1} in, cai^n out)
+    double* lam_ica;              // per ca_ion instance: adjoint of the ica that CaDynamics_E2 reads
+    const double* ab0;            // Exp2Syn A_eff^n, B_eff^n (2 columns of the instance count)
+    double* lam_ab;               // adjoint of A, B (step n+1 in, step n out)
+    double* grad_cgbar;           // Ca_HVA gbar
+    double* grad_ghdbar;          // hd_la ghdbar
+    double* grad_w2;              // Exp2Syn netcon weights
 };
 
 // Adam over tied parameter groups (optimizer.cpp:351-393): group g covers

@@ -994,14 +994,14 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
         const int inst = packed & 0x3fffffff;
         if (type == 0) {
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
-            if (D.log) {
-                const int pos = atomicAdd(D.log_count, 1);
-                if (pos < D.log_cap) D.log[pos] = inst;
-            }
         } else {
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
             atomicAdd(&D.e2.col(E2_A)[inst], wf);
             atomicAdd(&D.e2.col(E2_B)[inst], wf);
+        }
+        if (D.log) {          // the adjoint's record of the step's deliveries (packed as in the ring)
+            const int pos = atomicAdd(D.log_count, 1);
+            if (pos < D.log_cap) D.log[pos] = packed;
         }
     }
     __syncthreads();

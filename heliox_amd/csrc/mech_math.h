@@ -132,6 +132,41 @@ __device__ __forceinline__ void hdla_rate(double v, double vhalfl, double tau, c
     taul = tau * bett / (c.hd_qtl * c.hd_qt * c.hd_a0t * (1.0 + a));
 }
 
+// Reference forms as templates, for the adjoint: evaluated on dual numbers they
+// give d/dv of exactly these formulas (CA_HVA.cu:97-113, hd_la.cu:80-101, the
+// cnexp updates CA_HVA.cu:170-177 and hd_la.cu:123-127).
+template <class T>
+__device__ __forceinline__ T cahva_vtrap_t(T x, double y) {
+    if (fabs(value_of(x) / y) < 1e-6) return y * (1.0 - x / y / 2.0);
+    else return x / (exp(x / y) - 1.0);
+}
+
+template <class T>
+__device__ __forceinline__ void cahva_rates_t(T volt, T& mInf, T& mTau, T& hInf, T& hTau) {
+    const T mAlpha = 0.055 * cahva_vtrap_t(-27.0 - volt, 3.8);
+    const T mBeta = 0.94 * exp((-75.0 - volt) / 17.0);
+    mInf = mAlpha / (mAlpha + mBeta);
+    mTau = 1.0 / (mAlpha + mBeta);
+    const T hAlpha = 0.000457 * exp((-13.0 - volt) / 50.0);
+    const T hBeta = 0.0065 / (exp((-volt - 15.0) / 28.0) + 1.0);
+    hInf = hAlpha / (hAlpha + hBeta);
+    hTau = 1.0 / (hAlpha + hBeta);
+}
+
+template <class T>
+__device__ __forceinline__ void hdla_rate_t(T v, double vhalfl, double tau, const MechConsts& c, T& linf, T& taul) {
+    const T a = exp(0.0378 * c.hd_zetat * (v - c.hd_vhalft));
+    linf = 1.0 / (1.0 + exp(-(v - vhalfl) / c.hd_kl));
+    const T bett = exp(0.0378 * c.hd_zetat * c.hd_gmt * (v - c.hd_vhalft));
+    taul = tau * bett / (c.hd_qtl * c.hd_qt * c.hd_a0t * (1.0 + a));
+}
+
+// x + (1 - exp(-dt / tau)) (inf - x)
+template <class T>
+__device__ __forceinline__ T cnexp_t(double x, T inf, T tau, double dt) {
+    return x + (1.0 - exp(-dt / tau)) * (inf - x);
+}
+
 // ---------------- CaDynamics_E2 ----------------
 __device__ __forceinline__ double cadyn_step(double cai, double ica, double gamma, double decay, double depth,
                                              double minCai, double dt) {

@@ -192,6 +192,25 @@ enum TimerId { T_MECH = 0, T_SPARSE, T_POINT, T_SOLVE, T_SPIKE, T_EVENTS, T_OTHE
 
 }  // namespace
 
+// Parameters the adjoint differentiates: a mechanism's parameter column, or the
+// weight of the netcon into a synapse instance.  Their gradients are addressable
+// as variables "grad_<var>" of the mechanism (and "grad_weight").
+struct Trainable {
+    int mech;
+    const char* var;
+};
+constexpr int kNumTrainable = 7;
+constexpr Trainable kTrainable[kNumTrainable] = {
+    {M_HH, "gnabar"}, {M_HH, "gkbar"}, {M_PAS, "g_pas"}, {M_EXPSYN, "weight"},
+    {M_CAHVA, "gbar"}, {M_HDLA, "ghdbar"}, {M_EXP2SYN, "weight"}};
+enum TrainableId { T_GNABAR = 0, T_GKBAR, T_GPAS, T_WES, T_CGBAR, T_GHDBAR, T_WE2 };
+
+inline int trainable_id(int mech, const std::string& var) {
+    for (int k = 0; k < kNumTrainable; ++k)
+        if (kTrainable[k].mech == mech && var == kTrainable[k].var) return k;
+    return -1;
+}
+
 struct hx_sim {
     std::string err;
     double dt = 0.025;
@@ -347,9 +366,10 @@ struct hx_sim {
     bool state_pending = false;
     bool final_step = false;   // the last step of a run call also stores every assigned variable
     bool initialized = false;
-    // adjoint tape (hx_tape_begin): row n holds v^{n+1} (after step n's solve), the
-    // hh gates x^n and ExpSyn g_eff^n that step n used, and the ExpSyn instances
-    // that received events at step n
+    // adjoint tape (hx_tape_begin): row n holds v^{n+1} (after step n's solve); the
+    // states step n's current pass used: hh, Ca_HVA and hd_la gates, cai per ca_ion
+    // instance, ExpSyn g_eff and Exp2Syn A_eff, B_eff (events of the step included);
+    // and the synapse instances that received events at step n.  v^0 is kept apart.
     bool tape_on = false;
     int tape_cap = 0, tape_n = 0, tape_evcap = 0;
     double *d_tape_v = nullptr, *d_tape_x = nullptr, *d_tape_g = nullptr;
@@ -357,7 +377,12 @@ struct hx_sim {
     // adjoint work arrays and per-instance gradients (hx_adjoint)
     double *d_adj_delta = nullptr, *d_lv = nullptr, *d_lv2 = nullptr, *d_lx = nullptr, *d_lg = nullptr,
            *d_dT = nullptr, *d_rhsT = nullptr, *d_vT = nullptr, *d_wT = nullptr;
-    double *d_grad_gnabar = nullptr, *d_grad_gkbar = nullptr, *d_grad_gpas = nullptr, *d_grad_w = nullptr;
+    // per-instance gradients of the trainable parameters (kTrainable order)
+    double* d_grad[kNumTrainable] = {};
+    // extra tape rows and adjoint work arrays of Ca_HVA, hd_la, CaDynamics_E2 and Exp2Syn
+    double *d_tape_v0 = nullptr, *d_tape_c = nullptr, *d_tape_l = nullptr, *d_tape_cai = nullptr,
+           *d_tape_ab = nullptr;
+    double *d_lc = nullptr, *d_ll = nullptr, *d_lcai = nullptr, *d_lica = nullptr, *d_lab = nullptr;
     bool have_grad = false;
     bool adj_delta_dirty = true;
     struct AdamHost {
@@ -399,9 +424,12 @@ struct hx_sim {
     int opt_add_group(int opt, const std::vector<double*>& w, const std::vector<double*>& g, double impedance);
     void tape_free() {
         for (void* p : {static_cast<void*>(d_tape_v), static_cast<void*>(d_tape_x), static_cast<void*>(d_tape_g),
-                        static_cast<void*>(d_tape_evn), static_cast<void*>(d_tape_ev)})
+                        static_cast<void*>(d_tape_evn), static_cast<void*>(d_tape_ev), static_cast<void*>(d_tape_v0),
+                        static_cast<void*>(d_tape_c), static_cast<void*>(d_tape_l), static_cast<void*>(d_tape_cai),
+                        static_cast<void*>(d_tape_ab)})
             if (p) (void)hipFree(p);
         d_tape_v = d_tape_x = d_tape_g = nullptr;
+        d_tape_v0 = d_tape_c = d_tape_l = d_tape_cai = d_tape_ab = nullptr;
         d_tape_evn = d_tape_ev = nullptr;
         tape_cap = 0;
     }
@@ -1364,15 +1392,11 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     }
     // gradients of the adjoint (grad_<parameter>) and netcon weights, addressable by
     // handles so optimizers can be given (weight, gradient) pairs
-    if ((id == M_HH && (var == "grad_gnabar" || var == "grad_gkbar")) || (id == M_PAS && var == "grad_g_pas") ||
-        (id == M_EXPSYN && var == "grad_weight")) {
-        if (idx < 0 || idx >= m.n) return r;
+    if (var.compare(0, 5, "grad_") == 0) {
+        const int tk = trainable_id(id, var.substr(5));
+        if (tk < 0 || idx < 0 || idx >= m.n) return r;
         ensure_grad_arrays();
-        double* base = var == "grad_gnabar" ? d_grad_gnabar
-                       : var == "grad_gkbar" ? d_grad_gkbar
-                       : var == "grad_g_pas" ? d_grad_gpas
-                                             : d_grad_w;
-        r.dev = base + m.perm[idx];
+        r.dev = d_grad[tk] + m.perm[idx];
         return r;
     }
     if ((id == M_EXPSYN || id == M_EXP2SYN) && var == "weight") {
@@ -1664,6 +1688,27 @@ void hx_sim::tape_record() {
         const MechDev& e = mech[M_EXPSYN].dev;
         HXC(hipMemcpyAsync(d_tape_g + n * e.n, e.col(ES_G), sizeof(double) * e.n, hipMemcpyDeviceToDevice,
                            stream));
+    }
+    if (d_tape_c) {            // Ca_HVA m, h are consecutive columns
+        const MechDev& c = mech[M_CAHVA].dev;
+        HXC(hipMemcpyAsync(d_tape_c + n * 2 * c.stride, c.col(CH_M), sizeof(double) * 2 * c.stride,
+                           hipMemcpyDeviceToDevice, stream));
+    }
+    if (d_tape_l) {
+        const MechDev& h = mech[M_HDLA].dev;
+        HXC(hipMemcpyAsync(d_tape_l + n * h.n, h.col(HD_L), sizeof(double) * h.n, hipMemcpyDeviceToDevice, stream));
+    }
+    if (d_tape_cai) {
+        const MechDev& ca = mech[M_CA_ION].dev;
+        HXC(hipMemcpyAsync(d_tape_cai + n * ca.n, ca.col(ION_CONCI), sizeof(double) * ca.n,
+                           hipMemcpyDeviceToDevice, stream));
+    }
+    if (d_tape_ab) {
+        const MechDev& e = mech[M_EXP2SYN].dev;
+        HXC(hipMemcpyAsync(d_tape_ab + n * 2 * e.n, e.col(E2_A), sizeof(double) * e.n, hipMemcpyDeviceToDevice,
+                           stream));
+        HXC(hipMemcpyAsync(d_tape_ab + (n * 2 + 1) * e.n, e.col(E2_B), sizeof(double) * e.n,
+                           hipMemcpyDeviceToDevice, stream));
     }
     ++tape_n;
 }
@@ -2035,6 +2080,8 @@ void hx_sim::finitialize(double v_init) {
         launch_clear_ints(d_tape_evn, tape_cap, stream);
     }
     launch_set_v(d_v, nnode, v_init, stream);
+    if (tape_on)
+        HXC(hipMemcpyAsync(d_tape_v0, d_v, sizeof(double) * nnode, hipMemcpyDeviceToDevice, stream));
     launch_gap_transfers();
     StepArgs A = step_args(0.0, 0, 0);
     for (int id = 0; id < M_COUNT; ++id)           // CoreNEURON order, ions before their users
@@ -3098,10 +3145,8 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
     const auto& R = registry();
     for (int id = 0; id < M_COUNT; ++id) {
         if (!sim->mech[id].present) continue;
-        if (id != M_PAS && id != M_NA_ION && id != M_K_ION && id != M_HH && id != M_ICLAMP && id != M_EXPSYN &&
-            id != M_VECSTIM && id != M_NETSTIM)
-            return sim->fail("the adjoint supports pas, hh, ExpSyn, IClamp, VecStim, NetStim and the na/k ions; "
-                             "the model has %s", R[id].name);
+        if (id == M_HALFGAP)
+            return sim->fail("the adjoint does not support gap junctions (the model has %s)", R[id].name);
     }
     for (int x : {M_NA_ION, M_K_ION})
         if (sim->mech[x].present)
@@ -3112,6 +3157,12 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
     sim->tape_free();
     const size_t cap = static_cast<size_t>(max_steps);
     HXC(hipMalloc(&sim->d_tape_v, sizeof(double) * cap * sim->nnode));
+    HXC(hipMalloc(&sim->d_tape_v0, sizeof(double) * sim->nnode));
+    auto has = [&](int id) { return sim->mech[id].present && sim->mech[id].n > 0; };
+    if (has(M_CAHVA)) HXC(hipMalloc(&sim->d_tape_c, sizeof(double) * cap * 2 * sim->mech[M_CAHVA].dev.stride));
+    if (has(M_HDLA)) HXC(hipMalloc(&sim->d_tape_l, sizeof(double) * cap * sim->mech[M_HDLA].n));
+    if (has(M_CA_ION)) HXC(hipMalloc(&sim->d_tape_cai, sizeof(double) * cap * sim->mech[M_CA_ION].n));
+    if (has(M_EXP2SYN)) HXC(hipMalloc(&sim->d_tape_ab, sizeof(double) * cap * 2 * sim->mech[M_EXP2SYN].n));
     if (sim->mech[M_HH].present && sim->mech[M_HH].n > 0)
         HXC(hipMalloc(&sim->d_tape_x, sizeof(double) * cap * 3 * sim->mech[M_HH].dev.stride));
     if (sim->mech[M_EXPSYN].present && sim->mech[M_EXPSYN].n > 0)
@@ -3171,6 +3222,15 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         const HostMech& pas = sim->mech[M_PAS];
         sim->d_lx = dalloc<double>(owned, std::max<long long>(1, 3 * (hh.present ? hh.dev.stride : 0)));
         sim->d_lg = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
+        auto cnt = [&](int id, long long per) {
+            const HostMech& m = sim->mech[id];
+            return std::max<long long>(1, m.present ? per : 0);
+        };
+        sim->d_lc = dalloc<double>(owned, cnt(M_CAHVA, 2 * sim->mech[M_CAHVA].dev.stride));
+        sim->d_ll = dalloc<double>(owned, cnt(M_HDLA, sim->mech[M_HDLA].n));
+        sim->d_lcai = dalloc<double>(owned, cnt(M_CA_ION, sim->mech[M_CA_ION].n));
+        sim->d_lica = dalloc<double>(owned, cnt(M_CA_ION, sim->mech[M_CA_ION].n));
+        sim->d_lab = dalloc<double>(owned, cnt(M_EXP2SYN, 2 * static_cast<long long>(sim->mech[M_EXP2SYN].n)));
         sim->ensure_grad_arrays();
     }
     if (!sim->d_adj_delta || sim->adj_delta_dirty) {
@@ -3194,10 +3254,23 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     HXC(hipMemsetAsync(sim->d_lv, 0, sizeof(double) * N, st));
     HXC(hipMemsetAsync(sim->d_lx, 0, sizeof(double) * std::max<long long>(1, 3 * xs), st));
     HXC(hipMemsetAsync(sim->d_lg, 0, sizeof(double) * std::max(1, es.present ? es.n : 0), st));
-    HXC(hipMemsetAsync(sim->d_grad_gnabar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0), st));
-    HXC(hipMemsetAsync(sim->d_grad_gkbar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0), st));
-    HXC(hipMemsetAsync(sim->d_grad_gpas, 0, sizeof(double) * std::max(1, pas.present ? pas.n : 0), st));
-    HXC(hipMemsetAsync(sim->d_grad_w, 0, sizeof(double) * std::max(1, es.present ? es.n : 0), st));
+    (void)pas;
+    for (int k = 0; k < kNumTrainable; ++k) {
+        const HostMech& m = sim->mech[kTrainable[k].mech];
+        HXC(hipMemsetAsync(sim->d_grad[k], 0, sizeof(double) * std::max(1, m.present ? m.n : 0), st));
+    }
+    const HostMech& cah = sim->mech[M_CAHVA];
+    const HostMech& hdl = sim->mech[M_HDLA];
+    const HostMech& cai = sim->mech[M_CA_ION];
+    const HostMech& e2 = sim->mech[M_EXP2SYN];
+    const bool with_c = cah.present && cah.n > 0, with_l = hdl.present && hdl.n > 0;
+    const bool with_ca = cai.present && cai.n > 0, with_e2 = e2.present && e2.n > 0;
+    const long long cs = with_c ? cah.dev.stride : 0;
+    HXC(hipMemsetAsync(sim->d_lc, 0, sizeof(double) * std::max<long long>(1, 2 * cs), st));
+    HXC(hipMemsetAsync(sim->d_ll, 0, sizeof(double) * std::max(1, with_l ? hdl.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_lcai, 0, sizeof(double) * std::max(1, with_ca ? cai.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_lica, 0, sizeof(double) * std::max(1, with_ca ? cai.n : 0), st));
+    HXC(hipMemsetAsync(sim->d_lab, 0, sizeof(double) * std::max(1, with_e2 ? 2 * e2.n : 0), st));
     const StepArgs SA = sim->step_args(sim->t, 0, 0);
     AdjStep A{};
     A.N = N;
@@ -3215,10 +3288,20 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.rhsT = sim->d_rhsT;
     A.vT = sim->d_vT;
     A.mu = sim->d_rhsT;
-    A.grad_gnabar = sim->d_grad_gnabar;
-    A.grad_gkbar = sim->d_grad_gkbar;
-    A.grad_gpas = sim->d_grad_gpas;
-    A.grad_w = sim->d_grad_w;
+    A.grad_gnabar = sim->d_grad[T_GNABAR];
+    A.grad_gkbar = sim->d_grad[T_GKBAR];
+    A.grad_gpas = sim->d_grad[T_GPAS];
+    A.grad_w = sim->d_grad[T_WES];
+    A.c = SA.c;
+    A.cstride = cs;
+    A.lam_c = sim->d_lc;
+    A.lam_l = sim->d_ll;
+    A.lam_cai = with_ca ? sim->d_lcai : nullptr;
+    A.lam_ica = (with_ca && sim->mech[M_CADYN].present && sim->mech[M_CADYN].n > 0) ? sim->d_lica : nullptr;
+    A.lam_ab = sim->d_lab;
+    A.grad_cgbar = sim->d_grad[T_CGBAR];
+    A.grad_ghdbar = sim->d_grad[T_GHDBAR];
+    A.grad_w2 = sim->d_grad[T_WE2];
     SolveArgs S{};
     S.nunit = sim->nunit;
     S.unit_node_begin = sim->d_unit_node_begin;
@@ -3244,6 +3327,11 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         A.geff = sim->d_tape_g ? sim->d_tape_g + static_cast<size_t>(n) * es.n : nullptr;
         A.ev_count = sim->d_tape_evn + n;
         A.ev = sim->d_tape_ev + static_cast<size_t>(n) * sim->tape_evcap;
+        A.v0 = n >= 1 ? sim->d_tape_v + (n - 1) * row : sim->d_tape_v0;
+        A.c0 = with_c ? sim->d_tape_c + static_cast<size_t>(n) * 2 * cs : nullptr;
+        A.l0 = with_l ? sim->d_tape_l + static_cast<size_t>(n) * hdl.n : nullptr;
+        A.cai0 = with_ca ? sim->d_tape_cai + static_cast<size_t>(n) * cai.n : nullptr;
+        A.ab0 = with_e2 ? sim->d_tape_ab + static_cast<size_t>(n) * 2 * e2.n : nullptr;
         A.lam_v = lv;
         A.lam_v_new = lv2;
         launch_adj_before_solve(A, st);
@@ -3265,13 +3353,10 @@ int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out,
     API_BEGIN
     if (!sim->have_grad) return sim->fail("no gradients (call hx_adjoint)");
     const std::string mn = mech ? mech : "", vn = var ? var : "";
-    double* src = nullptr;
-    int id = -1;
-    if (mn == "hh" && vn == "gnabar") { src = sim->d_grad_gnabar; id = M_HH; }
-    else if (mn == "hh" && vn == "gkbar") { src = sim->d_grad_gkbar; id = M_HH; }
-    else if (mn == "pas" && vn == "g_pas") { src = sim->d_grad_gpas; id = M_PAS; }
-    else if (mn == "ExpSyn" && vn == "weight") { src = sim->d_grad_w; id = M_EXPSYN; }
-    if (!src || !sim->mech[id].present) return sim->fail("no gradient for %s.%s", mn.c_str(), vn.c_str());
+    const int id = mech_id(mn);
+    const int tk = id < 0 ? -1 : trainable_id(id, vn);
+    if (tk < 0 || !sim->mech[id].present) return sim->fail("no gradient for %s.%s", mn.c_str(), vn.c_str());
+    double* src = sim->d_grad[tk];
     const HostMech& m = sim->mech[id];
     if (cap < m.n) return sim->fail("output too small");
     std::vector<double> g(m.n);
@@ -3299,20 +3384,18 @@ int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, i
     if (n <= 0) return sim->fail("empty parameter group");
     const std::string mn = mech ? mech : "", vn = var ? var : "";
     sim->ensure_grad_arrays();
-    double* grad = nullptr;
-    int id = -1;
-    if (mn == "hh" && vn == "gnabar") { grad = sim->d_grad_gnabar; id = M_HH; }
-    else if (mn == "hh" && vn == "gkbar") { grad = sim->d_grad_gkbar; id = M_HH; }
-    else if (mn == "pas" && vn == "g_pas") { grad = sim->d_grad_gpas; id = M_PAS; }
-    else if (mn == "ExpSyn" && vn == "weight") { grad = sim->d_grad_w; id = M_EXPSYN; }
-    if (id < 0 || !sim->mech[id].present) return sim->fail("no trainable parameter %s.%s", mn.c_str(), vn.c_str());
-    if (!grad) return sim->fail("gradients are allocated by the first hx_adjoint call");
+    const int id = mech_id(mn);
+    const int tk = id < 0 ? -1 : trainable_id(id, vn);
+    if (tk < 0 || !sim->mech[id].present) return sim->fail("no trainable parameter %s.%s", mn.c_str(), vn.c_str());
+    double* grad = sim->d_grad[tk];
     const HostMech& m = sim->mech[id];
     std::vector<double*> w, g;
     for (int k = 0; k < n; ++k) {
         if (inst[k] < 0 || inst[k] >= m.n) return sim->fail("instance %d out of range", inst[k]);
         const int dj = m.perm[inst[k]];
-        w.push_back(id == M_EXPSYN ? sim->d_es_weight + dj : sim->resolve(mn, vn, inst[k]).dev);
+        w.push_back(id == M_EXPSYN ? sim->d_es_weight + dj
+                    : id == M_EXP2SYN ? sim->d_e2_weight + dj
+                                      : sim->resolve(mn, vn, inst[k]).dev);
         g.push_back(grad + dj);
     }
     return sim->opt_add_group(opt, w, g, impedance);
@@ -3375,18 +3458,13 @@ int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* 
 
 
 void hx_sim::ensure_grad_arrays() {
-    if (d_grad_gnabar) return;
-    const HostMech& hh = mech[M_HH];
-    const HostMech& es = mech[M_EXPSYN];
-    const HostMech& pas = mech[M_PAS];
-    d_grad_gnabar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
-    d_grad_gkbar = dalloc<double>(owned, std::max(1, hh.present ? hh.n : 0));
-    d_grad_gpas = dalloc<double>(owned, std::max(1, pas.present ? pas.n : 0));
-    d_grad_w = dalloc<double>(owned, std::max(1, es.present ? es.n : 0));
-    HXC(hipMemset(d_grad_gnabar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0)));
-    HXC(hipMemset(d_grad_gkbar, 0, sizeof(double) * std::max(1, hh.present ? hh.n : 0)));
-    HXC(hipMemset(d_grad_gpas, 0, sizeof(double) * std::max(1, pas.present ? pas.n : 0)));
-    HXC(hipMemset(d_grad_w, 0, sizeof(double) * std::max(1, es.present ? es.n : 0)));
+    if (d_grad[0]) return;
+    for (int k = 0; k < kNumTrainable; ++k) {
+        const HostMech& m = mech[kTrainable[k].mech];
+        const int n = std::max(1, m.present ? m.n : 0);
+        d_grad[k] = dalloc<double>(owned, n);
+        HXC(hipMemset(d_grad[k], 0, sizeof(double) * n));
+    }
 }
 
 int hx_sim::opt_add_group(int opt, const std::vector<double*>& w, const std::vector<double*>& g, double impedance) {

@@ -193,7 +193,8 @@ int hx_get_vecplay_keys(hx_sim* sim, char* buf, int cap);
  * impedance times inv_record_steps and writes the same value to all its weights; the
  * gradients are zeroed after each step.  Weights and gradients are variable handles: any
  * variable, including ExpSyn/Exp2Syn "weight" (netcon weights) and the adjoint's gradients
- * hh "grad_gnabar" / "grad_gkbar", pas "grad_g_pas" and ExpSyn "grad_weight". ---- */
+ * hh "grad_gnabar" / "grad_gkbar", pas "grad_g_pas", Ca_HVA "grad_gbar", hd_la "grad_ghdbar"
+ * and ExpSyn / Exp2Syn "grad_weight". ---- */
 int hx_create_optimizer(hx_sim* sim, const char* type);
 int hx_configure_optimizer(hx_sim* sim, int opt, double momentum, double beta1, double beta2, double eps);
 int hx_optimizer_add_param(hx_sim* sim, int opt, int weight_handle, int grad_handle, double impedance);
@@ -270,8 +271,10 @@ long long hx_get_info(hx_sim* sim, const char* key);
  *      parameter gradients that the reference's learn surface feeds its optimizer
  *      (LearnRuntime::replay_compute_dw_from_cached_signals_into,
  *      LearnRuntime.cpp:2298-2457), here as the exact gradient of a voltage loss
- *      through the fixed-step simulation.  Models: pas, hh, ExpSyn (VecStim or
- *      detector sources), IClamp, na/k ions with fixed reversal potentials. ---- */
+ *      through the fixed-step simulation.  Models: pas, hh, Ca_HVA, hd_la (Ih),
+ *      CaDynamics_E2, ExpSyn, Exp2Syn (VecStim, NetStim or detector sources), IClamp;
+ *      na/k ions with fixed reversal potentials, ca_ion with a fixed eca or eca from
+ *      cai every step (style 0100).  Not: gap junctions, VecPlay. ---- */
 /* Record the next run into HBM, up to max_steps steps (0 stops and frees the tape).
  * Call before hx_finitialize: deliveries at finitialize belong to step 0. */
 int hx_tape_begin(hx_sim* sim, int max_steps);
@@ -282,7 +285,9 @@ int hx_tape_length(hx_sim* sim);
  * backward sweep and leaves per-instance gradients for hx_get_gradient. */
 int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* target, int nsample, double* loss);
 /* dLoss/dparam per instance (user order): ("hh","gnabar"), ("hh","gkbar"),
- * ("pas","g_pas"), ("ExpSyn","weight") (the weight of the netcon into that instance). */
+ * ("pas","g_pas"), ("Ca_HVA","gbar"), ("hd_la","ghdbar"), ("ExpSyn","weight") and
+ * ("Exp2Syn","weight") (the weight of the netcon into that instance).  The same values
+ * are the variables "grad_<var>" of the mechanism, e.g. ("Ca_HVA", "grad_gbar", i). */
 int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out, int cap);
 
 /* ---- Adam over tied parameter groups (AdamOptimizer::step_gpu, optimizer.cpp:351-457;
