@@ -129,22 +129,43 @@ def host_threads() -> int:
     return max(1, n)
 
 
+def perturb_config3(spec, seed: int = 1):
+    """Target model for the config-3 training step: per cell, Ca_HVA gbar, hd_la ghdbar and
+    hh gnabar (each tied over the cell) scaled by U(0.8, 1.2), and every Exp2Syn netcon
+    weight by U(0.8, 1.2)."""
+    import copy
+    import numpy as np
+    out = copy.deepcopy(spec)
+    cell = spec.cell_of_node()
+    rng = np.random.default_rng(0x3C3 + seed)
+    f = rng.uniform(0.8, 1.2, (spec.ncell, 3))
+    for k, (mech, var) in enumerate((("Ca_HVA", "gbar"), ("hd_la", "ghdbar"), ("hh", "gnabar"))):
+        m = out.mechs[mech]
+        m.params[var] = m.params[var] * f[cell[m.nodes], k]
+    nc = out.netcons["Exp2Syn"]
+    nc.weight = nc.weight * rng.uniform(0.8, 1.2, nc.weight.size)
+    return out
+
+
 def train_bench(args):
-    """Config 5: one differentiable training step = taped forward run (1000 cells x 500
-    compartments, 200 ms), adjoint backward pass for the soma-v MSE against the perturbed
-    model's trace, and one Adam step (lr 1e-3) over 13 parameters per cell (gnabar, gkbar,
-    g_pas tied per cell; 10 ExpSyn weights)."""
+    """One differentiable training step = taped forward run, adjoint backward pass for the
+    soma-v MSE against the perturbed model's trace, and one Adam step (lr 1e-3).
+    Config 5 (default): 1000 cells x 500 compartments, 200 ms; gnabar, gkbar, g_pas tied
+    per cell and the 10 ExpSyn weights of each cell.  --train-config 3: config-3 cells
+    (5000 compartments, --train-cells of them, 25 ms by default); Ca_HVA gbar, hd_la ghdbar,
+    hh gnabar, gkbar and pas g tied per cell and the 200 Exp2Syn weights of each cell."""
     import numpy as np
     import torch
     from heliox_amd import Sim, build_config
     from heliox_amd.synth import perturb_config5
 
-    tstop = 200.0
-    base = build_config(5, args.train_cells, tstop)
+    c3 = args.train_config == 3
+    tstop = args.train_tstop if args.train_tstop > 0 else (25.0 if c3 else 200.0)
+    base = build_config(3 if c3 else 5, args.train_cells, tstop)
     nstep = int(round(tstop / base.dt))
     soma = list(range(base.ncell))
     tg = Sim()
-    tg.load_model_from_spec(perturb_config5(base, seed=1), add_monitors=False)
+    tg.load_model_from_spec(perturb_config3(base) if c3 else perturb_config5(base, seed=1), add_monitors=False)
     for c in soma:
         tg.add_monitor("global", "v", c)
     tg.finitialize(-65.0)
@@ -167,23 +188,29 @@ def train_bench(args):
 
     forward_backward()                           # warm-up (no parameter update)
     opt = g.adam_create(0.9, 0.999, 1e-8)
-    for mech, var in (("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas")):
+    tied = (("Ca_HVA", "gbar"), ("hd_la", "ghdbar"), ("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas")) if c3 \
+        else (("hh", "gnabar"), ("hh", "gkbar"), ("pas", "g_pas"))
+    for mech, var in tied:
         cn = cell[base.mechs[mech].nodes]
         for c in range(base.ncell):
             g.adam_add_group(opt, mech, var, np.nonzero(cn == c)[0])
-    for k in range(base.mechs["ExpSyn"].nodes.size):
-        g.adam_add_group(opt, "ExpSyn", "weight", [k])
+    syn = "Exp2Syn" if c3 else "ExpSyn"
+    for k in range(base.mechs[syn].nodes.size):
+        g.adam_add_group(opt, syn, "weight", [k])
     loss, tf, tb = forward_backward()
     t2 = time.perf_counter()
     g.adam_step(opt, 1e-3, 1.0)
     ta = time.perf_counter() - t2
     total = tf + tb + ta
-    print(json.dumps({"metric": "config-5 training steps/s (1000x500-comp fp64, 200 ms forward + adjoint + Adam)",
-                      "value": 1.0 / total, "unit": "training steps/s", "n_gpus": 1, "steps": 1, "warmup": 1,
-                      "ms_per_step": total * 1e3, "higher_is_better": True, "scaling": "weak",
+    ncomp = base.nnode // base.ncell
+    name = f"config-{3 if c3 else 5} training steps/s ({base.ncell}x{ncomp}-comp fp64, {tstop:g} ms forward + adjoint + Adam)"
+    print(json.dumps({"metric": name, "value": 1.0 / total, "unit": "training steps/s", "n_gpus": 1, "steps": 1,
+                      "warmup": 1, "ms_per_step": total * 1e3, "higher_is_better": True, "scaling": "weak",
                       "vs_baseline": None, "dtype": "f64", "data": "synthetic",
-                      "config": {"workload": f"config 5: {base.ncell} cells x 500 compartments, {nstep} steps",
-                                 "forward_s": tf, "adjoint_s": tb, "adam_s": ta, "loss": loss}}))
+                      "config": {"workload": f"config {3 if c3 else 5}: {base.ncell} cells x {ncomp} compartments, "
+                                             f"{nstep} steps",
+                                 "forward_s": tf, "adjoint_s": tb, "adam_s": ta, "loss": loss,
+                                 "adjoint_us_per_step": tb * 1e6 / nstep}}))
 
 
 MFMA_F32_PEAK_TFS = 157.3
@@ -303,6 +330,9 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--train", action="store_true", help="time the config-5 training step instead")
     ap.add_argument("--train-cells", type=int, default=1000)
+    ap.add_argument("--train-config", type=int, default=5, choices=(3, 5),
+                    help="model of the training step: 5 (default) or 3 (its calcium and Exp2Syn mechanisms)")
+    ap.add_argument("--train-tstop", type=float, default=0.0, help="forward run of the training step (ms)")
     ap.add_argument("--cell-groups", type=int, default=0,
                     help="cell groups issued on separate streams (0: the library's choice, 1: one stream)")
     ap.add_argument("--model-root", action="store_true",
