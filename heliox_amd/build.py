@@ -47,10 +47,17 @@ def _compile(src: str) -> str:
     return obj
 
 
+def sources() -> list:
+    """The library's sources, with every mechanism plugin under csrc/mechs/."""
+    plugins = sorted(os.path.join("mechs", f) for f in os.listdir(os.path.join(CSRC, "mechs")) if f.endswith(".hip"))
+    return SOURCES + plugins
+
+
 def build(verbose: bool = True) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    os.makedirs(os.path.join(BUILD, "mechs"), exist_ok=True)
+    srcs = sources()
+    with ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
+        objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", tmp] + objs + ["-ldl"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -36,9 +36,33 @@
 #include "h5out.h"
 #include "hx_internal.h"
 #include "learn.h"
+#include "plugin.h"
 #include "random123.h"
 #include "schedule.h"
 #include "solve_chunk.h"
+
+// ---------------------------------------------------------------------------
+// mechanism plugins registered at library load (plugin.h)
+// ---------------------------------------------------------------------------
+namespace hx {
+namespace {
+std::vector<PluginMeta>& plugin_registry() {
+    static std::vector<PluginMeta> r;
+    return r;
+}
+}  // namespace
+bool register_plugin(const PluginMeta& meta) {
+    plugin_registry().push_back(meta);
+    return true;
+}
+const PluginMeta* find_plugin(const char* name) {
+    for (const auto& m : plugin_registry())
+        if (std::strcmp(m.name, name) == 0) return &m;
+    return nullptr;
+}
+int plugin_count() { return static_cast<int>(plugin_registry().size()); }
+const PluginMeta& plugin_at(int k) { return plugin_registry()[k]; }
+}  // namespace hx
 
 using namespace hx;
 
@@ -224,6 +248,26 @@ struct hx_sim {
     std::vector<double> a, b, area, cm;
     HostMech mech[M_COUNT];
     std::map<std::string, double> globals[M_COUNT];
+    // mechanisms added through the plugin seam, in insertion order
+    struct PluginInst {
+        const PluginMeta* meta = nullptr;
+        HostMech h;
+    };
+    std::vector<PluginInst> plugins;
+    PluginInst* plugin_named(const std::string& name) {
+        for (auto& p : plugins)
+            if (name == p.meta->name) return &p;
+        return nullptr;
+    }
+    unsigned plugin_ions() const {     // ions some plugin reads or writes (bit 0 na, 1 k, 2 ca)
+        unsigned u = 0;
+        for (const auto& p : plugins) u |= p.meta->ion_read | p.meta->ion_write;
+        return u;
+    }
+    PluginArgs plugin_args(const PluginInst& p, double tcur) const;
+    void launch_plugin_inits(double tcur);
+    void launch_plugin_currents(double tcur);
+    void launch_plugin_states(double tcur);
     std::vector<int> pre_gid, pre_node;
     std::vector<double> pre_thr;
     std::vector<std::vector<double>> vecstim;
@@ -755,6 +799,15 @@ void hx_sim::build_layout() {
             m.dense = ok;
         }
     }
+    for (auto& p : plugins) {
+        HostMech& m = p.h;
+        std::vector<int> idx(m.n);
+        std::iota(idx.begin(), idx.end(), 0);
+        std::stable_sort(idx.begin(), idx.end(), [&](int x, int y) { return node_perm[m.node[x]] < node_perm[m.node[y]]; });
+        m.iperm = idx;
+        m.perm.assign(m.n, 0);
+        for (int j = 0; j < m.n; ++j) m.perm[idx[j]] = j;
+    }
     // a mechanism that reads an ion can be fused only if the ion is dense too
     dense_mask = 0;
     for (int id = 0; id < M_COUNT; ++id) {
@@ -793,7 +846,7 @@ void hx_sim::recompute_fused() {
 // a monitor on ca_ion or CaDynamics_E2, taping or signal capture.
 void hx_sim::refresh_cadyn_eager() {
     bool ok = fused && mech[M_CADYN].present && (dense_mask & (1u << M_CADYN)) && !tape_on &&
-              !(learn && learn->capturing());
+              !(learn && learn->capturing()) && !(plugin_ions() & plugin::kCa);   // a plugin's ica comes later
     for (size_t i = 0; ok && i < mon_name.size(); ++i)
         if (mon_name[i].first == "ca_ion" || mon_name[i].first == "CaDynamics_E2") ok = false;
     cadyn_eager = ok;
@@ -844,6 +897,36 @@ void hx_sim::upload() {
         HostMech& im = mech[ion_ids[x]];
         if (!im.present) continue;
         for (int j = 0; j < im.n; ++j) ion_at[x][node_perm[im.node[im.iperm[j]]]] = j;
+    }
+    // plugin mechanisms: columns in device instance order, solver-order nodes, and the
+    // instances of the ions they use (which must be present on their nodes)
+    for (auto& p : plugins) {
+        HostMech& m = p.h;
+        MechDev& d = m.dev;
+        d = MechDev();
+        d.n = m.n;
+        d.stride = ((m.n + 63) / 64) * 64;
+        const int ncol = p.meta->ncol;
+        std::vector<double> blk(static_cast<size_t>(std::max(ncol, 1)) * std::max<long long>(d.stride, 1), 0.0);
+        for (int c = 0; c < ncol; ++c)
+            for (int j = 0; j < m.n; ++j) blk[c * d.stride + j] = m.col[c][m.iperm[j]];
+        d.base = dupload(owned, blk);
+        std::vector<int> nodes(m.n);
+        for (int j = 0; j < m.n; ++j) nodes[j] = node_perm[m.node[m.iperm[j]]];
+        d.node = dupload(owned, nodes);
+        const unsigned use = p.meta->ion_read | p.meta->ion_write;
+        static const char* ion_names[3] = {"na_ion", "k_ion", "ca_ion"};
+        for (int x = 0; x < 3; ++x) {
+            if (!(use & (1u << x))) continue;
+            std::vector<int> map(m.n);
+            for (int j = 0; j < m.n; ++j) {
+                map[j] = ion_at[x][nodes[j]];
+                if (map[j] < 0)
+                    throw std::runtime_error(std::string(p.meta->name) + " uses " + ion_names[x] + ", which node " +
+                                             std::to_string(m.node[m.iperm[j]]) + " does not have");
+            }
+            d.ion[x] = dupload(owned, map);
+        }
     }
     std::vector<double> uval_host(static_cast<size_t>(M_COUNT) * kUniformCols, 0.0);
     for (int id = 0; id < M_COUNT; ++id) {
@@ -1042,7 +1125,7 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
     }
     groups.clear();
     const auto& R = registry();
-    bool coupled = !pre_fanout_empty || !gaps.empty();
+    bool coupled = !pre_fanout_empty || !gaps.empty() || !plugins.empty();
     for (int id = 0; id < M_COUNT; ++id) {
         if (!mech[id].present || mech[id].n == 0) continue;
         if (id == M_ICLAMP || id == M_HALFGAP) coupled = true;        // point currents outside the node kernel
@@ -1376,7 +1459,18 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
         return r;
     }
     int id = mech_id(mn);
-    if (id < 0 || !mech[id].present) return r;
+    if (id < 0) {
+        PluginInst* p = plugin_named(mn);
+        if (!p || idx < 0 || idx >= p->h.n) return r;
+        for (int c = 0; c < p->meta->ncol; ++c)
+            if (var == p->meta->cols[c]) {
+                r.dev = p->h.dev.col(c) + p->h.perm[idx];
+                r.klass = c >= p->meta->nparam + p->meta->nstate ? 1 : 0;
+                r.point = (p->meta->flags & plugin::kPoint) != 0;
+            }
+        return r;
+    }
+    if (!mech[id].present) return r;
     const auto& M = registry()[id];
     HostMech& m = mech[id];
     if (M.ion) {
@@ -1457,6 +1551,7 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
         unsigned need = 0;
         for (int id = 0; id < M_COUNT; ++id)
             if (mech[id].present && !(dense_mask & (1u << id))) need |= static_cast<unsigned>(R[id].ion_use);
+        need |= plugin_ions();     // plugins read erev and add their currents after the node kernel
         A.ion_store = 0;
         for (int x = 0; x < 3; ++x) {
             const bool ext = assigned || (need & (1u << x));
@@ -1549,6 +1644,41 @@ void hx_sim::launch_point_currents(double tcur) {
     for (int id : pts)   // synapse currents are added by the node kernel
         if (mech[id].present && !(A.fold_mask & (1u << id))) launch_point_current(id, A, stream);
     tend(T_POINT);
+}
+
+PluginArgs hx_sim::plugin_args(const PluginInst& p, double tcur) const {
+    PluginArgs P{};
+    P.m = p.h.dev;
+    P.ion[0] = mech[M_NA_ION].dev;
+    P.ion[1] = mech[M_K_ION].dev;
+    P.ion[2] = mech[M_CA_ION].dev;
+    P.v = d_v;
+    P.d = d_d;
+    P.rhs = d_rhs;
+    P.area = d_area;
+    P.t = tcur;
+    P.dt = dt;
+    P.celsius = celsius;
+    return P;
+}
+
+// Plugins run after the built-in mechanisms: their currents after the node kernel and
+// the point processes (CoreNEURON order puts user mechanisms after the built-in
+// ones), their states after the solve, before the step's record.
+void hx_sim::launch_plugin_inits(double tcur) {
+    for (const auto& p : plugins) p.meta->launch_init(plugin_args(p, tcur), stream);
+}
+void hx_sim::launch_plugin_currents(double tcur) {
+    if (plugins.empty()) return;
+    tbegin(T_OTHER);
+    for (const auto& p : plugins) p.meta->launch_current(plugin_args(p, tcur), stream);
+    tend(T_OTHER);
+}
+void hx_sim::launch_plugin_states(double tcur) {
+    if (plugins.empty()) return;
+    tbegin(T_OTHER);
+    for (const auto& p : plugins) p.meta->launch_state(plugin_args(p, tcur), stream);
+    tend(T_OTHER);
 }
 
 void hx_sim::launch_events(int kk, double tk) {
@@ -1853,6 +1983,7 @@ void hx_sim::step_once() {
         launch_mech_pass(0, 1, tmid);
     }
     launch_point_currents(tmid);
+    launch_plugin_currents(tmid);
     SolveArgs S{};
     S.nunit = nunit;
     S.unit_node_begin = d_unit_node_begin;
@@ -1887,6 +2018,7 @@ void hx_sim::step_once() {
         launch_point_state(M_EXP2SYN, A, stream);
         tend(T_POINT);
     }
+    launch_plugin_states(t);
     if (fused) {
         state_pending = true;
     } else {
@@ -2086,12 +2218,14 @@ void hx_sim::finitialize(double v_init) {
     StepArgs A = step_args(0.0, 0, 0);
     for (int id = 0; id < M_COUNT; ++id)           // CoreNEURON order, ions before their users
         if (mech[id].present) launch_init(id, A, stream);
+    launch_plugin_inits(0.0);
     launch_record();
     launch_detect(0, 0.0);
     launch_events(0, 0.0);
     final_step = true;
     launch_mech_pass(0, 1, 0.0);
     launch_point_currents(0.0);
+    launch_plugin_currents(0.0);
     final_step = false;
     initialized = true;
     sync_outputs();
@@ -2205,7 +2339,29 @@ int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* nodes) {
     if (sim->loaded) return sim->fail("model already loaded");
     if (sim->nnode == 0) return sim->fail("set nodes before inserting mechanisms");
     const int id = mech_id(mech ? mech : "");
-    if (id < 0) return sim->fail("unknown mechanism '%s'", mech ? mech : "");
+    if (id < 0) {
+        const PluginMeta* pm = find_plugin(mech ? mech : "");
+        if (!pm) return sim->fail("unknown mechanism '%s'", mech ? mech : "");
+        if (sim->plugin_named(pm->name)) return sim->fail("mechanism '%s' inserted twice", mech);
+        if (n < 0 || (n > 0 && !nodes)) return sim->fail("invalid instance list");
+        std::vector<char> seen(sim->nnode, 0);
+        for (int j = 0; j < n; ++j) {
+            if (nodes[j] < 0 || nodes[j] >= sim->nnode) return sim->fail("%s: node index out of range", mech);
+            if (!(pm->flags & plugin::kPoint)) {
+                if (seen[nodes[j]]) return sim->fail("%s: density mechanism twice on node %d", mech, nodes[j]);
+                seen[nodes[j]] = 1;
+            }
+        }
+        hx_sim::PluginInst pi;
+        pi.meta = pm;
+        pi.h.present = true;
+        pi.h.n = n;
+        pi.h.node.assign(nodes, nodes + n);
+        pi.h.col.assign(pm->ncol, {});
+        for (int c = 0; c < pm->ncol; ++c) pi.h.col[c].assign(n, pm->dflt[c]);
+        sim->plugins.push_back(std::move(pi));
+        return 0;
+    }
     HostMech& m = sim->mech[id];
     if (m.present) return sim->fail("mechanism '%s' inserted twice", mech);
     if (n < 0 || (n > 0 && !nodes)) return sim->fail("invalid instance list");
@@ -2238,7 +2394,18 @@ int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, co
         return 0;
     }
     const int id = mech_id(mn);
-    if (id < 0 || !sim->mech[id].present) return sim->fail("mechanism '%s' not inserted", mn.c_str());
+    if (id < 0) {
+        hx_sim::PluginInst* p = sim->plugin_named(mn);
+        if (!p) return sim->fail("mechanism '%s' not inserted", mn.c_str());
+        int c = -1;
+        for (int k = 0; k < p->meta->ncol; ++k)
+            if (vn == p->meta->cols[k]) c = k;
+        if (c < 0) return sim->fail("%s has no variable '%s'", mn.c_str(), vn.c_str());
+        if (n != p->h.n) return sim->fail("%s.%s: expected %d values", mn.c_str(), vn.c_str(), p->h.n);
+        p->h.col[c].assign(vals, vals + n);
+        return 0;
+    }
+    if (!sim->mech[id].present) return sim->fail("mechanism '%s' not inserted", mn.c_str());
     const int c = col_id(id, vn);
     if (c < 0) return sim->fail("%s has no variable '%s'", mn.c_str(), vn.c_str());
     if (n != sim->mech[id].n) return sim->fail("%s.%s: expected %d values", mn.c_str(), vn.c_str(), sim->mech[id].n);
@@ -2616,6 +2783,34 @@ int hx_flush_recorders(hx_sim* sim) {
     API_END
 }
 
+int hx_mechanism_names(char* buf, int cap) {
+    std::string out;
+    auto line = [&](const char* name, const char* kind, int ncol, int nparam, int nstate, const char* const* cols) {
+        out += name;
+        out += '\t';
+        out += kind;
+        out += '\t' + std::to_string(nparam) + '\t' + std::to_string(nstate) + '\t';
+        for (int c = 0; c < ncol; ++c) {
+            if (c) out += ',';
+            out += cols[c];
+        }
+        out += '\n';
+    };
+    const auto& R = registry();
+    for (int id = 0; id < M_COUNT; ++id)
+        line(R[id].name, "builtin", R[id].ncol, R[id].nparam, R[id].nstate, R[id].cols.data());
+    for (int k = 0; k < plugin_count(); ++k) {
+        const PluginMeta& m = plugin_at(k);
+        line(m.name, "plugin", m.ncol, m.nparam, m.nstate, m.cols);
+    }
+    if (buf && cap > 0) {
+        const size_t n = std::min(out.size(), static_cast<size_t>(cap - 1));
+        std::memcpy(buf, out.data(), n);
+        buf[n] = '\0';
+    }
+    return static_cast<int>(out.size()) + 1;
+}
+
 int hx_set_hdf5_enabled(hx_sim* sim, int enable) {
     API_BEGIN
     if (!enable) {
@@ -2728,7 +2923,21 @@ int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, in
         return sim->nnode;
     }
     int id = mech_id(mn);
-    if (id < 0 || !sim->mech[id].present) return sim->fail("mechanism '%s' not present", mn.c_str());
+    if (id < 0) {
+        hx_sim::PluginInst* p = sim->plugin_named(mn);
+        if (!p) return sim->fail("mechanism '%s' not present", mn.c_str());
+        int c = -1;
+        for (int k = 0; k < p->meta->ncol; ++k)
+            if (vn == p->meta->cols[k]) c = k;
+        if (c < 0) return sim->fail("%s has no variable '%s'", mn.c_str(), vn.c_str());
+        const HostMech& m = p->h;
+        if (cap < m.n) return sim->fail("output too small");
+        std::vector<double> g(m.n);
+        if (m.n) HXC(hipMemcpy(g.data(), m.dev.col(c), sizeof(double) * m.n, hipMemcpyDeviceToHost));
+        for (int j = 0; j < m.n; ++j) out[j] = g[m.perm[j]];
+        return m.n;
+    }
+    if (!sim->mech[id].present) return sim->fail("mechanism '%s' not present", mn.c_str());
     if (id == M_CADYN && (vn == "cai" || vn == "ica")) {
         // CaDynamics_E2 keeps cai / ica in the ca_ion column of its node: one copy of
         // that column, then a gather through the node -> ion instance map
@@ -3147,6 +3356,10 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
         if (!sim->mech[id].present) continue;
         if (id == M_HALFGAP)
             return sim->fail("the adjoint does not support gap junctions (the model has %s)", R[id].name);
+    }
+    if (!sim->plugins.empty()) {
+        return sim->fail("the adjoint does not support plugin mechanisms (the model has %s)",
+                         sim->plugins[0].meta->name);
     }
     for (int x : {M_NA_ION, M_K_ION})
         if (sim->mech[x].present)

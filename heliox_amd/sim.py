@@ -19,12 +19,13 @@ fail.
 from __future__ import annotations
 
 import ctypes as C
+import dataclasses
 import os
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
-from .spec import ModelSpec
+from .spec import ModelSpec, register_mechanism
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libheliox_amd.so")
@@ -59,6 +60,7 @@ SIGNATURES = {
     "hx_set_user_mod_num": (C.c_int, [_P, C.c_int]),
     "hx_model_read_export": (C.c_int, [_P]),
     "hx_model_digest": (C.c_int, [_P, C.c_char_p, C.c_int]),
+    "hx_mechanism_names": (C.c_int, [C.c_char_p, C.c_int]),
     "hx_finitialize": (C.c_int, [_P, C.c_double]),
     "hx_run": (C.c_int, [_P, C.c_double]),
     "hx_continue_run": (C.c_int, [_P, C.c_double]),
@@ -178,7 +180,35 @@ def lib() -> C.CDLL:
             f.restype = res
             f.argtypes = args
         _lib = L
+        for m in mechanisms():
+            if m.kind == "plugin":
+                register_mechanism(m.name, m.columns[: m.nparam])
     return _lib
+
+
+@dataclasses.dataclass(frozen=True)
+class MechanismInfo:
+    """One mechanism the library can insert: its columns are its parameters, then its
+    states, then its assigned variables."""
+    name: str
+    kind: str             # "builtin" or "plugin"
+    nparam: int
+    nstate: int
+    columns: Tuple[str, ...]
+
+
+def mechanisms() -> List[MechanismInfo]:
+    """Every mechanism the library knows, built-in ones first, then plugins in
+    registration order (hx_mechanism_names)."""
+    L = _lib if _lib is not None else lib()
+    n = L.hx_mechanism_names(None, 0)
+    buf = C.create_string_buffer(n)
+    L.hx_mechanism_names(buf, n)
+    out = []
+    for line in buf.value.decode().splitlines():
+        name, kind, npar, nst, cols = line.split("\t")
+        out.append(MechanismInfo(name, kind, int(npar), int(nst), tuple(c for c in cols.split(",") if c)))
+    return out
 
 
 def _dp(a: np.ndarray):

@@ -38,9 +38,26 @@ MECH_PARAMS: Dict[str, Tuple[str, ...]] = {
     "na_ion": ("erev", "conci", "conco"),
     "k_ion": ("erev", "conci", "conco"),
     "ca_ion": ("erev", "conci", "conco"),
+    # added to the library through its mechanism plugin seam (csrc/mechs/Im.hip)
+    "Im": ("gImbar",),
 }
 ION_NAMES = ("na_ion", "k_ion", "ca_ion")
 POINT_PROCESSES = ("IClamp", "HalfGap", "ExpSyn", "Exp2Syn", "VecStim", "NetStim")
+
+
+def register_mechanism(name: str, params: Tuple[str, ...]) -> None:
+    """Accept ``name`` in model specs, with its parameter columns.
+
+    For a mechanism compiled into the library through its plugin seam (registered by
+    name there, as the reference's MechanismFactory does, mechanism.h:125-197);
+    loading the library registers every plugin it reports.  Re-registering a name
+    with other columns is an error.
+    """
+    params = tuple(params)
+    old = MECH_PARAMS.get(name)
+    if old is not None and old != params:
+        raise ValueError(f"mechanism {name} is already known with parameters {old}")
+    MECH_PARAMS[name] = params
 
 
 @dataclass

@@ -56,6 +56,13 @@ int hx_model_set_nodes(hx_sim* sim, int ncell, int nnode, const int* parent, con
 int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* node_indices);
 /* One parameter column, n values in instance order (read_data_from_coredat). */
 int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, const double* values);
+/* Every mechanism hx_model_insert accepts (MechanismFactory's registry, mechanism.h:125-164):
+ * the built-in set and the plugins registered in the library's build (plugin.h,
+ * HX_REGISTER_MECHANISM, the reference's REGISTER_MECHANISM mechanism.h:167-171), one
+ * "name<TAB>builtin|plugin<TAB>nparam<TAB>nstate<TAB>col,col,...\n" line each (columns:
+ * parameters, then states, then assigned variables).  Writes up to cap bytes
+ * (NUL-terminated) and returns the length needed including the NUL. */
+int hx_mechanism_names(char* buf, int cap);
 /* Mechanism global (GlobalVarNames, e.g. hd_la ehd/kl/vhalft/a0t/zetat/gmt/q10/qtl). */
 int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double value);
 /* Ion style bits per ion instance (eion.cuh:155-197: 04 conc init, 040 erev init, 0100 erev each step). */

@@ -763,9 +763,61 @@ struct NetStim : Mech {
     }
 };
 
+// ---------------------------------------------------------------------------
+// Im, the muscarinic K current (user-mech/Im.cu:9-130); run by the library through its
+// mechanism plugin seam
+// ---------------------------------------------------------------------------
+struct ImMech : TMech {
+    std::vector<int> k;
+    double *gImbar, *ik, *gIm, *m_, *ek, *mInf, *mTau, *mAlpha, *mBeta, *k_erev, *k_cur;
+    ImMech() { name = "Im"; }
+    void alloc() override {
+        ensure("gImbar", 0.00001);
+        for (auto k2 : {"ik", "gIm", "m", "ek", "mInf", "mTau", "mAlpha", "mBeta"}) ensure(k2, 0.0);
+    }
+    void bind() override {
+        gImbar = C("gImbar").data(); ik = C("ik").data(); gIm = C("gIm").data(); m_ = C("m").data();
+        ek = C("ek").data(); mInf = C("mInf").data(); mTau = C("mTau").data(); mAlpha = C("mAlpha").data();
+        mBeta = C("mBeta").data();
+        k.resize(n);
+        for (int i = 0; i < n; ++i) k[i] = ion_inst(m, "k_ion", node[i]);
+        k_erev = m->mechs["k_ion"]->col["erev"].data(); k_cur = m->mechs["k_ion"]->col["cur"].data();
+    }
+    void rates(int i, double v) {                       // Im.cu:63-70
+        double qt = std::pow(2.3, ((34.0 - 21.0) / 10.0));
+        mAlpha[i] = 3.3e-3 * std::exp(2.5 * 0.04 * (v - (-35.0)));
+        mBeta[i] = 3.3e-3 * std::exp(-2.5 * 0.04 * (v - (-35.0)));
+        mInf[i] = mAlpha[i] / (mAlpha[i] + mBeta[i]);
+        mTau[i] = (1.0 / (mAlpha[i] + mBeta[i])) / qt;
+    }
+    void init(const double* v) override {
+        for (int i = 0; i < n; ++i) {
+            ek[i] = k_erev[k[i]];
+            m_[i] = 0.0;
+            rates(i, v[node[i]]);
+            m_[i] = mInf[i];
+        }
+    }
+    double cur(int i, double volt, double, bool updateIon) override {
+        ek[i] = k_erev[k[i]];
+        gIm[i] = gImbar[i] * m_[i];
+        ik[i] = gIm[i] * (volt - ek[i]);
+        if (updateIon) k_cur[k[i]] += ik[i];
+        return ik[i];
+    }
+    void state(const double* v, double dt, double) override {
+        for (int i = 0; i < n; ++i) {
+            ek[i] = k_erev[k[i]];
+            rates(i, v[node[i]]);
+            m_[i] = m_[i] + (1.0 - std::exp(dt * ((-1.0) / mTau[i]))) *
+                                (-(mInf[i] / mTau[i]) / ((-1.0) / mTau[i]) - m_[i]);
+        }
+    }
+};
+
 // CoreNEURON type order used by the oracle (NEURON built-ins, then user mechanisms).
 const char* kMechOrder[] = {"pas", "na_ion", "k_ion", "hh", "IClamp", "ExpSyn", "Exp2Syn", "VecStim", "NetStim",
-                            "ca_ion", "CaDynamics_E2", "Ca_HVA", "HalfGap", "hd_la"};
+                            "ca_ion", "CaDynamics_E2", "Ca_HVA", "HalfGap", "hd_la", "Im"};
 
 std::unique_ptr<Mech> make_mech(const std::string& nm) {
     if (nm == "na_ion") return std::make_unique<Ion>("na_ion", 1.0, 10.0, 140.0);
@@ -782,6 +834,7 @@ std::unique_ptr<Mech> make_mech(const std::string& nm) {
     if (nm == "Exp2Syn") return std::make_unique<Exp2Syn>();
     if (nm == "VecStim") return std::make_unique<VecStim>();
     if (nm == "NetStim") return std::make_unique<NetStim>();
+    if (nm == "Im") return std::make_unique<ImMech>();
     return nullptr;
 }
 

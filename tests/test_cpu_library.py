@@ -199,3 +199,22 @@ def test_error_paths_without_gpu():
     assert L.hx_model_add_netcon(h, 0, 0, b"ExpSyn", 0, 1.0, 1.0) == -1
     assert L.hx_finitialize(h, -65.0) == -1 and "not loaded" in s.last_error()
     assert s.get_variable_handle("global", "v", 0) == -1
+
+
+def test_plugin_mechanisms_are_listed_and_accepted():
+    """Mechanisms added through the plugin seam are registered by name at library load,
+    reported after the built-in ones, and accepted by model specs."""
+    import heliox_amd
+    from heliox_amd.spec import MECH_PARAMS
+    ms = heliox_amd.mechanisms()
+    kinds = [m.kind for m in ms]
+    assert kinds == sorted(kinds)            # "builtin" rows, then "plugin" rows
+    im = [m for m in ms if m.name == "Im"]
+    assert len(im) == 1 and im[0].kind == "plugin"
+    assert im[0].columns[:2] == ("gImbar", "m") and im[0].nparam == 1 and im[0].nstate == 1
+    assert MECH_PARAMS["Im"] == ("gImbar",)
+    for m in ms:
+        if m.kind == "builtin" and m.name in MECH_PARAMS:
+            assert set(MECH_PARAMS[m.name]) <= set(m.columns), m.name
+    with pytest.raises(ValueError):
+        heliox_amd.register_mechanism("Im", ("other",))

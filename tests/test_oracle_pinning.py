@@ -336,6 +336,42 @@ def test_hdla_gate_relaxation_under_clamp(v1, celsius):
     assert abs(x[-1] - x[0]) > 1e-3
 
 
+def im_textbook(v):
+    """Im of Hay et al. 2011 as a logistic and a hyperbolic secant: with
+    alpha, beta = 3.3e-3 exp(+-0.1 (v + 35)), m_inf = 1 / (1 + exp(-0.2 (v + 35))) and
+    tau = 1 / (6.6e-3 cosh(0.1 (v + 35)) qt), qt = 2.3^((34 - 21) / 10) (Im.cu:63-70)."""
+    x = v + 35.0
+    qt = 2.3 ** 1.3
+    return 1.0 / (1.0 + math.exp(-0.2 * x)), 1.0 / (6.6e-3 * math.cosh(0.1 * x) * qt)
+
+
+def im_cell(gimbar, ek=-85.0):
+    spec = single_compartment()
+    spec.cm[:] = CLAMP_CM
+    n = np.array([0], np.int32)
+    spec.mechs["k_ion"] = MechSpec(n, {"erev": np.array([ek])}, iontype=np.zeros(1, np.int32))
+    spec.mechs["Im"] = MechSpec(n.copy(), {"gImbar": np.array([gimbar])})
+    return spec
+
+
+@pytest.mark.parametrize("v1", [-80.0, -50.0, -35.0, -10.0, 20.0])
+def test_im_gate_relaxation_and_ik_under_clamp(v1):
+    """Im's m relaxes to m_inf(v1) with tau(v1), and ik = gImbar m (v - ek) of the gate
+    before each step's state update lands in k_ion.cur (Im.cu:72-100)."""
+    v0, gimbar, ek = -65.0, 2e-3, -85.0
+    o = oracle.OracleSim(im_cell(gimbar, ek), monitors=[("Im", "m", 0), ("k_ion", "cur", 0), ("Im", "ek", 0)])
+    clamp_step(o, v0, v1, 200.0)
+    m, ik, ekr = o.monitor(0), o.monitor(1), o.monitor(2)
+    m0, _ = im_textbook(v0)
+    m1, t1 = im_textbook(v1)
+    assert np.max(np.abs(m - relaxation(m0, m1, t1, m.size))) < 1e-10
+    assert abs(m[-1] - m[0]) > 1e-3
+    assert np.allclose(ik[1:], gimbar * m[:-1] * (v1 - ek), rtol=1e-12, atol=0)
+    assert np.all(ekr == ek)
+    # the clamp holds v to ~1e-10 mV, which moves tau by a few parts in 1e12
+    assert abs(o.get("Im", "mTau", 0) / t1 - 1) < 1e-9
+
+
 @pytest.mark.parametrize("v0,gbar", [(-10.0, 1e-3), (-30.0, 5e-4), (10.0, 2e-3)])
 def test_cadynamics_drive_under_constant_ica(v0, gbar):
     """With v held and eca fixed at its initial Nernst value (ion style 04|040, no
