@@ -170,12 +170,34 @@ struct EventRing {
     unsigned* done;               // workgroups of the delivery launch that have finished (then back to 0)
 };
 
+// A packed fan-out target: bits 30-31 its kind (0 ExpSyn, 1 Exp2Syn, 2 NetStim), bits
+// 0-29 the instance.  Kind 2 sets the sign bit, so the kind is read with an unsigned shift.
+constexpr int kTargetNetStim = 2;
+__host__ __device__ inline int pack_target(int kind, int inst) {
+    return static_cast<int>((static_cast<unsigned>(kind) << 30) | static_cast<unsigned>(inst));
+}
+__host__ __device__ inline int target_kind(int packed) { return static_cast<int>(static_cast<unsigned>(packed) >> 30); }
+__host__ __device__ inline int target_inst(int packed) { return packed & 0x3fffffff; }
+
 // Fan-out tables: source -> synapse targets (packed type|instance) with delays.
 struct FanOut {
     const int* begin;             // [nsrc+1]
     const int* target;
     const double* delay;
 };
+
+// Events into NetStims that receive netcons, by delivery step: entry (round << 24) |
+// instance and its delivery time.  The round is the pass of the step's delivery loop
+// in which the event reaches the NetStim (1: it was there when the step began).
+struct NsInbox {
+    int* count;                   // [nslot]
+    int* entry;                   // [nslot * cap]
+    double* time;                 // [nslot * cap]
+    int nslot;
+    int cap;
+    int* error;                   // bit 0: a slot overflowed
+};
+constexpr int kNsRoundShift = 24;
 
 struct SpikeArgs {
     int npre;
@@ -192,6 +214,7 @@ struct SpikeArgs {
     int log_cap;
     FanOut fo;
     EventRing ring;
+    NsInbox ib;                   // fan-out targets of type 2 (NetStims)
     const double* ttab;           // t of every step since finitialize
     int kmax;                     // last valid ttab index
     double half_dt;
@@ -200,6 +223,7 @@ struct SpikeArgs {
 struct InputArgs {
     const double* eff_time;       // sorted effective VecStim event times
     const int* inst;              // VecStim instance of each event
+    const int* round;             // pass of the delivery loop that emits each event's spike
     int n;
     int* cursor;                  // first unprocessed event
     double tcut;                  // t_k + dt/2
@@ -207,9 +231,51 @@ struct InputArgs {
     int k;
     FanOut fo;
     EventRing ring;
+    NsInbox ib;
     const double* ttab;
     int kmax;
     double half_dt;
+};
+
+// NetStims that receive events (netstim.cpp:211-330 with one stream per instance),
+// run on the device by k_netstim: per instance its state, its pending self events and
+// its random stream; instance j of these is NetStim instance inst[j].
+constexpr int kNsQueue = 8;       // pending self events per instance
+constexpr int kNsMini = 8;        // events reaching one instance in one pass
+constexpr int kNsRounds = 64;     // passes of one step's delivery loop
+constexpr int kNsRng = 10;        // words of stream state per instance
+struct NsArgs {
+    int n;
+    const int* inst;
+    double* interval;
+    double* number;
+    double* noise;                // clamped to [0, 1] at finitialize
+    const double* weight;         // weight of the instance's incoming netcon
+    double* on;
+    double* ispike;
+    double* event;
+    double* q_t;                  // [n * kNsQueue] self-event times
+    int* q_kind;                  // 0 self event, 1 init event
+    long long* q_born;            // (step << 8) | pass that sent it (pass 0: finitialize)
+    int* q_n;
+    unsigned* rng;                // [n * kNsRng]: counter, block, word index, key
+    int* mini_n;                  // [n]
+    int* mini_e;                  // [n * kNsMini]
+    NsInbox ib;
+    FanOut fo;                    // outputs of each of these instances
+    EventRing ring;
+    const double* ttab;
+    int kmax;
+    double half_dt;
+    double t;                     // t_k
+    int k;
+    double* log_t;                // spikes of these NetStims: time and NetStim instance
+    int* log_inst;
+    int* log_count;
+    int log_cap;
+    int* error;                   // bit 1: a pass brought more than kNsMini events to one
+                                  // instance; bit 2: more than kNsRounds passes; bit 3: a
+                                  // self-event queue overflowed
 };
 
 struct DeliverArgs {
@@ -331,6 +397,7 @@ void launch_adj_gather(const double* tape_v, long long row, const int* nodes, in
 void launch_adam(const AdamArgs& a, hipStream_t s);
 void launch_spike(const SpikeArgs& a, hipStream_t s);
 void launch_input(const InputArgs& a, hipStream_t s);
+void launch_netstim(const NsArgs& a, hipStream_t s);
 void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s);
 void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s);
 void launch_vecplay_reset(VecPlayDev* items, int n, hipStream_t s);

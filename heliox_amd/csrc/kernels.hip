@@ -20,12 +20,14 @@
 //   k_spike ........ threshold detection, wave-ballot compaction into the spike
 //                    log, fan-out of deliveries into the device event ring
 //   k_input ........ VecStim trains (sorted on the host) entering the ring
+//   k_netstim ...... NetStims that receive events: the step's delivery loop for them
 //   k_deliver ...... NET_RECEIVE of the events due this step
 //   k_vecplay, k_record, k_gap, init kernels.
 #include <algorithm>
 
 #include "hx_internal.h"
 #include "mech_math.h"
+#include "random123.h"
 #include "solve_chunk.h"
 
 namespace hx {
@@ -923,6 +925,30 @@ __device__ __forceinline__ void ring_push(const EventRing& R, int m, int packed)
     else atomicOr(R.overflow, 1);
 }
 
+__device__ __forceinline__ void inbox_push(const NsInbox& B, int m, int j, double T, int round) {
+    const int slot = m & (B.nslot - 1);
+    const int pos = atomicAdd(&B.count[slot], 1);
+    if (pos < B.cap) {
+        const long long at = static_cast<long long>(slot) * B.cap + pos;
+        B.entry[at] = (round << kNsRoundShift) | j;
+        B.time[at] = T;
+    } else {
+        atomicOr(B.error, 1);
+    }
+}
+
+// One fan-out target of a spike at time ts emitted in pass `round` of step k's delivery
+// loop: synapses take it from the event ring at their delivery step; a NetStim takes it
+// from its inbox, in the next pass of step k when it is due in step k, else in the first
+// pass of its step (by then it waits in the NetStim's queue).
+__device__ __forceinline__ void fan_out(const EventRing& R, const NsInbox& B, const double* ttab, int k, int kmax,
+                                        double half_dt, double ts, int round, int target, double delay) {
+    const double T = ts + delay;
+    const int m = delivery_step(ttab, k, kmax, T, half_dt);
+    if (target_kind(target) == kTargetNetStim) inbox_push(B, m, target_inst(target), T, m == k ? round + 1 : 1);
+    else ring_push(R, m, target);
+}
+
 __global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     bool fire = false;
@@ -951,10 +977,9 @@ __global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) {
         S.log_t[pos] = S.t;
         S.log_gid[pos] = S.gid[i];
     }
-    for (int e = S.fo.begin[i]; e < S.fo.begin[i + 1]; ++e) {
-        const int m = delivery_step(S.ttab, S.k, S.kmax, S.t + S.fo.delay[e], S.half_dt);
-        ring_push(S.ring, m, S.fo.target[e]);
-    }
+    // detected spikes are in place before the delivery loop's first pass
+    for (int e = S.fo.begin[i]; e < S.fo.begin[i + 1]; ++e)
+        fan_out(S.ring, S.ib, S.ttab, S.k, S.kmax, S.half_dt, S.t, 0, S.fo.target[e], S.fo.delay[e]);
 }
 
 __global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
@@ -965,15 +990,207 @@ __global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
         const int cnt = __syncthreads_count(take);
         if (take) {
             const int s = I.inst[idx];
-            for (int e = I.fo.begin[s]; e < I.fo.begin[s + 1]; ++e) {
-                const int m = delivery_step(I.ttab, I.k, I.kmax, I.t + I.fo.delay[e], I.half_dt);
-                ring_push(I.ring, m, I.fo.target[e]);
-            }
+            const int round = I.round ? I.round[idx] : 1;
+            for (int e = I.fo.begin[s]; e < I.fo.begin[s + 1]; ++e)
+                fan_out(I.ring, I.ib, I.ttab, I.k, I.kmax, I.half_dt, I.t, round, I.fo.target[e], I.fo.delay[e]);
         }
         cur += cnt;
         if (cnt < static_cast<int>(blockDim.x)) break;
     }
     if (threadIdx.x == 0) *I.cursor = cur;
+}
+
+// The delivery loop of step k (simulate.cpp:916-939) for the NetStims that receive
+// events, in one workgroup.  Pass r hands each instance the events that reach it in
+// that pass (inbox entries of round r) and its self events due by t_k + dt/2 that were
+// sent before pass r, and processes them in time order as NET_RECEIVE
+// (netstim.cpp:247-290, one stream per instance):
+//   init event:  if on, init_sequence, self event at t;
+//   self event:  if on, ispike += 1, spike at t, next_invl, if still on self event at
+//                t + event;
+//   netcon event with int(weight) > 0 while off: init_sequence, next_invl,
+//                event -= interval (1 - noise), self event at t + event;
+//                int(weight) < 0: off.
+// A spike fans out at once; what it brings to a NetStim in this step arrives in pass
+// r + 1.  Passes repeat while any instance has something due, as the reference's loop
+// repeats while anything was sent (at most kNsRounds).  Events of one instance at equal
+// times go self events first, then netcon events.
+__device__ __forceinline__ double ns_invl(Stream123& rng, bool& rng_live, const unsigned* rng_words,
+                                          double interval, double noise) {
+    if (interval <= 0.0) interval = 0.01;                  // netstim.cpp:140-155
+    if (noise == 0) return interval;
+    if (!rng_live) {
+        rng.load(rng_words);
+        rng_live = true;
+    }
+    return (1.0 - noise) * interval + noise * interval * rng.negexp();
+}
+
+__device__ bool ns_process(const NsArgs& A, int j, int r, long long off, double tcut) {
+    constexpr int kMax = kNsQueue + kNsMini;
+    double bt[kMax];
+    int bk[kMax];                                          // 0 netcon event, 1 self, 2 init
+    int nb = 0;
+    const long long q0 = static_cast<long long>(j) * kNsQueue;
+    const int qn = A.q_n[j];
+    const long long born_now = static_cast<long long>(A.k) << 8;
+    int keep = 0;
+    for (int q = 0; q < qn; ++q) {
+        const double tq = A.q_t[q0 + q];
+        const long long born = A.q_born[q0 + q];
+        const int kind = A.q_kind[q0 + q];
+        if (tq <= tcut && born < born_now + r) {
+            bt[nb] = tq;
+            bk[nb] = kind == 1 ? 2 : 1;
+            ++nb;
+        } else {
+            A.q_t[q0 + keep] = tq;
+            A.q_born[q0 + keep] = born;
+            A.q_kind[q0 + keep] = kind;
+            ++keep;
+        }
+    }
+    const int nm = min(atomicExch(&A.mini_n[j], 0), kNsMini);
+    for (int p = 0; p < nm; ++p) {
+        bt[nb] = A.ib.time[off + A.mini_e[j * kNsMini + p]];
+        bk[nb] = 0;
+        ++nb;
+    }
+    bool due = false;
+    if (nb > 0) {
+        for (int a = 1; a < nb; ++a) {                     // stable: self events stay ahead
+            const double x = bt[a];
+            const int y = bk[a];
+            int b = a - 1;
+            while (b >= 0 && bt[b] > x) {
+                bt[b + 1] = bt[b];
+                bk[b + 1] = bk[b];
+                --b;
+            }
+            bt[b + 1] = x;
+            bk[b + 1] = y;
+        }
+        const int inst = A.inst[j];
+        const double interval = A.interval[j], number = A.number[j], noise = A.noise[j];
+        double on = A.on[j], ispike = A.ispike[j], event = A.event[j];
+        Stream123 rng;
+        bool rng_live = false;
+        const unsigned* rw = A.rng + static_cast<long long>(j) * kNsRng;
+        const double t = A.t;
+        auto send_self = [&](double T, int kind) {
+            if (keep < kNsQueue) {
+                A.q_t[q0 + keep] = T;
+                A.q_born[q0 + keep] = born_now + r;
+                A.q_kind[q0 + keep] = kind;
+                ++keep;
+            } else {
+                atomicOr(A.error, 8);
+            }
+        };
+        auto init_sequence = [&]() {
+            if (number > 0.0) {
+                event = 0.0;
+                on = 1.0;
+                ispike = 0.0;
+            }
+        };
+        auto next_invl = [&]() {
+            if (number > 0) event = ns_invl(rng, rng_live, rw, interval, noise);
+            if (ispike >= number) on = 0.0;
+        };
+        for (int b = 0; b < nb; ++b) {
+            if (bk[b] == 2) {
+                if (on == 1.0) {
+                    init_sequence();
+                    send_self(t + 0.0, 0);
+                }
+            } else if (bk[b] == 1) {
+                if (on == 1.0) {
+                    ispike += 1.0;
+                    const int pos = atomicAdd(A.log_count, 1);
+                    if (pos < A.log_cap) {
+                        A.log_t[pos] = t;
+                        A.log_inst[pos] = inst;
+                    }
+                    for (int e = A.fo.begin[j]; e < A.fo.begin[j + 1]; ++e)
+                        fan_out(A.ring, A.ib, A.ttab, A.k, A.kmax, A.half_dt, t, r, A.fo.target[e], A.fo.delay[e]);
+                    next_invl();
+                    if (on == 1.0) send_self(t + event, 0);
+                }
+            } else {
+                const int w = static_cast<int>(A.weight[j]);
+                if (w > 0 && on == 0.0) {
+                    init_sequence();
+                    next_invl();
+                    event -= interval * (1. - noise);
+                    send_self(t + event, 0);
+                } else if (w < 0) {
+                    on = 0.0;
+                }
+            }
+        }
+        A.on[j] = on;
+        A.ispike[j] = ispike;
+        A.event[j] = event;
+        if (rng_live) rng.save(A.rng + static_cast<long long>(j) * kNsRng);
+    }
+    A.q_n[j] = keep;
+    for (int q = 0; q < keep; ++q) due |= A.q_t[q0 + q] <= tcut;
+    return due;
+}
+
+__global__ void __launch_bounds__(1024) k_netstim(NsArgs A) {
+    __shared__ int s_more, s_later, s_cnt;
+    const int slot = A.k & (A.ib.nslot - 1);
+    const long long off = static_cast<long long>(slot) * A.ib.cap;
+    const double tcut = A.t + A.half_dt;
+    auto slot_count = [&]() {
+        return min(__hip_atomic_load(&A.ib.count[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), A.ib.cap);
+    };
+    if (threadIdx.x == 0) {
+        s_more = 0;
+        s_later = 0;
+        s_cnt = slot_count();
+    }
+    __syncthreads();
+    // every thread takes every decision below from the same shared values, so all of
+    // them run the same passes and meet at every barrier
+    for (int r = 1;; ++r) {
+        const int cnt = s_cnt;
+        for (int e = threadIdx.x; e < cnt; e += blockDim.x) {
+            const int packed = A.ib.entry[off + e];
+            const int round = packed >> kNsRoundShift;
+            if (round > r) s_later = 1;
+            if (round != r) continue;
+            const int j = packed & ((1 << kNsRoundShift) - 1);
+            const int p = atomicAdd(&A.mini_n[j], 1);
+            if (p < kNsMini) A.mini_e[j * kNsMini + p] = e;
+            else atomicOr(A.error, 2);
+        }
+        __syncthreads();
+        for (int j = threadIdx.x; j < A.n; j += blockDim.x)
+            if (ns_process(A, j, r, off, tcut)) s_more = 1;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int cnt2 = slot_count();
+            s_more = (s_more || s_later || cnt2 > cnt) ? 1 : 0;
+            s_later = 0;
+            s_cnt = cnt2;
+        }
+        __syncthreads();
+        const bool more = s_more != 0;
+        __syncthreads();                                   // every thread has read s_more
+        if (!more) break;
+        if (r == kNsRounds) {
+            if (threadIdx.x == 0) atomicOr(A.error, 4);
+            break;
+        }
+        if (threadIdx.x == 0) s_more = 0;
+        __syncthreads();
+    }
+    // the step's entries are consumed (a second loop for the same step, finitialize's then
+    // the first step's, sees only what arrives in between)
+    if (threadIdx.x == 0) A.ib.count[slot] = 0;
 }
 
 // NET_RECEIVE of the events of step k's ring slot (expsyn.cpp net_receive,
@@ -990,11 +1207,11 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
     const long long off = static_cast<long long>(slot) * D.ring.cap;
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < cnt; e += gridDim.x * blockDim.x) {
         const int packed = D.ring.entry[off + e];
-        const int type = packed >> 30;
+        const int type = target_kind(packed);
         const int inst = packed & 0x3fffffff;
         if (type == 0) {
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
-        } else {
+        } else if (type == 1) {            // (NetStim targets go to their own inbox)
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
             atomicAdd(&D.e2.col(E2_A)[inst], wf);
             atomicAdd(&D.e2.col(E2_B)[inst], wf);
@@ -1172,6 +1389,10 @@ void launch_spike(const SpikeArgs& a, hipStream_t s) {
 
 void launch_input(const InputArgs& a, hipStream_t s) {
     if (a.n > 0) hipLaunchKernelGGL(k_input, dim3(1), dim3(kBlock), 0, s, a);
+}
+
+void launch_netstim(const NsArgs& a, hipStream_t s) {
+    if (a.n > 0) hipLaunchKernelGGL(k_netstim, dim3(1), dim3(1024), 0, s, a);
 }
 
 void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s) {

@@ -331,6 +331,14 @@ struct hx_sim {
     double* d_pre_fo_delay = nullptr;
     double *d_es_weight = nullptr, *d_e2_weight = nullptr;
     double max_delay = 0;
+    // NetStims that receive netcons run on the device (k_netstim); the others are trains
+    // made on the host
+    std::vector<int> ns_dyn;                  // NetStim instance -> index among these, or -1
+    std::vector<int> ns_dyn_inst;             // index -> NetStim instance
+    std::vector<double> ns_dyn_w;             // weight of its incoming netcon
+    NsArgs nsa{};                             // device state (nsa.n == 0: none)
+    int ns_log_cap = 0;
+    void upload_ns_dyn_state();
     double* d_spk_t = nullptr;
     int* d_spk_gid = nullptr;
     int* d_spk_count = nullptr;
@@ -353,6 +361,7 @@ struct hx_sim {
         EventRing ring{};
         double* d_in_time = nullptr;
         int* d_in_inst = nullptr;
+        int* d_in_round = nullptr;                // pass of the delivery loop that emits each input
         int* d_in_cursor = nullptr;
         int n_in = 0;
         int *d_vs_fo_begin = nullptr, *d_vs_fo_target = nullptr;
@@ -1064,20 +1073,54 @@ void hx_sim::upload() {
     // input sources: VecStim instances, then NetStim instances
     const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
     const int nns = mech[M_NETSTIM].present ? mech[M_NETSTIM].n : 0;
-    std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs + nns);
+    // NetStims with an incoming netcon run on the device; the rest stay host-made trains
+    ns_dyn.assign(nns, -1);
+    ns_dyn_inst.clear();
+    ns_dyn_w.clear();
+    for (auto& kv : by_syn)
+        if (kv.second.mech == M_NETSTIM) {
+            ns_dyn[kv.second.inst] = static_cast<int>(ns_dyn_inst.size());
+            ns_dyn_inst.push_back(kv.second.inst);
+            ns_dyn_w.push_back(kv.second.weight);
+        }
+    const int ndyn = static_cast<int>(ns_dyn_inst.size());
+    if (ndyn >= (1 << kNsRoundShift)) throw std::runtime_error("too many NetStims receive netcons");
+    std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs + nns), dyn_fo(ndyn);
     std::vector<double> esw(mech[M_EXPSYN].present ? mech[M_EXPSYN].n : 0, 0.0);
     std::vector<double> e2w(mech[M_EXP2SYN].present ? mech[M_EXP2SYN].n : 0, 0.0);
     max_delay = 0;
     for (auto& kv : by_syn) {
         const NetCon& nc = kv.second;
-        const int dinst = mech[nc.mech].perm[nc.inst];
-        const int packed = ((nc.mech == M_EXP2SYN ? 1 : 0) << 30) | dinst;
-        if (nc.mech == M_EXPSYN) esw[dinst] = nc.weight;
-        else e2w[dinst] = nc.weight;
+        int packed;
+        if (nc.mech == M_NETSTIM) {
+            packed = pack_target(kTargetNetStim, ns_dyn[nc.inst]);
+        } else {
+            const int dinst = mech[nc.mech].perm[nc.inst];
+            packed = pack_target(nc.mech == M_EXP2SYN ? 1 : 0, dinst);
+            if (nc.mech == M_EXPSYN) esw[dinst] = nc.weight;
+            else e2w[dinst] = nc.weight;
+        }
         if (nc.src_kind == 0) pre_fo[pre_dev[nc.src]].push_back({packed, nc.delay});
         else if (nc.src_kind == 1) vs_fo[nc.src].push_back({packed, nc.delay});
+        else if (ns_dyn[nc.src] >= 0) dyn_fo[ns_dyn[nc.src]].push_back({packed, nc.delay});
         else vs_fo[nvs + nc.src].push_back({packed, nc.delay});
         max_delay = std::max(max_delay, nc.delay);
+    }
+    // every packed target decodes to an instance of its kind (the kernels index with it)
+    {
+        const int nes = mech[M_EXPSYN].present ? mech[M_EXPSYN].n : 0;
+        const int ne2 = mech[M_EXP2SYN].present ? mech[M_EXP2SYN].n : 0;
+        auto check = [&](const std::vector<std::vector<std::pair<int, double>>>& fo) {
+            for (const auto& v : fo)
+                for (const auto& pr : v) {
+                    const int kind = target_kind(pr.first), inst = target_inst(pr.first);
+                    const int lim = kind == 0 ? nes : kind == 1 ? ne2 : kind == kTargetNetStim ? ndyn : 0;
+                    if (inst < 0 || inst >= lim) throw std::runtime_error("internal: bad fan-out target");
+                }
+        };
+        check(pre_fo);
+        check(vs_fo);
+        check(dyn_fo);
     }
     long long ntgt = 0;
     {
@@ -1095,6 +1138,38 @@ void hx_sim::upload() {
     }
     d_es_weight = dupload(owned, esw);
     d_e2_weight = dupload(owned, e2w);
+    nsa = NsArgs{};
+    nsa.n = ndyn;
+    if (ndyn > 0) {
+        nsa.inst = dupload(owned, ns_dyn_inst);
+        nsa.weight = dupload(owned, ns_dyn_w);
+        nsa.interval = dalloc<double>(owned, ndyn);
+        nsa.number = dalloc<double>(owned, ndyn);
+        nsa.noise = dalloc<double>(owned, ndyn);
+        nsa.on = dalloc<double>(owned, ndyn);
+        nsa.ispike = dalloc<double>(owned, ndyn);
+        nsa.event = dalloc<double>(owned, ndyn);
+        nsa.q_t = dalloc<double>(owned, static_cast<size_t>(ndyn) * kNsQueue);
+        nsa.q_kind = dalloc<int>(owned, static_cast<size_t>(ndyn) * kNsQueue);
+        nsa.q_born = dalloc<long long>(owned, static_cast<size_t>(ndyn) * kNsQueue);
+        nsa.q_n = dalloc<int>(owned, ndyn);
+        nsa.rng = dalloc<unsigned>(owned, static_cast<size_t>(ndyn) * kNsRng);
+        nsa.mini_n = dalloc<int>(owned, ndyn);
+        nsa.mini_e = dalloc<int>(owned, static_cast<size_t>(ndyn) * kNsMini);
+        std::vector<int> b(ndyn + 1, 0), tg;
+        std::vector<double> de;
+        for (int j = 0; j < ndyn; ++j) {
+            for (auto& pr : dyn_fo[j]) { tg.push_back(pr.first); de.push_back(pr.second); }
+            b[j + 1] = static_cast<int>(tg.size());
+        }
+        nsa.fo = FanOut{dupload(owned, b), dupload(owned, tg), dupload(owned, de)};
+        ns_log_cap = std::max(1 << 20, 64 * ndyn);
+        nsa.log_t = dalloc<double>(owned, ns_log_cap);
+        nsa.log_inst = dalloc<int>(owned, ns_log_cap);
+        nsa.log_count = dalloc<int>(owned, 1);
+        nsa.log_cap = ns_log_cap;
+        nsa.error = dalloc<int>(owned, 1);
+    }
 
     spk_cap = std::max(1 << 20, npre * 64);
     d_spk_t = dalloc<double>(owned, spk_cap);
@@ -1125,7 +1200,7 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
     }
     groups.clear();
     const auto& R = registry();
-    bool coupled = !pre_fanout_empty || !gaps.empty() || !plugins.empty();
+    bool coupled = !pre_fanout_empty || !gaps.empty() || !plugins.empty() || nsa.n > 0;
     for (int id = 0; id < M_COUNT; ++id) {
         if (!mech[id].present || mech[id].n == 0) continue;
         if (id == M_ICLAMP || id == M_HALFGAP) coupled = true;        // point currents outside the node kernel
@@ -1186,9 +1261,9 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
         cg.vs_used.assign(vs_fo.size(), 0);
         for (size_t i = 0; i < vs_fo.size(); ++i) {
             for (auto& pr : vs_fo[i]) {
-                const int type = pr.first >> 30, inst = pr.first & ((1 << 30) - 1);
-                const int node = syn_node[type][inst];
-                if (G > 1 && (node < cg.node0 || node >= cg.node1)) continue;
+                const int type = target_kind(pr.first), inst = target_inst(pr.first);
+                // (a NetStim target makes the model one group)
+                if (G > 1 && (syn_node[type][inst] < cg.node0 || syn_node[type][inst] >= cg.node1)) continue;
                 tg.push_back(pr.first);
                 de.push_back(pr.second);
                 cg.vs_used[i] = 1;
@@ -1219,6 +1294,18 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
     }
     if (G > 1 && !ev_main) HXC(hipEventCreateWithFlags(&ev_main, hipEventDisableTiming));
     if (G > 1 && !ev_stagger) HXC(hipEventCreateWithFlags(&ev_stagger, hipEventDisableTiming));
+    if (nsa.n > 0) {
+        // the NetStim inbox has the event ring's slots; a step's entries are bounded by
+        // each instance's one source firing a few times per step
+        NsInbox& ib = nsa.ib;
+        ib.nslot = nslot;
+        ib.cap = static_cast<int>(std::min<long long>(1 << 22, std::max<long long>(4096, 8LL * nsa.n)));
+        ib.count = dalloc<int>(owned, nslot);
+        ib.entry = dalloc<int>(owned, static_cast<size_t>(nslot) * ib.cap);
+        ib.time = dalloc<double>(owned, static_cast<size_t>(nslot) * ib.cap);
+        ib.error = nsa.error;
+        HXC(hipMemset(ib.count, 0, sizeof(int) * nslot));
+    }
 }
 
 // NetStim (netstim.cpp:211-330, one random stream per instance) as a train of
@@ -1309,6 +1396,7 @@ void hx_sim::make_netstim_trains(int horizon) {
     netstim.assign(nns, {});
     ensure_ttab(horizon + 1);
     for (int j = 0; j < nns; ++j) {
+        if (j < static_cast<int>(ns_dyn.size()) && ns_dyn[j] >= 0) continue;   // runs on the device
         const double id1 = m.col[NS_ID1][j];
         const NetStimParams P{m.col[NS_INTERVAL][j], m.col[NS_NUMBER][j], m.col[NS_START][j], m.col[NS_NOISE][j],
                               id1 < 0 ? static_cast<uint32_t>(j) : static_cast<uint32_t>(id1),
@@ -1322,32 +1410,62 @@ void hx_sim::make_netstim_trains(int horizon) {
 // processed at the first step whose window t+dt/2 reaches it, but never before
 // the previous element of the same train (vecevent.cpp:172-199 chains the
 // self-events), hence the running maximum.
+//
+// Each element also carries the pass of its step's delivery loop that emits its spike
+// (simulate.cpp:916-939 repeats the loop while anything was sent), which orders what a
+// NetStim receiving these spikes sees within one step: a VecStim element is processed in
+// pass 1 when its self event was queued in an earlier step, else in the pass after its
+// predecessor's; a NetStim's first spike comes in pass 2 (the init event in pass 1 sends
+// a self event at t), later ones like VecStim elements.
 void hx_sim::upload_inputs() {
-    std::vector<std::pair<double, int>> ev;
+    struct In {
+        double t;
+        int src, round;
+    };
+    std::vector<In> ev;
     const int nvs = mech[M_VECSTIM].present ? mech[M_VECSTIM].n : 0;
     const int nns = mech[M_NETSTIM].present ? mech[M_NETSTIM].n : 0;
-    auto add_train = [&](const std::vector<double>& train, int s) {
-        double run_max = -INFINITY;
-        for (double e : train) {
-            run_max = std::max(run_max, e);
-            ev.push_back({run_max, s});
+    const double half = dt / 2;
+    auto step_of = [&](double T) {   // first step m with t_m + dt/2 >= T
+        int m = std::max(0, static_cast<int>(std::floor(T / dt)) - 2);
+        if (static_cast<int>(ttab.size()) < m + 8) extend_step_times(ttab, m + 64, dt);
+        while (m > 0 && ttab[m - 1] + half >= T) --m;
+        while (ttab[m] + half < T) {
+            ++m;
+            if (m + 1 >= static_cast<int>(ttab.size())) extend_step_times(ttab, m + 64, dt);
+        }
+        return m;
+    };
+    auto add_train = [&](const std::vector<double>& train, int s, int first_round) {
+        double prev = -INFINITY;
+        int round = 0;
+        for (size_t i = 0; i < train.size(); ++i) {
+            const double cur = std::max(prev, train[i]);
+            if (i == 0) round = first_round;
+            // only an element this close can share its predecessor's step
+            else if (cur - prev <= 2 * dt && cur / dt < 5e7) round = step_of(cur) == step_of(prev) ? round + 1 : 1;
+            else round = 1;
+            prev = cur;
+            ev.push_back({cur, s, std::min(round, kNsRounds - 1)});
         }
     };
-    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) add_train(vecstim[s], s);
-    for (int j = 0; j < nns && j < static_cast<int>(netstim.size()); ++j) add_train(netstim[j], nvs + j);
-    std::stable_sort(ev.begin(), ev.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) add_train(vecstim[s], s, 1);
+    for (int j = 0; j < nns && j < static_cast<int>(netstim.size()); ++j) add_train(netstim[j], nvs + j, 2);
+    std::stable_sort(ev.begin(), ev.end(), [](const In& x, const In& y) { return x.t < y.t; });
     for (auto& cg : groups) {
         // each group keeps the events of the VecStims that drive its synapses
         std::vector<double> tt;
-        std::vector<int> ii;
+        std::vector<int> ii, rr;
         for (auto& e : ev)
-            if (e.second < static_cast<int>(cg.vs_used.size()) && cg.vs_used[e.second]) {
-                tt.push_back(e.first);
-                ii.push_back(e.second);
+            if (e.src < static_cast<int>(cg.vs_used.size()) && cg.vs_used[e.src]) {
+                tt.push_back(e.t);
+                ii.push_back(e.src);
+                rr.push_back(e.round);
             }
         cg.n_in = static_cast<int>(tt.size());
         cg.d_in_time = dupload(owned, tt);
         cg.d_in_inst = dupload(owned, ii);
+        cg.d_in_round = dupload(owned, rr);
     }
     inputs_dirty = false;
 }
@@ -1502,6 +1620,14 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
         // CaDynamics_E2 keeps cai / ica in the ca_ion columns of its node
         if (idx < 0 || idx >= m.n) return r;
         return resolve("ca_ion", var == "cai" ? "conci" : "cur", m.node[idx]);
+    }
+    if (id == M_NETSTIM && (var == "on" || var == "ispike" || var == "event")) {
+        // state of a NetStim that receives events (the others are trains made on the host)
+        if (idx < 0 || idx >= static_cast<int>(ns_dyn.size()) || ns_dyn[idx] < 0) return r;
+        const int j = ns_dyn[idx];
+        r.dev = (var == "on" ? nsa.on : var == "ispike" ? nsa.ispike : nsa.event) + j;
+        r.point = true;        // changes at delivery, which the fused schedule runs before the record
+        return r;
     }
     const int c = col_id(id, var);
     if (c < 0 || idx < 0 || idx >= m.n) return r;
@@ -1687,13 +1813,16 @@ void hx_sim::launch_events(int kk, double tk) {
 
 // VecStim input and delivery of step kk for one cell group's synapses.
 void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
-    if (!(mech[M_EXPSYN].present || mech[M_EXP2SYN].present)) return;
+    const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present;
+    if (!syn && nsa.n == 0) return;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
     if (cg.n_in > 0) {
         InputArgs I{};
         I.eff_time = cg.d_in_time;
         I.inst = cg.d_in_inst;
+        I.round = cg.d_in_round;
+        I.ib = nsa.ib;
         I.n = cg.n_in;
         I.cursor = cg.d_in_cursor;
         I.tcut = tk + dt / 2;
@@ -1705,6 +1834,20 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
         I.kmax = static_cast<int>(ttab.size()) - 1;
         I.half_dt = dt / 2;
         launch_input(I, on);
+    }
+    if (nsa.n > 0) {                 // NetStims receiving events: one group, the main stream
+        NsArgs A = nsa;
+        A.ring = cg.ring;
+        A.ttab = d_ttab;
+        A.kmax = static_cast<int>(ttab.size()) - 1;
+        A.half_dt = dt / 2;
+        A.t = tk;
+        A.k = kk;
+        launch_netstim(A, on);
+    }
+    if (!syn) {
+        tend(T_EVENTS, on);
+        return;
     }
     DeliverArgs D{};
     D.ring = cg.ring;
@@ -1746,6 +1889,7 @@ void hx_sim::launch_detect(int kk, double tk) {
     S.log_cap = spk_cap;
     S.fo = FanOut{d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay};
     S.ring = groups[0].ring;   // detector netcons exist only with a single group
+    S.ib = nsa.ib;
     S.ttab = d_ttab;
     S.kmax = static_cast<int>(ttab.size()) - 1;
     S.half_dt = dt / 2;
@@ -2061,6 +2205,14 @@ void hx_sim::sync_outputs() {
         HXC(hipMemcpy(&ov, cg.ring.overflow, sizeof(int), hipMemcpyDeviceToHost));
         if (ov) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
     }
+    if (nsa.n > 0) {
+        int e = 0;
+        HXC(hipMemcpy(&e, nsa.error, sizeof(int), hipMemcpyDeviceToHost));
+        if (e & 1) throw std::runtime_error("NetStim event inbox overflow");
+        if (e & 2) throw std::runtime_error("more than 8 events reached one NetStim in one pass of a step");
+        if (e & 4) throw std::runtime_error("a step's delivery loop needed more than 64 passes (NetStim interval too small?)");
+        if (e & 8) throw std::runtime_error("a NetStim has more than 8 pending self events");
+    }
     int ns = 0;
     HXC(hipMemcpy(&ns, d_spk_count, sizeof(int), hipMemcpyDeviceToHost));
     if (ns > spk_cap) throw std::runtime_error("spike log overflow");
@@ -2169,6 +2321,63 @@ int hx_sim::run_steps(int nstep) {
     return 0;
 }
 
+// INITIAL of the NetStims that receive events (netstim.cpp:211-246, one stream per
+// instance, sequence 0): noise clamped to [0, 1]; with start >= 0 and number > 0 the
+// instance is on and its init event waits at start + invl - interval (1 - noise) (0 if
+// negative).  Parameters are taken from the host copy, as the trains of the others are.
+void hx_sim::upload_ns_dyn_state() {
+    const int n = nsa.n;
+    if (n == 0) return;
+    HXC(hipStreamSynchronize(stream));      // nothing of an earlier run still uses the state
+    const HostMech& m = mech[M_NETSTIM];
+    std::vector<double> interval(n), number(n), noise(n), on(n, 0.0), ispike(n, 0.0), event(n, 0.0);
+    std::vector<double> qt(static_cast<size_t>(n) * kNsQueue, 0.0);
+    std::vector<int> qkind(static_cast<size_t>(n) * kNsQueue, 0), qn(n, 0);
+    std::vector<long long> qborn(static_cast<size_t>(n) * kNsQueue, 0);
+    std::vector<unsigned> rw(static_cast<size_t>(n) * kNsRng);
+    for (int j = 0; j < n; ++j) {
+        const int i = ns_dyn_inst[j];
+        interval[j] = m.col[NS_INTERVAL][i];
+        number[j] = m.col[NS_NUMBER][i];
+        noise[j] = std::min(1.0, std::max(0.0, m.col[NS_NOISE][i]));
+        Stream123 rng;
+        const double id1 = m.col[NS_ID1][i];
+        rng.set_ids(id1 < 0 ? static_cast<uint32_t>(i) : static_cast<uint32_t>(id1),
+                    static_cast<uint32_t>(m.col[NS_ID2][i]), static_cast<uint32_t>(m.col[NS_ID3][i]));
+        rng.set_seq(0, 0);
+        const double start = m.col[NS_START][i];
+        if (start >= 0.0 && number[j] > 0) {
+            on[j] = 1.0;
+            double mean = interval[j] <= 0.0 ? 0.01 : interval[j];
+            if (noise[j] != 0) mean = (1.0 - noise[j]) * mean + noise[j] * mean * rng.negexp();
+            event[j] = start + mean - interval[j] * (1.0 - noise[j]);
+            if (event[j] < 0.0) event[j] = 0.0;
+            qt[static_cast<size_t>(j) * kNsQueue] = event[j];
+            qkind[static_cast<size_t>(j) * kNsQueue] = 1;
+            qn[j] = 1;
+        }
+        rng.save(&rw[static_cast<size_t>(j) * kNsRng]);
+    }
+    auto up = [&](auto* dst, const auto& v) {
+        HXC(hipMemcpy(dst, v.data(), sizeof(v[0]) * v.size(), hipMemcpyHostToDevice));
+    };
+    up(nsa.interval, interval);
+    up(nsa.number, number);
+    up(nsa.noise, noise);
+    up(nsa.on, on);
+    up(nsa.ispike, ispike);
+    up(nsa.event, event);
+    up(nsa.q_t, qt);
+    up(nsa.q_kind, qkind);
+    up(nsa.q_born, qborn);
+    up(nsa.q_n, qn);
+    up(nsa.rng, rw);
+    HXC(hipMemset(nsa.mini_n, 0, sizeof(int) * n));
+    HXC(hipMemset(nsa.log_count, 0, sizeof(int)));
+    HXC(hipMemset(nsa.error, 0, sizeof(int)));
+    HXC(hipMemset(nsa.ib.count, 0, sizeof(int) * nsa.ib.nslot));
+}
+
 // Simulate::finitialize (simulate.cpp:106-141, 271-339)
 void hx_sim::finitialize(double v_init) {
     if (mech[M_NETSTIM].present && mech[M_NETSTIM].n > 0) {
@@ -2207,6 +2416,7 @@ void hx_sim::finitialize(double v_init) {
     }
     launch_clear_ints(d_pre_flag, npre, stream);
     launch_clear_ints(d_spk_count, 1, stream);
+    upload_ns_dyn_state();
     if (tape_on) {
         tape_n = 0;
         launch_clear_ints(d_tape_evn, tape_cap, stream);
@@ -2456,7 +2666,8 @@ int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
 int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double w, double delay) {
     if (sim->loaded) return sim->fail("model already loaded");
     const int id = mech_id(target ? target : "");
-    if (id != M_EXPSYN && id != M_EXP2SYN) return sim->fail("netcon target must be ExpSyn or Exp2Syn");
+    if (id != M_EXPSYN && id != M_EXP2SYN && id != M_NETSTIM)
+        return sim->fail("netcon target must be ExpSyn, Exp2Syn or NetStim");
     if (!sim->mech[id].present || inst < 0 || inst >= sim->mech[id].n) return sim->fail("netcon target instance out of range");
     if (src_kind == 0 && (src < 0 || src >= static_cast<int>(sim->pre_node.size())))
         return sim->fail("netcon source detector out of range");
@@ -3032,6 +3243,53 @@ int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap) {
         gid[i] = sim->spikes[i].second;
     }
     return n;
+}
+
+// Spikes of every NetStim since finitialize, ordered by time then instance: those of
+// host-made trains (an element's spike is at the step time t_m of the first step whose
+// window t_m + dt/2 reaches it, once that step's delivery loop has run) and those logged
+// by the device for the NetStims that receive events.
+int hx_get_netstim_spikes(hx_sim* sim, double* t, int* inst, int cap) {
+    if (!check_loaded(sim)) return -1;
+    API_BEGIN
+    std::vector<std::pair<double, int>> all;
+    if (sim->initialized) {
+        const int last = std::max(sim->k - 1, 0);
+        sim->ensure_ttab(last + 1);
+        const double half = sim->dt / 2;
+        const auto& tt = sim->ttab;
+        for (int j = 0; j < static_cast<int>(sim->netstim.size()); ++j) {
+            double run = -INFINITY;
+            for (double e : sim->netstim[j]) {
+                run = std::max(run, e);
+                const auto it = std::lower_bound(tt.begin(), tt.begin() + last + 1, run,
+                                                 [&](double tm, double T) { return tm + half < T; });
+                if (it == tt.begin() + last + 1) break;
+                all.push_back({*it, j});
+            }
+        }
+        if (sim->nsa.n > 0) {
+            HXC(hipStreamSynchronize(sim->stream));
+            int c = 0;
+            HXC(hipMemcpy(&c, sim->nsa.log_count, sizeof(int), hipMemcpyDeviceToHost));
+            if (c > sim->ns_log_cap) throw std::runtime_error("NetStim spike log overflow");
+            std::vector<double> lt(c);
+            std::vector<int> li(c);
+            if (c > 0) {
+                HXC(hipMemcpy(lt.data(), sim->nsa.log_t, sizeof(double) * c, hipMemcpyDeviceToHost));
+                HXC(hipMemcpy(li.data(), sim->nsa.log_inst, sizeof(int) * c, hipMemcpyDeviceToHost));
+            }
+            for (int i = 0; i < c; ++i) all.push_back({lt[i], li[i]});
+        }
+    }
+    std::sort(all.begin(), all.end());
+    const int n = std::min<int>(std::max(cap, 0), static_cast<int>(all.size()));
+    for (int i = 0; i < n; ++i) {
+        t[i] = all[i].first;
+        inst[i] = all[i].second;
+    }
+    return static_cast<int>(all.size());
+    API_END
 }
 
 // Simulate::output_spikes (simulate.cpp:892-909): <folder>/spk.dat, one "%.8g\t%d" line per

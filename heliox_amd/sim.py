@@ -85,6 +85,7 @@ SIGNATURES = {
     "hx_has_vecplay": (C.c_int, [_P, _S, _S, C.c_int]),
     "hx_get_spike_count": (C.c_int, [_P]),
     "hx_get_spikes": (C.c_int, [_P, _D, _I, C.c_int]),
+    "hx_get_netstim_spikes": (C.c_int, [_P, _D, _I, C.c_int]),
     "hx_get_spk_by_gid": (C.c_int, [_P, C.c_int, _D, C.c_int]),
     "hx_set_event_capacity": (C.c_int, [_P, C.c_int]),
     "hx_set_fusion": (C.c_int, [_P, C.c_int]),
@@ -538,6 +539,17 @@ class Sim:
         g = np.empty(n, np.int32)
         L.hx_get_spikes(self._h, _dp(t), _ip(g), n)
         return t, g
+
+    def netstim_spikes(self):
+        """(times, NetStim instances) of every NetStim spike since finitialize, ordered by
+        time then instance."""
+        L = lib()
+        n = self._chk(L.hx_get_netstim_spikes(self._h, None, None, 0), "netstim_spikes")
+        t = np.empty(n)
+        i = np.empty(n, np.int32)
+        if n:
+            self._chk(L.hx_get_netstim_spikes(self._h, _dp(t), _ip(i), n), "netstim_spikes")
+        return t, i
 
     def output_spikes(self, folder: str) -> str:
         """Write ``<folder>/spk.dat`` in the reference's format (Simulate::output_spikes);

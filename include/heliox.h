@@ -146,6 +146,10 @@ int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
 /* ---- spikes (Simulate::output_spikes simulate.cpp:892-909, get_spk_by_gid) ---- */
 int hx_get_spike_count(hx_sim* sim);
 int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap);
+/* Spikes of every NetStim since finitialize, ordered by time then instance: the
+   NetStim's own spike record (netstim.cpp:278-330, net_event at the delivering step's
+   time).  Returns the total count (-1 on error) and fills at most cap of them. */
+int hx_get_netstim_spikes(hx_sim* sim, double* t, int* inst, int cap);
 int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap);
 /* Simulate::output_spikes (simulate.cpp:892-909): writes <folder>/spk.dat (the folder is
  * created if needed) with one "%.8g<TAB>%d" line per spike of the spikes recorded so far,

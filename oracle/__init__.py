@@ -34,7 +34,11 @@ Parity status of each oracle function (``tests/test_oracle_pinning.py`` unless n
                          Random123's published known-answer vectors, the stream's
                          id/draw layout against those blocks, noiseless trains
                          against start + k interval, noisy intervals against the
-                         exponential law
+                         exponential law; netcon events against closed-form
+                         bursts (trigger while off, ignored while on, switched off,
+                         int-truncated weights, chains within one step)
+  Im ................... pinned: m relaxation to the logistic m_inf with the
+                         sech-form tau under clamp, ik into k_ion.cur
 """
 from __future__ import annotations
 

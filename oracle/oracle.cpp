@@ -31,7 +31,9 @@
 //   VecStim .............. src/spike/vecevent.cpp:94-217, src/spike/articell.cpp:18-35
 //   NetStim .............. src/spike/netstim.cpp:211-330 with one stream per instance
 //                          (src/utils/nrnran123.cpp:23-110; Philox4x32-10 as published
-//                          by Salmon et al., SC11)
+//                          by Salmon et al., SC11), netcon events included; every
+//                          processed event keeps the delivery loop going
+//   Im ................... src/mech/user-mech/Im.cu:9-130
 //   VecPlay .............. src/vecplay.cu:19-111
 //   Adam ................. src/optimizer/optimizer.cpp:351-413
 //
@@ -165,6 +167,7 @@ struct Model {
     std::vector<std::pair<double, int>> rec_spikes;
     std::vector<std::vector<double>> spk_output;
 
+    static constexpr uint32_t kNoSource = 0xffffffffu;
     struct PostSynState {             // PostSyn_trait (postsyn.h)
         Mech* mech = nullptr;
         int type_id = 0;
@@ -973,10 +976,27 @@ void Model::netstim_init() {                  // netstim.cpp:211-246 (initialize
     }
 }
 
+// The reference counts a send only where the next self event is scheduled, so the last
+// spike of a sequence can wait in its slot until something else keeps the delivery loop
+// going; here every processed event keeps the loop going, and that spike is gathered in
+// the same step like any other.
 bool Model::netstim_receive(int isyn, int flag) {   // netstim.cpp:247-290 (net_receive_cpu)
     auto* ns = static_cast<NetStim*>(postsyns[ns_postsyn].mech);
     double& on = ns->C("on")[isyn];
     bool sent = false;
+    if (flag == NORMAL_EVENT) {                      // netstim.cpp:262-274
+        const int w = static_cast<int>(postsyns[ns_postsyn].weight[isyn]);   // truncated, as there
+        if (w > 0 && on == 0.0) {
+            ns->init_sequence(isyn);
+            ns->next_invl(isyn);
+            double& event = ns->C("event")[isyn];
+            event -= ns->C("interval")[isyn] * (1. - ns->C("noise")[isyn]);
+            net_send_netstim(isyn, t + event, SELF_EVENT);
+            sent = true;
+        } else if (w < 0) {
+            on = 0.0;
+        }
+    }
     if (flag == NETSTIM_INIT_EVENT && on == 1.0) {
         ns->init_sequence(isyn);
         net_send_netstim(isyn, t + 0.0, SELF_EVENT);
@@ -1000,6 +1020,7 @@ void Model::network_spike_receive() {         // simulate.cpp:916-939
             int nn = ps.mech->n;
             for (int inode = 0; inode < nn; inode++) {
                 uint32_t spk_idx = ps.spk_vec_idx[inode];
+                if (spk_idx == kNoSource) continue;      // no netcon into this instance
                 if (spk_flags[spk_idx] == NORMAL_EVENT) {
                     Spike spk = spk_vec[spk_idx];
                     spk.syn_id = inode;
@@ -1250,7 +1271,7 @@ static int finalize_model(Model* m) {
             Model::PostSynState ps;
             ps.mech = mm;
             ps.type_id = type_id;
-            ps.spk_vec_idx.assign(mm->n, 0);
+            ps.spk_vec_idx.assign(mm->n, Model::kNoSource);
             ps.delay.assign(mm->n, 0.0);
             ps.weight.assign(mm->n, 0.0);
             ps.receive_idx.assign(mm->n + 1, 0);

@@ -155,3 +155,103 @@ def test_noisy_intervals_are_exponential():
     assert abs(gaps.mean() - 5.0) < 0.1
     # P(gap > 5) = exp(-1) up to the dt/2 rounding of each delivery
     assert abs(np.mean(gaps > 5.0) - math.exp(-1.0)) < 0.01
+
+
+# ---------------------------------------------------------------------------
+# NetStims that receive events (netstim.cpp:262-274): a netcon into a NetStim turns it
+# on (weight > 0, when it is off) or off (weight < 0); the weight is truncated to an int
+# ---------------------------------------------------------------------------
+def gated_model(ns_params, triggers, weights, delays, chain=None):
+    """NetStim instances each driven by one VecStim (its own trigger times); every NetStim
+    drives an ExpSyn on one passive compartment.  chain: (src NetStim, dst NetStim, w, delay)
+    netcons between NetStims, replacing the VecStim netcon of dst."""
+    n = len(ns_params)
+    spec = ModelSpec(ncell=1, parent=np.array([-1], np.int32), a=np.zeros(1), b=np.zeros(1),
+                     area=np.array([1256.6]), cm=np.ones(1), dt=DT)
+    spec.mechs["pas"] = MechSpec(np.zeros(1, np.int32), {"g_pas": np.array([1e-4]), "e_pas": np.array([-65.0])})
+    spec.mechs["ExpSyn"] = MechSpec(np.zeros(n, np.int32), {"tau": np.full(n, 2.0), "e": np.zeros(n)})
+    cols = {k: np.array([p[k] for p in ns_params], float) for k in ("interval", "number", "start", "noise")}
+    spec.mechs["NetStim"] = MechSpec(np.zeros(n, np.int32), cols)
+    spec.mechs["VecStim"] = MechSpec(np.zeros(n, np.int32), {})
+    spec.vecstim_offsets = np.concatenate([[0], np.cumsum([len(t) for t in triggers])]).astype(np.int64)
+    spec.vecstim_times = np.concatenate([np.asarray(t, float) for t in triggers])
+    spec.netcons["ExpSyn"] = NetConSpec(inst=np.arange(n, dtype=np.int32), src_kind=np.full(n, 2, np.int8),
+                                        src=np.arange(n, dtype=np.int32), weight=np.full(n, 1e-3),
+                                        delay=np.full(n, 1.0))
+    kind = np.full(n, 1, np.int8)
+    src = np.arange(n, dtype=np.int32)
+    w = np.asarray(weights, float)
+    d = np.asarray(delays, float)
+    for (a, b, wc, dc) in (chain or []):
+        kind[b], src[b], w[b], d[b] = 2, a, wc, dc
+    spec.netcons["NetStim"] = NetConSpec(inst=np.arange(n, dtype=np.int32), src_kind=kind, src=src, weight=w, delay=d)
+    return spec
+
+
+def run_oracle(spec, tstop):
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(-65.0)
+    o.run(tstop)
+    return o
+
+
+def chain_after(t0, interval, count):
+    """Step times of a noiseless burst started at step time t0: each next self event at
+    the previous spike's step time + interval, delivered at the first step reaching it."""
+    tt = step_times(int(math.ceil((t0 + interval * count) / DT)) + 4)
+    out = [t0]
+    for _ in range(count - 1):
+        T = out[-1] + interval
+        m = int(np.searchsorted(tt + DT / 2, T))
+        out.append(tt[m])
+    return out
+
+
+def test_trigger_starts_a_burst_and_is_ignored_while_on():
+    """start < 0: the NetStim waits; a positive event while it is off starts a burst of
+    `number` spikes, the first in the delivering step (event = invl - interval = 0), the
+    next every `interval`; an event while it is on does nothing; after the last spike it is
+    off again and the next trigger starts a new burst."""
+    p = dict(interval=2.0, number=3, start=-1.0, noise=0.0)
+    spec = gated_model([p], [[10.0, 11.0, 30.0]], [1.0], [0.5])
+    o = run_oracle(spec, 60.0)
+    ot, oi = o.netstim_spikes()
+    t1, t3 = delivered([10.5])[0], delivered([30.5])[0]
+    want = chain_after(t1, 2.0, 3) + chain_after(t3, 2.0, 3)
+    assert np.array_equal(ot, np.array(want)), (ot, want)
+    assert o.get("NetStim", "on", 0) == 0.0 and o.get("NetStim", "ispike", 0) == 3.0
+
+
+def test_negative_event_turns_a_running_netstim_off():
+    p = dict(interval=10.0, number=100, start=5.0, noise=0.0)
+    spec = gated_model([p], [[52.0]], [-1.0], [0.0])
+    o = run_oracle(spec, 150.0)
+    ot, _ = o.netstim_spikes()
+    want = delivered([5.0 + 10.0 * k for k in range(5)])
+    assert np.array_equal(ot, want), (ot, want)
+    assert o.get("NetStim", "on", 0) == 0.0 and o.get("NetStim", "ispike", 0) == 5.0
+
+
+def test_fractional_weights_truncate_to_zero():
+    """The weight is read as an int: 0.9 starts nothing, -0.9 stops nothing."""
+    off = dict(interval=2.0, number=3, start=-1.0, noise=0.0)
+    running = dict(interval=10.0, number=6, start=5.0, noise=0.0)
+    spec = gated_model([off, running], [[10.0], [22.0]], [0.9, -0.9], [0.0, 0.0])
+    o = run_oracle(spec, 100.0)
+    ot, oi = o.netstim_spikes()
+    assert ot[oi == 0].size == 0
+    assert ot[oi == 1].size == 6
+
+
+def test_netstim_chain_within_one_step():
+    """A (running) drives B (waiting) with delay 0: B's burst starts in the step of each of
+    A's spikes, including the one at t = 0 delivered during finitialize."""
+    a = dict(interval=10.0, number=3, start=0.0, noise=0.0)
+    b = dict(interval=1.0, number=2, start=-1.0, noise=0.0)
+    spec = gated_model([a, b], [[], []], [0.0, 0.0], [0.0, 0.0], chain=[(0, 1, 1.0, 0.0)])
+    o = run_oracle(spec, 60.0)
+    ot, oi = o.netstim_spikes()
+    ta = delivered([0.0, 10.0, 20.0])
+    assert np.array_equal(ot[oi == 0], ta)
+    want_b = sum((chain_after(t, 1.0, 2) for t in ta), [])
+    assert np.array_equal(ot[oi == 1], np.array(want_b)), (ot[oi == 1], want_b)
