@@ -335,6 +335,8 @@ def main():
     ap.add_argument("--train-tstop", type=float, default=0.0, help="forward run of the training step (ms)")
     ap.add_argument("--cell-groups", type=int, default=0,
                     help="cell groups issued on separate streams (0: the library's choice, 1: one stream)")
+    ap.add_argument("--unit-cells", type=int, default=0,
+                    help="cells per tree-solve wavefront (0: the library's choice)")
     ap.add_argument("--model-root", action="store_true",
                     help="solve each cell toward its model root instead of its centre")
     ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
@@ -371,6 +373,8 @@ def main():
     sim = Sim()
     sim.set_cell_groups(args.cell_groups)
     sim.set_solver_root(not args.model_root)
+    if args.unit_cells:
+        sim.set_solve_unit_cells(args.unit_cells)
     sim.load_model_from_spec(spec)
     t_build = time.perf_counter() - t_build
     groups = sim.info("cell_groups")

@@ -98,7 +98,9 @@ struct StepArgs {
     int cadyn_after;              // update CaDynamics_E2 right after this pass's ica (its state
                                   // depends on ica and cai only, so this is the step's own update)
     int do_current;
-    int write_assigned;           // also store assigned outputs (i, ina, gna, minf, ...)
+    int write_assigned;           // also store the current's assigned outputs (i, ina, gna, ...)
+    int write_rates;              // also store the state update's rates (minf, mtau, ...)
+    int write_dcurdv;             // store the ions' dcurdv (0: it still holds the 0 stored at init)
     unsigned ion_store;           // ion x (0 na, 1 k, 2 ca): bit 2x stores cur, bit 2x+1 stores erev
     unsigned fold_mask;           // point processes whose currents the node kernel adds (bit = MechId)
     int ion_type[3];              // iontype shared by every instance of ion x, or -1 (read per instance)

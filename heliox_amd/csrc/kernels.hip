@@ -77,7 +77,7 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
     sts_(m.col(HH_M) + j, s.m);
     sts_(m.col(HH_H) + j, s.h);
     sts_(m.col(HH_N) + j, s.n);
-    if (A.write_assigned) {
+    if (A.write_rates) {
         double minf, mtau, hinf, htau, ninf, ntau;
         hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
         m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
@@ -92,7 +92,7 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
     cahva_gates_r(v, A.dt, s.m, s.h);
     sts_(m.col(CH_M) + j, s.m);
     sts_(m.col(CH_H) + j, s.h);
-    if (A.write_assigned) {
+    if (A.write_rates) {
         double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
         cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
         m.col(CH_ECA)[j] = ca_erev[ci];
@@ -106,7 +106,7 @@ __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m
     const double vhalfl = ldp(m, HD_VHALFL, j), tau = ldp(m, HD_TAU, j);
     l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
     sts_(m.col(HD_L) + j, l);
-    if (A.write_assigned) {
+    if (A.write_rates) {
         double linf, taul;
         hdla_rate(v, vhalfl, tau, A.c, linf, taul);
         m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul;
@@ -201,7 +201,7 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
 
 __device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {
     if (A.ion_store & (1u << (2 * x))) sts_(ion.col(ION_CUR) + i, cur);
-    if (A.write_assigned) ion.col(ION_DCURDV)[i] = 0.;
+    if (A.write_dcurdv) ion.col(ION_DCURDV)[i] = 0.;
 }
 
 #define HAS(bit) (A.dense_mask & (1u << (bit)))
@@ -310,7 +310,7 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
     const int node = m.node[j];
     const double v = A.v[node];
     if (MECH == M_NA_ION || MECH == M_K_ION || MECH == M_CA_ION) {
-        if (A.do_current) ion_cur(m, j, MECH == M_CA_ION ? 2.0 : 1.0, A.c.ktf, A.write_assigned);
+        if (A.do_current) ion_cur(m, j, MECH == M_CA_ION ? 2.0 : 1.0, A.c.ktf, A.write_dcurdv);
         return;
     }
     const MechDev& na = A.m[M_NA_ION];

@@ -308,6 +308,8 @@ struct hx_sim {
     int pass_cadyn_skip = 0, pass_cadyn_after = 0;
     void refresh_cadyn_eager();
     bool write_assigned = false;
+    bool init_pass = false;              // finitialize's current pass is running
+
     bool need_split_for_monitor = false;
 
     // device
@@ -1669,6 +1671,12 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.do_current = do_current;
     const bool assigned = write_assigned || final_step;
     A.write_assigned = assigned ? 1 : 0;
+    // A call's last step stores the rates once, in its closing state pass (the fused
+    // pass before it updates the previous step's states, whose rates that pass
+    // overwrites).  dcurdv holds the 0 that finitialize's pass stored unless a handle
+    // made every step store the assigned variables.
+    A.write_rates = (write_assigned || (final_step && !do_current)) ? 1 : 0;
+    A.write_dcurdv = (write_assigned || init_pass) ? 1 : 0;
     // An ion's cur and erev are stored when something outside the fused kernel
     // reads them: a mechanism run instance-parallel, CaDynamics_E2 (reads ica in
     // the next state update) or a handle/monitor on an assigned variable.
@@ -1865,7 +1873,8 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     // one step, so a burst is spread over one 1024-thread workgroup per 8192 entries of
     // slot capacity (at most 64); with only VecStim inputs a step's events are few, and
     // one workgroup starts soonest beside the other cell group's kernels (measured:
-    // config 3 ran 2.5% slower with the grid and a merged input kernel).
+    // config 3 ran 2.5% slower with the grid and a merged input kernel, and 3% slower
+    // with 256-thread workgroups).
     const int nblk = pre_fanout_empty ? 1 : std::min(64, (cg.ring.cap + 8191) / 8192);
     launch_deliver(D, nblk, on);
     tend(T_EVENTS, on);
@@ -2433,9 +2442,11 @@ void hx_sim::finitialize(double v_init) {
     launch_detect(0, 0.0);
     launch_events(0, 0.0);
     final_step = true;
+    init_pass = true;
     launch_mech_pass(0, 1, 0.0);
     launch_point_currents(0.0);
     launch_plugin_currents(0.0);
+    init_pass = false;
     final_step = false;
     initialized = true;
     sync_outputs();

@@ -259,3 +259,32 @@ def test_cadynamics_get_array_at_size(gpu_lib):
     # the same values through the ion's own column, by node
     conci = g.get_array("ca_ion", "conci")
     assert np.array_equal(np.sort(conci), np.sort(g.get_array("CaDynamics_E2", "cai")))
+
+
+@pytest.mark.parametrize("config,ncell,chunks", [(3, 2, [10.0, 0.5, 7.25]), (2, 4, [12.0]), (5, 4, [3.0, 3.0])])
+def test_every_column_after_a_run(gpu_lib, config, ncell, chunks):
+    """With no monitor or handle on an assigned variable, a call's last step and its closing
+    state pass store every column once: currents and their assigned outputs from the last
+    current evaluation, rates from the closing state update, ion dcurdv as 0.  Every column
+    of every mechanism then reads back as the oracle's after its last step."""
+    from heliox_amd import mechanisms
+    spec = build_config(config, ncell, sum(chunks))
+    print(f"case every column config={config} chunks={chunks}", flush=True)
+    o, g = run_both(spec, sum(chunks), chunks=chunks)
+    cols = {m.name: m.columns for m in mechanisms() if m.kind == "builtin"}
+    checked = 0
+    for mech in spec.mechs:
+        if mech in ("VecStim", "NetStim"):
+            continue
+        for c in cols[mech]:
+            try:
+                ref = o.array(mech, c)
+            except Exception:
+                continue                    # a column the oracle does not keep
+            got = g.get_array(mech, c)
+            scale = max(1.0, float(np.max(np.abs(ref))))
+            err = float(np.max(np.abs(got - ref)))
+            assert err <= 1e-9 * scale, f"{mech}.{c}: {err}"
+            checked += 1
+    print(f"  {checked} columns", flush=True)
+    assert checked > 20
