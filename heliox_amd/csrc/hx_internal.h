@@ -73,12 +73,21 @@ struct MechDev {
 
 // Global constants of the hot-path mechanisms, computed once on the host
 // with the same expressions the reference evaluates per call.
+constexpr double kFaradayCaDyn = 96485.3321233100184;   // CaDynamics_E2.cu:109
+
 struct MechConsts {
     double hh_q10;                // pow(3, (celsius - 6.3) / 10)            hh_templated.cu:87
     double hd_qt;                 // pow(q10, (celsius - 33) / 10)           hd_la.cu:94
     double hd_ehd, hd_kl, hd_vhalft, hd_a0t, hd_zetat, hd_gmt, hd_qtl;
     double hd_inv_kl;             // 1 / hd_kl
+    int hd_pow;                   // gmt is 0.4: the two exponentials of the rate are G^5 and G^2
+    double hd_k5;                 // 0.0378 zetat / 5, G = exp(hd_k5 (v - vhalft))
     double ktf;                   // 1000 R (celsius + 273.15) / F           eion.cuh:33-36
+    // CaDynamics_E2 with gamma, decay, depth and minCai each one value over the model: its
+    // update is cai + cd_c1 (ica cd_g + cd_min - cai), c1 = 1 - exp(-dt / decay),
+    // g = -1e4 gamma decay / (2 F depth)
+    int cd_uniform;
+    double cd_c1, cd_g, cd_min;
 };
 
 struct StepArgs {

@@ -116,6 +116,7 @@ __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m
 
 // returns the new cai (the caller stores it)
 __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& m, int j, double cai, double ica) {
+    if (A.c.cd_uniform) return cadyn_uniform(cai, ica, A.c);
     return cadyn_step_r(cai, ica, ldp(m, CD_GAMMA, j), ldp(m, CD_DECAY, j), ldp(m, CD_DEPTH, j),
                         ldp(m, CD_MINCAI, j), A.dt);
 }

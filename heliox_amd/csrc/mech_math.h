@@ -20,7 +20,6 @@
 
 namespace hx {
 
-constexpr double kFaradayCaDyn = 96485.3321233100184;   // CaDynamics_E2.cu:109
 
 __device__ __forceinline__ double nernst(double ci, double co, double z, double ktf) {
     if (z == 0) return 0.;
@@ -187,15 +186,27 @@ __device__ __forceinline__ double cadyn_step(double cai, double ica, double gamm
 // multiplications by their reciprocals.  Results differ from the reference
 // forms by a few ulps.  The reference forms stay in use where their
 // intermediate values are outputs (assigned variables) and in the adjoint.
+// a / b from the hardware reciprocal, two Newton steps and a remainder correction: within
+// one ulp of the rounded quotient, for the normal, finite operands the rates produce.
+__device__ __forceinline__ double div_r(double a, double b) {
+    double r = __builtin_amdgcn_rcp(b);
+    double e = fma(-b, r, 1.0);
+    r = fma(r, e, r);
+    e = fma(-b, r, 1.0);
+    r = fma(r, e, r);
+    const double q = a * r;
+    return fma(fma(-b, q, a), r, q);
+}
+
 __device__ __forceinline__ double vtrap_r(double x, double y, double inv_y) {
     const double r = x * inv_y;                      // x / y
     if (fabs(r) < 1e-6) return y * (1 - r * 0.5);
-    return x / (exp(r) - 1);
+    return div_r(x, exp(r) - 1);
 }
 
 __device__ __forceinline__ double gate_step(double x, double a, double b, double k, double dt) {
     const double sum = a + b;
-    return x + (1.0 - exp(-dt * (k * sum))) * (a / sum - x);
+    return x + (1.0 - exp(-dt * (k * sum))) * (div_r(a, sum) - x);
 }
 
 // hh: the three gates of one compartment
@@ -207,7 +218,7 @@ __device__ __forceinline__ double gate_step(double x, double a, double b, double
 __device__ __forceinline__ double vtrap_e(double x, double y, double inv_y, double ex) {   // ex = exp(x / y)
     const double r = x * inv_y;
     if (fabs(r) < 1e-6) return y * (1 - r * 0.5);
-    return x / (ex - 1);
+    return div_r(x, ex - 1);
 }
 
 __device__ __forceinline__ void hh_gates_r(double v, double q10, double dt, double& m, double& h, double& n) {
@@ -219,7 +230,7 @@ __device__ __forceinline__ void hh_gates_r(double v, double q10, double dt, doub
     const double am = 0.1 * vtrap_e(-(v + 40), 10.0, 0.1, E);
     const double bm = 4 * exp(-(v + 65) * (1.0 / 18));
     const double ah = 0.07 * (F2 * F2);
-    const double bh = 1.0 / (E * kExpHalf + 1);
+    const double bh = div_r(1.0, E * kExpHalf + 1);
     const double an = 0.01 * vtrap_e(-(v + 55), 10.0, 0.1, E * kExpMinus3Half);
     const double bn = 0.125 * F;
     m = gate_step(m, am, bm, q10, dt);
@@ -232,28 +243,44 @@ __device__ __forceinline__ void cahva_gates_r(double v, double dt, double& m, do
     const double ma = 0.055 * vtrap_r(-27.0 - v, 3.8, 1.0 / 3.8);
     const double mb = 0.94 * exp((-75.0 - v) * (1.0 / 17.0));
     const double ha = 0.000457 * exp((-13.0 - v) * 0.02);
-    const double hb = 0.0065 / (exp((-v - 15.0) * (1.0 / 28.0)) + 1.0);
+    const double hb = div_r(0.0065, exp((-v - 15.0) * (1.0 / 28.0)) + 1.0);
     m = gate_step(m, ma, mb, 1.0, dt);
     h = gate_step(h, ha, hb, 1.0, dt);
 }
 
 // hd_la: l + (1 - exp(-dt / taul)) (linf - l) with -dt / taul folded into one division
+// With gmt = 0.4 (the model's value), bett = G^2 and a = G^5 for G = exp(0.0378 zetat
+// (v - vhalft) / 5): one exponential instead of two, a few ulps from the two-call form.
 __device__ __forceinline__ double hdla_gate_r(double v, double l, double vhalfl, double tau, const MechConsts& c,
                                               double dt) {
-    const double a = exp(0.0378 * c.hd_zetat * (v - c.hd_vhalft));
-    const double linf = 1.0 / (1.0 + exp(-(v - vhalfl) * c.hd_inv_kl));
-    const double bett = exp(0.0378 * c.hd_zetat * c.hd_gmt * (v - c.hd_vhalft));
-    const double rate = (c.hd_qtl * c.hd_qt * c.hd_a0t * (1.0 + a)) / (tau * bett);   // 1 / taul
+    double a, bett;
+    if (c.hd_pow) {
+        const double G = exp(c.hd_k5 * (v - c.hd_vhalft));
+        bett = G * G;
+        a = bett * bett * G;
+    } else {
+        a = exp(0.0378 * c.hd_zetat * (v - c.hd_vhalft));
+        bett = exp(0.0378 * c.hd_zetat * c.hd_gmt * (v - c.hd_vhalft));
+    }
+    const double linf = div_r(1.0, 1.0 + exp(-(v - vhalfl) * c.hd_inv_kl));
+    const double rate = div_r(c.hd_qtl * c.hd_qt * c.hd_a0t * (1.0 + a), tau * bett);   // 1 / taul
     return l + (1.0 - exp(-dt * rate)) * (linf - l);
 }
 
 // CaDynamics_E2: steady_term = -(drive - (-minCai)/decay) / (-1/decay) = drive decay + minCai
+// (with its parameters one value over the model, cadyn_uniform below)
 __device__ __forceinline__ double cadyn_step_r(double cai, double ica, double gamma, double decay, double depth,
                                                double minCai, double dt) {
     const double drive_ica = -(10000.0) * (ica * gamma) / (2.0 * kFaradayCaDyn * depth);
     const double exp_factor = exp(-dt / decay);
     const double steady_term = drive_ica * decay + minCai;
     return cai + (1.0 - exp_factor) * (steady_term - cai);
+}
+
+// The same update with its per-model constants made on the host (MechConsts::cd_*):
+// cai + c1 (ica g + minCai - cai); a few ulps from cadyn_step_r.
+__device__ __forceinline__ double cadyn_uniform(double cai, double ica, const MechConsts& c) {
+    return cai + c.cd_c1 * (ica * c.cd_g + c.cd_min - cai);
 }
 
 // ---------------- synapses ----------------

@@ -1715,6 +1715,20 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.c.hd_zetat = G(M_HDLA, "zetat", 2.2);
     A.c.hd_gmt = G(M_HDLA, "gmt", 0.4);
     A.c.hd_qtl = G(M_HDLA, "qtl", 1.0);
+    A.c.hd_pow = A.c.hd_gmt == 0.4 ? 1 : 0;
+    A.c.hd_k5 = 0.0378 * A.c.hd_zetat * 0.2;
+    {
+        const HostMech& cd = mech[M_CADYN];
+        const unsigned all = (1u << CD_GAMMA) | (1u << CD_DECAY) | (1u << CD_DEPTH) | (1u << CD_MINCAI);
+        A.c.cd_uniform = cd.present && cd.n > 0 && uniform_on && (cd.dev.umask & all) == all ? 1 : 0;
+        if (A.c.cd_uniform) {
+            const double gamma = cd.col[CD_GAMMA][0], decay = cd.col[CD_DECAY][0];
+            const double depth = cd.col[CD_DEPTH][0];
+            A.c.cd_c1 = 1.0 - std::exp(-dt / decay);
+            A.c.cd_g = -(10000.0) * gamma / (2.0 * kFaradayCaDyn * depth) * decay;
+            A.c.cd_min = cd.col[CD_MINCAI][0];
+        }
+    }
     const double R = 1.380649e-23 * 6.02214076e+23, F = 1.602176634e-19 * 6.02214076e+23;
     A.c.ktf = 1000. * R * (celsius + 273.15) / F;
     return A;

@@ -28,18 +28,39 @@ def run(spec, tstop, uniform=True, mons=None, edit=None):
 
 
 def test_scalar_reads_give_the_same_bits(gpu_lib):
+    """With CaDynamics_E2 per instance (one gamma moved by 1e-7), the other uniform
+    columns read as scalars give the same bits as per-instance reads."""
     spec = build_config(3, 2, 5.0)
+    g = spec.mechs["CaDynamics_E2"].params["gamma"]
+    g[0] *= 1.0000001
     mons = [("global", "v", 0), ("global", "v", spec.nnode - 1), ("hh", "m", 7), ("CaDynamics_E2", "cai", 9)]
     print("case uniform columns config3 2 cells", flush=True)
     a = run(spec, 5.0, True, mons)
     b = run(spec, 5.0, False, mons)
     # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2
-    # gamma/decay/depth/minCai, and the erev of na and k (style 0: no kernel writes it);
-    # ca's conco is rewritten at finitialize (style 04) and stays per instance
-    assert a.info("uniform_columns") == 13
+    # decay/depth/minCai (gamma made per instance here), and the erev of na and k (style 0:
+    # no kernel writes it); ca's conco is rewritten at finitialize (style 04) and stays per
+    # instance
+    assert a.info("uniform_columns") == 12
     assert b.info("uniform_columns") == 0
-    assert a.info("uniform_bytes") == 13 * 8 * spec.nnode
+    assert a.info("uniform_bytes") == 12 * 8 * spec.nnode
     assert np.array_equal(a.traces(), b.traces())
+
+
+def test_uniform_calcium_constants_agree_to_rounding(gpu_lib):
+    """With all four CaDynamics_E2 parameters one value over the model, its update uses
+    constants made once on the host (1 - exp(-dt/decay) and the drive factor): the same
+    results as the per-instance form to rounding."""
+    spec = build_config(3, 2, 5.0)
+    mons = [("global", "v", 0), ("global", "v", spec.nnode - 1), ("CaDynamics_E2", "cai", 9),
+            ("CaDynamics_E2", "cai", spec.nnode - 3)]
+    print("case uniform CaDynamics_E2 constants", flush=True)
+    a = run(spec, 5.0, True, mons)
+    b = run(spec, 5.0, False, mons)
+    assert a.info("uniform_columns") == 13
+    ta, tb = a.traces(), b.traces()
+    assert np.max(np.abs(ta[:2] - tb[:2])) < 1e-9
+    assert np.max(np.abs(ta[2:] - tb[2:]) / np.abs(tb[2:])) < 1e-12
 
 
 def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
