@@ -301,6 +301,49 @@ def lrds_bench(args):
         "roofline": roofline, "cpu_baseline": cpu}))
 
 
+VECPLAY_BYTES_PER_ITEM = 136   # item record read and written (2 x 48), tvec/yvec reads (32), target (8)
+
+
+def network_bench(args):
+    """Config 4 at full size: 10,000 cells x 200 compartments, 100 netcons per cell (1e6,
+    delays 1-5 ms), 500 gap-junction pairs, VecPlay current into 500 cells.  A step is one
+    step of the whole network; the line reports the step rate and each kernel class's
+    time per launch (HIP events on the library stream), VecPlay among them."""
+    import torch
+    from heliox_amd import Sim, build_config
+    dt = 0.025
+    spec = build_config(4, args.network_cells, (args.warmup + args.steps + 10) * dt)
+    sim = Sim()
+    sim.load_model_from_spec(spec, add_monitors=False)
+    sim.finitialize(-65.0)
+    sim.continue_run((args.warmup + 0.5) * dt)
+    sim.set_profiling(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    sim.continue_run((args.steps + 0.5) * dt)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    spikes = sim.spikes()[0].size
+    sim.set_profiling(True)
+    sim.continue_run((args.steps + 0.5) * dt)
+    kernels = {}
+    for k in ("mech", "sparse", "point", "solve", "spike", "events", "other"):
+        ms, n = sim.kernel_time(k)
+        if n:
+            kernels[k] = {"ms_total": ms, "launches": n, "us_per_launch": ms * 1e3 / n}
+    nvp = len(spec.vecplay)
+    print(json.dumps({
+        "metric": "compartment-steps/s (config 4 network, 10000x200-comp fp64)",
+        "value": spec.nnode * args.steps / wall, "unit": "compartment-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+        "config": {"workload": f"config 4: {spec.ncell} cells x {spec.nnode // spec.ncell} compartments, "
+                               f"{spec.netcons['ExpSyn'].inst.size} netcons, {spec.gap_src_node.size} gap halves, "
+                               f"{nvp} VecPlay items", "spikes_in_timed_steps": spikes},
+        "kernel_times": kernels,
+        "vecplay": {"items": nvp, "alg_bytes_per_launch": nvp * VECPLAY_BYTES_PER_ITEM}}))
+
+
 def calibrate_copy(gib: float = 1.0, reps: int = 5):
     """A plain device copy of known size, for scaling rocprof FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -339,6 +382,8 @@ def main():
                     help="cells per tree-solve wavefront (0: the library's choice)")
     ap.add_argument("--model-root", action="store_true",
                     help="solve each cell toward its model root instead of its centre")
+    ap.add_argument("--network", action="store_true", help="time the full-size config-4 network instead")
+    ap.add_argument("--network-cells", type=int, default=10000)
     ap.add_argument("--lrds", action="store_true", help="time the LRDS replay of the learn surface instead")
     ap.add_argument("--lrds-n", type=int, default=2048)
     ap.add_argument("--lrds-ticks", type=int, default=256)
@@ -363,6 +408,9 @@ def main():
         return
     if args.lrds:
         lrds_bench(args)
+        return
+    if args.network:
+        network_bench(args)
         return
 
     from heliox_amd import Sim, build_config
