@@ -181,9 +181,14 @@ struct EventRing {
     unsigned* done;               // workgroups of the delivery launch that have finished (then back to 0)
 };
 
-// A packed fan-out target: bits 30-31 its kind (0 ExpSyn, 1 Exp2Syn, 2 NetStim), bits
-// 0-29 the instance.  Kind 2 sets the sign bit, so the kind is read with an unsigned shift.
+// A packed fan-out target: bits 30-31 its kind (0 ExpSyn, 1 Exp2Syn, 2 NetStim, 3 a synapse
+// plugin), bits 0-29 the instance (for kind 3: bits 26-29 the plugin's synapse slot, bits
+// 0-25 the instance).  Kinds 2 and 3 set the sign bit, so the kind is read with an unsigned
+// shift.
 constexpr int kTargetNetStim = 2;
+constexpr int kTargetPlugin = 3;
+constexpr int kMaxPostsyn = 4;          // synapse plugins one model may use
+constexpr int kPostsynSlotShift = 26;
 __host__ __device__ inline int pack_target(int kind, int inst) {
     return static_cast<int>((static_cast<unsigned>(kind) << 30) | static_cast<unsigned>(inst));
 }
@@ -292,6 +297,7 @@ struct NsArgs {
 struct DeliverArgs {
     EventRing ring;
     int k;
+    int* plugin_recv[kMaxPostsyn];    // events per instance of each synapse plugin (kind 3)
     MechDev es;                   // ExpSyn
     MechDev e2;                   // Exp2Syn
     const double* es_weight;

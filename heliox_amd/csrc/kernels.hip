@@ -1212,6 +1212,9 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
         const int inst = packed & 0x3fffffff;
         if (type == 0) {
             atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
+        } else if (type == kTargetPlugin) {   // counted; the plugin's NET_RECEIVE kernel follows
+            atomicAdd(&D.plugin_recv[(inst >> kPostsynSlotShift) & (kMaxPostsyn - 1)]
+                                    [inst & ((1 << kPostsynSlotShift) - 1)], 1);
         } else if (type == 1) {            // (NetStim targets go to their own inbox)
             const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
             atomicAdd(&D.e2.col(E2_A)[inst], wf);

@@ -19,11 +19,15 @@
 //       returns the membrane current (mA/cm2, or nA for a point process) at v and adds
 //       its ion currents to io.cur[ion]; it may store assigned variables
 //   __device__ static void state(Inst&, double v, const IonIO&, const Env&);
-// and is registered in a source file under csrc/mechs/ with HX_REGISTER_MECHANISM(Struct)
+// and, with kPostsyn in kFlags (a synapse that netcons target; the reference's
+// REGISTER_POSTSYN, mechanism.h:173 / postsyn_template.cuh:6-51),
+//   __device__ static void net_receive(Inst&, double weight, double delay, const Env&);
+// It is registered in a source file under csrc/mechs/ with HX_REGISTER_MECHANISM(Struct)
 // (plugin_kernels.h).  The library then runs it with instance-parallel kernels: the
 // finite-difference Jacobian of the current (mech_template.cuh:616-646), the current and
-// ion current accumulation after the built-in mechanisms of each current pass, and the
-// state update after the solve of each step.
+// ion current accumulation after the built-in mechanisms of each current pass, the state
+// update after the solve of each step, and, for a synapse, NET_RECEIVE of the step's
+// events after the built-in synapses' delivery.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -32,7 +36,7 @@
 namespace hx {
 
 namespace plugin {
-constexpr unsigned kPoint = 1u, kElectrode = 2u;
+constexpr unsigned kPoint = 1u, kElectrode = 2u, kPostsyn = 4u;
 constexpr unsigned kNa = 1u, kK = 2u, kCa = 4u;   // ion bits, in the ion index order na, k, ca
 
 // One instance's columns: x[c] is column c of this instance.
@@ -64,6 +68,11 @@ struct PluginArgs {
     double* rhs;
     const double* area;
     double t, dt, celsius;
+    // synapses: events of the step per instance (counted by the delivery kernel), and the
+    // weight and delay of each instance's netcon (one netcon per instance)
+    int* recv_count;
+    const double* recv_w;
+    const double* recv_delay;
 };
 
 // What the registration records: the metadata the builder and the handles need, and
@@ -77,6 +86,7 @@ struct PluginMeta {
     void (*launch_init)(const PluginArgs&, hipStream_t);
     void (*launch_current)(const PluginArgs&, hipStream_t);
     void (*launch_state)(const PluginArgs&, hipStream_t);
+    void (*launch_receive)(const PluginArgs&, hipStream_t);   // synapses only, else nullptr
 };
 
 // Registers a plugin (from a static initializer); returns true.

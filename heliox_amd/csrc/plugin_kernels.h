@@ -84,6 +84,20 @@ __global__ void __launch_bounds__(kBlock) k_plugin_state(PluginArgs P) {
     M::state(x, P.v[P.m.node[j]], io, plugin::Env{P.t, P.dt, P.celsius});
 }
 
+// NET_RECEIVE (postsyn_template.cuh:20-51): an instance has one netcon, so the step's
+// events into it are alike; they are received one after another, as many as arrived.
+template <class M>
+__global__ void __launch_bounds__(kBlock) k_plugin_receive(PluginArgs P) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= P.m.n) return;
+    const int n = P.recv_count[j];
+    if (n == 0) return;
+    plugin::Inst x{P.m.base, P.m.stride, j};
+    const plugin::Env env{P.t, P.dt, P.celsius};
+    for (int e = 0; e < n; ++e) M::net_receive(x, P.recv_w[j], P.recv_delay[j], env);
+    P.recv_count[j] = 0;
+}
+
 inline dim3 plugin_grid(int n) { return dim3(static_cast<unsigned>(n > 0 ? (n + kBlock - 1) / kBlock : 1)); }
 
 template <class M>
@@ -100,14 +114,21 @@ void launch_state(const PluginArgs& P, hipStream_t s) {
 }
 
 template <class M>
+void launch_receive(const PluginArgs& P, hipStream_t s) {
+    if (P.m.n > 0) hipLaunchKernelGGL(k_plugin_receive<M>, plugin_grid(P.m.n), dim3(kBlock), 0, s, P);
+}
+
+template <class M>
 PluginMeta meta_of() {
     static_assert(sizeof(M::kCols) / sizeof(M::kCols[0]) == sizeof(M::kDefault) / sizeof(M::kDefault[0]),
                   "one default per column");
     static_assert(M::kParams + M::kStates <= static_cast<int>(sizeof(M::kCols) / sizeof(M::kCols[0])),
                   "parameters and states are columns");
+    void (*recv)(const PluginArgs&, hipStream_t) = nullptr;
+    if constexpr ((M::kFlags & plugin::kPostsyn) != 0) recv = &launch_receive<M>;
     return PluginMeta{M::kName, static_cast<int>(sizeof(M::kCols) / sizeof(M::kCols[0])), M::kParams, M::kStates,
                       M::kCols, M::kDefault, M::kFlags, M::kIonRead, M::kIonWrite, &launch_init<M>,
-                      &launch_current<M>, &launch_state<M>};
+                      &launch_current<M>, &launch_state<M>, recv};
 }
 
 }  // namespace plugin_detail

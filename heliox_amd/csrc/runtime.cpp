@@ -180,7 +180,9 @@ struct HostMech {
     MechDev dev;
 };
 
+// mech: a MechId, or kPluginMechBase + the index of a synapse plugin in the model
 struct NetCon { int src_kind; int src; int mech; int inst; double weight; double delay; };
+constexpr int kPluginMechBase = 1000;
 
 struct VecPlayHost {
     std::string mech, var;
@@ -252,7 +254,16 @@ struct hx_sim {
     struct PluginInst {
         const PluginMeta* meta = nullptr;
         HostMech h;
+        int slot = -1;                            // synapse plugins: slot of the packed targets
+        int* d_recv_count = nullptr;              // events of the step per instance
+        double* d_recv_w = nullptr;               // the instance's netcon weight and delay
+        double* d_recv_delay = nullptr;
     };
+    bool has_postsyn_plugins() const {
+        for (const auto& p : plugins)
+            if (p.meta->flags & plugin::kPostsyn) return true;
+        return false;
+    }
     std::vector<PluginInst> plugins;
     PluginInst* plugin_named(const std::string& name) {
         for (auto& p : plugins)
@@ -1090,11 +1101,29 @@ void hx_sim::upload() {
     std::vector<std::vector<std::pair<int, double>>> pre_fo(npre), vs_fo(nvs + nns), dyn_fo(ndyn);
     std::vector<double> esw(mech[M_EXPSYN].present ? mech[M_EXPSYN].n : 0, 0.0);
     std::vector<double> e2w(mech[M_EXP2SYN].present ? mech[M_EXP2SYN].n : 0, 0.0);
+    // synapse plugins: a slot each, and their instances' netcon weights and delays
+    std::vector<std::vector<double>> plugin_w, plugin_delay;
+    for (auto& p : plugins) {
+        p.slot = -1;
+        if (!(p.meta->flags & plugin::kPostsyn)) continue;
+        p.slot = static_cast<int>(plugin_w.size());
+        if (p.slot >= kMaxPostsyn)
+            throw std::runtime_error("a model may use at most " + std::to_string(kMaxPostsyn) + " synapse plugins");
+        if (p.h.n >= (1 << kPostsynSlotShift)) throw std::runtime_error("too many instances of a synapse plugin");
+        plugin_w.emplace_back(p.h.n, 0.0);
+        plugin_delay.emplace_back(p.h.n, 0.0);
+    }
     max_delay = 0;
     for (auto& kv : by_syn) {
         const NetCon& nc = kv.second;
         int packed;
-        if (nc.mech == M_NETSTIM) {
+        if (nc.mech >= kPluginMechBase) {
+            PluginInst& p = plugins[nc.mech - kPluginMechBase];
+            const int dinst = p.h.perm[nc.inst];
+            packed = pack_target(kTargetPlugin, (p.slot << kPostsynSlotShift) | dinst);
+            plugin_w[p.slot][dinst] = nc.weight;
+            plugin_delay[p.slot][dinst] = nc.delay;
+        } else if (nc.mech == M_NETSTIM) {
             packed = pack_target(kTargetNetStim, ns_dyn[nc.inst]);
         } else {
             const int dinst = mech[nc.mech].perm[nc.inst];
@@ -1115,8 +1144,17 @@ void hx_sim::upload() {
         auto check = [&](const std::vector<std::vector<std::pair<int, double>>>& fo) {
             for (const auto& v : fo)
                 for (const auto& pr : v) {
-                    const int kind = target_kind(pr.first), inst = target_inst(pr.first);
-                    const int lim = kind == 0 ? nes : kind == 1 ? ne2 : kind == kTargetNetStim ? ndyn : 0;
+                    const int kind = target_kind(pr.first);
+                    int inst = target_inst(pr.first), lim = 0;
+                    if (kind == 0) lim = nes;
+                    else if (kind == 1) lim = ne2;
+                    else if (kind == kTargetNetStim) lim = ndyn;
+                    else {
+                        const int slot = inst >> kPostsynSlotShift;
+                        inst &= (1 << kPostsynSlotShift) - 1;
+                        for (const auto& p : plugins)
+                            if (p.slot == slot) lim = p.h.n;
+                    }
                     if (inst < 0 || inst >= lim) throw std::runtime_error("internal: bad fan-out target");
                 }
         };
@@ -1140,6 +1178,13 @@ void hx_sim::upload() {
     }
     d_es_weight = dupload(owned, esw);
     d_e2_weight = dupload(owned, e2w);
+    for (auto& p : plugins) {
+        if (p.slot < 0) continue;
+        p.d_recv_w = dupload(owned, plugin_w[p.slot]);
+        p.d_recv_delay = dupload(owned, plugin_delay[p.slot]);
+        p.d_recv_count = dalloc<int>(owned, std::max(p.h.n, 1));
+        HXC(hipMemset(p.d_recv_count, 0, sizeof(int) * std::max(p.h.n, 1)));
+    }
     nsa = NsArgs{};
     nsa.n = ndyn;
     if (ndyn > 0) {
@@ -1807,6 +1852,9 @@ PluginArgs hx_sim::plugin_args(const PluginInst& p, double tcur) const {
     P.t = tcur;
     P.dt = dt;
     P.celsius = celsius;
+    P.recv_count = p.d_recv_count;
+    P.recv_w = p.d_recv_w;
+    P.recv_delay = p.d_recv_delay;
     return P;
 }
 
@@ -1835,7 +1883,8 @@ void hx_sim::launch_events(int kk, double tk) {
 
 // VecStim input and delivery of step kk for one cell group's synapses.
 void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
-    const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present;
+    const bool psyn = has_postsyn_plugins();
+    const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present || psyn;
     if (!syn && nsa.n == 0) return;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
@@ -1878,6 +1927,8 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     D.e2 = mech[M_EXP2SYN].dev;
     D.es_weight = d_es_weight;
     D.e2_weight = d_e2_weight;
+    for (const auto& p : plugins)
+        if (p.slot >= 0) D.plugin_recv[p.slot] = p.d_recv_count;
     if (tape_on && tape_n < tape_cap) {
         D.log_count = d_tape_evn + tape_n;
         D.log = d_tape_ev + static_cast<size_t>(tape_n) * tape_evcap;
@@ -1891,6 +1942,9 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     // with 256-thread workgroups).
     const int nblk = pre_fanout_empty ? 1 : std::min(64, (cg.ring.cap + 8191) / 8192);
     launch_deliver(D, nblk, on);
+    // the synapse plugins' NET_RECEIVE of what was counted (one group: plugins couple the model)
+    for (const auto& p : plugins)
+        if (p.slot >= 0) p.meta->launch_receive(plugin_args(p, tk), on);
     tend(T_EVENTS, on);
 }
 
@@ -2439,6 +2493,8 @@ void hx_sim::finitialize(double v_init) {
     }
     launch_clear_ints(d_pre_flag, npre, stream);
     launch_clear_ints(d_spk_count, 1, stream);
+    for (const auto& p : plugins)
+        if (p.d_recv_count) launch_clear_ints(p.d_recv_count, p.h.n, stream);
     upload_ns_dyn_state();
     if (tape_on) {
         tape_n = 0;
@@ -2690,10 +2746,19 @@ int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
 
 int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double w, double delay) {
     if (sim->loaded) return sim->fail("model already loaded");
-    const int id = mech_id(target ? target : "");
-    if (id != M_EXPSYN && id != M_EXP2SYN && id != M_NETSTIM)
-        return sim->fail("netcon target must be ExpSyn, Exp2Syn or NetStim");
-    if (!sim->mech[id].present || inst < 0 || inst >= sim->mech[id].n) return sim->fail("netcon target instance out of range");
+    int id = mech_id(target ? target : "");
+    if (id < 0) {                     // a synapse plugin
+        hx_sim::PluginInst* p = sim->plugin_named(target ? target : "");
+        if (!p || !(p->meta->flags & plugin::kPostsyn))
+            return sim->fail("netcon target must be ExpSyn, Exp2Syn, NetStim or a synapse plugin");
+        if (inst < 0 || inst >= p->h.n) return sim->fail("netcon target instance out of range");
+        id = kPluginMechBase + static_cast<int>(p - sim->plugins.data());
+    } else {
+        if (id != M_EXPSYN && id != M_EXP2SYN && id != M_NETSTIM)
+            return sim->fail("netcon target must be ExpSyn, Exp2Syn, NetStim or a synapse plugin");
+        if (!sim->mech[id].present || inst < 0 || inst >= sim->mech[id].n)
+            return sim->fail("netcon target instance out of range");
+    }
     if (src_kind == 0 && (src < 0 || src >= static_cast<int>(sim->pre_node.size())))
         return sim->fail("netcon source detector out of range");
     if (src_kind == 1 && (!sim->mech[M_VECSTIM].present || src < 0 || src >= sim->mech[M_VECSTIM].n))

@@ -39,6 +39,9 @@ Parity status of each oracle function (``tests/test_oracle_pinning.py`` unless n
                          int-truncated weights, chains within one step)
   Im ................... pinned: m relaxation to the logistic m_inf with the
                          sech-form tau under clamp, ik into k_ion.cur
+  syn_record ........... pinned: an event's AMPA / NMDA (or GABA) share, the
+                         normalised two-exponential conductances, the
+                         Jahr-Stevens block in the current, the tau clamp
 """
 from __future__ import annotations
 

@@ -34,6 +34,7 @@
 //                          by Salmon et al., SC11), netcon events included; every
 //                          processed event keeps the delivery loop going
 //   Im ................... src/mech/user-mech/Im.cu:9-130
+//   syn_record ........... src/spike/user_postsyn_mech/syn_record.cuh:8-203
 //   VecPlay .............. src/vecplay.cu:19-111
 //   Adam ................. src/optimizer/optimizer.cpp:351-413
 //
@@ -818,9 +819,97 @@ struct ImMech : TMech {
     }
 };
 
+// ---------------------------------------------------------------------------
+// syn_record: AMPA + NMDA (excitatory, w > 0) or GABA (w <= 0) double-exponential
+// synapse, a postsyn point process (user_postsyn_mech/syn_record.cuh:8-203); run by the
+// library through its mechanism plugin seam
+// ---------------------------------------------------------------------------
+struct SynRecord : TMech {
+    SynRecord() { name = "syn_record"; point_process = true; }
+    void alloc() override {
+        for (auto c : {"AMPA_tau1", "AMPA_tau2", "NMDA_tau1", "NMDA_tau2", "GABA_tau1", "GABA_tau2", "AMPA_e",
+                       "NMDA_e", "GABA_e", "NMDA_C", "NMDA_rho"})
+            ensure(c, 0.0);
+        ensure("w", 1.0); ensure("r_na", 2.0); ensure("dv", 1e-3); ensure("Use_e", 1.0); ensure("Use_i", 1.0);
+        ensure("Dep", 0.0); ensure("Fac", 0.0); ensure("u0", 0.0);
+        for (auto c : {"i", "AMPA_g", "NMDA_g", "GABA_g", "v_prev", "didv", "pure_i", "g_mul", "dgdv", "dgdg", "Use",
+                       "AMPA_A", "AMPA_B", "NMDA_A", "NMDA_B", "GABA_A", "GABA_B", "AMPA_factor", "NMDA_factor",
+                       "GABA_factor"})
+            ensure(c, 0.0);
+    }
+    double& X(const char* c, int i) { return C(c)[i]; }
+    double sigma(double v, int i) { return 1.0 / (1.0 + X("NMDA_C", i) * std::exp(-X("NMDA_rho", i) * v)); }
+    void init(const double*) override {                 // syn_record.cuh:104-125
+        for (int i = 0; i < n; ++i) {
+            auto pair = [&](const char* tau1, const char* tau2, const char* A, const char* B, const char* factor) {
+                double t1 = X(tau1, i), t2 = X(tau2, i);
+                if (t1 / t2 > 0.9999) { t1 = 0.9999 * t2; X(tau1, i) = t1; }
+                if (t1 / t2 < 1e-9) { t1 = 1e-9 * t2; X(tau1, i) = t1; }
+                X(A, i) = 0.0; X(B, i) = 0.0;
+                double tp = (t1 * t2) / (t2 - t1) * std::log(t2 / t1);
+                X(factor, i) = 1.0 / (-std::exp(-tp / t1) + std::exp(-tp / t2));
+            };
+            pair("AMPA_tau1", "AMPA_tau2", "AMPA_A", "AMPA_B", "AMPA_factor");
+            pair("NMDA_tau1", "NMDA_tau2", "NMDA_A", "NMDA_B", "NMDA_factor");
+            pair("GABA_tau1", "GABA_tau2", "GABA_A", "GABA_B", "GABA_factor");
+            X("Use", i) = X("w", i) > 0.0 ? X("Use_e", i) : X("Use_i", i);
+        }
+    }
+    double cur(int i, double v, double, bool) override {   // syn_record.cuh:128-148
+        X("v_prev", i) = v;
+        double current = 0.0;
+        if (X("w", i) > 0.0) {
+            X("AMPA_g", i) = X("AMPA_B", i) - X("AMPA_A", i);
+            X("NMDA_g", i) = X("NMDA_B", i) - X("NMDA_A", i);
+            double s = sigma(v, i);
+            current = std::fabs(X("w", i)) *
+                      (X("AMPA_g", i) * (v - X("AMPA_e", i)) + X("NMDA_g", i) * s * (v - X("NMDA_e", i)));
+        } else {
+            X("GABA_g", i) = X("GABA_B", i) - X("GABA_A", i);
+            current = std::fabs(X("w", i)) * X("GABA_g", i) * (v - X("GABA_e", i));
+        }
+        X("i", i) = current;
+        return current;
+    }
+    void state(const double* vv, double dt, double) override {   // syn_record.cuh:151-178
+        for (int i = 0; i < n; ++i) {
+            auto decay = [&](const char* x, const char* tau) { X(x, i) *= std::exp(-dt / X(tau, i)); };
+            decay("AMPA_A", "AMPA_tau1"); decay("AMPA_B", "AMPA_tau2");
+            decay("NMDA_A", "NMDA_tau1"); decay("NMDA_B", "NMDA_tau2");
+            decay("GABA_A", "GABA_tau1"); decay("GABA_B", "GABA_tau2");
+            const double v = vv[node[i]];
+            const double w = X("w", i);
+            if (w > 0.0) {
+                X("didv", i) = std::fabs(w) * (X("AMPA_g", i) + X("NMDA_g", i) * sigma(X("v_prev", i), i));
+                X("pure_i", i) = X("AMPA_g", i) * (v - X("AMPA_e", i)) +
+                                 X("NMDA_g", i) * sigma(X("v_prev", i), i) * (v - X("NMDA_e", i));
+                X("g_mul", i) = std::fabs(w) * X("NMDA_g", i) * (v - X("NMDA_e", i));
+                X("dgdv", i) = (sigma(X("v_prev", i) + X("dv", i), i) - sigma(X("v_prev", i), i)) / X("dv", i);
+                X("dgdg", i) = 0.0;
+            } else {
+                X("didv", i) = std::fabs(w) * X("GABA_g", i);
+                X("pure_i", i) = -X("GABA_g", i) * (v - X("GABA_e", i));
+                X("g_mul", i) = X("dgdv", i) = X("dgdg", i) = 0.0;
+            }
+        }
+    }
+    void receive(int isyn, double w_event) {            // syn_record.cuh:181-199
+        if (X("w", isyn) > 0.0) {
+            double ra = X("r_na", isyn);
+            double a_fac = w_event * X("AMPA_factor", isyn) / (1.0 + ra);
+            double n_fac = w_event * X("NMDA_factor", isyn) * ra / (1.0 + ra);
+            X("AMPA_A", isyn) += a_fac; X("AMPA_B", isyn) += a_fac;
+            X("NMDA_A", isyn) += n_fac; X("NMDA_B", isyn) += n_fac;
+        } else {
+            double g_fac = w_event * X("GABA_factor", isyn);
+            X("GABA_A", isyn) += g_fac; X("GABA_B", isyn) += g_fac;
+        }
+    }
+};
+
 // CoreNEURON type order used by the oracle (NEURON built-ins, then user mechanisms).
 const char* kMechOrder[] = {"pas", "na_ion", "k_ion", "hh", "IClamp", "ExpSyn", "Exp2Syn", "VecStim", "NetStim",
-                            "ca_ion", "CaDynamics_E2", "Ca_HVA", "HalfGap", "hd_la", "Im"};
+                            "ca_ion", "CaDynamics_E2", "Ca_HVA", "HalfGap", "hd_la", "Im", "syn_record"};
 
 std::unique_ptr<Mech> make_mech(const std::string& nm) {
     if (nm == "na_ion") return std::make_unique<Ion>("na_ion", 1.0, 10.0, 140.0);
@@ -838,6 +927,7 @@ std::unique_ptr<Mech> make_mech(const std::string& nm) {
     if (nm == "VecStim") return std::make_unique<VecStim>();
     if (nm == "NetStim") return std::make_unique<NetStim>();
     if (nm == "Im") return std::make_unique<ImMech>();
+    if (nm == "syn_record") return std::make_unique<SynRecord>();
     return nullptr;
 }
 
@@ -1074,6 +1164,12 @@ void Model::network_spike_receive() {         // simulate.cpp:916-939
                     int isyn = (int)ps.receive_idx[i];
                     es->receive(isyn, ps.weight[isyn]);
                 }
+            } else if (ps.mech->name == "syn_record") {
+                auto* sr = static_cast<SynRecord*>(ps.mech);
+                for (int i = 0; i < ps.receive_count; i++) {
+                    int isyn = (int)ps.receive_idx[i];
+                    sr->receive(isyn, ps.weight[isyn]);
+                }
             }
         }
     } while (hasSent);
@@ -1267,7 +1363,7 @@ static int finalize_model(Model* m) {
         if (mm->write_state_ion) m->state_ion_first.push_back(mm);
         if (!mm->is_ion && !mm->write_state_ion) m->state_rest.push_back(mm);
         std::string s = nm;
-        if (s == "ExpSyn" || s == "Exp2Syn" || s == "VecStim" || s == "NetStim") {
+        if (s == "ExpSyn" || s == "Exp2Syn" || s == "VecStim" || s == "NetStim" || s == "syn_record") {
             Model::PostSynState ps;
             ps.mech = mm;
             ps.type_id = type_id;

@@ -92,3 +92,74 @@ def test_adjoint_refuses_plugins(gpu_lib):
     g.load_model_from_spec(with_im(build_config(1, 4, 10.0)))
     with pytest.raises(HelioxError, match="plugin"):
         g.tape_begin(10)
+
+
+# ---------------------------------------------------------------------------
+# syn_record (user_postsyn_mech/syn_record.cuh): a synapse plugin that netcons target
+# ---------------------------------------------------------------------------
+SR_TAUS = {"AMPA_tau1": 0.2, "AMPA_tau2": 1.7, "NMDA_tau1": 2.0, "NMDA_tau2": 30.0, "GABA_tau1": 0.5,
+           "GABA_tau2": 6.0}
+
+
+def with_syn_record(spec, nsyn_per_cell=6, seed=5, drive="vecstim"):
+    """syn_record instances on random nodes of every cell, two thirds excitatory; driven by
+    VecStim trains (drive="vecstim") or by the other cells' detectors (drive="cells")."""
+    from heliox_amd.spec import NetConSpec
+    rng = np.random.default_rng(seed)
+    cell = spec.cell_of_node()
+    nodes = []
+    for c in range(spec.ncell):
+        own = np.nonzero(cell == c)[0]
+        nodes.extend(rng.choice(own, nsyn_per_cell, replace=False))
+    nodes = np.sort(np.array(nodes, np.int32))
+    n = nodes.size
+    p = {k: np.full(n, v) for k, v in SR_TAUS.items()}
+    w = np.where(rng.random(n) < 2 / 3, 1.0, -1.0)
+    p.update({"w": w, "r_na": np.full(n, 2.0), "NMDA_C": np.full(n, 0.28), "NMDA_rho": np.full(n, 0.062),
+              "AMPA_e": np.zeros(n), "NMDA_e": np.zeros(n), "GABA_e": np.full(n, -80.0)})
+    spec.mechs["syn_record"] = MechSpec(nodes, p)
+    weight = rng.uniform(0.002, 0.01, n)
+    delay = rng.uniform(0.5, 2.0, n)
+    if drive == "vecstim":
+        spec.mechs["VecStim"] = MechSpec(np.zeros(n, np.int32), {})
+        trains = [np.sort(rng.uniform(1.0, 80.0, rng.integers(3, 9))) for _ in range(n)]
+        spec.vecstim_offsets = np.concatenate([[0], np.cumsum([t.size for t in trains])]).astype(np.int64)
+        spec.vecstim_times = np.concatenate(trains)
+        kind, src = np.ones(n, np.int8), np.arange(n, dtype=np.int32)
+    else:
+        kind = np.zeros(n, np.int8)
+        src = ((cell[nodes] + 1) % spec.ncell).astype(np.int32)   # the next cell's detector
+    spec.netcons["syn_record"] = NetConSpec(inst=np.arange(n, dtype=np.int32), src_kind=kind, src=src,
+                                            weight=weight, delay=delay)
+    return spec
+
+
+@pytest.mark.parametrize("drive", ["vecstim", "cells"])
+@pytest.mark.parametrize("fusion", [True, False])
+def test_syn_record_plugin_parity(gpu_lib, drive, fusion):
+    spec = with_syn_record(build_config(1, 4, 100.0), drive=drive)
+    print(f"case syn_record drive={drive} fusion={fusion} n={spec.mechs['syn_record'].n}", flush=True)
+    o, g = run_both(spec, 100.0, fusion=fusion)
+    err = float(np.max(np.abs(o.traces() - g.traces())))
+    print(f"  max |dv| = {err:.3e} mV", flush=True)
+    assert err < V_TOL
+    compare_spikes(o, g, spec.dt)
+    for var in ("AMPA_A", "AMPA_B", "NMDA_B", "GABA_B", "i", "AMPA_factor", "didv", "dgdv"):
+        a, b = o.array("syn_record", var), g.get_array("syn_record", var)
+        scale = max(1e-30, float(np.max(np.abs(a))))
+        assert np.max(np.abs(a - b)) <= 1e-6 * scale, var
+    # the synapses received events: their conductance states moved
+    assert np.max(g.get_array("syn_record", "NMDA_B")) > 0
+
+
+def test_netcon_into_a_non_synapse_plugin_is_refused(gpu_lib):
+    from heliox_amd.spec import NetConSpec
+    spec = with_im(build_config(1, 4, 10.0))
+    spec.mechs["VecStim"] = MechSpec(np.zeros(1, np.int32), {})
+    spec.vecstim_offsets = np.array([0, 1], np.int64)
+    spec.vecstim_times = np.array([1.0])
+    spec.netcons["Im"] = NetConSpec(inst=np.array([0], np.int32), src_kind=np.array([1], np.int8),
+                                    src=np.array([0], np.int32), weight=np.array([1.0]), delay=np.array([0.0]))
+    g = Sim()
+    with pytest.raises(HelioxError, match="synapse plugin"):
+        g.load_model_from_spec(spec)

@@ -706,3 +706,84 @@ def test_adam_closed_form():
         vr = b2 * vr + (1 - b2) * g * g
         wr = wr - lr * (mr / (1 - b1 ** step)) / (np.sqrt(vr / (1 - b2 ** step)) + eps)
     assert np.allclose(w, wr, rtol=1e-14)
+
+
+# ---------------------------------------------------------------------------
+# syn_record (user_postsyn_mech/syn_record.cuh), run by the library as a synapse plugin
+# ---------------------------------------------------------------------------
+def syn_record_cell(v1, w_syn, weight, t_event, taus, rna=2.0, nmda_c=0.28, nmda_rho=0.062):
+    spec = single_compartment()
+    spec.cm[:] = CLAMP_CM
+    n = np.array([0], np.int32)
+    p = {k: np.array([val]) for k, val in taus.items()}
+    p.update({"w": np.array([w_syn]), "r_na": np.array([rna]), "NMDA_C": np.array([nmda_c]),
+              "NMDA_rho": np.array([nmda_rho]), "AMPA_e": np.array([0.0]), "NMDA_e": np.array([0.0]),
+              "GABA_e": np.array([-80.0])})
+    spec.mechs["syn_record"] = MechSpec(n, p)
+    spec.mechs["VecStim"] = MechSpec(n.copy(), {})
+    spec.vecstim_offsets = np.array([0, 1], np.int64)
+    spec.vecstim_times = np.array([t_event])
+    spec.netcons["syn_record"] = NetConSpec(inst=np.array([0], np.int32), src_kind=np.array([1], np.int8),
+                                            src=np.array([0], np.int32), weight=np.array([weight]),
+                                            delay=np.array([0.0]))
+    return spec
+
+
+def two_exp_factor(t1, t2):
+    """1 / peak of exp(-t/t2) - exp(-t/t1): the normalisation that makes a unit event peak at 1."""
+    tp = t1 * t2 / (t2 - t1) * math.log(t2 / t1)
+    return 1.0 / (math.exp(-tp / t2) - math.exp(-tp / t1))
+
+
+TAUS = {"AMPA_tau1": 0.2, "AMPA_tau2": 1.7, "NMDA_tau1": 2.0, "NMDA_tau2": 30.0, "GABA_tau1": 0.5, "GABA_tau2": 6.0}
+
+
+@pytest.mark.parametrize("v1", [-70.0, -30.0, 10.0])
+def test_syn_record_excitatory_event_closed_form(v1):
+    """An event of weight W splits W / (1 + r_na) to AMPA and W r_na / (1 + r_na) to NMDA;
+    each conductance is then the normalised difference of exponentials (peak = its share),
+    and i = |w| (g_AMPA (v - e_AMPA) + g_NMDA sigma(v) (v - e_NMDA)) with the Jahr-Stevens
+    block sigma(v) = 1 / (1 + C exp(-rho v)), from the conductances before each step's decay."""
+    W, t_ev, dt = 0.004, 1.0, 0.025
+    spec = syn_record_cell(v1, 1.0, W, t_ev, TAUS)
+    o = oracle.OracleSim(spec, monitors=[("syn_record", "AMPA_g", 0), ("syn_record", "NMDA_g", 0),
+                                         ("syn_record", "i", 0), ("syn_record", "AMPA_A", 0)])
+    clamp_step(o, -65.0, v1, 20.0)
+    ga, gn, i, aa = (o.monitor(j) for j in range(4))
+    # AMPA_A just after the delivering step's state update, then one decay per step
+    kd = int(np.argmax(aa > 0))
+    assert kd > 0 and aa[kd - 1] == 0.0
+    n = np.arange(aa.size - kd)
+    fa = two_exp_factor(0.2, 1.7)
+    a0 = W * fa / 3.0
+    assert np.allclose(aa[kd:], a0 * np.exp(-(n + 1) * dt / 0.2), rtol=1e-12, atol=1e-300)
+    # a step's g is B - A before that step's decay, n steps after the delivering one
+    # (0 in the delivering step itself)
+    ga_ref = a0 * (np.exp(-n * dt / 1.7) - np.exp(-n * dt / 0.2))
+    assert ga[kd] == 0.0 and np.allclose(ga[kd:], ga_ref, rtol=1e-9, atol=1e-18)
+    fn = two_exp_factor(2.0, 30.0)
+    gn_ref = W * 2.0 / 3.0 * fn * (np.exp(-n * dt / 30.0) - np.exp(-n * dt / 2.0))
+    assert np.allclose(gn[kd:], gn_ref, rtol=1e-9, atol=1e-18)
+    # the peaks are the shares of W (to the step's sampling)
+    assert abs(ga.max() / (W / 3.0) - 1) < 0.02 and abs(gn.max() / (2 * W / 3.0) - 1) < 0.01
+    sig = 1.0 / (1.0 + 0.28 * math.exp(-0.062 * v1))
+    assert np.allclose(i[kd:], ga[kd:] * v1 + gn[kd:] * sig * v1, rtol=1e-9, atol=1e-18)
+
+
+def test_syn_record_inhibitory_event_and_tau_clamp():
+    """w <= 0 routes the event to GABA with its own factor; tau1 >= 0.9999 tau2 is lowered to
+    0.9999 tau2 at INITIAL (syn_record.cuh:108-110)."""
+    W, dt = 0.003, 0.025
+    taus = dict(TAUS, GABA_tau1=6.0, GABA_tau2=6.0)
+    spec = syn_record_cell(-50.0, -1.0, W, 2.0, taus)
+    o = oracle.OracleSim(spec, monitors=[("syn_record", "GABA_g", 0), ("syn_record", "i", 0)])
+    clamp_step(o, -65.0, -50.0, 30.0)
+    assert o.get("syn_record", "GABA_tau1", 0) == 0.9999 * 6.0
+    assert o.get("syn_record", "Use", 0) == 1.0
+    g, i = o.monitor(0), o.monitor(1)
+    k0 = int(np.argmax(g > 0))                # one step after the delivering one
+    n = np.arange(1, g.size - k0 + 1)
+    t1, t2 = 0.9999 * 6.0, 6.0
+    ref = W * two_exp_factor(t1, t2) * (np.exp(-n * dt / t2) - np.exp(-n * dt / t1))
+    assert np.allclose(g[k0:], ref, rtol=1e-6, atol=1e-18)
+    assert np.allclose(i[k0:], g[k0:] * (-50.0 + 80.0), rtol=1e-9, atol=1e-18)
