@@ -761,6 +761,9 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
     const __amdgpu_buffer_rsrc_t ru = cell_buffer(C.S.rhs + C.nb, C.nn);
     const __amdgpu_buffer_rsrc_t rw = cell_buffer(C.S.w + C.nb, C.nn);
     double cd, ce;
+    // the serial chunk arithmetic alone runs at raised issue priority (the same wave at
+    // raised priority throughout takes too many issue slots from the waves beside it)
+    __builtin_amdgcn_s_setprio(3);
     dispatch_chunk_bound(ri.maxlen, [&](auto km) {
         constexpr int KM = decltype(km)::value;
         int rp[KM], wo[KM], tp;
@@ -778,6 +781,7 @@ __device__ __forceinline__ void fwd_round(const SolveCtx& C, const FwdBuf& B, Fw
         };
         chunk_forward_math<KM>(has_parent, StageIn{st, rp}, out, rcp_nr, cd, ce);
     });
+    __builtin_amdgcn_s_setprio(0);
     if (act && has_parent) pairs[slot] = SlotPair{cd, ce};
     round_boundary();
 }
@@ -824,6 +828,7 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>&
     const __amdgpu_buffer_rsrc_t rv = cell_buffer(C.S.v + C.nb, C.nn);
     const __amdgpu_buffer_rsrc_t rx = cell_buffer(C.S.rhs + C.nb, C.nn);
     double vtail = 0.0;
+    __builtin_amdgcn_s_setprio(3);
     dispatch_chunk_bound(ri.maxlen, [&](auto km) {
         constexpr int KM = decltype(km)::value;
         int rp[KM], wo[KM], tp;
@@ -836,6 +841,7 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>&
         if constexpr (kX != 0) chunk_back_math<KM>(StageInX{{st, rp}}, out, vpar);
         else chunk_back_math<KM>(StageIn{st, rp}, out, vpar);
     });
+    __builtin_amdgcn_s_setprio(0);
     if (act) C.slots[2 * slot] = vtail;   // the tail's new voltage
     round_boundary();
 }
