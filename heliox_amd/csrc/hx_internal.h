@@ -215,6 +215,16 @@ struct NsInbox {
 };
 constexpr int kNsRoundShift = 24;
 
+// What the host checks after a call: the event rings' overflow flags, the NetStim error
+// bits and the spike count, gathered by one kernel into pinned host memory.
+struct StatusArgs {
+    const int* const* ring_overflow;   // [ngroups]
+    int ngroups;
+    const int* ns_error;               // null without event-receiving NetStims
+    const int* spk_count;
+    int* out;                          // host: [0] overflow (OR), [1] NetStim error, [2] spikes
+};
+
 struct SpikeArgs {
     int npre;
     const double* v;
@@ -422,6 +432,7 @@ void launch_record(double* const* ptrs, int n, double* out, hipStream_t s);
 void launch_gap(const double* v, const int* src_node, double* vgap_col, const int* halfgap_inst, int n,
                 hipStream_t s);
 void launch_clear_ints(int* p, long long n, hipStream_t s);
+void launch_status(const StatusArgs& a, hipStream_t s);
 void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t s);
 
 }  // namespace hx

@@ -80,9 +80,9 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
     if (A.write_rates) {
         double minf, mtau, hinf, htau, ninf, ntau;
         hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
-        m.col(HH_MINF)[j] = minf; m.col(HH_MTAU)[j] = mtau;
-        m.col(HH_HINF)[j] = hinf; m.col(HH_HTAU)[j] = htau;
-        m.col(HH_NINF)[j] = ninf; m.col(HH_NTAU)[j] = ntau;
+        sts_(m.col(HH_MINF) + j, minf); sts_(m.col(HH_MTAU) + j, mtau);
+        sts_(m.col(HH_HINF) + j, hinf); sts_(m.col(HH_HTAU) + j, htau);
+        sts_(m.col(HH_NINF) + j, ninf); sts_(m.col(HH_NTAU) + j, ntau);
     }
     return s;
 }
@@ -95,9 +95,9 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
     if (A.write_rates) {
         double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
         cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
-        m.col(CH_ECA)[j] = ca_erev[ci];
-        m.col(CH_MINF)[j] = mInf; m.col(CH_MTAU)[j] = mTau; m.col(CH_MALPHA)[j] = mAlpha; m.col(CH_MBETA)[j] = mBeta;
-        m.col(CH_HINF)[j] = hInf; m.col(CH_HTAU)[j] = hTau; m.col(CH_HALPHA)[j] = hAlpha; m.col(CH_HBETA)[j] = hBeta;
+        sts_(m.col(CH_ECA) + j, ca_erev[ci]);
+        sts_(m.col(CH_MINF) + j, mInf); sts_(m.col(CH_MTAU) + j, mTau); sts_(m.col(CH_MALPHA) + j, mAlpha); sts_(m.col(CH_MBETA) + j, mBeta);
+        sts_(m.col(CH_HINF) + j, hInf); sts_(m.col(CH_HTAU) + j, hTau); sts_(m.col(CH_HALPHA) + j, hAlpha); sts_(m.col(CH_HBETA) + j, hBeta);
     }
     return s;
 }
@@ -109,7 +109,7 @@ __device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m
     if (A.write_rates) {
         double linf, taul;
         hdla_rate(v, vhalfl, tau, A.c, linf, taul);
-        m.col(HD_LINF)[j] = linf; m.col(HD_TAUL)[j] = taul;
+        sts_(m.col(HD_LINF) + j, linf); sts_(m.col(HD_TAUL) + j, taul);
     }
     return l;
 }
@@ -132,7 +132,7 @@ __device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, i
     double i1 = gp * (v1 - ep);
     double i0 = gp * (v - ep);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) m.col(PAS_I)[j] = i0;
+    if (A.write_assigned) sts_(m.col(PAS_I) + j, i0);
     return i0;
 }
 
@@ -146,8 +146,8 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
     double i0 = hh_current(v, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
     g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) {
-        m.col(HH_ENA)[j] = ena; m.col(HH_EK)[j] = ek; m.col(HH_INA)[j] = ina; m.col(HH_IK)[j] = ik;
-        m.col(HH_IL)[j] = il; m.col(HH_GNA)[j] = gna; m.col(HH_GK)[j] = gk;
+        sts_(m.col(HH_ENA) + j, ena); sts_(m.col(HH_EK) + j, ek); sts_(m.col(HH_INA) + j, ina); sts_(m.col(HH_IK) + j, ik);
+        sts_(m.col(HH_IL) + j, il); sts_(m.col(HH_GNA) + j, gna); sts_(m.col(HH_GK) + j, gk);
     }
     return i0;
 }
@@ -161,7 +161,7 @@ __device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m,
     double i0 = gg * (v - eca);
     g = (i1 - i0) * 1000.0;   // / 0.001
     if (A.write_assigned) {
-        m.col(CH_ECA)[j] = eca; m.col(CH_G)[j] = gg; m.col(CH_ICA)[j] = i0; m.col(CH_IMECH)[j] = i0;
+        sts_(m.col(CH_ECA) + j, eca); sts_(m.col(CH_G) + j, gg); sts_(m.col(CH_ICA) + j, i0); sts_(m.col(CH_IMECH) + j, i0);
     }
     return i0;
 }
@@ -173,7 +173,7 @@ __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, 
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) { m.col(HD_GHD)[j] = ghd; m.col(HD_I)[j] = i0; }
+    if (A.write_assigned) { sts_(m.col(HD_GHD) + j, ghd); sts_(m.col(HD_I) + j, i0); }
     return i0;
 }
 
@@ -181,10 +181,10 @@ __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, 
 // recompute erev from the concentrations when iontype has 0100.  Used by the
 // instance-parallel ion kernel; the fused kernel keeps cur in registers.
 __device__ __forceinline__ void ion_cur(const MechDev& m, int j, double z, double ktf, int write_dcurdv) {
-    m.col(ION_CUR)[j] = 0.;
-    if (write_dcurdv) m.col(ION_DCURDV)[j] = 0.;
+    sts_(m.col(ION_CUR) + j, 0.);
+    if (write_dcurdv) sts_(m.col(ION_DCURDV) + j, 0.);
     if (m.iontype[j] & 0100)
-        m.col(ION_EREV)[j] = nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf);
+        sts_(m.col(ION_EREV) + j, nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf));
 }
 
 // erev of ion x at dense instance i for this step's current evaluation.  ci:
@@ -202,7 +202,7 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
 
 __device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {
     if (A.ion_store & (1u << (2 * x))) sts_(ion.col(ION_CUR) + i, cur);
-    if (A.write_dcurdv) ion.col(ION_DCURDV)[i] = 0.;
+    if (A.write_dcurdv) sts_(ion.col(ION_DCURDV) + i, 0.);
 }
 
 #define HAS(bit) (A.dense_mask & (1u << (bit)))
@@ -1306,6 +1306,14 @@ __global__ void k_copy_ptrs(double* const* src, double* const* dst, int n) {
     if (i < n) *dst[i] = *src[i];
 }
 
+__global__ void k_status(StatusArgs a) {
+    int ov = 0;
+    for (int g = 0; g < a.ngroups; ++g) ov |= *a.ring_overflow[g];
+    a.out[0] = ov;
+    a.out[1] = a.ns_error ? *a.ns_error : 0;
+    a.out[2] = *a.spk_count;
+}
+
 __global__ void k_clear_ints(int* p, long long n) {
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0;
@@ -1433,5 +1441,7 @@ void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t
 void launch_clear_ints(int* p, long long n, hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_clear_ints, grid_for(n), dim3(kBlock), 0, s, p, n);
 }
+
+void launch_status(const StatusArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_status, dim3(1), dim3(1), 0, s, a); }
 
 }  // namespace hx

@@ -355,6 +355,8 @@ struct hx_sim {
     double* d_spk_t = nullptr;
     int* d_spk_gid = nullptr;
     int* d_spk_count = nullptr;
+    int* const* d_ring_overflow = nullptr;   // each group's ring overflow flag
+    int* h_status = nullptr;                 // pinned: StatusArgs::out
     int spk_cap = 0;
     bool inputs_dirty = true;
     // Cell groups.  Cells are split into contiguous groups, each with its own
@@ -532,6 +534,7 @@ struct hx_sim {
         for (auto& tm : timers)
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
+        if (h_status) (void)hipHostFree(h_status);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -1338,6 +1341,11 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
             HXC(hipStreamCreate(&cg.s));
             HXC(hipEventCreateWithFlags(&cg.done, hipEventDisableTiming));
         }
+    }
+    {
+        std::vector<int*> ov;
+        for (auto& cg : groups) ov.push_back(cg.ring.overflow);
+        d_ring_overflow = dupload(owned, ov);
     }
     if (G > 1 && !ev_main) HXC(hipEventCreateWithFlags(&ev_main, hipEventDisableTiming));
     if (G > 1 && !ev_stagger) HXC(hipEventCreateWithFlags(&ev_stagger, hipEventDisableTiming));
@@ -2275,23 +2283,28 @@ void hx_sim::finish_pending() {
 }
 
 void hx_sim::sync_outputs() {
+    if (!d_spk_count || !d_ring_overflow) {   // no model loaded
+        HXC(hipStreamSynchronize(stream));
+        return;
+    }
+    // one kernel gathers the flags and the spike count into pinned host memory, so the
+    // host reads them after the synchronisation without a copy each
+    if (!h_status) HXC(hipHostMalloc(reinterpret_cast<void**>(&h_status), 4 * sizeof(int), hipHostMallocDefault));
+    StatusArgs sa{d_ring_overflow, static_cast<int>(groups.size()), nsa.n > 0 ? nsa.error : nullptr, d_spk_count,
+                  h_status};
+    launch_status(sa, stream);
+    HXC(hipGetLastError());
     HXC(hipStreamSynchronize(stream));
     if (profiling) tcollect();
-    for (auto& cg : groups) {
-        int ov = 0;
-        HXC(hipMemcpy(&ov, cg.ring.overflow, sizeof(int), hipMemcpyDeviceToHost));
-        if (ov) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
-    }
+    if (h_status[0]) throw std::runtime_error("event ring overflow: raise the per-step capacity with hx_set_event_capacity");
     if (nsa.n > 0) {
-        int e = 0;
-        HXC(hipMemcpy(&e, nsa.error, sizeof(int), hipMemcpyDeviceToHost));
+        const int e = h_status[1];
         if (e & 1) throw std::runtime_error("NetStim event inbox overflow");
         if (e & 2) throw std::runtime_error("more than 8 events reached one NetStim in one pass of a step");
         if (e & 4) throw std::runtime_error("a step's delivery loop needed more than 64 passes (NetStim interval too small?)");
         if (e & 8) throw std::runtime_error("a NetStim has more than 8 pending self events");
     }
-    int ns = 0;
-    HXC(hipMemcpy(&ns, d_spk_count, sizeof(int), hipMemcpyDeviceToHost));
+    const int ns = h_status[2];
     if (ns > spk_cap) throw std::runtime_error("spike log overflow");
     {
         std::vector<std::pair<double, int>> fresh;
