@@ -443,6 +443,9 @@ def main():
     sim.continue_run((args.steps + 0.5) * dt)      # returns after the stream is synchronized
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # the timed call's last state update may wait for the next call (the first node pass of
+    # the timed call applied the warm-up call's in the same way): 1 if it did
+    deferred = sim.info("state_pending")
 
     value = nnode * args.steps / wall
     ms_per_step = wall * 1e3 / args.steps
@@ -532,6 +535,7 @@ def main():
                                f"Poisson VecStim input, dt 0.025 ms",
                    "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
+        "state_update_deferred": bool(deferred),
         "roofline": roofline,
         "roofline_single_stream": alone,
         "step_bytes": step_bytes(spec, ms_per_step, uniform_bytes),

@@ -432,6 +432,14 @@ struct hx_sim {
     double t = 0.0;
     int k = 0;                       // step index since finitialize
     bool state_pending = false;
+    // A run/continue_run/fadvance call may end with its last state update still pending
+    // (close_deferral, default on): the next call's first node pass applies it as every
+    // step applies the previous one, and any other entry point first completes it with
+    // the closing pass the call would have run (settle).  Only those three entry points
+    // set defer_allowed around their steps.
+    bool close_deferral = true;
+    bool defer_allowed = false;
+    bool pending_sampled = false;   // the pending step's (voltage) samples are already recorded
     bool final_step = false;   // the last step of a run call also stores every assigned variable
     bool initialized = false;
     // adjoint tape (hx_tape_begin): row n holds v^{n+1} (after step n's solve); the
@@ -620,6 +628,9 @@ struct hx_sim {
     void step_once_groups();
     void step_once();
     void finish_pending();
+    bool can_defer_close() const;
+    void sample_pending_step();
+    int settle();
     int run_steps(int nstep);
     void sync_outputs();
     void finitialize(double v_init);
@@ -2104,9 +2115,10 @@ void hx_sim::step_once_groups() {
     tn += 0.5 * dt;
     tn += 0.5 * dt;
     const bool pending = state_pending;
+    const bool sample = pending && !pending_sampled;   // a deferred call end sampled already
     const StepArgs post = step_args(tn, 1, 0);
     const size_t nm = mon_ref.size();
-    if (pending && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    if (sample && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
     pass_cadyn_skip = cadyn_done ? 1 : 0;
     pass_cadyn_after = cadyn_eager ? 1 : 0;
     // First step of a run: each group starts once the previous group's node pass is
@@ -2122,7 +2134,7 @@ void hx_sim::step_once_groups() {
         launch_events_group(g, k, tk, s);
         launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
         if (stagger && g + 1 < static_cast<int>(groups.size())) HXC(hipEventRecord(ev_stagger, s));
-        if (pending && cg.mon1 > cg.mon0)
+        if (sample && cg.mon1 > cg.mon0)
             hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
         SolveArgs S{};
         S.nunit = cg.unit1 - cg.unit0;
@@ -2176,7 +2188,8 @@ void hx_sim::step_once_groups() {
             tend(T_POINT, s);
         }
     }
-    if (pending && nm) mon_buf_fill++;
+    if (sample && nm) mon_buf_fill++;
+    pending_sampled = false;
     cadyn_done = cadyn_eager;
     pass_cadyn_skip = pass_cadyn_after = 0;
     t = tn;
@@ -2205,7 +2218,8 @@ void hx_sim::step_once() {
         launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
         cadyn_done = cadyn_eager;
         pass_cadyn_skip = pass_cadyn_after = 0;
-        if (state_pending) launch_record();
+        if (state_pending && !pending_sampled) launch_record();
+        pending_sampled = false;
     } else {
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
@@ -2269,17 +2283,61 @@ void hx_sim::finish_pending() {
         for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
             CellGroup& cg = groups[g];
             launch_mech_pass(1, 0, t, g, cg.s);
-            if (cg.mon1 > cg.mon0)
+            if (!pending_sampled && cg.mon1 > cg.mon0)
                 hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0,
                                   cg.s);
         }
-        if (nm) mon_buf_fill++;
+        if (nm && !pending_sampled) mon_buf_fill++;
+        pending_sampled = false;
         state_pending = false;
         return;
     }
     launch_mech_pass(1, 0, t);
-    launch_record();
+    if (!pending_sampled) launch_record();
+    pending_sampled = false;
     state_pending = false;
+}
+
+// The closing pass may wait for the next call when nothing samples the states
+// inside the step loop: every monitor samples a voltage (taken at the call's end,
+// sample_pending_step), no tape and no signal capture.
+bool hx_sim::can_defer_close() const {
+    return defer_allowed && close_deferral && fused && state_pending && (mon_ref.empty() || mon_all_v) &&
+           !tape_on && !(learn && learn->capturing());
+}
+
+// A deferred call end still records the last step's samples: a voltage after the
+// solve, which the pending state update does not change.
+void hx_sim::sample_pending_step() {
+    const size_t nm = mon_ref.size();
+    if (nm == 0) return;
+    if (mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    if (multi_stream) {
+        for (auto& cg : groups)
+            if (cg.mon1 > cg.mon0)
+                hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0,
+                                  cg.s);
+        mon_buf_fill++;
+    } else {
+        launch_record();
+    }
+    pending_sampled = true;
+}
+
+// Completes a deferred state update with the pass the call would have closed with
+// (it also stores the rates, as a call's closing pass does) and waits for it.
+int hx_sim::settle() {
+    if (!state_pending) return 0;
+    try {
+        final_step = true;
+        finish_pending();
+        final_step = false;
+        HXC(hipStreamSynchronize(stream));
+    } catch (const std::exception& e) {
+        final_step = false;
+        return fail("%s", e.what());
+    }
+    return 0;
 }
 
 void hx_sim::sync_outputs() {
@@ -2391,7 +2449,8 @@ int hx_sim::run_steps(int nstep) {
             final_step = s == nstep - 1;
             step_once();
         }
-        finish_pending();
+        if (can_defer_close()) sample_pending_step();
+        else finish_pending();
     } catch (...) {
         if (multi_stream) {
             for (auto& cg : groups) (void)hipStreamSynchronize(cg.s);
@@ -2480,6 +2539,7 @@ void hx_sim::finitialize(double v_init) {
     t = 0.0;
     k = 0;
     state_pending = false;
+    pending_sampled = false;
     cadyn_done = false;
     pass_cadyn_skip = pass_cadyn_after = 0;
     ensure_ttab(1);
@@ -2559,6 +2619,19 @@ template <class T>
 uint64_t fnv_vec(const std::vector<T>& v) { return fnv1a(v.data(), v.size() * sizeof(T)); }
 }  // namespace
 
+// The stepping entry points (run, continue_run, fadvance) may leave their last state
+// update pending; every other entry point that takes a handle completes it first.
+#define HX_SETTLE(sim)                                                  \
+    do {                                                                \
+        if ((sim) && (sim)->state_pending && (sim)->settle() != 0) return -1; \
+    } while (0)
+
+struct DeferScope {
+    hx_sim* s;
+    explicit DeferScope(hx_sim* sim) : s(sim) { s->defer_allowed = true; }
+    ~DeferScope() { s->defer_allowed = false; }
+};
+
 static bool check_loaded(hx_sim* sim) {
     if (!sim->loaded) { sim->fail("model not loaded (call hx_load_model)"); return false; }
     return true;
@@ -2581,6 +2654,7 @@ void hx_destroy(hx_sim* sim) { delete sim; }
 const char* hx_last_error(hx_sim* sim) { return sim ? sim->err.c_str() : "null handle"; }
 
 int hx_set_device(hx_sim* sim, const char* dev) {
+    HX_SETTLE(sim);
     if (!dev || std::string(dev) != "gpu")
         return sim->fail("device '%s' is not served by this library (only \"gpu\")", dev ? dev : "");
     int n = 0;
@@ -2589,6 +2663,7 @@ int hx_set_device(hx_sim* sim, const char* dev) {
 }
 
 int hx_set_dt(hx_sim* sim, double dt) {
+    HX_SETTLE(sim);
     if (!(dt > 0)) return sim->fail("dt must be positive");
     sim->dt_set = true;
     if (sim->loaded && dt != sim->dt) {
@@ -2604,11 +2679,13 @@ int hx_set_dt(hx_sim* sim, double dt) {
 double hx_get_dt(hx_sim* sim) { return sim->dt; }
 
 int hx_set_celsius(hx_sim* sim, double c) {
+    HX_SETTLE(sim);
     sim->celsius = c;
     return 0;
 }
 
 int hx_set_data_path(hx_sim* sim, const char* path) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("cannot set the data path after the model is loaded");
     if (!path || !*path) return sim->fail("empty data path");
     sim->data_path = path;
@@ -2616,6 +2693,7 @@ int hx_set_data_path(hx_sim* sim, const char* path) {
 }
 
 int hx_set_user_mod_num(hx_sim* sim, int num) {
+    HX_SETTLE(sim);
     if (num <= 0) return sim->fail("user_mod_num must be positive");
     sim->user_mod_num = num;
     return 0;
@@ -2623,6 +2701,7 @@ int hx_set_user_mod_num(hx_sim* sim, int num) {
 
 int hx_model_set_nodes(hx_sim* sim, int ncell, int nnode, const int* parent, const double* a, const double* b,
                        const double* area) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (ncell <= 0 || nnode < ncell || !parent || !a || !b || !area) return sim->fail("invalid node arrays");
     for (int i = 0; i < ncell; ++i)
@@ -2640,6 +2719,7 @@ int hx_model_set_nodes(hx_sim* sim, int ncell, int nnode, const int* parent, con
 }
 
 int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* nodes) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (sim->nnode == 0) return sim->fail("set nodes before inserting mechanisms");
     const int id = mech_id(mech ? mech : "");
@@ -2690,6 +2770,7 @@ int hx_model_insert(hx_sim* sim, const char* mech, int n, const int* nodes) {
 }
 
 int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, const double* vals) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded; use variable handles");
     std::string mn = mech ? mech : "", vn = var ? var : "";
     if (mn == "capacitance" && vn == "cm") {
@@ -2718,6 +2799,7 @@ int hx_model_set_param(hx_sim* sim, const char* mech, const char* var, int n, co
 }
 
 int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double value) {
+    HX_SETTLE(sim);
     const int id = mech_id(mech ? mech : "");
     if (id != M_HH && id != M_HDLA) return sim->fail("mechanism '%s' has no globals", mech ? mech : "");
     static const char* hh_g[] = {"celsius"};
@@ -2731,6 +2813,7 @@ int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double v
 }
 
 int hx_model_set_iontype(hx_sim* sim, const char* ion, int n, const int* it) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     const int id = mech_id(ion ? ion : "");
     if (id < 0 || !registry()[id].ion || !sim->mech[id].present) return sim->fail("ion '%s' not inserted", ion ? ion : "");
@@ -2740,6 +2823,7 @@ int hx_model_set_iontype(hx_sim* sim, const char* ion, int n, const int* it) {
 }
 
 int hx_model_add_presyn(hx_sim* sim, int gid, int node, double thr) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (node < 0 || node >= sim->nnode) return sim->fail("presyn node out of range");
     sim->pre_gid.push_back(gid);
@@ -2749,6 +2833,7 @@ int hx_model_add_presyn(hx_sim* sim, int gid, int node, double thr) {
 }
 
 int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
+    HX_SETTLE(sim);
     HostMech& m = sim->mech[M_VECSTIM];
     if (!m.present || inst < 0 || inst >= m.n) return sim->fail("VecStim instance %d does not exist", inst);
     if (n < 0 || (n > 0 && !times)) return sim->fail("invalid spike-time array");
@@ -2758,6 +2843,7 @@ int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
 }
 
 int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double w, double delay) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     int id = mech_id(target ? target : "");
     if (id < 0) {                     // a synapse plugin
@@ -2785,6 +2871,7 @@ int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, 
 }
 
 int hx_model_add_gap(hx_sim* sim, int src_node, int hg) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (src_node < 0 || src_node >= sim->nnode) return sim->fail("gap source node out of range");
     if (!sim->mech[M_HALFGAP].present || hg < 0 || hg >= sim->mech[M_HALFGAP].n)
@@ -2794,6 +2881,7 @@ int hx_model_add_gap(hx_sim* sim, int src_node, int hg) {
 }
 
 int hx_model_digest(hx_sim* sim, char* out, int cap) {
+    HX_SETTLE(sim);
     std::string d;
     char buf[512];
     auto add = [&](const char* fmt, auto... args) {
@@ -2860,6 +2948,7 @@ int hx_model_digest(hx_sim* sim, char* out, int cap) {
 }
 
 int hx_model_read_export(hx_sim* sim) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (sim->data_path.empty()) return sim->fail("no data path set");
     if (sim->nnode != 0) return sim->fail("the model already has nodes");
@@ -2880,6 +2969,7 @@ int hx_model_read_export(hx_sim* sim) {
 }
 
 int hx_load_model(hx_sim* sim) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("model already loaded");
     if (!sim->data_path.empty() && hx_model_read_export(sim) != 0) return -1;
     if (sim->nnode == 0) return sim->fail("no nodes");
@@ -2910,6 +3000,7 @@ int hx_load_model(hx_sim* sim) {
 }
 
 int hx_finitialize(hx_sim* sim, double v_init) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     sim->finitialize(v_init);
@@ -2926,6 +3017,7 @@ int hx_run(hx_sim* sim, double tstop) {
         sim->t = 0.0;
         sim->k = 0;
     }
+    DeferScope ds(sim);
     if (nstep > 0) sim->run_steps(nstep);
     return sim->after_run();
     API_END
@@ -2935,6 +3027,7 @@ int hx_continue_run(hx_sim* sim, double runtime) {
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     int nstep = static_cast<int>(runtime / sim->dt);
+    DeferScope ds(sim);
     if (nstep > 0) sim->run_steps(nstep);
     return sim->after_run();
     API_END
@@ -2943,6 +3036,7 @@ int hx_continue_run(hx_sim* sim, double runtime) {
 int hx_sim::after_run() { return spike_output ? hx_output_spikes(this, output_dir.c_str()) : 0; }
 
 int hx_set_spike_output_enabled(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     sim->spike_output = enable != 0;
     return 0;
 }
@@ -2950,6 +3044,7 @@ int hx_set_spike_output_enabled(hx_sim* sim, int enable) {
 int hx_is_spike_output_enabled(hx_sim* sim) { return sim->spike_output ? 1 : 0; }
 
 int hx_set_output_dir(hx_sim* sim, const char* dir) {
+    HX_SETTLE(sim);
     if (!dir || !*dir) return sim->fail("set_output_dir: empty directory");
     sim->output_dir = dir;
     return 0;
@@ -2957,6 +3052,7 @@ int hx_set_output_dir(hx_sim* sim, const char* dir) {
 
 // ---- gap junctions at run time (simulate.cpp:998-1100) ----
 int hx_add_gap_source(hx_sim* sim, int sid, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!mech || !var) return sim->fail("add_gap_source: null variable name");
     if (sid < 0) {
         sid = sim->next_sid++;
@@ -2974,6 +3070,7 @@ int hx_add_gap_source(hx_sim* sim, int sid, const char* mech, const char* var, i
 }
 
 int hx_add_gap_target(hx_sim* sim, int sid, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     auto it = sim->gap_meta.find(sid);
     if (it == sim->gap_meta.end()) return sim->fail("Gap junction with sid %d does not exist", sid);
@@ -2991,6 +3088,7 @@ int hx_add_gap_target(hx_sim* sim, int sid, const char* mech, const char* var, i
 }
 
 int hx_clear_all_gap_junctions(hx_sim* sim) {
+    HX_SETTLE(sim);
     sim->gap_meta.clear();
     sim->next_sid = 0;
     sim->dg_src.clear();
@@ -3001,12 +3099,14 @@ int hx_clear_all_gap_junctions(hx_sim* sim) {
 }
 
 int hx_get_next_available_sid(hx_sim* sim) {
+    HX_SETTLE(sim);
     int sid = sim->next_sid;
     while (sim->gap_meta.count(sid)) ++sid;
     return sid;
 }
 
 int hx_get_gap_junction_sids(hx_sim* sim, int* sids, int cap) {
+    HX_SETTLE(sim);
     int n = 0;
     for (auto& kv : sim->gap_meta) {
         if (sids && n < cap) sids[n] = kv.first;
@@ -3017,6 +3117,7 @@ int hx_get_gap_junction_sids(hx_sim* sim, int* sids, int cap) {
 
 int hx_get_gap_junction(hx_sim* sim, int sid, char* mech, int mech_cap, char* var, int var_cap, int* idx,
                         int* num_targets) {
+    HX_SETTLE(sim);
     auto it = sim->gap_meta.find(sid);
     if (it == sim->gap_meta.end()) return -1;
     auto put = [](char* dst, int cap, const std::string& src) {
@@ -3032,6 +3133,7 @@ int hx_get_gap_junction(hx_sim* sim, int sid, char* mech, int mech_cap, char* va
 
 // ---- monitor and VecPlay lookups (SimRuntimeCore get_monitor_handle, get_vecplay_keys) ----
 int hx_get_monitor_handle(hx_sim* sim, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!mech || !var) return -1;
     for (size_t i = 0; i < sim->mon_name.size(); ++i)
         if (sim->mon_name[i].first == mech && sim->mon_name[i].second == var && sim->mon_idx[i] == idx)
@@ -3040,6 +3142,7 @@ int hx_get_monitor_handle(hx_sim* sim, const char* mech, const char* var, int id
 }
 
 int hx_get_vecplay_keys(hx_sim* sim, char* buf, int cap) {
+    HX_SETTLE(sim);
     std::string all;
     for (auto& vp : sim->vecplay) all += vp.mech + "\t" + vp.var + "\t" + std::to_string(vp.idx) + "\n";
     if (buf && cap > 0) std::snprintf(buf, static_cast<size_t>(cap), "%s", all.c_str());
@@ -3049,6 +3152,7 @@ int hx_get_vecplay_keys(hx_sim* sim, char* buf, int cap) {
 int hx_fadvance(hx_sim* sim) {
     if (!check_loaded(sim)) return -1;
     API_BEGIN
+    DeferScope ds(sim);
     sim->run_steps(1);
     return 0;
     API_END
@@ -3057,6 +3161,7 @@ int hx_fadvance(hx_sim* sim) {
 double hx_get_t(hx_sim* sim) { return sim->t; }
 
 int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!mech || !var) return sim->fail("null monitor name");
     Ref r;
     if (sim->loaded) {
@@ -3076,11 +3181,13 @@ int hx_add_monitor(hx_sim* sim, const char* mech, const char* var, int idx) {
 }
 
 int hx_get_monitor_len(hx_sim* sim, int h) {
+    HX_SETTLE(sim);
     if (h < 0 || h >= static_cast<int>(sim->mon_data.size())) return sim->fail("bad monitor handle");
     return static_cast<int>(sim->mon_data[h].size());
 }
 
 int hx_get_monitor_data(hx_sim* sim, int h, double* out, int cap) {
+    HX_SETTLE(sim);
     if (h < 0 || h >= static_cast<int>(sim->mon_data.size())) return sim->fail("bad monitor handle");
     auto& d = sim->mon_data[h];
     int n = std::min<int>(cap, static_cast<int>(d.size()));
@@ -3089,6 +3196,7 @@ int hx_get_monitor_data(hx_sim* sim, int h, double* out, int cap) {
 }
 
 int hx_flush_recorders(hx_sim* sim) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     sim->sync_outputs();
@@ -3126,6 +3234,7 @@ int hx_mechanism_names(char* buf, int cap) {
 }
 
 int hx_set_hdf5_enabled(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     API_BEGIN
     if (!enable) {
         sim->h5_on = false;
@@ -3142,6 +3251,7 @@ int hx_set_hdf5_enabled(hx_sim* sim, int enable) {
 int hx_is_hdf5_enabled(hx_sim* sim) { return sim->h5_on ? 1 : 0; }
 
 int hx_get_variable_handle(hx_sim* sim, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
@@ -3153,6 +3263,7 @@ int hx_get_variable_handle(hx_sim* sim, const char* mech, const char* var, int i
 }
 
 int hx_get_variable_by_handle(hx_sim* sim, int h, double* out) {
+    HX_SETTLE(sim);
     if (h < 0 || h >= static_cast<int>(sim->handles.size()) || !out) return sim->fail("bad variable handle");
     API_BEGIN
     HXC(hipStreamSynchronize(sim->stream));
@@ -3162,6 +3273,7 @@ int hx_get_variable_by_handle(hx_sim* sim, int h, double* out) {
 }
 
 int hx_set_variable_by_handle(hx_sim* sim, int h, double value) {
+    HX_SETTLE(sim);
     if (h < 0 || h >= static_cast<int>(sim->handles.size())) return sim->fail("bad variable handle");
     API_BEGIN
     HXC(hipStreamSynchronize(sim->stream));
@@ -3172,12 +3284,14 @@ int hx_set_variable_by_handle(hx_sim* sim, int h, double value) {
 }
 
 int hx_get_variables_by_handles(hx_sim* sim, int n, const int* hs, double* out) {
+    HX_SETTLE(sim);
     for (int i = 0; i < n; ++i)
         if (hx_get_variable_by_handle(sim, hs[i], out + i) != 0) return -1;
     return 0;
 }
 
 int hx_get_variables_by_handles_f32_into(hx_sim* sim, int n, const int* hs, float* out) {
+    HX_SETTLE(sim);
     for (int i = 0; i < n; ++i) {
         double x;
         if (hx_get_variable_by_handle(sim, hs[i], &x) != 0) return -1;
@@ -3187,12 +3301,14 @@ int hx_get_variables_by_handles_f32_into(hx_sim* sim, int n, const int* hs, floa
 }
 
 int hx_set_variables_by_handles(hx_sim* sim, int n, const int* hs, const double* vals) {
+    HX_SETTLE(sim);
     for (int i = 0; i < n; ++i)
         if (hx_set_variable_by_handle(sim, hs[i], vals[i]) != 0) return -1;
     return 0;
 }
 
 int hx_get_variable_value(hx_sim* sim, const char* mech, const char* var, int idx, double* out) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
@@ -3204,6 +3320,7 @@ int hx_get_variable_value(hx_sim* sim, const char* mech, const char* var, int id
 }
 
 int hx_set_variable_value(hx_sim* sim, double value, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     Ref r = sim->resolve(mech ? mech : "", var ? var : "", idx);
@@ -3216,6 +3333,7 @@ int hx_set_variable_value(hx_sim* sim, double value, const char* mech, const cha
 }
 
 int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, int cap) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     std::string mn = mech ? mech : "", vn = var ? var : "";
@@ -3281,6 +3399,7 @@ int hx_get_array(hx_sim* sim, const char* mech, const char* var, double* out, in
 }
 
 int hx_add_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tv, const double* yv) {
+    HX_SETTLE(sim);
     if (n <= 0 || !tv || !yv) return sim->fail("vecplay needs at least one (t, y) point");
     if (hx_has_vecplay(sim, mech, var, idx) == 1) return hx_update_vecplay(sim, mech, var, idx, n, tv, yv);
     VecPlayHost vp;
@@ -3308,6 +3427,7 @@ int hx_add_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int 
 }
 
 int hx_update_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, int n, const double* tv, const double* yv) {
+    HX_SETTLE(sim);
     for (auto& vp : sim->vecplay)
         if (vp.mech == mech && vp.var == var && vp.idx == idx) {
             vp.tvec.assign(tv, tv + n);
@@ -3320,6 +3440,7 @@ int hx_update_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, i
 }
 
 int hx_remove_vecplay(hx_sim* sim, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     for (size_t i = 0; i < sim->vecplay.size(); ++i) {
         auto& vp = sim->vecplay[i];
         if (vp.mech == mech && vp.var == var && vp.idx == idx) {
@@ -3332,6 +3453,7 @@ int hx_remove_vecplay(hx_sim* sim, const char* mech, const char* var, int idx) {
 }
 
 int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx) {
+    HX_SETTLE(sim);
     for (auto& vp : sim->vecplay)
         if (vp.mech == mech && vp.var == var && vp.idx == idx) return 1;
     return 0;
@@ -3353,6 +3475,7 @@ int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap) {
 // window t_m + dt/2 reaches it, once that step's delivery loop has run) and those logged
 // by the device for the NetStims that receive events.
 int hx_get_netstim_spikes(hx_sim* sim, double* t, int* inst, int cap) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     std::vector<std::pair<double, int>> all;
@@ -3424,6 +3547,7 @@ int hx_get_spk_by_gid(hx_sim* sim, int gid, double* out, int cap) {
 }
 
 int hx_set_event_capacity(hx_sim* sim, int per_step) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("set the event capacity before hx_load_model");
     if (per_step <= 0) return sim->fail("capacity must be positive");
     sim->event_cap_request = per_step;
@@ -3431,6 +3555,7 @@ int hx_set_event_capacity(hx_sim* sim, int per_step) {
 }
 
 int hx_set_cell_groups(hx_sim* sim, int ngroup) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("set the cell groups before hx_load_model");
     if (ngroup < 0) return sim->fail("group count must be >= 0");
     sim->group_request = ngroup;
@@ -3438,12 +3563,14 @@ int hx_set_cell_groups(hx_sim* sim, int ngroup) {
 }
 
 int hx_set_solver_root(hx_sim* sim, int centre) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("set the solver root before hx_load_model");
     sim->solve_root_centre = centre != 0;
     return 0;
 }
 
 int hx_set_solve_unit_cells(hx_sim* sim, int cells) {
+    HX_SETTLE(sim);
     if (sim->loaded) return sim->fail("set the solve unit size before hx_load_model");
     if (cells < 0) return sim->fail("solve unit size must be >= 0 (0: the library's choice)");
     sim->unit_request = cells;
@@ -3451,16 +3578,19 @@ int hx_set_solve_unit_cells(hx_sim* sim, int cells) {
 }
 
 int hx_set_group_streams(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     sim->group_streams_allowed = enable != 0;
     return 0;
 }
 
 int hx_set_uniform_columns(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     sim->uniform_on = enable != 0;
     return 0;
 }
 
 int hx_set_fusion(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     sim->fusion_allowed = enable ? 1 : 0;
     if (sim->loaded) {
         API_BEGIN
@@ -3471,7 +3601,14 @@ int hx_set_fusion(hx_sim* sim, int enable) {
     return 0;
 }
 
+int hx_set_close_deferral(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
+    sim->close_deferral = enable != 0;
+    return 0;
+}
+
 int hx_set_profiling(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     sim->profiling = enable != 0;
     sim->prof_mask = ~0u;
     for (auto& tm : sim->timers) { tm.ms = 0; tm.launches = 0; }
@@ -3479,6 +3616,7 @@ int hx_set_profiling(hx_sim* sim, int enable) {
 }
 
 int hx_set_profiling_classes(hx_sim* sim, const char* classes) {
+    HX_SETTLE(sim);
     unsigned mask = 0;
     std::string all = classes ? classes : "";
     size_t pos = 0;
@@ -3502,6 +3640,7 @@ int hx_set_profiling_classes(hx_sim* sim, const char* classes) {
 }
 
 int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches) {
+    HX_SETTLE(sim);
     for (int i = 0; i < T_COUNT; ++i)
         if (kernel && std::string(kernel) == kTimerNames[i]) {
             if (ms) *ms = sim->timers[i].ms;
@@ -3687,6 +3826,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
     if (k == "cell_groups") return static_cast<long long>(sim->groups.size());
     if (k == "multi_stream") return sim->last_multi_stream ? 1 : 0;
+    if (k == "state_pending") return sim->state_pending ? 1 : 0;
     if (k == "uniform_columns" || k == "uniform_bytes") {
         long long cols = 0, bytes = 0;
         for (int id = 0; id < M_COUNT; ++id) {
@@ -3704,6 +3844,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
 // adjoint (no reference counterpart) and Adam
 // ---------------------------------------------------------------------------
 int hx_tape_begin(hx_sim* sim, int max_steps) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     sim->tape_on = false;
@@ -3756,6 +3897,7 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
 int hx_tape_length(hx_sim* sim) { return sim->tape_on ? sim->tape_n : 0; }
 
 int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* target, int nsample, double* loss) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (!sim->tape_on || sim->tape_n == 0) return sim->fail("no taped steps (hx_tape_begin, finitialize, run)");
@@ -3923,6 +4065,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
 }
 
 int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out, int cap) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (!sim->have_grad) return sim->fail("no gradients (call hx_adjoint)");
@@ -3941,6 +4084,7 @@ int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out,
 }
 
 int hx_adam_create(hx_sim* sim, double beta1, double beta2, double eps) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     hx_sim::AdamHost o;
     o.beta1 = beta1;
@@ -3952,6 +4096,7 @@ int hx_adam_create(hx_sim* sim, double beta1, double beta2, double eps) {
 
 int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, int n, const int* inst,
                       double impedance) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
@@ -3977,6 +4122,7 @@ int hx_adam_add_group(hx_sim* sim, int opt, const char* mech, const char* var, i
 }
 
 int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
@@ -4018,6 +4164,7 @@ int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps) {
 }
 
 int hx_adam_get_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("bad optimizer id");
     const auto& o = sim->adams[opt];
     const int ng = static_cast<int>(o.imp.size());
@@ -4062,6 +4209,7 @@ int hx_sim::opt_add_group(int opt, const std::vector<double*>& w, const std::vec
 // weight), gradients are zeroed after each step
 // ---------------------------------------------------------------------------
 int hx_create_optimizer(hx_sim* sim, const char* type) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     std::string t = type ? type : "";
     std::transform(t.begin(), t.end(), t.begin(), [](unsigned char c) { return std::tolower(c); });
@@ -4075,6 +4223,7 @@ int hx_create_optimizer(hx_sim* sim, const char* type) {
 }
 
 int hx_configure_optimizer(hx_sim* sim, int opt, double momentum, double beta1, double beta2, double eps) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     auto& o = sim->adams[opt];
     o.momentum = momentum;
@@ -4086,6 +4235,7 @@ int hx_configure_optimizer(hx_sim* sim, int opt, double momentum, double beta1, 
 
 int hx_optimizer_add_param_batch(hx_sim* sim, int opt, int n, const int* weight_handles, const int* grad_handles,
                                  double impedance) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     if (n <= 0 || !weight_handles || !grad_handles)
@@ -4104,14 +4254,17 @@ int hx_optimizer_add_param_batch(hx_sim* sim, int opt, int n, const int* weight_
 }
 
 int hx_optimizer_add_param(hx_sim* sim, int opt, int weight_handle, int grad_handle, double impedance) {
+    HX_SETTLE(sim);
     return hx_optimizer_add_param_batch(sim, opt, 1, &weight_handle, &grad_handle, impedance);
 }
 
 int hx_optimizer_step_with_inv_record_steps(hx_sim* sim, int opt, double lr, double inv_record_steps) {
+    HX_SETTLE(sim);
     return hx_adam_step(sim, opt, lr, inv_record_steps);
 }
 
 int hx_optimizer_step(hx_sim* sim, int opt, double lr, double record_time, double dt) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer_step: optimizer %d not found", opt);
     if (record_time <= 0.0 || dt <= 0.0)
         return sim->fail("optimizer_step: invalid record_time (%f) or dt (%f)", record_time, dt);
@@ -4119,6 +4272,7 @@ int hx_optimizer_step(hx_sim* sim, int opt, double lr, double record_time, doubl
 }
 
 int hx_optimizer_add_external_grads(hx_sim* sim, int opt, int n, const int* weight_handles, double impedance) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
@@ -4139,6 +4293,7 @@ int hx_optimizer_add_external_grads(hx_sim* sim, int opt, int n, const int* weig
 }
 
 int hx_optimizer_set_external_grads_f32(hx_sim* sim, int opt, int n, const float* grads) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     auto& o = sim->adams[opt];
     if (!o.d_ext) return sim->fail("optimizer_set_external_grads_f32: optimizer %d has no external grads binding", opt);
@@ -4153,6 +4308,7 @@ int hx_optimizer_set_external_grads_f32(hx_sim* sim, int opt, int n, const float
 }
 
 int hx_optimizer_clear_external_grads(hx_sim* sim, int opt) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     auto& o = sim->adams[opt];
     if (!o.d_ext) return 0;
@@ -4164,6 +4320,7 @@ int hx_optimizer_clear_external_grads(hx_sim* sim, int opt) {
 }
 
 int hx_optimizer_reset_state(hx_sim* sim, int opt) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     auto& o = sim->adams[opt];
     if (o.type == 2) o.step = 0;
@@ -4175,6 +4332,7 @@ int hx_optimizer_reset_state(hx_sim* sim, int opt) {
 
 int hx_optimizer_get_adam_state(hx_sim* sim, int opt, long long* step, double* m, double* v, int cap, double* beta1,
                                 double* beta2, double* eps) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     const auto& o = sim->adams[opt];
     if (o.type != 2) return sim->fail("optimizer %d is not Adam", opt);
@@ -4186,6 +4344,7 @@ int hx_optimizer_get_adam_state(hx_sim* sim, int opt, long long* step, double* m
 
 int hx_optimizer_set_adam_state(hx_sim* sim, int opt, long long step, int n, const double* m, const double* v,
                                 double beta1, double beta2, double eps) {
+    HX_SETTLE(sim);
     if (opt < 0 || opt >= static_cast<int>(sim->adams.size())) return sim->fail("optimizer %d not found", opt);
     auto& o = sim->adams[opt];
     if (o.type != 2) return sim->fail("optimizer %d is not Adam", opt);
@@ -4206,6 +4365,7 @@ int hx_optimizer_set_adam_state(hx_sim* sim, int opt, long long step, int n, con
 // learn gradient surface (LearnRuntime.cpp:197-2457)
 // ---------------------------------------------------------------------------
 int hx_set_dense_blocks_f32(hx_sim* sim, int nblk, const float* const* blocks, const int* bn, const int* k_len) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     if (nblk < 0 || (nblk > 0 && (!blocks || !bn || !k_len))) return sim->fail("set_dense_blocks_f32: bad arguments");
@@ -4217,6 +4377,7 @@ int hx_set_dense_blocks_f32(hx_sim* sim, int nblk, const float* const* blocks, c
 }
 
 int hx_clear_dense_blocks(hx_sim* sim) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     sim->learn_rt().clear_dense_blocks();
@@ -4255,6 +4416,7 @@ bool check_tstop(hx_sim* sim, const char* fn, int total_steps, double tstop_ms) 
 
 int hx_simulate_output_vs_into(hx_sim* sim, float* output_vs_tn, int t_steps_plus1, int n_output,
                                const int* output_v_handles, double tstop_ms, double v_init) {
+    HX_SETTLE(sim);
     static const char* fn = "simulate_output_vs_into";
     if (!check_loaded(sim)) return -1;
     if (!output_vs_tn) return sim->fail("%s: output buffer is null", fn);
@@ -4354,6 +4516,7 @@ int hx_simulate_and_capture_mapped_signals_cached(
     const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
     const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
     const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     return capture_common(sim, "simulate_and_capture_mapped_signals_cached", output_vs_tn, total_steps_plus1,
                           n_output, output_v_handles, n_pure_i, pure_i_handles, pure_i_dest, pure_i_scale, n_didv,
@@ -4367,6 +4530,7 @@ int hx_simulate_and_capture_mapped_signals_into(
     const int* pure_i_handles, const int* pure_i_dest, const float* pure_i_scale, int n_didv, const int* didv_handles,
     const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
     const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init) {
+    HX_SETTLE(sim);
     static const char* fn = "simulate_and_capture_mapped_signals_into";
     if (!check_loaded(sim)) return -1;
     if (!output_vs_tn || !it_lr_tn || !ditdv_lr_tn || !ditdvpre_lr_tn)
@@ -4445,6 +4609,7 @@ int hx_replay_compute_dw_from_cached_signals_into(hx_sim* sim, const float* dLtd
                                                   float* dw_out_n, double dt_ms, int percise, double grad_scale,
                                                   double eps, double grad_l2norm_threshold, int clip_strategy,
                                                   int clip_check_every) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     API_BEGIN
     return replay_common(sim, "replay_compute_dw_from_cached_signals_into", LearnRuntime::SRC_CACHE, dLtdv_lr_to,
@@ -4460,6 +4625,7 @@ int hx_replay_compute_dw_dx_from_cached_signals_into(hx_sim* sim, const float* d
                                                      float* dx_lr_it, double dt_ms, int percise, double grad_scale,
                                                      double eps, double grad_l2norm_threshold, int clip_strategy,
                                                      int clip_check_every) {
+    HX_SETTLE(sim);
     static const char* fn = "replay_compute_dw_dx_from_cached_signals_into";
     if (!check_loaded(sim)) return -1;
     if (n_input <= 0) return sim->fail("%s: empty poutput/pinput", fn);
@@ -4477,6 +4643,7 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
                                               int n_input, const int* pre_of_col, float* dw_out_n, float* dx_lr_it,
                                               double dt_ms, int percise, double grad_scale, double eps,
                                               double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    HX_SETTLE(sim);
     static const char* fn = "replay_compute_dw_dx_from_signals_into";
     if (!check_loaded(sim)) return -1;
     API_BEGIN
@@ -4511,6 +4678,7 @@ int hx_replay_compute_dw_dx_from_signals_into_noalloc(
     const float* dLtdv_lr_to, int ksteps_total, int n_output, const int* poutput, const int* pinput, int n_input,
     const int* pre_of_col, float* dw_out_n, float* dx_lr_it, double dt_ms, int percise, double grad_scale, double eps,
     double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    HX_SETTLE(sim);
     static const char* fn = "replay_compute_dw_dx_from_signals_into_noalloc";
     if (!check_loaded(sim)) return -1;
     API_BEGIN
@@ -4546,6 +4714,7 @@ int hx_simulate_and_replay_dw_dx_streaming_into(
     const int* didv_dest, const float* didv_scale, int n_didvpre, const int* didvpre_handles, const int* didvpre_dest,
     const float* didvpre_scale, double tstop_ms, int k_mul, int percise, double v_init, double dt_ms,
     double grad_scale, double eps, double grad_l2norm_threshold, int clip_strategy, int clip_check_every) {
+    HX_SETTLE(sim);
     static const char* fn = "simulate_and_replay_dw_dx_streaming_into";
     if (!check_loaded(sim)) return -1;
     API_BEGIN
@@ -4603,12 +4772,14 @@ int hx_simulate_and_replay_dw_dx_streaming_into(
 }
 
 int hx_set_replay_timing(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     sim->learn_rt().timing = enable != 0;
     return 0;
 }
 
 int hx_get_replay_kernel_time(hx_sim* sim, double* ms, long long* launches) {
+    HX_SETTLE(sim);
     if (!check_loaded(sim)) return -1;
     LearnRuntime& L = sim->learn_rt();
     if (ms) *ms = L.corr_ms;

@@ -89,6 +89,7 @@ SIGNATURES = {
     "hx_get_spk_by_gid": (C.c_int, [_P, C.c_int, _D, C.c_int]),
     "hx_set_event_capacity": (C.c_int, [_P, C.c_int]),
     "hx_set_fusion": (C.c_int, [_P, C.c_int]),
+    "hx_set_close_deferral": (C.c_int, [_P, C.c_int]),
     "hx_set_uniform_columns": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling_classes": (C.c_int, [_P, _S]),
@@ -317,6 +318,9 @@ class Sim:
 
     def set_fusion(self, enable: bool) -> int:
         return self._rc(lib().hx_set_fusion(self._h, 1 if enable else 0))
+
+    def set_close_deferral(self, enable: bool) -> int:
+        return self._rc(lib().hx_set_close_deferral(self._h, 1 if enable else 0))
 
     def set_uniform_columns(self, enable: bool) -> int:
         """Read parameter columns holding one value as scalars (default on)."""

@@ -233,6 +233,13 @@ int hx_set_event_capacity(hx_sim* sim, int per_step);
 /* enable = 1 (default): fold each step's state update into the next step's current pass when that is
  * exact; 0: always run the reference's separate current and state passes. */
 int hx_set_fusion(hx_sim* sim, int enable);
+/* No reference counterpart.  enable = 1 (default): hx_run, hx_continue_run and hx_fadvance may
+ * return with their last step's state update (nrn_state) still pending when no monitor, tape or
+ * signal capture samples the states; the next stepping call's first node pass applies it, as every
+ * step applies the previous one, and any other entry point first completes it with the pass the
+ * call would have ended with.  Results are the same bits either way; 0: every call ends with
+ * that pass. */
+int hx_set_close_deferral(hx_sim* sim, int enable);
 /* No reference counterpart.  enable = 1 (default): a mechanism parameter column that holds
  * one value for every instance at hx_load_model is read by the node kernels as that value
  * instead of once per instance from HBM (the full column stays in HBM and is what handles,
@@ -275,7 +282,8 @@ int hx_set_solve_unit_cells(hx_sim* sim, int cells);
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused",
- * "cell_groups", "multi_stream" (1 if the last run used per-group streams). */
+ * "cell_groups", "multi_stream" (1 if the last run used per-group streams), "state_pending"
+ * (1 while the last stepping call's state update waits, see hx_set_close_deferral). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the

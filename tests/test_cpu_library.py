@@ -29,6 +29,28 @@ def test_library_exports_every_header_symbol():
     assert set(syms) == set(SIGNATURES), set(syms) ^ set(SIGNATURES)
 
 
+def test_entry_points_complete_a_deferred_state_update():
+    """A stepping call may return with its last state update pending; every other
+    entry point that takes a handle must complete it (HX_SETTLE) before it reads or
+    changes the model.  The exempt ones read only host-side values."""
+    src = open(os.path.join(ROOT, "heliox_amd", "csrc", "runtime.cpp")).read()
+    stepping = {"hx_run", "hx_continue_run", "hx_fadvance"}
+    host_only = {"hx_destroy", "hx_last_error", "hx_get_dt", "hx_get_t", "hx_get_info",
+                 "hx_is_spike_output_enabled", "hx_is_hdf5_enabled", "hx_get_spike_count",
+                 "hx_tape_length", "hx_get_spikes", "hx_get_spk_by_gid", "hx_output_spikes"}
+    seen = set()
+    for m in re.finditer(r"^(?:int|void|double|long long|const char\*) (hx_\w+)\(\s*hx_sim\* sim", src, re.M):
+        name = m.group(1)
+        seen.add(name)
+        body = src[src.find("{", m.end()):][:200]
+        first = body[1:].strip().split("\n")[0]
+        if name in stepping:
+            assert "DeferScope" in src[m.end():src.find("\n}\n", m.end())], name
+        elif name not in host_only:
+            assert first == "HX_SETTLE(sim);", f"{name} does not complete a deferred state update first"
+    assert stepping <= seen and len(seen) > 80
+
+
 def test_nm_exports_match_header():
     so = os.path.join(ROOT, "heliox_amd", "libheliox_amd.so")
     out = os.popen(f"nm -D --defined-only {so}").read()
