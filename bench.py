@@ -446,6 +446,7 @@ def main():
     # the timed call's last state update may wait for the next call (the first node pass of
     # the timed call applied the warm-up call's in the same way): 1 if it did
     deferred = sim.info("state_pending")
+    outputs_deferred = sim.info("outputs_pending")
 
     value = nnode * args.steps / wall
     ms_per_step = wall * 1e3 / args.steps
@@ -536,6 +537,7 @@ def main():
                    "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "state_update_deferred": bool(deferred),
+        "last_step_outputs_on_demand": bool(outputs_deferred),
         "roofline": roofline,
         "roofline_single_stream": alone,
         "step_bytes": step_bytes(spec, ms_per_step, uniform_bytes),

@@ -108,6 +108,7 @@ struct StepArgs {
                                   // depends on ica and cai only, so this is the step's own update)
     int do_current;
     int write_assigned;           // also store the current's assigned outputs (i, ina, gna, ...)
+    int point_assigned;           // the node kernel's synapse fold stores the synapses' outputs (i, g)
     int write_rates;              // also store the state update's rates (minf, mtau, ...)
     int write_dcurdv;             // store the ions' dcurdv (0: it still holds the 0 stored at init)
     unsigned ion_store;           // ion x (0 na, 1 k, 2 ca): bit 2x stores cur, bit 2x+1 stores erev

@@ -362,7 +362,7 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
 // ---------------------------------------------------------------------------
 template <int MECH>
 __device__ __forceinline__ void point_current(const StepArgs& A, const MechDev& m, int j, double v, double& i0,
-                                              double& g) {
+                                              double& g, int store) {
     const double v1 = v + 0.001;
     double i1 = 0.0;
     i0 = 0.0;
@@ -372,23 +372,23 @@ __device__ __forceinline__ void point_current(const StepArgs& A, const MechDev& 
         if (A.t < del + dur && A.t >= del) cur = m.col(IC_AMP)[j];
         i1 = cur;
         i0 = cur;
-        if (A.write_assigned) m.col(IC_I)[j] = cur;
+        if (store) m.col(IC_I)[j] = cur;
     } else if (MECH == M_HALFGAP) {
         const double vg = m.col(HG_VGAP)[j], gg = m.col(HG_G)[j];
         i1 = (vg - v1) * gg;
         i0 = (vg - v) * gg;
-        if (A.write_assigned) m.col(HG_I)[j] = i0;
+        if (store) m.col(HG_I)[j] = i0;
     } else if (MECH == M_EXPSYN) {
         const double gg = m.col(ES_G)[j], e = m.col(ES_E)[j];
         i1 = gg * (v1 - e);
         i0 = gg * (v - e);
-        if (A.write_assigned) m.col(ES_I)[j] = i0;
+        if (store) m.col(ES_I)[j] = i0;
     } else if (MECH == M_EXP2SYN) {
         const double gg = m.col(E2_B)[j] - m.col(E2_A)[j];
         const double e = m.col(E2_E)[j];
         i1 = gg * (v1 - e);
         i0 = gg * (v - e);
-        if (A.write_assigned) { m.col(E2_G)[j] = gg; m.col(E2_I)[j] = i0; }
+        if (store) { m.col(E2_G)[j] = gg; m.col(E2_I)[j] = i0; }
     }
     g = (i1 - i0) * 1000.0;   // / 0.001
 }
@@ -415,7 +415,7 @@ __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, 
         const double mfact = 1.e2 / A.area[i];
         for (int j = f; j < l; ++j) {
             double i0, g;
-            point_current<MECH>(A, m, j, v, i0, g);
+            point_current<MECH>(A, m, j, v, i0, g, A.point_assigned);
             rhs -= i0 * mfact;
             d += g * mfact;
         }
@@ -434,7 +434,7 @@ __global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
     double rhs = 0.0, d = 0.0;
     for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) {
         double i0, g;
-        point_current<MECH>(A, m, j, v, i0, g);
+        point_current<MECH>(A, m, j, v, i0, g, A.point_assigned);
         g *= mfact;
         i0 *= mfact;
         if (MECH == M_ICLAMP || MECH == M_HALFGAP) {   // ELECTRODE_CURRENT: the sign flips
@@ -804,7 +804,8 @@ __device__ __forceinline__ void back_load(const SolveCtx& C, BackBuf<kX>& B, con
     B.ri = ri;
 }
 
-// kX: x = vn - v goes to rhs (the reference leaves the solution there).
+// kX: x = vn - v goes to rhs (the reference leaves the solution there), and the old
+// voltage to w, where an outputs-only node pass after the call reads it.
 template <int kX>
 __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>& B, BackBuf<kX>& N,
                                            const RoundV& next) {
@@ -827,6 +828,7 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>&
     const double vpar = (act && parent_slot != kNone) ? C.slots[2 * parent_slot] : 0.0;
     const __amdgpu_buffer_rsrc_t rv = cell_buffer(C.S.v + C.nb, C.nn);
     const __amdgpu_buffer_rsrc_t rx = cell_buffer(C.S.rhs + C.nb, C.nn);
+    const __amdgpu_buffer_rsrc_t rw = cell_buffer(C.S.w + C.nb, C.nn);
     double vtail = 0.0;
     __builtin_amdgcn_s_setprio(3);
     dispatch_chunk_bound(ri.maxlen, [&](auto km) {
@@ -835,7 +837,10 @@ __device__ __forceinline__ void back_round(const SolveCtx& C, const BackBuf<kX>&
         round_positions<KM>(ri, len, C.lane, rp, wo, tp);
         auto out = [&](int k, double vn, double vo) {
             store_f64(rv, wo[k], vn);
-            if constexpr (kX != 0) store_f64(rx, wo[k], vn - vo);
+            if constexpr (kX != 0) {
+                store_f64(rx, wo[k], vn - vo);
+                store_f64(rw, wo[k], vo);   // w (read for this node already) keeps the old voltage
+            }
             if (k == len - 1) vtail = vn;
         };
         if constexpr (kX != 0) chunk_back_math<KM>(StageInX{{st, rp}}, out, vpar);

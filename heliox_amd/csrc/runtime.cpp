@@ -440,6 +440,13 @@ struct hx_sim {
     bool close_deferral = true;
     bool defer_allowed = false;
     bool pending_sampled = false;   // the pending step's (voltage) samples are already recorded
+    // A call that may defer its closing pass, on a model whose density mechanisms all run
+    // in the node kernel, also leaves that kernel's assigned outputs of its last step
+    // (ina, ica, i, ion cur and erev, ...) unstored (lazy_outputs_run); they are made when
+    // something reads them (outputs_pending, settle) by an outputs-only node pass over the
+    // last step's voltages, which the solve keeps in w, and its states, still pending.
+    bool lazy_outputs_run = false;
+    bool outputs_pending = false;
     bool final_step = false;   // the last step of a run call also stores every assigned variable
     bool initialized = false;
     // adjoint tape (hx_tape_begin): row n holds v^{n+1} (after step n's solve); the
@@ -612,6 +619,7 @@ struct hx_sim {
     void ensure_ttab(int kneed);
     Ref resolve(const std::string& mechname, const std::string& var, int idx);
     StepArgs step_args(double tcur, int do_state, int do_current) const;
+    unsigned ion_store_bits(bool assigned) const;
     // ------------------------------------------------------------ stepping
     void launch_mech_pass(int do_state, int do_current, double tcur, int grp = -1, hipStream_t on = nullptr);
     void launch_point_currents(double tcur);
@@ -629,6 +637,9 @@ struct hx_sim {
     void step_once();
     void finish_pending();
     bool can_defer_close() const;
+    bool close_may_defer() const;
+    bool lazy_outputs_ok() const;
+    void launch_outputs_pass();
     void sample_pending_step();
     int settle();
     int run_steps(int nstep);
@@ -1712,6 +1723,24 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     return r;
 }
 
+// An ion's cur and erev are stored when something outside the fused kernel reads
+// them: a mechanism run instance-parallel, CaDynamics_E2 (reads ica in the next
+// state update) or a handle/monitor on an assigned variable (assigned).
+unsigned hx_sim::ion_store_bits(bool assigned) const {
+    const auto& R = registry();
+    unsigned need = 0;
+    for (int id = 0; id < M_COUNT; ++id)
+        if (mech[id].present && !(dense_mask & (1u << id))) need |= static_cast<unsigned>(R[id].ion_use);
+    need |= plugin_ions();     // plugins read erev and add their currents after the node kernel
+    unsigned bits = 0;
+    for (int x = 0; x < 3; ++x) {
+        const bool ext = assigned || (need & (1u << x));
+        if (ext || (x == 2 && mech[M_CADYN].present && !pass_cadyn_after)) bits |= 1u << (2 * x);
+        if (ext) bits |= 2u << (2 * x);
+    }
+    return bits;
+}
+
 StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     StepArgs A{};
     A.N = nnode;
@@ -1733,31 +1762,20 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.cadyn_skip = do_state ? pass_cadyn_skip : 0;
     A.cadyn_after = do_current ? pass_cadyn_after : 0;
     A.do_current = do_current;
-    const bool assigned = write_assigned || final_step;
+    // A call whose outputs are made on demand (lazy_final) stores none of the node kernel's
+    // assigned outputs on its last step; the synapses' outputs are stored as usual.
+    const bool lazy_final = final_step && lazy_outputs_run && do_current;
+    const bool assigned = write_assigned || (final_step && !lazy_final);
     A.write_assigned = assigned ? 1 : 0;
+    A.point_assigned = (assigned || lazy_final) ? 1 : 0;
     // A call's last step stores the rates once, in its closing state pass (the fused
     // pass before it updates the previous step's states, whose rates that pass
     // overwrites).  dcurdv holds the 0 that finitialize's pass stored unless a handle
     // made every step store the assigned variables.
     A.write_rates = (write_assigned || (final_step && !do_current)) ? 1 : 0;
+    A.ion_store = ion_store_bits(assigned);
+    for (int x = 0; x < 3; ++x) A.ion_type[x] = ion_type_uniform[x];
     A.write_dcurdv = (write_assigned || init_pass) ? 1 : 0;
-    // An ion's cur and erev are stored when something outside the fused kernel
-    // reads them: a mechanism run instance-parallel, CaDynamics_E2 (reads ica in
-    // the next state update) or a handle/monitor on an assigned variable.
-    {
-        const auto& R = registry();
-        unsigned need = 0;
-        for (int id = 0; id < M_COUNT; ++id)
-            if (mech[id].present && !(dense_mask & (1u << id))) need |= static_cast<unsigned>(R[id].ion_use);
-        need |= plugin_ions();     // plugins read erev and add their currents after the node kernel
-        A.ion_store = 0;
-        for (int x = 0; x < 3; ++x) {
-            const bool ext = assigned || (need & (1u << x));
-            if (ext || (x == 2 && mech[M_CADYN].present && !pass_cadyn_after)) A.ion_store |= 1u << (2 * x);
-            if (ext) A.ion_store |= 2u << (2 * x);
-            A.ion_type[x] = ion_type_uniform[x];
-        }
-    }
     A.fold_mask = 0;
     for (int id : {M_EXPSYN, M_EXP2SYN})
         if (mech[id].present && mech[id].n > 0) A.fold_mask |= 1u << id;
@@ -2119,8 +2137,11 @@ void hx_sim::step_once_groups() {
     const StepArgs post = step_args(tn, 1, 0);
     const size_t nm = mon_ref.size();
     if (sample && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
+    // the last step of a call with outputs on demand leaves calcium to the state update,
+    // so the outputs pass reads the concentration its current evaluation used
+    const bool eager = cadyn_eager && !(final_step && lazy_outputs_run);
     pass_cadyn_skip = cadyn_done ? 1 : 0;
-    pass_cadyn_after = cadyn_eager ? 1 : 0;
+    pass_cadyn_after = eager ? 1 : 0;
     // First step of a run: each group starts once the previous group's node pass is
     // done, so from then on one group's tree solve (latency-bound) runs beside the
     // other's node pass (HBM-bound) instead of two node passes and then two solves
@@ -2190,7 +2211,7 @@ void hx_sim::step_once_groups() {
     }
     if (sample && nm) mon_buf_fill++;
     pending_sampled = false;
-    cadyn_done = cadyn_eager;
+    cadyn_done = eager;
     pass_cadyn_skip = pass_cadyn_after = 0;
     t = tn;
     k += 1;
@@ -2213,10 +2234,11 @@ void hx_sim::step_once() {
         // currents with this step's deliveries in place
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        const bool eager = cadyn_eager && !(final_step && lazy_outputs_run);   // as in step_once_groups
         pass_cadyn_skip = cadyn_done ? 1 : 0;
-        pass_cadyn_after = cadyn_eager ? 1 : 0;
+        pass_cadyn_after = eager ? 1 : 0;
         launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
-        cadyn_done = cadyn_eager;
+        cadyn_done = eager;
         pass_cadyn_skip = pass_cadyn_after = 0;
         if (state_pending && !pending_sampled) launch_record();
         pending_sampled = false;
@@ -2301,9 +2323,44 @@ void hx_sim::finish_pending() {
 // The closing pass may wait for the next call when nothing samples the states
 // inside the step loop: every monitor samples a voltage (taken at the call's end,
 // sample_pending_step), no tape and no signal capture.
-bool hx_sim::can_defer_close() const {
-    return defer_allowed && close_deferral && fused && state_pending && (mon_ref.empty() || mon_all_v) &&
-           !tape_on && !(learn && learn->capturing());
+bool hx_sim::close_may_defer() const {
+    return defer_allowed && close_deferral && fused && (mon_ref.empty() || mon_all_v) && !tape_on &&
+           !(learn && learn->capturing());
+}
+bool hx_sim::can_defer_close() const { return state_pending && close_may_defer(); }
+
+// Outputs on demand need the node kernel to make every density mechanism's outputs
+// (an instance-parallel mechanism or a plugin adds ion currents after it) and no
+// handle or transfer that reads outputs inside the step loop.
+bool hx_sim::lazy_outputs_ok() const {
+    if (!close_may_defer() || write_assigned || !dg_src.empty() || !plugins.empty()) return false;
+    for (int id : kSparseOrder)
+        if (mech[id].present && !(dense_mask & (1u << id))) return false;
+    return dense_mask != 0;
+}
+
+// The node kernel's assigned outputs of the call's last step: its current evaluation
+// again, on the voltages before that step's solve (kept in w by k_solve<1>) and the
+// states it used (their update is still pending).  Its d and rhs go to w too (each
+// thread reads its own voltage there before it stores), so the solve's pivots and x
+// stay in d and rhs.
+void hx_sim::launch_outputs_pass() {
+    const bool f = final_step, l = lazy_outputs_run;
+    final_step = true;
+    lazy_outputs_run = false;      // this pass stores the outputs
+    pass_cadyn_after = 0;
+    StepArgs A = step_args(t - 0.5 * dt, 0, 1);
+    final_step = f;
+    lazy_outputs_run = l;
+    A.v = d_w;
+    A.d = d_w;
+    A.rhs = d_w;
+    A.fold_mask = 0;
+    A.point_assigned = 0;
+    tbegin(T_MECH);
+    launch_dense(A, stream);
+    tend(T_MECH);
+    outputs_pending = false;
 }
 
 // A deferred call end still records the last step's samples: a voltage after the
@@ -2329,6 +2386,7 @@ void hx_sim::sample_pending_step() {
 int hx_sim::settle() {
     if (!state_pending) return 0;
     try {
+        if (outputs_pending) launch_outputs_pass();
         final_step = true;
         finish_pending();
         final_step = false;
@@ -2435,6 +2493,8 @@ int hx_sim::run_steps(int nstep) {
     // last step of the call stores them all, so they read back as after the
     // reference's last step.
     final_step = false;
+    outputs_pending = false;           // this call's last step makes new ones
+    lazy_outputs_run = lazy_outputs_ok();
     // cell groups on their own streams: they start after everything already on
     // the library stream, and the library stream waits for all of them
     multi_stream = want_multi_stream();
@@ -2449,8 +2509,13 @@ int hx_sim::run_steps(int nstep) {
             final_step = s == nstep - 1;
             step_once();
         }
-        if (can_defer_close()) sample_pending_step();
-        else finish_pending();
+        if (can_defer_close()) {
+            sample_pending_step();
+            outputs_pending = lazy_outputs_run;
+        } else {
+            if (lazy_outputs_run) launch_outputs_pass();
+            finish_pending();
+        }
     } catch (...) {
         if (multi_stream) {
             for (auto& cg : groups) (void)hipStreamSynchronize(cg.s);
@@ -2540,6 +2605,8 @@ void hx_sim::finitialize(double v_init) {
     k = 0;
     state_pending = false;
     pending_sampled = false;
+    outputs_pending = false;
+    lazy_outputs_run = false;
     cadyn_done = false;
     pass_cadyn_skip = pass_cadyn_after = 0;
     ensure_ttab(1);
@@ -3827,6 +3894,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "cell_groups") return static_cast<long long>(sim->groups.size());
     if (k == "multi_stream") return sim->last_multi_stream ? 1 : 0;
     if (k == "state_pending") return sim->state_pending ? 1 : 0;
+    if (k == "outputs_pending") return sim->outputs_pending ? 1 : 0;
     if (k == "uniform_columns" || k == "uniform_bytes") {
         long long cols = 0, bytes = 0;
         for (int id = 0; id < M_COUNT; ++id) {

@@ -237,8 +237,10 @@ int hx_set_fusion(hx_sim* sim, int enable);
  * return with their last step's state update (nrn_state) still pending when no monitor, tape or
  * signal capture samples the states; the next stepping call's first node pass applies it, as every
  * step applies the previous one, and any other entry point first completes it with the pass the
- * call would have ended with.  Results are the same bits either way; 0: every call ends with
- * that pass. */
+ * call would have ended with.  When every density mechanism runs in the fused node kernel, that
+ * kernel's assigned outputs of the last step are made the same way, on the first entry point that
+ * is not a stepping call.  Results are the same bits either way; 0: every call ends with that
+ * pass and stores its outputs. */
 int hx_set_close_deferral(hx_sim* sim, int enable);
 /* No reference counterpart.  enable = 1 (default): a mechanism parameter column that holds
  * one value for every instance at hx_load_model is read by the node kernels as that value
@@ -283,7 +285,8 @@ int hx_set_solve_unit_cells(hx_sim* sim, int cells);
 int hx_set_group_streams(hx_sim* sim, int enable);
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused",
  * "cell_groups", "multi_stream" (1 if the last run used per-group streams), "state_pending"
- * (1 while the last stepping call's state update waits, see hx_set_close_deferral). */
+ * (1 while the last stepping call's state update waits, see hx_set_close_deferral),
+ * "outputs_pending" (1 while its node-kernel outputs wait). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the

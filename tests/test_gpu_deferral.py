@@ -1,7 +1,9 @@
-"""A stepping call that returns with its last state update pending (close deferral)
-gives the same bits as one that ends with the closing state pass: voltage traces,
-spikes and every column of every mechanism, read after the last call, between calls,
-and after writes, a fusion switch or a restarted run between calls."""
+"""A stepping call that returns with its last state update pending (close deferral),
+and on a model whose density mechanisms all run in the node kernel with that kernel's
+assigned outputs made on demand, gives the same bits as one that ends with the closing
+state pass: voltage traces, spikes and every column of every mechanism, read after the
+last call, between calls, and after writes, a fusion switch or a restarted run between
+calls."""
 import dataclasses
 
 import numpy as np
@@ -57,6 +59,10 @@ def test_deferred_close_same_bits(gpu_lib, config, ncell, monitors):
         # nothing read between these calls: the pending update carries over (the split
         # schedule, chosen for a model whose VecPlay drives a node variable, has none)
         assert a.info("state_pending") == a.info("fused") and b.info("state_pending") == 0
+        # config 3 runs every density mechanism in the node kernel: its last step's
+        # outputs are made on demand
+        assert a.info("outputs_pending") == (1 if config == 3 else 0)
+        assert b.info("outputs_pending") == 0
     a.fadvance()
     b.fadvance()
     n = assert_same(spec, a, b)
@@ -73,11 +79,14 @@ def test_deferred_close_with_cell_groups(gpu_lib, config, ncell):
         a.continue_run(c)
         b.continue_run(c)
     assert a.info("multi_stream") == 1 and a.info("state_pending") == 1
+    assert a.info("outputs_pending") == (1 if config == 3 else 0)
     assert assert_same(spec, a, b) > 10
+    assert a.info("outputs_pending") == 0
 
 
-def test_reads_and_writes_between_deferred_calls(gpu_lib):
-    spec = dataclasses.replace(build_config(2, 6, 2.0), monitors=[])
+@pytest.mark.parametrize("config,ncell", [(2, 6), (3, 2)])
+def test_reads_and_writes_between_deferred_calls(gpu_lib, config, ncell):
+    spec = dataclasses.replace(build_config(config, ncell, 2.0), monitors=[])
     a, b = make(spec, True), make(spec, False)
     for g in (a, b):
         g.continue_run(12 * DT)
