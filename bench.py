@@ -438,6 +438,9 @@ def main():
     # only the dominant kernel is timed with events on the stream (each timed
     # class adds two event records per step to the timed region)
     sim.set_profiling(not args.no_kernel_timing, classes=None if args.all_kernel_timing else ["mech"])
+    # the warm-up call's last state update, if it waits, is applied by the timed call's first
+    # node pass, as every step applies the previous one's
+    carried_in = sim.info("state_pending")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     sim.continue_run((args.steps + 0.5) * dt)      # returns after the stream is synchronized
@@ -536,6 +539,7 @@ def main():
                                f"Poisson VecStim input, dt 0.025 ms",
                    "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
+        "state_update_carried_in": bool(carried_in),
         "state_update_deferred": bool(deferred),
         "last_step_outputs_on_demand": bool(outputs_deferred),
         "roofline": roofline,

@@ -400,6 +400,7 @@ struct hx_sim {
     std::vector<double> ttab;
     double* d_ttab = nullptr;
     int ttab_cap = 0;
+    int ttab_up = 0;                 // entries of ttab already in d_ttab (the table only grows)
     // gap
     int* d_gap_src = nullptr;
     int* d_gap_inst = nullptr;
@@ -617,6 +618,7 @@ struct hx_sim {
     void upload_vecplay();
     void upload_monitors();
     void ensure_ttab(int kneed);
+    void ensure_mon_rows(long long rows);
     Ref resolve(const std::string& mechname, const std::string& var, int idx);
     StepArgs step_args(double tcur, int do_state, int do_current) const;
     unsigned ion_store_bits(bool assigned) const;
@@ -1629,10 +1631,28 @@ void hx_sim::ensure_ttab(int kneed) {
     if (ttab_cap < static_cast<int>(ttab.size())) {
         ttab_cap = static_cast<int>(ttab.size()) * 2;
         d_ttab = dalloc<double>(owned, ttab_cap);
-        HXC(hipMemcpy(d_ttab, ttab.data(), sizeof(double) * ttab.size(), hipMemcpyHostToDevice));
-    } else {
-        HXC(hipMemcpy(d_ttab, ttab.data(), sizeof(double) * ttab.size(), hipMemcpyHostToDevice));
+        ttab_up = 0;
     }
+    // only new entries travel: a call whose steps the table already covers copies nothing
+    const int n = static_cast<int>(ttab.size());
+    if (ttab_up < n) {
+        HXC(hipMemcpy(d_ttab + ttab_up, ttab.data() + ttab_up, sizeof(double) * (n - ttab_up),
+                      hipMemcpyHostToDevice));
+        ttab_up = n;
+    }
+}
+
+// Monitor sample rows: a call of n steps records n rows (finitialize one).  The buffer
+// grows geometrically, from at least 1024 rows while that stays within 64 MB, so calls
+// of similar length do not allocate.
+void hx_sim::ensure_mon_rows(long long rows) {
+    if (mon_ref.empty() || mon_buf_cap >= rows) return;
+    const long long nm = static_cast<long long>(mon_ref.size());
+    long long want = std::max(rows, 2 * mon_buf_cap);
+    want = std::max(want, std::min<long long>(1024, std::max<long long>(1, (64LL << 20) / (8 * nm))));
+    mon_buf_cap = want;
+    d_mon_buf = dalloc<double>(owned, static_cast<size_t>(want * nm));
+    mon_buf_fill = 0;
 }
 
 Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
@@ -2385,6 +2405,8 @@ void hx_sim::sample_pending_step() {
 // (it also stores the rates, as a call's closing pass does) and waits for it.
 int hx_sim::settle() {
     if (!state_pending) return 0;
+    const bool prof = profiling;
+    profiling = false;                 // the kernel timers cover stepping calls only
     try {
         if (outputs_pending) launch_outputs_pass();
         final_step = true;
@@ -2393,8 +2415,10 @@ int hx_sim::settle() {
         HXC(hipStreamSynchronize(stream));
     } catch (const std::exception& e) {
         final_step = false;
+        profiling = prof;
         return fail("%s", e.what());
     }
+    profiling = prof;
     return 0;
 }
 
@@ -2483,11 +2507,7 @@ int hx_sim::run_steps(int nstep) {
     }
     if (mon_dirty) upload_monitors();
     if (vecplay_dirty) upload_vecplay();
-    if (!mon_ref.empty() && mon_buf_cap < nstep + 2) {
-        mon_buf_cap = nstep + 2;
-        d_mon_buf = dalloc<double>(owned, static_cast<size_t>(mon_buf_cap) * mon_ref.size());
-        mon_buf_fill = 0;
-    }
+    ensure_mon_rows(nstep + 2);
     // Assigned variables (ion currents and reversal potentials, hh ina, minf,
     // ...) with no reader inside the step are not stored on every step; the
     // last step of the call stores them all, so they read back as after the
@@ -2610,10 +2630,7 @@ void hx_sim::finitialize(double v_init) {
     cadyn_done = false;
     pass_cadyn_skip = pass_cadyn_after = 0;
     ensure_ttab(1);
-    if (!mon_ref.empty() && mon_buf_cap < 2) {
-        mon_buf_cap = 2;
-        d_mon_buf = dalloc<double>(owned, static_cast<size_t>(mon_buf_cap) * mon_ref.size());
-    }
+    ensure_mon_rows(2);
     mon_buf_fill = 0;
     for (auto& md : mon_data) md.clear();
     h5_written.assign(mon_data.size(), 0);     // the file keeps growing across finitialize
@@ -3674,8 +3691,9 @@ int hx_set_close_deferral(hx_sim* sim, int enable) {
     return 0;
 }
 
+// The kernel timers are host state: these three neither read nor change the model, so
+// they leave a pending state update pending (a timed call then starts as every call does).
 int hx_set_profiling(hx_sim* sim, int enable) {
-    HX_SETTLE(sim);
     sim->profiling = enable != 0;
     sim->prof_mask = ~0u;
     for (auto& tm : sim->timers) { tm.ms = 0; tm.launches = 0; }
@@ -3683,7 +3701,6 @@ int hx_set_profiling(hx_sim* sim, int enable) {
 }
 
 int hx_set_profiling_classes(hx_sim* sim, const char* classes) {
-    HX_SETTLE(sim);
     unsigned mask = 0;
     std::string all = classes ? classes : "";
     size_t pos = 0;
@@ -3707,7 +3724,6 @@ int hx_set_profiling_classes(hx_sim* sim, const char* classes) {
 }
 
 int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches) {
-    HX_SETTLE(sim);
     for (int i = 0; i < T_COUNT; ++i)
         if (kernel && std::string(kernel) == kTimerNames[i]) {
             if (ms) *ms = sim->timers[i].ms;

@@ -37,7 +37,8 @@ def test_entry_points_complete_a_deferred_state_update():
     stepping = {"hx_run", "hx_continue_run", "hx_fadvance"}
     host_only = {"hx_destroy", "hx_last_error", "hx_get_dt", "hx_get_t", "hx_get_info",
                  "hx_is_spike_output_enabled", "hx_is_hdf5_enabled", "hx_get_spike_count",
-                 "hx_tape_length", "hx_get_spikes", "hx_get_spk_by_gid", "hx_output_spikes"}
+                 "hx_tape_length", "hx_get_spikes", "hx_get_spk_by_gid", "hx_output_spikes",
+                 "hx_set_profiling", "hx_set_profiling_classes", "hx_get_kernel_time"}
     seen = set()
     for m in re.finditer(r"^(?:int|void|double|long long|const char\*) (hx_\w+)\(\s*hx_sim\* sim", src, re.M):
         name = m.group(1)

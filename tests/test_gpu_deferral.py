@@ -78,6 +78,12 @@ def test_deferred_close_with_cell_groups(gpu_lib, config, ncell):
     for c in (10 * DT, 3 * DT, 10 * DT):
         a.continue_run(c)
         b.continue_run(c)
+        # the kernel timers are host state: switching them leaves the update pending
+        for g in (a, b):
+            g.set_profiling(True, classes=["mech"])
+        assert a.info("state_pending") == 1
+    a.kernel_time("mech")
+    assert a.info("state_pending") == 1                             # reading the timers too
     assert a.info("multi_stream") == 1 and a.info("state_pending") == 1
     assert a.info("outputs_pending") == (1 if config == 3 else 0)
     assert assert_same(spec, a, b) > 10
