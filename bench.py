@@ -350,10 +350,17 @@ def calibrate_copy(gib: float = 1.0, reps: int = 5):
     n = int(gib * (1 << 30) // 8)
     x = torch.ones(n, dtype=torch.float64, device="cuda")
     y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
     for _ in range(reps):
         y.copy_(x)
+    e1.record()
     torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes_read": n * 8, "copy_bytes_written": n * 8, "reps": reps}))
+    s = e0.elapsed_time(e1) / 1e3 / reps
+    print(json.dumps({"copy_bytes_read": n * 8, "copy_bytes_written": n * 8, "reps": reps + 1,
+                      "copy_GBps_read_plus_written": round(2 * n * 8 / s / 1e9, 1)}))
 
 
 def main():

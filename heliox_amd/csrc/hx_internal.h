@@ -99,6 +99,8 @@ struct StepArgs {
     double* rhs;
     const double* area;
     const double* cm;             // capacitance, added to d by the current pass
+    int cm_uniform;               // cm holds cm_value on every node: read as that value
+    double cm_value;
     double cfac;                  // 1e-3 * cj (capac.cpp:68-80)
     MechDev m[M_COUNT];
     unsigned dense_mask;          // mechanisms processed by the fused node kernel

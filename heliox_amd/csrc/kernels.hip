@@ -264,7 +264,7 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     if (!A.do_current) return;
     // the capacitance term of the diagonal (capac.cpp:68-80) is added here,
     // ahead of the membrane conductances, so the solve reads one diagonal
-    double rhs = 0.0, d = live ? A.cfac * A.cm[i] : 0.0, g, cur;
+    double rhs = 0.0, d = live ? A.cfac * (A.cm_uniform ? A.cm_value : A.cm[i]) : 0.0, g, cur;
     double prhs = 0.0, pd = 0.0;
     if (A.fold_mask & (1u << M_EXPSYN)) fold_point<M_EXPSYN>(A, i, live, v, s_first, s_last, prhs, pd);
     if (A.fold_mask & (1u << M_EXP2SYN)) fold_point<M_EXP2SYN>(A, i, live, v, s_first, s_last, prhs, pd);

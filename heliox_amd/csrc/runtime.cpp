@@ -292,6 +292,8 @@ struct hx_sim {
     int event_cap_request = 0;
     int fusion_allowed = 1;
     bool uniform_on = true;              // parameter columns with one value read as scalars
+    bool cm_uniform = false;             // cm holds one value on every node (as the columns above)
+    double cm_value = 0.0;
     bool loaded = false;
 
     // layout
@@ -921,6 +923,9 @@ void hx_sim::upload() {
     d_sa = dupload(owned, perm_nodes(solve_a));
     d_sb = dupload(owned, perm_nodes(solve_b));
     d_cm = dupload(owned, perm_nodes(cm));
+    cm_uniform = nnode > 0;
+    for (int i = 1; i < nnode && cm_uniform; ++i) cm_uniform = std::memcmp(&cm[i], &cm[0], sizeof(double)) == 0;
+    cm_value = nnode > 0 ? cm[0] : 0.0;
     d_area = dupload(owned, perm_nodes(area));
     d_unit_node_begin = dupload(owned, unit_node_begin);
     d_unit_desc_begin = dupload(owned, unit_desc_begin);
@@ -1671,6 +1676,7 @@ Ref hx_sim::resolve(const std::string& mn, const std::string& var, int idx) {
     if (mn == "capacitance") {
         if (idx < 0 || idx >= nnode || var != "cm") return r;
         r.dev = d_cm + node_perm[idx];
+        cm_uniform = false;              // a handle may write it: read per node from now on
         return r;
     }
     int id = mech_id(mn);
@@ -1772,6 +1778,8 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
     A.rhs = d_rhs;
     A.area = d_area;
     A.cm = d_cm;
+    A.cm_uniform = (cm_uniform && uniform_on) ? 1 : 0;
+    A.cm_value = cm_value;
     A.cfac = 0.001 * (1.0 / dt);
     for (int id = 0; id < M_COUNT; ++id) {
         A.m[id] = mech[id].dev;
@@ -3918,6 +3926,10 @@ long long hx_get_info(hx_sim* sim, const char* key) {
             const int nb = __builtin_popcount(sim->mech[id].dev.umask);
             cols += nb;
             bytes += 8LL * nb * sim->mech[id].n;
+        }
+        if (sim->cm_uniform && sim->uniform_on) {
+            cols += 1;
+            bytes += 8LL * sim->nnode;
         }
         return k == "uniform_columns" ? cols : bytes;
     }

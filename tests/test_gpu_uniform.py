@@ -40,10 +40,10 @@ def test_scalar_reads_give_the_same_bits(gpu_lib):
     # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2
     # decay/depth/minCai (gamma made per instance here), and the erev of na and k (style 0:
     # no kernel writes it); ca's conco is rewritten at finitialize (style 04) and stays per
-    # instance
-    assert a.info("uniform_columns") == 12
+    # instance; and the capacitance cm, one value on every node
+    assert a.info("uniform_columns") == 13
     assert b.info("uniform_columns") == 0
-    assert a.info("uniform_bytes") == 12 * 8 * spec.nnode
+    assert a.info("uniform_bytes") == 13 * 8 * spec.nnode
     assert np.array_equal(a.traces(), b.traces())
 
 
@@ -57,7 +57,7 @@ def test_uniform_calcium_constants_agree_to_rounding(gpu_lib):
     print("case uniform CaDynamics_E2 constants", flush=True)
     a = run(spec, 5.0, True, mons)
     b = run(spec, 5.0, False, mons)
-    assert a.info("uniform_columns") == 13
+    assert a.info("uniform_columns") == 14
     ta, tb = a.traces(), b.traces()
     assert np.max(np.abs(ta[:2] - tb[:2])) < 1e-9
     assert np.max(np.abs(ta[2:] - tb[2:]) / np.abs(tb[2:])) < 1e-12
@@ -81,6 +81,8 @@ def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
         assert g.info("uniform_columns") == before - 1
         assert g.set_variable_value(65.0, "na_ion", "erev", na_node) == 0     # ions: by node
         assert g.info("uniform_columns") == before - 2
+        assert g.set_variable_value(1.5, "capacitance", "cm", 100) == 0       # a node array
+        assert g.info("uniform_columns") == before - 3
 
     g = run(spec, 40.0, True, mons, edit)
     ref = dataclasses.replace(spec, mechs=dict(spec.mechs))
@@ -92,6 +94,8 @@ def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
     ena = ref.mechs["na_ion"].params["erev"].copy()
     ena[k_na] = 65.0
     ref.mechs["na_ion"].params["erev"] = ena
+    ref.cm = spec.cm.copy()
+    ref.cm[100] = 1.5
     o = oracle.OracleSim(ref, monitors=mons)
     o.finitialize(-65.0)
     o.run(40.0)
