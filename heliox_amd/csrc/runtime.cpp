@@ -359,6 +359,8 @@ struct hx_sim {
     int* d_spk_count = nullptr;
     int* const* d_ring_overflow = nullptr;   // each group's ring overflow flag
     int* h_status = nullptr;                 // pinned: StatusArgs::out
+    double* h_mon = nullptr;                 // pinned: the monitor samples of a call
+    size_t h_mon_cap = 0;                    // doubles
     int spk_cap = 0;
     bool inputs_dirty = true;
     // Cell groups.  Cells are split into contiguous groups, each with its own
@@ -553,6 +555,7 @@ struct hx_sim {
             for (auto e : tm.pool) (void)hipEventDestroy(e);
         for (void* p : owned) (void)hipFree(p);
         if (h_status) (void)hipHostFree(h_status);
+        if (h_mon) (void)hipHostFree(h_mon);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -1631,7 +1634,9 @@ void hx_sim::ensure_ttab(int kneed) {
     const int margin = static_cast<int>(std::ceil(max_delay / dt)) + 8;
     const int want = kneed + margin;
     if (static_cast<int>(ttab.size()) < want + 1) {
-        extend_step_times(ttab, want + 1, dt);
+        // grown geometrically, so most calls find their steps in the table already
+        const int have = static_cast<int>(ttab.size());
+        extend_step_times(ttab, std::max(want + 1, std::max(2 * have, 1024)), dt);
     }
     if (ttab_cap < static_cast<int>(ttab.size())) {
         ttab_cap = static_cast<int>(ttab.size()) * 2;
@@ -2438,6 +2443,17 @@ void hx_sim::sync_outputs() {
     // one kernel gathers the flags and the spike count into pinned host memory, so the
     // host reads them after the synchronisation without a copy each
     if (!h_status) HXC(hipHostMalloc(reinterpret_cast<void**>(&h_status), 4 * sizeof(int), hipHostMallocDefault));
+    // the call's monitor samples travel behind it on the stream, into pinned memory
+    const size_t nmon = mon_ref.empty() ? 0 : static_cast<size_t>(mon_buf_fill) * mon_ref.size();
+    if (nmon > 0) {
+        if (h_mon_cap < nmon) {
+            if (h_mon) HXC(hipHostFree(h_mon));
+            h_mon = nullptr;
+            h_mon_cap = std::max(nmon, 2 * h_mon_cap);
+            HXC(hipHostMalloc(reinterpret_cast<void**>(&h_mon), sizeof(double) * h_mon_cap, hipHostMallocDefault));
+        }
+        HXC(hipMemcpyAsync(h_mon, d_mon_buf, sizeof(double) * nmon, hipMemcpyDeviceToHost, stream));
+    }
     StatusArgs sa{d_ring_overflow, static_cast<int>(groups.size()), nsa.n > 0 ? nsa.error : nullptr, d_spk_count,
                   h_status};
     launch_status(sa, stream);
@@ -2475,12 +2491,10 @@ void hx_sim::sync_outputs() {
             spk_by_gid[e.second].push_back(e.first);
         }
     }
-    if (!mon_ref.empty() && mon_buf_fill > 0) {
+    if (nmon > 0) {
         const size_t nm = mon_ref.size();
-        std::vector<double> buf(static_cast<size_t>(mon_buf_fill) * nm);
-        HXC(hipMemcpy(buf.data(), d_mon_buf, sizeof(double) * buf.size(), hipMemcpyDeviceToHost));
         for (long long s = 0; s < mon_buf_fill; ++s)
-            for (size_t i = 0; i < nm; ++i) mon_data[i].push_back(buf[s * nm + mon_col[i]]);
+            for (size_t i = 0; i < nm; ++i) mon_data[i].push_back(h_mon[s * nm + mon_col[i]]);
         mon_buf_fill = 0;
     }
     if (h5_on) h5_append();
