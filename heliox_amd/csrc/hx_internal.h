@@ -74,6 +74,10 @@ struct MechDev {
 // Global constants of the hot-path mechanisms, computed once on the host
 // with the same expressions the reference evaluates per call.
 constexpr double kFaradayCaDyn = 96485.3321233100184;   // CaDynamics_E2.cu:109
+// Default concentrations of na, k and ca (mM) that INITIAL sets where an ion's style has
+// 04 (eion.cuh:183-197)
+constexpr double kIonConciInit[3] = {10.0, 140.0, 5.e-5};
+constexpr double kIonConcoInit[3] = {140.0, 4.0, 2.0};
 
 struct MechConsts {
     double hh_q10;                // pow(3, (celsius - 6.3) / 10)            hh_templated.cu:87

@@ -476,8 +476,9 @@ __global__ void __launch_bounds__(kBlock) k_init(StepArgs A) {
     if (j >= m.n) return;
     if (MECH == M_NA_ION || MECH == M_K_ION || MECH == M_CA_ION) {
         const double z = MECH == M_CA_ION ? 2.0 : 1.0;
-        const double ci0 = MECH == M_NA_ION ? 10.0 : (MECH == M_K_ION ? 140.0 : 5.e-5);
-        const double co0 = MECH == M_NA_ION ? 140.0 : (MECH == M_K_ION ? 4.0 : 2.0);
+        const int x = MECH == M_NA_ION ? 0 : (MECH == M_K_ION ? 1 : 2);
+        const double ci0 = kIonConciInit[x];
+        const double co0 = kIonConcoInit[x];
         int it = m.iontype[j];
         if (it & 04) { m.col(ION_CONCI)[j] = ci0; m.col(ION_CONCO)[j] = co0; }
         if (it & 040) m.col(ION_EREV)[j] = nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, A.c.ktf);

@@ -1013,13 +1013,20 @@ void hx_sim::upload() {
             int any = 0;
             for (int t : m.iontype) any |= t;
             const int cols[2] = {ION_EREV, ION_CONCO};
-            const bool ok[2] = {!(any & (040 | 0100)), (any & 0100) && !(any & 04)};
+            const bool ok[2] = {!(any & (040 | 0100)), (any & 0100) != 0};
+            // conco as the steps read it: finitialize sets it to the ion's default outside
+            // concentration where the style has 04 (k_init), and nothing writes it after that
+            const int x = id == M_NA_ION ? 0 : id == M_K_ION ? 1 : 2;
+            std::vector<double> after_init(m.col[ION_CONCO]);
+            for (int j = 0; j < m.n; ++j)
+                if (m.iontype[j] & 04) after_init[j] = kIonConcoInit[x];
             for (int k = 0; k < 2; ++k) {
                 if (!ok[k]) continue;
                 const int c = cols[k];
-                const double x0 = m.col[c][0];
+                const std::vector<double>& col = c == ION_CONCO ? after_init : m.col[c];
+                const double x0 = col[0];
                 bool same = true;
-                for (int j = 1; j < m.n && same; ++j) same = std::memcmp(&m.col[c][j], &x0, sizeof(double)) == 0;
+                for (int j = 1; j < m.n && same; ++j) same = std::memcmp(&col[j], &x0, sizeof(double)) == 0;
                 if (same) {
                     d.umask |= 1u << c;
                     uval_host[static_cast<size_t>(id) * kUniformCols + c] = x0;

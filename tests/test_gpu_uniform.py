@@ -39,11 +39,11 @@ def test_scalar_reads_give_the_same_bits(gpu_lib):
     b = run(spec, 5.0, False, mons)
     # config 3: pas g/e, hh gl/el, hd_la vhalfl/tau, Ca_HVA gbar, CaDynamics_E2
     # decay/depth/minCai (gamma made per instance here), and the erev of na and k (style 0:
-    # no kernel writes it); ca's conco is rewritten at finitialize (style 04) and stays per
-    # instance; and the capacitance cm, one value on every node
-    assert a.info("uniform_columns") == 13
+    # no kernel writes it); ca's conco, which finitialize sets to 2 mM everywhere (style 04)
+    # and nothing writes after that; and the capacitance cm, one value on every node
+    assert a.info("uniform_columns") == 14
     assert b.info("uniform_columns") == 0
-    assert a.info("uniform_bytes") == 13 * 8 * spec.nnode
+    assert a.info("uniform_bytes") == 14 * 8 * spec.nnode
     assert np.array_equal(a.traces(), b.traces())
 
 
@@ -57,7 +57,7 @@ def test_uniform_calcium_constants_agree_to_rounding(gpu_lib):
     print("case uniform CaDynamics_E2 constants", flush=True)
     a = run(spec, 5.0, True, mons)
     b = run(spec, 5.0, False, mons)
-    assert a.info("uniform_columns") == 14
+    assert a.info("uniform_columns") == 15
     ta, tb = a.traces(), b.traces()
     assert np.max(np.abs(ta[:2] - tb[:2])) < 1e-9
     assert np.max(np.abs(ta[2:] - tb[2:]) / np.abs(tb[2:])) < 1e-12
@@ -106,3 +106,32 @@ def test_handle_write_returns_the_column_to_instance_reads(gpu_lib):
     u = run(spec, 40.0, True, mons)
     assert np.max(np.abs(u.traces()[3] - g.traces()[3])) > 1e-3
     assert n_pas > 100
+
+
+def test_conco_written_after_finitialize_takes_effect(gpu_lib):
+    """ca_ion's conco is one value after finitialize (style 04 sets it) and read as that
+    value; a write through a handle after finitialize returns it to per-instance reads,
+    and the changed Nernst potential shows in the trace as in the oracle's."""
+    spec = build_config(3, 2, 5.0)
+    node = spec.nnode - 7
+    mons = [("global", "v", 0), ("global", "v", node), ("CaDynamics_E2", "cai", node)]
+    print("case conco written after finitialize", flush=True)
+    g = Sim()
+    g.set_cell_groups(1)
+    g.load_model_from_spec(dataclasses.replace(spec, monitors=mons))
+    before = g.info("uniform_columns")
+    g.finitialize(-65.0)
+    assert g.set_variable_value(8.0, "ca_ion", "conco", node) == 0
+    assert g.info("uniform_columns") == before - 1
+    g.run(5.0)
+    o = oracle.OracleSim(spec, monitors=mons)
+    o.finitialize(-65.0)
+    o.set("ca_ion", "conco", node, 8.0)
+    o.run(5.0)
+    err = float(np.max(np.abs(o.traces()[:2] - g.traces()[:2])))
+    print(f"  max |dv| vs oracle {err:.3e}", flush=True)
+    assert err < V_TOL
+    assert np.max(np.abs(o.traces()[2] - g.traces()[2]) / o.traces()[2]) < 1e-9
+    # the unchanged model differs at that node (ica depends on eca)
+    u = run(spec, 5.0, True, mons)
+    assert np.max(np.abs(u.traces()[1] - g.traces()[1])) > 1e-9
