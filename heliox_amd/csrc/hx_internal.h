@@ -440,6 +440,15 @@ void launch_gap(const double* v, const int* src_node, double* vgap_col, const in
                 hipStream_t s);
 void launch_clear_ints(int* p, long long n, hipStream_t s);
 void launch_status(const StatusArgs& a, hipStream_t s);
+// Up to kTapeSegs device-to-device copies in one launch (a step's tape row).
+constexpr int kTapeSegs = 8;
+struct TapeCopy {
+    const double* src[kTapeSegs];
+    double* dst[kTapeSegs];
+    long long n[kTapeSegs];
+    int nseg;
+};
+void launch_tape(const TapeCopy& t, hipStream_t s);
 void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t s);
 
 }  // namespace hx

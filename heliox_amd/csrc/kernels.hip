@@ -1320,6 +1320,13 @@ __global__ void k_status(StatusArgs a) {
     a.out[2] = *a.spk_count;
 }
 
+__global__ void __launch_bounds__(kBlock) k_tape(TapeCopy T) {
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (int s = 0; s < T.nseg; ++s)
+        for (long long j = i; j < T.n[s]; j += stride) T.dst[s][j] = T.src[s][j];
+}
+
 __global__ void k_clear_ints(int* p, long long n) {
     const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0;
@@ -1449,5 +1456,13 @@ void launch_clear_ints(int* p, long long n, hipStream_t s) {
 }
 
 void launch_status(const StatusArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_status, dim3(1), dim3(1), 0, s, a); }
+
+void launch_tape(const TapeCopy& t, hipStream_t s) {
+    long long most = 0;
+    for (int k = 0; k < t.nseg; ++k) most = std::max(most, t.n[k]);
+    if (most <= 0) return;
+    const long long blocks = std::min<long long>((most + kBlock - 1) / kBlock, 4096);
+    hipLaunchKernelGGL(k_tape, dim3(static_cast<unsigned>(blocks)), dim3(kBlock), 0, s, t);
+}
 
 }  // namespace hx

@@ -2106,38 +2106,41 @@ void hx_sim::tape_record() {
         throw std::runtime_error("adjoint tape full (" + std::to_string(tape_cap) + " steps): call hx_tape_begin "
                                  "with more steps");
     const size_t n = static_cast<size_t>(tape_n);
-    HXC(hipMemcpyAsync(d_tape_v + n * nnode, d_v, sizeof(double) * nnode, hipMemcpyDeviceToDevice, stream));
+    // the step's row: one launch copies every segment
+    TapeCopy T{};
+    auto seg = [&](const double* src, double* dst, long long cnt) {
+        T.src[T.nseg] = src;
+        T.dst[T.nseg] = dst;
+        T.n[T.nseg] = cnt;
+        ++T.nseg;
+    };
+    seg(d_v, d_tape_v + n * nnode, nnode);
     if (mech[M_HH].present && mech[M_HH].n > 0) {
         const MechDev& h = mech[M_HH].dev;   // columns m, h, n are consecutive
-        HXC(hipMemcpyAsync(d_tape_x + n * 3 * h.stride, h.col(HH_M), sizeof(double) * 3 * h.stride,
-                           hipMemcpyDeviceToDevice, stream));
+        seg(h.col(HH_M), d_tape_x + n * 3 * h.stride, 3 * h.stride);
     }
     if (mech[M_EXPSYN].present && mech[M_EXPSYN].n > 0) {
         const MechDev& e = mech[M_EXPSYN].dev;
-        HXC(hipMemcpyAsync(d_tape_g + n * e.n, e.col(ES_G), sizeof(double) * e.n, hipMemcpyDeviceToDevice,
-                           stream));
+        seg(e.col(ES_G), d_tape_g + n * e.n, e.n);
     }
     if (d_tape_c) {            // Ca_HVA m, h are consecutive columns
         const MechDev& c = mech[M_CAHVA].dev;
-        HXC(hipMemcpyAsync(d_tape_c + n * 2 * c.stride, c.col(CH_M), sizeof(double) * 2 * c.stride,
-                           hipMemcpyDeviceToDevice, stream));
+        seg(c.col(CH_M), d_tape_c + n * 2 * c.stride, 2 * c.stride);
     }
     if (d_tape_l) {
         const MechDev& h = mech[M_HDLA].dev;
-        HXC(hipMemcpyAsync(d_tape_l + n * h.n, h.col(HD_L), sizeof(double) * h.n, hipMemcpyDeviceToDevice, stream));
+        seg(h.col(HD_L), d_tape_l + n * h.n, h.n);
     }
     if (d_tape_cai) {
         const MechDev& ca = mech[M_CA_ION].dev;
-        HXC(hipMemcpyAsync(d_tape_cai + n * ca.n, ca.col(ION_CONCI), sizeof(double) * ca.n,
-                           hipMemcpyDeviceToDevice, stream));
+        seg(ca.col(ION_CONCI), d_tape_cai + n * ca.n, ca.n);
     }
     if (d_tape_ab) {
         const MechDev& e = mech[M_EXP2SYN].dev;
-        HXC(hipMemcpyAsync(d_tape_ab + n * 2 * e.n, e.col(E2_A), sizeof(double) * e.n, hipMemcpyDeviceToDevice,
-                           stream));
-        HXC(hipMemcpyAsync(d_tape_ab + (n * 2 + 1) * e.n, e.col(E2_B), sizeof(double) * e.n,
-                           hipMemcpyDeviceToDevice, stream));
+        seg(e.col(E2_A), d_tape_ab + n * 2 * e.n, e.n);
+        seg(e.col(E2_B), d_tape_ab + (n * 2 + 1) * e.n, e.n);
     }
+    launch_tape(T, stream);
     ++tape_n;
 }
 
