@@ -135,3 +135,42 @@ def test_conco_written_after_finitialize_takes_effect(gpu_lib):
     # the unchanged model differs at that node (ica depends on eca)
     u = run(spec, 5.0, True, mons)
     assert np.max(np.abs(u.traces()[1] - g.traces()[1])) > 1e-9
+
+
+def test_conco_with_mixed_styles(gpu_lib):
+    """conco counts as one value only if it is one value as the steps read it: instances
+    whose style lacks 04 keep their loaded conco.  With one such instance at 3 mM the
+    column is read per instance (and matches the oracle); with that instance at the init
+    default (2 mM) it is one value again.  One CaDynamics_E2 gamma is moved by 1e-7 so its
+    per-model constants stay off and scalar and per-instance reads give the same bits."""
+    spec = build_config(3, 2, 4.0)
+    spec.mechs["CaDynamics_E2"].params["gamma"][0] *= 1.0000001
+    node = 11
+    mons = [("global", "v", 0), ("global", "v", node), ("CaDynamics_E2", "cai", node)]
+
+    def variant(conco):
+        ca = spec.mechs["ca_ion"]
+        it = ca.iontype.copy()
+        it[node] = 0o40 | 0o100                    # no 04: finitialize leaves conco as loaded
+        params = dict(ca.params)
+        co = params["conco"].copy()
+        co[node] = conco
+        params["conco"] = co
+        mechs = dict(spec.mechs)
+        mechs["ca_ion"] = dataclasses.replace(ca, params=params, iontype=it)
+        return dataclasses.replace(spec, mechs=mechs)
+
+    print("case conco with mixed styles", flush=True)
+    mixed = variant(3.0)
+    a = run(mixed, 4.0, True, mons)
+    b = run(mixed, 4.0, False, mons)
+    same = run(variant(2.0), 4.0, True, mons)
+    ref = run(spec, 4.0, True, mons)
+    assert a.info("uniform_columns") == ref.info("uniform_columns") - 1
+    assert same.info("uniform_columns") == ref.info("uniform_columns")
+    assert np.array_equal(a.traces(), b.traces())
+    o = oracle.OracleSim(mixed, monitors=mons)
+    o.finitialize(-65.0)
+    o.run(4.0)
+    assert float(np.max(np.abs(o.traces()[:2] - a.traces()[:2]))) < V_TOL
+    assert np.max(np.abs(o.traces()[2] - a.traces()[2]) / o.traces()[2]) < 1e-9
