@@ -45,12 +45,13 @@ __device__ __forceinline__ int ion_of(const MechDev& m, int which, int j) {
     return m.ion[which] ? m.ion[which][j] : j;
 }
 
-// hh gates: lambda_x <- alpha lambda_x, lambda_v[node] += dx^{n+1}/dv^{n+1} . lambda_x
-__global__ void k_adj_hh_state(AdjStep A) {
-    const MechDev& m = A.m[M_HH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
+// Per-instance bodies of the density mechanisms.  Each takes the instance j and
+// its node, updates the mechanism's own adjoints and returns what it adds to the
+// node's lambda_v or d, so the per-mechanism kernels and the node-parallel kernels
+// below add the same terms in the same order (the same bits either way).
+
+// hh gates: lambda_x <- alpha lambda_x; returns dx^{n+1}/dv^{n+1} . lambda_x
+__device__ __forceinline__ double hh_state_at(const AdjStep& A, int j, int node) {
     const Dual v1{A.v1[node], 1.0};
     Dual minf, mtau, hinf, htau, ninf, ntau;
     hh_rates(v1, A.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
@@ -64,7 +65,192 @@ __global__ void k_adj_hh_state(AdjStep A) {
         dv += xn[g].d * lx;
         A.lam_x[g * A.xstride + j] = exp(A.dt * (-1.0 / tau[g])) * lx;   // d cnexp / d x
     }
-    A.lam_v[node] += dv;
+    return dv;
+}
+
+// Ca_HVA gates (cnexp at v^{n+1}): lambda_x <- exp(-dt/tau) lambda_x; returns dx/dv lambda_x
+__device__ __forceinline__ double cahva_state_at(const AdjStep& A, int j, int node) {
+    const Dual v1{A.v1[node], 1.0};
+    Dual mInf, mTau, hInf, hTau;
+    cahva_rates_t(v1, mInf, mTau, hInf, hTau);
+    const Dual mn = cnexp_t(A.c0[j], mInf, mTau, A.dt);
+    const Dual hn = cnexp_t(A.c0[A.cstride + j], hInf, hTau, A.dt);
+    const double lm = A.lam_c[j], lh = A.lam_c[A.cstride + j];
+    A.lam_c[j] = exp(-A.dt / mTau.v) * lm;
+    A.lam_c[A.cstride + j] = exp(-A.dt / hTau.v) * lh;
+    return mn.d * lm + hn.d * lh;
+}
+
+// hd_la gate
+__device__ __forceinline__ double hdla_state_at(const AdjStep& A, int j, int node) {
+    const MechDev& m = A.m[M_HDLA];
+    const Dual v1{A.v1[node], 1.0};
+    Dual linf, taul;
+    hdla_rate_t(v1, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
+    const Dual ln = cnexp_t(A.l0[j], linf, taul, A.dt);
+    const double ll = A.lam_l[j];
+    A.lam_l[j] = exp(-A.dt / taul.v) * ll;
+    return ln.d * ll;
+}
+
+// CaDynamics_E2: lambda_ica^n from lambda_cai^{n+1}, then lambda_cai^n <- e lambda_cai^{n+1}
+__device__ __forceinline__ void cadyn_at(const AdjStep& A, int j) {
+    const MechDev& m = A.m[M_CADYN];
+    const int ci = ion_of(m, 2, j);
+    const double decay = m.col(CD_DECAY)[j];
+    const double e = exp(A.dt * (-1.0 / decay));
+    const double lc = A.lam_cai[ci];
+    A.lam_ica[ci] = (1.0 - e) * decay * (-(10000.0) * m.col(CD_GAMMA)[j] / (2.0 * kFaradayCaDyn * m.col(CD_DEPTH)[j])) * lc;
+    A.lam_cai[ci] = e * lc;
+}
+
+// membrane conductances G at step n
+__device__ __forceinline__ double cond_pas_at(const AdjStep& A, int j) { return A.m[M_PAS].col(PAS_G)[j]; }
+
+__device__ __forceinline__ double cond_hh_at(const AdjStep& A, int j) {
+    const MechDev& m = A.m[M_HH];
+    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
+    return m.col(HH_GNABAR)[j] * mm * mm * mm * hh + m.col(HH_GKBAR)[j] * nn * nn * nn * nn + m.col(HH_GL)[j];
+}
+
+__device__ __forceinline__ double cond_cahva_at(const AdjStep& A, int j) {
+    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
+    return A.m[M_CAHVA].col(CH_GBAR)[j] * mm * mm * hh;
+}
+
+__device__ __forceinline__ double cond_hdla_at(const AdjStep& A, int j) {
+    return A.m[M_HDLA].col(HD_GHDBAR)[j] * A.l0[j];
+}
+
+__device__ __forceinline__ void hh_param_at(const AdjStep& A, int j, int node) {
+    const MechDev& m = A.m[M_HH];
+    const double mu = A.mu[node], v1 = A.v1[node];
+    const double ena = A.m[M_NA_ION].col(ION_EREV)[ion_of(m, 0, j)];
+    const double ek = A.m[M_K_ION].col(ION_EREV)[ion_of(m, 1, j)];
+    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
+    const double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
+    A.lam_x[j] -= mu * 3.0 * gnabar * mm * mm * hh * (v1 - ena);
+    A.lam_x[A.xstride + j] -= mu * gnabar * mm * mm * mm * (v1 - ena);
+    A.lam_x[2 * A.xstride + j] -= mu * 4.0 * gkbar * nn * nn * nn * (v1 - ek);
+    A.grad_gnabar[j] -= mu * mm * mm * mm * hh * (v1 - ena);
+    A.grad_gkbar[j] -= mu * nn * nn * nn * nn * (v1 - ek);
+}
+
+__device__ __forceinline__ void pas_param_at(const AdjStep& A, int j, int node) {
+    A.grad_gpas[j] -= A.mu[node] * (A.v1[node] - A.m[M_PAS].col(PAS_E)[j]);
+}
+
+// eca of step n at ca_ion instance ci and d eca / d cai (0 where eca is fixed)
+__device__ __forceinline__ double eca_of(const AdjStep& A, int ci, double& deca) {
+    const MechDev& ca = A.m[M_CA_ION];
+    if (ca.iontype[ci] & 0100) {
+        const double c = A.cai0[ci];
+        deca = -A.c.ktf / 2.0 / c;
+        return nernst(c, ca.col(ION_CONCO)[ci], 2.0, A.c.ktf);
+    }
+    deca = 0.0;
+    return ca.col(ION_EREV)[ci];
+}
+
+// Ca_HVA: through the solve (at v^{n+1}) and through the ica CaDynamics_E2 read (at v^n);
+// lnew is the node's lambda_v^n
+__device__ __forceinline__ void cahva_param_at(const AdjStep& A, int j, int node, double* lnew) {
+    const MechDev& m = A.m[M_CAHVA];
+    const int ci = ion_of(m, 2, j);
+    double deca;
+    const double eca = eca_of(A, ci, deca);
+    const double gbar = m.col(CH_GBAR)[j];
+    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
+    const double g = gbar * mm * mm * hh;
+    // solve: dL/dq += -mu dG/dq (v^{n+1} - eca) + mu G deca/dq
+    const double mu = A.mu[node];
+    const double d1 = A.v1[node] - eca;
+    double lm = -mu * 2.0 * gbar * mm * hh * d1;
+    double lh = -mu * gbar * mm * mm * d1;
+    double gg = -mu * mm * mm * hh * d1;
+    double lcai = mu * g * deca;
+    // ica^n = G (v^n - eca): its adjoint from CaDynamics_E2
+    const double li = A.lam_ica ? A.lam_ica[ci] : 0.0;
+    if (li != 0.0) {
+        const double d0 = A.v0[node] - eca;
+        *lnew += g * li;
+        lm += 2.0 * gbar * mm * hh * d0 * li;
+        lh += gbar * mm * mm * d0 * li;
+        gg += mm * mm * hh * d0 * li;
+        lcai -= g * deca * li;
+    }
+    A.lam_c[j] += lm;
+    A.lam_c[A.cstride + j] += lh;
+    A.grad_cgbar[j] += gg;
+    if (A.lam_cai) A.lam_cai[ci] += lcai;
+}
+
+__device__ __forceinline__ void hdla_param_at(const AdjStep& A, int j, int node) {
+    const MechDev& m = A.m[M_HDLA];
+    const double mu = A.mu[node], d1 = A.v1[node] - A.c.hd_ehd;
+    A.lam_l[j] -= mu * m.col(HD_GHDBAR)[j] * d1;
+    A.grad_ghdbar[j] -= mu * A.l0[j] * d1;
+}
+
+// ---- per-mechanism kernels (instance-parallel; one density instance per node) ----
+#define HX_ADJ_INSTANCE(MECH)                                  \
+    const MechDev& m = A.m[MECH];                              \
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;       \
+    if (j >= m.n) return;                                      \
+    const int node = m.node[j];                                \
+    (void)node
+
+__global__ void k_adj_hh_state(AdjStep A) { HX_ADJ_INSTANCE(M_HH); A.lam_v[node] += hh_state_at(A, j, node); }
+__global__ void k_adj_cahva_state(AdjStep A) { HX_ADJ_INSTANCE(M_CAHVA); A.lam_v[node] += cahva_state_at(A, j, node); }
+__global__ void k_adj_hdla_state(AdjStep A) { HX_ADJ_INSTANCE(M_HDLA); A.lam_v[node] += hdla_state_at(A, j, node); }
+__global__ void k_adj_cadyn(AdjStep A) { HX_ADJ_INSTANCE(M_CADYN); cadyn_at(A, j); }
+__global__ void k_adj_cond_pas(AdjStep A) { HX_ADJ_INSTANCE(M_PAS); A.dT[node] += cond_pas_at(A, j); }
+__global__ void k_adj_cond_hh(AdjStep A) { HX_ADJ_INSTANCE(M_HH); A.dT[node] += cond_hh_at(A, j); }
+__global__ void k_adj_cond_cahva(AdjStep A) { HX_ADJ_INSTANCE(M_CAHVA); A.dT[node] += cond_cahva_at(A, j); }
+__global__ void k_adj_cond_hdla(AdjStep A) { HX_ADJ_INSTANCE(M_HDLA); A.dT[node] += cond_hdla_at(A, j); }
+__global__ void k_adj_hh_param(AdjStep A) { HX_ADJ_INSTANCE(M_HH); hh_param_at(A, j, node); }
+__global__ void k_adj_pas_param(AdjStep A) { HX_ADJ_INSTANCE(M_PAS); pas_param_at(A, j, node); }
+__global__ void k_adj_cahva_param(AdjStep A) { HX_ADJ_INSTANCE(M_CAHVA); cahva_param_at(A, j, node, A.lam_v_new + node); }
+__global__ void k_adj_hdla_param(AdjStep A) { HX_ADJ_INSTANCE(M_HDLA); hdla_param_at(A, j, node); }
+#undef HX_ADJ_INSTANCE
+
+// ---- node-parallel kernels ----
+// Before the solve: the gate adjoints of the mechanisms in fuse_state (one instance on
+// every node, instance i at node i), then the transposed system d = C + delta + G,
+// rhs = lambda_v, v = 0, with the conductances of the mechanisms in fuse_cond.  The host
+// runs every other mechanism's kernel so that each node's sums keep the order
+// hh, Ca_HVA, hd_la (lambda_v) and pas, hh, Ca_HVA, hd_la (d).
+__global__ void k_adj_before_nodes(AdjStep A) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.N) return;
+    const unsigned fs = A.fuse_state, fc = A.fuse_cond;
+    double lv = A.lam_v[i];
+    if (fs & kAdjHH) lv += hh_state_at(A, i, i);
+    if (fs & kAdjCaHVA) lv += cahva_state_at(A, i, i);
+    if (fs & kAdjHdla) lv += hdla_state_at(A, i, i);
+    if (fs & kAdjCaDyn) cadyn_at(A, i);
+    double d = A.cfac * A.cm[i] + A.delta[i];
+    if (fc & kAdjPas) d += cond_pas_at(A, i);
+    if (fc & kAdjHH) d += cond_hh_at(A, i);
+    if (fc & kAdjCaHVA) d += cond_cahva_at(A, i);
+    if (fc & kAdjHdla) d += cond_hdla_at(A, i);
+    A.dT[i] = d;
+    A.rhsT[i] = lv;
+    A.vT[i] = 0.0;
+}
+
+// After the solve: lambda_v^n = C mu, then the parameter terms of the mechanisms in
+// fuse_param (only Ca_HVA's adds to lambda_v^n, after C mu as in its own kernel).
+__global__ void k_adj_after_nodes(AdjStep A) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= A.N) return;
+    const unsigned fp = A.fuse_param;
+    double lnew = A.cfac * A.cm[i] * A.mu[i];
+    if (fp & kAdjHH) hh_param_at(A, i, i);
+    if (fp & kAdjPas) pas_param_at(A, i, i);
+    if (fp & kAdjCaHVA) cahva_param_at(A, i, i, &lnew);
+    if (fp & kAdjHdla) hdla_param_at(A, i, i);
+    A.lam_v_new[i] = lnew;
 }
 
 // ExpSyn decay: lambda_geff = exp(-dt/tau) lambda_g (in place)
@@ -75,51 +261,6 @@ __global__ void k_adj_syn_state(AdjStep A) {
     A.lam_g[j] = exp(-A.dt / m.col(ES_TAU)[j]) * A.lam_g[j];
 }
 
-// Ca_HVA gates (cnexp at v^{n+1}): lambda_x <- exp(-dt/tau) lambda_x, lambda_v += dx/dv lambda_x
-__global__ void k_adj_cahva_state(AdjStep A) {
-    const MechDev& m = A.m[M_CAHVA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const Dual v1{A.v1[node], 1.0};
-    Dual mInf, mTau, hInf, hTau;
-    cahva_rates_t(v1, mInf, mTau, hInf, hTau);
-    const Dual mn = cnexp_t(A.c0[j], mInf, mTau, A.dt);
-    const Dual hn = cnexp_t(A.c0[A.cstride + j], hInf, hTau, A.dt);
-    const double lm = A.lam_c[j], lh = A.lam_c[A.cstride + j];
-    A.lam_v[node] += mn.d * lm + hn.d * lh;
-    A.lam_c[j] = exp(-A.dt / mTau.v) * lm;
-    A.lam_c[A.cstride + j] = exp(-A.dt / hTau.v) * lh;
-}
-
-// hd_la gate
-__global__ void k_adj_hdla_state(AdjStep A) {
-    const MechDev& m = A.m[M_HDLA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const Dual v1{A.v1[node], 1.0};
-    Dual linf, taul;
-    hdla_rate_t(v1, m.col(HD_VHALFL)[j], m.col(HD_TAU)[j], A.c, linf, taul);
-    const Dual ln = cnexp_t(A.l0[j], linf, taul, A.dt);
-    const double ll = A.lam_l[j];
-    A.lam_v[node] += ln.d * ll;
-    A.lam_l[j] = exp(-A.dt / taul.v) * ll;
-}
-
-// CaDynamics_E2: lambda_ica^n from lambda_cai^{n+1}, then lambda_cai^n <- e lambda_cai^{n+1}
-__global__ void k_adj_cadyn(AdjStep A) {
-    const MechDev& m = A.m[M_CADYN];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int ci = ion_of(m, 2, j);
-    const double decay = m.col(CD_DECAY)[j];
-    const double e = exp(A.dt * (-1.0 / decay));
-    const double lc = A.lam_cai[ci];
-    A.lam_ica[ci] = (1.0 - e) * decay * (-(10000.0) * m.col(CD_GAMMA)[j] / (2.0 * kFaradayCaDyn * m.col(CD_DEPTH)[j])) * lc;
-    A.lam_cai[ci] = e * lc;
-}
-
 // Exp2Syn decay: lambda_{A,B eff} = exp(-dt/tau_{1,2}) lambda_{A,B}
 __global__ void k_adj_syn2_state(AdjStep A) {
     const MechDev& m = A.m[M_EXP2SYN];
@@ -127,47 +268,6 @@ __global__ void k_adj_syn2_state(AdjStep A) {
     if (j >= m.n) return;
     A.lam_ab[j] *= exp(A.dt * (-1.0 / m.col(E2_TAU1)[j]));
     A.lam_ab[m.n + j] *= exp(A.dt * (-1.0 / m.col(E2_TAU2)[j]));
-}
-
-// transposed system: d = C + delta, rhs = lambda_v, v = 0
-__global__ void k_adj_assemble(AdjStep A) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= A.N) return;
-    A.dT[i] = A.cfac * A.cm[i] + A.delta[i];
-    A.rhsT[i] = A.lam_v[i];
-    A.vT[i] = 0.0;
-}
-
-// membrane conductances G at step n (one instance per node for pas and hh)
-__global__ void k_adj_cond_pas(AdjStep A) {
-    const MechDev& m = A.m[M_PAS];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    A.dT[m.node[j]] += m.col(PAS_G)[j];
-}
-
-__global__ void k_adj_cond_hh(AdjStep A) {
-    const MechDev& m = A.m[M_HH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
-    A.dT[m.node[j]] += m.col(HH_GNABAR)[j] * mm * mm * mm * hh + m.col(HH_GKBAR)[j] * nn * nn * nn * nn +
-                       m.col(HH_GL)[j];
-}
-
-__global__ void k_adj_cond_cahva(AdjStep A) {
-    const MechDev& m = A.m[M_CAHVA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
-    A.dT[m.node[j]] += m.col(CH_GBAR)[j] * mm * mm * hh;
-}
-
-__global__ void k_adj_cond_hdla(AdjStep A) {
-    const MechDev& m = A.m[M_HDLA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    A.dT[m.node[j]] += m.col(HD_GHDBAR)[j] * A.l0[j];
 }
 
 // Exp2Syn grouped by node: sum of (B_eff - A_eff) x 1e2/area
@@ -190,95 +290,6 @@ __global__ void k_adj_cond_syn(AdjStep A) {
     double g = 0.0;
     for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.geff[j];
     A.dT[node] += g * (1.e2 / A.area[node]);
-}
-
-// lambda_v^n = C mu
-__global__ void k_adj_node(AdjStep A) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= A.N) return;
-    A.lam_v_new[i] = A.cfac * A.cm[i] * A.mu[i];
-}
-
-__global__ void k_adj_hh_param(AdjStep A) {
-    const MechDev& m = A.m[M_HH];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const double mu = A.mu[node], v1 = A.v1[node];
-    const double ena = A.m[M_NA_ION].col(ION_EREV)[ion_of(m, 0, j)];
-    const double ek = A.m[M_K_ION].col(ION_EREV)[ion_of(m, 1, j)];
-    const double mm = A.x0[j], hh = A.x0[A.xstride + j], nn = A.x0[2 * A.xstride + j];
-    const double gnabar = m.col(HH_GNABAR)[j], gkbar = m.col(HH_GKBAR)[j];
-    A.lam_x[j] -= mu * 3.0 * gnabar * mm * mm * hh * (v1 - ena);
-    A.lam_x[A.xstride + j] -= mu * gnabar * mm * mm * mm * (v1 - ena);
-    A.lam_x[2 * A.xstride + j] -= mu * 4.0 * gkbar * nn * nn * nn * (v1 - ek);
-    A.grad_gnabar[j] -= mu * mm * mm * mm * hh * (v1 - ena);
-    A.grad_gkbar[j] -= mu * nn * nn * nn * nn * (v1 - ek);
-}
-
-__global__ void k_adj_pas_param(AdjStep A) {
-    const MechDev& m = A.m[M_PAS];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    A.grad_gpas[j] -= A.mu[node] * (A.v1[node] - m.col(PAS_E)[j]);
-}
-
-// eca of step n at ca_ion instance ci and d eca / d cai (0 where eca is fixed)
-__device__ __forceinline__ double eca_of(const AdjStep& A, int ci, double& deca) {
-    const MechDev& ca = A.m[M_CA_ION];
-    if (ca.iontype[ci] & 0100) {
-        const double c = A.cai0[ci];
-        deca = -A.c.ktf / 2.0 / c;
-        return nernst(c, ca.col(ION_CONCO)[ci], 2.0, A.c.ktf);
-    }
-    deca = 0.0;
-    return ca.col(ION_EREV)[ci];
-}
-
-// Ca_HVA: through the solve (at v^{n+1}) and through the ica CaDynamics_E2 read (at v^n)
-__global__ void k_adj_cahva_param(AdjStep A) {
-    const MechDev& m = A.m[M_CAHVA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const int ci = ion_of(m, 2, j);
-    double deca;
-    const double eca = eca_of(A, ci, deca);
-    const double gbar = m.col(CH_GBAR)[j];
-    const double mm = A.c0[j], hh = A.c0[A.cstride + j];
-    const double g = gbar * mm * mm * hh;
-    // solve: dL/dq += -mu dG/dq (v^{n+1} - eca) + mu G deca/dq
-    const double mu = A.mu[node];
-    const double d1 = A.v1[node] - eca;
-    double lm = -mu * 2.0 * gbar * mm * hh * d1;
-    double lh = -mu * gbar * mm * mm * d1;
-    double gg = -mu * mm * mm * hh * d1;
-    double lcai = mu * g * deca;
-    // ica^n = G (v^n - eca): its adjoint from CaDynamics_E2
-    const double li = A.lam_ica ? A.lam_ica[ci] : 0.0;
-    if (li != 0.0) {
-        const double d0 = A.v0[node] - eca;
-        A.lam_v_new[node] += g * li;
-        lm += 2.0 * gbar * mm * hh * d0 * li;
-        lh += gbar * mm * mm * d0 * li;
-        gg += mm * mm * hh * d0 * li;
-        lcai -= g * deca * li;
-    }
-    A.lam_c[j] += lm;
-    A.lam_c[A.cstride + j] += lh;
-    A.grad_cgbar[j] += gg;
-    if (A.lam_cai) A.lam_cai[ci] += lcai;
-}
-
-__global__ void k_adj_hdla_param(AdjStep A) {
-    const MechDev& m = A.m[M_HDLA];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const double mu = A.mu[node], d1 = A.v1[node] - A.c.hd_ehd;
-    A.lam_l[j] -= mu * m.col(HD_GHDBAR)[j] * d1;
-    A.grad_ghdbar[j] -= mu * A.l0[j] * d1;
 }
 
 // Exp2Syn: lambda_{A,eff} += mu (v^{n+1} - e) 1e2/area, lambda_{B,eff} -= the same
@@ -378,19 +389,28 @@ inline dim3 grid_of(long long n, int block = kBlock) {
 // per-node lambda_v and d (one density instance per node; point processes go by
 // node groups) and lambda_cai / lambda_ica (one CaDynamics_E2 per ca_ion instance,
 // written by it before the solve and by Ca_HVA after), so no two launches race.
+// The node-parallel kernels take the mechanisms in a.fuse_*; the rest keep their own
+// kernels, launched where each node's sums keep their order.
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
-    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_state, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cahva_state, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_hdla_state, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_CADYN].n > 0) hipLaunchKernelGGL(k_adj_cadyn, grid_of(a.m[M_CADYN].n), dim3(kBlock), 0, s, a);
+    auto own = [&](int id, unsigned bit, unsigned fused) { return a.m[id].n > 0 && !(fused & bit); };
+    if (own(M_HH, kAdjHH, a.fuse_state)) hipLaunchKernelGGL(k_adj_hh_state, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (own(M_CAHVA, kAdjCaHVA, a.fuse_state))
+        hipLaunchKernelGGL(k_adj_cahva_state, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (own(M_HDLA, kAdjHdla, a.fuse_state))
+        hipLaunchKernelGGL(k_adj_hdla_state, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
+    if (own(M_CADYN, kAdjCaDyn, a.fuse_state))
+        hipLaunchKernelGGL(k_adj_cadyn, grid_of(a.m[M_CADYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_state, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(k_adj_assemble, grid_of(a.N), dim3(kBlock), 0, s, a);
-    if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_cond_hh, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cond_cahva, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_cond_hdla, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_adj_before_nodes, grid_of(a.N), dim3(kBlock), 0, s, a);
+    if (own(M_PAS, kAdjPas, a.fuse_cond))
+        hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
+    if (own(M_HH, kAdjHH, a.fuse_cond)) hipLaunchKernelGGL(k_adj_cond_hh, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (own(M_CAHVA, kAdjCaHVA, a.fuse_cond))
+        hipLaunchKernelGGL(k_adj_cond_cahva, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (own(M_HDLA, kAdjHdla, a.fuse_cond))
+        hipLaunchKernelGGL(k_adj_cond_hdla, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].ngrp > 0)
         hipLaunchKernelGGL(k_adj_cond_syn, grid_of(a.m[M_EXPSYN].ngrp), dim3(kBlock), 0, s, a);
     if (a.m[M_EXP2SYN].ngrp > 0)
@@ -398,11 +418,13 @@ void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
 }
 
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_adj_node, grid_of(a.N), dim3(kBlock), 0, s, a);
-    if (a.m[M_HH].n > 0) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_PAS].n > 0) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_CAHVA].n > 0) hipLaunchKernelGGL(k_adj_cahva_param, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_HDLA].n > 0) hipLaunchKernelGGL(k_adj_hdla_param, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
+    auto own = [&](int id, unsigned bit) { return a.m[id].n > 0 && !(a.fuse_param & bit); };
+    hipLaunchKernelGGL(k_adj_after_nodes, grid_of(a.N), dim3(kBlock), 0, s, a);
+    if (own(M_HH, kAdjHH)) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
+    if (own(M_PAS, kAdjPas)) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
+    if (own(M_CAHVA, kAdjCaHVA))
+        hipLaunchKernelGGL(k_adj_cahva_param, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
+    if (own(M_HDLA, kAdjHdla)) hipLaunchKernelGGL(k_adj_hdla_param, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_param, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);

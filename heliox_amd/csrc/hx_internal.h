@@ -367,7 +367,12 @@ struct AdjStep {
     double* grad_cgbar;           // Ca_HVA gbar
     double* grad_ghdbar;          // hd_la ghdbar
     double* grad_w2;              // Exp2Syn netcon weights
+    // mechanisms the node-parallel adjoint kernels take (kAdj* bits; each has one instance
+    // on every node, instance i at node i): gate adjoints and CaDynamics_E2 (fuse_state),
+    // conductances (fuse_cond), parameter terms (fuse_param)
+    unsigned fuse_state, fuse_cond, fuse_param;
 };
+constexpr unsigned kAdjPas = 1, kAdjHH = 2, kAdjCaHVA = 4, kAdjHdla = 8, kAdjCaDyn = 16;
 
 // Adam over tied parameter groups (optimizer.cpp:351-393): group g covers
 // entries [begin[g], begin[g+1]) of the weight and gradient pointer lists.

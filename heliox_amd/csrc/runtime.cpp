@@ -291,6 +291,7 @@ struct hx_sim {
     std::vector<VecPlayHost> vecplay;
     int event_cap_request = 0;
     int fusion_allowed = 1;
+    unsigned adj_fuse_bits = 0;          // last hx_adjoint's node-parallel masks (state | cond << 8 | param << 16)
     bool uniform_on = true;              // parameter columns with one value read as scalars
     bool cm_uniform = false;             // cm holds one value on every node (as the columns above)
     double cm_value = 0.0;
@@ -3932,6 +3933,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "nround_max") return sim->max_rounds;
     if (k == "dense_mask") return sim->dense_mask;
     if (k == "fused") return sim->fused ? 1 : 0;
+    if (k == "adjoint_fused") return sim->adj_fuse_bits;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());
     if (k == "solve_units") return sim->nunit;
     if (k == "handles") return static_cast<long long>(sim->handles.size());
@@ -4138,6 +4140,33 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.grad_cgbar = sim->d_grad[T_CGBAR];
     A.grad_ghdbar = sim->d_grad[T_GHDBAR];
     A.grad_w2 = sim->d_grad[T_WE2];
+    // The node-parallel kernels take the mechanisms with one instance on every node (the
+    // node kernel's layout): gate adjoints only as the tail of hh, Ca_HVA, hd_la and
+    // conductances only as the head of pas, hh, Ca_HVA, hd_la, so that every node's sums
+    // keep the per-mechanism kernels' order.  hx_set_fusion(0) leaves every mechanism to
+    // its own kernels.
+    if (sim->fusion_allowed) {
+        auto has = [&](int id) { return sim->mech[id].present && sim->mech[id].n > 0; };
+        auto dense = [&](int id) { return has(id) && (sim->dense_mask & (1u << id)) != 0; };
+        const int st_id[3] = {M_HH, M_CAHVA, M_HDLA};
+        const unsigned st_bit[3] = {kAdjHH, kAdjCaHVA, kAdjHdla};
+        for (int k = 2; k >= 0; --k) {
+            if (!has(st_id[k])) continue;
+            if (!dense(st_id[k])) break;
+            A.fuse_state |= st_bit[k];
+        }
+        if (dense(M_CADYN)) A.fuse_state |= kAdjCaDyn;
+        const int cd_id[4] = {M_PAS, M_HH, M_CAHVA, M_HDLA};
+        const unsigned cd_bit[4] = {kAdjPas, kAdjHH, kAdjCaHVA, kAdjHdla};
+        for (int k = 0; k < 4; ++k) {
+            if (!has(cd_id[k])) continue;
+            if (!dense(cd_id[k])) break;
+            A.fuse_cond |= cd_bit[k];
+        }
+        for (int k = 0; k < 4; ++k)
+            if (dense(cd_id[k])) A.fuse_param |= cd_bit[k];
+    }
+    sim->adj_fuse_bits = A.fuse_state | (A.fuse_cond << 8) | (A.fuse_param << 16);
     SolveArgs S{};
     S.nunit = sim->nunit;
     S.unit_node_begin = sim->d_unit_node_begin;

@@ -110,6 +110,24 @@ def test_synaptic_weight_gradients_match_fd(problem):
         assert fd_relative(base, target, "ExpSyn", "weight", np.arange(nc.weight.size) == k) == 0.0
 
 
+def test_node_parallel_kernels_give_the_same_bits(problem):
+    """pas is on every node and hh on the somas only: the backward step's node-parallel
+    kernels take pas's conductance and parameter term, hh keeps its own kernels.  Each
+    mechanism's own kernels (hx_set_fusion(0)) give the same bits on the same tape."""
+    base, target, loss, grads, g = problem
+    assert g.info("adjoint_fused") == (1 << 8 | 1 << 16), hex(g.info("adjoint_fused"))
+    g.set_fusion(False)
+    try:
+        loss2 = g.adjoint(np.arange(base.ncell), target)
+        assert g.info("adjoint_fused") == 0
+        assert loss2 == loss
+        for k, v in grads.items():
+            np.testing.assert_array_equal(g.gradient(*k), v, err_msg=str(k))
+    finally:
+        g.set_fusion(True)
+    assert g.adjoint(np.arange(base.ncell), target) == loss
+
+
 def test_adam_step_on_tied_groups(problem):
     base, _, _, grads, g = problem
     cell = base.cell_of_node()

@@ -92,11 +92,11 @@ def problem(request, gpu_lib):
     assert g.tape_length() == nstep
     loss = g.adjoint(np.array([0]), target)
     grads = {k: g.gradient(*k) for k in TIED + [("Exp2Syn", "weight")]}
-    return base, target, loss, grads
+    return base, target, loss, grads, g
 
 
 def test_loss_matches_oracle(problem):
-    base, target, loss, _ = problem
+    base, target, loss, _, _ = problem
     ref = loss_of(base, target)
     print(f"case config-3 adjoint loss {loss:.12e} oracle {ref:.12e}", flush=True)
     assert abs(loss - ref) <= 1e-9 * abs(ref)
@@ -104,7 +104,7 @@ def test_loss_matches_oracle(problem):
 
 @pytest.mark.parametrize("mech,var", TIED)
 def test_tied_gradients_match_fd(problem, mech, var):
-    base, target, _, grads = problem
+    base, target, _, grads, _ = problem
     vals = base.mechs[mech].params[var]
     mask = np.ones(vals.size, bool)
     adj = float(np.sum(vals * grads[(mech, var)]))     # d/d alpha of param *= (1 + alpha)
@@ -114,7 +114,7 @@ def test_tied_gradients_match_fd(problem, mech, var):
 
 
 def test_exp2syn_weight_gradients_match_fd(problem):
-    base, target, _, grads = problem
+    base, target, _, grads, _ = problem
     nc = base.netcons["Exp2Syn"]
     gw = grads[("Exp2Syn", "weight")]
     infl = np.abs(gw[nc.inst] * nc.weight)
@@ -128,3 +128,23 @@ def test_exp2syn_weight_gradients_match_fd(problem):
     quiet = np.nonzero(infl == 0)[0]
     if quiet.size:
         assert fd_relative(base, target, "Exp2Syn", "weight", np.arange(nc.weight.size) == quiet[0]) == 0.0
+
+
+def test_node_parallel_kernels_give_the_same_bits(problem):
+    """Every mechanism of this model has an instance on every node, so the backward step
+    runs them all in its two node-parallel kernels; each mechanism's own kernels
+    (hx_set_fusion(0)) give the same loss and gradients, bit for bit, on the same tape."""
+    _, target, loss, grads, g = problem
+    every = 0b1111                      # pas, hh, Ca_HVA, hd_la
+    gates = 0b11110                     # hh, Ca_HVA, hd_la and CaDynamics_E2
+    assert g.info("adjoint_fused") == (gates | every << 8 | every << 16), hex(g.info("adjoint_fused"))
+    g.set_fusion(False)
+    try:
+        loss2 = g.adjoint(np.array([0]), target)
+        assert g.info("adjoint_fused") == 0
+        assert loss2 == loss
+        for k, v in grads.items():
+            np.testing.assert_array_equal(g.gradient(*k), v, err_msg=str(k))
+    finally:
+        g.set_fusion(True)
+    assert g.adjoint(np.array([0]), target) == loss
