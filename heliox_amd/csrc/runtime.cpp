@@ -4125,7 +4125,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.dT = sim->d_dT;
     A.rhsT = sim->d_rhsT;
     A.vT = sim->d_vT;
-    A.mu = sim->d_rhsT;
+    A.mu = sim->d_vT;     // the solve's new voltage from v = 0 is x = M^-T lambda
     A.grad_gnabar = sim->d_grad[T_GNABAR];
     A.grad_gkbar = sim->d_grad[T_GKBAR];
     A.grad_gpas = sim->d_grad[T_GPAS];
@@ -4180,7 +4180,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     S.w = sim->d_wT;
     S.a = sim->d_sb;      // M^T: the coefficients trade places
     S.b = sim->d_sa;
-    S.store_dx = 1;       // mu = M^-T lambda is read from rhs
+    S.store_dx = 0;       // D and x are not needed: v starts at 0, so the new v is x
     double* lv = sim->d_lv;
     double* lv2 = sim->d_lv2;
     const size_t row = static_cast<size_t>(N);
