@@ -192,6 +192,50 @@ __device__ __forceinline__ void hdla_param_at(const AdjStep& A, int j, int node)
     A.grad_ghdbar[j] -= mu * A.l0[j] * d1;
 }
 
+// synapse decay adjoints: lambda_geff = exp(-dt/tau) lambda_g (ExpSyn, in place),
+// lambda_{A,B eff} = exp(-dt/tau_{1,2}) lambda_{A,B} (Exp2Syn)
+__device__ __forceinline__ void syn_state_at(const AdjStep& A, int j) {
+    A.lam_g[j] = exp(-A.dt / A.m[M_EXPSYN].col(ES_TAU)[j]) * A.lam_g[j];
+}
+
+__device__ __forceinline__ void syn2_state_at(const AdjStep& A, int j) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    A.lam_ab[j] *= exp(A.dt * (-1.0 / m.col(E2_TAU1)[j]));
+    A.lam_ab[m.n + j] *= exp(A.dt * (-1.0 / m.col(E2_TAU2)[j]));
+}
+
+// conductance of node group q (the synapses on one node): sum of g_eff x 1e2/area (ExpSyn),
+// of (B_eff - A_eff) x 1e2/area (Exp2Syn)
+__device__ __forceinline__ double cond_syn_at(const AdjStep& A, int q, int node) {
+    const MechDev& m = A.m[M_EXPSYN];
+    double g = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.geff[j];
+    return g * (1.e2 / A.area[node]);
+}
+
+__device__ __forceinline__ double cond_syn2_at(const AdjStep& A, int q, int node) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    double g = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.ab0[m.n + j] - A.ab0[j];
+    return g * (1.e2 / A.area[node]);
+}
+
+// lambda_geff += -mu (v^{n+1} - e) 1e2/area
+__device__ __forceinline__ void syn_param_at(const AdjStep& A, int j) {
+    const MechDev& m = A.m[M_EXPSYN];
+    const int node = m.node[j];
+    A.lam_g[j] -= A.mu[node] * (A.v1[node] - m.col(ES_E)[j]) * (1.e2 / A.area[node]);
+}
+
+// Exp2Syn: lambda_{A,eff} += mu (v^{n+1} - e) 1e2/area, lambda_{B,eff} -= the same
+__device__ __forceinline__ void syn2_param_at(const AdjStep& A, int j) {
+    const MechDev& m = A.m[M_EXP2SYN];
+    const int node = m.node[j];
+    const double t = A.mu[node] * (A.v1[node] - m.col(E2_E)[j]) * (1.e2 / A.area[node]);
+    A.lam_ab[j] += t;
+    A.lam_ab[m.n + j] -= t;
+}
+
 // ---- per-mechanism kernels (instance-parallel; one density instance per node) ----
 #define HX_ADJ_INSTANCE(MECH)                                  \
     const MechDev& m = A.m[MECH];                              \
@@ -222,7 +266,14 @@ __global__ void k_adj_hdla_param(AdjStep A) { HX_ADJ_INSTANCE(M_HDLA); hdla_para
 // hh, Ca_HVA, hd_la (lambda_v) and pas, hh, Ca_HVA, hd_la (d).
 __global__ void k_adj_before_nodes(AdjStep A) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= A.N) return;
+    if (i >= A.N) {
+        // with fold_syn, threads N.. take the synapses' decay adjoints (ExpSyn, then Exp2Syn)
+        if (!A.fold_syn) return;
+        const int j = i - A.N, nes = A.m[M_EXPSYN].n;
+        if (j < nes) syn_state_at(A, j);
+        else if (j - nes < A.m[M_EXP2SYN].n) syn2_state_at(A, j - nes);
+        return;
+    }
     const unsigned fs = A.fuse_state, fc = A.fuse_cond;
     double lv = A.lam_v[i];
     if (fs & kAdjHH) lv += hh_state_at(A, i, i);
@@ -234,6 +285,16 @@ __global__ void k_adj_before_nodes(AdjStep A) {
     if (fc & kAdjHH) d += cond_hh_at(A, i);
     if (fc & kAdjCaHVA) d += cond_cahva_at(A, i);
     if (fc & kAdjHdla) d += cond_hdla_at(A, i);
+    if (A.fold_syn) {   // after every density conductance, as the group kernels add theirs
+        if (A.es_grp) {
+            const int q = A.es_grp[i];
+            if (q >= 0) d += cond_syn_at(A, q, i);
+        }
+        if (A.e2_grp) {
+            const int q = A.e2_grp[i];
+            if (q >= 0) d += cond_syn2_at(A, q, i);
+        }
+    }
     A.dT[i] = d;
     A.rhsT[i] = lv;
     A.vT[i] = 0.0;
@@ -243,7 +304,14 @@ __global__ void k_adj_before_nodes(AdjStep A) {
 // fuse_param (only Ca_HVA's adds to lambda_v^n, after C mu as in its own kernel).
 __global__ void k_adj_after_nodes(AdjStep A) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= A.N) return;
+    if (i >= A.N) {
+        // with fold_syn, threads N.. take the synapses' parameter terms
+        if (!A.fold_syn) return;
+        const int j = i - A.N, nes = A.m[M_EXPSYN].n;
+        if (j < nes) syn_param_at(A, j);
+        else if (j - nes < A.m[M_EXP2SYN].n) syn2_param_at(A, j - nes);
+        return;
+    }
     const unsigned fp = A.fuse_param;
     double lnew = A.cfac * A.cm[i] * A.mu[i];
     if (fp & kAdjHH) hh_param_at(A, i, i);
@@ -253,64 +321,31 @@ __global__ void k_adj_after_nodes(AdjStep A) {
     A.lam_v_new[i] = lnew;
 }
 
-// ExpSyn decay: lambda_geff = exp(-dt/tau) lambda_g (in place)
-__global__ void k_adj_syn_state(AdjStep A) {
-    const MechDev& m = A.m[M_EXPSYN];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    A.lam_g[j] = exp(-A.dt / m.col(ES_TAU)[j]) * A.lam_g[j];
-}
+#define HX_ADJ_SYN(MECH)                                       \
+    const MechDev& m = A.m[MECH];                              \
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;       \
+    if (j >= m.n) return
+#define HX_ADJ_GROUP(MECH)                                     \
+    const MechDev& m = A.m[MECH];                              \
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;       \
+    if (q >= m.ngrp) return
 
-// Exp2Syn decay: lambda_{A,B eff} = exp(-dt/tau_{1,2}) lambda_{A,B}
-__global__ void k_adj_syn2_state(AdjStep A) {
-    const MechDev& m = A.m[M_EXP2SYN];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    A.lam_ab[j] *= exp(A.dt * (-1.0 / m.col(E2_TAU1)[j]));
-    A.lam_ab[m.n + j] *= exp(A.dt * (-1.0 / m.col(E2_TAU2)[j]));
-}
-
-// Exp2Syn grouped by node: sum of (B_eff - A_eff) x 1e2/area
-__global__ void k_adj_cond_syn2(AdjStep A) {
-    const MechDev& m = A.m[M_EXP2SYN];
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= m.ngrp) return;
-    const int node = m.grp_node[q];
-    double g = 0.0;
-    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.ab0[m.n + j] - A.ab0[j];
-    A.dT[node] += g * (1.e2 / A.area[node]);
-}
-
-// synapses grouped by node: sum of g_eff x 1e2/area
+__global__ void k_adj_syn_state(AdjStep A) { HX_ADJ_SYN(M_EXPSYN); syn_state_at(A, j); }
+__global__ void k_adj_syn2_state(AdjStep A) { HX_ADJ_SYN(M_EXP2SYN); syn2_state_at(A, j); }
+__global__ void k_adj_syn_param(AdjStep A) { HX_ADJ_SYN(M_EXPSYN); syn_param_at(A, j); }
+__global__ void k_adj_syn2_param(AdjStep A) { HX_ADJ_SYN(M_EXP2SYN); syn2_param_at(A, j); }
 __global__ void k_adj_cond_syn(AdjStep A) {
-    const MechDev& m = A.m[M_EXPSYN];
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= m.ngrp) return;
+    HX_ADJ_GROUP(M_EXPSYN);
     const int node = m.grp_node[q];
-    double g = 0.0;
-    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += A.geff[j];
-    A.dT[node] += g * (1.e2 / A.area[node]);
+    A.dT[node] += cond_syn_at(A, q, node);
 }
-
-// Exp2Syn: lambda_{A,eff} += mu (v^{n+1} - e) 1e2/area, lambda_{B,eff} -= the same
-__global__ void k_adj_syn2_param(AdjStep A) {
-    const MechDev& m = A.m[M_EXP2SYN];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    const double t = A.mu[node] * (A.v1[node] - m.col(E2_E)[j]) * (1.e2 / A.area[node]);
-    A.lam_ab[j] += t;
-    A.lam_ab[m.n + j] -= t;
+__global__ void k_adj_cond_syn2(AdjStep A) {
+    HX_ADJ_GROUP(M_EXP2SYN);
+    const int node = m.grp_node[q];
+    A.dT[node] += cond_syn2_at(A, q, node);
 }
-
-// lambda_geff += -mu (v^{n+1} - e) 1e2/area
-__global__ void k_adj_syn_param(AdjStep A) {
-    const MechDev& m = A.m[M_EXPSYN];
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= m.n) return;
-    const int node = m.node[j];
-    A.lam_g[j] -= A.mu[node] * (A.v1[node] - m.col(ES_E)[j]) * (1.e2 / A.area[node]);
-}
+#undef HX_ADJ_SYN
+#undef HX_ADJ_GROUP
 
 // events delivered at step n: ExpSyn dL/dw += lambda_geff, Exp2Syn dL/dw += factor
 // (lambda_A + lambda_B) (one block)
@@ -400,10 +435,12 @@ void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
         hipLaunchKernelGGL(k_adj_hdla_state, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
     if (own(M_CADYN, kAdjCaDyn, a.fuse_state))
         hipLaunchKernelGGL(k_adj_cadyn, grid_of(a.m[M_CADYN].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXP2SYN].n > 0)
+    const long long nsyn = a.fold_syn ? static_cast<long long>(a.m[M_EXPSYN].n) + a.m[M_EXP2SYN].n : 0;
+    if (!a.fold_syn && a.m[M_EXPSYN].n > 0)
+        hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+    if (!a.fold_syn && a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_state, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(k_adj_before_nodes, grid_of(a.N), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_adj_before_nodes, grid_of(a.N + nsyn), dim3(kBlock), 0, s, a);
     if (own(M_PAS, kAdjPas, a.fuse_cond))
         hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
     if (own(M_HH, kAdjHH, a.fuse_cond)) hipLaunchKernelGGL(k_adj_cond_hh, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
@@ -411,22 +448,24 @@ void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
         hipLaunchKernelGGL(k_adj_cond_cahva, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
     if (own(M_HDLA, kAdjHdla, a.fuse_cond))
         hipLaunchKernelGGL(k_adj_cond_hdla, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXPSYN].ngrp > 0)
+    if (!a.fold_syn && a.m[M_EXPSYN].ngrp > 0)
         hipLaunchKernelGGL(k_adj_cond_syn, grid_of(a.m[M_EXPSYN].ngrp), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXP2SYN].ngrp > 0)
+    if (!a.fold_syn && a.m[M_EXP2SYN].ngrp > 0)
         hipLaunchKernelGGL(k_adj_cond_syn2, grid_of(a.m[M_EXP2SYN].ngrp), dim3(kBlock), 0, s, a);
 }
 
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
     auto own = [&](int id, unsigned bit) { return a.m[id].n > 0 && !(a.fuse_param & bit); };
-    hipLaunchKernelGGL(k_adj_after_nodes, grid_of(a.N), dim3(kBlock), 0, s, a);
+    const long long nsyn = a.fold_syn ? static_cast<long long>(a.m[M_EXPSYN].n) + a.m[M_EXP2SYN].n : 0;
+    hipLaunchKernelGGL(k_adj_after_nodes, grid_of(a.N + nsyn), dim3(kBlock), 0, s, a);
     if (own(M_HH, kAdjHH)) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
     if (own(M_PAS, kAdjPas)) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
     if (own(M_CAHVA, kAdjCaHVA))
         hipLaunchKernelGGL(k_adj_cahva_param, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
     if (own(M_HDLA, kAdjHdla)) hipLaunchKernelGGL(k_adj_hdla_param, grid_of(a.m[M_HDLA].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXPSYN].n > 0) hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
-    if (a.m[M_EXP2SYN].n > 0)
+    if (!a.fold_syn && a.m[M_EXPSYN].n > 0)
+        hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
+    if (!a.fold_syn && a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_param, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].n > 0 || a.m[M_EXP2SYN].n > 0) hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
 }

@@ -371,6 +371,12 @@ struct AdjStep {
     // on every node, instance i at node i): gate adjoints and CaDynamics_E2 (fuse_state),
     // conductances (fuse_cond), parameter terms (fuse_param)
     unsigned fuse_state, fuse_cond, fuse_param;
+    // fold_syn: the node-parallel kernels also take the synapses (decay adjoints and
+    // parameter terms on threads N.., each node's grouped conductances after its density
+    // ones); es_grp / e2_grp map a node to its ExpSyn / Exp2Syn group (-1: none)
+    int fold_syn;
+    const int* es_grp;
+    const int* e2_grp;
 };
 constexpr unsigned kAdjPas = 1, kAdjHH = 2, kAdjCaHVA = 4, kAdjHdla = 8, kAdjCaDyn = 16;
 

@@ -291,6 +291,7 @@ struct hx_sim {
     std::vector<VecPlayHost> vecplay;
     int event_cap_request = 0;
     int fusion_allowed = 1;
+    int* d_syn_grp[2] = {nullptr, nullptr};   // adjoint: node -> ExpSyn / Exp2Syn group
     unsigned adj_fuse_bits = 0;          // last hx_adjoint's node-parallel masks (state | cond << 8 | param << 16)
     bool uniform_on = true;              // parameter columns with one value read as scalars
     bool cm_uniform = false;             // cm holds one value on every node (as the columns above)
@@ -4165,8 +4166,35 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         }
         for (int k = 0; k < 4; ++k)
             if (dense(cd_id[k])) A.fuse_param |= cd_bit[k];
+        // the synapses join when every density conductance is in the node kernel, so that
+        // their grouped conductances still come after the density ones on each node
+        bool all_cond = true;
+        for (int k = 0; k < 4; ++k) all_cond = all_cond && (!has(cd_id[k]) || (A.fuse_cond & cd_bit[k]));
+        if (all_cond && (has(M_EXPSYN) || has(M_EXP2SYN))) {
+            A.fold_syn = 1;
+            // node -> its group (instances sorted by node, one group per node)
+            int* maps[2] = {nullptr, nullptr};
+            for (int k = 0; k < 2; ++k) {
+                const int id = k == 0 ? M_EXPSYN : M_EXP2SYN;
+                if (!has(id)) continue;
+                if (!sim->d_syn_grp[k]) sim->d_syn_grp[k] = dalloc<int>(owned, N);
+                std::vector<int> g(N, -1);
+                const std::vector<int>& nodes = sim->syn_node[k];
+                int q = -1;
+                for (size_t j = 0; j < nodes.size(); ++j) {
+                    if (j == 0 || nodes[j] != nodes[j - 1]) ++q;
+                    g[nodes[j]] = q;
+                }
+                HXC(hipMemcpyAsync(sim->d_syn_grp[k], g.data(), sizeof(int) * N, hipMemcpyHostToDevice, st));
+                HXC(hipStreamSynchronize(st));
+                maps[k] = sim->d_syn_grp[k];
+            }
+            A.es_grp = maps[0];
+            A.e2_grp = maps[1];
+        }
     }
-    sim->adj_fuse_bits = A.fuse_state | (A.fuse_cond << 8) | (A.fuse_param << 16);
+    sim->adj_fuse_bits = A.fuse_state | (A.fuse_cond << 8) | (A.fuse_param << 16) |
+                         (static_cast<unsigned>(A.fold_syn) << 24);
     SolveArgs S{};
     S.nunit = sim->nunit;
     S.unit_node_begin = sim->d_unit_node_begin;

@@ -131,13 +131,14 @@ def test_exp2syn_weight_gradients_match_fd(problem):
 
 
 def test_node_parallel_kernels_give_the_same_bits(problem):
-    """Every mechanism of this model has an instance on every node, so the backward step
-    runs them all in its two node-parallel kernels; each mechanism's own kernels
+    """Every density mechanism of this model has an instance on every node, so the backward
+    step runs them and the synapses in its two node-parallel kernels; each mechanism's own kernels
     (hx_set_fusion(0)) give the same loss and gradients, bit for bit, on the same tape."""
     _, target, loss, grads, g = problem
     every = 0b1111                      # pas, hh, Ca_HVA, hd_la
     gates = 0b11110                     # hh, Ca_HVA, hd_la and CaDynamics_E2
-    assert g.info("adjoint_fused") == (gates | every << 8 | every << 16), hex(g.info("adjoint_fused"))
+    synapses = 1 << 24                  # Exp2Syn's decay, conductance and parameter terms too
+    assert g.info("adjoint_fused") == (gates | every << 8 | every << 16 | synapses), hex(g.info("adjoint_fused"))
     g.set_fusion(False)
     try:
         loss2 = g.adjoint(np.array([0]), target)
