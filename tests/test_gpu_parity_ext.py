@@ -178,6 +178,34 @@ def test_full_size_prefix(gpu_lib, config, ncell, nref):
     assert np.all(np.isfinite(v))
 
 
+@pytest.mark.parametrize("config,ncell", [(3, 2000), (2, 10000)])
+def test_full_size_cells_across_groups(gpu_lib, config, ncell):
+    """At full size the cells run as two groups on two streams, in solve units of a few
+    cells.  The first cell, the cells either side of the groups' boundary and the last two
+    cells, each against an oracle model of that cell alone (the cells are independent and
+    each has its own random stream, so build_config(first_cell=c) is cell c)."""
+    tstop = 5.0
+    picks = [0, ncell // 2 - 1, ncell // 2, ncell - 2, ncell - 1]
+    full = build_config(config, ncell, tstop)
+    mons = [("global", "v", c) for c in picks]          # node c is cell c's root
+    print(f"case full-size cells across groups config={config} ncell={ncell} cells={picks}", flush=True)
+    g = Sim()
+    g.load_model_from_spec(dataclasses.replace(full, monitors=mons))
+    g.finitialize(-65.0)
+    g.run(tstop)
+    assert g.info("cell_groups") == 2 and g.info("multi_stream") == 1
+    tr = g.traces()
+    for k, c in enumerate(picks):
+        o = oracle.OracleSim(build_config(config, 1, tstop, first_cell=c), monitors=[("global", "v", 0)])
+        o.finitialize(-65.0)
+        o.run(tstop)
+        ot = o.traces()
+        assert ot.shape == (1, tr.shape[1])
+        err = float(np.max(np.abs(ot[0] - tr[k])))
+        print(f"  cell {c}: max |dv| {err:.3e}", flush=True)
+        assert err < V_TOL, (c, err)
+
+
 def test_axial_coefficient_writes_reach_the_solver(gpu_lib):
     """a and b written through handles mid-run: the solve runs on each cell's
     centre-rooted tree, where the links between the model root and the centre
