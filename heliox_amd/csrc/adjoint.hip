@@ -301,7 +301,8 @@ __global__ void k_adj_before_nodes(AdjStep A) {
 }
 
 // After the solve: lambda_v^n = C mu, then the parameter terms of the mechanisms in
-// fuse_param (only Ca_HVA's adds to lambda_v^n, after C mu as in its own kernel).
+// fuse_param (only Ca_HVA's adds to lambda_v^n, after C mu as in its own kernel), then
+// the loss term when the host hands it over (no kernel after this one adds to lambda_v^n).
 __global__ void k_adj_after_nodes(AdjStep A) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= A.N) {
@@ -318,6 +319,10 @@ __global__ void k_adj_after_nodes(AdjStep A) {
     if (fp & kAdjPas) pas_param_at(A, i, i);
     if (fp & kAdjCaHVA) cahva_param_at(A, i, i, &lnew);
     if (fp & kAdjHdla) hdla_param_at(A, i, i);
+    if (A.loss_v) {   // the loss term of v^n, last, as k_adj_loss adds it
+        const int j = A.loss_of_node[i];
+        if (j >= 0) lnew += 2.0 * A.loss_scale * (A.loss_v[i] - A.loss_tgt[j]);
+    }
     A.lam_v_new[i] = lnew;
 }
 

@@ -377,6 +377,12 @@ struct AdjStep {
     int fold_syn;
     const int* es_grp;
     const int* e2_grp;
+    // loss term of lambda_v^n added by k_adj_after_nodes (loss_v null: by k_adj_loss):
+    // node i adds 2 loss_scale (loss_v[i] - loss_tgt[loss_of_node[i]]) where that index is >= 0
+    const double* loss_v;
+    const double* loss_tgt;
+    const int* loss_of_node;
+    double loss_scale;
 };
 constexpr unsigned kAdjPas = 1, kAdjHH = 2, kAdjCaHVA = 4, kAdjHdla = 8, kAdjCaDyn = 16;
 

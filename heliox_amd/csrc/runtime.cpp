@@ -4193,8 +4193,25 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
             A.e2_grp = maps[1];
         }
     }
+    // the loss term joins k_adj_after_nodes when no later kernel adds to lambda_v^n (Ca_HVA's
+    // own parameter kernel would) and the loss nodes are distinct (one thread per node)
+    int* d_lmap = nullptr;
+    if (sim->fusion_allowed) {
+        const HostMech& ch = sim->mech[M_CAHVA];
+        if (!(ch.present && ch.n > 0) || (A.fuse_param & kAdjCaHVA)) {
+            std::vector<int> lmap(N, -1);
+            bool distinct = true;
+            for (int j = 0; j < nloss; ++j) {
+                if (lmap[ln[j]] >= 0) distinct = false;
+                lmap[ln[j]] = j;
+            }
+            if (distinct) d_lmap = dupload(owned, lmap);
+        }
+    }
+    A.loss_of_node = d_lmap;
+    A.loss_scale = scale;
     sim->adj_fuse_bits = A.fuse_state | (A.fuse_cond << 8) | (A.fuse_param << 16) |
-                         (static_cast<unsigned>(A.fold_syn) << 24);
+                         (static_cast<unsigned>(A.fold_syn) << 24) | ((d_lmap ? 1u : 0u) << 25);
     SolveArgs S{};
     S.nunit = sim->nunit;
     S.unit_node_begin = sim->d_unit_node_begin;
@@ -4227,10 +4244,12 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         A.ab0 = with_e2 ? sim->d_tape_ab + static_cast<size_t>(n) * 2 * e2.n : nullptr;
         A.lam_v = lv;
         A.lam_v_new = lv2;
+        A.loss_v = (d_lmap && n >= 1) ? sim->d_tape_v + (n - 1) * row : nullptr;
+        A.loss_tgt = n >= 1 ? d_tgt + static_cast<size_t>(n - 1) * nloss : nullptr;
         launch_adj_before_solve(A, st);
         launch_solve(S, sim->max_slots, st);
         launch_adj_after_solve(A, st);
-        if (n >= 1)
+        if (n >= 1 && !d_lmap)
             launch_adj_loss(sim->d_tape_v + (n - 1) * row, d_ln, d_tgt + static_cast<size_t>(n - 1) * nloss, nloss,
                             scale, lv2, st);
         std::swap(lv, lv2);

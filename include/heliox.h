@@ -289,7 +289,7 @@ int hx_set_group_streams(hx_sim* sim, int enable);
  * "outputs_pending" (1 while its node-kernel outputs wait), "adjoint_fused" (the mechanisms the
  * last hx_adjoint ran in its node-parallel kernels: bits 0-7 gate adjoints, 8-15 conductances,
  * 16-23 parameter terms; bit 0 pas, 1 hh, 2 Ca_HVA, 3 hd_la, 4 CaDynamics_E2; bit 24: the synapses
- * too). */
+ * too; bit 25: the loss term too). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the

@@ -115,7 +115,7 @@ def test_node_parallel_kernels_give_the_same_bits(problem):
     kernels take pas's conductance and parameter term, hh keeps its own kernels.  Each
     mechanism's own kernels (hx_set_fusion(0)) give the same bits on the same tape."""
     base, target, loss, grads, g = problem
-    assert g.info("adjoint_fused") == (1 << 8 | 1 << 16), hex(g.info("adjoint_fused"))
+    assert g.info("adjoint_fused") == (1 << 8 | 1 << 16 | 1 << 25), hex(g.info("adjoint_fused"))
     g.set_fusion(False)
     try:
         loss2 = g.adjoint(np.arange(base.ncell), target)

@@ -138,7 +138,9 @@ def test_node_parallel_kernels_give_the_same_bits(problem):
     every = 0b1111                      # pas, hh, Ca_HVA, hd_la
     gates = 0b11110                     # hh, Ca_HVA, hd_la and CaDynamics_E2
     synapses = 1 << 24                  # Exp2Syn's decay, conductance and parameter terms too
-    assert g.info("adjoint_fused") == (gates | every << 8 | every << 16 | synapses), hex(g.info("adjoint_fused"))
+    loss_term = 1 << 25                 # and the loss term
+    assert g.info("adjoint_fused") == (gates | every << 8 | every << 16 | synapses | loss_term), \
+        hex(g.info("adjoint_fused"))
     g.set_fusion(False)
     try:
         loss2 = g.adjoint(np.array([0]), target)
