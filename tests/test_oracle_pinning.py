@@ -143,6 +143,126 @@ def test_sealed_cable_steady_state():
 
 
 # ---------------------------------------------------------------------------
+# axial assembly with unequal areas (simulate.cpp:541-554): a[i] carries the
+# parent's area and b[i] the node's own, so every check below has a != b
+# ---------------------------------------------------------------------------
+def axial_coefficients(parent, gax, area):
+    """The model arrays for edge conductances gax[i] (uS, node i to its parent):
+    a[i] = -1e2 gax / area[parent], b[i] = -1e2 gax / area[i]."""
+    a = np.zeros(len(parent))
+    b = np.zeros(len(parent))
+    for i, p in enumerate(parent):
+        if p >= 0:
+            a[i] = -1e2 * gax[i] / area[p]
+            b[i] = -1e2 * gax[i] / area[i]
+    return a, b
+
+
+def physics_step(parent, gax, area, cm, gpas, epas, v, inj, dt):
+    """One backward-Euler step written from the membrane equation of each
+    compartment k (current densities in mA/cm2, areas in um2, gax in uS):
+        1e-3 cm_k (v'_k - v_k) / dt = -gpas (v'_k - e) + sum_j 1e2 gax_kj / A_k (v'_j - v'_k) + inj_k
+    solved as a dense linear system."""
+    n = len(parent)
+    M = np.diag(1e-3 * cm / dt + gpas)
+    r = 1e-3 * cm / dt * v + gpas * epas + inj
+    for i, p in enumerate(parent):
+        if p < 0:
+            continue
+        for k, j in ((i, p), (p, i)):
+            c = 1e2 * gax[i] / area[k]
+            M[k, k] += c
+            M[k, j] -= c
+    return np.linalg.solve(M, r)
+
+
+def passive_tree_spec(parent, gax, area, cm, gpas, epas, amp, dt):
+    a, b = axial_coefficients(parent, gax, area)
+    n = len(parent)
+    spec = ModelSpec(ncell=1, parent=np.asarray(parent, np.int32), a=a, b=b, area=np.asarray(area, float),
+                     cm=np.asarray(cm, float), dt=dt)
+    spec.mechs["pas"] = MechSpec(np.arange(n, dtype=np.int32), {"g_pas": np.full(n, gpas), "e_pas": np.full(n, epas)})
+    spec.mechs["IClamp"] = MechSpec(np.array([0], np.int32), {"delay": np.array([0.5]), "dur": np.array([1.0]),
+                                                              "amp": np.array([amp])})
+    return spec
+
+
+def test_two_compartments_unequal_areas_backward_euler():
+    """Soma (A0) and one dendritic compartment (A1 = A0 / 5) coupled by gax:
+    each compartment's coupling term is 1e2 gax / A_k, so the two rows differ
+    by the area ratio; IClamp at the soma from 0.5 to 1.5 ms."""
+    dt, gax, gpas, epas, amp = 0.025, 0.03, 2e-4, -70.0, 0.4
+    parent, area, cm = [-1, 0], np.array([1500.0, 300.0]), np.array([1.0, 1.7])
+    spec = passive_tree_spec(parent, [0.0, gax], area, cm, gpas, epas, amp, dt)
+    spec.monitors = [("global", "v", 0), ("global", "v", 1)]
+    o = oracle.OracleSim(spec)
+    o.finitialize(-62.0)
+    o.run(2.0)
+    got = o.traces()
+    # the two rows written out by hand
+    v, t, ref = np.array([-62.0, -62.0]), 0.0, [np.array([-62.0, -62.0])]
+    c0, c1 = 1e-3 * cm / dt
+    g0, g1 = 1e2 * gax / area[0], 1e2 * gax / area[1]
+    for _ in range(got.shape[1] - 1):
+        tmid = t + 0.5 * dt
+        inj = amp * 1e2 / area[0] if 0.5 <= tmid < 1.5 else 0.0
+        M = np.array([[c0 + gpas + g0, -g0], [-g1, c1 + gpas + g1]])
+        v = np.linalg.solve(M, [c0 * v[0] + gpas * epas + inj, c1 * v[1] + gpas * epas])
+        t = tmid + 0.5 * dt
+        ref.append(v)
+    ref = np.array(ref).T
+    assert np.max(np.abs(got - ref)) < 1e-10
+    # the dendrite moved, and far more than the tolerance
+    assert abs(got[1].max() - got[1, 0]) > 1.0
+
+
+def tapered_tree(rng, n):
+    parent = np.array([-1] + [int(rng.integers(max(0, i - 4), i)) for i in range(1, n)], np.int32)
+    diam = np.linspace(4.0, 0.5, n) * rng.uniform(0.8, 1.2, n)
+    L = rng.uniform(5.0, 40.0, n)
+    area = math.pi * diam * L
+    Ra = 150.0
+    gax = np.zeros(n)
+    for i in range(1, n):
+        # half-segment resistances in series (Mohm), conductance in uS
+        r = 1e-2 * Ra * (L[i] / 2 / (math.pi * (diam[i] / 2) ** 2) + L[parent[i]] / 2 / (math.pi * (diam[parent[i]] / 2) ** 2))
+        gax[i] = 1.0 / r
+    return parent, gax, area
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_tapered_tree_backward_euler_and_charge_conservation(seed):
+    """A branched tree with tapering diameters (a != b on every edge): every
+    step equals the dense backward-Euler solve of the membrane equations, and
+    the area-weighted sum of capacitive and membrane currents equals the
+    injected current (the axial currents cancel in pairs)."""
+    rng = np.random.default_rng(seed)
+    n, dt, gpas, epas, amp = 40, 0.025, 1e-4, -65.0, 0.3
+    parent, gax, area = tapered_tree(rng, n)
+    cm = rng.uniform(0.8, 2.0, n)
+    spec = passive_tree_spec(parent, gax, area, cm, gpas, epas, amp, dt)
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(-60.0)
+    v = o.array("global", "v").copy()
+    t = 0.0
+    for step in range(80):
+        tmid = t + 0.5 * dt
+        on = 0.5 <= tmid < 1.5
+        inj = np.zeros(n)
+        inj[0] = amp * 1e2 / area[0] if on else 0.0
+        o.fadvance()
+        got = o.array("global", "v").copy()
+        ref = physics_step(parent, gax, area, cm, gpas, epas, v, inj, dt)
+        assert np.max(np.abs(got - ref)) < 1e-10, step
+        # sum_k A_k (C dv/dt + I_m) = injected current (um2 mA/cm2 = 1e-2 nA)
+        imem = 1e-3 * cm * (got - v) / dt + gpas * (got - epas)
+        total = float(np.sum(area * imem)) * 1e-2
+        assert abs(total - (amp if on else 0.0)) < 1e-9 * max(1.0, float(np.sum(area * np.abs(imem))) * 1e-2), step
+        v, t = got, tmid + 0.5 * dt
+    assert np.max(np.abs(v - (-60.0))) > 0.1
+
+
+# ---------------------------------------------------------------------------
 # hh (hh_templated.cu) against the textbook Hodgkin-Huxley rate functions
 # ---------------------------------------------------------------------------
 def hh_textbook(v, celsius=6.3):
@@ -334,6 +454,36 @@ def test_hdla_gate_relaxation_under_clamp(v1, celsius):
     x = o.monitor(0)
     assert np.max(np.abs(x - relaxation(l0, l1, t1, x.size))) < 1e-10
     assert abs(x[-1] - x[0]) > 1e-3
+
+
+@pytest.mark.parametrize("ehd", [-30.0, -47.0])
+@pytest.mark.parametrize("l0", [0.05, 0.6])
+def test_hdla_current_moves_v_toward_ehd(ehd, l0):
+    """Ih's current i = ghdbar l (v - ehd) (hd_la.cu:113-115) with ehd set as a
+    global and l started away from linf(v): a compartment carrying only Ih
+    follows the backward-Euler recurrence
+        v' = v - ghdbar l (v - ehd) / (1e-3 cm / dt + ghdbar l),
+    with l advanced after each solve by the pinned relaxation
+    l' = l + (1 - exp(-dt / taul(v'))) (linf(v') - l)."""
+    dt, cm, ghdbar, v0 = 0.025, 1.0, 2e-3, -70.0
+    spec = single_compartment(cm=cm, dt=dt)
+    spec.mechs["hd_la"] = MechSpec(np.array([0], np.int32), {"ghdbar": np.array([ghdbar])}, globals={"ehd": ehd})
+    o = oracle.OracleSim(spec, monitors=[])
+    o.finitialize(v0)
+    assert abs(o.get("hd_la", "l", 0) - hdla_textbook(v0, 6.3)[0]) < 1e-14
+    o.set("hd_la", "l", 0, l0)
+    v, l = v0, l0
+    for step in range(40):
+        o.fadvance()
+        # the step's current uses the state before the step's update
+        assert abs(o.get("hd_la", "i", 0) - ghdbar * l * (v - ehd)) < 1e-13, step
+        v = v - ghdbar * l * (v - ehd) / (1e-3 * cm / dt + ghdbar * l)
+        linf, taul = hdla_textbook(v, 6.3)
+        l = l + (1 - math.exp(-dt / taul)) * (linf - l)
+        assert abs(o.array("global", "v")[0] - v) < 1e-10, step
+        assert abs(o.get("hd_la", "l", 0) - l) < 1e-12, step
+    # v moved toward ehd by far more than the tolerance
+    assert abs(v - v0) > 0.5 and abs(v - ehd) < abs(v0 - ehd)
 
 
 def im_textbook(v):
