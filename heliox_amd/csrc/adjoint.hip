@@ -368,12 +368,17 @@ __global__ void __launch_bounds__(256) k_adj_events(AdjStep A) {
     }
 }
 
-// loss term of v^n: lambda_v^n[node] += 2 scale (v^n - target^n)
-__global__ void k_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale,
-                           double* lam) {
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= n) return;
-    lam[nodes[j]] += 2.0 * scale * (v[nodes[j]] - target[j]);
+// loss term of v^n: lambda_v^n[node] += 2 scale (v^n - target^n_j) for every loss index j
+// of the node, one thread per distinct node adding its terms in list order
+__global__ void k_adj_loss(const double* v, const int* nodes, const int* begin, const int* idx, int n,
+                           const double* target, double scale, double* lam) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n) return;
+    const int node = nodes[q];
+    const double vn = v[node];
+    double acc = lam[node];
+    for (int e = begin[q]; e < begin[q + 1]; ++e) acc += 2.0 * scale * (vn - target[idx[e]]);
+    lam[node] = acc;
 }
 
 // out[r * nnodes + j] = tape_v[r * row + nodes[j]]
@@ -475,9 +480,10 @@ void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
     if (a.m[M_EXPSYN].n > 0 || a.m[M_EXP2SYN].n > 0) hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
 }
 
-void launch_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale, double* lam,
-                     hipStream_t s) {
-    if (n > 0) hipLaunchKernelGGL(k_adj_loss, grid_of(n), dim3(kBlock), 0, s, v, nodes, target, n, scale, lam);
+void launch_adj_loss(const double* v, const int* nodes, const int* begin, const int* idx, int n,
+                     const double* target, double scale, double* lam, hipStream_t s) {
+    if (n > 0)
+        hipLaunchKernelGGL(k_adj_loss, grid_of(n), dim3(kBlock), 0, s, v, nodes, begin, idx, n, target, scale, lam);
 }
 
 void launch_adj_gather(const double* tape_v, long long row, const int* nodes, int nnodes, int nrows, double* out,

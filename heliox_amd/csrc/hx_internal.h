@@ -441,8 +441,8 @@ void launch_set_v(double* v, int n, double val, hipStream_t s);
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s);
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s);
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s);
-void launch_adj_loss(const double* v, const int* nodes, const double* target, int n, double scale, double* lam,
-                     hipStream_t s);
+void launch_adj_loss(const double* v, const int* nodes, const int* begin, const int* idx, int n,
+                     const double* target, double scale, double* lam, hipStream_t s);
 void launch_adj_gather(const double* tape_v, long long row, const int* nodes, int nnodes, int nrows, double* out,
                        hipStream_t s);
 void launch_adam(const AdamArgs& a, hipStream_t s);

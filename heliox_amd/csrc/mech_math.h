@@ -187,7 +187,10 @@ __device__ __forceinline__ double cadyn_step(double cai, double ica, double gamm
 // forms by a few ulps.  The reference forms stay in use where their
 // intermediate values are outputs (assigned variables) and in the adjoint.
 // a / b from the hardware reciprocal, two Newton steps and a remainder correction: within
-// one ulp of the rounded quotient, for the normal, finite operands the rates produce.
+// one ulp of the rounded quotient, for the normal, finite operands the rates produce.  An
+// infinite or subnormal divisor (a rate's exp overflowing at an extreme voltage) makes the
+// Newton steps give NaN; such lanes take the IEEE division instead, so a / inf is 0 as in
+// the reference forms.
 __device__ __forceinline__ double div_r(double a, double b) {
     double r = __builtin_amdgcn_rcp(b);
     double e = fma(-b, r, 1.0);
@@ -195,7 +198,9 @@ __device__ __forceinline__ double div_r(double a, double b) {
     e = fma(-b, r, 1.0);
     r = fma(r, e, r);
     const double q = a * r;
-    return fma(fma(-b, q, a), r, q);
+    const double res = fma(fma(-b, q, a), r, q);
+    if (__builtin_expect(!__builtin_isfinite(res), 0)) return a / b;
+    return res;
 }
 
 __device__ __forceinline__ double vtrap_r(double x, double y, double inv_y) {

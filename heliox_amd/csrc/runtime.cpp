@@ -238,6 +238,13 @@ inline int trainable_id(int mech, const std::string& var) {
 }
 
 struct hx_sim {
+    // A device block that a repeated call refills: it is reallocated only to grow, the
+    // old block freed once the library stream has drained, so loops of such calls
+    // (finitialize, adjoint, optimizer and monitor changes) hold one block each.
+    struct DevSlot {
+        void* p = nullptr;
+        size_t bytes = 0;
+    };
     std::string err;
     double dt = 0.025;
     bool dt_set = false;                 // set by the caller (else a CoreNEURON export's dt is taken)
@@ -282,6 +289,11 @@ struct hx_sim {
     std::vector<int> pre_gid, pre_node;
     std::vector<double> pre_thr;
     std::vector<std::vector<double>> vecstim;
+    // the trains the current run reads: vecstim at finitialize, then what VecStim.play
+    // calls during the run leave (vecstim_play)
+    std::vector<std::vector<double>> vecstim_run;
+    bool vecstim_run_differs = false;
+    int vecstim_play(int inst, const double* times, int n);
     // NetStim trains (self-event times), made on the host up to step ns_horizon
     std::vector<std::vector<double>> netstim;
     int ns_horizon = 0;
@@ -292,6 +304,10 @@ struct hx_sim {
     int event_cap_request = 0;
     int fusion_allowed = 1;
     int* d_syn_grp[2] = {nullptr, nullptr};   // adjoint: node -> ExpSyn / Exp2Syn group
+    // adjoint loss: nodes and targets per call, the distinct nodes with their loss
+    // indices (node -> first index of its list), and node -> loss index when distinct
+    DevSlot adj_ln_slot, adj_tgt_slot, adj_samp_slot, adj_un_slot, adj_ubeg_slot, adj_uidx_slot, adj_lmap_slot;
+    std::vector<int> adj_lmap_nodes;             // the loss nodes adj_lmap_slot holds the map of
     unsigned adj_fuse_bits = 0;          // last hx_adjoint's node-parallel masks (state | cond << 8 | param << 16)
     bool uniform_on = true;              // parameter columns with one value read as scalars
     bool cm_uniform = false;             // cm holds one value on every node (as the columns above)
@@ -330,6 +346,9 @@ struct hx_sim {
     // device
     std::vector<void*> owned;
     hipStream_t stream = nullptr;
+    void* slot_reserve(DevSlot& s, size_t bytes);
+    template <class T>
+    T* slot_upload(DevSlot& s, const std::vector<T>& h);
     double *d_sa = nullptr, *d_sb = nullptr;   // solver coefficients (solver tree), node order
     double *d_v = nullptr, *d_d = nullptr, *d_rhs = nullptr, *d_a = nullptr, *d_b = nullptr, *d_cm = nullptr,
            *d_area = nullptr, *d_w = nullptr;
@@ -383,6 +402,7 @@ struct hx_sim {
         double* d_in_time = nullptr;
         int* d_in_inst = nullptr;
         int* d_in_round = nullptr;                // pass of the delivery loop that emits each input
+        DevSlot in_time_slot, in_inst_slot, in_round_slot;
         int* d_in_cursor = nullptr;
         int n_in = 0;
         int *d_vs_fo_begin = nullptr, *d_vs_fo_target = nullptr;
@@ -405,6 +425,7 @@ struct hx_sim {
     // time table
     std::vector<double> ttab;
     double* d_ttab = nullptr;
+    DevSlot ttab_slot;
     int ttab_cap = 0;
     int ttab_up = 0;                 // entries of ttab already in d_ttab (the table only grows)
     // gap
@@ -412,6 +433,7 @@ struct hx_sim {
     int* d_gap_inst = nullptr;
     // vecplay
     VecPlayDev* d_vecplay = nullptr;
+    DevSlot vecplay_slot;
     std::vector<std::tuple<std::string, std::string, int>> vecplay_keys;
     bool vecplay_dirty = true;
     // recorder
@@ -423,6 +445,7 @@ struct hx_sim {
     std::vector<std::vector<double>> mon_data;
     double** d_mon_ptr = nullptr;
     double* d_mon_buf = nullptr;
+    DevSlot mon_ptr_slot, mon_buf_slot;
     long long mon_buf_cap = 0;     // samples
     long long mon_buf_fill = 0;
     bool mon_dirty = true;
@@ -490,6 +513,7 @@ struct hx_sim {
         double** d_w = nullptr;
         double** d_g = nullptr;
         double *d_imp = nullptr, *d_m = nullptr, *d_v = nullptr;
+        DevSlot s_begin, s_w, s_g, s_imp, s_m, s_v;
     };
     std::vector<AdamHost> adams;
     // gap junctions added at run time (Simulate::add_gap_source/target, simulate.cpp:998-1100)
@@ -503,6 +527,7 @@ struct hx_sim {
     std::vector<double*> dg_src, dg_dst;
     double** d_dg_src = nullptr;
     double** d_dg_dst = nullptr;
+    DevSlot dg_src_slot, dg_dst_slot;
     bool dg_dirty = false;
     bool static_gaps_on = true;       // cleared by hx_clear_all_gap_junctions
     void launch_gap_transfers();
@@ -571,6 +596,8 @@ struct hx_sim {
         }
         pre_gid.clear(); pre_node.clear(); pre_thr.clear();
         vecstim.clear();
+        vecstim_run.clear();
+        vecstim_run_differs = false;
         netcons.clear();
         gaps.clear();
         if (vecplay.size() > keep_vecplay) vecplay.resize(keep_vecplay);
@@ -655,6 +682,33 @@ struct hx_sim {
     void sync_outputs();
     void finitialize(double v_init);
 };
+
+void* hx_sim::slot_reserve(DevSlot& s, size_t bytes) {
+    bytes = std::max<size_t>(bytes, 1);
+    if (s.p && s.bytes >= bytes) return s.p;
+    if (s.p) {
+        HXC(hipStreamSynchronize(stream));     // queued kernels may still read the old block
+        owned.erase(std::find(owned.begin(), owned.end(), s.p));
+        void* old = s.p;
+        s.p = nullptr;
+        s.bytes = 0;
+        HXC(hipFree(old));
+    }
+    HXC(hipMalloc(&s.p, bytes));
+    owned.push_back(s.p);
+    s.bytes = bytes;
+    return s.p;
+}
+
+template <class T>
+T* hx_sim::slot_upload(DevSlot& s, const std::vector<T>& h) {
+    T* p = static_cast<T*>(slot_reserve(s, h.size() * sizeof(T)));
+    if (!h.empty()) {
+        HXC(hipStreamSynchronize(stream));     // queued kernels may still read the block
+        HXC(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+    }
+    return p;
+}
 
 // ===========================================================================
 // layout
@@ -1545,7 +1599,7 @@ void hx_sim::upload_inputs() {
             ev.push_back({cur, s, std::min(round, kNsRounds - 1)});
         }
     };
-    for (int s = 0; s < nvs && s < static_cast<int>(vecstim.size()); ++s) add_train(vecstim[s], s, 1);
+    for (int s = 0; s < nvs && s < static_cast<int>(vecstim_run.size()); ++s) add_train(vecstim_run[s], s, 1);
     for (int j = 0; j < nns && j < static_cast<int>(netstim.size()); ++j) add_train(netstim[j], nvs + j, 2);
     std::stable_sort(ev.begin(), ev.end(), [](const In& x, const In& y) { return x.t < y.t; });
     for (auto& cg : groups) {
@@ -1559,11 +1613,45 @@ void hx_sim::upload_inputs() {
                 rr.push_back(e.round);
             }
         cg.n_in = static_cast<int>(tt.size());
-        cg.d_in_time = dupload(owned, tt);
-        cg.d_in_inst = dupload(owned, ii);
-        cg.d_in_round = dupload(owned, rr);
+        cg.d_in_time = slot_upload(cg.in_time_slot, tt);
+        cg.d_in_inst = slot_upload(cg.in_inst_slot, ii);
+        cg.d_in_round = slot_upload(cg.in_round_slot, rr);
     }
     inputs_dirty = false;
+}
+
+// VecEvent::play -> update_sequence (vecevent.cpp:280-309): the instance's vector becomes
+// `times`, read from its first element by the next finitialize (INITIAL, vecevent.cpp:
+// 94-107).  A run already initialised keeps what the instance has read: element()
+// (vecevent.cpp:123-156) has taken D + 1 elements after D deliveries and queued the
+// self event of the last, so the run delivers that one and then times[D + 1],
+// times[D + 2], ...; an instance that has read past its end takes nothing more.
+// The deliveries so far are the elements whose effective time (the running maximum,
+// as upload_inputs orders them) lies within the window of the last delivery, that of
+// finitialize or of step k - 1; those entries keep their place at the head of the
+// sorted input list, so the device's input cursor stays valid when the list is rebuilt.
+int hx_sim::vecstim_play(int inst, const double* times, int n) {
+    vecstim[inst].assign(times, times + n);
+    if (!initialized) {
+        inputs_dirty = true;
+        return 0;
+    }
+    std::vector<double>& run = vecstim_run[inst];
+    const double cut = ttab[k > 0 ? k - 1 : 0] + dt / 2;
+    size_t D = 0;
+    double prev = -INFINITY;
+    while (D < run.size()) {
+        const double cur = std::max(prev, run[D]);
+        if (cur > cut) break;
+        prev = cur;
+        ++D;
+    }
+    if (D == run.size()) return 0;              // nothing queued: index -1 (or an empty vector)
+    run.resize(D + 1);
+    for (int i = static_cast<int>(D) + 1; i < n; ++i) run.push_back(times[i]);
+    vecstim_run_differs = true;
+    upload_inputs();
+    return 0;
 }
 
 void hx_sim::upload_vecplay() {
@@ -1598,7 +1686,7 @@ void hx_sim::upload_vecplay() {
         vecplay_keys.push_back(key);
         items.push_back(it);
     }
-    d_vecplay = dupload(owned, items);
+    d_vecplay = slot_upload(vecplay_slot, items);
     vecplay_dirty = false;
 }
 
@@ -1634,7 +1722,7 @@ void hx_sim::upload_monitors() {
         groups[g].mon1 = static_cast<int>(std::lower_bound(order.begin(), order.end(), g + 1,
                                                            [&](int m, int gg) { return grp[m] < gg; }) - order.begin());
     }
-    d_mon_ptr = dupload(owned, ptrs);
+    d_mon_ptr = slot_upload(mon_ptr_slot, ptrs);
     mon_dirty = false;
 }
 
@@ -1649,7 +1737,7 @@ void hx_sim::ensure_ttab(int kneed) {
     }
     if (ttab_cap < static_cast<int>(ttab.size())) {
         ttab_cap = static_cast<int>(ttab.size()) * 2;
-        d_ttab = dalloc<double>(owned, ttab_cap);
+        d_ttab = static_cast<double*>(slot_reserve(ttab_slot, sizeof(double) * ttab_cap));
         ttab_up = 0;
     }
     // only new entries travel: a call whose steps the table already covers copies nothing
@@ -1670,7 +1758,7 @@ void hx_sim::ensure_mon_rows(long long rows) {
     long long want = std::max(rows, 2 * mon_buf_cap);
     want = std::max(want, std::min<long long>(1024, std::max<long long>(1, (64LL << 20) / (8 * nm))));
     mon_buf_cap = want;
-    d_mon_buf = dalloc<double>(owned, static_cast<size_t>(want * nm));
+    d_mon_buf = static_cast<double*>(slot_reserve(mon_buf_slot, sizeof(double) * static_cast<size_t>(want * nm)));
     mon_buf_fill = 0;
 }
 
@@ -2152,8 +2240,8 @@ void hx_sim::launch_gap_transfers() {
     const bool stat = static_gaps_on && !gaps.empty();
     if (!stat && dg_src.empty()) return;
     if (dg_dirty) {
-        d_dg_src = dg_src.empty() ? nullptr : dupload(owned, dg_src);
-        d_dg_dst = dg_dst.empty() ? nullptr : dupload(owned, dg_dst);
+        d_dg_src = dg_src.empty() ? nullptr : slot_upload(dg_src_slot, dg_src);
+        d_dg_dst = dg_dst.empty() ? nullptr : slot_upload(dg_dst_slot, dg_dst);
         dg_dirty = false;
     }
     tbegin(T_OTHER);
@@ -2652,6 +2740,11 @@ void hx_sim::finitialize(double v_init) {
         make_netstim_trains(std::max(ns_horizon, kNetStimHorizon0));
         inputs_dirty = true;
     }
+    if (inputs_dirty || vecstim_run_differs) {   // every VecStim starts its own vector again
+        vecstim_run = vecstim;
+        vecstim_run_differs = false;
+        inputs_dirty = true;
+    }
     if (inputs_dirty) upload_inputs();
     if (vecplay_dirty) upload_vecplay();
     if (mon_dirty) upload_monitors();
@@ -2958,6 +3051,20 @@ int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times) {
     sim->vecstim[inst].assign(times, times + n);
     sim->inputs_dirty = true;
     return 0;
+}
+
+int hx_call_mech_func(hx_sim* sim, const char* mech, const char* func, int inst, int n, const double* data) {
+    HX_SETTLE(sim);
+    API_BEGIN
+    const std::string mn = mech ? mech : "", fn = func ? func : "";
+    // the reference's FunctionRegistry holds one function (vecevent.h:42-45)
+    if (mn != "VecStim" || fn != "play") return sim->fail("function not registered: %s.%s", mn.c_str(), fn.c_str());
+    HostMech& m = sim->mech[M_VECSTIM];
+    if (!m.present || inst < 0 || inst >= m.n) return sim->fail("VecStim instance %d does not exist", inst);
+    if (n <= 0) return 0;                       // update_sequence returns without a change
+    if (!data) return sim->fail("VecStim.play: null spike-time array");
+    return sim->vecstim_play(inst, data, n);
+    API_END
 }
 
 int hx_model_add_netcon(hx_sim* sim, int src_kind, int src, const char* target, int inst, double w, double delay) {
@@ -4036,11 +4143,32 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     }
     hipStream_t st = sim->stream;
     auto& owned = sim->owned;
-    int* d_ln = dupload(owned, ln);
+    int* d_ln = sim->slot_upload(sim->adj_ln_slot, ln);
     std::vector<double> tgt(target, target + static_cast<size_t>(nsample) * nloss);
-    double* d_tgt = dupload(owned, tgt);
+    double* d_tgt = sim->slot_upload(sim->adj_tgt_slot, tgt);
+    // a node listed more than once gets each of its loss terms, in list order, from
+    // one thread: the distinct nodes, and for each the positions it has in the list
+    std::vector<int> un, ubeg, uidx;
+    {
+        std::vector<int> order(nloss);
+        std::iota(order.begin(), order.end(), 0);
+        std::stable_sort(order.begin(), order.end(), [&](int x, int y) { return ln[x] < ln[y]; });
+        for (int q = 0; q < nloss; ++q) {
+            if (q == 0 || ln[order[q]] != ln[order[q - 1]]) {
+                un.push_back(ln[order[q]]);
+                ubeg.push_back(q);
+            }
+            uidx.push_back(order[q]);
+        }
+        ubeg.push_back(nloss);
+    }
+    const int nun = static_cast<int>(un.size());
+    int* d_un = sim->slot_upload(sim->adj_un_slot, un);
+    int* d_ubeg = sim->slot_upload(sim->adj_ubeg_slot, ubeg);
+    int* d_uidx = sim->slot_upload(sim->adj_uidx_slot, uidx);
     // loss: mean over samples 1..nsample and loss nodes of (v - target)^2
-    double* d_samp = dalloc<double>(owned, static_cast<size_t>(nsample) * nloss);
+    double* d_samp = static_cast<double*>(
+        sim->slot_reserve(sim->adj_samp_slot, sizeof(double) * static_cast<size_t>(nsample) * nloss));
     launch_adj_gather(sim->d_tape_v, N, d_ln, nloss, nsample, d_samp, st);
     std::vector<double> samp(static_cast<size_t>(nsample) * nloss);
     HXC(hipMemcpyAsync(samp.data(), d_samp, sizeof(double) * samp.size(), hipMemcpyDeviceToHost, st));
@@ -4199,13 +4327,15 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     if (sim->fusion_allowed) {
         const HostMech& ch = sim->mech[M_CAHVA];
         if (!(ch.present && ch.n > 0) || (A.fuse_param & kAdjCaHVA)) {
-            std::vector<int> lmap(N, -1);
-            bool distinct = true;
-            for (int j = 0; j < nloss; ++j) {
-                if (lmap[ln[j]] >= 0) distinct = false;
-                lmap[ln[j]] = j;
+            if (nun == nloss) {           // distinct nodes
+                if (sim->adj_lmap_nodes != ln || !sim->adj_lmap_slot.p) {
+                    std::vector<int> lmap(N, -1);
+                    for (int j = 0; j < nloss; ++j) lmap[ln[j]] = j;
+                    sim->slot_upload(sim->adj_lmap_slot, lmap);
+                    sim->adj_lmap_nodes = ln;
+                }
+                d_lmap = static_cast<int*>(sim->adj_lmap_slot.p);
             }
-            if (distinct) d_lmap = dupload(owned, lmap);
         }
     }
     A.loss_of_node = d_lmap;
@@ -4229,8 +4359,8 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     double* lv = sim->d_lv;
     double* lv2 = sim->d_lv2;
     const size_t row = static_cast<size_t>(N);
-    launch_adj_loss(sim->d_tape_v + (nsample - 1) * row, d_ln, d_tgt + static_cast<size_t>(nsample - 1) * nloss,
-                    nloss, scale, lv, st);
+    launch_adj_loss(sim->d_tape_v + (nsample - 1) * row, d_un, d_ubeg, d_uidx, nun,
+                    d_tgt + static_cast<size_t>(nsample - 1) * nloss, scale, lv, st);
     for (int n = nsample - 1; n >= 0; --n) {
         A.v1 = sim->d_tape_v + n * row;
         A.x0 = sim->d_tape_x ? sim->d_tape_x + static_cast<size_t>(n) * 3 * xs : nullptr;
@@ -4250,8 +4380,8 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         launch_solve(S, sim->max_slots, st);
         launch_adj_after_solve(A, st);
         if (n >= 1 && !d_lmap)
-            launch_adj_loss(sim->d_tape_v + (n - 1) * row, d_ln, d_tgt + static_cast<size_t>(n - 1) * nloss, nloss,
-                            scale, lv2, st);
+            launch_adj_loss(sim->d_tape_v + (n - 1) * row, d_un, d_ubeg, d_uidx, nun,
+                            d_tgt + static_cast<size_t>(n - 1) * nloss, scale, lv2, st);
         std::swap(lv, lv2);
     }
     HXC(hipStreamSynchronize(st));
@@ -4326,12 +4456,12 @@ int hx_adam_step(hx_sim* sim, int opt, double lr, double inv_record_steps) {
     auto& owned = sim->owned;
     const int ng = static_cast<int>(o.imp.size());
     if (o.dirty) {   // (re)upload the groups; the host copies of m and v are current
-        o.d_begin = dupload(owned, o.begin);
-        o.d_w = dupload(owned, o.w);
-        o.d_g = dupload(owned, o.g);
-        o.d_imp = dupload(owned, o.imp);
-        o.d_m = dupload(owned, o.m);
-        o.d_v = dupload(owned, o.v);
+        o.d_begin = sim->slot_upload(o.s_begin, o.begin);
+        o.d_w = sim->slot_upload(o.s_w, o.w);
+        o.d_g = sim->slot_upload(o.s_g, o.g);
+        o.d_imp = sim->slot_upload(o.s_imp, o.imp);
+        o.d_m = sim->slot_upload(o.s_m, o.m);
+        o.d_v = sim->slot_upload(o.s_v, o.v);
         o.dirty = false;
     }
     ++o.step;

@@ -53,6 +53,7 @@ SIGNATURES = {
     "hx_model_set_iontype": (C.c_int, [_P, _S, C.c_int, _I]),
     "hx_model_add_presyn": (C.c_int, [_P, C.c_int, C.c_int, C.c_double]),
     "hx_model_set_vecstim": (C.c_int, [_P, C.c_int, C.c_int, _D]),
+    "hx_call_mech_func": (C.c_int, [_P, C.c_char_p, C.c_char_p, C.c_int, C.c_int, _D]),
     "hx_model_add_netcon": (C.c_int, [_P, C.c_int, C.c_int, _S, C.c_int, C.c_double, C.c_double]),
     "hx_model_add_gap": (C.c_int, [_P, C.c_int, C.c_int]),
     "hx_load_model": (C.c_int, [_P]),
@@ -851,10 +852,27 @@ class Sim:
             raise HelioxError(f"set_user_mod_num: {self.last_error()}")
 
     def call_mech_func(self, mech_name: str, func_name: str, *args) -> float:
-        """The reference's FunctionRegistry calls belong to mechanism families outside this
-        library; none is registered."""
-        self._pyfail(f"call_mech_func: no function {mech_name}.{func_name}")
-        return -1.0
+        """A registered mechanism function (SimWrapper.cpp:461-468, FunctionRegistry
+        func_table.cuh:97-130).  The one the reference registers is
+        ``VecStim.play(index, times)`` (vecevent.h:42-45, vecevent.cpp:280-309): the
+        instance's spike times become ``times``; an empty list changes nothing.  The next
+        finitialize reads the new times from the first; in a run already initialised the
+        instance delivers the event it has queued and then continues from the new times at
+        the position it has reached (``hx_call_mech_func``).  Returns 0.  As the reference's
+        registry throws, an unregistered name or a wrong argument count raises
+        ``RuntimeError``."""
+        self._py_err = None
+        if (mech_name, func_name) != ("VecStim", "play"):
+            raise HelioxError(f"function not registered: {mech_name}.{func_name}")
+        if len(args) != 2:
+            raise HelioxError(f"{mech_name}.{func_name}: takes 2 arguments (index, times), got {len(args)}")
+        idx, times = args
+        if isinstance(times, (int, float)):
+            times = [times]
+        tr = np.ascontiguousarray(np.asarray(times, dtype=np.float64).ravel())
+        rc = lib().hx_call_mech_func(self._h, _b(mech_name), _b(func_name), int(idx), tr.size, _dp(tr))
+        self._chk(rc, f"call_mech_func {mech_name}.{func_name}")
+        return 0.0
 
     def set_dense_blocks_f32(self, blocks) -> int:
         """Upload (bn, bn, K_len) float32 blocks; returns K_len or -1 (SimWrapper.cpp:533-572)."""

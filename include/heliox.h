@@ -69,15 +69,28 @@ int hx_model_set_global(hx_sim* sim, const char* mech, const char* var, double v
 int hx_model_set_iontype(hx_sim* sim, const char* ion, int n, const int* iontype);
 /* Threshold detector of a real cell (PreSyn, presyn.cpp:133-177); returns the detector index. */
 int hx_model_add_presyn(hx_sim* sim, int gid, int node, double threshold);
-/* VecStim spike times of one instance (VecEvent::update_sequence, vecevent.cpp:292-309). */
+/* VecStim spike times of one instance (VecEvent::update_sequence, vecevent.cpp:292-309),
+ * read from the first by the next finitialize (an empty array leaves no spikes). */
 int hx_model_set_vecstim(hx_sim* sim, int inst, int n, const double* times);
+/* SimWrapper::call_mech_func (SimWrapper.cpp:461-468) through FunctionRegistry
+ * (func_table.cuh:97-130), whose one registered function is VecStim.play (vecevent.h:42-45,
+ * VecEvent::play -> update_sequence, vecevent.cpp:280-309): mech "VecStim", func "play",
+ * inst the VecStim instance, times[n] its new spike times.  n <= 0 changes nothing.  The
+ * next finitialize reads the new times from the first.  In a run already initialised the
+ * instance keeps what it has read, as the reference's element() does: after D deliveries it
+ * has read D + 1 elements and queued the last, so it delivers that one and then
+ * times[D + 1], times[D + 2], ...; an instance that has read past its end takes nothing
+ * more until finitialize.  Any other name returns -1 ("function not registered"). */
+int hx_call_mech_func(hx_sim* sim, const char* mech, const char* func, int inst, int n, const double* times);
 /* NetCon into synapse `target` instance `inst` (ExpSyn / Exp2Syn).  src_kind 0: detector index,
  * 1: VecStim instance, 2: NetStim instance.  One source per synapse instance; a later netcon
  * replaces an earlier one (coredat_to_innerdat.cpp:356-364).
  * NetStim (netstim.cpp:211-330) is inserted like any mechanism, with parameters interval,
  * number, start, noise (defaults 10, 10, 50, 0) and id1, id2, id3, the ids of its own
- * Random123 Philox4x32 stream (id1 < 0, the default: the instance index).  Its trains are
- * made on the host at finitialize and as runs need them; it takes no incoming events.  The
+ * Random123 Philox4x32 stream (id1 < 0, the default: the instance index).  A NetStim that no
+ * netcon targets runs from a train made on the host at finitialize and as runs need them;
+ * one that netcons target runs on the device, taking its incoming events as NET_RECEIVE
+ * does (netstim.cpp:247-290: start, stop by a negative weight, weights truncated).  The
  * reference draws every instance from one shared stream and redraws all instances' intervals
  * on any event (netstim.cpp:118-161); here each instance draws only its own intervals from
  * its own stream, restarted at sequence 0 by every finitialize.  Parameter writes through
@@ -387,8 +400,10 @@ int hx_replay_compute_dw_dx_from_signals_into(hx_sim* sim, const float* it_lr_nt
                                               double dt_ms, int percise, double grad_scale, double eps,
                                               double grad_l2norm_threshold, int clip_strategy, int clip_check_every);
 /* No counterpart in the reference: hx_replay_compute_dw_dx_from_signals_into for callers
- * that cannot allocate device memory (code under HIP graph capture, tight serving or
- * training loops, harnesses that forbid hipMalloc).  Same arguments, checks and results;
+ * that cannot allocate device memory (tight serving or training loops, harnesses that
+ * forbid hipMalloc).  It cannot be captured into a HIP graph: it copies the host signals in
+ * and the results back synchronously and synchronises the library's stream before it
+ * returns.  Same arguments, checks and results;
  * every device buffer (the signals, the dv/dw history ring, the per-tick vectors) is
  * carved from one fixed 64 MiB device array that the library holds on each GPU it runs
  * on until the process ends, so the call makes no hipMalloc/hipFree.  A problem whose

@@ -84,6 +84,7 @@ def lib():
         L.hxo_set_iontype.argtypes = [C.c_void_p, C.c_char_p, C.c_int, _I]
         L.hxo_add_presyn.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_double]
         L.hxo_set_vecstim.argtypes = [C.c_void_p, C.c_int, C.c_int, _D]
+        L.hxo_vecstim_play.argtypes = [C.c_void_p, C.c_int, C.c_int, _D]
         L.hxo_add_netcon.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_char_p, C.c_int, C.c_double, C.c_double]
         L.hxo_add_vecplay.argtypes = [C.c_void_p, C.c_char_p, C.c_char_p, C.c_int, C.c_int, _D, _D]
         L.hxo_add_gap.argtypes = [C.c_void_p, C.c_int, C.c_int]
@@ -246,6 +247,11 @@ class OracleSim:
 
     def set(self, mech: str, var: str, idx: int, val: float):
         _check(lib().hxo_set_var(self.h, mech.encode(), var.encode(), idx, float(val)), f"set {mech}.{var}")
+
+    def vecstim_play(self, inst: int, times) -> None:
+        """VecStim.play(inst, times) at the current point of the run (vecevent.cpp:280-309)."""
+        tr = np.ascontiguousarray(np.asarray(times, np.float64).ravel())
+        _check(lib().hxo_vecstim_play(self.h, int(inst), tr.size, _dp(tr)), "vecstim_play")
 
     def array(self, mech: str, var: str) -> np.ndarray:
         n = self.spec.nnode if mech in ("global", "node") else self.spec.mechs[mech].n

@@ -1350,6 +1350,17 @@ int hxo_set_vecstim(void* h, int inst, int n, const double* times) {
     return 0;
 }
 
+// VecEvent::play -> update_sequence (vecevent.cpp:280-309): a call with no element
+// changes nothing; otherwise the instance's vector is replaced, and element() reads
+// it from the instance's current index on (from the first after finitialize).
+int hxo_vecstim_play(void* h, int inst, int n, const double* times) {
+    auto* m = static_cast<Model*>(h);
+    auto it = m->mechs.find("VecStim");
+    if (it == m->mechs.end() || inst < 0 || inst >= it->second->n) return -1;
+    if (n <= 0) return 0;
+    return hxo_set_vecstim(h, inst, n, times);
+}
+
 static int finalize_model(Model* m) {
     // mechanism lists in CoreNEURON type order
     m->current_list.clear(); m->state_ion_first.clear(); m->state_rest.clear(); m->postsyns.clear();

@@ -154,3 +154,71 @@ def test_adam_step_on_tied_groups(problem):
     g.adam_step(opt, lr, inv)
     _, mg2, _ = g.adam_state(opt, len(groups))
     assert np.allclose(mg2, 0.9 * mg, rtol=1e-14)
+
+
+def test_repeated_loss_node_matches_fd(problem):
+    """A node listed twice in the loss counts twice: soma 0 appears as loss columns 0 and
+    2 with different targets; the gradient matches the oracle's finite differences of the
+    same loss, and the loss the host reports."""
+    base, target, _, _, _ = problem
+    nodes = np.array([0, 1, 0])
+    tgt = np.stack([target[:, 0], target[:, 1], target[:, 0] + 0.7], axis=1)
+    nstep = target.shape[0]
+    g = Sim()
+    g.load_model_from_spec(base, add_monitors=False)
+    g.tape_begin(nstep)
+    g.finitialize(-65.0)
+    g.run(TSTOP)
+    loss = g.adjoint(nodes, tgt)
+    grad = g.gradient("hh", "gnabar")
+
+    def loss_rep(spec):
+        v = soma_trace(spec, TSTOP)[:, nodes]
+        return float(np.mean((v - tgt) ** 2))
+
+    assert abs(loss - loss_rep(base)) <= 1e-9 * abs(loss)
+    cell = base.cell_of_node()
+    hh = base.mechs["hh"]
+    for c in range(base.ncell):
+        mask = cell[hh.nodes] == c
+        adj = float(np.sum(hh.params["gnabar"][mask] * grad[mask]))
+        h = 1e-4
+        fd = (loss_rep(scaled(base, "hh", "gnabar", mask, 1 + h)) -
+              loss_rep(scaled(base, "hh", "gnabar", mask, 1 - h))) / (2 * h)
+        print(f"  repeated loss node, hh.gnabar cell {c}: adjoint {adj:.12e} fd {fd:.12e}", flush=True)
+        assert abs(adj - fd) <= REL_TOL * abs(fd), (adj, fd)
+
+
+def test_training_loop_holds_its_device_memory(problem):
+    """Twenty tape / run / adjoint / optimizer cycles after two warm-up cycles leave the
+    free device memory where it was: the per-call buffers are reused."""
+    import torch
+
+    base, target, _, _, _ = problem
+    nstep = target.shape[0]
+    g = Sim()
+    g.load_model_from_spec(base, add_monitors=False)
+    opt = g.adam_create(0.9, 0.999, 1e-8)
+    cell = base.cell_of_node()
+    hh = base.mechs["hh"]
+    for c in range(base.ncell):
+        g.adam_add_group(opt, "hh", "gnabar", np.nonzero(cell[hh.nodes] == c)[0], impedance=1.0)
+
+    def cycle():
+        g.tape_begin(nstep)
+        g.finitialize(-65.0)
+        g.run(TSTOP)
+        g.adjoint(np.arange(base.ncell), target)
+        g.adam_step(opt, 1e-6, 1.0)
+
+    cycle()
+    cycle()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(20):
+        cycle()
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    print(f"  free device memory before {free0} after {free1}", flush=True)
+    assert free1 == free0
+
