@@ -1130,6 +1130,13 @@ void Model::network_spike_receive() {         // simulate.cpp:916-939
                 Spike spk = ps.buffer.top();
                 if (spk.deliver_time > tt) break;
                 ps.buffer.pop();
+                // the reference's receive list holds one entry per instance (postsyn.cpp:79-81)
+                // and is written past its end when an instance receives several events in one
+                // pass (a VecStim whose elements fall due together); the list grows here
+                if (ps.receive_count == (int)ps.receive_idx.size()) {
+                    ps.receive_idx.resize(2 * ps.receive_idx.size());
+                    ps.receive_flag.resize(2 * ps.receive_flag.size(), -1);
+                }
                 ps.receive_idx[ps.receive_count] = (uint32_t)spk.syn_id;
                 ps.receive_flag[ps.receive_count] = spk.flag;
                 ps.receive_count++;

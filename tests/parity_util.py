@@ -1,4 +1,5 @@
 """Helpers for comparing the HIP path with the CPU oracle on the same model."""
+import ctypes
 import dataclasses
 
 import numpy as np
@@ -44,3 +45,14 @@ def compare_spikes(o, g, dt):
         if a.size:
             assert np.max(np.abs(a - b)) <= dt * 1.000001, f"gid {gid}: spike times differ by more than dt"
     return ot.size
+
+
+def device_free_bytes() -> int:
+    """Free device memory after the device has drained (hipDeviceSynchronize, hipMemGetInfo)
+    from the HIP runtime the library is linked against, already loaded in the process."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    assert hip.hipDeviceSynchronize() == 0
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return int(free.value)
+

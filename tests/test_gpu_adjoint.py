@@ -192,7 +192,7 @@ def test_repeated_loss_node_matches_fd(problem):
 def test_training_loop_holds_its_device_memory(problem):
     """Twenty tape / run / adjoint / optimizer cycles after two warm-up cycles leave the
     free device memory where it was: the per-call buffers are reused."""
-    import torch
+    from parity_util import device_free_bytes
 
     base, target, _, _, _ = problem
     nstep = target.shape[0]
@@ -213,12 +213,10 @@ def test_training_loop_holds_its_device_memory(problem):
 
     cycle()
     cycle()
-    torch.cuda.synchronize()
-    free0 = torch.cuda.mem_get_info()[0]
+    free0 = device_free_bytes()
     for _ in range(20):
         cycle()
-    torch.cuda.synchronize()
-    free1 = torch.cuda.mem_get_info()[0]
+    free1 = device_free_bytes()
     print(f"  free device memory before {free0} after {free1}", flush=True)
     assert free1 == free0
 

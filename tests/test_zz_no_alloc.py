@@ -95,23 +95,20 @@ def test_noalloc_replay_refuses_problems_beyond_its_scratch(sim):
 
 def test_noalloc_replay_allocates_nothing(sim):
     """After one call, further calls with other tick counts, with and without the precise
-    term and clipping, leave the free device memory unchanged (hipMemGetInfo through
-    torch).  The dense blocks are set before the measured region: setting them allocates."""
-    import torch
+    term and clipping, leave the free device memory unchanged (hipMemGetInfo).  The dense blocks are set before the measured region: setting them allocates."""
+    from parity_util import device_free_bytes
 
     N, T, blocks, sig, pre, po, pin, dL = problem(11, (48, 40), 5, 20)
     assert sim.set_dense_blocks_f32(blocks) == 5
     rc, _, _ = call(sim, "hx_replay_compute_dw_dx_from_signals_into_noalloc", N, T, sig, pre, po, pin, dL, True, 1e6)
     assert rc == 0, sim.last_error()
-    torch.cuda.synchronize()
-    free0 = torch.cuda.mem_get_info()[0]
+    free0 = device_free_bytes()
     for t_cut, percise, thr in [(T, True, 1e6), (T - 4, False, 0.5), (T - 11, True, 0.05), (T, False, 1e6)] * 3:
         sub = [x[:, :t_cut].copy() for x in sig]
         rc, dw, _ = call(sim, "hx_replay_compute_dw_dx_from_signals_into_noalloc", N, t_cut, sub, pre, po, pin,
                          dL[: t_cut - 1].copy(), percise, thr)
         assert rc == 0, sim.last_error()
         assert np.all(np.isfinite(dw))
-    torch.cuda.synchronize()
-    free1 = torch.cuda.mem_get_info()[0]
+    free1 = device_free_bytes()
     print(f"  free device memory before {free0} after {free1}", flush=True)
     assert free1 == free0
