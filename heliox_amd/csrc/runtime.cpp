@@ -2761,9 +2761,10 @@ void hx_sim::finitialize(double v_init) {
     mon_buf_fill = 0;
     for (auto& md : mon_data) md.clear();
     h5_written.assign(mon_data.size(), 0);     // the file keeps growing across finitialize
-    spikes.clear();
+    // the spike record keeps growing across finitialize, as the reference's rec_spikes and
+    // per-gid spk_output do (simulate.cpp:880, presyn.cpp:155; nothing clears them); a
+    // crossing found after the last step belongs to a step that is not taken now
     spikes_held.clear();
-    spk_by_gid.clear();
     const int nvp = static_cast<int>(vecplay.size());
     if (nvp) {
         launch_vecplay_reset(d_vecplay, nvp, stream);

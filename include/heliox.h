@@ -156,7 +156,10 @@ int hx_update_vecplay(hx_sim* sim, const char* mech, const char* var, int idx, i
 int hx_remove_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
 int hx_has_vecplay(hx_sim* sim, const char* mech, const char* var, int idx);
 
-/* ---- spikes (Simulate::output_spikes simulate.cpp:892-909, get_spk_by_gid) ---- */
+/* ---- spikes (Simulate::output_spikes simulate.cpp:892-909, get_spk_by_gid) ----
+ * The record (time, gid) of every threshold crossing since the model was loaded: like the
+ * reference's rec_spikes and per-gid spk_output (simulate.cpp:880, presyn.cpp:155), it is
+ * not cleared by finitialize. */
 int hx_get_spike_count(hx_sim* sim);
 int hx_get_spikes(hx_sim* sim, double* t, int* gid, int cap);
 /* Spikes of every NetStim since finitialize, ordered by time then instance: the

@@ -123,8 +123,9 @@ def test_play_between_runs_and_right_after_finitialize(gpu_lib):
     # element of the trains it holds, so those stay queued
     for sim in (o, g):
         sim.finitialize(-65.0)
-    play_all(lambda k, x: o.vecstim_play(k, x + 0.2), spec.n_vecstim, skip_empty_call=0)
-    play_all(lambda k, x: g.call_mech_func("VecStim", "play", k, x + 0.2), spec.n_vecstim, skip_empty_call=0)
+    play_all(lambda k, x: o.vecstim_play(k, np.asarray(x) + 0.2), spec.n_vecstim, skip_empty_call=0)
+    play_all(lambda k, x: g.call_mech_func("VecStim", "play", k, np.asarray(x) + 0.2), spec.n_vecstim,
+             skip_empty_call=0)
     for sim in (o, g):
         sim.continue_run(15.0)
     check(o, g, spec)
