@@ -176,6 +176,7 @@ struct SolveArgs {
     const double* a;
     const double* b;
     int store_dx;                 // 1: leave D in d and x = vn - v in rhs (as the reference does); 0: neither
+    int waves;                    // solve units per workgroup, one wavefront each (1..kSolveMaxWaves)
 };
 
 // Event ring: one slot per delivery step (mod nslot), fixed capacity per slot.
@@ -425,10 +426,18 @@ constexpr int kStageStride = kRoundMax + 1;
 // kUnitLdsBudget so that four units fit in a CU's 160 KB.
 constexpr int kSolveUnitTarget = 1024;
 constexpr size_t kUnitLdsBudget = 40 * 1024;
-inline size_t solve_lds_bytes(int max_chunks) {
+// A workgroup of the tree solve holds up to kSolveMaxWaves units, one wavefront each:
+// the CU spreads a workgroup's wavefronts over its four SIMDs, so four units in one
+// workgroup put one solve wavefront on each SIMD.
+constexpr int kSolveMaxWaves = 4;
+// LDS of one unit in doubles (junction pairs, then the stage), rounded to 16 bytes so
+// that every unit's pairs stay 16-byte aligned inside a multi-unit workgroup.
+__host__ __device__ inline int solve_lds_doubles(int max_chunks) {
     const int mc = max_chunks > 0 ? max_chunks : 1;
-    return static_cast<size_t>(mc) * 2 * sizeof(double) +
-           static_cast<size_t>(kStageArrays * kStageStride) * sizeof(double);
+    return (2 * mc + kStageArrays * kStageStride + 1) & ~1;
+}
+inline size_t solve_lds_bytes(int max_chunks) {
+    return static_cast<size_t>(solve_lds_doubles(max_chunks)) * sizeof(double);
 }
 
 // launch wrappers (kernels.hip)

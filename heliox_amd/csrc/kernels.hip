@@ -867,16 +867,20 @@ __device__ __forceinline__ void drain_vector_memory() { __builtin_amdgcn_s_waitc
 // trip solves two rounds and the buffers never trade registers.  Round indices
 // past either end are clamped to a real round, whose loads are issued but
 // never used.
+// A workgroup holds S.waves units, one wavefront each, with an LDS region each; there
+// is no workgroup barrier, so a wavefront whose unit finishes early just exits.
 template <int kX>
-__global__ void __launch_bounds__(kWave) k_solve(SolveArgs S, const RoundInfo* rounds_all, const uint2* desc,
-                                                 int max_chunks) {
+__global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve(SolveArgs S, const RoundInfo* rounds_all,
+                                                                  const uint2* desc, int max_chunks) {
     extern __shared__ double lds[];
-    const int c = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int c = blockIdx.x * S.waves + wv;
+    if (c >= S.nunit) return;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int rb = S.unit_round_begin[c];
     const int nround = S.unit_round_begin[c + 1] - rb;
     const int last = nround - 1;
-    double* slots = lds;
+    double* slots = lds + static_cast<size_t>(wv) * solve_lds_doubles(max_chunks);
     double* stage = slots + 2 * max_chunks;
     if (lane < kStageArrays) stage[lane * kStageStride + kNeutral] = lane == SA_DB ? 1.0 : 0.0;
     round_boundary();
@@ -1405,13 +1409,16 @@ void launch_set_v(double* v, int n, double val, hipStream_t s) {
 
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
     if (a.nunit <= 0) return;
-    const size_t lds = solve_lds_bytes(max_chunks);
+    SolveArgs b = a;
+    b.waves = std::min(std::max(a.waves, 1), kSolveMaxWaves);
+    const size_t lds = solve_lds_bytes(max_chunks) * b.waves;
+    const dim3 grid((a.nunit + b.waves - 1) / b.waves), block(kWave * b.waves);
     if (a.store_dx)
-        hipLaunchKernelGGL(k_solve<1>, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
-                           reinterpret_cast<const uint2*>(a.desc), max_chunks);
+        hipLaunchKernelGGL(k_solve<1>, grid, block, lds, s, b, b.rounds, reinterpret_cast<const uint2*>(b.desc),
+                           max_chunks);
     else
-        hipLaunchKernelGGL(k_solve<0>, dim3(a.nunit), dim3(kWave), lds, s, a, a.rounds,
-                           reinterpret_cast<const uint2*>(a.desc), max_chunks);
+        hipLaunchKernelGGL(k_solve<0>, grid, block, lds, s, b, b.rounds, reinterpret_cast<const uint2*>(b.desc),
+                           max_chunks);
 }
 
 void launch_spike(const SpikeArgs& a, hipStream_t s) {

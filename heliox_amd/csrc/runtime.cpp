@@ -322,6 +322,8 @@ struct hx_sim {
     int nunit = 0;
     int unit_cells = 1;                  // cells per unit of the current layout
     int unit_request = 0;                // 0: the library's choice
+    int solve_waves_request = 0;         // units per solve workgroup (0: the library's choice)
+    int solve_waves = 1;                 // in use (set at load)
     // the solver's tree (user node indices) and its coupling coefficients
     std::vector<int> solve_parent;
     std::vector<double> solve_a, solve_b;
@@ -1001,6 +1003,9 @@ void hx_sim::upload() {
             throw std::runtime_error("a solve unit has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
                                      " B solver schedule exceeds the " + std::to_string(prop.sharedMemPerBlock) +
                                      " B of LDS per workgroup");
+        // as many units per workgroup as asked (default kSolveMaxWaves) and the LDS allows
+        const int want = solve_waves_request > 0 ? solve_waves_request : kSolveMaxWaves;
+        solve_waves = std::max(1, std::min<int>(want, static_cast<int>(prop.sharedMemPerBlock / lds)));
     }
 
     // ion node -> device instance maps
@@ -2291,6 +2296,7 @@ void hx_sim::step_once_groups() {
         if (sample && cg.mon1 > cg.mon0)
             hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
         SolveArgs S{};
+        S.waves = solve_waves;
         S.nunit = cg.unit1 - cg.unit0;
         S.unit_node_begin = d_unit_node_begin + cg.unit0;
         S.unit_desc_begin = d_unit_desc_begin + cg.unit0;
@@ -2383,6 +2389,7 @@ void hx_sim::step_once() {
     launch_point_currents(tmid);
     launch_plugin_currents(tmid);
     SolveArgs S{};
+    S.waves = solve_waves;
     S.nunit = nunit;
     S.unit_node_begin = d_unit_node_begin;
     S.unit_desc_begin = d_unit_desc_begin;
@@ -3803,6 +3810,15 @@ int hx_set_solve_unit_cells(hx_sim* sim, int cells) {
     return 0;
 }
 
+int hx_set_solve_waves(hx_sim* sim, int waves) {
+    HX_SETTLE(sim);
+    if (sim->loaded) return sim->fail("set the solve units per workgroup before hx_load_model");
+    if (waves < 0 || waves > kSolveMaxWaves)
+        return sim->fail("solve units per workgroup must be 0..%d (0: the library's choice)", kSolveMaxWaves);
+    sim->solve_waves_request = waves;
+    return 0;
+}
+
 int hx_set_group_streams(hx_sim* sim, int enable) {
     HX_SETTLE(sim);
     sim->group_streams_allowed = enable != 0;
@@ -4047,6 +4063,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "solve_units") return sim->nunit;
     if (k == "handles") return static_cast<long long>(sim->handles.size());
     if (k == "solve_unit_cells") return sim->unit_cells;
+    if (k == "solve_waves") return sim->solve_waves;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
@@ -4344,6 +4361,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     sim->adj_fuse_bits = A.fuse_state | (A.fuse_cond << 8) | (A.fuse_param << 16) |
                          (static_cast<unsigned>(A.fold_syn) << 24) | ((d_lmap ? 1u : 0u) << 25);
     SolveArgs S{};
+    S.waves = sim->solve_waves;
     S.nunit = sim->nunit;
     S.unit_node_begin = sim->d_unit_node_begin;
     S.unit_desc_begin = sim->d_unit_desc_begin;

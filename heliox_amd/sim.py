@@ -137,6 +137,7 @@ SIGNATURES = {
     "hx_set_group_streams": (C.c_int, [_P, C.c_int]),
     "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
+    "hx_set_solve_waves": (C.c_int, [_P, C.c_int]),
     "hx_output_spikes": (C.c_int, [_P, C.c_char_p]),
     "hx_set_spike_output_enabled": (C.c_int, [_P, C.c_int]),
     "hx_is_spike_output_enabled": (C.c_int, [_P]),
@@ -1060,6 +1061,11 @@ class Sim:
         """Cells per solve unit (one wavefront each); 0 lets the library choose.  Call
         before loading the model; results do not depend on it."""
         self._chk(lib().hx_set_solve_unit_cells(self._h, int(cells)), "set_solve_unit_cells")
+
+    def set_solve_waves(self, waves: int) -> None:
+        """Solve units per workgroup (one wavefront each); 0 lets the library choose.  Call
+        before loading the model; results do not depend on it."""
+        self._chk(lib().hx_set_solve_waves(self._h, int(waves)), "set_solve_waves")
 
     def set_group_streams(self, enable: bool) -> None:
         """Allow the cell groups' own streams in the following runs (same results either way)."""

@@ -296,6 +296,11 @@ int hx_set_solver_root(hx_sim* sim, int centre);
  * wavefront per SIMD), fewer where a unit's schedule would exceed 40 KB of LDS.  Results
  * do not depend on it.  Call before hx_load_model. */
 int hx_set_solve_unit_cells(hx_sim* sim, int cells);
+/* Solve units per workgroup (no counterpart in the reference): the tree solve's workgroup
+ * holds this many units, one wavefront each, which the CU spreads over its SIMDs.  0
+ * (default): 4, fewer where their LDS would exceed a workgroup's.  Results do not depend
+ * on it.  Call before hx_load_model. */
+int hx_set_solve_waves(hx_sim* sim, int waves);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
