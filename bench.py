@@ -359,8 +359,20 @@ def calibrate_copy(gib: float = 1.0, reps: int = 5):
     e1.record()
     torch.cuda.synchronize()
     s = e0.elapsed_time(e1) / 1e3 / reps
-    print(json.dumps({"copy_bytes_read": n * 8, "copy_bytes_written": n * 8, "reps": reps + 1,
-                      "copy_GBps_read_plus_written": round(2 * n * 8 / s / 1e9, 1)}))
+    out = {"copy_bytes_read": n * 8, "copy_bytes_written": n * 8, "reps": reps + 1,
+           "copy_GBps_read_plus_written": round(2 * n * 8 / s / 1e9, 1)}
+    # the node kernel's own access mix through a streaming kernel of the library: one
+    # group launch's 5e6 compartments, 11 columns read and 9 written per compartment
+    # (160 B), and the same with every parameter column read (26 + 9, 280 B)
+    import ctypes
+    from heliox_amd import lib
+    for nr, nw in ((11, 9), (26, 9), (1, 1)):
+        n_el = 5000192 if nr > 1 else n
+        ms = ctypes.c_double()
+        if lib().hx_measure_stream(nr, nw, n_el, 20, ctypes.byref(ms)) == 0:
+            out[f"stream_{nr}r{nw}w_GBps"] = round((nr + nw) * 8 * n_el / (ms.value * 1e-3) / 1e9, 1)
+            out[f"stream_{nr}r{nw}w_us"] = round(ms.value * 1e3, 1)
+    print(json.dumps(out))
 
 
 def main():

@@ -448,6 +448,8 @@ void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s);
+// streaming probe (nread, nwrite) in {(1,1), (11,9), (26,9)}; false for other mixes
+bool launch_stream(int nread, int nwrite, const double* in, double* out, long long n, hipStream_t s);
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s);
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s);
 void launch_adj_loss(const double* v, const int* nodes, const int* begin, const int* idx, int n,

@@ -1421,6 +1421,33 @@ void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
                            max_chunks);
 }
 
+// Streaming ceiling of the node kernel's access mix: each thread reads R fp64 columns
+// and writes W at its index, with the node kernel's non-temporal hints.  A measurement
+// of what this GPU moves for that mix, not part of any step.
+template <int R, int W>
+__global__ void __launch_bounds__(kBlock) k_stream(const double* __restrict__ in, double* __restrict__ out,
+                                                   long long n) {
+    const long long i = static_cast<long long>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n) return;
+    double x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) x[r] = __builtin_nontemporal_load(in + r * n + i);
+    double acc = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc += x[r];
+#pragma unroll
+    for (int w = 0; w < W; ++w) __builtin_nontemporal_store(acc + w, out + w * n + i);
+}
+
+bool launch_stream(int nread, int nwrite, const double* in, double* out, long long n, hipStream_t s) {
+    const dim3 g(static_cast<unsigned>((n + kBlock - 1) / kBlock));
+    if (nread == 1 && nwrite == 1) hipLaunchKernelGGL((k_stream<1, 1>), g, dim3(kBlock), 0, s, in, out, n);
+    else if (nread == 11 && nwrite == 9) hipLaunchKernelGGL((k_stream<11, 9>), g, dim3(kBlock), 0, s, in, out, n);
+    else if (nread == 26 && nwrite == 9) hipLaunchKernelGGL((k_stream<26, 9>), g, dim3(kBlock), 0, s, in, out, n);
+    else return false;
+    return true;
+}
+
 void launch_spike(const SpikeArgs& a, hipStream_t s) {
     if (a.npre > 0) hipLaunchKernelGGL(k_spike, grid_for(a.npre), dim3(kBlock), 0, s, a);
 }

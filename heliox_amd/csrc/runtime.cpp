@@ -3851,6 +3851,31 @@ int hx_set_close_deferral(hx_sim* sim, int enable) {
 
 // The kernel timers are host state: these three neither read nor change the model, so
 // they leave a pending state update pending (a timed call then starts as every call does).
+int hx_measure_stream(int nread, int nwrite, long long n, int reps, double* ms) {
+    if (n <= 0 || reps <= 0 || !ms) return -1;
+    double *in = nullptr, *out = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = -1;
+    if (hipMalloc(&in, sizeof(double) * nread * n) == hipSuccess &&
+        hipMalloc(&out, sizeof(double) * nwrite * n) == hipSuccess &&
+        hipMemset(in, 0, sizeof(double) * nread * n) == hipSuccess && hipEventCreate(&e0) == hipSuccess &&
+        hipEventCreate(&e1) == hipSuccess && launch_stream(nread, nwrite, in, out, n, nullptr)) {
+        (void)hipEventRecord(e0, nullptr);
+        for (int k = 0; k < reps; ++k) launch_stream(nread, nwrite, in, out, n, nullptr);
+        (void)hipEventRecord(e1, nullptr);
+        float t = 0.f;
+        if (hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&t, e0, e1) == hipSuccess) {
+            *ms = static_cast<double>(t) / reps;
+            rc = 0;
+        }
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (in) (void)hipFree(in);
+    if (out) (void)hipFree(out);
+    return rc;
+}
+
 int hx_set_profiling(hx_sim* sim, int enable) {
     sim->profiling = enable != 0;
     sim->prof_mask = ~0u;

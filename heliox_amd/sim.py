@@ -103,6 +103,7 @@ SIGNATURES = {
     "hx_adam_step": (C.c_int, [_P, C.c_int, C.c_double, C.c_double]),
     "hx_adam_get_state": (C.c_int, [_P, C.c_int, C.POINTER(C.c_longlong), _D, _D, C.c_int]),
     "hx_get_kernel_time": (C.c_int, [_P, _S, _D, C.POINTER(C.c_longlong)]),
+    "hx_measure_stream": (C.c_int, [C.c_int, C.c_int, C.c_longlong, C.c_int, _D]),
     "hx_get_info": (C.c_longlong, [_P, _S]),
     "hx_emulate_tree_solve": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, _I, _I]),
     "hx_set_dense_blocks_f32": (C.c_int, [_P, C.c_int, C.POINTER(_F), _I, _I]),

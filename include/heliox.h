@@ -272,6 +272,13 @@ int hx_set_profiling(hx_sim* sim, int enable);
  * Fewer timed classes means fewer events on the stream, so less perturbation. */
 int hx_set_profiling_classes(hx_sim* sim, const char* classes);
 int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* launches);
+/* Measurement helper (no counterpart in the reference): the mean time in ms of `reps`
+ * launches of a streaming kernel that reads `nread` and writes `nwrite` fp64 arrays of n
+ * elements at each thread's index with non-temporal hints -- the practical HBM rate of the
+ * node kernel's access mix.  (nread, nwrite) is (1, 1), (11, 9) (the node kernel's config-3
+ * columns) or (26, 9) (the same with every parameter column read); anything else returns
+ * -1.  Allocates and frees its own arrays. */
+int hx_measure_stream(int nread, int nwrite, long long n, int reps, double* ms);
 /* Cell groups (no counterpart in the reference; an MI355X scheduling choice).  When
  * nothing couples cells across groups -- no detector-driven netcons, gaps or point
  * currents outside the node kernel, every density mechanism in the node kernel -- the
