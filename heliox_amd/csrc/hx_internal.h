@@ -108,6 +108,7 @@ struct StepArgs {
     double cfac;                  // 1e-3 * cj (capac.cpp:68-80)
     MechDev m[M_COUNT];
     unsigned dense_mask;          // mechanisms processed by the fused node kernel
+    int hh_owns_ions;             // sparse hh stores the na / k currents (the ion kernels do not run)
     int do_state;                 // finish the previous step's state update first
     int cadyn_skip;               // ... except CaDynamics_E2, already updated by the last current pass
     int cadyn_after;              // update CaDynamics_E2 right after this pass's ica (its state

@@ -341,8 +341,17 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
         const int ni = ion_index(m, 0, j), ki = ion_index(m, 1, j);
         double ina, ik;
         cur = hh_cur(A, m, j, v, hs, na.col(ION_EREV)[ni], kk.col(ION_EREV)[ki], g, ina, ik);
-        na.col(ION_CUR)[ni] += ina;
-        kk.col(ION_CUR)[ki] += ik;
+        if (A.hh_owns_ions) {         // the only writer of these currents: no ion kernel zeroed them
+            na.col(ION_CUR)[ni] = ina;
+            kk.col(ION_CUR)[ki] = ik;
+            if (A.write_dcurdv) {
+                na.col(ION_DCURDV)[ni] = 0.0;
+                kk.col(ION_DCURDV)[ki] = 0.0;
+            }
+        } else {
+            na.col(ION_CUR)[ni] += ina;
+            kk.col(ION_CUR)[ki] += ik;
+        }
     }
     if (MECH == M_CAHVA) {
         const int ci = ion_index(m, 2, j);

@@ -334,6 +334,7 @@ struct hx_sim {
     int ion_type_uniform[3] = {-1, -1, -1};
     unsigned dense_mask = 0;
     bool fused = false;
+    bool hh_owns_ions = false;           // sparse hh stores the na / k currents (see the layout)
     // CaDynamics_E2 updated by the current pass that computes its ica (see k_dense):
     // allowed when nothing samples calcium between the two passes
     bool cadyn_eager = false;
@@ -932,6 +933,21 @@ void hx_sim::build_layout() {
         if ((use & 4) && !mech[M_CA_ION].dense) ok = false;
         if (ok) dense_mask |= 1u << id;
         else m.dense = false;
+    }
+    // A sparse hh whose na and k currents no other mechanism adds to stores them itself
+    // instead of adding to currents the ion kernels zeroed, and the two ion launches are
+    // left out of the stepping current passes (with no 0100 style there is nothing else for
+    // them to do; ion instances without hh keep the 0 the finitialize pass stored).
+    {
+        auto plain_ion = [&](int id) {
+            const HostMech& m = mech[id];
+            if (!m.present || (dense_mask & (1u << id))) return false;
+            for (int t : m.iontype)
+                if (t & 0100) return false;
+            return true;
+        };
+        hh_owns_ions = mech[M_HH].present && mech[M_HH].n > 0 && !(dense_mask & (1u << M_HH)) &&
+                       plain_ion(M_NA_ION) && plain_ion(M_K_ION) && !(plugin_ions() & 3u);
     }
     recompute_fused();
 }
@@ -1893,6 +1909,7 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
         if (!uniform_on) A.m[id].umask = 0;
     }
     A.dense_mask = dense_mask;
+    A.hh_owns_ions = (hh_owns_ions && !init_pass) ? 1 : 0;
     A.do_state = do_state;
     A.cadyn_skip = do_state ? pass_cadyn_skip : 0;
     A.cadyn_after = do_current ? pass_cadyn_after : 0;
@@ -1987,14 +2004,20 @@ void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp
         launch_sparse(id, B, s);
     };
     tbegin(T_SPARSE, s);
+    // an ion's kernel only zeroes its current (and makes erev under style 0100): nothing
+    // to do in a state pass, nor in a stepping current pass when hh stores its ions
+    auto is_ion = [](int id) { return id == M_NA_ION || id == M_K_ION || id == M_CA_ION; };
     if (do_state && !do_current) {
         // ion writers first (simulate.cpp:822-834)
         if (mech[M_CADYN].present && !(dense_mask & (1u << M_CADYN))) sparse(M_CADYN);
         for (int id : kSparseOrder)
-            if (id != M_CADYN && mech[id].present && !(dense_mask & (1u << id))) sparse(id);
+            if (id != M_CADYN && !is_ion(id) && mech[id].present && !(dense_mask & (1u << id))) sparse(id);
     } else {
-        for (int id : kSparseOrder)
+        const bool skip_nak = hh_owns_ions && !init_pass;
+        for (int id : kSparseOrder) {
+            if (skip_nak && (id == M_NA_ION || id == M_K_ION)) continue;
             if (mech[id].present && !(dense_mask & (1u << id))) sparse(id);
+        }
     }
     tend(T_SPARSE, s);
 }
