@@ -126,6 +126,14 @@ struct StepArgs {
     MechConsts c;
 };
 
+// Nodes carrying IClamp or HalfGap instances (sorted), with each node's group of either
+// mechanism (MechDev::grp_node / grp_begin index) or -1: one launch adds both currents.
+struct PointUnion {
+    int n = 0;
+    const int* node = nullptr;
+    const int* grp[2] = {nullptr, nullptr};   // IClamp, HalfGap
+};
+
 // Chunked tree-solve schedule (one wavefront per solve unit: a few
 // consecutive cells solved as one forest).  Indices are relative to the unit
 // (units are limited to 65535 nodes and 65535 chunks), so a descriptor packs
@@ -445,6 +453,7 @@ inline size_t solve_lds_bytes(int max_chunks) {
 void launch_dense(const StepArgs& a, hipStream_t s);
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
+void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s);
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);

@@ -433,14 +433,11 @@ __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, 
 }
 
 template <int MECH>
-__global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
+__device__ __forceinline__ void point_group(const StepArgs& A, int q, double v, double mfact, double& rhs,
+                                            double& d) {
     const MechDev& m = A.m[MECH];
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= m.ngrp) return;
-    const int node = m.grp_node[q];
-    const double v = A.v[node];
-    const double mfact = 1.e2 / A.area[node];
-    double rhs = 0.0, d = 0.0;
+    rhs = 0.0;
+    d = 0.0;
     for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) {
         double i0, g;
         point_current<MECH>(A, m, j, v, i0, g, A.point_assigned);
@@ -454,8 +451,42 @@ __global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
             d += g;
         }
     }
+}
+
+template <int MECH>
+__global__ void __launch_bounds__(kBlock) k_point(StepArgs A) {
+    const MechDev& m = A.m[MECH];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= m.ngrp) return;
+    const int node = m.grp_node[q];
+    double rhs, d;
+    point_group<MECH>(A, q, A.v[node], 1.e2 / A.area[node], rhs, d);
     A.rhs[node] += rhs;
     A.d[node] += d;
+}
+
+// IClamp and HalfGap in one launch, one thread per node carrying either: the node's
+// IClamp sum is added to its rhs and d first, then its HalfGap sum, the additions the
+// two single-mechanism launches make one after the other (same bits).
+__global__ void __launch_bounds__(kBlock) k_point_electrodes(StepArgs A, PointUnion U) {
+    const int u = blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= U.n) return;
+    const int node = U.node[u];
+    const double v = A.v[node];
+    const double mfact = 1.e2 / A.area[node];
+    double r = A.rhs[node], dd = A.d[node], rhs, d;
+    if (U.grp[0][u] >= 0) {
+        point_group<M_ICLAMP>(A, U.grp[0][u], v, mfact, rhs, d);
+        r += rhs;
+        dd += d;
+    }
+    if (U.grp[1][u] >= 0) {
+        point_group<M_HALFGAP>(A, U.grp[1][u], v, mfact, rhs, d);
+        r += rhs;
+        dd += d;
+    }
+    A.rhs[node] = r;
+    A.d[node] = dd;
 }
 
 template <int MECH>
@@ -1385,6 +1416,10 @@ void launch_point_current(int mech, const StepArgs& a, hipStream_t s) {
         case M_HALFGAP: hipLaunchKernelGGL(k_point<M_HALFGAP>, grid_for(n), dim3(kBlock), 0, s, a); break;
         default: break;
     }
+}
+
+void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s) {
+    if (u.n > 0) hipLaunchKernelGGL(k_point_electrodes, grid_for(u.n), dim3(kBlock), 0, s, a, u);
 }
 
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s) {

@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <iterator>
 #include <functional>
 #include <cmath>
 #include <cstdarg>
@@ -335,6 +336,8 @@ struct hx_sim {
     unsigned dense_mask = 0;
     bool fused = false;
     bool hh_owns_ions = false;           // sparse hh stores the na / k currents (see the layout)
+    PointUnion point_union;              // IClamp / HalfGap nodes for the one-launch electrode currents
+    std::vector<int> point_grp_node[2];  // host copies of the IClamp / HalfGap group nodes
     // CaDynamics_E2 updated by the current pass that computes its ica (see k_dense):
     // allowed when nothing samples calcium between the two passes
     bool cadyn_eager = false;
@@ -981,6 +984,8 @@ void hx_sim::refresh_cadyn_eager() {
 }
 
 void hx_sim::upload() {
+    point_grp_node[0].clear();
+    point_grp_node[1].clear();
     const auto& R = registry();
     if (!stream) HXC(hipStreamCreate(&stream));
     auto perm_nodes = [&](const std::vector<double>& u) {
@@ -1022,6 +1027,25 @@ void hx_sim::upload() {
         // as many units per workgroup as asked (default kSolveMaxWaves) and the LDS allows
         const int want = solve_waves_request > 0 ? solve_waves_request : kSolveMaxWaves;
         solve_waves = std::max(1, std::min<int>(want, static_cast<int>(prop.sharedMemPerBlock / lds)));
+    }
+
+    // nodes carrying IClamp or HalfGap, with their group of each
+    point_union = PointUnion{};
+    if (!point_grp_node[0].empty() && !point_grp_node[1].empty()) {
+        std::vector<int> un;
+        std::set_union(point_grp_node[0].begin(), point_grp_node[0].end(), point_grp_node[1].begin(),
+                       point_grp_node[1].end(), std::back_inserter(un));
+        std::vector<int> g[2];
+        for (int x = 0; x < 2; ++x) {
+            g[x].assign(un.size(), -1);
+            const std::vector<int>& gn = point_grp_node[x];
+            for (size_t q = 0; q < gn.size(); ++q)
+                g[x][std::lower_bound(un.begin(), un.end(), gn[q]) - un.begin()] = static_cast<int>(q);
+        }
+        point_union.n = static_cast<int>(un.size());
+        point_union.node = dupload(owned, un);
+        point_union.grp[0] = dupload(owned, g[0]);
+        point_union.grp[1] = dupload(owned, g[1]);
     }
 
     // ion node -> device instance maps
@@ -1138,6 +1162,8 @@ void hx_sim::upload() {
             d.ngrp = static_cast<int>(gnode.size());
             d.grp_node = dupload(owned, gnode);
             d.grp_begin = dupload(owned, gbeg);
+            if (id == M_ICLAMP) point_grp_node[0] = gnode;
+            if (id == M_HALFGAP) point_grp_node[1] = gnode;
             if (id == M_EXPSYN || id == M_EXP2SYN) {
                 const int nblk = (nnode + kBlock - 1) / kBlock;
                 std::vector<int> bb(nblk + 1);
@@ -2029,8 +2055,15 @@ void hx_sim::launch_point_currents(double tcur) {
     for (int id : pts) any |= mech[id].present && mech[id].n > 0 && !(A.fold_mask & (1u << id));
     if (!any) return;
     tbegin(T_POINT);
-    for (int id : pts)   // synapse currents are added by the node kernel
-        if (mech[id].present && !(A.fold_mask & (1u << id))) launch_point_current(id, A, stream);
+    // IClamp and HalfGap in one launch when no synapse current comes between them
+    const bool pair = point_union.n > 0 && !(mech[M_EXPSYN].present && !(A.fold_mask & (1u << M_EXPSYN))) &&
+                      !(mech[M_EXP2SYN].present && !(A.fold_mask & (1u << M_EXP2SYN)));
+    if (pair) {
+        launch_point_electrodes(A, point_union, stream);
+    } else {
+        for (int id : pts)   // synapse currents are added by the node kernel
+            if (mech[id].present && !(A.fold_mask & (1u << id))) launch_point_current(id, A, stream);
+    }
     tend(T_POINT);
 }
 
