@@ -263,6 +263,33 @@ struct SpikeArgs {
     double half_dt;
 };
 
+struct VecPlayDev;
+
+// The work after a step's solve, one launch (k_after_solve); the launcher sets the
+// block offsets from the counts.  A task with no items gets no blocks.
+struct AfterSolve {
+    int b_ptr, b_spike, b_vp, b_es, b_e2;   // first block of each task (gap transfers from 0)
+    const double* v;
+    const int* gap_src;                     // gap transfers of the model: vgap[gap_inst[i]] = v[gap_src[i]]
+    double* vgap;
+    const int* gap_inst;
+    int ngap;
+    double* const* psrc;                    // transfers added at run time: *pdst[i] = *psrc[i]
+    double* const* pdst;
+    int nptr;
+    SpikeArgs S;                            // threshold detection of the next step (npre 0: none)
+    VecPlayDev* vp;                         // VecPlay at the step's end time (nvp 0: none)
+    int nvp;
+    double t;
+    double* es_g;                           // ExpSyn decay over instances [es0, es1)
+    const double* es_tau;
+    int es0, es1;
+    double *e2_a, *e2_b;                    // Exp2Syn decay over instances [e20, e21)
+    const double *e2_tau1, *e2_tau2;
+    int e20, e21;
+    double dt;
+};
+
 struct InputArgs {
     const double* eff_time;       // sorted effective VecStim event times
     const int* inst;              // VecStim instance of each event
@@ -454,6 +481,7 @@ void launch_dense(const StepArgs& a, hipStream_t s);
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s);
+void launch_after_solve(AfterSolve p, hipStream_t s);
 void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);

@@ -1006,8 +1006,8 @@ __device__ __forceinline__ void fan_out(const EventRing& R, const NsInbox& B, co
     else ring_push(R, m, target);
 }
 
-__global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// detector i (every lane of the wavefront takes part: the log slots are compacted per wave)
+__device__ __forceinline__ void spike_detect(const SpikeArgs& S, int i) {
     bool fire = false;
     if (i < S.npre) {
         const double vv = S.v[S.node[i]];
@@ -1038,6 +1038,8 @@ __global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) {
     for (int e = S.fo.begin[i]; e < S.fo.begin[i + 1]; ++e)
         fan_out(S.ring, S.ib, S.ttab, S.k, S.kmax, S.half_dt, S.t, 0, S.fo.target[e], S.fo.delay[e]);
 }
+
+__global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) { spike_detect(S, blockIdx.x * blockDim.x + threadIdx.x); }
 
 __global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
     int cur = *I.cursor;
@@ -1291,8 +1293,7 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
 // ---------------------------------------------------------------------------
 // VecPlay continuous playback (vecplay.cu:19-111)
 // ---------------------------------------------------------------------------
-__global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void vecplay_item(VecPlayDev* items, int n, double t, int do_play, int i) {
     if (i >= n) return;
     VecPlayDev it = items[i];
     const double* tv = it.tvec;
@@ -1326,6 +1327,41 @@ __global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
 store:
     *it.target = val;
     items[i] = it;
+}
+
+__global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
+    vecplay_item(items, n, t, do_play, blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// The work after a step's solve in one launch, each task on its own run of blocks:
+// gap transfers (the model's, then those added at run time), threshold detection of the
+// next step, VecPlay at the step's end time, and the synapses' state update.  The tasks
+// touch disjoint data (the host keeps VecPlay out of it unless every target is an IClamp
+// variable), so running them side by side gives the bits of the separate launches.
+__global__ void __launch_bounds__(kBlock) k_after_solve(AfterSolve P) {
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (b < P.b_ptr) {
+        const int i = b * kBlock + tid;
+        if (i < P.ngap) P.vgap[P.gap_inst[i]] = P.v[P.gap_src[i]];
+    } else if (b < P.b_spike) {
+        const int i = (b - P.b_ptr) * kBlock + tid;
+        if (i < P.nptr) *P.pdst[i] = *P.psrc[i];
+    } else if (b < P.b_vp) {
+        spike_detect(P.S, (b - P.b_spike) * kBlock + tid);
+    } else if (b < P.b_es) {
+        vecplay_item(P.vp, P.nvp, P.t, 0, (b - P.b_vp) * kBlock + tid);
+    } else if (b < P.b_e2) {
+        const int j = P.es0 + (b - P.b_es) * kBlock + tid;
+        if (j < P.es1) P.es_g[j] = expsyn_decay(P.es_g[j], P.es_tau[j], P.dt);
+    } else {
+        const int j = P.e20 + (b - P.b_e2) * kBlock + tid;
+        if (j < P.e21) {
+            const double aa = P.e2_a[j], bb = P.e2_b[j];
+            P.e2_a[j] = exp2syn_decay(aa, P.e2_tau1[j], P.dt);
+            P.e2_b[j] = exp2syn_decay(bb, P.e2_tau2[j], P.dt);
+        }
+    }
 }
 
 __global__ void k_vecplay_reset(VecPlayDev* items, int n) {
@@ -1416,6 +1452,17 @@ void launch_point_current(int mech, const StepArgs& a, hipStream_t s) {
         case M_HALFGAP: hipLaunchKernelGGL(k_point<M_HALFGAP>, grid_for(n), dim3(kBlock), 0, s, a); break;
         default: break;
     }
+}
+
+void launch_after_solve(AfterSolve p, hipStream_t s) {
+    auto nb = [](long long n) { return static_cast<int>(n > 0 ? (n + kBlock - 1) / kBlock : 0); };
+    p.b_ptr = nb(p.ngap);
+    p.b_spike = p.b_ptr + nb(p.nptr);
+    p.b_vp = p.b_spike + nb(p.S.npre);
+    p.b_es = p.b_vp + nb(p.nvp);
+    p.b_e2 = p.b_es + nb(p.es1 - p.es0);
+    const int end = p.b_e2 + nb(p.e21 - p.e20);
+    if (end > 0) hipLaunchKernelGGL(k_after_solve, dim3(end), dim3(kBlock), 0, s, p);
 }
 
 void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s) {

@@ -337,6 +337,10 @@ struct hx_sim {
     bool fused = false;
     bool hh_owns_ions = false;           // sparse hh stores the na / k currents (see the layout)
     PointUnion point_union;              // IClamp / HalfGap nodes for the one-launch electrode currents
+    bool vecplay_iclamp_only = true;     // every VecPlay target is an IClamp variable
+    AfterSolve after_solve_args(double tn, int knext, int grp) const;
+    SpikeArgs spike_args(int kk, double tk, int pre0, int pre1, const EventRing& ring) const;
+    void upload_gap_ptrs();
     std::vector<int> point_grp_node[2];  // host copies of the IClamp / HalfGap group nodes
     // CaDynamics_E2 updated by the current pass that computes its ica (see k_dense):
     // allowed when nothing samples calcium between the two passes
@@ -1734,6 +1738,8 @@ void hx_sim::upload_vecplay() {
         items.push_back(it);
     }
     d_vecplay = slot_upload(vecplay_slot, items);
+    vecplay_iclamp_only = true;
+    for (const auto& vp : vecplay) vecplay_iclamp_only = vecplay_iclamp_only && vp.mech == "IClamp";
     vecplay_dirty = false;
 }
 
@@ -2176,30 +2182,80 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     tend(T_EVENTS, on);
 }
 
-void hx_sim::launch_detect(int kk, double tk) {
-    if (npre == 0) return;
-    tbegin(T_SPIKE);
+// Threshold detection of detectors [pre0, pre1) at step kk (time tk), fanning out into
+// `ring` (detector netcons exist only with a single group).
+SpikeArgs hx_sim::spike_args(int kk, double tk, int pre0, int pre1, const EventRing& ring) const {
     SpikeArgs S{};
-    S.npre = npre;
+    S.npre = pre1 - pre0;
     S.v = d_v;
-    S.node = d_pre_node;
-    S.thr = d_pre_thr;
-    S.flag = d_pre_flag;
-    S.gid = d_pre_gid;
+    S.node = d_pre_node + pre0;
+    S.thr = d_pre_thr + pre0;
+    S.flag = d_pre_flag + pre0;
+    S.gid = d_pre_gid + pre0;
     S.t = tk;
     S.k = kk;
     S.log_t = d_spk_t;
     S.log_gid = d_spk_gid;
     S.log_count = d_spk_count;
     S.log_cap = spk_cap;
-    S.fo = FanOut{d_pre_fo_begin, d_pre_fo_target, d_pre_fo_delay};
-    S.ring = groups[0].ring;   // detector netcons exist only with a single group
+    S.fo = FanOut{d_pre_fo_begin + pre0, d_pre_fo_target, d_pre_fo_delay};
+    S.ring = ring;
     S.ib = nsa.ib;
     S.ttab = d_ttab;
     S.kmax = static_cast<int>(ttab.size()) - 1;
     S.half_dt = dt / 2;
-    launch_spike(S, stream);
+    return S;
+}
+
+void hx_sim::launch_detect(int kk, double tk) {
+    if (npre == 0) return;
+    tbegin(T_SPIKE);
+    launch_spike(spike_args(kk, tk, 0, npre, groups[0].ring), stream);
     tend(T_SPIKE);
+}
+
+// The work after the solve of the step ending at tn (the next step is knext), as one
+// launch: for cell group grp (its detectors and synapses; the groups have no gaps and no
+// VecPlay) or, with grp < 0, the whole model.
+AfterSolve hx_sim::after_solve_args(double tn, int knext, int grp) const {
+    AfterSolve P{};
+    P.v = d_v;
+    P.dt = dt;
+    P.t = tn;
+    if (grp < 0) {
+        if (static_gaps_on && !gaps.empty()) {
+            P.gap_src = d_gap_src;
+            P.gap_inst = d_gap_inst;
+            P.vgap = mech[M_HALFGAP].dev.col(HG_VGAP);
+            P.ngap = static_cast<int>(gaps.size());
+        }
+        P.psrc = d_dg_src;
+        P.pdst = d_dg_dst;
+        P.nptr = static_cast<int>(dg_src.size());
+        if (npre > 0) P.S = spike_args(knext, tn, 0, npre, groups[0].ring);
+        P.vp = d_vecplay;
+        P.nvp = static_cast<int>(vecplay.size());
+    } else {
+        const CellGroup& cg = groups[grp];
+        if (cg.pre1 > cg.pre0) P.S = spike_args(knext, tn, cg.pre0, cg.pre1, cg.ring);
+    }
+    const MechDev& es = mech[M_EXPSYN].dev;
+    if (mech[M_EXPSYN].present && es.n > 0) {
+        P.es_g = es.col(ES_G);
+        P.es_tau = es.col(ES_TAU);
+        P.es0 = grp < 0 ? 0 : groups[grp].es0;
+        P.es1 = grp < 0 ? es.n : groups[grp].es1;
+    }
+    const MechDev& e2 = mech[M_EXP2SYN].dev;
+    if (mech[M_EXP2SYN].present && e2.n > 0) {
+        P.e2_a = e2.col(E2_A);
+        P.e2_b = e2.col(E2_B);
+        P.e2_tau1 = e2.col(E2_TAU1);
+        P.e2_tau2 = e2.col(E2_TAU2);
+        P.e20 = grp < 0 ? 0 : groups[grp].e20;
+        P.e21 = grp < 0 ? e2.n : groups[grp].e21;
+    }
+    return P;
 }
 
 void hx_sim::launch_record() {
@@ -2300,16 +2356,20 @@ void hx_sim::tape_record() {
 void hx_sim::launch_gap_transfers() {
     const bool stat = static_gaps_on && !gaps.empty();
     if (!stat && dg_src.empty()) return;
-    if (dg_dirty) {
-        d_dg_src = dg_src.empty() ? nullptr : slot_upload(dg_src_slot, dg_src);
-        d_dg_dst = dg_dst.empty() ? nullptr : slot_upload(dg_dst_slot, dg_dst);
-        dg_dirty = false;
-    }
+    upload_gap_ptrs();
     tbegin(T_OTHER);
     if (stat)
         launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
     launch_copy_ptrs(d_dg_src, d_dg_dst, static_cast<int>(dg_src.size()), stream);
     tend(T_OTHER);
+}
+
+void hx_sim::upload_gap_ptrs() {
+    if (dg_dirty) {
+        d_dg_src = dg_src.empty() ? nullptr : slot_upload(dg_src_slot, dg_src);
+        d_dg_dst = dg_dst.empty() ? nullptr : slot_upload(dg_dst_slot, dg_dst);
+        dg_dirty = false;
+    }
 }
 
 bool hx_sim::want_multi_stream() const {
@@ -2328,7 +2388,6 @@ void hx_sim::step_once_groups() {
     tn += 0.5 * dt;
     const bool pending = state_pending;
     const bool sample = pending && !pending_sampled;   // a deferred call end sampled already
-    const StepArgs post = step_args(tn, 1, 0);
     const size_t nm = mon_ref.size();
     if (sample && nm && mon_buf_fill >= mon_buf_cap) throw std::runtime_error("monitor buffer exhausted");
     // the last step of a call with outputs on demand leaves calcium to the state update,
@@ -2369,40 +2428,10 @@ void hx_sim::step_once_groups() {
         tbegin(T_SOLVE, s);
         launch_solve(S, max_slots, s);
         tend(T_SOLVE, s);
-        if (cg.pre1 > cg.pre0) {
-            tbegin(T_SPIKE, s);
-            SpikeArgs P{};
-            P.npre = cg.pre1 - cg.pre0;
-            P.v = d_v;
-            P.node = d_pre_node + cg.pre0;
-            P.thr = d_pre_thr + cg.pre0;
-            P.flag = d_pre_flag + cg.pre0;
-            P.gid = d_pre_gid + cg.pre0;
-            P.t = tn;
-            P.k = k + 1;
-            P.log_t = d_spk_t;
-            P.log_gid = d_spk_gid;
-            P.log_count = d_spk_count;
-            P.log_cap = spk_cap;
-            P.fo = FanOut{d_pre_fo_begin + cg.pre0, d_pre_fo_target, d_pre_fo_delay};
-            P.ring = cg.ring;
-            P.ttab = d_ttab;
-            P.kmax = static_cast<int>(ttab.size()) - 1;
-            P.half_dt = dt / 2;
-            launch_spike(P, s);
-            tend(T_SPIKE, s);
-        }
-        if (mech[M_EXPSYN].present || mech[M_EXP2SYN].present) {
-            tbegin(T_POINT, s);
-            StepArgs D = post;
-            D.pt0 = cg.es0;
-            D.pt1 = cg.es1;
-            launch_point_state(M_EXPSYN, D, s);
-            D.pt0 = cg.e20;
-            D.pt1 = cg.e21;
-            launch_point_state(M_EXP2SYN, D, s);
-            tend(T_POINT, s);
-        }
+        // the group's detection of the next step and its synapses' decay, one launch
+        tbegin(T_SPIKE, s);
+        launch_after_solve(after_solve_args(tn, k + 1, g), s);
+        tend(T_SPIKE, s);
     }
     if (sample && nm) mon_buf_fill++;
     pending_sampled = false;
@@ -2463,21 +2492,35 @@ void hx_sim::step_once() {
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
     if (tape_on) tape_record();
-    launch_gap_transfers();
+    // gap transfers, detection of the next step (spike_deliver detects on v_{k}), VecPlay
+    // at the step's end and the synapses' decay: one launch when VecPlay writes only IClamp
+    // variables, which none of the others touch, and no transfer added at run time (which
+    // may name any variable) is in the step
+    const bool one_launch = (!has_vp || vecplay_iclamp_only) && dg_src.empty();
+    if (!one_launch) launch_gap_transfers();
     // t += dt/2 twice, exactly as the reference accumulates it
     double tn = tk;
     tn += 0.5 * dt;
     tn += 0.5 * dt;
     t = tn;
     k += 1;
-    launch_detect(k, t);              // spike_deliver of the next step detects on v_{k}
-    if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, t, 0, stream); tend(T_OTHER); }
-    StepArgs A = step_args(t, 1, 0);
-    if (mech[M_EXPSYN].present || mech[M_EXP2SYN].present) {
-        tbegin(T_POINT);
-        launch_point_state(M_EXPSYN, A, stream);
-        launch_point_state(M_EXP2SYN, A, stream);
-        tend(T_POINT);
+    if (one_launch) {
+        upload_gap_ptrs();
+        tbegin(T_SPIKE);
+        launch_after_solve(after_solve_args(t, k, -1), stream);
+        tend(T_SPIKE);
+    } else {
+        launch_detect(k, t);
+        tbegin(T_OTHER);
+        launch_vecplay(d_vecplay, nvp, t, 0, stream);
+        tend(T_OTHER);
+        StepArgs A = step_args(t, 1, 0);
+        if (mech[M_EXPSYN].present || mech[M_EXP2SYN].present) {
+            tbegin(T_POINT);
+            launch_point_state(M_EXPSYN, A, stream);
+            launch_point_state(M_EXP2SYN, A, stream);
+            tend(T_POINT);
+        }
     }
     launch_plugin_states(t);
     if (fused) {
