@@ -399,6 +399,13 @@ def main():
                     help="cell groups issued on separate streams (0: the library's choice, 1: one stream)")
     ap.add_argument("--unit-cells", type=int, default=0,
                     help="cells per tree-solve wavefront (0: the library's choice)")
+    ap.add_argument("--solve-waves", type=int, default=0,
+                    help="tree-solve wavefronts per workgroup (0: the library's choice)")
+    ap.add_argument("--no-group-turns", action="store_true",
+                    help="order the cell groups' node passes only on a run's first step (same results)")
+    ap.add_argument("--generic-node-kernel", action="store_true",
+                    help="run every node-kernel launch through the generic kernel (no compile-time "
+                         "steady-step instance; same results)")
     ap.add_argument("--model-root", action="store_true",
                     help="solve each cell toward its model root instead of its centre")
     ap.add_argument("--network", action="store_true", help="time the full-size config-4 network instead")
@@ -442,6 +449,12 @@ def main():
     sim.set_solver_root(not args.model_root)
     if args.unit_cells:
         sim.set_solve_unit_cells(args.unit_cells)
+    if args.solve_waves:
+        sim.set_solve_waves(args.solve_waves)
+    if args.generic_node_kernel:
+        sim.set_dense_steady(False)
+    if args.no_group_turns:
+        sim.set_group_turns(False)
     sim.load_model_from_spec(spec)
     t_build = time.perf_counter() - t_build
     groups = sim.info("cell_groups")

@@ -477,7 +477,9 @@ inline size_t solve_lds_bytes(int max_chunks) {
 }
 
 // launch wrappers (kernels.hip)
-void launch_dense(const StepArgs& a, hipStream_t s);
+// steady: a launch whose flags are a steady step of a mechanism set with a compile-time
+// instance runs that instance (same bits as the generic kernel); returns whether it did
+bool launch_dense(const StepArgs& a, hipStream_t s, bool steady);
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s);

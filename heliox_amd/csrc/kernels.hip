@@ -72,12 +72,15 @@ __device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) {
     return {lds_(m.col(CH_M) + j), lds_(m.col(CH_H) + j)};
 }
 
-__device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s) {
+// wr: also store the update's rates (minf, mtau, ...); wa: also store the current's
+// assigned outputs (i, ina, gna, ...).
+__device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s,
+                                            bool wr) {
     hh_gates_r(v, A.c.hh_q10, A.dt, s.m, s.h, s.n);
     sts_(m.col(HH_M) + j, s.m);
     sts_(m.col(HH_H) + j, s.h);
     sts_(m.col(HH_N) + j, s.n);
-    if (A.write_rates) {
+    if (wr) {
         double minf, mtau, hinf, htau, ninf, ntau;
         hh_rates(v, A.c.hh_q10, minf, mtau, hinf, htau, ninf, ntau);
         sts_(m.col(HH_MINF) + j, minf); sts_(m.col(HH_MTAU) + j, mtau);
@@ -88,11 +91,11 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
 }
 
 __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
-                                                  CaHVAState s, const double* ca_erev, int ci) {
+                                                  CaHVAState s, const double* ca_erev, int ci, bool wr) {
     cahva_gates_r(v, A.dt, s.m, s.h);
     sts_(m.col(CH_M) + j, s.m);
     sts_(m.col(CH_H) + j, s.h);
-    if (A.write_rates) {
+    if (wr) {
         double mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta;
         cahva_rates(v, mInf, mTau, mAlpha, mBeta, hInf, hTau, hAlpha, hBeta);
         sts_(m.col(CH_ECA) + j, ca_erev[ci]);
@@ -102,11 +105,11 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
     return s;
 }
 
-__device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l) {
+__device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l, bool wr) {
     const double vhalfl = ldp(m, HD_VHALFL, j), tau = ldp(m, HD_TAU, j);
     l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
     sts_(m.col(HD_L) + j, l);
-    if (A.write_rates) {
+    if (wr) {
         double linf, taul;
         hdla_rate(v, vhalfl, tau, A.c, linf, taul);
         sts_(m.col(HD_LINF) + j, linf); sts_(m.col(HD_TAUL) + j, taul);
@@ -126,18 +129,18 @@ __device__ __forceinline__ double cadyn_state(const StepArgs& A, const MechDev& 
 // (mech_template.cuh:616-626); ion currents of the I(v) evaluation are
 // returned for the caller to accumulate
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ double pas_cur(const StepArgs& A, const MechDev& m, int j, double v, double& g) {
+__device__ __forceinline__ double pas_cur(const MechDev& m, int j, double v, double& g, bool wa) {
     double gp = ldp(m, PAS_G, j), ep = ldp(m, PAS_E, j);
     double v1 = v + 0.001;
     double i1 = gp * (v1 - ep);
     double i0 = gp * (v - ep);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) sts_(m.col(PAS_I) + j, i0);
+    if (wa) sts_(m.col(PAS_I) + j, i0);
     return i0;
 }
 
-__device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, int j, double v, const HHState& s,
-                                         double ena, double ek, double& g, double& ina, double& ik) {
+__device__ __forceinline__ double hh_cur(const MechDev& m, int j, double v, const HHState& s, double ena, double ek,
+                                         double& g, double& ina, double& ik, bool wa) {
     double gnabar = ldp(m, HH_GNABAR, j), gkbar = ldp(m, HH_GKBAR, j);
     double gl = ldp(m, HH_GL, j), el = ldp(m, HH_EL, j);
     double gna, gk, il;
@@ -145,35 +148,35 @@ __device__ __forceinline__ double hh_cur(const StepArgs& A, const MechDev& m, in
     double i1 = hh_current(v1, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
     double i0 = hh_current(v, gnabar, gkbar, gl, el, s.m, s.h, s.n, ena, ek, gna, ina, gk, ik, il);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) {
+    if (wa) {
         sts_(m.col(HH_ENA) + j, ena); sts_(m.col(HH_EK) + j, ek); sts_(m.col(HH_INA) + j, ina); sts_(m.col(HH_IK) + j, ik);
         sts_(m.col(HH_IL) + j, il); sts_(m.col(HH_GNA) + j, gna); sts_(m.col(HH_GK) + j, gk);
     }
     return i0;
 }
 
-__device__ __forceinline__ double cahva_cur(const StepArgs& A, const MechDev& m, int j, double v,
-                                            const CaHVAState& s, double eca, double& g) {
+__device__ __forceinline__ double cahva_cur(const MechDev& m, int j, double v, const CaHVAState& s, double eca,
+                                            double& g, bool wa) {
     double gbar = ldp(m, CH_GBAR, j);
     double v1 = v + 0.001;
     double gg = gbar * s.m * s.m * s.h;
     double i1 = gg * (v1 - eca);
     double i0 = gg * (v - eca);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) {
+    if (wa) {
         sts_(m.col(CH_ECA) + j, eca); sts_(m.col(CH_G) + j, gg); sts_(m.col(CH_ICA) + j, i0); sts_(m.col(CH_IMECH) + j, i0);
     }
     return i0;
 }
 
 __device__ __forceinline__ double hdla_cur(const StepArgs& A, const MechDev& m, int j, double v, double l,
-                                           double& g) {
+                                           double& g, bool wa) {
     double ghd = ldp(m, HD_GHDBAR, j) * l;
     double v1 = v + 0.001;
     double i1 = ghd * (v1 - A.c.hd_ehd);
     double i0 = ghd * (v - A.c.hd_ehd);
     g = (i1 - i0) * 1000.0;   // / 0.001
-    if (A.write_assigned) { sts_(m.col(HD_GHD) + j, ghd); sts_(m.col(HD_I) + j, i0); }
+    if (wa) { sts_(m.col(HD_GHD) + j, ghd); sts_(m.col(HD_I) + j, i0); }
     return i0;
 }
 
@@ -200,19 +203,61 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
     return ldp(ion, ION_EREV, i);
 }
 
-__device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur) {
+__device__ __forceinline__ void dense_ion_store(const StepArgs& A, const MechDev& ion, int x, int i, double cur,
+                                                bool wdc) {
     if (A.ion_store & (1u << (2 * x))) sts_(ion.col(ION_CUR) + i, cur);
-    if (A.write_dcurdv) sts_(ion.col(ION_DCURDV) + i, 0.);
+    if (wdc) sts_(ion.col(ION_DCURDV) + i, 0.);
 }
-
-#define HAS(bit) (A.dense_mask & (1u << (bit)))
 
 // Point-process currents of one mechanism on the nodes of this block, summed
 // in instance order (instances are sorted by node).  s_first / s_last: LDS
 // tables of kBlock ints.  Every thread of the block must call it.
 template <int MECH>
 __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, double v, int* s_first,
-                                           int* s_last, double& rhs, double& d);
+                                           int* s_last, double& rhs, double& d, int store);
+
+// What one node-kernel launch does.  RtPass reads it from the launch's arguments;
+// SteadyPass<MASK, FOLD> fixes it at compile time for a steady step (the previous
+// step's state update and this step's currents, with CaDynamics_E2 updated right
+// after its ica, storing nothing but states, d and rhs), so that instance has no
+// branches on flags and the compiler schedules its loads and arithmetic freely.
+// Both run the same arithmetic in the same order: same bits.
+struct RtPass {
+    const StepArgs& A;
+    __device__ bool has(int b) const { return (A.dense_mask >> b) & 1u; }
+    __device__ bool folds(int b) const { return (A.fold_mask >> b) & 1u; }
+    __device__ bool do_state() const { return A.do_state != 0; }
+    __device__ bool do_current() const { return A.do_current != 0; }
+    __device__ bool cadyn_skip() const { return A.cadyn_skip != 0; }
+    __device__ bool cadyn_after() const { return A.cadyn_after != 0; }
+    __device__ bool write_assigned() const { return A.write_assigned != 0; }
+    __device__ bool write_rates() const { return A.write_rates != 0; }
+    __device__ bool write_dcurdv() const { return A.write_dcurdv != 0; }
+    __device__ int point_assigned() const { return A.point_assigned; }
+};
+
+template <unsigned MASK, unsigned FOLD>
+struct SteadyPass {
+    static constexpr bool has(int b) { return (MASK >> b) & 1u; }
+    static constexpr bool folds(int b) { return (FOLD >> b) & 1u; }
+    static constexpr bool do_state() { return true; }
+    static constexpr bool do_current() { return true; }
+    static constexpr bool cadyn_skip() { return has(M_CADYN); }
+    static constexpr bool cadyn_after() { return has(M_CADYN); }
+    static constexpr bool write_assigned() { return false; }
+    static constexpr bool write_rates() { return false; }
+    static constexpr bool write_dcurdv() { return false; }
+    static constexpr int point_assigned() { return 0; }
+};
+
+// Whether a launch's arguments are the steady step SteadyPass<MASK, FOLD> fixes.
+template <unsigned MASK, unsigned FOLD>
+bool is_steady(const StepArgs& a) {
+    const bool cd = (MASK >> M_CADYN) & 1u;
+    return a.dense_mask == MASK && a.fold_mask == FOLD && a.do_state && a.do_current &&
+           (a.cadyn_skip != 0) == cd && (a.cadyn_after != 0) == cd && !a.write_assigned && !a.write_rates &&
+           !a.write_dcurdv && !a.point_assigned;
+}
 
 // ---------------------------------------------------------------------------
 // fused node-parallel kernel for dense mechanisms: the previous step's state
@@ -221,8 +266,8 @@ __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, 
 // the block's nodes added in their place.  Ion currents are summed in
 // registers and each ion array is written once.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
-    __shared__ int s_first[kBlock], s_last[kBlock];
+template <class P>
+__device__ __forceinline__ void dense_node(const StepArgs& A, const P& p, int* s_first, int* s_last) {
     const int i = A.node0 + blockIdx.x * blockDim.x + threadIdx.x;
     const bool live = i < A.N;
     const double v = live ? A.v[i] : 0.0;
@@ -232,9 +277,10 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     HHState hs{};
     CaHVAState cs{};
     double hl = 0.0, cai = 0.0;
-    const bool have_cai = A.do_state && HAS(M_CADYN) && !A.cadyn_skip;
+    const bool have_cai = p.do_state() && p.has(M_CADYN) && !p.cadyn_skip();
+    const bool wr = p.write_rates(), wa = p.write_assigned();
     if (live) {
-        if (A.do_state) {
+        if (p.do_state()) {
             // every state load ahead of the first state store: a load written after a
             // store (which may alias it, as far as the compiler can tell) waits for it
             double* conci = ca.col(ION_CONCI);
@@ -245,37 +291,39 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
                 ci0 = lds_(conci + i);
                 ica0 = lds_(ca.col(ION_CUR) + i);
             }
-            if (HAS(M_HH)) h0 = hh_load(A.m[M_HH], i);
-            if (HAS(M_CAHVA)) c0 = cahva_load(A.m[M_CAHVA], i);
-            if (HAS(M_HDLA)) l0 = lds_(A.m[M_HDLA].col(HD_L) + i);
+            if (p.has(M_HH)) h0 = hh_load(A.m[M_HH], i);
+            if (p.has(M_CAHVA)) c0 = cahva_load(A.m[M_CAHVA], i);
+            if (p.has(M_HDLA)) l0 = lds_(A.m[M_HDLA].col(HD_L) + i);
             if (have_cai) {
                 cai = cadyn_state(A, A.m[M_CADYN], i, ci0, ica0);
                 sts_(conci + i, cai);
             }
-            if (HAS(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, h0);
-            if (HAS(M_CAHVA)) cs = cahva_state(A, A.m[M_CAHVA], i, v, c0, ca.col(ION_EREV), i);
-            if (HAS(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, l0);
-        } else if (A.do_current) {
-            if (HAS(M_HH)) hs = hh_load(A.m[M_HH], i);
-            if (HAS(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
-            if (HAS(M_HDLA)) hl = lds_(A.m[M_HDLA].col(HD_L) + i);
+            if (p.has(M_HH)) hs = hh_state(A, A.m[M_HH], i, v, h0, wr);
+            if (p.has(M_CAHVA)) cs = cahva_state(A, A.m[M_CAHVA], i, v, c0, ca.col(ION_EREV), i, wr);
+            if (p.has(M_HDLA)) hl = hdla_state(A, A.m[M_HDLA], i, v, l0, wr);
+        } else if (p.do_current()) {
+            if (p.has(M_HH)) hs = hh_load(A.m[M_HH], i);
+            if (p.has(M_CAHVA)) cs = cahva_load(A.m[M_CAHVA], i);
+            if (p.has(M_HDLA)) hl = lds_(A.m[M_HDLA].col(HD_L) + i);
         }
     }
-    if (!A.do_current) return;
+    if (!p.do_current()) return;
     // the capacitance term of the diagonal (capac.cpp:68-80) is added here,
     // ahead of the membrane conductances, so the solve reads one diagonal
     double rhs = 0.0, d = live ? A.cfac * (A.cm_uniform ? A.cm_value : A.cm[i]) : 0.0, g, cur;
     double prhs = 0.0, pd = 0.0;
-    if (A.fold_mask & (1u << M_EXPSYN)) fold_point<M_EXPSYN>(A, i, live, v, s_first, s_last, prhs, pd);
-    if (A.fold_mask & (1u << M_EXP2SYN)) fold_point<M_EXP2SYN>(A, i, live, v, s_first, s_last, prhs, pd);
+    if (p.folds(M_EXPSYN))
+        fold_point<M_EXPSYN>(A, i, live, v, s_first, s_last, prhs, pd, p.point_assigned());
+    if (p.folds(M_EXP2SYN))
+        fold_point<M_EXP2SYN>(A, i, live, v, s_first, s_last, prhs, pd, p.point_assigned());
     if (!live) return;
     double ena = 0.0, ek = 0.0, eca = 0.0, ina = 0.0, ik = 0.0, ica = 0.0;
-    if (HAS(M_PAS)) { cur = pas_cur(A, A.m[M_PAS], i, v, g); rhs -= cur; d += g; }
-    if (HAS(M_NA_ION)) ena = dense_ion_erev(A, na, 0, i, 1.0, false, 0.0);
-    if (HAS(M_K_ION)) ek = dense_ion_erev(A, kk, 1, i, 1.0, false, 0.0);
-    if (HAS(M_HH)) {
+    if (p.has(M_PAS)) { cur = pas_cur(A.m[M_PAS], i, v, g, wa); rhs -= cur; d += g; }
+    if (p.has(M_NA_ION)) ena = dense_ion_erev(A, na, 0, i, 1.0, false, 0.0);
+    if (p.has(M_K_ION)) ek = dense_ion_erev(A, kk, 1, i, 1.0, false, 0.0);
+    if (p.has(M_HH)) {
         double ina_h, ik_h;
-        cur = hh_cur(A, A.m[M_HH], i, v, hs, ena, ek, g, ina_h, ik_h);
+        cur = hh_cur(A.m[M_HH], i, v, hs, ena, ek, g, ina_h, ik_h, wa);
         ina += ina_h;
         ik += ik_h;
         rhs -= cur; d += g;
@@ -283,21 +331,33 @@ __global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
     rhs += prhs;   // ExpSyn, Exp2Syn (mechanism types 5, 6)
     d += pd;
     // cai for the Nernst potential and, when CaDynamics_E2 runs after this pass, for its update
-    const bool need_ci = HAS(M_CADYN) && A.cadyn_after;
+    const bool need_ci = p.has(M_CADYN) && p.cadyn_after();
     const double ci = have_cai ? cai : (need_ci ? lds_(ca.col(ION_CONCI) + i) : 0.0);
-    if (HAS(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai || need_ci, ci);
-    if (HAS(M_CAHVA)) {
-        cur = cahva_cur(A, A.m[M_CAHVA], i, v, cs, eca, g);
+    if (p.has(M_CA_ION)) eca = dense_ion_erev(A, ca, 2, i, 2.0, have_cai || need_ci, ci);
+    if (p.has(M_CAHVA)) {
+        cur = cahva_cur(A.m[M_CAHVA], i, v, cs, eca, g, wa);
         ica += cur;
         rhs -= cur; d += g;
     }
-    if (HAS(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, hl, g); rhs -= cur; d += g; }
+    if (p.has(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, hl, g, wa); rhs -= cur; d += g; }
     A.d[i] = d;
     A.rhs[i] = rhs;
-    if (HAS(M_NA_ION)) dense_ion_store(A, na, 0, i, ina);
-    if (HAS(M_K_ION)) dense_ion_store(A, kk, 1, i, ik);
-    if (HAS(M_CA_ION)) dense_ion_store(A, ca, 2, i, ica);
+    const bool wdc = p.write_dcurdv();
+    if (p.has(M_NA_ION)) dense_ion_store(A, na, 0, i, ina, wdc);
+    if (p.has(M_K_ION)) dense_ion_store(A, kk, 1, i, ik, wdc);
+    if (p.has(M_CA_ION)) dense_ion_store(A, ca, 2, i, ica, wdc);
     if (need_ci) sts_(ca.col(ION_CONCI) + i, cadyn_state(A, A.m[M_CADYN], i, ci, ica));
+}
+
+__global__ void __launch_bounds__(kBlock) k_dense(StepArgs A) {
+    __shared__ int s_first[kBlock], s_last[kBlock];
+    dense_node(A, RtPass{A}, s_first, s_last);
+}
+
+template <unsigned MASK, unsigned FOLD>
+__global__ void __launch_bounds__(kBlock) k_dense_steady(StepArgs A) {
+    __shared__ int s_first[kBlock], s_last[kBlock];
+    dense_node(A, SteadyPass<MASK, FOLD>{}, s_first, s_last);
 }
 
 // ---------------------------------------------------------------------------
@@ -326,9 +386,10 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
             double* conci = ca.col(ION_CONCI);
             conci[ci] = cadyn_state(A, m, j, conci[ci], ca.col(ION_CUR)[ci]);
         }
-        if (MECH == M_HH) hs = hh_state(A, m, j, v, hh_load(m, j));
-        if (MECH == M_CAHVA) cs = cahva_state(A, m, j, v, cahva_load(m, j), ca.col(ION_EREV), ion_index(m, 2, j));
-        if (MECH == M_HDLA) hl = hdla_state(A, m, j, v, m.col(HD_L)[j]);
+        if (MECH == M_HH) hs = hh_state(A, m, j, v, hh_load(m, j), A.write_rates);
+        if (MECH == M_CAHVA)
+            cs = cahva_state(A, m, j, v, cahva_load(m, j), ca.col(ION_EREV), ion_index(m, 2, j), A.write_rates);
+        if (MECH == M_HDLA) hl = hdla_state(A, m, j, v, m.col(HD_L)[j], A.write_rates);
     } else if (A.do_current) {
         if (MECH == M_HH) hs = hh_load(m, j);
         if (MECH == M_CAHVA) cs = cahva_load(m, j);
@@ -336,11 +397,11 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
     }
     if (!A.do_current || MECH == M_CADYN) return;
     double g = 0.0, cur = 0.0;
-    if (MECH == M_PAS) cur = pas_cur(A, m, j, v, g);
+    if (MECH == M_PAS) cur = pas_cur(m, j, v, g, A.write_assigned);
     if (MECH == M_HH) {
         const int ni = ion_index(m, 0, j), ki = ion_index(m, 1, j);
         double ina, ik;
-        cur = hh_cur(A, m, j, v, hs, na.col(ION_EREV)[ni], kk.col(ION_EREV)[ki], g, ina, ik);
+        cur = hh_cur(m, j, v, hs, na.col(ION_EREV)[ni], kk.col(ION_EREV)[ki], g, ina, ik, A.write_assigned);
         if (A.hh_owns_ions) {         // the only writer of these currents: no ion kernel zeroed them
             na.col(ION_CUR)[ni] = ina;
             kk.col(ION_CUR)[ki] = ik;
@@ -355,10 +416,10 @@ __global__ void __launch_bounds__(kBlock) k_sparse(StepArgs A) {
     }
     if (MECH == M_CAHVA) {
         const int ci = ion_index(m, 2, j);
-        cur = cahva_cur(A, m, j, v, cs, ca.col(ION_EREV)[ci], g);
+        cur = cahva_cur(m, j, v, cs, ca.col(ION_EREV)[ci], g, A.write_assigned);
         ca.col(ION_CUR)[ci] += cur;
     }
-    if (MECH == M_HDLA) cur = hdla_cur(A, m, j, v, hl, g);
+    if (MECH == M_HDLA) cur = hdla_cur(A, m, j, v, hl, g, A.write_assigned);
     A.rhs[node] -= cur;
     A.d[node] += g;
 }
@@ -404,7 +465,7 @@ __device__ __forceinline__ void point_current(const StepArgs& A, const MechDev& 
 
 template <int MECH>
 __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, double v, int* s_first,
-                                           int* s_last, double& rhs, double& d) {
+                                           int* s_last, double& rhs, double& d, int store) {
     const MechDev& m = A.m[MECH];
     const int b0 = A.node0 + blockIdx.x * kBlock;   // blk_begin covers the launch's blocks
     const int s0 = m.blk_begin[blockIdx.x], s1 = m.blk_begin[blockIdx.x + 1];
@@ -424,7 +485,7 @@ __device__ __forceinline__ void fold_point(const StepArgs& A, int i, bool live, 
         const double mfact = 1.e2 / A.area[i];
         for (int j = f; j < l; ++j) {
             double i0, g;
-            point_current<MECH>(A, m, j, v, i0, g, A.point_assigned);
+            point_current<MECH>(A, m, j, v, i0, g, store);
             rhs -= i0 * mfact;
             d += g * mfact;
         }
@@ -1421,9 +1482,39 @@ inline dim3 grid_for(long long n, int block = kBlock) {
 // ---------------------------------------------------------------------------
 // launch wrappers
 // ---------------------------------------------------------------------------
-void launch_dense(const StepArgs& a, hipStream_t s) {
-    if (a.N - a.node0 <= 0) return;
-    hipLaunchKernelGGL(k_dense, grid_for(a.N - a.node0), dim3(kBlock), 0, s, a);
+// Mechanism sets with a compile-time steady-step instance of the node kernel: every
+// density mechanism of the pyramidal-cell model (pas, hh, Ca_HVA, Ih, CaDynamics_E2 and
+// the three ions on every node) and pas alone (hh on part of the nodes runs
+// instance-parallel), each with the synapse folds a model may have.
+constexpr unsigned kMaskPyr = (1u << M_PAS) | (1u << M_NA_ION) | (1u << M_K_ION) | (1u << M_HH) |
+                              (1u << M_CA_ION) | (1u << M_CADYN) | (1u << M_CAHVA) | (1u << M_HDLA);
+constexpr unsigned kMaskPas = 1u << M_PAS;
+constexpr unsigned kFoldES = 1u << M_EXPSYN, kFoldE2 = 1u << M_EXP2SYN;
+
+template <unsigned MASK>
+bool launch_steady(const StepArgs& a, dim3 grid, hipStream_t s) {
+    for (unsigned fold : {0u, kFoldES, kFoldE2, kFoldES | kFoldE2}) {
+        if (fold == 0u && is_steady<MASK, 0u>(a))
+            hipLaunchKernelGGL((k_dense_steady<MASK, 0u>), grid, dim3(kBlock), 0, s, a);
+        else if (fold == kFoldES && is_steady<MASK, kFoldES>(a))
+            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldES>), grid, dim3(kBlock), 0, s, a);
+        else if (fold == kFoldE2 && is_steady<MASK, kFoldE2>(a))
+            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldE2>), grid, dim3(kBlock), 0, s, a);
+        else if (fold == (kFoldES | kFoldE2) && is_steady<MASK, kFoldES | kFoldE2>(a))
+            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldES | kFoldE2>), grid, dim3(kBlock), 0, s, a);
+        else
+            continue;
+        return true;
+    }
+    return false;
+}
+
+bool launch_dense(const StepArgs& a, hipStream_t s, bool steady) {
+    if (a.N - a.node0 <= 0) return false;
+    const dim3 grid = grid_for(a.N - a.node0);
+    if (steady && (launch_steady<kMaskPyr>(a, grid, s) || launch_steady<kMaskPas>(a, grid, s))) return true;
+    hipLaunchKernelGGL(k_dense, grid, dim3(kBlock), 0, s, a);
+    return false;
 }
 
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s) {

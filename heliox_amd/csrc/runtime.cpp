@@ -304,6 +304,8 @@ struct hx_sim {
     std::vector<VecPlayHost> vecplay;
     int event_cap_request = 0;
     int fusion_allowed = 1;
+    int dense_steady = 1;                      // compile-time node-kernel instances for steady steps
+    long long steady_launches = 0;             // node-kernel launches that ran such an instance
     int* d_syn_grp[2] = {nullptr, nullptr};   // adjoint: node -> ExpSyn / Exp2Syn group
     // adjoint loss: nodes and targets per call, the distinct nodes with their loss
     // indices (node -> first index of its list), and node -> loss index when distinct
@@ -421,6 +423,7 @@ struct hx_sim {
         int mon0 = 0, mon1 = 0;                   // monitor buffer columns of the group
         hipStream_t s = nullptr;
         hipEvent_t done = nullptr;
+        hipEvent_t pass = nullptr;                // this group's node pass of the latest step issued
     };
     std::vector<CellGroup> groups;                // one group unless the model decouples
     int group_request = 0;                        // hx_set_cell_groups (0: automatic)
@@ -432,6 +435,8 @@ struct hx_sim {
     hipEvent_t ev_stagger = nullptr;     // group g's first node pass of a run, awaited by group g+1
     bool stagger_next = false;           // the next grouped step starts the groups half a step apart
     int stagger_groups = 1;              // 0: all groups start together
+    int group_turns = 1;                 // hx_set_group_turns: the groups' node passes take turns
+    bool turns_prev = false;             // a grouped step of this run was issued (its passes are recorded)
     // time table
     std::vector<double> ttab;
     double* d_ttab = nullptr;
@@ -584,6 +589,7 @@ struct hx_sim {
         tape_free();
         for (auto& g : groups) {
             if (g.done) (void)hipEventDestroy(g.done);
+            if (g.pass) (void)hipEventDestroy(g.pass);
             if (g.s) (void)hipStreamDestroy(g.s);
         }
         if (ev_main) (void)hipEventDestroy(ev_main);
@@ -670,7 +676,9 @@ struct hx_sim {
     void launch_mech_pass(int do_state, int do_current, double tcur, int grp = -1, hipStream_t on = nullptr);
     void launch_point_currents(double tcur);
     void launch_events(int kk, double tk);
-    void launch_events_group(int g, int kk, double tk, hipStream_t on);
+    // parts: kEvInputs (VecStim inputs, NetStims) and / or kEvDeliver (delivery)
+    static constexpr unsigned kEvInputs = 1u, kEvDeliver = 2u;
+    void launch_events_group(int g, int kk, double tk, hipStream_t on, unsigned parts = kEvInputs | kEvDeliver);
     void launch_detect(int kk, double tk);
     void launch_record();
     void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
@@ -1392,6 +1400,7 @@ void hx_sim::upload() {
 void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt) {
     for (auto& g : groups) {
         if (g.done) (void)hipEventDestroy(g.done);
+        if (g.pass) (void)hipEventDestroy(g.pass);
         if (g.s) (void)hipStreamDestroy(g.s);
     }
     groups.clear();
@@ -1486,6 +1495,7 @@ void hx_sim::build_groups(const std::vector<std::vector<std::pair<int, double>>>
         if (G > 1) {
             HXC(hipStreamCreate(&cg.s));
             HXC(hipEventCreateWithFlags(&cg.done, hipEventDisableTiming));
+            HXC(hipEventCreateWithFlags(&cg.pass, hipEventDisableTiming));
         }
     }
     {
@@ -2019,9 +2029,9 @@ void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp
     }
     tbegin(T_MECH, s);
     if (do_current) {
-        launch_dense(A, s);
+        steady_launches += launch_dense(A, s, dense_steady != 0);
     } else if (dense_mask) {
-        launch_dense(A, s);
+        steady_launches += launch_dense(A, s, dense_steady != 0);
     }
     tend(T_MECH, s);
     bool any_sparse = false;
@@ -2115,14 +2125,15 @@ void hx_sim::launch_events(int kk, double tk) {
     for (int g = 0; g < static_cast<int>(groups.size()); ++g) launch_events_group(g, kk, tk, stream);
 }
 
-// VecStim input and delivery of step kk for one cell group's synapses.
-void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
+// VecStim input and delivery of step kk for one cell group's synapses (parts: the
+// inputs and NetStims, the delivery, or both, issued in that order).
+void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, unsigned parts) {
     const bool psyn = has_postsyn_plugins();
     const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present || psyn;
     if (!syn && nsa.n == 0) return;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
-    if (cg.n_in > 0) {
+    if ((parts & kEvInputs) && cg.n_in > 0) {
         InputArgs I{};
         I.eff_time = cg.d_in_time;
         I.inst = cg.d_in_inst;
@@ -2140,7 +2151,7 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
         I.half_dt = dt / 2;
         launch_input(I, on);
     }
-    if (nsa.n > 0) {                 // NetStims receiving events: one group, the main stream
+    if ((parts & kEvInputs) && nsa.n > 0) {   // NetStims receiving events: one group, the main stream
         NsArgs A = nsa;
         A.ring = cg.ring;
         A.ttab = d_ttab;
@@ -2150,7 +2161,7 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
         A.k = kk;
         launch_netstim(A, on);
     }
-    if (!syn) {
+    if (!syn || !(parts & kEvDeliver)) {
         tend(T_EVENTS, on);
         return;
     }
@@ -2398,18 +2409,37 @@ void hx_sim::step_once_groups() {
     // First step of a run: each group starts once the previous group's node pass is
     // done, so from then on one group's tree solve (latency-bound) runs beside the
     // other's node pass (HBM-bound) instead of two node passes and then two solves
-    // running together.  The ordering is through events only: results are unchanged.
-    const bool stagger = stagger_next;
+    // running together.  With turns (the default) every step keeps that order: a
+    // group's step waits for the previous group's node pass (group 0 for the last
+    // group's pass of the step before).  The wait sits ahead of the group's event
+    // kernels, so when a node pass ends, its group's solve (the next launch on that
+    // stream) is dispatched before the next group's node pass, which otherwise fills
+    // every CU first and leaves the solve's workgroups waiting for room.  The ordering
+    // is through events only: results are unchanged.
+    const bool turns = group_turns != 0;
+    const bool stagger = stagger_next && !turns;
     stagger_next = false;
-    for (int g = 0; g < static_cast<int>(groups.size()); ++g) {
+    const int G = static_cast<int>(groups.size());
+    for (int g = 0; g < G; ++g) {
         CellGroup& cg = groups[g];
         hipStream_t s = cg.s;
-        if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
-        launch_events_group(g, k, tk, s);
+        if (turns) {
+            // the inputs do not touch the other groups: they run during the previous
+            // group's node pass; the delivery after the wait keeps this group's node pass
+            // a few microseconds behind the previous group's solve launch
+            launch_events_group(g, k, tk, s, kEvInputs);
+            if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass, 0));
+            else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass, 0));
+            launch_events_group(g, k, tk, s, kEvDeliver);
+        } else {
+            if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
+            launch_events_group(g, k, tk, s);
+        }
         launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
-        if (stagger && g + 1 < static_cast<int>(groups.size())) HXC(hipEventRecord(ev_stagger, s));
+        if (stagger && g + 1 < G) HXC(hipEventRecord(ev_stagger, s));
         if (sample && cg.mon1 > cg.mon0)
             hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
+        if (turns) HXC(hipEventRecord(cg.pass, s));
         SolveArgs S{};
         S.waves = solve_waves;
         S.nunit = cg.unit1 - cg.unit0;
@@ -2433,6 +2463,7 @@ void hx_sim::step_once_groups() {
         launch_after_solve(after_solve_args(tn, k + 1, g), s);
         tend(T_SPIKE, s);
     }
+    turns_prev = turns;
     if (sample && nm) mon_buf_fill++;
     pending_sampled = false;
     cadyn_done = eager;
@@ -2597,7 +2628,7 @@ void hx_sim::launch_outputs_pass() {
     A.fold_mask = 0;
     A.point_assigned = 0;
     tbegin(T_MECH);
-    launch_dense(A, stream);
+    launch_dense(A, stream, dense_steady != 0);
     tend(T_MECH);
     outputs_pending = false;
 }
@@ -2751,6 +2782,7 @@ int hx_sim::run_steps(int nstep) {
         HXC(hipEventRecord(ev_main, stream));
         for (auto& cg : groups) HXC(hipStreamWaitEvent(cg.s, ev_main, 0));
         stagger_next = stagger_groups != 0;
+        turns_prev = false;
     }
     try {
         for (int s = 0; s < nstep; ++s) {
@@ -3942,6 +3974,18 @@ int hx_set_fusion(hx_sim* sim, int enable) {
     return 0;
 }
 
+int hx_set_group_turns(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
+    sim->group_turns = enable ? 1 : 0;
+    return 0;
+}
+
+int hx_set_dense_steady(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
+    sim->dense_steady = enable ? 1 : 0;
+    return 0;
+}
+
 int hx_set_close_deferral(hx_sim* sim, int enable) {
     HX_SETTLE(sim);
     sim->close_deferral = enable != 0;
@@ -4181,6 +4225,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "nchunk_max") return sim->max_slots;
     if (k == "nround_max") return sim->max_rounds;
     if (k == "dense_mask") return sim->dense_mask;
+    if (k == "steady_launches") return sim->steady_launches;
     if (k == "fused") return sim->fused ? 1 : 0;
     if (k == "adjoint_fused") return sim->adj_fuse_bits;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());

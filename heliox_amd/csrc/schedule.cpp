@@ -8,16 +8,17 @@
 // issues the same instructions however many of its lanes have a chunk, a
 // unit of several cells costs little more per round than one cell.  Each
 // tree is cut into chunks: unbranched runs of at most kChunk nodes (a node
-// with exactly one child continues its chunk).  A chunk's height is 0 for a leaf chunk and
-// 1 + the largest child height otherwise; chunks of equal height are
-// independent, so they form rounds of up to 64 lanes.  Elimination walks the
-// rounds by increasing height, back substitution by decreasing height, with a
-// barrier between rounds.  Chunk ids are breadth-first so that the chunks
-// hanging off one tail are consecutive LDS slots.  Each round is stored
-// position-major (see below) so its lanes access memory coalesced.
+// with exactly one child continues its chunk).  A round is a set of chunks
+// none of which hangs below another, up to 64 lanes; elimination walks the
+// rounds from the leaves in, each chunk after every chunk hanging off its
+// tail, and back substitution walks them out, with a barrier between rounds.
+// Chunk ids are breadth-first so that the chunks hanging off one tail are
+// consecutive LDS slots.  Each round is stored position-major (see below) so
+// its lanes access memory coalesced.
 #include <algorithm>
 #include <cstdint>
 #include <numeric>
+#include <queue>
 #include <stdexcept>
 #include <vector>
 
@@ -71,35 +72,51 @@ void build_unit_schedule(const std::vector<int>& forest_parent, int chunk_max, i
             chunks.push_back({clist[e], 0, static_cast<int>(q), 0, 0, {}});
     }
     const int nchunk = static_cast<int>(chunks.size());
-    std::vector<int> height(nchunk, 0);
-    for (int q = nchunk - 1; q >= 0; --q) {
-        int h = 0;
-        for (int c = 0; c < chunks[q].child_count; ++c) h = std::max(h, height[chunks[q].child_begin + c] + 1);
-        height[q] = h;
-    }
-    int hmax = 0;
-    for (int q = 0; q < static_cast<int>(roots.size()); ++q) hmax = std::max(hmax, height[q]);
-    std::vector<std::vector<int>> by_h(hmax + 1);
-    for (int q = 0; q < nchunk; ++q) by_h[height[q]].push_back(q);
-    // back-substitution order: root height first; within a height, longest chunks first
+    // Rounds by list scheduling, in elimination order: a chunk is ready once every
+    // chunk hanging off its tail is in an earlier round, and each round takes ready
+    // chunks deepest first (most chunk ancestors: the longest chain still ahead of it
+    // toward its root), up to `lanes` chunks and `round_max` nodes.  A chunk that would
+    // pass the node bound waits for the next round while shallower ones may still fill
+    // this one.  (Grouping chunks by height instead leaves the narrow rounds near the
+    // roots half empty: config 3, two cells, 47 -> 33 rounds.)  Which round a chunk
+    // lands in changes no arithmetic: its inputs, its children's terms (read from
+    // their slots in breadth-first order) and its results are the same.
+    std::vector<int> depth(nchunk, 0);
+    for (int q = 0; q < nchunk; ++q) depth[q] = chunks[q].parent < 0 ? 0 : depth[chunks[q].parent] + 1;
+    std::vector<int> waiting(nchunk);
+    for (int q = 0; q < nchunk; ++q) waiting[q] = chunks[q].child_count;
+    auto later = [&](int x, int y) { return depth[x] != depth[y] ? depth[x] < depth[y] : x > y; };
+    std::priority_queue<int, std::vector<int>, decltype(later)> ready(later);
+    for (int q = 0; q < nchunk; ++q)
+        if (waiting[q] == 0) ready.push(q);
     std::vector<std::vector<int>> rounds;
-    for (int h = hmax; h >= 0; --h) {
-        auto& v = by_h[h];
-        std::stable_sort(v.begin(), v.end(), [&](int x, int y) { return chunks[x].len > chunks[y].len; });
-        // a round holds at most `lanes` chunks and `round_max` nodes (one LDS stage)
-        std::vector<int> cur;
+    int placed = 0;
+    while (placed < nchunk) {
+        std::vector<int> cur, held;
         int nodes = 0;
-        for (int q : v) {
-            if (!cur.empty() && (static_cast<int>(cur.size()) == lanes || nodes + chunks[q].len > round_max)) {
-                rounds.push_back(cur);
-                cur.clear();
-                nodes = 0;
+        while (!ready.empty() && static_cast<int>(cur.size()) < lanes && nodes < round_max) {
+            const int q = ready.top();
+            ready.pop();
+            if (nodes + chunks[q].len > round_max) {
+                held.push_back(q);
+                continue;
             }
             cur.push_back(q);
             nodes += chunks[q].len;
         }
-        if (!cur.empty()) rounds.push_back(cur);
+        for (int q : held) ready.push(q);
+        if (cur.empty()) throw std::runtime_error("solver schedule: no chunk fits a round");
+        for (int q : cur) {
+            const int p = chunks[q].parent;
+            if (p >= 0 && --waiting[p] == 0) ready.push(p);
+        }
+        placed += static_cast<int>(cur.size());
+        // position-major storage below wants a round's chunks longest first
+        std::stable_sort(cur.begin(), cur.end(), [&](int x, int y) { return chunks[x].len > chunks[y].len; });
+        rounds.push_back(cur);
     }
+    // back-substitution order (roots first), the order the rounds are stored in
+    std::reverse(rounds.begin(), rounds.end());
     // solver order of the unit's nodes.  Inside a round the chunks are sorted by
     // length (longest first) and stored position-major: node k of every chunk
     // that has one, then node k+1, ...  Node k of lane l sits at

@@ -90,6 +90,8 @@ SIGNATURES = {
     "hx_get_spk_by_gid": (C.c_int, [_P, C.c_int, _D, C.c_int]),
     "hx_set_event_capacity": (C.c_int, [_P, C.c_int]),
     "hx_set_fusion": (C.c_int, [_P, C.c_int]),
+    "hx_set_dense_steady": (C.c_int, [_P, C.c_int]),
+    "hx_set_group_turns": (C.c_int, [_P, C.c_int]),
     "hx_set_close_deferral": (C.c_int, [_P, C.c_int]),
     "hx_set_uniform_columns": (C.c_int, [_P, C.c_int]),
     "hx_set_profiling": (C.c_int, [_P, C.c_int]),
@@ -321,6 +323,16 @@ class Sim:
 
     def set_fusion(self, enable: bool) -> int:
         return self._rc(lib().hx_set_fusion(self._h, 1 if enable else 0))
+
+    def set_group_turns(self, enable: bool) -> int:
+        """Make the cell groups' node passes take turns on every step (default on; same
+        results either way)."""
+        return self._rc(lib().hx_set_group_turns(self._h, 1 if enable else 0))
+
+    def set_dense_steady(self, enable: bool) -> int:
+        """Run steady node-kernel steps through their compile-time instance (default on;
+        same results either way)."""
+        return self._rc(lib().hx_set_dense_steady(self._h, 1 if enable else 0))
 
     def set_close_deferral(self, enable: bool) -> int:
         return self._rc(lib().hx_set_close_deferral(self._h, 1 if enable else 0))

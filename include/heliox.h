@@ -249,6 +249,11 @@ int hx_set_event_capacity(hx_sim* sim, int per_step);
 /* enable = 1 (default): fold each step's state update into the next step's current pass when that is
  * exact; 0: always run the reference's separate current and state passes. */
 int hx_set_fusion(hx_sim* sim, int enable);
+/* No reference counterpart.  enable = 1 (default): a node-kernel launch of a steady step (state
+ * update and currents, nothing stored but states, d and rhs) whose dense mechanism set has a
+ * compile-time instance (pas, hh, Ca_HVA, Ih, CaDynamics_E2 and the three ions on every node;
+ * pas alone) runs that instance; 0: always the generic kernel.  Same bits either way. */
+int hx_set_dense_steady(hx_sim* sim, int enable);
 /* No reference counterpart.  enable = 1 (default): hx_run, hx_continue_run and hx_fadvance may
  * return with their last step's state update (nrn_state) still pending when no monitor, tape or
  * signal capture samples the states; the next stepping call's first node pass applies it, as every
@@ -311,13 +316,19 @@ int hx_set_solve_waves(hx_sim* sim, int waves);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
+/* No reference counterpart.  enable = 1 (default): with the cell groups on their own streams,
+ * every step's node passes take turns (group g waits for group g-1's node pass, group 0 for the
+ * last group's pass of the step before), so each group's tree solve runs beside the next group's
+ * node pass; 0: only a run's first step is ordered that way.  Same results either way. */
+int hx_set_group_turns(hx_sim* sim, int enable);
 /* Layout facts: "nnode", "ncell", "nchunk_max", "nround_max", "dense_mask", "fused",
  * "cell_groups", "multi_stream" (1 if the last run used per-group streams), "state_pending"
  * (1 while the last stepping call's state update waits, see hx_set_close_deferral),
  * "outputs_pending" (1 while its node-kernel outputs wait), "adjoint_fused" (the mechanisms the
  * last hx_adjoint ran in its node-parallel kernels: bits 0-7 gate adjoints, 8-15 conductances,
  * 16-23 parameter terms; bit 0 pas, 1 hh, 2 Ca_HVA, 3 hd_la, 4 CaDynamics_E2; bit 24: the synapses
- * too; bit 25: the loss term too). */
+ * too; bit 25: the loss term too), "steady_launches" (node-kernel launches so far that ran a
+ * compile-time steady-step instance, see hx_set_dense_steady). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the
