@@ -74,9 +74,8 @@ __device__ __forceinline__ CaHVAState cahva_load(const MechDev& m, int j) {
 
 // wr: also store the update's rates (minf, mtau, ...); wa: also store the current's
 // assigned outputs (i, ina, gna, ...).
-__device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s,
-                                            bool wr) {
-    hh_gates_r(v, A.c.hh_q10, A.dt, s.m, s.h, s.n);
+__device__ __forceinline__ void hh_store(const StepArgs& A, const MechDev& m, int j, double v, const HHState& s,
+                                         bool wr) {
     sts_(m.col(HH_M) + j, s.m);
     sts_(m.col(HH_H) + j, s.h);
     sts_(m.col(HH_N) + j, s.n);
@@ -87,12 +86,16 @@ __device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m,
         sts_(m.col(HH_HINF) + j, hinf); sts_(m.col(HH_HTAU) + j, htau);
         sts_(m.col(HH_NINF) + j, ninf); sts_(m.col(HH_NTAU) + j, ntau);
     }
+}
+__device__ __forceinline__ HHState hh_state(const StepArgs& A, const MechDev& m, int j, double v, HHState s,
+                                            bool wr) {
+    hh_gates_r(v, A.c.hh_q10, A.dt, s.m, s.h, s.n);
+    hh_store(A, m, j, v, s, wr);
     return s;
 }
 
-__device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
-                                                  CaHVAState s, const double* ca_erev, int ci, bool wr) {
-    cahva_gates_r(v, A.dt, s.m, s.h);
+__device__ __forceinline__ void cahva_store(const MechDev& m, int j, double v, const CaHVAState& s,
+                                            const double* ca_erev, int ci, bool wr) {
     sts_(m.col(CH_M) + j, s.m);
     sts_(m.col(CH_H) + j, s.h);
     if (wr) {
@@ -102,18 +105,27 @@ __device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechD
         sts_(m.col(CH_MINF) + j, mInf); sts_(m.col(CH_MTAU) + j, mTau); sts_(m.col(CH_MALPHA) + j, mAlpha); sts_(m.col(CH_MBETA) + j, mBeta);
         sts_(m.col(CH_HINF) + j, hInf); sts_(m.col(CH_HTAU) + j, hTau); sts_(m.col(CH_HALPHA) + j, hAlpha); sts_(m.col(CH_HBETA) + j, hBeta);
     }
+}
+__device__ __forceinline__ CaHVAState cahva_state(const StepArgs& A, const MechDev& m, int j, double v,
+                                                  CaHVAState s, const double* ca_erev, int ci, bool wr) {
+    cahva_gates_r(v, A.dt, s.m, s.h);
+    cahva_store(m, j, v, s, ca_erev, ci, wr);
     return s;
 }
 
-__device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l, bool wr) {
-    const double vhalfl = ldp(m, HD_VHALFL, j), tau = ldp(m, HD_TAU, j);
-    l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
+__device__ __forceinline__ void hdla_store(const StepArgs& A, const MechDev& m, int j, double v, double l,
+                                           double vhalfl, double tau, bool wr) {
     sts_(m.col(HD_L) + j, l);
     if (wr) {
         double linf, taul;
         hdla_rate(v, vhalfl, tau, A.c, linf, taul);
         sts_(m.col(HD_LINF) + j, linf); sts_(m.col(HD_TAUL) + j, taul);
     }
+}
+__device__ __forceinline__ double hdla_state(const StepArgs& A, const MechDev& m, int j, double v, double l, bool wr) {
+    const double vhalfl = ldp(m, HD_VHALFL, j), tau = ldp(m, HD_TAU, j);
+    l = hdla_gate_r(v, l, vhalfl, tau, A.c, A.dt);
+    hdla_store(A, m, j, v, l, vhalfl, tau, wr);
     return l;
 }
 
@@ -187,7 +199,7 @@ __device__ __forceinline__ void ion_cur(const MechDev& m, int j, double z, doubl
     sts_(m.col(ION_CUR) + j, 0.);
     if (write_dcurdv) sts_(m.col(ION_DCURDV) + j, 0.);
     if (m.iontype[j] & 0100)
-        sts_(m.col(ION_EREV) + j, nernst(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf));
+        sts_(m.col(ION_EREV) + j, nernst_r(m.col(ION_CONCI)[j], m.col(ION_CONCO)[j], z, ktf));
 }
 
 // erev of ion x at dense instance i for this step's current evaluation.  ci:
@@ -196,7 +208,7 @@ __device__ __forceinline__ double dense_ion_erev(const StepArgs& A, const MechDe
                                                  bool have_ci, double ci) {
     const int type = A.ion_type[x] >= 0 ? A.ion_type[x] : ion.iontype[i];
     if (type & 0100) {
-        const double e = nernst(have_ci ? ci : lds_(ion.col(ION_CONCI) + i), ldp(ion, ION_CONCO, i), z, A.c.ktf);
+        const double e = nernst_r(have_ci ? ci : lds_(ion.col(ION_CONCI) + i), ldp(ion, ION_CONCO, i), z, A.c.ktf);
         if (A.ion_store & (2u << (2 * x))) sts_(ion.col(ION_EREV) + i, e);
         return e;
     }

@@ -17,6 +17,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include "hx_internal.h"
+#include "fastmath.h"
 
 namespace hx {
 
@@ -26,6 +27,17 @@ __device__ __forceinline__ double nernst(double ci, double co, double z, double 
     if (ci <= 0.) return 1e6;
     else if (co <= 0.) return -1e6;
     else return ktf / z * log(co / ci);
+}
+
+// The same with the forward step's logarithm (fastmath.h log_pos, within a few ulps of
+// log); the form above stays in use at finitialize and in the adjoint.
+__device__ __forceinline__ double nernst_r(double ci, double co, double z, double ktf) {
+    if (z == 0) return 0.;
+    if (ci <= 0.) return 1e6;
+    else if (co <= 0.) return -1e6;
+    const double q = co / ci;
+    const bool normal = q >= 2.2250738585072014e-308 && q <= 1.7976931348623157e308;
+    return ktf / z * (normal ? log_pos(q) : log(q));
 }
 
 // ---------------- hh ----------------

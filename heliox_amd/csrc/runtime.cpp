@@ -39,6 +39,7 @@
 #include "learn.h"
 #include "plugin.h"
 #include "random123.h"
+#include "fastmath.h"
 #include "schedule.h"
 #include "solve_chunk.h"
 
@@ -676,9 +677,7 @@ struct hx_sim {
     void launch_mech_pass(int do_state, int do_current, double tcur, int grp = -1, hipStream_t on = nullptr);
     void launch_point_currents(double tcur);
     void launch_events(int kk, double tk);
-    // parts: kEvInputs (VecStim inputs, NetStims) and / or kEvDeliver (delivery)
-    static constexpr unsigned kEvInputs = 1u, kEvDeliver = 2u;
-    void launch_events_group(int g, int kk, double tk, hipStream_t on, unsigned parts = kEvInputs | kEvDeliver);
+    void launch_events_group(int g, int kk, double tk, hipStream_t on);
     void launch_detect(int kk, double tk);
     void launch_record();
     void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
@@ -2125,15 +2124,14 @@ void hx_sim::launch_events(int kk, double tk) {
     for (int g = 0; g < static_cast<int>(groups.size()); ++g) launch_events_group(g, kk, tk, stream);
 }
 
-// VecStim input and delivery of step kk for one cell group's synapses (parts: the
-// inputs and NetStims, the delivery, or both, issued in that order).
-void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, unsigned parts) {
+// VecStim input and delivery of step kk for one cell group's synapses.
+void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     const bool psyn = has_postsyn_plugins();
     const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present || psyn;
     if (!syn && nsa.n == 0) return;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
-    if ((parts & kEvInputs) && cg.n_in > 0) {
+    if (cg.n_in > 0) {
         InputArgs I{};
         I.eff_time = cg.d_in_time;
         I.inst = cg.d_in_inst;
@@ -2151,7 +2149,7 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, unsig
         I.half_dt = dt / 2;
         launch_input(I, on);
     }
-    if ((parts & kEvInputs) && nsa.n > 0) {   // NetStims receiving events: one group, the main stream
+    if (nsa.n > 0) {                 // NetStims receiving events: one group, the main stream
         NsArgs A = nsa;
         A.ring = cg.ring;
         A.ttab = d_ttab;
@@ -2161,7 +2159,7 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, unsig
         A.k = kk;
         launch_netstim(A, on);
     }
-    if (!syn || !(parts & kEvDeliver)) {
+    if (!syn) {
         tend(T_EVENTS, on);
         return;
     }
@@ -2423,23 +2421,31 @@ void hx_sim::step_once_groups() {
     for (int g = 0; g < G; ++g) {
         CellGroup& cg = groups[g];
         hipStream_t s = cg.s;
+        // the group's voltage samples (every monitor samples a voltage here, and the node
+        // pass leaves v as it finds it)
+        auto record = [&]() {
+            if (sample && cg.mon1 > cg.mon0)
+                hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
+        };
         if (turns) {
-            // the inputs do not touch the other groups: they run during the previous
-            // group's node pass; the delivery after the wait keeps this group's node pass
-            // a few microseconds behind the previous group's solve launch
-            launch_events_group(g, k, tk, s, kEvInputs);
+            // the events and samples do not touch the other groups: they run during the
+            // previous group's node pass, and only the node pass waits.  The wait's own
+            // latency keeps this node pass behind the previous group's solve, which follows
+            // its node pass directly (measured: a solve launched that way is dispatched
+            // 10-15 us ahead; with the delivery after the wait as well the step was 1% slower)
+            launch_events_group(g, k, tk, s);
+            record();
             if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass, 0));
             else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass, 0));
-            launch_events_group(g, k, tk, s, kEvDeliver);
+            launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+            HXC(hipEventRecord(cg.pass, s));
         } else {
             if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
             launch_events_group(g, k, tk, s);
+            launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+            if (stagger && g + 1 < G) HXC(hipEventRecord(ev_stagger, s));
+            record();
         }
-        launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
-        if (stagger && g + 1 < G) HXC(hipEventRecord(ev_stagger, s));
-        if (sample && cg.mon1 > cg.mon0)
-            hx::launch_record(d_mon_ptr + cg.mon0, cg.mon1 - cg.mon0, d_mon_buf + mon_buf_fill * nm + cg.mon0, s);
-        if (turns) HXC(hipEventRecord(cg.pass, s));
         SolveArgs S{};
         S.waves = solve_waves;
         S.nunit = cg.unit1 - cg.unit0;
@@ -4064,6 +4070,15 @@ int hx_get_kernel_time(hx_sim* sim, const char* kernel, double* ms, long long* l
 // kernel's per-chunk arithmetic (reciprocals here are plain divisions).  Lanes
 // of a round touch disjoint nodes and slots, so running them one after the
 // other is what the wavefront computes.
+int hx_fastmath_log(const double* x, double* y, int n) {
+    if (n < 0 || (n > 0 && (!x || !y))) return -1;
+    for (int i = 0; i < n; ++i) {
+        if (!(x[i] >= 2.2250738585072014e-308 && x[i] <= 1.7976931348623157e308)) return -1;
+        y[i] = hx::log_pos(x[i]);
+    }
+    return 0;
+}
+
 int hx_random123_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out) {
     if (!ctr || !key || !out) return -1;
     Philox4x32::block(ctr, key, out);

@@ -167,6 +167,7 @@ SIGNATURES = {
     "hx_optimizer_set_adam_state": (C.c_int, [_P, C.c_int, C.c_longlong, C.c_int, _D, _D, C.c_double, C.c_double,
                                               C.c_double]),
     "hx_random123_philox4x32": (C.c_int, [C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    "hx_fastmath_log": (C.c_int, [C.POINTER(C.c_double), C.POINTER(C.c_double), C.c_int]),
     "hx_netstim_train": (C.c_int, [C.c_double, C.c_double, C.c_double, C.c_double, C.c_double, C.c_double,
                                    C.c_uint, C.c_uint, C.c_uint, _D, C.c_int]),
     "hx_emulate_tree_solve_units": (C.c_int, [C.c_int, C.c_int, _I, _D, _D, _D, C.c_double, _D, _D, _D, C.c_int,

@@ -472,6 +472,10 @@ int hx_emulate_tree_solve(int ncell, int nnode, const int* parent, const double*
  * Random123, src/third_party/Random123/philox.h, as published by Salmon et al., SC11): out =
  * philox(ctr[4], key[2]).  A diagnostic for known-answer checks of the NetStim streams. */
 int hx_random123_philox4x32(const uint32_t* ctr, const uint32_t* key, uint32_t* out);
+/* No reference counterpart: the node kernel's logarithm (the per-step Nernst potential), built
+ * for the host from the same source, for CPU checks of its accuracy.  y[i] = ln x[i] for n
+ * positive, finite, normal x; returns -1 (nothing defined) if any x is outside that range. */
+int hx_fastmath_log(const double* x, double* y, int n);
 /* The self-event times of one NetStim instance up to t_end with step dt, as the library makes
  * them at finitialize (see hx_model_add_netcon): a diagnostic of the host-side generator.
  * Writes up to cap times to out and returns their total count (-1 on error). */
