@@ -1040,25 +1040,6 @@ void hx_sim::upload() {
         solve_waves = std::max(1, std::min<int>(want, static_cast<int>(prop.sharedMemPerBlock / lds)));
     }
 
-    // nodes carrying IClamp or HalfGap, with their group of each
-    point_union = PointUnion{};
-    if (!point_grp_node[0].empty() && !point_grp_node[1].empty()) {
-        std::vector<int> un;
-        std::set_union(point_grp_node[0].begin(), point_grp_node[0].end(), point_grp_node[1].begin(),
-                       point_grp_node[1].end(), std::back_inserter(un));
-        std::vector<int> g[2];
-        for (int x = 0; x < 2; ++x) {
-            g[x].assign(un.size(), -1);
-            const std::vector<int>& gn = point_grp_node[x];
-            for (size_t q = 0; q < gn.size(); ++q)
-                g[x][std::lower_bound(un.begin(), un.end(), gn[q]) - un.begin()] = static_cast<int>(q);
-        }
-        point_union.n = static_cast<int>(un.size());
-        point_union.node = dupload(owned, un);
-        point_union.grp[0] = dupload(owned, g[0]);
-        point_union.grp[1] = dupload(owned, g[1]);
-    }
-
     // ion node -> device instance maps
     const int ion_ids[3] = {M_NA_ION, M_K_ION, M_CA_ION};
     for (int x = 0; x < 3; ++x) {
@@ -1209,6 +1190,26 @@ void hx_sim::upload() {
     {
         const double* d_uval = dupload(owned, uval_host);
         for (int id = 0; id < M_COUNT; ++id) mech[id].dev.uval = d_uval + static_cast<size_t>(id) * kUniformCols;
+    }
+
+    // nodes carrying IClamp or HalfGap, with their group of each (the loop above made the
+    // groups)
+    point_union = PointUnion{};
+    if (!point_grp_node[0].empty() && !point_grp_node[1].empty()) {
+        std::vector<int> un;
+        std::set_union(point_grp_node[0].begin(), point_grp_node[0].end(), point_grp_node[1].begin(),
+                       point_grp_node[1].end(), std::back_inserter(un));
+        std::vector<int> g[2];
+        for (int x = 0; x < 2; ++x) {
+            g[x].assign(un.size(), -1);
+            const std::vector<int>& gn = point_grp_node[x];
+            for (size_t q = 0; q < gn.size(); ++q)
+                g[x][std::lower_bound(un.begin(), un.end(), gn[q]) - un.begin()] = static_cast<int>(q);
+        }
+        point_union.n = static_cast<int>(un.size());
+        point_union.node = dupload(owned, un);
+        point_union.grp[0] = dupload(owned, g[0]);
+        point_union.grp[1] = dupload(owned, g[1]);
     }
 
     // spike detectors, in solver-node order so a cell group's detectors are a
@@ -4241,6 +4242,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "nround_max") return sim->max_rounds;
     if (k == "dense_mask") return sim->dense_mask;
     if (k == "steady_launches") return sim->steady_launches;
+    if (k == "electrode_nodes") return sim->point_union.n;
     if (k == "fused") return sim->fused ? 1 : 0;
     if (k == "adjoint_fused") return sim->adj_fuse_bits;
     if (k == "nround_total") return static_cast<long long>(sim->rounds.size());

@@ -328,7 +328,8 @@ int hx_set_group_turns(hx_sim* sim, int enable);
  * last hx_adjoint ran in its node-parallel kernels: bits 0-7 gate adjoints, 8-15 conductances,
  * 16-23 parameter terms; bit 0 pas, 1 hh, 2 Ca_HVA, 3 hd_la, 4 CaDynamics_E2; bit 24: the synapses
  * too; bit 25: the loss term too), "steady_launches" (node-kernel launches so far that ran a
- * compile-time steady-step instance, see hx_set_dense_steady). */
+ * compile-time steady-step instance, see hx_set_dense_steady), "electrode_nodes" (nodes whose
+ * IClamp and HalfGap currents one launch adds when the model has both). */
 long long hx_get_info(hx_sim* sim, const char* key);
 
 /* ---- adjoint (VJP) backward pass: no reference counterpart.  It produces the

@@ -5,13 +5,16 @@ pyramidal-cell model on every node; pas alone) give the same bits as the generic
 traces, spikes and every column after a run, across configurations, cell groups, fusion
 off (never steady), a monitor on an assigned variable (never steady) and chunked calls.
 The cell groups' node passes taking turns on every step (events between the group streams)
-give the same bits as ordering only a run's first step."""
+give the same bits as ordering only a run's first step.  A model with IClamp and HalfGap
+instances adds both currents in one launch over the nodes that carry either, and matches the
+oracle."""
 import dataclasses
 
 import numpy as np
 import pytest
 
 from heliox_amd import Sim, build_config
+from parity_util import V_TOL, compare_spikes, run_both
 
 pytestmark = pytest.mark.gpu
 
@@ -102,3 +105,17 @@ def test_group_turns_same_bits(gpu_lib, groups):
     b = run(spec, True, chunks=(1.0, 2.5, 0.5), groups=groups, turns=False)
     assert a.info("cell_groups") == groups and a.info("multi_stream") == 1
     same_everything(spec, a, b)
+
+
+def test_iclamp_and_halfgap_in_one_launch(gpu_lib):
+    spec = build_config(4, 40, 20.0)
+    assert spec.mechs["IClamp"].n > 0 and spec.mechs["HalfGap"].n > 0
+    print("case electrode currents in one launch, config 4, 40 cells", flush=True)
+    o, g = run_both(spec, 20.0)
+    nodes = np.union1d(spec.mechs["IClamp"].nodes, spec.mechs["HalfGap"].nodes).size
+    assert g.info("electrode_nodes") == nodes
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+    compare_spikes(o, g, spec.dt)
+    for col in ("i", "vgap"):
+        assert np.max(np.abs(o.array("HalfGap", col) - g.get_array("HalfGap", col))) < 1e-9
+    assert np.max(np.abs(o.array("IClamp", "i") - g.get_array("IClamp", "i"))) < 1e-12
