@@ -359,6 +359,12 @@ struct DeliverArgs {
     int* log_count;               // when set: every delivered event (packed as in the ring) is appended
     int* log;                     // to log[0 .. *log_count) (capacity log_cap), for the adjoint
     int log_cap;
+    // VecPlay at the current evaluation's time on blocks of their own (nvp 0: none); only
+    // for targets delivery never touches (IClamp variables), so the two tasks are independent
+    VecPlayDev* vp;
+    int nvp;
+    double t_vp;
+    int ndeliver;                 // blocks of the delivery task (set by launch_deliver)
 };
 
 // One backward step of the adjoint (adjoint.hip).  v1, x0, geff: the taped

@@ -1325,44 +1325,6 @@ __global__ void __launch_bounds__(1024) k_netstim(NsArgs A) {
     if (threadIdx.x == 0) A.ib.count[slot] = 0;
 }
 
-// NET_RECEIVE of the events of step k's ring slot (expsyn.cpp net_receive,
-// exp2syn_temp.cuh:62-67): ExpSyn g += w, Exp2Syn A, B += w factor, in any order
-// (fp64 atomics), as on the reference's GPU path.  The workgroups stride over the
-// slot, so a burst spreads over the chip; each counts itself done after its loop (which
-// used the count it read), and the last one empties the slot, so a second launch for
-// the same step (finitialize's, then the first step's) delivers only what was pushed
-// in between.
-__global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
-    const int slot = D.k & (D.ring.nslot - 1);
-    int cnt = D.ring.count[slot];
-    if (cnt > D.ring.cap) cnt = D.ring.cap;
-    const long long off = static_cast<long long>(slot) * D.ring.cap;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < cnt; e += gridDim.x * blockDim.x) {
-        const int packed = D.ring.entry[off + e];
-        const int type = target_kind(packed);
-        const int inst = packed & 0x3fffffff;
-        if (type == 0) {
-            atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
-        } else if (type == kTargetPlugin) {   // counted; the plugin's NET_RECEIVE kernel follows
-            atomicAdd(&D.plugin_recv[(inst >> kPostsynSlotShift) & (kMaxPostsyn - 1)]
-                                    [inst & ((1 << kPostsynSlotShift) - 1)], 1);
-        } else if (type == 1) {            // (NetStim targets go to their own inbox)
-            const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
-            atomicAdd(&D.e2.col(E2_A)[inst], wf);
-            atomicAdd(&D.e2.col(E2_B)[inst], wf);
-        }
-        if (D.log) {          // the adjoint's record of the step's deliveries (packed as in the ring)
-            const int pos = atomicAdd(D.log_count, 1);
-            if (pos < D.log_cap) D.log[pos] = packed;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x == 0 && (gridDim.x == 1 || atomicAdd(D.ring.done, 1u) == gridDim.x - 1)) {
-        D.ring.count[slot] = 0;
-        if (gridDim.x > 1) *D.ring.done = 0u;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // VecPlay continuous playback (vecplay.cu:19-111)
 // ---------------------------------------------------------------------------
@@ -1400,6 +1362,48 @@ __device__ __forceinline__ void vecplay_item(VecPlayDev* items, int n, double t,
 store:
     *it.target = val;
     items[i] = it;
+}
+
+// NET_RECEIVE of the events of step k's ring slot (expsyn.cpp net_receive,
+// exp2syn_temp.cuh:62-67): ExpSyn g += w, Exp2Syn A, B += w factor, in any order
+// (fp64 atomics), as on the reference's GPU path.  The workgroups stride over the
+// slot, so a burst spreads over the chip; each counts itself done after its loop (which
+// used the count it read), and the last one empties the slot, so a second launch for
+// the same step (finitialize's, then the first step's) delivers only what was pushed
+// in between.
+__global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
+    if (static_cast<int>(blockIdx.x) >= D.ndeliver) {      // the VecPlay task's blocks
+        vecplay_item(D.vp, D.nvp, D.t_vp, 1, (blockIdx.x - D.ndeliver) * blockDim.x + threadIdx.x);
+        return;
+    }
+    const int slot = D.k & (D.ring.nslot - 1);
+    int cnt = D.ring.count[slot];
+    if (cnt > D.ring.cap) cnt = D.ring.cap;
+    const long long off = static_cast<long long>(slot) * D.ring.cap;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < cnt; e += D.ndeliver * blockDim.x) {
+        const int packed = D.ring.entry[off + e];
+        const int type = target_kind(packed);
+        const int inst = packed & 0x3fffffff;
+        if (type == 0) {
+            atomicAdd(&D.es.col(ES_G)[inst], D.es_weight[inst]);
+        } else if (type == kTargetPlugin) {   // counted; the plugin's NET_RECEIVE kernel follows
+            atomicAdd(&D.plugin_recv[(inst >> kPostsynSlotShift) & (kMaxPostsyn - 1)]
+                                    [inst & ((1 << kPostsynSlotShift) - 1)], 1);
+        } else if (type == 1) {            // (NetStim targets go to their own inbox)
+            const double wf = D.e2_weight[inst] * D.e2.col(E2_FACTOR)[inst];
+            atomicAdd(&D.e2.col(E2_A)[inst], wf);
+            atomicAdd(&D.e2.col(E2_B)[inst], wf);
+        }
+        if (D.log) {          // the adjoint's record of the step's deliveries (packed as in the ring)
+            const int pos = atomicAdd(D.log_count, 1);
+            if (pos < D.log_cap) D.log[pos] = packed;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && (D.ndeliver == 1 || atomicAdd(D.ring.done, 1u) == D.ndeliver - 1u)) {
+        D.ring.count[slot] = 0;
+        if (D.ndeliver > 1) *D.ring.done = 0u;
+    }
 }
 
 __global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
@@ -1655,7 +1659,10 @@ void launch_netstim(const NsArgs& a, hipStream_t s) {
 }
 
 void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s) {
-    hipLaunchKernelGGL(k_deliver, dim3(std::max(1, nblk)), dim3(1024), 0, s, a);
+    DeliverArgs d = a;
+    d.ndeliver = std::max(1, nblk);
+    const int nvp_blk = d.nvp > 0 ? (d.nvp + 1023) / 1024 : 0;
+    hipLaunchKernelGGL(k_deliver, dim3(d.ndeliver + nvp_blk), dim3(1024), 0, s, d);
 }
 
 void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s) {

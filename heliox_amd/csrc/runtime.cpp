@@ -676,8 +676,9 @@ struct hx_sim {
     // ------------------------------------------------------------ stepping
     void launch_mech_pass(int do_state, int do_current, double tcur, int grp = -1, hipStream_t on = nullptr);
     void launch_point_currents(double tcur);
-    void launch_events(int kk, double tk);
-    void launch_events_group(int g, int kk, double tk, hipStream_t on);
+    // vp_t >= 0: the delivery launch also runs VecPlay at time vp_t (and returns true)
+    bool launch_events(int kk, double tk, double vp_t = -1.0);
+    bool launch_events_group(int g, int kk, double tk, hipStream_t on, double vp_t = -1.0);
     void launch_detect(int kk, double tk);
     void launch_record();
     void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
@@ -2121,15 +2122,18 @@ void hx_sim::launch_plugin_states(double tcur) {
     tend(T_OTHER);
 }
 
-void hx_sim::launch_events(int kk, double tk) {
-    for (int g = 0; g < static_cast<int>(groups.size()); ++g) launch_events_group(g, kk, tk, stream);
+bool hx_sim::launch_events(int kk, double tk, double vp_t) {
+    bool vp_done = false;
+    for (int g = 0; g < static_cast<int>(groups.size()); ++g)
+        vp_done |= launch_events_group(g, kk, tk, stream, g == 0 ? vp_t : -1.0);
+    return vp_done;
 }
 
 // VecStim input and delivery of step kk for one cell group's synapses.
-void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
+bool hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, double vp_t) {
     const bool psyn = has_postsyn_plugins();
     const bool syn = mech[M_EXPSYN].present || mech[M_EXP2SYN].present || psyn;
-    if (!syn && nsa.n == 0) return;
+    if (!syn && nsa.n == 0) return false;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
     if (cg.n_in > 0) {
@@ -2162,7 +2166,7 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     }
     if (!syn) {
         tend(T_EVENTS, on);
-        return;
+        return false;
     }
     DeliverArgs D{};
     D.ring = cg.ring;
@@ -2185,11 +2189,17 @@ void hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on) {
     // config 3 ran 2.5% slower with the grid and a merged input kernel, and 3% slower
     // with 256-thread workgroups).
     const int nblk = pre_fanout_empty ? 1 : std::min(64, (cg.ring.cap + 8191) / 8192);
+    if (vp_t >= 0.0) {
+        D.vp = d_vecplay;
+        D.nvp = static_cast<int>(vecplay.size());
+        D.t_vp = vp_t;
+    }
     launch_deliver(D, nblk, on);
     // the synapse plugins' NET_RECEIVE of what was counted (one group: plugins couple the model)
     for (const auto& p : plugins)
         if (p.slot >= 0) p.meta->launch_receive(plugin_args(p, tk), on);
     tend(T_EVENTS, on);
+    return vp_t >= 0.0;
 }
 
 // Threshold detection of detectors [pre0, pre1) at step kk (time tk), fanning out into
@@ -2494,8 +2504,11 @@ void hx_sim::step_once() {
         // target selects the split schedule), so they may precede the previous
         // step's deferred state update; the node kernel then adds the synapse
         // currents with this step's deliveries in place
-        launch_events(k, tk);
-        if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        // VecPlay writing only IClamp variables, which delivery never touches, runs on blocks
+        // of the delivery launch
+        const bool vp_in_events = has_vp && vecplay_iclamp_only;
+        const bool vp_done = launch_events(k, tk, vp_in_events ? tmid : -1.0);
+        if (has_vp && !vp_done) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
         const bool eager = cadyn_eager && !(final_step && lazy_outputs_run);   // as in step_once_groups
         pass_cadyn_skip = cadyn_done ? 1 : 0;
         pass_cadyn_after = eager ? 1 : 0;
