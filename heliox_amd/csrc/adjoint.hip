@@ -35,6 +35,13 @@
 // Exp2Syn: g = B_eff - A_eff (events add w factor to both), A and B decay by
 // exp(-dt / tau1), exp(-dt / tau2) after the solve; a delivered event's weight
 // gets factor (lambda_A + lambda_B).
+//
+// Gap junctions (HalfGap, an electrode current i = g (vgap - v) x 1e2/area): a
+// conductance G = g 1e2/area with reversal potential vgap, which is the source
+// node's v^n (the transfer after the previous step's solve) or, without a source,
+// a constant.  So G joins M's diagonal like any membrane conductance, dL/dg +=
+// -mu 1e2/area (v^{n+1} - vgap), and v^{n+1} = M^-1 (C v^n + G vgap) gives the
+// source node lambda_v^n += G mu at the instance's node.
 #include "hx_internal.h"
 #include "mech_math.h"
 
@@ -352,6 +359,43 @@ __global__ void k_adj_cond_syn2(AdjStep A) {
 #undef HX_ADJ_SYN
 #undef HX_ADJ_GROUP
 
+// HalfGap conductances of node group q (the instances on one node, in instance order)
+__global__ void k_adj_cond_gap(AdjStep A) {
+    const MechDev& m = A.m[M_HALFGAP];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= m.ngrp) return;
+    const int node = m.grp_node[q];
+    double g = 0.0;
+    for (int j = m.grp_begin[q]; j < m.grp_begin[q + 1]; ++j) g += m.col(HG_G)[j];
+    A.dT[node] += g * (1.e2 / A.area[node]);
+}
+
+// dL/dg of each HalfGap instance
+__global__ void k_adj_gap_param(AdjStep A) {
+    const MechDev& m = A.m[M_HALFGAP];
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= m.n) return;
+    const int node = m.node[j];
+    const int src = A.gap_partner[j];
+    const double vgap = src >= 0 ? A.v0[src] : m.col(HG_VGAP)[j];
+    A.grad_ggap[j] -= A.mu[node] * (1.e2 / A.area[node]) * (A.v1[node] - vgap);
+}
+
+// lambda_v^n of each source node += G mu at the nodes of the instances it feeds, summed in
+// instance order by one thread per source
+__global__ void k_adj_gap_cross(AdjStep A) {
+    const MechDev& m = A.m[M_HALFGAP];
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= A.ngap_src) return;
+    double acc = 0.0;
+    for (int e = A.gap_begin[q]; e < A.gap_begin[q + 1]; ++e) {
+        const int j = A.gap_inst[e];
+        const int node = m.node[j];
+        acc += m.col(HG_G)[j] * (1.e2 / A.area[node]) * A.mu[node];
+    }
+    A.lam_v_new[A.gap_src[q]] += acc;
+}
+
 // events delivered at step n: ExpSyn dL/dw += lambda_geff, Exp2Syn dL/dw += factor
 // (lambda_A + lambda_B) (one block)
 __global__ void __launch_bounds__(256) k_adj_events(AdjStep A) {
@@ -462,6 +506,8 @@ void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
         hipLaunchKernelGGL(k_adj_cond_syn, grid_of(a.m[M_EXPSYN].ngrp), dim3(kBlock), 0, s, a);
     if (!a.fold_syn && a.m[M_EXP2SYN].ngrp > 0)
         hipLaunchKernelGGL(k_adj_cond_syn2, grid_of(a.m[M_EXP2SYN].ngrp), dim3(kBlock), 0, s, a);
+    if (a.m[M_HALFGAP].ngrp > 0)
+        hipLaunchKernelGGL(k_adj_cond_gap, grid_of(a.m[M_HALFGAP].ngrp), dim3(kBlock), 0, s, a);
 }
 
 void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
@@ -478,6 +524,10 @@ void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
     if (!a.fold_syn && a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_param, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
     if (a.m[M_EXPSYN].n > 0 || a.m[M_EXP2SYN].n > 0) hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
+    if (a.m[M_HALFGAP].n > 0) {
+        hipLaunchKernelGGL(k_adj_gap_param, grid_of(a.m[M_HALFGAP].n), dim3(kBlock), 0, s, a);
+        if (a.ngap_src > 0) hipLaunchKernelGGL(k_adj_gap_cross, grid_of(a.ngap_src), dim3(kBlock), 0, s, a);
+    }
 }
 
 void launch_adj_loss(const double* v, const int* nodes, const int* begin, const int* idx, int n,

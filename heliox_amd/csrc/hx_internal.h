@@ -426,6 +426,15 @@ struct AdjStep {
     const double* loss_tgt;
     const int* loss_of_node;
     double loss_scale;
+    // gap junctions (HalfGap): the source node of each instance's vgap (-1: none, vgap is a
+    // constant), and the distinct source nodes with the instances they feed
+    // (gap_inst[gap_begin[q] .. gap_begin[q+1]) for source gap_src[q])
+    const int* gap_partner;
+    int ngap_src;
+    const int* gap_src;
+    const int* gap_begin;
+    const int* gap_inst;
+    double* grad_ggap;            // HalfGap g
 };
 constexpr unsigned kAdjPas = 1, kAdjHH = 2, kAdjCaHVA = 4, kAdjHdla = 8, kAdjCaDyn = 16;
 

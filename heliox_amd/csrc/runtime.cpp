@@ -227,11 +227,11 @@ struct Trainable {
     int mech;
     const char* var;
 };
-constexpr int kNumTrainable = 7;
+constexpr int kNumTrainable = 8;
 constexpr Trainable kTrainable[kNumTrainable] = {
     {M_HH, "gnabar"}, {M_HH, "gkbar"}, {M_PAS, "g_pas"}, {M_EXPSYN, "weight"},
-    {M_CAHVA, "gbar"}, {M_HDLA, "ghdbar"}, {M_EXP2SYN, "weight"}};
-enum TrainableId { T_GNABAR = 0, T_GKBAR, T_GPAS, T_WES, T_CGBAR, T_GHDBAR, T_WE2 };
+    {M_CAHVA, "gbar"}, {M_HDLA, "ghdbar"}, {M_EXP2SYN, "weight"}, {M_HALFGAP, "g"}};
+enum TrainableId { T_GNABAR = 0, T_GKBAR, T_GPAS, T_WES, T_CGBAR, T_GHDBAR, T_WE2, T_GGAP };
 
 inline int trainable_id(int mech, const std::string& var) {
     for (int k = 0; k < kNumTrainable; ++k)
@@ -311,6 +311,7 @@ struct hx_sim {
     // adjoint loss: nodes and targets per call, the distinct nodes with their loss
     // indices (node -> first index of its list), and node -> loss index when distinct
     DevSlot adj_ln_slot, adj_tgt_slot, adj_samp_slot, adj_un_slot, adj_ubeg_slot, adj_uidx_slot, adj_lmap_slot;
+    DevSlot adj_gp_slot, adj_gs_slot, adj_gb_slot, adj_gi_slot;   // gap junctions (HalfGap)
     std::vector<int> adj_lmap_nodes;             // the loss nodes adj_lmap_slot holds the map of
     unsigned adj_fuse_bits = 0;          // last hx_adjoint's node-parallel masks (state | cond << 8 | param << 16)
     bool uniform_on = true;              // parameter columns with one value read as scalars
@@ -4301,11 +4302,6 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
         return 0;
     }
     const auto& R = registry();
-    for (int id = 0; id < M_COUNT; ++id) {
-        if (!sim->mech[id].present) continue;
-        if (id == M_HALFGAP)
-            return sim->fail("the adjoint does not support gap junctions (the model has %s)", R[id].name);
-    }
     if (!sim->plugins.empty()) {
         return sim->fail("the adjoint does not support plugin mechanisms (the model has %s)",
                          sim->plugins[0].meta->name);
@@ -4315,7 +4311,10 @@ int hx_tape_begin(hx_sim* sim, int max_steps) {
             for (int t : sim->mech[x].iontype)
                 if (t & 0100) return sim->fail("the adjoint needs fixed reversal potentials (%s iontype 0100)",
                                                R[x].name);
-    if (!sim->vecplay.empty()) return sim->fail("the adjoint does not support VecPlay");
+    // VecPlay into IClamp variables changes currents that do not depend on v or on any
+    // trained parameter; any other target would need its values on the tape
+    if (!sim->vecplay.empty() && !sim->vecplay_iclamp_only)
+        return sim->fail("the adjoint supports VecPlay into IClamp variables only");
     sim->tape_free();
     const size_t cap = static_cast<size_t>(max_steps);
     HXC(hipMalloc(&sim->d_tape_v, sizeof(double) * cap * sim->nnode));
@@ -4486,6 +4485,36 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.grad_cgbar = sim->d_grad[T_CGBAR];
     A.grad_ghdbar = sim->d_grad[T_GHDBAR];
     A.grad_w2 = sim->d_grad[T_WE2];
+    A.grad_ggap = sim->d_grad[T_GGAP];
+    // gap junctions: each HalfGap instance's source node (solver order; -1: none) and the
+    // distinct sources with the instances they feed, in instance order
+    if (sim->mech[M_HALFGAP].present && sim->mech[M_HALFGAP].n > 0) {
+        const HostMech& hg = sim->mech[M_HALFGAP];
+        std::vector<int> partner(hg.n, -1);
+        std::vector<std::pair<int, int>> by_src;        // (source node, device instance)
+        for (const auto& gp : sim->gaps) {
+            const int j = hg.perm[gp.second], src = sim->node_perm[gp.first];
+            partner[j] = src;
+            by_src.push_back({src, j});
+        }
+        std::sort(by_src.begin(), by_src.end());
+        std::vector<int> srcs, beg, inst;
+        for (size_t e = 0; e < by_src.size(); ++e) {
+            if (e == 0 || by_src[e].first != by_src[e - 1].first) {
+                srcs.push_back(by_src[e].first);
+                beg.push_back(static_cast<int>(e));
+            }
+            inst.push_back(by_src[e].second);
+        }
+        beg.push_back(static_cast<int>(by_src.size()));
+        A.gap_partner = sim->slot_upload(sim->adj_gp_slot, partner);
+        A.ngap_src = static_cast<int>(srcs.size());
+        if (!srcs.empty()) {
+            A.gap_src = sim->slot_upload(sim->adj_gs_slot, srcs);
+            A.gap_begin = sim->slot_upload(sim->adj_gb_slot, beg);
+            A.gap_inst = sim->slot_upload(sim->adj_gi_slot, inst);
+        }
+    }
     // The node-parallel kernels take the mechanisms with one instance on every node (the
     // node kernel's layout): gate adjoints only as the tail of hh, Ca_HVA, hd_la and
     // conductances only as the head of pas, hh, Ca_HVA, hd_la, so that every node's sums

@@ -337,9 +337,11 @@ long long hx_get_info(hx_sim* sim, const char* key);
  *      (LearnRuntime::replay_compute_dw_from_cached_signals_into,
  *      LearnRuntime.cpp:2298-2457), here as the exact gradient of a voltage loss
  *      through the fixed-step simulation.  Models: pas, hh, Ca_HVA, hd_la (Ih),
- *      CaDynamics_E2, ExpSyn, Exp2Syn (VecStim, NetStim or detector sources), IClamp;
- *      na/k ions with fixed reversal potentials, ca_ion with a fixed eca or eca from
- *      cai every step (style 0100).  Not: gap junctions, VecPlay. ---- */
+ *      CaDynamics_E2, ExpSyn, Exp2Syn (VecStim, NetStim or detector sources), IClamp
+ *      (also driven by VecPlay), HalfGap gap junctions of the model; na/k ions with fixed
+ *      reversal potentials, ca_ion with a fixed eca or eca from cai every step (style
+ *      0100).  Not: VecPlay into other variables, gap transfers added at run time,
+ *      plugin mechanisms. ---- */
 /* Record the next run into HBM, up to max_steps steps (0 stops and frees the tape).
  * Call before hx_finitialize: deliveries at finitialize belong to step 0. */
 int hx_tape_begin(hx_sim* sim, int max_steps);
@@ -350,8 +352,8 @@ int hx_tape_length(hx_sim* sim);
  * backward sweep and leaves per-instance gradients for hx_get_gradient. */
 int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* target, int nsample, double* loss);
 /* dLoss/dparam per instance (user order): ("hh","gnabar"), ("hh","gkbar"),
- * ("pas","g_pas"), ("Ca_HVA","gbar"), ("hd_la","ghdbar"), ("ExpSyn","weight") and
- * ("Exp2Syn","weight") (the weight of the netcon into that instance).  The same values
+ * ("pas","g_pas"), ("Ca_HVA","gbar"), ("hd_la","ghdbar"), ("HalfGap","g"), ("ExpSyn","weight")
+ * and ("Exp2Syn","weight") (the weight of the netcon into that instance).  The same values
  * are the variables "grad_<var>" of the mechanism, e.g. ("Ca_HVA", "grad_gbar", i). */
 int hx_get_gradient(hx_sim* sim, const char* mech, const char* var, double* out, int cap);
 
