@@ -302,6 +302,7 @@ struct hx_sim {
     void make_netstim_trains(int horizon);
     std::vector<NetCon> netcons;
     std::vector<std::pair<int, int>> gaps;     // (src node, halfgap inst)
+    std::vector<std::pair<int, int>> gaps_eff; // the gaps the transfers use: the last of each instance
     std::vector<VecPlayHost> vecplay;
     int event_cap_request = 0;
     int fusion_allowed = 1;
@@ -1384,9 +1385,18 @@ void hx_sim::upload() {
     HXC(hipMemset(d_spk_count, 0, sizeof(int)));
     build_groups(vs_fo, ntgt);
 
-    // gap transfers
+    // gap transfers.  The reference copies them one after the other, so a HalfGap instance
+    // named by several gaps ends with the last one's source; the transfer kernel copies
+    // them side by side, so only that last gap of each instance is kept (gaps_eff).
+    {
+        std::vector<int> last(mech[M_HALFGAP].present ? mech[M_HALFGAP].n : 0, -1);
+        for (size_t e = 0; e < gaps.size(); ++e) last[gaps[e].second] = static_cast<int>(e);
+        gaps_eff.clear();
+        for (size_t e = 0; e < gaps.size(); ++e)
+            if (last[gaps[e].second] == static_cast<int>(e)) gaps_eff.push_back(gaps[e]);
+    }
     std::vector<int> gs, gi;
-    for (auto& g : gaps) { gs.push_back(node_perm[g.first]); gi.push_back(mech[M_HALFGAP].perm[g.second]); }
+    for (auto& g : gaps_eff) { gs.push_back(node_perm[g.first]); gi.push_back(mech[M_HALFGAP].perm[g.second]); }
     d_gap_src = dupload(owned, gs);
     d_gap_inst = dupload(owned, gi);
 
@@ -2248,7 +2258,7 @@ AfterSolve hx_sim::after_solve_args(double tn, int knext, int grp) const {
             P.gap_src = d_gap_src;
             P.gap_inst = d_gap_inst;
             P.vgap = mech[M_HALFGAP].dev.col(HG_VGAP);
-            P.ngap = static_cast<int>(gaps.size());
+            P.ngap = static_cast<int>(gaps_eff.size());
         }
         P.psrc = d_dg_src;
         P.pdst = d_dg_dst;
@@ -2380,7 +2390,7 @@ void hx_sim::launch_gap_transfers() {
     upload_gap_ptrs();
     tbegin(T_OTHER);
     if (stat)
-        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps.size()), stream);
+        launch_gap(d_v, d_gap_src, mech[M_HALFGAP].dev.col(HG_VGAP), d_gap_inst, static_cast<int>(gaps_eff.size()), stream);
     launch_copy_ptrs(d_dg_src, d_dg_dst, static_cast<int>(dg_src.size()), stream);
     tend(T_OTHER);
 }
@@ -4492,7 +4502,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
         const HostMech& hg = sim->mech[M_HALFGAP];
         std::vector<int> partner(hg.n, -1);
         std::vector<std::pair<int, int>> by_src;        // (source node, device instance)
-        for (const auto& gp : sim->gaps) {
+        for (const auto& gp : sim->gaps_eff) {
             const int j = hg.perm[gp.second], src = sim->node_perm[gp.first];
             partner[j] = src;
             by_src.push_back({src, j});

@@ -119,3 +119,17 @@ def test_iclamp_and_halfgap_in_one_launch(gpu_lib):
     for col in ("i", "vgap"):
         assert np.max(np.abs(o.array("HalfGap", col) - g.get_array("HalfGap", col))) < 1e-9
     assert np.max(np.abs(o.array("IClamp", "i") - g.get_array("IClamp", "i"))) < 1e-12
+
+
+def test_halfgap_named_by_two_gaps_takes_the_last(gpu_lib):
+    """The reference copies gap transfers one after the other, so an instance named twice
+    ends with the later gap's source; the oracle does the same."""
+    spec = build_config(4, 16, 10.0)
+    hg0 = int(spec.gap_halfgap[0])
+    other = int(np.setdiff1d(np.arange(spec.ncell), [spec.gap_src_node[0], spec.mechs["HalfGap"].nodes[hg0]])[0])
+    spec.gap_src_node = np.append(spec.gap_src_node, np.int32(other))
+    spec.gap_halfgap = np.append(spec.gap_halfgap, np.int32(hg0))
+    print("case HalfGap named by two gaps, config 4, 16 cells", flush=True)
+    o, g = run_both(spec, 10.0)
+    assert np.max(np.abs(o.traces() - g.traces())) < V_TOL
+    assert np.max(np.abs(o.array("HalfGap", "vgap") - g.get_array("HalfGap", "vgap"))) < 1e-9
