@@ -129,7 +129,7 @@ struct TMech : Mech {
 struct Model {
     int ncell = 0, len = 0;
     std::vector<int> parent;
-    std::vector<double> a, b, area, v, d, rhs, cm, icap;
+    std::vector<double> a, b, area, v, d, rhs, cm;
     double cj = 0, t = 0, dt = 0.025, celsius = 6.3;
 
     std::map<std::string, std::unique_ptr<Mech>> mechs;
@@ -965,10 +965,10 @@ void Model::solve_serial() {                  // simulate.cpp:558-581
     }
 }
 
-void Model::update() {                        // simulate.cpp:759-770, capac.cpp:54-66
+// The reference also stores the capacitive current cfac * cm * x here (capac.cpp:54-66);
+// no variable table of the reference or of the library exposes it, so it is left out.
+void Model::update() {                        // simulate.cpp:759-770
     for (int i = 0; i < len; i++) v[i] += rhs[i];
-    double cfac = 0.001 * cj;
-    for (int i = 0; i < len; ++i) icap[i] = cfac * cm[i] * rhs[i];
 }
 
 void Model::nonvint() {                       // simulate.cpp:779-852
@@ -1238,7 +1238,6 @@ double* Model::var_ptr(const std::string& mech, const std::string& var, int idx)
     if (mech == "capacitance") {
         if (idx < 0 || idx >= len) return nullptr;
         if (var == "cm") return cm.data() + idx;
-        if (var == "i_cap") return icap.data() + idx;
         return nullptr;
     }
     auto it = mechs.find(mech);
@@ -1286,7 +1285,7 @@ int hxo_set_nodes(void* h, int ncell, int nnode, const int* parent, const double
         if (parent[i] < 0 || parent[i] >= i) return -1;
     m->a.assign(a, a + nnode); m->b.assign(b, b + nnode); m->area.assign(area, area + nnode);
     m->cm.assign(cm, cm + nnode);
-    m->v.assign(nnode, 0.0); m->d.assign(nnode, 0.0); m->rhs.assign(nnode, 0.0); m->icap.assign(nnode, 0.0);
+    m->v.assign(nnode, 0.0); m->d.assign(nnode, 0.0); m->rhs.assign(nnode, 0.0);
     return 0;
 }
 

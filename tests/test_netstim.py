@@ -222,6 +222,29 @@ def test_trigger_starts_a_burst_and_is_ignored_while_on():
     assert o.get("NetStim", "on", 0) == 0.0 and o.get("NetStim", "ispike", 0) == 3.0
 
 
+@pytest.mark.parametrize("noise", [1.0, 0.5])
+def test_noisy_trigger_draws_the_first_interval(noise):
+    """A positive event turning a noisy NetStim on draws the first interval and removes
+    its deterministic part (event = invl(interval) - interval (1 - noise), netstim.cpp:262-274):
+    the first spike comes noise * interval * (-log u0) after the delivering step, the next
+    ones invl(interval) = (1 - noise) interval + noise interval (-log u_k) apart, with u_k
+    the instance's stream (ids (0, 0, 0), no draw at INITIAL since start < 0)."""
+    interval = 2.0
+    p = dict(interval=interval, number=3, start=-1.0, noise=noise)
+    spec = gated_model([p], [[10.0]], [1.0], [0.5])
+    o = run_oracle(spec, 40.0)
+    ot, _ = o.netstim_spikes()
+    w = philox4x32((0, 0, 0, 0), (0, 0))
+    u = [(x + 1.0) * (1.0 / 4294967297.0) for x in w]
+    t1 = delivered([10.5])[0]
+    want, T = [], t1 + noise * interval * (-math.log(u[0]))
+    for k in range(3):
+        want.append(delivered([T])[0])
+        T = want[-1] + (1.0 - noise) * interval + noise * interval * (-math.log(u[k + 1]))
+    assert np.array_equal(ot, np.array(want)), (ot, want)
+    assert o.get("NetStim", "on", 0) == 0.0 and o.get("NetStim", "ispike", 0) == 3.0
+
+
 def test_negative_event_turns_a_running_netstim_off():
     p = dict(interval=10.0, number=100, start=5.0, noise=0.0)
     spec = gated_model([p], [[52.0]], [-1.0], [0.0])

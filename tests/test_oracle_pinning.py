@@ -115,6 +115,32 @@ def test_passive_iclamp_backward_euler_closed_form():
     assert np.allclose(v, ref, rtol=0, atol=1e-10)
 
 
+def test_iclamp_window_on_exact_step_times():
+    """The pulse is on while the mid-step time t satisfies del <= t < del + dur
+    (iclamp.cu:18).  With dt = 1/32 every mid-step time is exact in binary, so del and
+    del + dur can sit exactly on mid-step times: the pulse then covers steps 10..15 and
+    no other, which the capacitor charging C dv/dt = I (pas with g = 0) shows one step
+    at a time."""
+    dt, area, cm, amp = 1.0 / 32, 500.0, 1.0, 0.004
+    spec = single_compartment(area=area, cm=cm, dt=dt)
+    n = np.array([0], np.int32)
+    spec.mechs["pas"] = MechSpec(n, {"g_pas": np.array([0.0]), "e_pas": np.array([-65.0])})
+    spec.mechs["IClamp"] = MechSpec(n.copy(), {"delay": np.array([10.5 * dt]), "dur": np.array([6 * dt]),
+                                               "amp": np.array([amp])})
+    spec.monitors = [("global", "v", 0)]
+    o = oracle.OracleSim(spec)
+    o.finitialize(-65.0)
+    o.run(24 * dt)
+    v = o.traces()[0]
+    step = amp * 1e2 / area / (1e-3 / dt * cm)
+    expect = [-65.0]
+    for k in range(24):
+        expect.append(expect[-1] + (step if 10 <= k <= 15 else 0.0))
+    assert len(v) == 25
+    assert np.allclose(v, expect, rtol=0, atol=1e-12)
+    assert v[10] == -65.0 and v[11] > -65.0 and v[16] == v[17] == v[24]
+
+
 def test_sealed_cable_steady_state():
     """A long passive cable with current injected at one end reaches the
     analytic sealed-end profile V(x) ~ cosh((L - x)/lambda) / cosh(L/lambda)."""
@@ -803,6 +829,34 @@ def test_threshold_detection_and_netcon_delay():
     assert abs(ts[0] - t[k]) < 1e-12
     m = k + int(np.argmax(t[k] + 1.0 <= t[k:] + 0.0125))
     assert g[m] == 0.0 and g[m + 1] > 0.0
+
+
+def test_threshold_is_strict_on_a_slow_ramp():
+    """Detection fires at the first step whose starting voltage is above the threshold
+    (pre_v > thr, presyn.cpp:140-157), stamped with that step's start time: a capacitor
+    charged at a constant 0.1 mV per step from -65 mV reaches -65 + 0.1 k after k steps,
+    and the threshold sits between steps 20 and 21."""
+    dt, area, cm = 0.025, 500.0, 1.0
+    step = 0.1
+    amp = step * (1e-3 / dt * cm) * area / 1e2
+    spec = single_compartment(area=area, cm=cm, dt=dt)
+    n = np.array([0], np.int32)
+    spec.mechs["pas"] = MechSpec(n, {"g_pas": np.array([0.0]), "e_pas": np.array([-65.0])})
+    spec.mechs["IClamp"] = MechSpec(n.copy(), {"delay": np.array([0.0]), "dur": np.array([1e9]),
+                                               "amp": np.array([amp])})
+    spec.presyn_gid = np.array([3], np.int32)
+    spec.presyn_node = np.array([0], np.int32)
+    spec.presyn_thr = np.array([-65.0 + 20.5 * step])
+    spec.monitors = [("global", "v", 0)]
+    o = oracle.OracleSim(spec)
+    o.finitialize(-65.0)
+    o.run(40 * dt)
+    v = o.monitor(0)
+    assert np.allclose(v, -65.0 + step * np.arange(v.size), rtol=0, atol=1e-9)
+    ts, gid = o.spikes()
+    t = step_times(dt, 40)
+    assert list(gid) == [3]
+    assert ts[0] == t[21]
 
 
 # ---------------------------------------------------------------------------
