@@ -367,6 +367,18 @@ struct DeliverArgs {
     int ndeliver;                 // blocks of the delivery task (set by launch_deliver)
 };
 
+// The cell groups' VecStim input and delivery of one step in one launch each, when the
+// groups share one stream: each group keeps its own trains, cursor and ring.
+constexpr int kMaxMergedGroups = 8;
+struct InputSet {
+    InputArgs a[kMaxMergedGroups];
+    int n;
+};
+struct RingSet {
+    EventRing r[kMaxMergedGroups];
+    int n;
+};
+
 // One backward step of the adjoint (adjoint.hip).  v1, x0, geff: the taped
 // v^{n+1} (node order), hh gates x^n (3 columns of xstride) and ExpSyn g_eff^n.
 struct AdjStep {
@@ -503,6 +515,8 @@ void launch_point_state(int mech, const StepArgs& a, hipStream_t s);
 void launch_init(int mech, const StepArgs& a, hipStream_t s);
 void launch_set_v(double* v, int n, double val, hipStream_t s);
 void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s);
+void launch_input_set(const InputSet& a, hipStream_t s);
+void launch_deliver_set(const DeliverArgs& a, const RingSet& rings, int nblk, hipStream_t s);
 // streaming probe (nread, nwrite) in {(1,1), (11,9), (26,9)}; false for other mixes
 bool launch_stream(int nread, int nwrite, const double* in, double* out, long long n, hipStream_t s);
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s);

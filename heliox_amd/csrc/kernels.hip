@@ -19,7 +19,8 @@
 //                    substitution and v update; junction values through LDS
 //   k_spike ........ threshold detection, wave-ballot compaction into the spike
 //                    log, fan-out of deliveries into the device event ring
-//   k_input ........ VecStim trains (sorted on the host) entering the ring
+//   k_input ........ VecStim trains (sorted on the host) entering the ring;
+//                    k_input_set: several cell groups sharing a stream, one launch
 //   k_netstim ...... NetStims that receive events: the step's delivery loop for them
 //   k_deliver ...... NET_RECEIVE of the events due this step
 //   k_vecplay, k_record, k_gap, init kernels.
@@ -1114,7 +1115,7 @@ __device__ __forceinline__ void spike_detect(const SpikeArgs& S, int i) {
 
 __global__ void __launch_bounds__(kBlock) k_spike(SpikeArgs S) { spike_detect(S, blockIdx.x * blockDim.x + threadIdx.x); }
 
-__global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
+__device__ __forceinline__ void input_task(const InputArgs& I) {
     int cur = *I.cursor;
     for (;;) {
         const int idx = cur + static_cast<int>(threadIdx.x);
@@ -1131,6 +1132,11 @@ __global__ void __launch_bounds__(kBlock) k_input(InputArgs I) {
     }
     if (threadIdx.x == 0) *I.cursor = cur;
 }
+
+__global__ void __launch_bounds__(kBlock) k_input(InputArgs I) { input_task(I); }
+
+// one workgroup per cell group
+__global__ void __launch_bounds__(kBlock) k_input_set(InputSet S) { input_task(S.a[blockIdx.x]); }
 
 // The delivery loop of step k (simulate.cpp:916-939) for the NetStims that receive
 // events, in one workgroup.  Pass r hands each instance the events that reach it in
@@ -1371,17 +1377,14 @@ store:
 // used the count it read), and the last one empties the slot, so a second launch for
 // the same step (finitialize's, then the first step's) delivers only what was pushed
 // in between.
-__global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
-    if (static_cast<int>(blockIdx.x) >= D.ndeliver) {      // the VecPlay task's blocks
-        vecplay_item(D.vp, D.nvp, D.t_vp, 1, (blockIdx.x - D.ndeliver) * blockDim.x + threadIdx.x);
-        return;
-    }
-    const int slot = D.k & (D.ring.nslot - 1);
-    int cnt = D.ring.count[slot];
-    if (cnt > D.ring.cap) cnt = D.ring.cap;
-    const long long off = static_cast<long long>(slot) * D.ring.cap;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < cnt; e += D.ndeliver * blockDim.x) {
-        const int packed = D.ring.entry[off + e];
+// Block b of the nb blocks delivering ring R's slot of step D.k.
+__device__ __forceinline__ void deliver_task(const DeliverArgs& D, const EventRing& R, int b, int nb) {
+    const int slot = D.k & (R.nslot - 1);
+    int cnt = R.count[slot];
+    if (cnt > R.cap) cnt = R.cap;
+    const long long off = static_cast<long long>(slot) * R.cap;
+    for (int e = b * blockDim.x + threadIdx.x; e < cnt; e += nb * blockDim.x) {
+        const int packed = R.entry[off + e];
         const int type = target_kind(packed);
         const int inst = packed & 0x3fffffff;
         if (type == 0) {
@@ -1400,10 +1403,28 @@ __global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0 && (D.ndeliver == 1 || atomicAdd(D.ring.done, 1u) == D.ndeliver - 1u)) {
-        D.ring.count[slot] = 0;
-        if (D.ndeliver > 1) *D.ring.done = 0u;
+    if (threadIdx.x == 0 && (nb == 1 || atomicAdd(R.done, 1u) == nb - 1u)) {
+        R.count[slot] = 0;
+        if (nb > 1) *R.done = 0u;
     }
+}
+
+__global__ void __launch_bounds__(1024) k_deliver(DeliverArgs D) {
+    if (static_cast<int>(blockIdx.x) >= D.ndeliver) {      // the VecPlay task's blocks
+        vecplay_item(D.vp, D.nvp, D.t_vp, 1, (blockIdx.x - D.ndeliver) * blockDim.x + threadIdx.x);
+        return;
+    }
+    deliver_task(D, D.ring, blockIdx.x, D.ndeliver);
+}
+
+// D.ndeliver blocks per ring of S, then the VecPlay task's blocks
+__global__ void __launch_bounds__(1024) k_deliver_set(DeliverArgs D, RingSet S) {
+    const int g = static_cast<int>(blockIdx.x) / D.ndeliver;
+    if (g >= S.n) {
+        vecplay_item(D.vp, D.nvp, D.t_vp, 1, (blockIdx.x - S.n * D.ndeliver) * blockDim.x + threadIdx.x);
+        return;
+    }
+    deliver_task(D, S.r[g], blockIdx.x - g * D.ndeliver, D.ndeliver);
 }
 
 __global__ void k_vecplay(VecPlayDev* items, int n, double t, int do_play) {
@@ -1663,6 +1684,18 @@ void launch_deliver(const DeliverArgs& a, int nblk, hipStream_t s) {
     d.ndeliver = std::max(1, nblk);
     const int nvp_blk = d.nvp > 0 ? (d.nvp + 1023) / 1024 : 0;
     hipLaunchKernelGGL(k_deliver, dim3(d.ndeliver + nvp_blk), dim3(1024), 0, s, d);
+}
+
+void launch_input_set(const InputSet& a, hipStream_t s) {
+    if (a.n > 0) hipLaunchKernelGGL(k_input_set, dim3(a.n), dim3(kBlock), 0, s, a);
+}
+
+void launch_deliver_set(const DeliverArgs& a, const RingSet& rings, int nblk, hipStream_t s) {
+    if (rings.n <= 0) return;
+    DeliverArgs d = a;
+    d.ndeliver = std::max(1, nblk);
+    const int nvp_blk = d.nvp > 0 ? (d.nvp + 1023) / 1024 : 0;
+    hipLaunchKernelGGL(k_deliver_set, dim3(d.ndeliver * rings.n + nvp_blk), dim3(1024), 0, s, d, rings);
 }
 
 void launch_vecplay(VecPlayDev* items, int n, double t, int do_play, hipStream_t s) {

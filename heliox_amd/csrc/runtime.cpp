@@ -681,6 +681,9 @@ struct hx_sim {
     // vp_t >= 0: the delivery launch also runs VecPlay at time vp_t (and returns true)
     bool launch_events(int kk, double tk, double vp_t = -1.0);
     bool launch_events_group(int g, int kk, double tk, hipStream_t on, double vp_t = -1.0);
+    InputArgs input_args(int g, int kk, double tk) const;
+    DeliverArgs deliver_args(int kk, double vp_t) const;
+    int deliver_blocks(int cap) const { return pre_fanout_empty ? 1 : std::min(64, (cap + 8191) / 8192); }
     void launch_detect(int kk, double tk);
     void launch_record();
     void build_groups(const std::vector<std::vector<std::pair<int, double>>>& vs_fo, long long ntgt);
@@ -2134,6 +2137,25 @@ void hx_sim::launch_plugin_states(double tcur) {
 }
 
 bool hx_sim::launch_events(int kk, double tk, double vp_t) {
+    const int G = static_cast<int>(groups.size());
+    if (G > 1 && G <= kMaxMergedGroups && nsa.n == 0 && !has_postsyn_plugins()) {
+        // the groups share the library stream: one input and one delivery launch for all
+        // of them (each group keeps its own trains, cursor and ring)
+        if (!mech[M_EXPSYN].present && !mech[M_EXP2SYN].present) return false;
+        tbegin(T_EVENTS, stream);
+        InputSet in{};
+        RingSet rs{};
+        int cap = 0;
+        for (int g = 0; g < G; ++g) {
+            if (groups[g].n_in > 0) in.a[in.n++] = input_args(g, kk, tk);
+            rs.r[rs.n++] = groups[g].ring;
+            cap = std::max(cap, groups[g].ring.cap);
+        }
+        launch_input_set(in, stream);
+        launch_deliver_set(deliver_args(kk, vp_t), rs, deliver_blocks(cap), stream);
+        tend(T_EVENTS, stream);
+        return vp_t >= 0.0;
+    }
     bool vp_done = false;
     for (int g = 0; g < static_cast<int>(groups.size()); ++g)
         vp_done |= launch_events_group(g, kk, tk, stream, g == 0 ? vp_t : -1.0);
@@ -2147,24 +2169,7 @@ bool hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, doubl
     if (!syn && nsa.n == 0) return false;
     CellGroup& cg = groups[g];
     tbegin(T_EVENTS, on);
-    if (cg.n_in > 0) {
-        InputArgs I{};
-        I.eff_time = cg.d_in_time;
-        I.inst = cg.d_in_inst;
-        I.round = cg.d_in_round;
-        I.ib = nsa.ib;
-        I.n = cg.n_in;
-        I.cursor = cg.d_in_cursor;
-        I.tcut = tk + dt / 2;
-        I.t = tk;
-        I.k = kk;
-        I.fo = FanOut{cg.d_vs_fo_begin, cg.d_vs_fo_target, cg.d_vs_fo_delay};
-        I.ring = cg.ring;
-        I.ttab = d_ttab;
-        I.kmax = static_cast<int>(ttab.size()) - 1;
-        I.half_dt = dt / 2;
-        launch_input(I, on);
-    }
+    if (cg.n_in > 0) launch_input(input_args(g, kk, tk), on);
     if (nsa.n > 0) {                 // NetStims receiving events: one group, the main stream
         NsArgs A = nsa;
         A.ring = cg.ring;
@@ -2179,8 +2184,47 @@ bool hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, doubl
         tend(T_EVENTS, on);
         return false;
     }
-    DeliverArgs D{};
+    DeliverArgs D = deliver_args(kk, vp_t);
     D.ring = cg.ring;
+    // Workgroups: spike-driven netcons can put up to a whole fan-out of every cell into
+    // one step, so a burst is spread over one 1024-thread workgroup per 8192 entries of
+    // slot capacity (at most 64); with only VecStim inputs a step's events are few, and
+    // one workgroup starts soonest beside the other cell group's kernels (measured:
+    // config 3 ran 2.5% slower with the grid and a merged input kernel, and 3% slower
+    // with 256-thread workgroups).
+    launch_deliver(D, deliver_blocks(cg.ring.cap), on);
+    // the synapse plugins' NET_RECEIVE of what was counted (one group: plugins couple the model)
+    for (const auto& p : plugins)
+        if (p.slot >= 0) p.meta->launch_receive(plugin_args(p, tk), on);
+    tend(T_EVENTS, on);
+    return vp_t >= 0.0;
+}
+
+// Group g's VecStim input of step kk (time tk).
+InputArgs hx_sim::input_args(int g, int kk, double tk) const {
+    const CellGroup& cg = groups[g];
+    InputArgs I{};
+    I.eff_time = cg.d_in_time;
+    I.inst = cg.d_in_inst;
+    I.round = cg.d_in_round;
+    I.ib = nsa.ib;
+    I.n = cg.n_in;
+    I.cursor = cg.d_in_cursor;
+    I.tcut = tk + dt / 2;
+    I.t = tk;
+    I.k = kk;
+    I.fo = FanOut{cg.d_vs_fo_begin, cg.d_vs_fo_target, cg.d_vs_fo_delay};
+    I.ring = cg.ring;
+    I.ttab = d_ttab;
+    I.kmax = static_cast<int>(ttab.size()) - 1;
+    I.half_dt = dt / 2;
+    return I;
+}
+
+// The delivery of step kk without its ring; VecPlay at vp_t on blocks of its own when
+// vp_t >= 0.
+DeliverArgs hx_sim::deliver_args(int kk, double vp_t) const {
+    DeliverArgs D{};
     D.k = kk;
     D.es = mech[M_EXPSYN].dev;
     D.e2 = mech[M_EXP2SYN].dev;
@@ -2193,24 +2237,12 @@ bool hx_sim::launch_events_group(int g, int kk, double tk, hipStream_t on, doubl
         D.log = d_tape_ev + static_cast<size_t>(tape_n) * tape_evcap;
         D.log_cap = tape_evcap;
     }
-    // Workgroups: spike-driven netcons can put up to a whole fan-out of every cell into
-    // one step, so a burst is spread over one 1024-thread workgroup per 8192 entries of
-    // slot capacity (at most 64); with only VecStim inputs a step's events are few, and
-    // one workgroup starts soonest beside the other cell group's kernels (measured:
-    // config 3 ran 2.5% slower with the grid and a merged input kernel, and 3% slower
-    // with 256-thread workgroups).
-    const int nblk = pre_fanout_empty ? 1 : std::min(64, (cg.ring.cap + 8191) / 8192);
     if (vp_t >= 0.0) {
         D.vp = d_vecplay;
         D.nvp = static_cast<int>(vecplay.size());
         D.t_vp = vp_t;
     }
-    launch_deliver(D, nblk, on);
-    // the synapse plugins' NET_RECEIVE of what was counted (one group: plugins couple the model)
-    for (const auto& p : plugins)
-        if (p.slot >= 0) p.meta->launch_receive(plugin_args(p, tk), on);
-    tend(T_EVENTS, on);
-    return vp_t >= 0.0;
+    return D;
 }
 
 // Threshold detection of detectors [pre0, pre1) at step kk (time tk), fanning out into

@@ -49,6 +49,34 @@ def test_groups_match_single_stream_and_oracle(gpu_lib, config, ncell, tstop):
     compare_spikes(o, multi, spec.dt)
 
 
+@pytest.mark.parametrize("config,ncell,tstop", [(2, 24, 30.0), (5, 40, 30.0)])
+def test_groups_on_one_stream_share_event_launches(gpu_lib, config, ncell, tstop):
+    """Cell groups issued on the library stream (group streams off, as under taping) take
+    their VecStim input and delivery in one launch each: the same bits as the groups on
+    their own streams and as one group."""
+    spec = build_config(config, ncell, tstop)
+    mons = [("global", "v", c) for c in range(ncell)]
+    print(f"case shared event launches config={config} ncell={ncell}", flush=True)
+    out = []
+    for groups, streams in ((0, False), (0, True), (1, True)):
+        g = Sim()
+        g.set_cell_groups(groups)
+        g.load_model_from_spec(dataclasses.replace(spec, monitors=list(mons)))
+        g.set_group_streams(streams)
+        g.finitialize(-65.0)
+        g.run(tstop)
+        assert g.info("multi_stream") == int(groups == 0 and streams)
+        out.append(g)
+    assert out[0].info("cell_groups") > 1
+    for other in out[1:]:
+        assert np.array_equal(out[0].traces(), other.traces())
+        for mech, col in (("ExpSyn", "g"), ("Exp2Syn", "A"), ("Exp2Syn", "B")):
+            if mech in spec.mechs:
+                assert np.array_equal(out[0].get_array(mech, col), other.get_array(mech, col)), (mech, col)
+        a, b = out[0].spikes(), other.spikes()
+        assert sorted(zip(a[0], a[1])) == sorted(zip(b[0], b[1]))
+
+
 def test_groups_fall_back_to_one_stream_with_state_monitors(gpu_lib):
     spec = build_config(2, 24, 10.0)
     mons = [("global", "v", 0), ("hh", "m", 3)]
