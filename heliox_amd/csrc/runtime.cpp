@@ -308,6 +308,8 @@ struct hx_sim {
     int fusion_allowed = 1;
     int dense_steady = 1;                      // compile-time node-kernel instances for steady steps
     long long steady_launches = 0;             // node-kernel launches that ran such an instance
+    hipEvent_t mech_end_mark = nullptr;        // the last mechanism pass's node-kernel timer end, if
+                                               // nothing was launched after it (else nullptr)
     int* d_syn_grp[2] = {nullptr, nullptr};   // adjoint: node -> ExpSyn / Exp2Syn group
     // adjoint loss: nodes and targets per call, the distinct nodes with their loss
     // indices (node -> first index of its list), and node -> loss index when distinct
@@ -427,6 +429,7 @@ struct hx_sim {
         hipStream_t s = nullptr;
         hipEvent_t done = nullptr;
         hipEvent_t pass = nullptr;                // this group's node pass of the latest step issued
+        hipEvent_t pass_mark = nullptr;           // what marks it: `pass`, or the node-kernel timer's end
     };
     std::vector<CellGroup> groups;                // one group unless the model decouples
     int group_request = 0;                        // hx_set_cell_groups (0: automatic)
@@ -645,10 +648,13 @@ struct hx_sim {
         tm.pending.push_back({static_cast<int>(tm.used), static_cast<int>(tm.used + 1)});
         tm.used += 2;
     }
-    void tend(int id, hipStream_t on = nullptr) {
-        if (!profiling || !(prof_mask & (1u << id))) return;
+    // returns the event recorded (nullptr when the class is not timed)
+    hipEvent_t tend(int id, hipStream_t on = nullptr) {
+        if (!profiling || !(prof_mask & (1u << id))) return nullptr;
         Timer& tm = timers[id];
-        HXC(hipEventRecord(tm.pool[tm.pending.back().second], on ? on : stream));
+        hipEvent_t e = tm.pool[tm.pending.back().second];
+        HXC(hipEventRecord(e, on ? on : stream));
+        return e;
     }
     void tcollect() {
         for (auto& tm : timers) {
@@ -2048,7 +2054,7 @@ void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp
     } else if (dense_mask) {
         steady_launches += launch_dense(A, s, dense_steady != 0);
     }
-    tend(T_MECH, s);
+    mech_end_mark = tend(T_MECH, s);
     bool any_sparse = false;
     for (int id : kSparseOrder) any_sparse |= mech[id].present && !(dense_mask & (1u << id));
     if (!any_sparse) return;
@@ -2060,6 +2066,7 @@ void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp
         }
         launch_sparse(id, B, s);
     };
+    mech_end_mark = nullptr;        // launches follow the node kernel's timer end
     tbegin(T_SPARSE, s);
     // an ion's kernel only zeroes its current (and makes erev under style 0100): nothing
     // to do in a state pass, nor in a stepping current pass when hh stores its ions
@@ -2489,10 +2496,16 @@ void hx_sim::step_once_groups() {
             // 10-15 us ahead; with the delivery after the wait as well the step was 1% slower)
             launch_events_group(g, k, tk, s);
             record();
-            if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass, 0));
-            else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass, 0));
+            if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass_mark, 0));
+            else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass_mark, 0));
             launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
-            HXC(hipEventRecord(cg.pass, s));
+            // the next group waits for this mark; when the node kernel is timed, the timer's end
+            // event (the last thing the pass recorded) marks the same point, one record fewer
+            cg.pass_mark = mech_end_mark;
+            if (!cg.pass_mark) {
+                HXC(hipEventRecord(cg.pass, s));
+                cg.pass_mark = cg.pass;
+            }
         } else {
             if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
             launch_events_group(g, k, tk, s);
