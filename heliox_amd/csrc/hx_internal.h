@@ -505,8 +505,11 @@ inline size_t solve_lds_bytes(int max_chunks) {
 
 // launch wrappers (kernels.hip)
 // steady: a launch whose flags are a steady step of a mechanism set with a compile-time
-// instance runs that instance (same bits as the generic kernel); returns whether it did
-bool launch_dense(const StepArgs& a, hipStream_t s, bool steady);
+// instance runs that instance (same bits as the generic kernel).  e0, e1 (may be null):
+// events set to the kernel's start and end as part of its dispatch (no marker of their
+// own on the stream).  Returns 0 if nothing was launched, 1 for the generic kernel, 2 for
+// a steady instance.
+int launch_dense(const StepArgs& a, hipStream_t s, bool steady, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_current(int mech, const StepArgs& a, hipStream_t s);
 void launch_point_electrodes(const StepArgs& a, const PointUnion& u, hipStream_t s);

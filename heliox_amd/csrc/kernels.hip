@@ -26,6 +26,8 @@
 //   k_vecplay, k_record, k_gap, init kernels.
 #include <algorithm>
 
+#include <hip/hip_ext.h>
+
 #include "hx_internal.h"
 #include "mech_math.h"
 #include "random123.h"
@@ -1529,16 +1531,16 @@ constexpr unsigned kMaskPas = 1u << M_PAS;
 constexpr unsigned kFoldES = 1u << M_EXPSYN, kFoldE2 = 1u << M_EXP2SYN;
 
 template <unsigned MASK>
-bool launch_steady(const StepArgs& a, dim3 grid, hipStream_t s) {
+bool launch_steady(const StepArgs& a, dim3 grid, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
     for (unsigned fold : {0u, kFoldES, kFoldE2, kFoldES | kFoldE2}) {
         if (fold == 0u && is_steady<MASK, 0u>(a))
-            hipLaunchKernelGGL((k_dense_steady<MASK, 0u>), grid, dim3(kBlock), 0, s, a);
+            hipExtLaunchKernelGGL((k_dense_steady<MASK, 0u>), grid, dim3(kBlock), 0, s, e0, e1, 0, a);
         else if (fold == kFoldES && is_steady<MASK, kFoldES>(a))
-            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldES>), grid, dim3(kBlock), 0, s, a);
+            hipExtLaunchKernelGGL((k_dense_steady<MASK, kFoldES>), grid, dim3(kBlock), 0, s, e0, e1, 0, a);
         else if (fold == kFoldE2 && is_steady<MASK, kFoldE2>(a))
-            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldE2>), grid, dim3(kBlock), 0, s, a);
+            hipExtLaunchKernelGGL((k_dense_steady<MASK, kFoldE2>), grid, dim3(kBlock), 0, s, e0, e1, 0, a);
         else if (fold == (kFoldES | kFoldE2) && is_steady<MASK, kFoldES | kFoldE2>(a))
-            hipLaunchKernelGGL((k_dense_steady<MASK, kFoldES | kFoldE2>), grid, dim3(kBlock), 0, s, a);
+            hipExtLaunchKernelGGL((k_dense_steady<MASK, kFoldES | kFoldE2>), grid, dim3(kBlock), 0, s, e0, e1, 0, a);
         else
             continue;
         return true;
@@ -1546,12 +1548,13 @@ bool launch_steady(const StepArgs& a, dim3 grid, hipStream_t s) {
     return false;
 }
 
-bool launch_dense(const StepArgs& a, hipStream_t s, bool steady) {
-    if (a.N - a.node0 <= 0) return false;
+int launch_dense(const StepArgs& a, hipStream_t s, bool steady, hipEvent_t e0, hipEvent_t e1) {
+    if (a.N - a.node0 <= 0) return 0;
     const dim3 grid = grid_for(a.N - a.node0);
-    if (steady && (launch_steady<kMaskPyr>(a, grid, s) || launch_steady<kMaskPas>(a, grid, s))) return true;
-    hipLaunchKernelGGL(k_dense, grid, dim3(kBlock), 0, s, a);
-    return false;
+    if (steady && (launch_steady<kMaskPyr>(a, grid, s, e0, e1) || launch_steady<kMaskPas>(a, grid, s, e0, e1)))
+        return 2;
+    hipExtLaunchKernelGGL(k_dense, grid, dim3(kBlock), 0, s, e0, e1, 0, a);
+    return 1;
 }
 
 void launch_sparse(int mech, const StepArgs& a, hipStream_t s) {

@@ -648,6 +648,27 @@ struct hx_sim {
         tm.pending.push_back({static_cast<int>(tm.used), static_cast<int>(tm.used + 1)});
         tm.used += 2;
     }
+    // A start/end pair for a launch that sets them itself as part of its dispatch
+    // (hipExtLaunchKernel): false, and no events, when the class is not timed.  The pair
+    // counts once tcommit says the launch happened.
+    bool treserve(int id, hipEvent_t& e0, hipEvent_t& e1) {
+        e0 = e1 = nullptr;
+        if (!profiling || !(prof_mask & (1u << id))) return false;
+        Timer& tm = timers[id];
+        while (tm.pool.size() < tm.used + 2) {
+            hipEvent_t e;
+            HXC(hipEventCreate(&e));
+            tm.pool.push_back(e);
+        }
+        e0 = tm.pool[tm.used];
+        e1 = tm.pool[tm.used + 1];
+        return true;
+    }
+    void tcommit(int id) {
+        Timer& tm = timers[id];
+        tm.pending.push_back({static_cast<int>(tm.used), static_cast<int>(tm.used + 1)});
+        tm.used += 2;
+    }
     // returns the event recorded (nullptr when the class is not timed)
     hipEvent_t tend(int id, hipStream_t on = nullptr) {
         if (!profiling || !(prof_mask & (1u << id))) return nullptr;
@@ -2048,13 +2069,14 @@ void hx_sim::launch_mech_pass(int do_state, int do_current, double tcur, int grp
         A.m[M_EXPSYN].blk_begin = cg->d_blk_es;
         A.m[M_EXP2SYN].blk_begin = cg->d_blk_e2;
     }
-    tbegin(T_MECH, s);
-    if (do_current) {
-        steady_launches += launch_dense(A, s, dense_steady != 0);
-    } else if (dense_mask) {
-        steady_launches += launch_dense(A, s, dense_steady != 0);
-    }
-    mech_end_mark = tend(T_MECH, s);
+    // the node kernel's timer events are set by its own dispatch, with no marker packets
+    // around it; the end event then also marks the pass for the cell groups' turns
+    hipEvent_t e0, e1;
+    const bool timed = treserve(T_MECH, e0, e1);
+    const int launched = (do_current || dense_mask) ? launch_dense(A, s, dense_steady != 0, e0, e1) : 0;
+    if (launched == 2) ++steady_launches;
+    if (timed && launched) tcommit(T_MECH);
+    mech_end_mark = timed && launched ? e1 : nullptr;
     bool any_sparse = false;
     for (int id : kSparseOrder) any_sparse |= mech[id].present && !(dense_mask & (1u << id));
     if (!any_sparse) return;
@@ -2499,8 +2521,8 @@ void hx_sim::step_once_groups() {
             if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass_mark, 0));
             else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass_mark, 0));
             launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
-            // the next group waits for this mark; when the node kernel is timed, the timer's end
-            // event (the last thing the pass recorded) marks the same point, one record fewer
+            // the next group waits for this mark; when the node kernel is timed, its end event
+            // (set by the kernel's dispatch, nothing launched after it) marks the same point
             cg.pass_mark = mech_end_mark;
             if (!cg.pass_mark) {
                 HXC(hipEventRecord(cg.pass, s));
