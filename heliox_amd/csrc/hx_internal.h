@@ -267,6 +267,14 @@ struct VecPlayDev;
 
 // The work after a step's solve, one launch (k_after_solve); the launcher sets the
 // block offsets from the counts.  A task with no items gets no blocks.
+// Up to kTapeSegs device-to-device copies in one launch (a step's tape row).
+constexpr int kTapeSegs = 8;
+struct TapeCopy {
+    const double* src[kTapeSegs];
+    double* dst[kTapeSegs];
+    long long n[kTapeSegs];
+    int nseg;
+};
 struct AfterSolve {
     int b_ptr, b_spike, b_vp, b_es, b_e2;   // first block of each task (gap transfers from 0)
     const double* v;
@@ -288,6 +296,13 @@ struct AfterSolve {
     const double *e2_tau1, *e2_tau2;
     int e20, e21;
     double dt;
+    // the adjoint tape's row of the step (nseg 0: none): the segments are copied on blocks
+    // of their own; the synapse states, which the decay tasks change, are taped by those
+    // tasks before they decay them (es_tape[j], e2_tape_a[j], e2_tape_b[j]; null: not taped)
+    TapeCopy tape;
+    double* es_tape;
+    double *e2_tape_a, *e2_tape_b;
+    int b_tape;
 };
 
 struct InputArgs {
@@ -540,14 +555,6 @@ void launch_gap(const double* v, const int* src_node, double* vgap_col, const in
                 hipStream_t s);
 void launch_clear_ints(int* p, long long n, hipStream_t s);
 void launch_status(const StatusArgs& a, hipStream_t s);
-// Up to kTapeSegs device-to-device copies in one launch (a step's tape row).
-constexpr int kTapeSegs = 8;
-struct TapeCopy {
-    const double* src[kTapeSegs];
-    double* dst[kTapeSegs];
-    long long n[kTapeSegs];
-    int nseg;
-};
 void launch_tape(const TapeCopy& t, hipStream_t s);
 void launch_copy_ptrs(double* const* src, double* const* dst, int n, hipStream_t s);
 

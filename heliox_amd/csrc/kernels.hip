@@ -1453,14 +1453,27 @@ __global__ void __launch_bounds__(kBlock) k_after_solve(AfterSolve P) {
         vecplay_item(P.vp, P.nvp, P.t, 0, (b - P.b_vp) * kBlock + tid);
     } else if (b < P.b_e2) {
         const int j = P.es0 + (b - P.b_es) * kBlock + tid;
-        if (j < P.es1) P.es_g[j] = expsyn_decay(P.es_g[j], P.es_tau[j], P.dt);
-    } else {
+        if (j < P.es1) {
+            const double g = P.es_g[j];
+            if (P.es_tape) P.es_tape[j] = g;
+            P.es_g[j] = expsyn_decay(g, P.es_tau[j], P.dt);
+        }
+    } else if (b < P.b_tape) {
         const int j = P.e20 + (b - P.b_e2) * kBlock + tid;
         if (j < P.e21) {
             const double aa = P.e2_a[j], bb = P.e2_b[j];
+            if (P.e2_tape_a) {
+                P.e2_tape_a[j] = aa;
+                P.e2_tape_b[j] = bb;
+            }
             P.e2_a[j] = exp2syn_decay(aa, P.e2_tau1[j], P.dt);
             P.e2_b[j] = exp2syn_decay(bb, P.e2_tau2[j], P.dt);
         }
+    } else {
+        const long long i = static_cast<long long>(b - P.b_tape) * kBlock + tid;
+        const long long stride = static_cast<long long>(gridDim.x - P.b_tape) * kBlock;
+        for (int sg = 0; sg < P.tape.nseg; ++sg)
+            for (long long j = i; j < P.tape.n[sg]; j += stride) P.tape.dst[sg][j] = P.tape.src[sg][j];
     }
 }
 
@@ -1592,7 +1605,10 @@ void launch_after_solve(AfterSolve p, hipStream_t s) {
     p.b_vp = p.b_spike + nb(p.S.npre);
     p.b_es = p.b_vp + nb(p.nvp);
     p.b_e2 = p.b_es + nb(p.es1 - p.es0);
-    const int end = p.b_e2 + nb(p.e21 - p.e20);
+    p.b_tape = p.b_e2 + nb(p.e21 - p.e20);
+    long long most = 0;
+    for (int k = 0; k < p.tape.nseg; ++k) most = std::max(most, p.tape.n[k]);
+    const int end = p.b_tape + static_cast<int>(std::min<long long>(nb(most), 4096));
     if (end > 0) hipLaunchKernelGGL(k_after_solve, dim3(end), dim3(kBlock), 0, s, p);
 }
 

@@ -570,6 +570,7 @@ struct hx_sim {
         tape_cap = 0;
     }
     void tape_record();
+    TapeCopy tape_row(bool syn) const;
     double grad_sq(int which);
     // profiling
     bool profiling = false;
@@ -2401,11 +2402,17 @@ void hx_sim::require_sample_point(const Ref& r) {
 // One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
 // have been detected (end of the previous step or finitialize).
 void hx_sim::tape_record() {
+    launch_tape(tape_row(true), stream);
+    ++tape_n;
+}
+
+// The next tape row's copies (the synapse states among them when syn, else the decay
+// tasks of the after-solve launch tape those).
+TapeCopy hx_sim::tape_row(bool syn) const {
     if (tape_n >= tape_cap)
         throw std::runtime_error("adjoint tape full (" + std::to_string(tape_cap) + " steps): call hx_tape_begin "
                                  "with more steps");
     const size_t n = static_cast<size_t>(tape_n);
-    // the step's row: one launch copies every segment
     TapeCopy T{};
     auto seg = [&](const double* src, double* dst, long long cnt) {
         T.src[T.nseg] = src;
@@ -2418,7 +2425,7 @@ void hx_sim::tape_record() {
         const MechDev& h = mech[M_HH].dev;   // columns m, h, n are consecutive
         seg(h.col(HH_M), d_tape_x + n * 3 * h.stride, 3 * h.stride);
     }
-    if (mech[M_EXPSYN].present && mech[M_EXPSYN].n > 0) {
+    if (syn && mech[M_EXPSYN].present && mech[M_EXPSYN].n > 0) {
         const MechDev& e = mech[M_EXPSYN].dev;
         seg(e.col(ES_G), d_tape_g + n * e.n, e.n);
     }
@@ -2434,13 +2441,12 @@ void hx_sim::tape_record() {
         const MechDev& ca = mech[M_CA_ION].dev;
         seg(ca.col(ION_CONCI), d_tape_cai + n * ca.n, ca.n);
     }
-    if (d_tape_ab) {
+    if (syn && d_tape_ab) {
         const MechDev& e = mech[M_EXP2SYN].dev;
         seg(e.col(E2_A), d_tape_ab + n * 2 * e.n, e.n);
         seg(e.col(E2_B), d_tape_ab + (n * 2 + 1) * e.n, e.n);
     }
-    launch_tape(T, stream);
-    ++tape_n;
+    return T;
 }
 
 // Gap transfers after the update (and at finitialize): the model's HalfGap
@@ -2620,12 +2626,12 @@ void hx_sim::step_once() {
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
-    if (tape_on) tape_record();
     // gap transfers, detection of the next step (spike_deliver detects on v_{k}), VecPlay
     // at the step's end and the synapses' decay: one launch when VecPlay writes only IClamp
     // variables, which none of the others touch, and no transfer added at run time (which
-    // may name any variable) is in the step
+    // may name any variable) is in the step; the step's tape row then rides on it too
     const bool one_launch = (!has_vp || vecplay_iclamp_only) && dg_src.empty();
+    if (tape_on && !one_launch) tape_record();
     if (!one_launch) launch_gap_transfers();
     // t += dt/2 twice, exactly as the reference accumulates it
     double tn = tk;
@@ -2635,8 +2641,20 @@ void hx_sim::step_once() {
     k += 1;
     if (one_launch) {
         upload_gap_ptrs();
+        AfterSolve P = after_solve_args(t, k, -1);
+        if (tape_on) {
+            const size_t n = static_cast<size_t>(tape_n);
+            P.tape = tape_row(false);
+            if (P.es_g) P.es_tape = d_tape_g + n * mech[M_EXPSYN].dev.n;
+            if (P.e2_a && d_tape_ab) {
+                const size_t ne2 = static_cast<size_t>(mech[M_EXP2SYN].dev.n);
+                P.e2_tape_a = d_tape_ab + n * 2 * ne2;
+                P.e2_tape_b = d_tape_ab + (n * 2 + 1) * ne2;
+            }
+            ++tape_n;
+        }
         tbegin(T_SPIKE);
-        launch_after_solve(after_solve_args(t, k, -1), stream);
+        launch_after_solve(P, stream);
         tend(T_SPIKE);
     } else {
         launch_detect(k, t);
