@@ -343,6 +343,50 @@ __global__ void k_adj_after_nodes(AdjStep A) {
     if (q >= m.ngrp) return
 
 __global__ void k_adj_syn_state(AdjStep A) { HX_ADJ_SYN(M_EXPSYN); syn_state_at(A, j); }
+
+// Instance tasks side by side in one launch, each on its own run of blocks.  The host
+// puts tasks together only where their outputs are disjoint: at most one of them adds to
+// a node's lambda_v, the others write their mechanism's own adjoints and gradients.
+enum AdjTask : int { AT_HH_STATE, AT_SYN_STATE, AT_SYN2_STATE, AT_HH_PARAM, AT_PAS_PARAM, AT_SYN_PARAM, AT_SYN2_PARAM };
+constexpr int kAdjSideMax = 4;
+struct AdjSide {
+    int task[kAdjSideMax];
+    int begin[kAdjSideMax + 1];   // first block of each task, then the end
+    int n;
+};
+__global__ void __launch_bounds__(kBlock) k_adj_side(AdjStep A, AdjSide S) {
+    int t = 0;
+    while (t + 1 < S.n && static_cast<int>(blockIdx.x) >= S.begin[t + 1]) ++t;
+    const int j = (static_cast<int>(blockIdx.x) - S.begin[t]) * kBlock + static_cast<int>(threadIdx.x);
+    switch (S.task[t]) {
+        case AT_HH_STATE:
+            if (j < A.m[M_HH].n) {
+                const int node = A.m[M_HH].node[j];
+                A.lam_v[node] += hh_state_at(A, j, node);
+            }
+            break;
+        case AT_SYN_STATE:
+            if (j < A.m[M_EXPSYN].n) syn_state_at(A, j);
+            break;
+        case AT_SYN2_STATE:
+            if (j < A.m[M_EXP2SYN].n) syn2_state_at(A, j);
+            break;
+        case AT_HH_PARAM:
+            if (j < A.m[M_HH].n) hh_param_at(A, j, A.m[M_HH].node[j]);
+            break;
+        case AT_PAS_PARAM:
+            if (j < A.m[M_PAS].n) pas_param_at(A, j, A.m[M_PAS].node[j]);
+            break;
+        case AT_SYN_PARAM:
+            if (j < A.m[M_EXPSYN].n) syn_param_at(A, j);
+            break;
+        case AT_SYN2_PARAM:
+            if (j < A.m[M_EXP2SYN].n) syn2_param_at(A, j);
+            break;
+        default:
+            break;
+    }
+}
 __global__ void k_adj_syn2_state(AdjStep A) { HX_ADJ_SYN(M_EXP2SYN); syn2_state_at(A, j); }
 __global__ void k_adj_syn_param(AdjStep A) { HX_ADJ_SYN(M_EXPSYN); syn_param_at(A, j); }
 __global__ void k_adj_syn2_param(AdjStep A) { HX_ADJ_SYN(M_EXP2SYN); syn2_param_at(A, j); }
@@ -480,8 +524,45 @@ inline dim3 grid_of(long long n, int block = kBlock) {
 // written by it before the solve and by Ca_HVA after), so no two launches race.
 // The node-parallel kernels take the mechanisms in a.fuse_*; the rest keep their own
 // kernels, launched where each node's sums keep their order.
+static void launch_adj_before_nodes_and_cond(const AdjStep& a, hipStream_t s);
+static void launch_adj_events_and_gaps(const AdjStep& a, hipStream_t s);
+
+// Launches the tasks of S (blocks per task from the instance counts) as one k_adj_side.
+static void launch_side(const AdjStep& a, AdjSide S, hipStream_t s) {
+    auto count = [&](int task) {
+        switch (task) {
+            case AT_HH_STATE: case AT_HH_PARAM: return a.m[M_HH].n;
+            case AT_SYN_STATE: case AT_SYN_PARAM: return a.m[M_EXPSYN].n;
+            case AT_SYN2_STATE: case AT_SYN2_PARAM: return a.m[M_EXP2SYN].n;
+            case AT_PAS_PARAM: return a.m[M_PAS].n;
+            default: return 0;
+        }
+    };
+    int b = 0;
+    for (int t = 0; t < S.n; ++t) {
+        S.begin[t] = b;
+        b += (count(S.task[t]) + kBlock - 1) / kBlock;
+    }
+    S.begin[S.n] = b;
+    if (b > 0) hipLaunchKernelGGL(k_adj_side, dim3(b), dim3(kBlock), 0, s, a, S);
+}
+
 void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
     auto own = [&](int id, unsigned bit, unsigned fused) { return a.m[id].n > 0 && !(fused & bit); };
+    // hh's state adjoint (the only one adding to lambda_v here) and the synapses' decay
+    // adjoints side by side in one launch, when no other mechanism keeps its own kernels
+    if (!own(M_CAHVA, kAdjCaHVA, a.fuse_state) && !own(M_HDLA, kAdjHdla, a.fuse_state) &&
+        !own(M_CADYN, kAdjCaDyn, a.fuse_state) && !a.fold_syn) {
+        AdjSide S{};
+        if (own(M_HH, kAdjHH, a.fuse_state)) S.task[S.n++] = AT_HH_STATE;
+        if (a.m[M_EXPSYN].n > 0) S.task[S.n++] = AT_SYN_STATE;
+        if (a.m[M_EXP2SYN].n > 0) S.task[S.n++] = AT_SYN2_STATE;
+        if (S.n > 1) {
+            launch_side(a, S, s);
+            launch_adj_before_nodes_and_cond(a, s);
+            return;
+        }
+    }
     if (own(M_HH, kAdjHH, a.fuse_state)) hipLaunchKernelGGL(k_adj_hh_state, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
     if (own(M_CAHVA, kAdjCaHVA, a.fuse_state))
         hipLaunchKernelGGL(k_adj_cahva_state, grid_of(a.m[M_CAHVA].n), dim3(kBlock), 0, s, a);
@@ -494,6 +575,14 @@ void launch_adj_before_solve(const AdjStep& a, hipStream_t s) {
         hipLaunchKernelGGL(k_adj_syn_state, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
     if (!a.fold_syn && a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_state, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
+    (void)nsyn;
+    launch_adj_before_nodes_and_cond(a, s);
+}
+
+// The node-parallel kernel before the solve and the conductance kernels after it.
+static void launch_adj_before_nodes_and_cond(const AdjStep& a, hipStream_t s) {
+    auto own = [&](int id, unsigned bit, unsigned fused) { return a.m[id].n > 0 && !(fused & bit); };
+    const long long nsyn = a.fold_syn ? static_cast<long long>(a.m[M_EXPSYN].n) + a.m[M_EXP2SYN].n : 0;
     hipLaunchKernelGGL(k_adj_before_nodes, grid_of(a.N + nsyn), dim3(kBlock), 0, s, a);
     if (own(M_PAS, kAdjPas, a.fuse_cond))
         hipLaunchKernelGGL(k_adj_cond_pas, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
@@ -514,6 +603,20 @@ void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
     auto own = [&](int id, unsigned bit) { return a.m[id].n > 0 && !(a.fuse_param & bit); };
     const long long nsyn = a.fold_syn ? static_cast<long long>(a.m[M_EXPSYN].n) + a.m[M_EXP2SYN].n : 0;
     hipLaunchKernelGGL(k_adj_after_nodes, grid_of(a.N + nsyn), dim3(kBlock), 0, s, a);
+    // hh's and pas's parameter terms and the synapses' (none adds to lambda_v) side by side
+    // in one launch, when Ca_HVA and hd_la (which do) run in the node-parallel kernel or not at all
+    if (!own(M_CAHVA, kAdjCaHVA) && !own(M_HDLA, kAdjHdla) && !a.fold_syn) {
+        AdjSide S{};
+        if (own(M_HH, kAdjHH)) S.task[S.n++] = AT_HH_PARAM;
+        if (own(M_PAS, kAdjPas)) S.task[S.n++] = AT_PAS_PARAM;
+        if (a.m[M_EXPSYN].n > 0) S.task[S.n++] = AT_SYN_PARAM;
+        if (a.m[M_EXP2SYN].n > 0) S.task[S.n++] = AT_SYN2_PARAM;
+        if (S.n > 1) {
+            launch_side(a, S, s);
+            launch_adj_events_and_gaps(a, s);
+            return;
+        }
+    }
     if (own(M_HH, kAdjHH)) hipLaunchKernelGGL(k_adj_hh_param, grid_of(a.m[M_HH].n), dim3(kBlock), 0, s, a);
     if (own(M_PAS, kAdjPas)) hipLaunchKernelGGL(k_adj_pas_param, grid_of(a.m[M_PAS].n), dim3(kBlock), 0, s, a);
     if (own(M_CAHVA, kAdjCaHVA))
@@ -523,6 +626,11 @@ void launch_adj_after_solve(const AdjStep& a, hipStream_t s) {
         hipLaunchKernelGGL(k_adj_syn_param, grid_of(a.m[M_EXPSYN].n), dim3(kBlock), 0, s, a);
     if (!a.fold_syn && a.m[M_EXP2SYN].n > 0)
         hipLaunchKernelGGL(k_adj_syn2_param, grid_of(a.m[M_EXP2SYN].n), dim3(kBlock), 0, s, a);
+    launch_adj_events_and_gaps(a, s);
+}
+
+// The events' weight terms and the gap junctions' terms, after the parameter terms.
+static void launch_adj_events_and_gaps(const AdjStep& a, hipStream_t s) {
     if (a.m[M_EXPSYN].n > 0 || a.m[M_EXP2SYN].n > 0) hipLaunchKernelGGL(k_adj_events, dim3(1), dim3(256), 0, s, a);
     if (a.m[M_HALFGAP].n > 0) {
         hipLaunchKernelGGL(k_adj_gap_param, grid_of(a.m[M_HALFGAP].n), dim3(kBlock), 0, s, a);
