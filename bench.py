@@ -147,6 +147,14 @@ def perturb_config3(spec, seed: int = 1):
     return out
 
 
+def solver_options(sim, args):
+    """Tree-solve layout options of the command line (none changes a result)."""
+    if args.unit_cells:
+        sim.set_solve_unit_cells(args.unit_cells)
+    if args.solve_waves:
+        sim.set_solve_waves(args.solve_waves)
+
+
 def train_bench(args):
     """One differentiable training step = taped forward run, adjoint backward pass for the
     soma-v MSE against the perturbed model's trace, and one Adam step (lr 1e-3).
@@ -173,6 +181,7 @@ def train_bench(args):
     target = np.ascontiguousarray(tg.traces()[:, 1:].T)
     del tg
     g = Sim()
+    solver_options(g, args)
     g.load_model_from_spec(base, add_monitors=False)
     g.tape_begin(nstep)
     cell = base.cell_of_node()
@@ -314,6 +323,7 @@ def network_bench(args):
     dt = 0.025
     spec = build_config(4, args.network_cells, (args.warmup + args.steps + 10) * dt)
     sim = Sim()
+    solver_options(sim, args)
     sim.load_model_from_spec(spec, add_monitors=False)
     sim.finitialize(-65.0)
     sim.continue_run((args.warmup + 0.5) * dt)
@@ -339,7 +349,8 @@ def network_bench(args):
         "vs_baseline": None, "dtype": "f64", "data": "synthetic",
         "config": {"workload": f"config 4: {spec.ncell} cells x {spec.nnode // spec.ncell} compartments, "
                                f"{spec.netcons['ExpSyn'].inst.size} netcons, {spec.gap_src_node.size} gap halves, "
-                               f"{nvp} VecPlay items", "spikes_in_timed_steps": spikes},
+                               f"{nvp} VecPlay items", "spikes_in_timed_steps": spikes,
+                   "solve_unit_cells": sim.info("solve_unit_cells")},
         "kernel_times": kernels,
         "vecplay": {"items": nvp, "alg_bytes_per_launch": nvp * VECPLAY_BYTES_PER_ITEM}}))
 
@@ -447,10 +458,7 @@ def main():
     sim = Sim()
     sim.set_cell_groups(args.cell_groups)
     sim.set_solver_root(not args.model_root)
-    if args.unit_cells:
-        sim.set_solve_unit_cells(args.unit_cells)
-    if args.solve_waves:
-        sim.set_solve_waves(args.solve_waves)
+    solver_options(sim, args)
     if args.generic_node_kernel:
         sim.set_dense_steady(False)
     if args.no_group_turns:
