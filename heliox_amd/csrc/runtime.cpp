@@ -2575,6 +2575,11 @@ void hx_sim::step_once_groups() {
 }
 
 void hx_sim::step_once() {
+    // a full tape stops the call before the step issues anything, so the model stays at
+    // the last taped step
+    if (tape_on && tape_n >= tape_cap)
+        throw std::runtime_error("adjoint tape full (" + std::to_string(tape_cap) + " steps): call hx_tape_begin "
+                                 "with more steps");
     if (multi_stream) {
         step_once_groups();
         return;

@@ -220,3 +220,18 @@ def test_training_loop_holds_its_device_memory(problem):
     print(f"  free device memory before {free0} after {free1}", flush=True)
     assert free1 == free0
 
+
+def test_full_tape_stops_before_the_step(gpu_lib):
+    """A run longer than the tape stops at the first step that would not fit, before that
+    step issues anything: the tape holds its steps and the backward sweep runs on them."""
+    spec = build_config(5, 2, 5.0)
+    g = Sim()
+    g.load_model_from_spec(spec, add_monitors=False)
+    g.tape_begin(10)
+    g.finitialize(-65.0)
+    with pytest.raises(Exception, match="tape full"):
+        g.run(1.0)
+    assert g.tape_length() == 10
+    loss = g.adjoint(np.arange(spec.ncell), np.full((10, spec.ncell), -65.0))
+    assert np.isfinite(loss)
+    assert np.all(np.isfinite(g.gradient("pas", "g_pas")))
