@@ -2399,8 +2399,8 @@ void hx_sim::require_sample_point(const Ref& r) {
     }
 }
 
-// One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
-// have been detected (end of the previous step or finitialize).
+// The step's tape row (v after the solve and the states its current pass used), as one
+// launch of its own.
 void hx_sim::tape_record() {
     launch_tape(tape_row(true), stream);
     ++tape_n;
@@ -2574,6 +2574,8 @@ void hx_sim::step_once_groups() {
     state_pending = true;
 }
 
+// One Simulate::fadvance (simulate.cpp:410-442).  On entry spikes for step k
+// have been detected (end of the previous step or finitialize).
 void hx_sim::step_once() {
     // a full tape stops the call before the step issues anything, so the model stays at
     // the last taped step
