@@ -157,9 +157,9 @@ def test_handles_and_reinitialisation(gpu_lib):
     assert np.array_equal(first, g.traces())
 
 
-@pytest.mark.parametrize("config,ncell,nref", [(3, 2000, 3), (2, 10000, 4)])
+@pytest.mark.parametrize("config,ncell,nref", [(3, 2000, 3), (2, 10000, 4), (5, 1000, 4), (1, 1000, 6)])
 def test_full_size_prefix(gpu_lib, config, ncell, nref):
-    """Cells of configs 2 and 3 are independent, so the first cells of the
+    """Cells of configs 1, 2, 3 and 5 are independent, so the first cells of the
     full-size GPU model must match an oracle model of just those cells."""
     tstop = 5.0
     full = build_config(config, ncell, tstop)
@@ -178,7 +178,7 @@ def test_full_size_prefix(gpu_lib, config, ncell, nref):
     assert np.all(np.isfinite(v))
 
 
-@pytest.mark.parametrize("config,ncell", [(3, 2000), (2, 10000)])
+@pytest.mark.parametrize("config,ncell", [(3, 2000), (2, 10000), (5, 1000)])
 def test_full_size_cells_across_groups(gpu_lib, config, ncell):
     """At full size the cells run as two groups on two streams, in solve units of a few
     cells.  The first cell, the cells either side of the groups' boundary and the last two
