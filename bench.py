@@ -153,6 +153,8 @@ def solver_options(sim, args):
         sim.set_solve_unit_cells(args.unit_cells)
     if args.solve_waves:
         sim.set_solve_waves(args.solve_waves)
+    if args.solve_streamed:
+        sim.set_solve_resident(False)
 
 
 def train_bench(args):
@@ -412,6 +414,9 @@ def main():
                     help="cells per tree-solve wavefront (0: the library's choice)")
     ap.add_argument("--solve-waves", type=int, default=0,
                     help="tree-solve wavefronts per workgroup (0: the library's choice)")
+    ap.add_argument("--solve-streamed", action="store_true",
+                    help="stream every solve unit's rounds from HBM, also where the unit fits in LDS "
+                         "(same results)")
     ap.add_argument("--no-group-turns", action="store_true",
                     help="order the cell groups' node passes only on a run's first step (same results)")
     ap.add_argument("--generic-node-kernel", action="store_true",

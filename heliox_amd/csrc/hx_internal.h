@@ -186,6 +186,8 @@ struct SolveArgs {
     const double* b;
     int store_dx;                 // 1: leave D in d and x = vn - v in rhs (as the reference does); 0: neither
     int waves;                    // solve units per workgroup, one wavefront each (1..kSolveMaxWaves)
+    int res_nodes;                // > 0: each unit is solved held whole in LDS, sized for this many nodes
+    int res_rounds;               //   and this many rounds (the largest unit's); 0: rounds streamed from HBM
 };
 
 // Event ring: one slot per delivery step (mod nslot), fixed capacity per slot.
@@ -516,6 +518,20 @@ __host__ __device__ inline int solve_lds_doubles(int max_chunks) {
 }
 inline size_t solve_lds_bytes(int max_chunks) {
     return static_cast<size_t>(solve_lds_doubles(max_chunks)) * sizeof(double);
+}
+// A unit held whole in LDS: junction pairs, then one record of kStageArrays doubles per
+// node (max_nodes records, a neutral record and a sink record, rounded to an even count so
+// that what follows stays 16-byte aligned), the unit's round table (6 doubles a round) and
+// its chunk descriptors (one double each; a unit has one descriptor per chunk).  Units are
+// solved this way when this stays within kResUnitBudget, so four fit in a CU's 160 KB.
+constexpr size_t kResUnitBudget = 40 * 1024;
+__host__ __device__ inline int res_record_doubles(int max_nodes) { return ((max_nodes + 2) * kStageArrays + 1) & ~1; }
+__host__ __device__ inline int res_lds_doubles(int max_nodes, int max_chunks, int max_rounds) {
+    const int mc = max_chunks > 0 ? max_chunks : 1;
+    return (2 * mc + res_record_doubles(max_nodes) + 6 * max_rounds + mc + 1) & ~1;
+}
+inline size_t res_lds_bytes(int max_nodes, int max_chunks, int max_rounds) {
+    return static_cast<size_t>(res_lds_doubles(max_nodes, max_chunks, max_rounds)) * sizeof(double);
 }
 
 // launch wrappers (kernels.hip)

@@ -17,6 +17,8 @@
 //                    capacitance + axial assembly, the
 //                    Hines elimination over chunked unbranched runs, back
 //                    substitution and v update; junction values through LDS
+//   k_solve_res .... the same for units small enough to be held whole in LDS:
+//                    read once, solved in LDS records, written once
 //   k_spike ........ threshold detection, wave-ballot compaction into the spike
 //                    log, fan-out of deliveries into the device event ring
 //   k_input ........ VecStim trains (sorted on the host) entering the ring;
@@ -1039,6 +1041,211 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve(SolveArgs S, c
 }
 
 // ---------------------------------------------------------------------------
+// tree solve with the unit held in LDS
+// ---------------------------------------------------------------------------
+// A unit whose nodes, round table and descriptors fit kResUnitBudget of LDS (cells of a
+// few hundred nodes) is read from HBM once: d, rhs, a, b and v of each node go to one
+// 40-byte LDS record, elimination and back substitution run over the same rounds and
+// chunks as k_solve with s, w, the pivots and the new voltages kept in the records, and
+// the results are written once.  The per-chunk arithmetic and the order of every sum are
+// k_solve's, so the results are the same bits.  A round then waits on LDS instead of an
+// HBM round trip and has no staging, and s and w never go to HBM (48 instead of 80 bytes
+// per node).  A record's fields sit at fixed offsets, so one address serves a node's five
+// reads.
+
+// Node k of the lane's chunk reads record rp[k] (in doubles: record index x 5; the
+// neutral record past the chunk's length) and writes record wp[k] (the sink record past
+// the length, so that padding slots leave the neutral record as it is).
+struct ResIn {
+    const double* st;
+    const int* rp;
+    __device__ __forceinline__ FwdNode fwd(int k) const {
+        const double* r = st + rp[k];
+        return {r[SA_DB], r[SA_RM], r[SA_A], r[SA_B], r[SA_V]};
+    }
+    __device__ __forceinline__ BackNode back(int k) const {
+        const double* r = st + rp[k];
+        return {r[SA_RM], r[SA_A], 0.0};
+    }
+};
+
+template <int KM>
+__device__ __forceinline__ void res_positions(const RoundU& ri, int len, int lane, int neutral, int* rp, int* wp,
+                                              int& tp) {
+    tp = neutral * kStageArrays;
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        const int p = ri.node_base + ri.offset(k) + lane;
+        rp[k] = (k < len ? p : neutral) * kStageArrays;
+        wp[k] = (k < len ? p : neutral + 1) * kStageArrays;
+        if (k == len - 1) tp = p * kStageArrays;
+    }
+}
+
+// Round r's table entry (every lane reads the same 48 bytes) and the lane's descriptor.
+__device__ __forceinline__ RoundU res_round(const uint4* rtab, int r) {
+    const uint4* p = rtab + 3 * r;
+    return uniform_round(RoundV{p[0], p[1], p[2]});
+}
+__device__ __forceinline__ uint2 res_desc(const uint2* dtab, int ndesc, const RoundU& ri, int lane) {
+    const int top = ri.desc_count > 0 ? ri.desc_count - 1 : 0;
+    const int e = ri.desc_begin + (lane < top ? lane : top);
+    return dtab[e < ndesc ? e : ndesc - 1];    // padding rounds: any descriptor of the unit
+}
+
+constexpr int kResBatch = 4;    // nodes a lane moves per batch at the start and the end
+
+// One wavefront per unit, S.waves units per workgroup, each with its own LDS region.
+template <int kX>
+__global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs S, const RoundInfo* rounds_all,
+                                                                      const uint2* desc_all, int max_chunks) {
+    extern __shared__ double lds[];
+    const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int c = blockIdx.x * S.waves + wv;
+    if (c >= S.nunit) return;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int rb = S.unit_round_begin[c];
+    const int nround = S.unit_round_begin[c + 1] - rb;
+    const int db0 = S.unit_desc_begin[c];
+    const int ndesc = S.unit_desc_begin[c + 1] - db0;
+    const int nb = S.unit_node_begin[c];
+    const int nn = S.unit_node_begin[c + 1] - nb;
+    const int neutral = S.res_nodes;                  // the sink record is neutral + 1
+    double* slots = lds + static_cast<size_t>(wv) * res_lds_doubles(S.res_nodes, max_chunks, S.res_rounds);
+    double* st = slots + 2 * max_chunks;
+    uint4* rtab = reinterpret_cast<uint4*>(st + res_record_doubles(S.res_nodes));
+    uint2* dtab = reinterpret_cast<uint2*>(rtab + 3 * S.res_rounds);
+
+    // the unit's round table, descriptors and node records into LDS
+    {
+        const uint4* rsrc = reinterpret_cast<const uint4*>(rounds_all + rb);
+        for (int i = lane; i < 3 * nround; i += kWave) rtab[i] = rsrc[i];
+        for (int i = lane; i < ndesc; i += kWave) dtab[i] = desc_all[db0 + i];
+        const double* src[kStageArrays] = {S.d + nb, S.rhs + nb, S.a + nb, S.b + nb, S.v + nb};
+        for (int i0 = 0; i0 < nn; i0 += kWave * kResBatch) {
+            double x[kStageArrays][kResBatch];
+#pragma unroll
+            for (int j = 0; j < kResBatch; ++j) {
+                const int i = i0 + j * kWave + lane;
+                const int e = i < nn ? i : nn - 1;
+#pragma unroll
+                for (int q = 0; q < kStageArrays; ++q) x[q][j] = lds_(src[q] + e);
+            }
+#pragma unroll
+            for (int j = 0; j < kResBatch; ++j) {
+                const int i = i0 + j * kWave + lane;
+                if (i < nn) {
+#pragma unroll
+                    for (int q = 0; q < kStageArrays; ++q) st[i * kStageArrays + q] = x[q][j];
+                }
+            }
+        }
+        if (lane < 2 * kStageArrays) {     // the neutral record (db 1, the rest 0) and the sink
+            const int q = lane % kStageArrays;
+            st[(neutral + lane / kStageArrays) * kStageArrays + q] = q == SA_DB ? 1.0 : 0.0;
+        }
+    }
+    round_boundary();
+
+    // elimination, leaves to root: s to RM, w to A, the pivot D (kX) to DB
+    SlotPair* pairs = reinterpret_cast<SlotPair*>(slots);
+    for (int r = nround - 1; r >= 0; --r) {
+        const RoundU ri = res_round(rtab, r);
+        const uint2 q = res_desc(dtab, ndesc, ri, lane);
+        const bool act = lane < ri.desc_count;
+        const int slot = q.x & 0xFFFF;
+        const bool has_parent = (q.x >> 16) != kNone;
+        const int child_begin = q.y & 0xFFFF;
+        const int len = act ? (q.y >> 16) & 0xFF : 0;
+        const int nchild = act ? q.y >> 24 : 0;
+        double acd = 0.0, ace = 0.0;
+        if (nchild > 0) {
+            const SlotPair p0 = pairs[child_begin];
+            acd = p0.cd;
+            ace = p0.ce;
+            if (nchild > 1) {
+                const SlotPair p1 = pairs[child_begin + 1];
+                acd += p1.cd;
+                ace += p1.ce;
+                for (int ch = 2; ch < nchild; ++ch) {
+                    const SlotPair pc = pairs[child_begin + ch];
+                    acd += pc.cd;
+                    ace += pc.ce;
+                }
+            }
+        }
+        double cd, ce;
+        __builtin_amdgcn_s_setprio(3);
+        dispatch_chunk_bound(ri.maxlen, [&](auto km) {
+            constexpr int KM = decltype(km)::value;
+            int rp[KM], wp[KM], tp;
+            res_positions<KM>(ri, len, lane, neutral, rp, wp, tp);
+            if (nchild > 0) {
+                double db = st[tp + SA_DB], rm = st[tp + SA_RM];
+                tail_inject(db, rm, st[tp + SA_V], acd, ace);
+                st[tp + SA_DB] = db;
+                st[tp + SA_RM] = rm;
+            }
+            auto out = [&](int k, double D, double sv, double w) {
+                double* o = st + wp[k];
+                if constexpr (kX != 0) o[SA_DB] = D;
+                o[SA_RM] = sv;
+                o[SA_A] = w;
+            };
+            chunk_forward_math<KM>(has_parent, ResIn{st, rp}, out, rcp_nr, cd, ce);
+        });
+        __builtin_amdgcn_s_setprio(0);
+        if (act && has_parent) pairs[slot] = SlotPair{cd, ce};
+        round_boundary();
+    }
+
+    // back substitution, root to leaves: the new voltages to B (free after elimination)
+    for (int r = 0; r < nround; ++r) {
+        const RoundU ri = res_round(rtab, r);
+        const uint2 q = res_desc(dtab, ndesc, ri, lane);
+        const bool act = lane < ri.desc_count;
+        const int slot = q.x & 0xFFFF;
+        const int parent_slot = q.x >> 16;
+        const int len = act ? (q.y >> 16) & 0xFF : 0;
+        const double vpar = (act && parent_slot != kNone) ? slots[2 * parent_slot] : 0.0;
+        double vtail = 0.0;
+        __builtin_amdgcn_s_setprio(3);
+        dispatch_chunk_bound(ri.maxlen, [&](auto km) {
+            constexpr int KM = decltype(km)::value;
+            int rp[KM], wp[KM], tp;
+            res_positions<KM>(ri, len, lane, neutral, rp, wp, tp);
+            auto out = [&](int k, double vn, double) {
+                st[wp[k] + SA_B] = vn;
+                if (k == len - 1) vtail = vn;
+            };
+            chunk_back_math<KM>(ResIn{st, rp}, out, vpar);
+        });
+        __builtin_amdgcn_s_setprio(0);
+        if (act) slots[2 * slot] = vtail;   // the tail's new voltage
+        round_boundary();
+    }
+
+    // results: v; with kX also D in d, x = vn - v in rhs and the old voltage in w
+    for (int i0 = 0; i0 < nn; i0 += kWave * kResBatch) {
+#pragma unroll
+        for (int j = 0; j < kResBatch; ++j) {
+            const int i = i0 + j * kWave + lane;
+            if (i < nn) {
+                const double* rec = st + i * kStageArrays;
+                const double vn = rec[SA_B];
+                S.v[nb + i] = vn;
+                if constexpr (kX != 0) {
+                    const double vo = rec[SA_V];
+                    S.d[nb + i] = rec[SA_DB];
+                    S.rhs[nb + i] = vn - vo;
+                    S.w[nb + i] = vo;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // events
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int delivery_step(const double* ttab, int k, int kmax, double T, double half_dt) {
@@ -1649,6 +1856,14 @@ void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
     if (a.nunit <= 0) return;
     SolveArgs b = a;
     b.waves = std::min(std::max(a.waves, 1), kSolveMaxWaves);
+    if (b.res_nodes > 0) {
+        const size_t lds = res_lds_bytes(b.res_nodes, max_chunks, b.res_rounds) * b.waves;
+        const dim3 grid((a.nunit + b.waves - 1) / b.waves), block(kWave * b.waves);
+        const uint2* desc = reinterpret_cast<const uint2*>(b.desc);
+        if (a.store_dx) hipLaunchKernelGGL(k_solve_res<1>, grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        else hipLaunchKernelGGL(k_solve_res<0>, grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        return;
+    }
     const size_t lds = solve_lds_bytes(max_chunks) * b.waves;
     const dim3 grid((a.nunit + b.waves - 1) / b.waves), block(kWave * b.waves);
     if (a.store_dx)

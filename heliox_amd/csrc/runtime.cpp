@@ -332,6 +332,8 @@ struct hx_sim {
     int unit_request = 0;                // 0: the library's choice
     int solve_waves_request = 0;         // units per solve workgroup (0: the library's choice)
     int solve_waves = 1;                 // in use (set at load)
+    bool solve_resident_allowed = true;  // units that fit kResUnitBudget are solved held in LDS
+    int res_nodes = 0;                   // in use (set at load): nodes of the largest unit, 0: streamed
     // the solver's tree (user node indices) and its coupling coefficients
     std::vector<int> solve_parent;
     std::vector<double> solve_a, solve_b;
@@ -1069,9 +1071,17 @@ void hx_sim::upload() {
             throw std::runtime_error("a solve unit has " + std::to_string(max_slots) + " chunks; its " + std::to_string(lds) +
                                      " B solver schedule exceeds the " + std::to_string(prop.sharedMemPerBlock) +
                                      " B of LDS per workgroup");
+        // units small enough are held whole in LDS (k_solve_res), the others streamed
+        int max_unit_nodes = 0;
+        for (int u = 0; u < nunit; ++u)
+            max_unit_nodes = std::max(max_unit_nodes, unit_node_begin[u + 1] - unit_node_begin[u]);
+        const size_t rlds = res_lds_bytes(max_unit_nodes, max_slots, max_rounds);
+        const bool resident = solve_resident_allowed && rlds <= kResUnitBudget && rlds <= prop.sharedMemPerBlock;
+        res_nodes = resident ? max_unit_nodes : 0;
         // as many units per workgroup as asked (default kSolveMaxWaves) and the LDS allows
         const int want = solve_waves_request > 0 ? solve_waves_request : kSolveMaxWaves;
-        solve_waves = std::max(1, std::min<int>(want, static_cast<int>(prop.sharedMemPerBlock / lds)));
+        const size_t unit_lds = resident ? rlds : lds;
+        solve_waves = std::max(1, std::min<int>(want, static_cast<int>(prop.sharedMemPerBlock / unit_lds)));
     }
 
     // ion node -> device instance maps
@@ -2556,6 +2566,8 @@ void hx_sim::step_once_groups() {
         S.a = d_sa;
         S.b = d_sb;
         S.store_dx = store_dx() ? 1 : 0;
+        S.res_nodes = res_nodes;
+        S.res_rounds = max_rounds;
         tbegin(T_SOLVE, s);
         launch_solve(S, max_slots, s);
         tend(T_SOLVE, s);
@@ -2630,6 +2642,8 @@ void hx_sim::step_once() {
     S.a = d_sa;
     S.b = d_sb;
     S.store_dx = store_dx() ? 1 : 0;
+    S.res_nodes = res_nodes;
+    S.res_rounds = max_rounds;
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
@@ -4073,6 +4087,13 @@ int hx_set_solve_waves(hx_sim* sim, int waves) {
     return 0;
 }
 
+int hx_set_solve_resident(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
+    if (sim->loaded) return sim->fail("choose the tree solve's kernel before hx_load_model");
+    sim->solve_resident_allowed = enable != 0;
+    return 0;
+}
+
 int hx_set_group_streams(hx_sim* sim, int enable) {
     HX_SETTLE(sim);
     sim->group_streams_allowed = enable != 0;
@@ -4366,6 +4387,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "handles") return static_cast<long long>(sim->handles.size());
     if (k == "solve_unit_cells") return sim->unit_cells;
     if (k == "solve_waves") return sim->solve_waves;
+    if (k == "solve_resident") return sim->res_nodes > 0 ? 1 : 0;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;
@@ -4705,6 +4727,8 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     S.a = sim->d_sb;      // M^T: the coefficients trade places
     S.b = sim->d_sa;
     S.store_dx = 0;       // D and x are not needed: v starts at 0, so the new v is x
+    S.res_nodes = sim->res_nodes;
+    S.res_rounds = sim->max_rounds;
     double* lv = sim->d_lv;
     double* lv2 = sim->d_lv2;
     const size_t row = static_cast<size_t>(N);

@@ -141,6 +141,7 @@ SIGNATURES = {
     "hx_set_solver_root": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_waves": (C.c_int, [_P, C.c_int]),
+    "hx_set_solve_resident": (C.c_int, [_P, C.c_int]),
     "hx_output_spikes": (C.c_int, [_P, C.c_char_p]),
     "hx_set_spike_output_enabled": (C.c_int, [_P, C.c_int]),
     "hx_is_spike_output_enabled": (C.c_int, [_P]),
@@ -1080,6 +1081,11 @@ class Sim:
         """Solve units per workgroup (one wavefront each); 0 lets the library choose.  Call
         before loading the model; results do not depend on it."""
         self._chk(lib().hx_set_solve_waves(self._h, int(waves)), "set_solve_waves")
+
+    def set_solve_resident(self, enable: bool) -> None:
+        """Hold each solve unit whole in LDS when it fits (the default) or always stream its
+        rounds from HBM.  Call before loading the model; the same bits either way."""
+        self._chk(lib().hx_set_solve_resident(self._h, int(bool(enable))), "set_solve_resident")
 
     def set_group_streams(self, enable: bool) -> None:
         """Allow the cell groups' own streams in the following runs (same results either way)."""

@@ -313,6 +313,13 @@ int hx_set_solve_unit_cells(hx_sim* sim, int cells);
  * (default): 4, fewer where their LDS would exceed a workgroup's.  Results do not depend
  * on it.  Call before hx_load_model. */
 int hx_set_solve_waves(hx_sim* sim, int waves);
+/* Tree solve kernel (no counterpart in the reference): enable = 1 (default) holds each
+ * solve unit whole in LDS when the largest unit's nodes, rounds and chunks fit 40 KB
+ * (cells of up to about 900 nodes at one cell per unit): d, rhs, a, b and v are read once
+ * into one record per node and v is written once, every intermediate stays in LDS.  0, or
+ * a larger unit: the rounds are streamed through LDS from HBM.  The same bits either way;
+ * hx_get_info("solve_resident") reports the choice.  Call before hx_load_model. */
+int hx_set_solve_resident(hx_sim* sim, int enable);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
