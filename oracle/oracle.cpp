@@ -42,6 +42,12 @@
 // (coredat_to_innerdat.cpp:176-181).  The oracle uses the fixed order of
 // kMechOrder below, which is the NEURON built-in type order followed by the
 // user mechanisms; the HIP path documents its own accumulation order.
+//
+// Pinning: every function above is checked, in tests/test_oracle_pinning.py,
+// tests/test_netstim.py and tests/test_lrds_oracle.py, against closed forms, textbook
+// rates, known-answer vectors or brute force chosen so that a plausible slip (a dropped
+// term, a wrong sign, index or exponent) fails one of them; no function is left with
+// parity unpinned.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
