@@ -47,15 +47,19 @@ MECH_BYTES_PER_COMP = 280
 STEP_BYTES_PER_INSTANCE = {"pas": 16, "hh": 96, "hd_la": 40, "Ca_HVA": 40, "CaDynamics_E2": 56,
                            "Exp2Syn": 108, "ExpSyn": 76, "IClamp": 52}
 # per node: node kernel reads v, cm and writes rhs, d (32); the solve reads rhs, d,
-# a, b, v and the parent index and writes v (52)
+# a, b, v and the parent index and writes v (52).  Solving for the new voltage (rhs + d v
+# from the node kernel), the solve does not read v (44).
 STEP_BYTES_PER_NODE = 84
+SOLVE_V_BYTES = 8
 
 
-def step_bytes(spec, ms_per_step: float, not_read: int = 0):
+def step_bytes(spec, ms_per_step: float, not_read: int = 0, solve_voltage: bool = False):
     """Algorithmic HBM bytes of one whole step and the rate they imply at the measured
     step time (against the HBM peak): an end-to-end figure beside the node kernel's.
-    not_read: bytes of parameter columns served as one value (not read per instance)."""
-    total = STEP_BYTES_PER_NODE * spec.nnode - not_read
+    not_read: bytes of parameter columns served as one value (not read per instance);
+    solve_voltage: the solve yields the new voltage without reading v."""
+    per_node = STEP_BYTES_PER_NODE - (SOLVE_V_BYTES if solve_voltage else 0)
+    total = per_node * spec.nnode - not_read
     for name, m in spec.mechs.items():
         total += STEP_BYTES_PER_INSTANCE.get(name, 0) * m.n
     gbs = total / (ms_per_step * 1e-3) / 1e9
@@ -148,13 +152,16 @@ def perturb_config3(spec, seed: int = 1):
 
 
 def solver_options(sim, args):
-    """Tree-solve layout options of the command line (none changes a result)."""
+    """Tree-solve options of the command line (the layouts change no result; the two solve
+    forms agree to rounding)."""
     if args.unit_cells:
         sim.set_solve_unit_cells(args.unit_cells)
     if args.solve_waves:
         sim.set_solve_waves(args.solve_waves)
     if args.solve_streamed:
         sim.set_solve_resident(False)
+    if args.solve_change:
+        sim.set_solve_voltage(False)
 
 
 def train_bench(args):
@@ -417,6 +424,9 @@ def main():
     ap.add_argument("--solve-streamed", action="store_true",
                     help="stream every solve unit's rounds from HBM, also where the unit fits in LDS "
                          "(same results)")
+    ap.add_argument("--solve-change", action="store_true",
+                    help="solve for the change in voltage, as the reference does, also where the node "
+                         "kernel makes every term of the matrix (the forms agree to rounding)")
     ap.add_argument("--no-group-turns", action="store_true",
                     help="order the cell groups' node passes only on a run's first step (same results)")
     ap.add_argument("--generic-node-kernel", action="store_true",
@@ -583,13 +593,14 @@ def main():
                                f"hh+pas+Ih+Ca_HVA+CaDynamics_E2 everywhere, 200 Exp2Syn/cell with 5 Hz "
                                f"Poisson VecStim input, dt 0.025 ms",
                    "ncell": args.ncell, "compartments": nnode, "dt_ms": dt, "cell_groups": groups,
+                   "solve_voltage": sim.info("solve_voltage"),
                    "wall_s_per_simulated_s": ms_per_step * 40.0},
         "state_update_carried_in": bool(carried_in),
         "state_update_deferred": bool(deferred),
         "last_step_outputs_on_demand": bool(outputs_deferred),
         "roofline": roofline,
         "roofline_single_stream": alone,
-        "step_bytes": step_bytes(spec, ms_per_step, uniform_bytes),
+        "step_bytes": step_bytes(spec, ms_per_step, uniform_bytes, bool(sim.info("solve_voltage"))),
         "uniform_columns": {"columns": uniform_cols, "bytes_per_step_not_read": uniform_bytes,
                             "all_columns_read": streamed},
         "cpu_baseline": cpu,

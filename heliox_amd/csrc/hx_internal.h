@@ -111,6 +111,8 @@ struct StepArgs {
     int hh_owns_ions;             // sparse hh stores the na / k currents (the ion kernels do not run)
     int do_state;                 // finish the previous step's state update first
     int cadyn_skip;               // ... except CaDynamics_E2, already updated by the last current pass
+    int yform;                    // store rhs + d v in rhs: the solve then yields v_new itself (every
+                                  // d and rhs term of the step comes from this pass)
     int cadyn_after;              // update CaDynamics_E2 right after this pass's ica (its state
                                   // depends on ica and cai only, so this is the step's own update)
     int do_current;
@@ -186,6 +188,8 @@ struct SolveArgs {
     const double* b;
     int store_dx;                 // 1: leave D in d and x = vn - v in rhs (as the reference does); 0: neither
     int waves;                    // solve units per workgroup, one wavefront each (1..kSolveMaxWaves)
+    int yform;                    // 1: rhs holds rhs + d v, so elimination takes v as 0 and back
+                                  // substitution yields v_new directly (v is read only for x)
     int res_nodes;                // > 0: each unit is solved held whole in LDS, sized for this many nodes
     int res_rounds;               //   and this many rounds (the largest unit's); 0: rounds streamed from HBM
 };

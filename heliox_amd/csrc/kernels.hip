@@ -358,7 +358,9 @@ __device__ __forceinline__ void dense_node(const StepArgs& A, const P& p, int* s
     }
     if (p.has(M_HDLA)) { cur = hdla_cur(A, A.m[M_HDLA], i, v, hl, g, wa); rhs -= cur; d += g; }
     A.d[i] = d;
-    A.rhs[i] = rhs;
+    // with every d and rhs term of the step in this pass, rhs + d v makes the solve's
+    // unknown the new voltage itself: the axial terms cancel, so the solve never reads v
+    A.rhs[i] = A.yform ? fma(d, v, rhs) : rhs;
     const bool wdc = p.write_dcurdv();
     if (p.has(M_NA_ION)) dense_ion_store(A, na, 0, i, ina, wdc);
     if (p.has(M_K_ION)) dense_ion_store(A, kk, 1, i, ik, wdc);
@@ -825,7 +827,14 @@ __device__ __forceinline__ void fwd_load(const SolveCtx& C, FwdBuf& B, const Rou
         B.x[1][j] = rhs[e];
         B.x[2][j] = a[e];
         B.x[3][j] = b[e];
-        B.x[4][j] = v[e];
+    }
+    // v enters elimination only through the axial terms, which rhs + d v already holds
+    if (C.S.yform) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) B.x[4][j] = 0.0;
+    } else {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) B.x[4][j] = v[clamp_index(C.lane, j, ri.node_count)];
     }
     B.q = load_desc(C, ri);
     B.ri = ri;
@@ -1056,12 +1065,13 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve(SolveArgs S, c
 // Node k of the lane's chunk reads record rp[k] (in doubles: record index x 5; the
 // neutral record past the chunk's length) and writes record wp[k] (the sink record past
 // the length, so that padding slots leave the neutral record as it is).
+template <int kY>
 struct ResIn {
     const double* st;
     const int* rp;
     __device__ __forceinline__ FwdNode fwd(int k) const {
         const double* r = st + rp[k];
-        return {r[SA_DB], r[SA_RM], r[SA_A], r[SA_B], r[SA_V]};
+        return {r[SA_DB], r[SA_RM], r[SA_A], r[SA_B], kY ? 0.0 : r[SA_V]};
     }
     __device__ __forceinline__ BackNode back(int k) const {
         const double* r = st + rp[k];
@@ -1096,7 +1106,9 @@ __device__ __forceinline__ uint2 res_desc(const uint2* dtab, int ndesc, const Ro
 constexpr int kResBatch = 4;    // nodes a lane moves per batch at the start and the end
 
 // One wavefront per unit, S.waves units per workgroup, each with its own LDS region.
-template <int kX>
+// kY: rhs holds rhs + d v (SolveArgs::yform), so elimination takes v as 0; v is then read
+// only where x = v_new - v is stored (kX).
+template <int kX, int kY>
 __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs S, const RoundInfo* rounds_all,
                                                                       const uint2* desc_all, int max_chunks) {
     extern __shared__ double lds[];
@@ -1129,7 +1141,8 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs 
                 const int i = i0 + j * kWave + lane;
                 const int e = i < nn ? i : nn - 1;
 #pragma unroll
-                for (int q = 0; q < kStageArrays; ++q) x[q][j] = lds_(src[q] + e);
+                for (int q = 0; q < kStageArrays; ++q)
+                    x[q][j] = (q != SA_V || !kY || kX) ? lds_(src[q] + e) : 0.0;
             }
 #pragma unroll
             for (int j = 0; j < kResBatch; ++j) {
@@ -1182,7 +1195,7 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs 
             res_positions<KM>(ri, len, lane, neutral, rp, wp, tp);
             if (nchild > 0) {
                 double db = st[tp + SA_DB], rm = st[tp + SA_RM];
-                tail_inject(db, rm, st[tp + SA_V], acd, ace);
+                tail_inject(db, rm, kY ? 0.0 : st[tp + SA_V], acd, ace);
                 st[tp + SA_DB] = db;
                 st[tp + SA_RM] = rm;
             }
@@ -1192,7 +1205,7 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs 
                 o[SA_RM] = sv;
                 o[SA_A] = w;
             };
-            chunk_forward_math<KM>(has_parent, ResIn{st, rp}, out, rcp_nr, cd, ce);
+            chunk_forward_math<KM>(has_parent, ResIn<kY>{st, rp}, out, rcp_nr, cd, ce);
         });
         __builtin_amdgcn_s_setprio(0);
         if (act && has_parent) pairs[slot] = SlotPair{cd, ce};
@@ -1218,7 +1231,7 @@ __global__ void __launch_bounds__(kWave * kSolveMaxWaves) k_solve_res(SolveArgs 
                 st[wp[k] + SA_B] = vn;
                 if (k == len - 1) vtail = vn;
             };
-            chunk_back_math<KM>(ResIn{st, rp}, out, vpar);
+            chunk_back_math<KM>(ResIn<kY>{st, rp}, out, vpar);
         });
         __builtin_amdgcn_s_setprio(0);
         if (act) slots[2 * slot] = vtail;   // the tail's new voltage
@@ -1860,8 +1873,14 @@ void launch_solve(const SolveArgs& a, int max_chunks, hipStream_t s) {
         const size_t lds = res_lds_bytes(b.res_nodes, max_chunks, b.res_rounds) * b.waves;
         const dim3 grid((a.nunit + b.waves - 1) / b.waves), block(kWave * b.waves);
         const uint2* desc = reinterpret_cast<const uint2*>(b.desc);
-        if (a.store_dx) hipLaunchKernelGGL(k_solve_res<1>, grid, block, lds, s, b, b.rounds, desc, max_chunks);
-        else hipLaunchKernelGGL(k_solve_res<0>, grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        if (a.store_dx && a.yform)
+            hipLaunchKernelGGL((k_solve_res<1, 1>), grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        else if (a.store_dx)
+            hipLaunchKernelGGL((k_solve_res<1, 0>), grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        else if (a.yform)
+            hipLaunchKernelGGL((k_solve_res<0, 1>), grid, block, lds, s, b, b.rounds, desc, max_chunks);
+        else
+            hipLaunchKernelGGL((k_solve_res<0, 0>), grid, block, lds, s, b, b.rounds, desc, max_chunks);
         return;
     }
     const size_t lds = solve_lds_bytes(max_chunks) * b.waves;

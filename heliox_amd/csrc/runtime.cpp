@@ -333,6 +333,9 @@ struct hx_sim {
     int solve_waves_request = 0;         // units per solve workgroup (0: the library's choice)
     int solve_waves = 1;                 // in use (set at load)
     bool solve_resident_allowed = true;  // units that fit kResUnitBudget are solved held in LDS
+    bool solve_voltage_allowed = true;   // the solve may take rhs + d v and yield v_new itself
+    bool solve_voltage = false;          // in use: every d and rhs term of a step is the node kernel's
+    int pass_yform = 0;                  // the node pass being launched stores rhs + d v
     int res_nodes = 0;                   // in use (set at load): nodes of the largest unit, 0: streamed
     // the solver's tree (user node indices) and its coupling coefficients
     std::vector<int> solve_parent;
@@ -696,6 +699,7 @@ struct hx_sim {
     // ------------------------------------------------------------ layout
     void build_layout();
     void recompute_fused();
+    bool node_kernel_owns_matrix() const;
     void upload();
     void upload_inputs();
     void upload_vecplay();
@@ -1002,6 +1006,9 @@ void hx_sim::build_layout() {
     recompute_fused();
 }
 
+// the density mechanisms in the order of their kernels when they are not fused
+static const int kSparseOrder[] = {M_PAS, M_NA_ION, M_K_ION, M_HH, M_CA_ION, M_CADYN, M_CAHVA, M_HDLA};
+
 // Fusing the state update of step k-1 into the current pass of step k is exact
 // unless something observes or changes density-mechanism values between the two.
 void hx_sim::recompute_fused() {
@@ -1015,6 +1022,21 @@ void hx_sim::recompute_fused() {
     }
     if (need_split_for_monitor) fuse = false;
     fused = fuse;
+    solve_voltage = solve_voltage_allowed && node_kernel_owns_matrix();
+}
+
+// True when a stepping current pass takes every term of d and rhs from the node kernel:
+// no density mechanism on a kernel of its own, no IClamp or HalfGap instance (synapses are
+// folded into the node kernel), no plugin.  The node kernel can then store rhs + d v, and
+// the solve yields the new voltage without reading v: (D + L) x = r - L v, with D the node
+// kernel's diagonal and L the axial couplings, is (D + L) v_new = r + D v.
+bool hx_sim::node_kernel_owns_matrix() const {
+    if (dense_mask == 0 || !plugins.empty()) return false;
+    for (int id : kSparseOrder)
+        if (mech[id].present && !(dense_mask & (1u << id))) return false;
+    for (int id : {M_ICLAMP, M_HALFGAP})
+        if (mech[id].present && mech[id].n > 0) return false;
+    return true;
 }
 
 // CaDynamics_E2's state depends on ica and cai only, so in the fused schedule
@@ -2004,6 +2026,7 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
         if (!uniform_on) A.m[id].umask = 0;
     }
     A.dense_mask = dense_mask;
+    A.yform = pass_yform;
     A.hh_owns_ions = (hh_owns_ions && !init_pass) ? 1 : 0;
     A.do_state = do_state;
     A.cadyn_skip = do_state ? pass_cadyn_skip : 0;
@@ -2066,7 +2089,6 @@ StepArgs hx_sim::step_args(double tcur, int do_state, int do_current) const {
 // ===========================================================================
 // stepping
 // ===========================================================================
-static const int kSparseOrder[] = {M_PAS, M_NA_ION, M_K_ION, M_HH, M_CA_ION, M_CADYN, M_CAHVA, M_HDLA};
 
 // The mechanism pass over the whole model, or over one cell group (nodes,
 // synapse fold tables and instance ranges of that group) on stream `on`.
@@ -2536,7 +2558,9 @@ void hx_sim::step_once_groups() {
             record();
             if (g > 0) HXC(hipStreamWaitEvent(s, groups[g - 1].pass_mark, 0));
             else if (turns_prev) HXC(hipStreamWaitEvent(s, groups[G - 1].pass_mark, 0));
+            pass_yform = solve_voltage ? 1 : 0;
             launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+            pass_yform = 0;
             // the next group waits for this mark; when the node kernel is timed, its end event
             // (set by the kernel's dispatch, nothing launched after it) marks the same point
             cg.pass_mark = mech_end_mark;
@@ -2547,7 +2571,9 @@ void hx_sim::step_once_groups() {
         } else {
             if (stagger && g > 0) HXC(hipStreamWaitEvent(s, ev_stagger, 0));
             launch_events_group(g, k, tk, s);
+            pass_yform = solve_voltage ? 1 : 0;
             launch_mech_pass(pending ? 1 : 0, 1, tmid, g, s);
+            pass_yform = 0;
             if (stagger && g + 1 < G) HXC(hipEventRecord(ev_stagger, s));
             record();
         }
@@ -2568,6 +2594,7 @@ void hx_sim::step_once_groups() {
         S.store_dx = store_dx() ? 1 : 0;
         S.res_nodes = res_nodes;
         S.res_rounds = max_rounds;
+        S.yform = solve_voltage ? 1 : 0;
         tbegin(T_SOLVE, s);
         launch_solve(S, max_slots, s);
         tend(T_SOLVE, s);
@@ -2615,7 +2642,9 @@ void hx_sim::step_once() {
         const bool eager = cadyn_eager && !(final_step && lazy_outputs_run);   // as in step_once_groups
         pass_cadyn_skip = cadyn_done ? 1 : 0;
         pass_cadyn_after = eager ? 1 : 0;
+        pass_yform = solve_voltage ? 1 : 0;
         launch_mech_pass(state_pending ? 1 : 0, 1, tmid);
+        pass_yform = 0;
         cadyn_done = eager;
         pass_cadyn_skip = pass_cadyn_after = 0;
         if (state_pending && !pending_sampled) launch_record();
@@ -2623,7 +2652,9 @@ void hx_sim::step_once() {
     } else {
         launch_events(k, tk);
         if (has_vp) { tbegin(T_OTHER); launch_vecplay(d_vecplay, nvp, tmid, 1, stream); tend(T_OTHER); }
+        pass_yform = solve_voltage ? 1 : 0;
         launch_mech_pass(0, 1, tmid);
+        pass_yform = 0;
     }
     launch_point_currents(tmid);
     launch_plugin_currents(tmid);
@@ -2644,6 +2675,7 @@ void hx_sim::step_once() {
     S.store_dx = store_dx() ? 1 : 0;
     S.res_nodes = res_nodes;
     S.res_rounds = max_rounds;
+    S.yform = solve_voltage ? 1 : 0;
     tbegin(T_SOLVE);
     launch_solve(S, max_slots, stream);
     tend(T_SOLVE);
@@ -4094,6 +4126,13 @@ int hx_set_solve_resident(hx_sim* sim, int enable) {
     return 0;
 }
 
+int hx_set_solve_voltage(hx_sim* sim, int enable) {
+    HX_SETTLE(sim);
+    sim->solve_voltage_allowed = enable != 0;
+    if (sim->loaded) sim->recompute_fused();
+    return 0;
+}
+
 int hx_set_group_streams(hx_sim* sim, int enable) {
     HX_SETTLE(sim);
     sim->group_streams_allowed = enable != 0;
@@ -4388,6 +4427,7 @@ long long hx_get_info(hx_sim* sim, const char* key) {
     if (k == "solve_unit_cells") return sim->unit_cells;
     if (k == "solve_waves") return sim->solve_waves;
     if (k == "solve_resident") return sim->res_nodes > 0 ? 1 : 0;
+    if (k == "solve_voltage") return sim->solve_voltage ? 1 : 0;
     if (k == "nchunk_total") return static_cast<long long>(sim->descs.size());
     if (k == "event_slots") return sim->groups.empty() ? 0 : sim->groups[0].ring.nslot;
     if (k == "event_cap") return sim->groups.empty() ? 0 : sim->groups[0].ring.cap;

@@ -142,6 +142,7 @@ SIGNATURES = {
     "hx_set_solve_unit_cells": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_waves": (C.c_int, [_P, C.c_int]),
     "hx_set_solve_resident": (C.c_int, [_P, C.c_int]),
+    "hx_set_solve_voltage": (C.c_int, [_P, C.c_int]),
     "hx_output_spikes": (C.c_int, [_P, C.c_char_p]),
     "hx_set_spike_output_enabled": (C.c_int, [_P, C.c_int]),
     "hx_is_spike_output_enabled": (C.c_int, [_P]),
@@ -1086,6 +1087,12 @@ class Sim:
         """Hold each solve unit whole in LDS when it fits (the default) or always stream its
         rounds from HBM.  Call before loading the model; the same bits either way."""
         self._chk(lib().hx_set_solve_resident(self._h, int(bool(enable))), "set_solve_resident")
+
+    def set_solve_voltage(self, enable: bool) -> None:
+        """Let a model whose node kernel makes every term of d and rhs solve for the new
+        voltage directly (the default), or always solve for the change, as the reference
+        does.  The two agree to rounding."""
+        self._chk(lib().hx_set_solve_voltage(self._h, int(bool(enable))), "set_solve_voltage")
 
     def set_group_streams(self, enable: bool) -> None:
         """Allow the cell groups' own streams in the following runs (same results either way)."""

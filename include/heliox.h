@@ -320,6 +320,14 @@ int hx_set_solve_waves(hx_sim* sim, int waves);
  * a larger unit: the rounds are streamed through LDS from HBM.  The same bits either way;
  * hx_get_info("solve_resident") reports the choice.  Call before hx_load_model. */
 int hx_set_solve_resident(hx_sim* sim, int enable);
+/* Tree solve unknown (no counterpart in the reference): enable = 1 (default) lets a model
+ * whose node kernel makes every term of d and rhs (no density mechanism on its own kernel,
+ * no IClamp or HalfGap instance, no plugin) store rhs + d v, so that the solve yields the
+ * new voltage directly and never reads v (the axial terms cancel); the reference's form
+ * solves for x = v_new - v and adds it.  The two agree to rounding (about 1e-13 mV per
+ * step); rhs still holds x wherever it is read.  hx_get_info("solve_voltage") reports the
+ * form in use.  May be called at any time. */
+int hx_set_solve_voltage(hx_sim* sim, int enable);
 /* Allow (1, default) or forbid (0) issuing the cell groups on their own streams in the
  * following runs; with 0 every launch goes to the library stream.  Same results. */
 int hx_set_group_streams(hx_sim* sim, int enable);
