@@ -304,7 +304,6 @@ __global__ void k_adj_before_nodes(AdjStep A) {
     }
     A.dT[i] = d;
     A.rhsT[i] = lv;
-    A.vT[i] = 0.0;
 }
 
 // After the solve: lambda_v^n = C mu, then the parameter terms of the mechanisms in

@@ -420,7 +420,6 @@ struct AdjStep {
     double* lam_g;                // adjoint of ExpSyn g (g^{n+1} in, g^n out)
     double* dT;
     double* rhsT;
-    double* vT;
     const double* mu;             // M^{-T} lam_v (the transposed solve's solution)
     double* grad_gnabar;
     double* grad_gkbar;

@@ -4633,8 +4633,7 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     A.lam_g = sim->d_lg;
     A.dT = sim->d_dT;
     A.rhsT = sim->d_rhsT;
-    A.vT = sim->d_vT;
-    A.mu = sim->d_vT;     // the solve's new voltage from v = 0 is x = M^-T lambda
+    A.mu = sim->d_vT;     // the solve's new voltage (solved for directly) is x = M^-T lambda
     A.grad_gnabar = sim->d_grad[T_GNABAR];
     A.grad_gkbar = sim->d_grad[T_GKBAR];
     A.grad_gpas = sim->d_grad[T_GPAS];
@@ -4766,7 +4765,9 @@ int hx_adjoint(hx_sim* sim, int nloss, const int* loss_nodes, const double* targ
     S.w = sim->d_wT;
     S.a = sim->d_sb;      // M^T: the coefficients trade places
     S.b = sim->d_sa;
-    S.store_dx = 0;       // D and x are not needed: v starts at 0, so the new v is x
+    S.store_dx = 0;       // D and x are not needed
+    S.yform = 1;          // the transposed system's unknown starts at 0: the solve reads no v,
+                          // and the new v it writes is the solution itself
     S.res_nodes = sim->res_nodes;
     S.res_rounds = sim->max_rounds;
     double* lv = sim->d_lv;
